@@ -1,0 +1,223 @@
+#!/usr/bin/env python3
+"""Decode throughput of the Qwen3-8B-shaped Q6_K decoder on one MI355X.
+
+One step = one greedy decode step of every client through the whole model
+(embedding, 36 layers, 151936-row output, greedy select), weights and KV cache
+resident in HBM.  Prints one JSON line (see the repository's bench contract).
+
+  value     batch-1 decode tokens/s after a 512-token prompt (fp16 KV)
+  batch8    the same model with 8 clients (aggregate tokens/s)
+  roofline  the dominant kernel: the fused gate|up Q6_K matvec (RMSNorm +
+            SwiGLU epilogue), 2 x 12288 x 4096 weights = 82,575,360 B per
+            launch, timed with HIP events on the library's stream while it
+            walks all 36 layers (6.2 GB of distinct weights, so nothing is
+            served from the 256 MB Infinity Cache)
+  cpu_baseline  the oracle (C restatement of the reference CPU path), one
+            thread, one token through 1 and 4 layers + output, extrapolated
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from emufpga_amd import _lib  # noqa: E402
+from emufpga_amd.device import Context  # noqa: E402
+from emufpga_amd.gguf import row_bytes  # noqa: E402
+from emufpga_amd.serve import QWEN3_8B_Q6K, Model, Session  # noqa: E402
+
+METRIC = "decode tok/s at batch 1 and 8; achieved HBM GB/s vs 8 TB/s peak"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def layer_offsets(cfg):
+    rb_h = row_bytes(cfg.encoding, cfg.hidden)
+    rb_q = row_bytes(cfg.encoding, cfg.q_width)
+    off_g = cfg.q_width * rb_h + 2 * cfg.kv_width * rb_h + cfg.hidden * rb_q
+    off_u = off_g + cfg.ffn * rb_h
+    return rb_h, off_g, off_u
+
+
+def time_gate_up(ctx: Context, model: Model, rounds: int) -> tuple[float, int, int]:
+    """Average duration (ms) of the fused gate|up matvec over all layers."""
+    cfg = model.cfg
+    rb_h, off_g, off_u = layer_offsets(cfg)
+    rng = np.random.default_rng(0)
+    x = ctx.upload(rng.normal(size=cfg.hidden).astype(np.float32))
+    gain = ctx.upload(np.ones(cfg.hidden, np.float32))
+    y = ctx.alloc(cfg.ffn * 4)
+    bases = [model.tensor(_lib.EMU_T_LAYER, l)[0] for l in range(cfg.layers)]
+
+    def launch(base):
+        ctx.check(ctx.lib.emu_qmatvec_fused(ctx.h, cfg.encoding, C.c_void_p(base + off_g),
+                                            C.c_void_p(base + off_u), cfg.ffn, cfg.hidden, x.ptr, 1,
+                                            gain.ptr, cfg.eps, y.ptr, 0), "gate_up")
+
+    for base in bases:  # warm
+        launch(base)
+    ctx.sync()
+    ctx.event_record(0)
+    for _ in range(rounds):
+        for base in bases:
+            launch(base)
+    ctx.event_record(1)
+    ms = ctx.event_elapsed(0, 1) / (rounds * len(bases))
+    algo = 2 * cfg.ffn * rb_h
+    return ms, algo, rounds * len(bases)
+
+
+def cpu_baseline(model: Model) -> dict:
+    import oracle
+
+    cfg = model.cfg
+    n_layers = 4
+    w = {
+        "layers": np.concatenate([model.read_tensor(_lib.EMU_T_LAYER, l) for l in range(n_layers)]),
+        "embed": model.read_tensor(_lib.EMU_T_EMBED),
+        "output": model.read_tensor(_lib.EMU_T_OUTPUT),
+        "attn_norm": model.read_tensor(_lib.EMU_T_ATTN_NORM, dtype=np.float32),
+        "ffn_norm": model.read_tensor(_lib.EMU_T_FFN_NORM, dtype=np.float32),
+        "q_norm": model.read_tensor(_lib.EMU_T_Q_NORM, dtype=np.float32),
+        "k_norm": model.read_tensor(_lib.EMU_T_K_NORM, dtype=np.float32),
+        "out_norm": model.read_tensor(_lib.EMU_T_OUT_NORM, dtype=np.float32),
+    }
+    ocfg = oracle.DenseCfg(hidden=cfg.hidden, heads=cfg.heads, kv_heads=cfg.kv_heads, head_dim=cfg.head_dim,
+                           ffn=cfg.ffn, vocab=cfg.vocab, layers=cfg.layers, context=4, rope_theta=cfg.rope_theta,
+                           eps=cfg.eps, style=cfg.style, dtype=cfg.encoding, kv_f16=1, tied=0, qk_norm=1)
+    times = {}
+    for limit in (1, n_layers):
+        orc = oracle.DenseOracle(ocfg, w, 1)
+        t0 = time.perf_counter()
+        orc.step([17], layers_limit=limit)
+        times[limit] = time.perf_counter() - t0
+        log(f"cpu oracle: {limit} layer(s) + output in {times[limit]:.2f} s")
+    per_layer = (times[n_layers] - times[1]) / (n_layers - 1)
+    full = times[1] + (cfg.layers - 1) * per_layer
+    weight_bytes = model.weight_bytes()
+    return {
+        "value": round(1.0 / full, 5),
+        "unit": "tok/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"one batch-1 token at position 0 through the embedding, 1 and {n_layers} layers and the "
+                   f"151936-row output (single-threaded C restatement of the reference CPU path); per-layer time "
+                   f"({per_layer:.3f} s) extrapolated to {cfg.layers} layers: {full:.2f} s/token"),
+        "algorithmic_gbs": round(weight_bytes / full / 1e9, 3),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--context", type=int, default=2048)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-batch8", action="store_true")
+    ap.add_argument("--roofline-rounds", type=int, default=8)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (the decode path is "
+              "single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+        return 2
+
+    cfg = QWEN3_8B_Q6K
+    ctx = Context(0)
+    cus, arch = ctx.device_info()
+    log(f"device: {arch}, {cus} CUs")
+    t0 = time.perf_counter()
+    model = Model(ctx, cfg)
+    model.synth(20260101)
+    weight_bytes = model.weight_bytes()
+    log(f"synthesised {weight_bytes / 1e9:.3f} GB of Q6_K weights in {time.perf_counter() - t0:.1f} s")
+
+    rng = np.random.default_rng(42)
+    results = {}
+    for batch in ([1] if args.no_batch8 else [1, 8]):
+        sess = Session(model, batch, args.context, kv_f16=True)
+        prompt = rng.integers(0, cfg.vocab, size=(batch, args.prompt)).astype(np.uint32)
+        t0 = time.perf_counter()
+        sess.generate(prompt, 1 + args.warmup)  # prefill + warmup decode steps, untimed
+        log(f"batch {batch}: prompt {args.prompt} + {args.warmup} warmup steps in {time.perf_counter() - t0:.1f} s")
+        ctx.sync()
+        ms = sess.time_decode(args.steps)
+        ctx.sync()
+        pos = int(sess.positions()[0])
+        results[batch] = (ms, pos)
+        log(f"batch {batch}: {args.steps} steps in {ms:.2f} ms -> {batch * args.steps / (ms / 1e3):.1f} tok/s "
+            f"(context {pos - args.steps}..{pos})")
+        sess.close()
+
+    ms1, pos1 = results[1]
+    step_ms = ms1 / args.steps
+    tok_s = args.steps / (ms1 / 1e3)
+    ctx_mid = pos1 - args.steps // 2
+    kv_bytes = cfg.layers * 2 * cfg.kv_width * 2 * ctx_mid  # fp16 K and V read per token
+    step_gbs = (weight_bytes + kv_bytes) / (step_ms / 1e3) / 1e9
+
+    ku_ms, ku_bytes, launches = time_gate_up(ctx, model, args.roofline_rounds)
+    achieved = ku_bytes / (ku_ms / 1e3) / 1e9
+    log(f"gate|up matvec: {ku_ms * 1e3:.2f} us avg over {launches} launches -> {achieved:.0f} GB/s")
+
+    out = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"Qwen3-8B-shaped dense decoder, Q6_K weights (seeded N(0,0.02) synthetic), batch 1, "
+                         f"{args.prompt}-token prompt then greedy decode, fp16 KV cache sized {args.context}"),
+            "hidden": cfg.hidden, "layers": cfg.layers, "heads": cfg.heads, "kv_heads": cfg.kv_heads,
+            "head_dim": cfg.head_dim, "ffn": cfg.ffn, "vocab": cfg.vocab, "encoding": "Q6_K",
+            "context_at_timing": [pos1 - args.steps, pos1],
+        },
+        "step_hbm_gbs": round(step_gbs, 1),
+        "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
+        "weight_bytes_per_step": weight_bytes,
+        "roofline": {
+            "kernel": "qmv_kernel<FmtQ6K,1,dual,norm> (fused gate|up, 12288x4096 pair)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(ku_ms * 1e3, 3),
+            "algorithmic_bytes_per_launch": ku_bytes,
+        },
+    }
+    if 8 in results:
+        ms8, pos8 = results[8]
+        out["batch8"] = {"value": round(8 * args.steps / (ms8 / 1e3), 2), "unit": "tok/s",
+                         "ms_per_step": round(ms8 / args.steps, 4), "context_at_timing": [pos8 - args.steps, pos8]}
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(model)
+    print(json.dumps(out), flush=True)
+    model.close()
+    ctx.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,205 @@
+"""ctypes binding of libemuhip.so (the C ABI declared in include/emuhip.h).
+
+The native library is the product: if it is missing this module raises
+instead of falling back to any CPU path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libemuhip.so"
+
+# emu_status (include/emuhip.h)
+EMU_OK = 0
+EMU_E_SHORT = 1
+EMU_E_SHAPE = 2
+EMU_E_ACTIVATION_LEN = 3
+EMU_E_TRUNCATED = 4
+EMU_E_UNSUPPORTED = 5
+EMU_E_CONTEXT_FULL = 6
+EMU_E_CONFIG = 7
+EMU_E_HIP = 8
+EMU_E_ARG = 9
+EMU_E_NOMEM = 10
+
+# GGUF dtype ids (spm-gguf/src/parse.rs:10-29)
+F32, F16, Q8_0, Q2_K, Q5_K, Q6_K = 0, 1, 8, 10, 13, 14
+ENCODINGS = {"F32": F32, "F16": F16, "Q8_0": Q8_0, "Q2_K": Q2_K, "Q5_K": Q5_K, "Q6_K": Q6_K}
+
+EMU_MV_ACCUMULATE = 1
+EMU_ROPE_NEOX = 0
+EMU_ROPE_INTERLEAVED = 1
+EMU_STYLE_QWEN3 = 0
+EMU_STYLE_SMOL = 1
+(EMU_T_LAYER, EMU_T_EMBED, EMU_T_OUTPUT, EMU_T_ATTN_NORM, EMU_T_FFN_NORM, EMU_T_Q_NORM,
+ EMU_T_K_NORM, EMU_T_OUT_NORM) = range(8)
+
+
+class EmuError(RuntimeError):
+    """A non-OK status from the native library."""
+
+    def __init__(self, status: int, what: str, detail: str = ""):
+        self.status = status
+        msg = f"{what}: {strerror(status)} (status {status})"
+        if detail:
+            msg += f" [{detail}]"
+        super().__init__(msg)
+
+
+class DecodeError(EmuError):
+    """spm-codec-any DecodeError (decode.rs:8-19)."""
+
+
+class Short(DecodeError):
+    """Partial block (tensor.rs:105-107)."""
+
+
+class Unsupported(DecodeError):
+    """Encoding without a decoder (decode.rs:43-45)."""
+
+
+class LinearError(EmuError):
+    """spm-linear LinearError (resident.rs:6-34)."""
+
+
+class WeightCount(LinearError):
+    pass
+
+
+class ActivationLen(LinearError):
+    pass
+
+
+class Truncated(LinearError):
+    pass
+
+
+class ContextFull(EmuError):
+    """KvCache::append on a full context (spm-kv/src/cache.rs:50-54)."""
+
+
+class ConfigError(EmuError):
+    """Configuration errors the reference panics on (attend.rs:82-85)."""
+
+
+class HipError(EmuError):
+    pass
+
+
+class ArgumentError(EmuError):
+    pass
+
+
+_ERRORS = {
+    EMU_E_SHORT: Short,
+    EMU_E_SHAPE: WeightCount,
+    EMU_E_ACTIVATION_LEN: ActivationLen,
+    EMU_E_TRUNCATED: Truncated,
+    EMU_E_UNSUPPORTED: Unsupported,
+    EMU_E_CONTEXT_FULL: ContextFull,
+    EMU_E_CONFIG: ConfigError,
+    EMU_E_HIP: HipError,
+    EMU_E_ARG: ArgumentError,
+    EMU_E_NOMEM: EmuError,
+}
+
+
+class ModelConfig(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_uint32), ("heads", C.c_uint32), ("kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32), ("ffn", C.c_uint32), ("vocab", C.c_uint32),
+        ("layers", C.c_uint32), ("rope_theta", C.c_float), ("eps", C.c_float),
+        ("style", C.c_int32), ("encoding", C.c_int32), ("tied", C.c_int32),
+        ("qk_norm", C.c_int32),
+    ]
+
+
+P = C.c_void_p
+U32 = C.c_uint32
+SZ = C.c_size_t
+I = C.c_int
+F = C.c_float
+FP = C.POINTER(C.c_float)
+
+# name -> argtypes; every function returns int (emu_status) unless listed in _RESTYPE
+SIGNATURES = {
+    "emu_strerror": [I],
+    "emu_last_error": [P],
+    "emu_ctx_create": [I, C.POINTER(P)],
+    "emu_ctx_destroy": [P],
+    "emu_ctx_sync": [P],
+    "emu_ctx_stream": [P, C.POINTER(P)],
+    "emu_device_info": [P, C.POINTER(I), C.c_char_p, SZ],
+    "emu_malloc": [P, SZ, C.POINTER(P)],
+    "emu_free": [P, P],
+    "emu_memcpy_htod": [P, P, P, SZ],
+    "emu_memcpy_dtoh": [P, P, P, SZ],
+    "emu_memcpy_dtod": [P, P, P, SZ],
+    "emu_memset": [P, P, I, SZ],
+    "emu_event_record": [P, I],
+    "emu_event_elapsed": [P, I, I, FP],
+    "emu_block_layout": [I, C.POINTER(U32), C.POINTER(U32)],
+    "emu_dequant": [P, I, P, SZ, P],
+    "emu_qmatvec": [P, I, P, SZ, U32, U32, P, SZ, U32, P, U32],
+    "emu_qmatvec_fused": [P, I, P, P, U32, U32, P, U32, P, F, P, U32],
+    "emu_quantize_act": [P, P, U32, U32, P, P],
+    "emu_block_dots": [P, I, P, SZ, U32, U32, P, U32, P],
+    "emu_qmatvec_i8": [P, I, P, SZ, U32, U32, P, P, U32, P],
+    "emu_rms_norm": [P, P, P, U32, U32, F, P],
+    "emu_rope_table": [P, U32, U32, F, P],
+    "emu_rope": [P, P, U32, U32, U32, P, P, U32, I],
+    "emu_attend_cached": [P, P, P, P, I, U32, U32, U32, U32, F, P],
+    "emu_route": [P, P, U32, U32, U32, P, P],
+    "emu_argmax": [P, P, U32, U32, I, P],
+    "emu_model_create": [P, C.POINTER(ModelConfig), C.POINTER(P)],
+    "emu_model_destroy": [P],
+    "emu_model_tensor": [P, I, U32, C.POINTER(P), C.POINTER(SZ)],
+    "emu_model_synth": [P, C.c_uint64],
+    "emu_model_weight_bytes": [P, C.POINTER(C.c_uint64)],
+    "emu_session_create": [P, U32, U32, I, C.POINTER(P)],
+    "emu_session_destroy": [P],
+    "emu_session_reset": [P],
+    "emu_decode_step": [P, P, P, P],
+    "emu_generate": [P, P, U32, U32, P],
+    "emu_time_decode": [P, U32, FP],
+    "emu_session_positions": [P, P],
+    "emu_session_read_kv": [P, U32, U32, I, P, U32],
+}
+_RESTYPE = {"emu_strerror": C.c_char_p, "emu_last_error": C.c_char_p}
+
+_lib = None
+
+
+def load() -> C.CDLL:
+    """Load libemuhip.so (built by ``python -m emufpga_amd.build``)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python -m emufpga_amd.build` "
+            "(the HIP library is the only implementation; there is no fallback)")
+    lib = C.CDLL(str(LIB_PATH))
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = _RESTYPE.get(name, C.c_int)
+    _lib = lib
+    return lib
+
+
+def strerror(status: int) -> str:
+    return load().emu_strerror(status).decode()
+
+
+def check(status: int, what: str, ctx=None) -> None:
+    if status == EMU_OK:
+        return
+    detail = ""
+    if ctx is not None:
+        try:
+            detail = load().emu_last_error(ctx).decode()
+        except Exception:  # pragma: no cover - diagnostic only
+            detail = ""
+    raise _ERRORS.get(status, EmuError)(status, what, detail)

@@ -1,0 +1,310 @@
+// internal.hpp -- shared host/device definitions of libemuhip.
+//
+// Quantized formats are read through one abstraction: a *unit* is the
+// 32-weight slice of a GGUF block that one lane owns.  A unit is G groups of 8
+// consecutive columns; for each group the lane holds 8 unsigned codes (two
+// packed dwords), a multiplier and an addend, and weight i of the group is
+//     w = fma(code_i, mul, add)
+// which is exact: every format's weight is d*sc*q (exact in f32) minus an
+// exact d_min*m term, so the single rounding of the fma is the single rounding
+// the reference performs (components/cli/crates/spm-gguf/src/tensor.rs:103-210).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/emuhip.h"
+
+#define EMU_WAVE 64
+
+struct emu_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t events[16] = {};
+    int cus = 0;
+    char arch[64] = {0};
+    char last_error[256] = {0};
+};
+
+int emu_hip_fail(emu_ctx *ctx, hipError_t e, const char *what);
+
+#define EMU_HIP(ctx, call)                                                   \
+    do {                                                                     \
+        hipError_t emu_e_ = (call);                                          \
+        if (emu_e_ != hipSuccess) return emu_hip_fail((ctx), emu_e_, #call); \
+    } while (0)
+
+#define EMU_LAUNCH_CHECK(ctx) EMU_HIP(ctx, hipGetLastError())
+
+// ---------------------------------------------------------------- device --
+
+__device__ __forceinline__ uint2 ld8(const uint8_t *p)
+{
+    uint2 v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
+}
+__device__ __forceinline__ uint4 ld16(const uint8_t *p)
+{
+    uint4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
+}
+__device__ __forceinline__ uint32_t ld4(const uint8_t *p)
+{
+    uint32_t v;
+    __builtin_memcpy(&v, p, 4);
+    return v;
+}
+__device__ __forceinline__ uint16_t ld2(const uint8_t *p)
+{
+    uint16_t v;
+    __builtin_memcpy(&v, p, 2);
+    return v;
+}
+
+// f16 -> f32 is exact (hardware conversion handles subnormal halves), the same
+// value as f16_to_f32 of spm-gguf/src/tensor.rs:82-98.
+__device__ __forceinline__ float h2f(uint16_t bits)
+{
+    return __half2float(__ushort_as_half(bits));
+}
+
+// Byte i of w as a float: the backend selects v_cvt_f32_ubyte{0..3}.
+__device__ __forceinline__ float byte_f(uint32_t w, int i)
+{
+    return (float)((w >> (8 * i)) & 0xffu);
+}
+
+// Byte k (0..7) of an 8-byte pair.
+__device__ __forceinline__ uint32_t byte_of(uint2 v, int k)
+{
+    uint32_t w = k < 4 ? v.x : v.y;
+    return (w >> (8 * (k & 3))) & 0xffu;
+}
+
+// One decoded group: 8 unsigned codes (two packed dwords) and the group's
+// multiplier / addend.  Weight i of the group is fma(code_i, mul, add).
+struct Grp {
+    uint32_t q0, q1;
+    float mul, add;
+};
+
+// Exact weight i (0..7) of a group.
+__device__ __forceinline__ float grp_weight(const Grp &g, int i)
+{
+    return __builtin_fmaf(byte_f(i < 4 ? g.q0 : g.q1, i & 3), g.mul, g.add);
+}
+
+// Code i (0..7) of a group minus the format's bias: the signed integer the
+// format multiplies by its sub-block scale.
+template <int BIAS> __device__ __forceinline__ int grp_code(const Grp &g, int i)
+{
+    return (int)(((i < 4 ? g.q0 : g.q1) >> (8 * (i & 3))) & 0xffu) - BIAS;
+}
+
+// ---- Q6_K: 210-byte blocks, 256 weights (spm-gguf/src/tensor.rs:103-139) --
+// Unit (h, l8): h = half (0/1), l8 = 0..3 picks l in [8*l8, 8*l8+8).
+// Group j (0..3) covers elements 128h + 32j + 8*l8 + i with code
+//   j0: ql[l] & 15 | (qh[l] & 3) << 4        j1: ql[l+32] & 15 | (qh[l]>>2 & 3) << 4
+//   j2: ql[l] >> 4 | (qh[l]>>4 & 3) << 4     j3: ql[l+32] >> 4 | (qh[l]>>6 & 3) << 4
+// and scale sc[8h + l/16 + 2j]; weight = d*sc*(q-32) = fma(q, d*sc, -32*d*sc).
+struct FmtQ6K {
+    static constexpr int BB = 210, BE = 256, UPB = 8, G = 4, SUB = 16, BIAS = 32;
+    struct Raw {
+        uint2 a, b, c, s;
+        uint32_t d;
+    };
+    __device__ __forceinline__ static void load(const uint8_t *blk, int sub, Raw &r)
+    {
+        const int h = sub >> 2, l8 = sub & 3;
+        r.a = ld8(blk + 64 * h + 8 * l8);
+        r.b = ld8(blk + 64 * h + 32 + 8 * l8);
+        r.c = ld8(blk + 128 + 32 * h + 8 * l8);
+        r.s = ld8(blk + 192 + 8 * h);
+        r.d = ld2(blk + 208);
+    }
+    __device__ __forceinline__ static int col(int sub, int g)
+    {
+        return 128 * (sub >> 2) + 32 * g + 8 * (sub & 3);
+    }
+    __device__ __forceinline__ static Grp group(const Raw &r, int sub, int j)
+    {
+        const uint32_t lo = 0x0f0f0f0fu, hi = 0x30303030u;
+        const uint2 src = (j & 1) ? r.b : r.a;
+        const int ns = 4 * (j >> 1);
+        const uint32_t h0 = j < 2 ? (r.c.x << (4 - 2 * j)) : (r.c.x >> (2 * j - 4));
+        const uint32_t h1 = j < 2 ? (r.c.y << (4 - 2 * j)) : (r.c.y >> (2 * j - 4));
+        Grp g;
+        g.q0 = ((src.x >> ns) & lo) | (h0 & hi);
+        g.q1 = ((src.y >> ns) & lo) | (h1 & hi);
+        const float d = h2f((uint16_t)r.d);
+        const float sc = (float)(int8_t)byte_of(r.s, ((sub & 3) >> 1) + 2 * j);
+        g.mul = d * sc;
+        g.add = -32.0f * g.mul;
+        return g;
+    }
+};
+
+// ---- Q8_0: 34-byte blocks, 32 weights (spm-gguf/src/tensor.rs:193-210) ----
+// Unit (half): 16 weights, 2 groups of 8.  Codes are the int8 values with the
+// sign bit flipped (i8 + 128 as u8); weight = d*i8 = fma(u8, d, -128*d).
+struct FmtQ8_0 {
+    static constexpr int BB = 34, BE = 32, UPB = 2, G = 2, SUB = 32, BIAS = 128;
+    struct Raw {
+        uint4 v;
+        uint32_t d;
+    };
+    __device__ __forceinline__ static void load(const uint8_t *blk, int sub, Raw &r)
+    {
+        r.v = ld16(blk + 2 + 16 * sub);
+        r.d = ld2(blk);
+    }
+    __device__ __forceinline__ static int col(int sub, int g) { return 16 * sub + 8 * g; }
+    __device__ __forceinline__ static Grp group(const Raw &r, int, int gi)
+    {
+        const uint32_t f = 0x80808080u;
+        Grp g;
+        g.q0 = (gi ? r.v.z : r.v.x) ^ f;
+        g.q1 = (gi ? r.v.w : r.v.y) ^ f;
+        g.mul = h2f((uint16_t)r.d);
+        g.add = -128.0f * g.mul;
+        return g;
+    }
+};
+
+// ---- Q5_K: 176-byte blocks, 256 weights (spm-gguf/src/tensor.rs:144-188) --
+// Element 64g + 32*half + l: low = qs[32g+l] nibble `half`, high bit
+// qh[l] >> (2g+half), scale/min from scale_min_q5(2g+half).
+// Unit (g, l16): l in [16*l16, 16*l16+16), both halves: 32 weights, groups
+// gi = 2*half + k for k = 0,1 covering l = 16*l16 + 8k + i.
+// weight = d*sc*q - dmin*m = fma(q, d*sc, -(dmin*m)), one rounding.
+struct FmtQ5K {
+    static constexpr int BB = 176, BE = 256, UPB = 8, G = 4, SUB = 32, BIAS = 0;
+    struct Raw {
+        uint4 qs, qh;
+        uint32_t s0, s1, s2, dd;
+    };
+    __device__ __forceinline__ static void load(const uint8_t *blk, int sub, Raw &r)
+    {
+        const int g = sub >> 1, l16 = sub & 1;
+        r.qs = ld16(blk + 48 + 32 * g + 16 * l16);
+        r.qh = ld16(blk + 16 + 16 * l16);
+        r.dd = ld4(blk);
+        r.s0 = ld4(blk + 4);
+        r.s1 = ld4(blk + 8);
+        r.s2 = ld4(blk + 12);
+    }
+    __device__ __forceinline__ static int col(int sub, int gi)
+    {
+        return 64 * (sub >> 1) + 32 * (gi >> 1) + 16 * (sub & 1) + 8 * (gi & 1);
+    }
+    // scale_min_q5 (spm-gguf/src/tensor.rs:179-188) over the 12 packed bytes.
+    __device__ __forceinline__ static void scale_min(const Raw &r, int index, uint32_t &sc,
+                                                     uint32_t &m)
+    {
+        const uint32_t s[3] = {r.s0, r.s1, r.s2};
+        auto byte = [&](int i) -> uint32_t { return (s[i >> 2] >> (8 * (i & 3))) & 0xffu; };
+        if (index < 4) {
+            sc = byte(index) & 63u;
+            m = byte(index + 4) & 63u;
+        } else {
+            sc = (byte(index + 4) & 0x0fu) | ((byte(index - 4) >> 6) << 4);
+            m = (byte(index + 4) >> 4) | ((byte(index) >> 6) << 4);
+        }
+    }
+    __device__ __forceinline__ static Grp group(const Raw &r, int sub, int gi)
+    {
+        const int half = gi >> 1, k = gi & 1;
+        const int index = 2 * (sub >> 1) + half;
+        const uint32_t w0 = k ? r.qs.z : r.qs.x, w1 = k ? r.qs.w : r.qs.y;
+        const uint32_t h0 = k ? r.qh.z : r.qh.x, h1 = k ? r.qh.w : r.qh.y;
+        const uint32_t lo = 0x0f0f0f0fu;
+        Grp g;
+        g.q0 = (half ? ((w0 >> 4) & lo) : (w0 & lo)) | (((h0 >> index) & 0x01010101u) << 4);
+        g.q1 = (half ? ((w1 >> 4) & lo) : (w1 & lo)) | (((h1 >> index) & 0x01010101u) << 4);
+        uint32_t sc, m;
+        scale_min(r, index, sc, m);
+        g.mul = h2f((uint16_t)(r.dd & 0xffffu)) * (float)sc;
+        g.add = -(h2f((uint16_t)(r.dd >> 16)) * (float)m);
+        return g;
+    }
+};
+
+// ---- Q2_K: 84-byte blocks, 256 weights (published GGML block_q2_K) --------
+// Element 128N + 32j + 16s + l: code (qs[32N+16s+l] >> 2j) & 3, scale byte
+// sc[8N+2j+s] (low nibble scale, high nibble min), d at 80, dmin at 82.
+// Unit (N, s, l8): 8 bytes qs[32N+16s+8*l8 ..], group j = 0..3.
+// weight = d*(sc&15)*code - dmin*(sc>>4) = fma(code, d*(sc&15), -(dmin*(sc>>4))).
+struct FmtQ2K {
+    static constexpr int BB = 84, BE = 256, UPB = 8, G = 4, SUB = 16, BIAS = 0;
+    struct Raw {
+        uint2 qs, sc;
+        uint32_t dd;
+    };
+    __device__ __forceinline__ static void load(const uint8_t *blk, int sub, Raw &r)
+    {
+        const int N = sub >> 2, s = (sub >> 1) & 1, l8 = sub & 1;
+        r.qs = ld8(blk + 16 + 32 * N + 16 * s + 8 * l8);
+        r.sc = ld8(blk + 8 * N);
+        r.dd = ld4(blk + 80);
+    }
+    __device__ __forceinline__ static int col(int sub, int j)
+    {
+        return 128 * (sub >> 2) + 32 * j + 16 * ((sub >> 1) & 1) + 8 * (sub & 1);
+    }
+    __device__ __forceinline__ static Grp group(const Raw &r, int sub, int j)
+    {
+        Grp g;
+        g.q0 = (r.qs.x >> (2 * j)) & 0x03030303u;
+        g.q1 = (r.qs.y >> (2 * j)) & 0x03030303u;
+        const uint32_t packed = byte_of(r.sc, 2 * j + ((sub >> 1) & 1));
+        g.mul = h2f((uint16_t)(r.dd & 0xffffu)) * (float)(packed & 15u);
+        g.add = -(h2f((uint16_t)(r.dd >> 16)) * (float)(packed >> 4));
+        return g;
+    }
+};
+
+// ------------------------------------------------------------ reductions --
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, EMU_WAVE);
+    return v;
+}
+
+// ------------------------------------------------------------- launchers --
+// Implemented per translation unit; declared here for the model code.
+struct QmvArgs {
+    const uint8_t *w;      // rows x row_bytes
+    const uint8_t *w_up;   // SwiGLU partner matrix or null
+    size_t row_bytes;
+    int rows, cols, nb;    // nb = blocks per row
+    const float *x;        // n_tok x cols
+    const float *gain;     // RMS gain or null
+    float eps;
+    float *y;              // n_tok x rows
+    int accumulate;
+};
+
+int emu_launch_qmv(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok);
+int emu_row_bytes(int encoding, uint32_t cols, size_t *row_bytes);
+
+// Fused decode attention of one layer for every client (attn.hip).
+struct EmuAttnLaunch {
+    const float *qkv;
+    void *k_cache, *v_cache;
+    const uint32_t *positions;
+    const float *rope;
+    const float *q_norm, *k_norm;
+    float eps, score_mul, score_div;
+    int rope_fma, heads, kv_heads, head_dim, layers, layer, context, clients, kv_f16;
+    float *partial;
+    uint32_t *counters;
+    float *out;
+};
+int emu_launch_attn(emu_ctx *ctx, const EmuAttnLaunch &l);
+int emu_attn_max_chunks(int context);

@@ -1,0 +1,798 @@
+// model.hip -- dense decoder resident in HBM, client sessions, and the
+// decode step (serve API: spm-batch/src/step.rs:19-39).
+//
+// HBM residency: one allocation per model.  Each layer's seven matrices sit
+// back to back in the reference's consume order q, k, v, o, gate, up, down
+// (layouts/smollm2-135m.order:3-8), each as GGUF row-major blocks, so q|k|v
+// is one (q_width + 2*kv_width) x hidden matrix and gate|up a pair of
+// equal-shaped matrices.  Then the embedding, the output matrix (unless
+// tied) and the f32 norm gains.
+//
+// One decode step is a fixed launch sequence that reads every input from
+// device memory (tokens, positions), so it is captured once into a HIP graph
+// and replayed per step:
+//   embed -> per layer { qkv matvec (RMSNorm fused) -> attention (QK-norm,
+//   RoPE, KV append, split-context softmax) -> o matvec (+residual) ->
+//   gate|up matvec (RMSNorm + SwiGLU fused) -> down matvec (+residual) }
+//   -> output matvec (final RMSNorm fused) -> greedy select + advance.
+#include "internal.hpp"
+
+#include <math.h>
+#include <string.h>
+#include <vector>
+
+int emu_build_rope_table(uint32_t positions, uint32_t head_dim, float theta, int fma_form,
+                         std::vector<float> &table);
+
+namespace {
+
+constexpr int kThreads = 256;
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+} // namespace
+
+struct emu_model {
+    emu_ctx *ctx = nullptr;
+    emu_model_config cfg{};
+    uint8_t *base = nullptr;
+    size_t total = 0;
+    size_t rb_h = 0, rb_q = 0, rb_f = 0; // row bytes for cols = hidden, q_width, ffn
+    size_t layer_bytes = 0;
+    size_t off_q = 0, off_k = 0, off_v = 0, off_o = 0, off_g = 0, off_u = 0, off_d = 0;
+    size_t off_layers = 0, off_embed = 0, off_output = 0, off_attn_norm = 0, off_ffn_norm = 0,
+           off_q_norm = 0, off_k_norm = 0, off_out_norm = 0;
+    size_t embed_bytes = 0;
+};
+
+struct emu_session {
+    emu_model *m = nullptr;
+    uint32_t n = 0, context = 0;
+    int kv_f16 = 1;
+    void *k_cache = nullptr, *v_cache = nullptr;
+    size_t kv_bytes = 0;
+    uint32_t *positions = nullptr, *tokens = nullptr, *steps = nullptr, *prompt = nullptr,
+             *hist = nullptr, *ctrl = nullptr, *last = nullptr, *counters = nullptr;
+    float *state = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr,
+          *partial = nullptr, *rope = nullptr;
+    std::vector<uint32_t> host_pos;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace {
+
+// ------------------------------------------------------------ synthesis --
+// Counter-based N(0, std): splitmix64 of (seed, stream, element) -> Box-Muller.
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z)
+{
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ float gauss(uint64_t seed, uint64_t stream, uint64_t idx, float sd)
+{
+    const uint64_t h = splitmix64(seed ^ splitmix64(stream * 0x632be59bd9b4e019ull + idx));
+    const float u1 = (float)((h >> 40) + 1) * (1.0f / 16777216.0f); // (0, 1]
+    const float u2 = (float)(h & 0xffffffu) * (1.0f / 16777216.0f); // [0, 1)
+    return sd * sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+}
+
+__device__ __forceinline__ uint16_t f2h(float x) { return __half_as_ushort(__float2half_rn(x)); }
+
+__device__ __forceinline__ float clampf(float v, float lo, float hi) { return fminf(fmaxf(v, lo), hi); }
+
+// One thread per block; the block is assembled in private memory then stored.
+template <int ENC>
+__global__ __launch_bounds__(kThreads) void synth_kernel(uint8_t *dst, size_t nblocks, uint64_t seed,
+                                                         uint64_t stream, float sd)
+{
+    const size_t b = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    if (b >= nblocks) return;
+    if constexpr (ENC == EMU_ENC_Q8_0) {
+        uint8_t out[34];
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(gauss(seed, stream, b * 32 + i, sd)));
+        const uint16_t d16 = f2h(amax / 127.0f);
+        const float dd = h2f(d16);
+        out[0] = (uint8_t)d16;
+        out[1] = (uint8_t)(d16 >> 8);
+        for (int i = 0; i < 32; ++i) {
+            const float v = gauss(seed, stream, b * 32 + i, sd);
+            const float q = dd > 0.0f ? clampf(rintf(v / dd), -127.0f, 127.0f) : 0.0f;
+            out[2 + i] = (uint8_t)(int8_t)q;
+        }
+        for (int i = 0; i < 34; ++i) dst[b * 34 + i] = out[i];
+    } else if constexpr (ENC == EMU_ENC_Q6_K) {
+        uint8_t out[210];
+        for (int i = 0; i < 210; ++i) out[i] = 0;
+        float scale[16];
+        float mx = 0.0f;
+        for (int s = 0; s < 16; ++s) {
+            float amax = 0.0f;
+            for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(gauss(seed, stream, b * 256 + s * 16 + i, sd)));
+            scale[s] = amax / 31.0f;
+            mx = fmaxf(mx, scale[s]);
+        }
+        const uint16_t d16 = f2h(mx / 127.0f);
+        const float dd = h2f(d16);
+        int sc[16];
+        for (int s = 0; s < 16; ++s) {
+            sc[s] = dd > 0.0f ? (int)clampf(rintf(scale[s] / dd), -128.0f, 127.0f) : 0;
+            out[192 + s] = (uint8_t)(int8_t)sc[s];
+        }
+        out[208] = (uint8_t)d16;
+        out[209] = (uint8_t)(d16 >> 8);
+        for (int e = 0; e < 256; ++e) {
+            const float v = gauss(seed, stream, b * 256 + e, sd);
+            const float m = dd * (float)sc[e / 16];
+            const int q = m > 0.0f ? (int)clampf(rintf(v / m) + 32.0f, 0.0f, 63.0f) : 32;
+            const int h = e / 128, r = e % 128, j = r / 32, l = r % 32;
+            out[64 * h + l + 32 * (j & 1)] |= (uint8_t)((q & 15) << (4 * (j >> 1)));
+            out[128 + 32 * h + l] |= (uint8_t)((q >> 4) << (2 * j));
+        }
+        for (int i = 0; i < 210; ++i) dst[b * 210 + i] = out[i];
+    } else if constexpr (ENC == EMU_ENC_Q5_K) {
+        uint8_t out[176];
+        for (int i = 0; i < 176; ++i) out[i] = 0;
+        float scale[8], mneg[8];
+        float ms = 0.0f, mm = 0.0f;
+        for (int s = 0; s < 8; ++s) {
+            float lo = 0.0f, hi = -INFINITY;
+            for (int i = 0; i < 32; ++i) {
+                const float v = gauss(seed, stream, b * 256 + s * 32 + i, sd);
+                lo = fminf(lo, v);
+                hi = fmaxf(hi, v);
+            }
+            scale[s] = (hi - lo) / 31.0f;
+            mneg[s] = -lo;
+            ms = fmaxf(ms, scale[s]);
+            mm = fmaxf(mm, mneg[s]);
+        }
+        const uint16_t d16 = f2h(ms / 63.0f), m16 = f2h(mm / 63.0f);
+        const float dd = h2f(d16), dm = h2f(m16);
+        int sc[8], mi[8];
+        for (int s = 0; s < 8; ++s) {
+            sc[s] = dd > 0.0f ? (int)clampf(rintf(scale[s] / dd), 0.0f, 63.0f) : 0;
+            mi[s] = dm > 0.0f ? (int)clampf(rintf(mneg[s] / dm), 0.0f, 63.0f) : 0;
+        }
+        out[0] = (uint8_t)d16;
+        out[1] = (uint8_t)(d16 >> 8);
+        out[2] = (uint8_t)m16;
+        out[3] = (uint8_t)(m16 >> 8);
+        uint8_t *packed = out + 4;
+        for (int j = 0; j < 4; ++j) {
+            packed[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+            packed[j + 4] = (uint8_t)((mi[j] & 63) | ((mi[j + 4] >> 4) << 6));
+            packed[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((mi[j + 4] & 15) << 4));
+        }
+        for (int e = 0; e < 256; ++e) {
+            const int s = e / 32, g = e / 64, half = (e / 32) & 1, l = e % 32;
+            const float v = gauss(seed, stream, b * 256 + e, sd);
+            const float scl = dd * (float)sc[s];
+            const int q = scl > 0.0f ? (int)clampf(rintf((v + dm * (float)mi[s]) / scl), 0.0f, 31.0f) : 0;
+            out[48 + 32 * g + l] |= (uint8_t)((q & 15) << (4 * half));
+            out[16 + l] |= (uint8_t)((q >> 4) << (2 * g + half));
+        }
+        for (int i = 0; i < 176; ++i) dst[b * 176 + i] = out[i];
+    } else { // Q2_K
+        uint8_t out[84];
+        for (int i = 0; i < 84; ++i) out[i] = 0;
+        float scale[16], mneg[16];
+        float ms = 0.0f, mm = 0.0f;
+        for (int s = 0; s < 16; ++s) {
+            float lo = 0.0f, hi = -INFINITY;
+            for (int i = 0; i < 16; ++i) {
+                const float v = gauss(seed, stream, b * 256 + s * 16 + i, sd);
+                lo = fminf(lo, v);
+                hi = fmaxf(hi, v);
+            }
+            scale[s] = (hi - lo) / 3.0f;
+            mneg[s] = -lo;
+            ms = fmaxf(ms, scale[s]);
+            mm = fmaxf(mm, mneg[s]);
+        }
+        const uint16_t d16 = f2h(ms / 15.0f), m16 = f2h(mm / 15.0f);
+        const float dd = h2f(d16), dm = h2f(m16);
+        int sc[16], mi[16];
+        for (int s = 0; s < 16; ++s) {
+            sc[s] = dd > 0.0f ? (int)clampf(rintf(scale[s] / dd), 0.0f, 15.0f) : 0;
+            mi[s] = dm > 0.0f ? (int)clampf(rintf(mneg[s] / dm), 0.0f, 15.0f) : 0;
+            out[s] = (uint8_t)(sc[s] | (mi[s] << 4));
+        }
+        out[80] = (uint8_t)d16;
+        out[81] = (uint8_t)(d16 >> 8);
+        out[82] = (uint8_t)m16;
+        out[83] = (uint8_t)(m16 >> 8);
+        for (int e = 0; e < 256; ++e) {
+            const int N = e / 128, j = (e / 32) & 3, s = (e / 16) & 1, l = e % 16;
+            const int si = e / 16;
+            const float v = gauss(seed, stream, b * 256 + e, sd);
+            const float scl = dd * (float)sc[si];
+            const int q = scl > 0.0f ? (int)clampf(rintf((v + dm * (float)mi[si]) / scl), 0.0f, 3.0f) : 0;
+            out[16 + 32 * N + 16 * s + l] |= (uint8_t)(q << (2 * j));
+        }
+        for (int i = 0; i < 84; ++i) dst[b * 84 + i] = out[i];
+    }
+}
+
+__global__ void fill_kernel(float *p, size_t n, float v)
+{
+    const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+int synth_tensor(emu_ctx *ctx, int enc, uint8_t *dst, size_t bytes, uint64_t seed, uint64_t stream)
+{
+    uint32_t be = 0, bb = 0;
+    int st = emu_block_layout(enc, &be, &bb);
+    if (st != EMU_OK) return st;
+    const size_t nblocks = bytes / bb;
+    if (nblocks == 0) return EMU_OK;
+    const dim3 grid((unsigned)((nblocks + kThreads - 1) / kThreads));
+    const float sd = 0.02f;
+    switch (enc) {
+    case EMU_ENC_Q8_0: hipLaunchKernelGGL(synth_kernel<EMU_ENC_Q8_0>, grid, dim3(kThreads), 0, ctx->stream, dst, nblocks, seed, stream, sd); break;
+    case EMU_ENC_Q6_K: hipLaunchKernelGGL(synth_kernel<EMU_ENC_Q6_K>, grid, dim3(kThreads), 0, ctx->stream, dst, nblocks, seed, stream, sd); break;
+    case EMU_ENC_Q5_K: hipLaunchKernelGGL(synth_kernel<EMU_ENC_Q5_K>, grid, dim3(kThreads), 0, ctx->stream, dst, nblocks, seed, stream, sd); break;
+    case EMU_ENC_Q2_K: hipLaunchKernelGGL(synth_kernel<EMU_ENC_Q2_K>, grid, dim3(kThreads), 0, ctx->stream, dst, nblocks, seed, stream, sd); break;
+    default: return EMU_E_UNSUPPORTED;
+    }
+    EMU_LAUNCH_CHECK(ctx);
+    return EMU_OK;
+}
+
+// --------------------------------------------------------- step kernels --
+// Embedding row of tokens[c]: a unit-per-thread decode of one row.
+template <class F>
+__global__ __launch_bounds__(kThreads) void embed_kernel(const uint8_t *embed, size_t row_bytes, int hidden,
+                                                         const uint32_t *tokens, float *state)
+{
+    const int c = blockIdx.y;
+    const int u = blockIdx.x * kThreads + threadIdx.x;
+    const int units = hidden / F::BE * F::UPB;
+    if (u >= units) return;
+    const int blk = u / F::UPB, sub = u % F::UPB;
+    const uint8_t *row = embed + (size_t)tokens[c] * row_bytes;
+    typename F::Raw raw;
+    F::load(row + (size_t)blk * F::BB, sub, raw);
+    float *out = state + (size_t)c * hidden + blk * F::BE;
+#pragma unroll
+    for (int g = 0; g < F::G; ++g) {
+        const Grp gp = F::group(raw, sub, g);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[F::col(sub, g) + i] = grp_weight(gp, i);
+    }
+}
+
+__device__ __forceinline__ uint32_t total_key_u(float f)
+{
+    int32_t i = __float_as_int(f);
+    i ^= (int32_t)(((uint32_t)(i >> 31)) >> 1);
+    return (uint32_t)i ^ 0x80000000u;
+}
+
+// Greedy select + advance, one workgroup per client.
+// ctrl[0] = prompt length (0: every step is a free-running decode step),
+// ctrl[1] = capacity of the generated-token history per client.
+__global__ __launch_bounds__(1024) void finalize_kernel(const float *logits, int vocab, int tie_last,
+                                                        const uint32_t *prompt, int prompt_stride,
+                                                        uint32_t *hist, const uint32_t *ctrl,
+                                                        uint32_t *tokens, uint32_t *positions,
+                                                        uint32_t *steps, uint32_t *last)
+{
+    __shared__ uint64_t red[16];
+    const int c = blockIdx.x;
+    const float *lr = logits + (size_t)c * vocab;
+    uint64_t best = 0;
+    for (int i = threadIdx.x; i < vocab; i += blockDim.x) {
+        float v = lr[i];
+        uint64_t k;
+        if (tie_last) {
+            if (v == 0.0f) v = 0.0f;
+            k = ((uint64_t)total_key_u(v) << 32) | (uint32_t)i;
+        } else {
+            k = ((uint64_t)total_key_u(v) << 32) | (0xffffffffu - (uint32_t)i);
+        }
+        best = k > best ? k : best;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint64_t o = __shfl_xor(best, off, 64);
+        best = o > best ? o : best;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (int i = 1; i < (int)(blockDim.x >> 6); ++i) best = red[i] > best ? red[i] : best;
+    const uint32_t lo = (uint32_t)best;
+    const uint32_t am = tie_last ? lo : 0xffffffffu - lo;
+    const uint32_t plen = ctrl[0], cap = ctrl[1];
+    const uint32_t s = steps[c];
+    uint32_t next = am;
+    if (s + 1 < plen) next = prompt[(size_t)c * prompt_stride + s + 1];
+    if (s + 1 >= plen) {
+        const uint32_t gi = s + 1 - plen;
+        if (gi < cap) hist[(size_t)c * cap + gi] = am;
+    }
+    tokens[c] = next;
+    last[c] = am;
+    positions[c] = positions[c] + 1;
+    steps[c] = s + 1;
+}
+
+template <class F>
+int launch_embed(emu_ctx *ctx, const emu_model *m, const uint32_t *tokens, float *state, uint32_t n)
+{
+    const int units = (int)(m->cfg.hidden / F::BE * F::UPB);
+    dim3 grid((units + kThreads - 1) / kThreads, n);
+    hipLaunchKernelGGL(embed_kernel<F>, grid, dim3(kThreads), 0, ctx->stream, m->base + m->off_embed,
+                       m->rb_h, (int)m->cfg.hidden, tokens, state);
+    EMU_LAUNCH_CHECK(ctx);
+    return EMU_OK;
+}
+
+int run_step(emu_session *s)
+{
+    emu_model *m = s->m;
+    emu_ctx *ctx = m->ctx;
+    const emu_model_config &c = m->cfg;
+    const uint32_t H = c.hidden, hd = c.head_dim, QW = c.heads * hd, KW = c.kv_heads * hd, F = c.ffn;
+    const int n = (int)s->n;
+    int st = EMU_OK;
+    switch (c.encoding) {
+    case EMU_ENC_Q6_K: st = launch_embed<FmtQ6K>(ctx, m, s->tokens, s->state, s->n); break;
+    case EMU_ENC_Q8_0: st = launch_embed<FmtQ8_0>(ctx, m, s->tokens, s->state, s->n); break;
+    case EMU_ENC_Q5_K: st = launch_embed<FmtQ5K>(ctx, m, s->tokens, s->state, s->n); break;
+    case EMU_ENC_Q2_K: st = launch_embed<FmtQ2K>(ctx, m, s->tokens, s->state, s->n); break;
+    default: return EMU_E_UNSUPPORTED;
+    }
+    if (st != EMU_OK) return st;
+    uint32_t be = 0, bb = 0;
+    emu_block_layout(c.encoding, &be, &bb);
+    const int smol = c.style == EMU_STYLE_SMOL;
+    for (uint32_t layer = 0; layer < c.layers; ++layer) {
+        const uint8_t *lw = m->base + m->off_layers + (size_t)layer * m->layer_bytes;
+        QmvArgs a{};
+        // q|k|v with the attention RMSNorm fused.
+        a.w = lw + m->off_q;
+        a.row_bytes = m->rb_h;
+        a.rows = (int)(QW + 2 * KW);
+        a.cols = (int)H;
+        a.nb = (int)(H / be);
+        a.x = s->state;
+        a.gain = reinterpret_cast<const float *>(m->base + m->off_attn_norm) + (size_t)layer * H;
+        a.eps = c.eps;
+        a.y = s->qkv;
+        if ((st = emu_launch_qmv(ctx, c.encoding, a, n)) != EMU_OK) return st;
+        EmuAttnLaunch al{};
+        al.qkv = s->qkv;
+        al.k_cache = s->k_cache;
+        al.v_cache = s->v_cache;
+        al.positions = s->positions;
+        al.rope = s->rope;
+        al.q_norm = c.qk_norm ? reinterpret_cast<const float *>(m->base + m->off_q_norm) : nullptr;
+        al.k_norm = c.qk_norm ? reinterpret_cast<const float *>(m->base + m->off_k_norm) : nullptr;
+        al.eps = c.eps;
+        al.score_mul = smol ? 1.0f / sqrtf((float)hd) : 0.0f;
+        al.score_div = smol ? 0.0f : sqrtf((float)hd);
+        al.rope_fma = smol;
+        al.heads = (int)c.heads;
+        al.kv_heads = (int)c.kv_heads;
+        al.head_dim = (int)hd;
+        al.layers = (int)c.layers;
+        al.layer = (int)layer;
+        al.context = (int)s->context;
+        al.clients = n;
+        al.kv_f16 = s->kv_f16;
+        al.partial = s->partial;
+        al.counters = s->counters;
+        al.out = s->attn;
+        if ((st = emu_launch_attn(ctx, al)) != EMU_OK) return st;
+        // o projection + residual.
+        QmvArgs o{};
+        o.w = lw + m->off_o;
+        o.row_bytes = m->rb_q;
+        o.rows = (int)H;
+        o.cols = (int)QW;
+        o.nb = (int)(QW / be);
+        o.x = s->attn;
+        o.y = s->state;
+        o.accumulate = 1;
+        if ((st = emu_launch_qmv(ctx, c.encoding, o, n)) != EMU_OK) return st;
+        // gate|up with the FFN RMSNorm and SwiGLU fused.
+        QmvArgs g{};
+        g.w = lw + m->off_g;
+        g.w_up = lw + m->off_u;
+        g.row_bytes = m->rb_h;
+        g.rows = (int)F;
+        g.cols = (int)H;
+        g.nb = (int)(H / be);
+        g.x = s->state;
+        g.gain = reinterpret_cast<const float *>(m->base + m->off_ffn_norm) + (size_t)layer * H;
+        g.eps = c.eps;
+        g.y = s->act;
+        if ((st = emu_launch_qmv(ctx, c.encoding, g, n)) != EMU_OK) return st;
+        // down projection + residual.
+        QmvArgs d{};
+        d.w = lw + m->off_d;
+        d.row_bytes = m->rb_f;
+        d.rows = (int)H;
+        d.cols = (int)F;
+        d.nb = (int)(F / be);
+        d.x = s->act;
+        d.y = s->state;
+        d.accumulate = 1;
+        if ((st = emu_launch_qmv(ctx, c.encoding, d, n)) != EMU_OK) return st;
+    }
+    QmvArgs out{};
+    out.w = m->base + (c.tied ? m->off_embed : m->off_output);
+    out.row_bytes = m->rb_h;
+    out.rows = (int)c.vocab;
+    out.cols = (int)H;
+    out.nb = (int)(H / be);
+    out.x = s->state;
+    out.gain = reinterpret_cast<const float *>(m->base + m->off_out_norm);
+    out.eps = c.eps;
+    out.y = s->logits;
+    if ((st = emu_launch_qmv(ctx, c.encoding, out, n)) != EMU_OK) return st;
+    hipLaunchKernelGGL(finalize_kernel, dim3(s->n), dim3(1024), 0, ctx->stream, s->logits, (int)c.vocab,
+                       smol ? 1 : 0, s->prompt, (int)s->context, s->hist, s->ctrl, s->tokens, s->positions,
+                       s->steps, s->last);
+    EMU_LAUNCH_CHECK(ctx);
+    return EMU_OK;
+}
+
+int ensure_graph(emu_session *s)
+{
+    if (s->exec) return EMU_OK;
+    emu_ctx *ctx = s->m->ctx;
+    EMU_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    int st = run_step(s);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+    if (st != EMU_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return st;
+    }
+    if (e != hipSuccess) return emu_hip_fail(ctx, e, "hipStreamEndCapture");
+    e = hipGraphInstantiate(&s->exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return emu_hip_fail(ctx, e, "hipGraphInstantiate");
+    }
+    s->graph = g;
+    return EMU_OK;
+}
+
+int launch_steps(emu_session *s, uint32_t count)
+{
+    int st = ensure_graph(s);
+    if (st != EMU_OK) return st;
+    emu_ctx *ctx = s->m->ctx;
+    for (uint32_t i = 0; i < count; ++i) EMU_HIP(ctx, hipGraphLaunch(s->exec, ctx->stream));
+    for (auto &p : s->host_pos) p += count;
+    return EMU_OK;
+}
+
+int check_room(emu_session *s, uint64_t steps)
+{
+    for (uint32_t p : s->host_pos)
+        if ((uint64_t)p + steps > s->context) return EMU_E_CONTEXT_FULL;
+    return EMU_OK;
+}
+
+int set_ctrl(emu_session *s, uint32_t prompt_len, uint32_t cap)
+{
+    const uint32_t ctrl[2] = {prompt_len, cap};
+    return emu_memcpy_htod(s->m->ctx, s->ctrl, ctrl, sizeof ctrl);
+}
+
+} // namespace
+
+// ------------------------------------------------------------------ API --
+
+extern "C" int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_model **out)
+{
+    if (!ctx || !cfg || !out) return EMU_E_ARG;
+    *out = nullptr;
+    const emu_model_config &c = *cfg;
+    if (c.hidden == 0 || c.heads == 0 || c.kv_heads == 0 || c.head_dim == 0 || c.ffn == 0 || c.vocab == 0 ||
+        c.layers == 0)
+        return EMU_E_CONFIG;
+    if (c.heads % c.kv_heads != 0 || c.heads / c.kv_heads > 8) return EMU_E_CONFIG;
+    if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256) return EMU_E_CONFIG;
+    if (c.style != EMU_STYLE_QWEN3 && c.style != EMU_STYLE_SMOL) return EMU_E_CONFIG;
+    emu_model *m = new (std::nothrow) emu_model();
+    if (!m) return EMU_E_NOMEM;
+    m->ctx = ctx;
+    m->cfg = c;
+    const uint32_t QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim;
+    int st;
+    if ((st = emu_row_bytes(c.encoding, c.hidden, &m->rb_h)) != EMU_OK ||
+        (st = emu_row_bytes(c.encoding, QW, &m->rb_q)) != EMU_OK ||
+        (st = emu_row_bytes(c.encoding, c.ffn, &m->rb_f)) != EMU_OK) {
+        delete m;
+        return st == EMU_E_SHORT ? EMU_E_CONFIG : st;
+    }
+    m->off_q = 0;
+    m->off_k = m->off_q + (size_t)QW * m->rb_h;
+    m->off_v = m->off_k + (size_t)KW * m->rb_h;
+    m->off_o = m->off_v + (size_t)KW * m->rb_h;
+    m->off_g = m->off_o + (size_t)c.hidden * m->rb_q;
+    m->off_u = m->off_g + (size_t)c.ffn * m->rb_h;
+    m->off_d = m->off_u + (size_t)c.ffn * m->rb_h;
+    m->layer_bytes = m->off_d + (size_t)c.hidden * m->rb_f;
+    m->embed_bytes = (size_t)c.vocab * m->rb_h;
+    size_t off = 0;
+    m->off_layers = off;
+    off = align_up(off + m->layer_bytes * c.layers, 256);
+    m->off_embed = off;
+    off = align_up(off + m->embed_bytes, 256);
+    m->off_output = off;
+    if (!c.tied) off = align_up(off + m->embed_bytes, 256);
+    m->off_attn_norm = off;
+    off = align_up(off + sizeof(float) * c.layers * c.hidden, 256);
+    m->off_ffn_norm = off;
+    off = align_up(off + sizeof(float) * c.layers * c.hidden, 256);
+    m->off_q_norm = off;
+    off = align_up(off + sizeof(float) * c.layers * c.head_dim, 256);
+    m->off_k_norm = off;
+    off = align_up(off + sizeof(float) * c.layers * c.head_dim, 256);
+    m->off_out_norm = off;
+    off = align_up(off + sizeof(float) * c.hidden, 256);
+    m->total = off;
+    void *p = nullptr;
+    if ((st = emu_malloc(ctx, m->total, &p)) != EMU_OK) {
+        delete m;
+        return st;
+    }
+    m->base = static_cast<uint8_t *>(p);
+    *out = m;
+    return EMU_OK;
+}
+
+extern "C" int emu_model_destroy(emu_model *m)
+{
+    if (!m) return EMU_E_ARG;
+    emu_free(m->ctx, m->base);
+    delete m;
+    return EMU_OK;
+}
+
+extern "C" int emu_model_tensor(emu_model *m, int kind, uint32_t layer, void **d_ptr, size_t *bytes)
+{
+    if (!m || !d_ptr || !bytes) return EMU_E_ARG;
+    const emu_model_config &c = m->cfg;
+    if ((kind == EMU_T_LAYER) && layer >= c.layers) return EMU_E_ARG;
+    size_t off = 0, len = 0;
+    switch (kind) {
+    case EMU_T_LAYER: off = m->off_layers + (size_t)layer * m->layer_bytes; len = m->layer_bytes; break;
+    case EMU_T_EMBED: off = m->off_embed; len = m->embed_bytes; break;
+    case EMU_T_OUTPUT:
+        if (c.tied) return EMU_E_ARG;
+        off = m->off_output; len = m->embed_bytes; break;
+    case EMU_T_ATTN_NORM: off = m->off_attn_norm; len = sizeof(float) * c.layers * c.hidden; break;
+    case EMU_T_FFN_NORM: off = m->off_ffn_norm; len = sizeof(float) * c.layers * c.hidden; break;
+    case EMU_T_Q_NORM: off = m->off_q_norm; len = sizeof(float) * c.layers * c.head_dim; break;
+    case EMU_T_K_NORM: off = m->off_k_norm; len = sizeof(float) * c.layers * c.head_dim; break;
+    case EMU_T_OUT_NORM: off = m->off_out_norm; len = sizeof(float) * c.hidden; break;
+    default: return EMU_E_ARG;
+    }
+    *d_ptr = m->base + off;
+    *bytes = len;
+    return EMU_OK;
+}
+
+extern "C" int emu_model_synth(emu_model *m, uint64_t seed)
+{
+    if (!m) return EMU_E_ARG;
+    emu_ctx *ctx = m->ctx;
+    const emu_model_config &c = m->cfg;
+    const uint32_t QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim;
+    int st;
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        uint8_t *lw = m->base + m->off_layers + (size_t)l * m->layer_bytes;
+        const size_t sizes[7] = {(size_t)QW * m->rb_h, (size_t)KW * m->rb_h, (size_t)KW * m->rb_h,
+                                 (size_t)c.hidden * m->rb_q, (size_t)c.ffn * m->rb_h, (size_t)c.ffn * m->rb_h,
+                                 (size_t)c.hidden * m->rb_f};
+        const size_t offs[7] = {m->off_q, m->off_k, m->off_v, m->off_o, m->off_g, m->off_u, m->off_d};
+        for (int t = 0; t < 7; ++t)
+            if ((st = synth_tensor(ctx, c.encoding, lw + offs[t], sizes[t], seed, 16ull * (l + 1) + t)) != EMU_OK)
+                return st;
+    }
+    if ((st = synth_tensor(ctx, c.encoding, m->base + m->off_embed, m->embed_bytes, seed, 1)) != EMU_OK) return st;
+    if (!c.tied &&
+        (st = synth_tensor(ctx, c.encoding, m->base + m->off_output, m->embed_bytes, seed, 2)) != EMU_OK)
+        return st;
+    const size_t nf = (m->total - m->off_attn_norm) / sizeof(float);
+    hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((nf + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                       ctx->stream, reinterpret_cast<float *>(m->base + m->off_attn_norm), nf, 1.0f);
+    EMU_LAUNCH_CHECK(ctx);
+    return emu_ctx_sync(ctx);
+}
+
+extern "C" int emu_model_weight_bytes(const emu_model *m, uint64_t *bytes)
+{
+    if (!m || !bytes) return EMU_E_ARG;
+    *bytes = (uint64_t)m->layer_bytes * m->cfg.layers + m->embed_bytes;
+    return EMU_OK;
+}
+
+extern "C" int emu_session_create(emu_model *m, uint32_t n_clients, uint32_t context, int kv_f16,
+                                  emu_session **out)
+{
+    if (!m || !out || n_clients == 0 || n_clients > 8 || context == 0) return EMU_E_ARG;
+    if (context > 65536) return EMU_E_CONFIG; // positions fit u16 (spm-qwen3-slice/src/attention.rs:14-16)
+    *out = nullptr;
+    emu_ctx *ctx = m->ctx;
+    const emu_model_config &c = m->cfg;
+    emu_session *s = new (std::nothrow) emu_session();
+    if (!s) return EMU_E_NOMEM;
+    s->m = m;
+    s->n = n_clients;
+    s->context = context;
+    s->kv_f16 = kv_f16 ? 1 : 0;
+    s->host_pos.assign(n_clients, 0);
+    const uint32_t QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim;
+    s->kv_bytes = (size_t)n_clients * c.layers * KW * context * (s->kv_f16 ? 2 : 4);
+    const int chunks = emu_attn_max_chunks((int)context);
+    int st = EMU_OK;
+    auto alloc = [&](void **p, size_t bytes) {
+        if (st == EMU_OK) st = emu_malloc(ctx, bytes, p);
+    };
+    alloc(&s->k_cache, s->kv_bytes);
+    alloc(&s->v_cache, s->kv_bytes);
+    alloc((void **)&s->positions, sizeof(uint32_t) * n_clients);
+    alloc((void **)&s->tokens, sizeof(uint32_t) * n_clients);
+    alloc((void **)&s->steps, sizeof(uint32_t) * n_clients);
+    alloc((void **)&s->last, sizeof(uint32_t) * n_clients);
+    alloc((void **)&s->prompt, sizeof(uint32_t) * n_clients * context);
+    alloc((void **)&s->hist, sizeof(uint32_t) * n_clients * context);
+    alloc((void **)&s->ctrl, sizeof(uint32_t) * 4);
+    alloc((void **)&s->counters, sizeof(uint32_t) * n_clients * c.kv_heads);
+    alloc((void **)&s->state, sizeof(float) * n_clients * c.hidden);
+    alloc((void **)&s->qkv, sizeof(float) * n_clients * (QW + 2 * KW));
+    alloc((void **)&s->attn, sizeof(float) * n_clients * QW);
+    alloc((void **)&s->act, sizeof(float) * n_clients * c.ffn);
+    alloc((void **)&s->logits, sizeof(float) * n_clients * c.vocab);
+    alloc((void **)&s->partial, sizeof(float) * n_clients * c.heads * chunks * (c.head_dim + 2));
+    alloc((void **)&s->rope, sizeof(float) * (size_t)context * c.head_dim);
+    if (st == EMU_OK) {
+        std::vector<float> table;
+        emu_build_rope_table(context, c.head_dim, c.rope_theta, c.style == EMU_STYLE_SMOL, table);
+        st = emu_memcpy_htod(ctx, s->rope, table.data(), table.size() * sizeof(float));
+    }
+    if (st == EMU_OK) st = emu_memset(ctx, s->counters, 0, sizeof(uint32_t) * n_clients * c.kv_heads);
+    if (st == EMU_OK) st = emu_session_reset(s);
+    if (st != EMU_OK) {
+        emu_session_destroy(s);
+        return st;
+    }
+    *out = s;
+    return EMU_OK;
+}
+
+extern "C" int emu_session_destroy(emu_session *s)
+{
+    if (!s) return EMU_E_ARG;
+    emu_ctx *ctx = s->m->ctx;
+    if (s->exec) (void)hipGraphExecDestroy(s->exec);
+    if (s->graph) (void)hipGraphDestroy(s->graph);
+    void *ptrs[] = {s->k_cache, s->v_cache, s->positions, s->tokens, s->steps, s->last, s->prompt, s->hist,
+                    s->ctrl, s->counters, s->state, s->qkv, s->attn, s->act, s->logits, s->partial, s->rope};
+    for (void *p : ptrs) emu_free(ctx, p);
+    delete s;
+    return EMU_OK;
+}
+
+extern "C" int emu_session_reset(emu_session *s)
+{
+    if (!s) return EMU_E_ARG;
+    emu_ctx *ctx = s->m->ctx;
+    int st;
+    if ((st = emu_memset(ctx, s->positions, 0, sizeof(uint32_t) * s->n)) != EMU_OK) return st;
+    if ((st = emu_memset(ctx, s->steps, 0, sizeof(uint32_t) * s->n)) != EMU_OK) return st;
+    if ((st = emu_memset(ctx, s->k_cache, 0, s->kv_bytes)) != EMU_OK) return st;
+    if ((st = emu_memset(ctx, s->v_cache, 0, s->kv_bytes)) != EMU_OK) return st;
+    for (auto &p : s->host_pos) p = 0;
+    return emu_ctx_sync(ctx);
+}
+
+extern "C" int emu_decode_step(emu_session *s, const uint32_t *h_tokens, uint32_t *h_next, float *d_logits)
+{
+    if (!s || !h_tokens) return EMU_E_ARG;
+    for (uint32_t i = 0; i < s->n; ++i)
+        if (h_tokens[i] >= s->m->cfg.vocab) return EMU_E_ARG;
+    int st = check_room(s, 1);
+    if (st != EMU_OK) return st;
+    emu_ctx *ctx = s->m->ctx;
+    if ((st = emu_memcpy_htod(ctx, s->tokens, h_tokens, sizeof(uint32_t) * s->n)) != EMU_OK) return st;
+    if ((st = set_ctrl(s, 0, 0)) != EMU_OK) return st;
+    if ((st = launch_steps(s, 1)) != EMU_OK) return st;
+    if (d_logits &&
+        (st = emu_memcpy_dtod(ctx, d_logits, s->logits, sizeof(float) * s->n * s->m->cfg.vocab)) != EMU_OK)
+        return st;
+    if (h_next) return emu_memcpy_dtoh(ctx, h_next, s->last, sizeof(uint32_t) * s->n);
+    return emu_ctx_sync(ctx);
+}
+
+extern "C" int emu_generate(emu_session *s, const uint32_t *h_prompt, uint32_t prompt_len, uint32_t steps,
+                            uint32_t *h_out)
+{
+    if (!s || !h_prompt || prompt_len == 0 || (steps && !h_out)) return EMU_E_ARG;
+    if (steps == 0) return EMU_OK;
+    for (size_t i = 0; i < (size_t)s->n * prompt_len; ++i)
+        if (h_prompt[i] >= s->m->cfg.vocab) return EMU_E_ARG;
+    const uint64_t total = (uint64_t)prompt_len + steps - 1;
+    int st = check_room(s, total);
+    if (st != EMU_OK) return st;
+    emu_ctx *ctx = s->m->ctx;
+    // prompt buffer rows are `context` long
+    std::vector<uint32_t> buf((size_t)s->n * s->context, 0);
+    for (uint32_t c = 0; c < s->n; ++c)
+        memcpy(&buf[(size_t)c * s->context], h_prompt + (size_t)c * prompt_len, sizeof(uint32_t) * prompt_len);
+    if ((st = emu_memcpy_htod(ctx, s->prompt, buf.data(), buf.size() * sizeof(uint32_t))) != EMU_OK) return st;
+    std::vector<uint32_t> first(s->n);
+    for (uint32_t c = 0; c < s->n; ++c) first[c] = h_prompt[(size_t)c * prompt_len];
+    if ((st = emu_memcpy_htod(ctx, s->tokens, first.data(), sizeof(uint32_t) * s->n)) != EMU_OK) return st;
+    if ((st = emu_memset(ctx, s->steps, 0, sizeof(uint32_t) * s->n)) != EMU_OK) return st;
+    if ((st = set_ctrl(s, prompt_len, steps)) != EMU_OK) return st;
+    if ((st = launch_steps(s, (uint32_t)total)) != EMU_OK) return st;
+    std::vector<uint32_t> hist((size_t)s->n * steps);
+    if ((st = emu_memcpy_dtoh(ctx, hist.data(), s->hist, hist.size() * sizeof(uint32_t))) != EMU_OK) return st;
+    memcpy(h_out, hist.data(), hist.size() * sizeof(uint32_t));
+    return EMU_OK;
+}
+
+extern "C" int emu_time_decode(emu_session *s, uint32_t steps, float *ms)
+{
+    if (!s || !ms) return EMU_E_ARG;
+    int st = check_room(s, steps);
+    if (st != EMU_OK) return st;
+    emu_ctx *ctx = s->m->ctx;
+    if ((st = set_ctrl(s, 0, 0)) != EMU_OK) return st;
+    if ((st = ensure_graph(s)) != EMU_OK) return st;
+    if ((st = emu_ctx_sync(ctx)) != EMU_OK) return st;
+    if ((st = emu_event_record(ctx, 14)) != EMU_OK) return st;
+    if ((st = launch_steps(s, steps)) != EMU_OK) return st;
+    if ((st = emu_event_record(ctx, 15)) != EMU_OK) return st;
+    return emu_event_elapsed(ctx, 14, 15, ms);
+}
+
+extern "C" int emu_session_positions(emu_session *s, uint32_t *h_positions)
+{
+    if (!s || !h_positions) return EMU_E_ARG;
+    return emu_memcpy_dtoh(s->m->ctx, h_positions, s->positions, sizeof(uint32_t) * s->n);
+}
+
+extern "C" int emu_session_read_kv(emu_session *s, uint32_t client, uint32_t layer, int which_v, float *h_out,
+                                   uint32_t positions)
+{
+    if (!s || !h_out || client >= s->n || layer >= s->m->cfg.layers || positions > s->context) return EMU_E_ARG;
+    const emu_model_config &c = s->m->cfg;
+    const uint32_t hd = c.head_dim, nkv = c.kv_heads, kw = nkv * hd;
+    const size_t esz = s->kv_f16 ? 2 : 4;
+    const uint8_t *base = static_cast<const uint8_t *>(which_v ? s->v_cache : s->k_cache);
+    std::vector<uint8_t> tmp((size_t)nkv * s->context * hd * esz);
+    const size_t off = ((size_t)client * c.layers + layer) * nkv * s->context * hd * esz;
+    int st = emu_memcpy_dtoh(s->m->ctx, tmp.data(), base + off, tmp.size());
+    if (st != EMU_OK) return st;
+    for (uint32_t p = 0; p < positions; ++p)
+        for (uint32_t h = 0; h < nkv; ++h)
+            for (uint32_t d = 0; d < hd; ++d) {
+                const size_t src = ((size_t)h * s->context + p) * hd + d;
+                float v;
+                if (s->kv_f16) {
+                    uint16_t bits;
+                    memcpy(&bits, &tmp[src * 2], 2);
+                    v = __half2float(__ushort_as_half(bits));
+                } else {
+                    memcpy(&v, &tmp[src * 4], 4);
+                }
+                h_out[(size_t)p * kw + h * hd + d] = v;
+            }
+    return EMU_OK;
+}

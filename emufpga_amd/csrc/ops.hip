@@ -1,0 +1,323 @@
+// ops.hip -- RMSNorm, RoPE, cached attention, MoE router and greedy selection
+// as standalone entry points.  The decode step uses fused versions of the
+// same arithmetic (attn.hip, qmv.hip); these are the per-function parity
+// hooks and the building blocks of the MoE path.
+#include "internal.hpp"
+
+#include <math.h>
+#include <vector>
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float block_sum(float v, float *red)
+{
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float s = 0.0f;
+    const int nw = (blockDim.x + 63) >> 6;
+    for (int i = 0; i < nw; ++i) s += red[i];
+    return s;
+}
+
+// One workgroup per row.
+__global__ __launch_bounds__(kThreads) void rms_norm_kernel(const float *x, const float *gain,
+                                                            int width, float eps, float *out)
+{
+    __shared__ float red[4];
+    const float *xr = x + (size_t)blockIdx.x * width;
+    float *yr = out + (size_t)blockIdx.x * width;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < width; i += kThreads) s = __builtin_fmaf(xr[i], xr[i], s);
+    s = block_sum(s, red);
+    const float scale = 1.0f / sqrtf(s / (float)width + eps);
+    for (int i = threadIdx.x; i < width; i += kThreads) yr[i] = __fmul_rn(__fmul_rn(xr[i], scale), gain[i]);
+}
+
+// Thread per (token, head, pair).  Arithmetic kept uncontracted so a table
+// built with the reference's libm gives the reference's bits:
+// NEOX x' = x*cos - y*sin, y' = y*cos + x*sin (spm-qwen3-slice/src/attention.rs:22-23);
+// interleaved pairs (spm-granite-moe/src/attention.rs:20-23).
+__global__ __launch_bounds__(kThreads) void rope_kernel(float *x, int n_tok, int heads, int hd,
+                                                        const uint32_t *positions, const float2 *table,
+                                                        int table_positions, int style)
+{
+    const int half = hd / 2;
+    const size_t id = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    if (id >= (size_t)n_tok * heads * half) return;
+    const int i = (int)(id % half);
+    const int h = (int)((id / half) % heads);
+    const int t = (int)(id / ((size_t)half * heads));
+    uint32_t pos = positions[t];
+    if (pos >= (uint32_t)table_positions) pos = table_positions - 1; // host validated
+    const float2 cs = table[(size_t)pos * half + i];
+    float *head = x + ((size_t)t * heads + h) * hd;
+    const int a = style == EMU_ROPE_NEOX ? i : 2 * i;
+    const int b = style == EMU_ROPE_NEOX ? i + half : 2 * i + 1;
+    const float l = head[a], r = head[b];
+    head[a] = __fsub_rn(__fmul_rn(l, cs.x), __fmul_rn(r, cs.y));
+    head[b] = __fadd_rn(__fmul_rn(r, cs.x), __fmul_rn(l, cs.y));
+}
+
+// attend_cached (spm-kv/src/attend.rs:37-94): one workgroup per query head.
+// Threads own positions for the scores, then head lanes for the weighted sum.
+__global__ __launch_bounds__(kThreads) void attend_kernel(const float *q, const void *keys,
+                                                          const void *values, int kv_f16,
+                                                          int positions, int heads, int kv_heads,
+                                                          int hd, float scale, float *scores_ws,
+                                                          float *out)
+{
+    __shared__ float red[4];
+    const int head = blockIdx.x;
+    const int group = heads / kv_heads;
+    const int kvh = head / group;
+    const int stride = kv_heads * hd;
+    const float *qh = q + (size_t)head * hd;
+    float *sc = scores_ws + (size_t)head * positions;
+    auto kv_at = [&](const void *base, size_t idx) -> float {
+        return kv_f16 ? __half2float(static_cast<const __half *>(base)[idx])
+                      : static_cast<const float *>(base)[idx];
+    };
+    float m = -INFINITY;
+    for (int p = threadIdx.x; p < positions; p += kThreads) {
+        float dot = 0.0f;
+        for (int i = 0; i < hd; ++i) dot = __builtin_fmaf(qh[i], kv_at(keys, (size_t)p * stride + kvh * hd + i), dot);
+        const float s = dot * scale;
+        sc[p] = s;
+        m = fmaxf(m, s);
+    }
+    // block max
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float l = 0.0f;
+    for (int p = threadIdx.x; p < positions; p += kThreads) {
+        const float e = expf(sc[p] - m);
+        sc[p] = e;
+        l += e;
+    }
+    l = block_sum(l, red);
+    __syncthreads();
+    for (int d = threadIdx.x; d < hd; d += kThreads) {
+        float acc = 0.0f;
+        for (int p = 0; p < positions; ++p)
+            acc = __builtin_fmaf(sc[p] / l, kv_at(values, (size_t)p * stride + kvh * hd + d), acc);
+        out[(size_t)head * hd + d] = acc;
+    }
+}
+
+// Rust f32::total_cmp key, as an order-preserving unsigned.
+__device__ __forceinline__ uint32_t total_key_u(float f)
+{
+    int32_t i = __float_as_int(f);
+    i ^= (int32_t)(((uint32_t)(i >> 31)) >> 1);
+    return (uint32_t)i ^ 0x80000000u;
+}
+
+// Reduction key: tie_last == 0 -> greatest total-order value, lowest index;
+// tie_last == 1 -> greatest value with -0 == +0, highest index.
+__device__ __forceinline__ uint64_t select_key(float v, uint32_t idx, int tie_last)
+{
+    if (tie_last) {
+        if (v == 0.0f) v = 0.0f;
+        return ((uint64_t)total_key_u(v) << 32) | idx;
+    }
+    return ((uint64_t)total_key_u(v) << 32) | (0xffffffffu - idx);
+}
+
+__device__ __forceinline__ uint32_t key_index(uint64_t k, int tie_last)
+{
+    const uint32_t lo = (uint32_t)k;
+    return tie_last ? lo : 0xffffffffu - lo;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint64_t o = __shfl_xor(k, off, 64);
+        k = o > k ? o : k;
+    }
+    return k;
+}
+
+// One workgroup per row.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float *x, int width, int tie_last, int32_t *out)
+{
+    __shared__ uint64_t red[16];
+    const float *xr = x + (size_t)blockIdx.x * width;
+    uint64_t best = 0;
+    for (int i = threadIdx.x; i < width; i += blockDim.x) {
+        const uint64_t k = select_key(xr[i], (uint32_t)i, tie_last);
+        best = k > best ? k : best;
+    }
+    best = wave_max_u64(best);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = red[0];
+        for (int i = 1; i < (int)(blockDim.x >> 6); ++i) b = red[i] > b ? red[i] : b;
+        out[blockIdx.x] = (int32_t)key_index(b, tie_last);
+    }
+}
+
+// moe::route: one wavefront per token; n_experts <= 256, k <= 64.
+__global__ __launch_bounds__(64) void route_kernel(const float *logits, int n_experts, int k,
+                                                   int32_t *ids, float *weights)
+{
+    __shared__ float p[256];
+    __shared__ float sel[64];
+    const int t = blockIdx.x;
+    const float *lr = logits + (size_t)t * n_experts;
+    const int lane = threadIdx.x;
+    float m = -INFINITY;
+    for (int e = lane; e < n_experts; e += 64) m = fmaxf(m, lr[e]);
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    for (int e = lane; e < n_experts; e += 64) p[e] = expf(lr[e] - m);
+    __syncthreads();
+    // Sequential sum in expert order, as the reference's left fold.
+    float sum = 0.0f;
+    if (lane == 0)
+        for (int e = 0; e < n_experts; ++e) sum = __fadd_rn(sum, p[e]);
+    sum = __shfl(sum, 0, 64);
+    __syncthreads();
+    for (int e = lane; e < n_experts; e += 64) p[e] = p[e] / sum;
+    __syncthreads();
+    // k rounds of (greatest total-order value, lowest id), removing the winner.
+    for (int r = 0; r < k; ++r) {
+        uint64_t best = 0;
+        for (int e = lane; e < n_experts; e += 64) {
+            if (p[e] == -INFINITY) continue;
+            const uint64_t key = select_key(p[e], (uint32_t)e, 0);
+            best = key > best ? key : best;
+        }
+        best = wave_max_u64(best);
+        const int e = (int)key_index(best, 0);
+        if (lane == 0) {
+            ids[(size_t)t * k + r] = e;
+            sel[r] = p[e];
+            p[e] = -INFINITY;
+        }
+        __syncthreads();
+    }
+    if (lane == 0) {
+        float total = 0.0f;
+        for (int r = 0; r < k; ++r) total = __fadd_rn(total, sel[r]);
+        for (int r = 0; r < k; ++r) weights[(size_t)t * k + r] = sel[r] / total;
+    }
+}
+
+} // namespace
+
+extern "C" int emu_rms_norm(emu_ctx *ctx, const float *d_x, const float *d_gain, uint32_t n_rows,
+                            uint32_t width, float eps, float *d_out)
+{
+    if (!ctx || !d_x || !d_gain || !d_out || width == 0) return EMU_E_ARG;
+    if (n_rows == 0) return EMU_OK;
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(n_rows), dim3(kThreads), 0, ctx->stream, d_x, d_gain,
+                       (int)width, eps, d_out);
+    EMU_LAUNCH_CHECK(ctx);
+    return EMU_OK;
+}
+
+// Angles as spm-qwen3-slice/src/attention.rs:14-19 computes them:
+// angle = pos / theta^(2i/d), in f32 with the host libm.
+int emu_build_rope_table(uint32_t positions, uint32_t head_dim, float theta, int fma_form,
+                         std::vector<float> &table)
+{
+    const uint32_t half = head_dim / 2;
+    table.resize((size_t)positions * half * 2);
+    for (uint32_t pos = 0; pos < positions; ++pos) {
+        for (uint32_t i = 0; i < half; ++i) {
+            float angle;
+            if (fma_form) {
+                // spm-ops/src/attention.rs:24-27: base^(-2i/d) * pos
+                volatile float e = -2.0f * (float)i;
+                volatile float ex = e / (float)head_dim;
+                volatile float pw = powf(theta, ex);
+                angle = pw * (float)pos;
+            } else {
+                volatile float e = 2.0f * (float)i;
+                volatile float ex = e / (float)head_dim;
+                volatile float pw = powf(theta, ex);
+                angle = (float)pos / pw;
+            }
+            table[((size_t)pos * half + i) * 2] = cosf(angle);
+            table[((size_t)pos * half + i) * 2 + 1] = sinf(angle);
+        }
+    }
+    return EMU_OK;
+}
+
+extern "C" int emu_rope_table(emu_ctx *ctx, uint32_t positions, uint32_t head_dim, float theta,
+                              float *d_table)
+{
+    if (!ctx || !d_table || head_dim == 0 || head_dim % 2) return EMU_E_ARG;
+    if (positions > 65536) return EMU_E_CONFIG; // positions fit u16 (attention.rs:14-16)
+    std::vector<float> t;
+    emu_build_rope_table(positions, head_dim, theta, 0, t);
+    return emu_memcpy_htod(ctx, d_table, t.data(), t.size() * sizeof(float));
+}
+
+extern "C" int emu_rope(emu_ctx *ctx, float *d_x, uint32_t n_tok, uint32_t heads, uint32_t head_dim,
+                        const uint32_t *d_positions, const float *d_table, uint32_t table_positions,
+                        int style)
+{
+    if (!ctx || !d_x || !d_positions || !d_table || head_dim % 2 || table_positions == 0) return EMU_E_ARG;
+    if (style != EMU_ROPE_NEOX && style != EMU_ROPE_INTERLEAVED) return EMU_E_ARG;
+    const size_t n = (size_t)n_tok * heads * (head_dim / 2);
+    if (n == 0) return EMU_OK;
+    hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                       ctx->stream, d_x, (int)n_tok, (int)heads, (int)head_dim, d_positions,
+                       reinterpret_cast<const float2 *>(d_table), (int)table_positions, style);
+    EMU_LAUNCH_CHECK(ctx);
+    return EMU_OK;
+}
+
+extern "C" int emu_attend_cached(emu_ctx *ctx, const float *d_q, const void *d_keys, const void *d_values,
+                                 int kv_f16, uint32_t positions, uint32_t heads, uint32_t kv_heads,
+                                 uint32_t head_dim, float scale, float *d_out)
+{
+    if (!ctx || !d_q || !d_keys || !d_values || !d_out || head_dim == 0) return EMU_E_ARG;
+    if (kv_heads == 0 || heads % kv_heads != 0) return EMU_E_CONFIG; // attend.rs:82-85
+    if (positions == 0 || heads == 0) return EMU_OK;
+    void *ws = nullptr;
+    int st = emu_malloc(ctx, sizeof(float) * (size_t)heads * positions, &ws);
+    if (st != EMU_OK) return st;
+    hipLaunchKernelGGL(attend_kernel, dim3(heads), dim3(kThreads), 0, ctx->stream, d_q, d_keys, d_values,
+                       kv_f16, (int)positions, (int)heads, (int)kv_heads, (int)head_dim, scale,
+                       static_cast<float *>(ws), d_out);
+    hipError_t e = hipGetLastError();
+    emu_free(ctx, ws);
+    if (e != hipSuccess) return emu_hip_fail(ctx, e, "attend_kernel");
+    return EMU_OK;
+}
+
+extern "C" int emu_route(emu_ctx *ctx, const float *d_logits, uint32_t n_tok, uint32_t n_experts,
+                         uint32_t k, int32_t *d_ids, float *d_weights)
+{
+    if (!ctx || !d_logits || !d_ids || !d_weights) return EMU_E_ARG;
+    if (n_experts == 0 || n_experts > 256 || k == 0 || k > n_experts || k > 64) return EMU_E_CONFIG;
+    if (n_tok == 0) return EMU_OK;
+    hipLaunchKernelGGL(route_kernel, dim3(n_tok), dim3(64), 0, ctx->stream, d_logits, (int)n_experts,
+                       (int)k, d_ids, d_weights);
+    EMU_LAUNCH_CHECK(ctx);
+    return EMU_OK;
+}
+
+extern "C" int emu_argmax(emu_ctx *ctx, const float *d_x, uint32_t n_rows, uint32_t width, int tie_last,
+                          int32_t *d_out)
+{
+    if (!ctx || !d_x || !d_out || width == 0) return EMU_E_ARG;
+    if (n_rows == 0) return EMU_OK;
+    hipLaunchKernelGGL(argmax_kernel, dim3(n_rows), dim3(1024), 0, ctx->stream, d_x, (int)width,
+                       tie_last ? 1 : 0, d_out);
+    EMU_LAUNCH_CHECK(ctx);
+    return EMU_OK;
+}

@@ -1,0 +1,188 @@
+"""Serve API: a dense decoder resident in HBM and client sessions.
+
+Mirrors components/serve/crates/spm-batch: ``Session.decode_step`` is
+decode_step (src/step.rs:19-39) for every client at once, each client at its
+own position with its own KV cache (Client, src/session.rs:13-38), and
+``Session.generate`` is the caller loop of examples/serve-demo.rs:62-91
+(prefill one prompt token per step, then greedy decode), run device-resident.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from ._lib import (EMU_STYLE_QWEN3, EMU_STYLE_SMOL, EMU_T_ATTN_NORM, EMU_T_EMBED, EMU_T_FFN_NORM,
+                   EMU_T_K_NORM, EMU_T_LAYER, EMU_T_OUT_NORM, EMU_T_OUTPUT, EMU_T_Q_NORM, Q6_K, Q8_0,
+                   ModelConfig)
+from .device import Context
+
+
+@dataclass(frozen=True)
+class DenseConfig:
+    hidden: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    ffn: int
+    vocab: int
+    layers: int
+    rope_theta: float
+    eps: float
+    style: int
+    encoding: int
+    tied: bool
+    qk_norm: bool
+
+    def native(self) -> ModelConfig:
+        return ModelConfig(self.hidden, self.heads, self.kv_heads, self.head_dim, self.ffn, self.vocab,
+                           self.layers, self.rope_theta, self.eps, self.style, self.encoding,
+                           int(self.tied), int(self.qk_norm))
+
+    @property
+    def q_width(self) -> int:
+        return self.heads * self.head_dim
+
+    @property
+    def kv_width(self) -> int:
+        return self.kv_heads * self.head_dim
+
+
+# Qwen3-8B shape (spm-qwen3-slice/src/model.rs:10-12, attention.rs:1-3, math.rs:4, attention.rs:18)
+QWEN3_8B_Q6K = DenseConfig(4096, 32, 8, 128, 12288, 151936, 36, 1e6, 1e-6, EMU_STYLE_QWEN3, Q6_K, False, True)
+# SmolLM2-135M shape (spm-smol/src/config.rs:24-45), linears + tied embedding in Q8_0
+SMOLLM2_135M_Q8 = DenseConfig(576, 9, 3, 64, 1536, 49152, 30, 1e5, 1e-5, EMU_STYLE_SMOL, Q8_0, True, False)
+
+
+class Model:
+    """Weights of a dense decoder in one HBM allocation (emu_model)."""
+
+    def __init__(self, ctx: Context, cfg: DenseConfig):
+        self.ctx, self.cfg = ctx, cfg
+        h = C.c_void_p()
+        native = cfg.native()
+        ctx.check(ctx.lib.emu_model_create(ctx.h, C.byref(native), C.byref(h)), "emu_model_create")
+        self.h = h
+
+    def close(self) -> None:
+        if self.h is not None:
+            self.ctx.lib.emu_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def synth(self, seed: int) -> None:
+        self.ctx.check(self.ctx.lib.emu_model_synth(self.h, seed), "emu_model_synth")
+
+    def tensor(self, kind: int, layer: int = 0) -> tuple[int, int]:
+        p, n = C.c_void_p(), C.c_size_t()
+        self.ctx.check(self.ctx.lib.emu_model_tensor(self.h, kind, layer, C.byref(p), C.byref(n)),
+                       "emu_model_tensor")
+        return p.value, n.value
+
+    def read_tensor(self, kind: int, layer: int = 0, dtype=np.uint8) -> np.ndarray:
+        addr, n = self.tensor(kind, layer)
+        out = np.empty(n, np.uint8)
+        self.ctx.check(self.ctx.lib.emu_memcpy_dtoh(self.ctx.h, out.ctypes.data_as(C.c_void_p),
+                                                    C.c_void_p(addr), n), "emu_memcpy_dtoh")
+        return out.view(dtype)
+
+    def write_tensor(self, kind: int, data: np.ndarray, layer: int = 0) -> None:
+        addr, n = self.tensor(kind, layer)
+        data = np.ascontiguousarray(data).view(np.uint8).reshape(-1)
+        if data.size != n:
+            raise ValueError(f"tensor holds {n} bytes, got {data.size}")
+        self.ctx.check(self.ctx.lib.emu_memcpy_htod(self.ctx.h, C.c_void_p(addr),
+                                                    data.ctypes.data_as(C.c_void_p), n), "emu_memcpy_htod")
+
+    def weight_bytes(self) -> int:
+        v = C.c_uint64()
+        self.ctx.check(self.ctx.lib.emu_model_weight_bytes(self.h, C.byref(v)), "emu_model_weight_bytes")
+        return v.value
+
+    def host_weights(self) -> dict:
+        """Every tensor copied to host memory (for the checker)."""
+        c = self.cfg
+        layers = np.concatenate([self.read_tensor(EMU_T_LAYER, l) for l in range(c.layers)])
+        out = {
+            "layers": layers,
+            "embed": self.read_tensor(EMU_T_EMBED),
+            "attn_norm": self.read_tensor(EMU_T_ATTN_NORM, dtype=np.float32),
+            "ffn_norm": self.read_tensor(EMU_T_FFN_NORM, dtype=np.float32),
+            "q_norm": self.read_tensor(EMU_T_Q_NORM, dtype=np.float32),
+            "k_norm": self.read_tensor(EMU_T_K_NORM, dtype=np.float32),
+            "out_norm": self.read_tensor(EMU_T_OUT_NORM, dtype=np.float32),
+        }
+        out["output"] = out["embed"] if c.tied else self.read_tensor(EMU_T_OUTPUT)
+        return out
+
+
+class Session:
+    """A set of clients decoding in lockstep (emu_session)."""
+
+    def __init__(self, model: Model, n_clients: int, context: int, kv_f16: bool = True):
+        self.model, self.ctx = model, model.ctx
+        self.n, self.context, self.kv_f16 = n_clients, context, kv_f16
+        h = C.c_void_p()
+        self.ctx.check(self.ctx.lib.emu_session_create(model.h, n_clients, context, int(kv_f16), C.byref(h)),
+                       "emu_session_create")
+        self.h = h
+
+    def close(self) -> None:
+        if self.h is not None:
+            self.ctx.lib.emu_session_destroy(self.h)
+            self.h = None
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self) -> None:
+        self.ctx.check(self.ctx.lib.emu_session_reset(self.h), "emu_session_reset")
+
+    def decode_step(self, tokens, want_logits: bool = False):
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        nxt = np.empty(self.n, np.uint32)
+        logits_buf = self.ctx.alloc(self.n * self.model.cfg.vocab * 4) if want_logits else None
+        self.ctx.check(self.ctx.lib.emu_decode_step(self.h, toks.ctypes.data_as(C.c_void_p),
+                                                    nxt.ctypes.data_as(C.c_void_p),
+                                                    logits_buf.ptr if logits_buf else None), "emu_decode_step")
+        if want_logits:
+            return nxt, logits_buf.read(np.float32).reshape(self.n, self.model.cfg.vocab)
+        return nxt
+
+    def generate(self, prompts: np.ndarray, steps: int) -> np.ndarray:
+        prompts = np.ascontiguousarray(prompts, np.uint32).reshape(self.n, -1)
+        out = np.empty((self.n, steps), np.uint32)
+        self.ctx.check(self.ctx.lib.emu_generate(self.h, prompts.ctypes.data_as(C.c_void_p), prompts.shape[1],
+                                                 steps, out.ctypes.data_as(C.c_void_p)), "emu_generate")
+        return out
+
+    def time_decode(self, steps: int) -> float:
+        ms = C.c_float()
+        self.ctx.check(self.ctx.lib.emu_time_decode(self.h, steps, C.byref(ms)), "emu_time_decode")
+        return ms.value
+
+    def positions(self) -> np.ndarray:
+        out = np.empty(self.n, np.uint32)
+        self.ctx.check(self.ctx.lib.emu_session_positions(self.h, out.ctypes.data_as(C.c_void_p)),
+                       "emu_session_positions")
+        return out
+
+    def read_kv(self, client: int, layer: int, values: bool, positions: int) -> np.ndarray:
+        out = np.empty(positions * self.model.cfg.kv_width, np.float32)
+        self.ctx.check(self.ctx.lib.emu_session_read_kv(self.h, client, layer, int(values),
+                                                        out.ctypes.data_as(C.c_void_p), positions),
+                       "emu_session_read_kv")
+        return out.reshape(positions, -1)
+
+
+__all__ = ["DenseConfig", "Model", "Session", "QWEN3_8B_Q6K", "SMOLLM2_135M_Q8", "_lib"]

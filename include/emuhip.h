@@ -1,0 +1,250 @@
+/*
+ * emuhip.h -- C ABI of libemuhip.so, the MI355X (gfx950) implementation of
+ * emufpga's token-loop hot path: GGUF block dequant-dot matvec, decode
+ * attention with RoPE and RMSNorm, the MoE router and the selected-expert FFN,
+ * and the per-token decode step that drives them.
+ *
+ * Conventions
+ *  - Every entry point returns an emu_status; nothing aborts or throws across
+ *    the boundary.  The reference's panics (config bugs, a full KV context)
+ *    become EMU_E_CONFIG / EMU_E_CONTEXT_FULL.
+ *  - Pointers named d_* are device pointers (from emu_malloc or any HIP
+ *    allocation on the context's device).  Pointers named h_* are host memory.
+ *  - Compute calls are asynchronous on the context's stream; emu_ctx_sync waits.
+ *  - A context is not thread-safe (it mirrors the reference's `&mut` borrows);
+ *    separate contexts may be used from separate threads.
+ *  - Quantized tensors are GGUF blocks, row-major (each row is cols/block_elems
+ *    whole blocks), uploaded byte-for-byte: no repacking.
+ *  - Reference citations are relative to the emufpga repository root.
+ */
+#ifndef EMUHIP_H
+#define EMUHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum emu_status {
+    EMU_OK = 0,
+    /* Partial block: "byte length is not divisible by 210/176/34"
+     * (components/cli/crates/spm-gguf/src/tensor.rs:105-107,146-148,195-197);
+     * DecodeError::Short (components/format/crates/spm-codec-any/src/decode.rs:8-19). */
+    EMU_E_SHORT = 1,
+    /* LinearError::WeightCount (components/tensor/crates/spm-linear/src/resident.rs:9-14);
+     * "invalid matrix/vector shape" (spm-qwen3-slice/src/math.rs:13-15). */
+    EMU_E_SHAPE = 2,
+    /* LinearError::ActivationLen (spm-linear/src/resident.rs:15-21, stream.rs:63-71). */
+    EMU_E_ACTIVATION_LEN = 3,
+    /* LinearError::Truncated (spm-linear/src/resident.rs:27-33, stream.rs:44-49). */
+    EMU_E_TRUNCATED = 4,
+    /* DecodeError::Unsupported (spm-codec-any/src/decode.rs:43-45); unknown
+     * GGUF dtype (spm-gguf/src/parse.rs:10-29). */
+    EMU_E_UNSUPPORTED = 5,
+    /* KvCache::append "context exhausted" panic (spm-serve spm-kv/src/cache.rs:50-54). */
+    EMU_E_CONTEXT_FULL = 6,
+    /* attend_cached "heads must group evenly" panic (spm-kv/src/attend.rs:82-85),
+     * RoPE position past u16 (spm-qwen3-slice/src/attention.rs:14-16), bad model shape. */
+    EMU_E_CONFIG = 7,
+    EMU_E_HIP = 8,   /* a HIP runtime call failed */
+    EMU_E_ARG = 9,   /* null pointer or out-of-range argument */
+    EMU_E_NOMEM = 10 /* device or host allocation refused (tensor.rs:108-110) */
+} emu_status;
+
+/* GGUF dtype ids (spm-gguf/src/parse.rs:10-29). */
+typedef enum emu_encoding {
+    EMU_ENC_F32 = 0,
+    EMU_ENC_F16 = 1,
+    EMU_ENC_Q8_0 = 8,
+    EMU_ENC_Q2_K = 10,
+    EMU_ENC_Q5_K = 13,
+    EMU_ENC_Q6_K = 14
+} emu_encoding;
+
+typedef struct emu_ctx emu_ctx;
+typedef struct emu_model emu_model;
+typedef struct emu_session emu_session;
+
+/* ---- context, memory ---------------------------------------------------- */
+const char *emu_strerror(int status);
+/* Text of the last HIP error seen by this context ("" if none). */
+const char *emu_last_error(const emu_ctx *ctx);
+int emu_ctx_create(int device, emu_ctx **out);
+int emu_ctx_destroy(emu_ctx *ctx);
+int emu_ctx_sync(emu_ctx *ctx);
+/* The hipStream_t the context launches on (returned as void*). */
+int emu_ctx_stream(emu_ctx *ctx, void **stream);
+/* Device properties: compute units and the device's gfx arch name. */
+int emu_device_info(emu_ctx *ctx, int *compute_units, char *arch, size_t arch_len);
+
+int emu_malloc(emu_ctx *ctx, size_t bytes, void **d_out);
+int emu_free(emu_ctx *ctx, void *d_ptr);
+int emu_memcpy_htod(emu_ctx *ctx, void *d_dst, const void *h_src, size_t bytes);
+int emu_memcpy_dtoh(emu_ctx *ctx, void *h_dst, const void *d_src, size_t bytes);
+int emu_memcpy_dtod(emu_ctx *ctx, void *d_dst, const void *d_src, size_t bytes);
+int emu_memset(emu_ctx *ctx, void *d_dst, int value, size_t bytes);
+
+/* Event timing on the context's stream: record into slot (0..15), then read
+ * the elapsed milliseconds between two recorded slots (waits for the later). */
+int emu_event_record(emu_ctx *ctx, int slot);
+int emu_event_elapsed(emu_ctx *ctx, int start_slot, int end_slot, float *ms);
+
+/* (block elements, block bytes) of a GGUF dtype: layout() of
+ * spm-gguf/src/parse.rs:10-29.  EMU_E_UNSUPPORTED for other ids. */
+int emu_block_layout(int encoding, uint32_t *block_elems, uint32_t *block_bytes);
+
+/* ---- decode (parity hook) ----------------------------------------------- */
+/* Replaces decode_q6_k / decode_q5_k / decode_q8_0
+ * (spm-gguf/src/tensor.rs:103,144,193) and adds Q2_K, which the reference
+ * lacks.  d_out receives (src_len/block_bytes)*block_elems f32 in the same
+ * element order.  EMU_E_SHORT when src_len is not whole blocks. */
+int emu_dequant(emu_ctx *ctx, int encoding, const void *d_src, size_t src_len, float *d_out);
+
+/* ---- quantized matvec --------------------------------------------------- */
+/* y[t][r] = sum_c W[r][c] * x[t][c] for t < n_tok, r < rows: the projection of
+ * spm_linear::streamed (components/tensor/crates/spm-linear/src/stream.rs:31-55),
+ * spm-qwen3-slice weights::projection_batch (weights.rs:27-39) and
+ * spm-granite-moe weights::project_expert (weights.rs:41-55).
+ * W: rows x cols GGUF blocks (w_len bytes, must equal rows * row bytes:
+ * EMU_E_SHAPE otherwise, EMU_E_SHORT if cols is not whole blocks).
+ * x: n_tok x cols f32 (x_len elements; EMU_E_ACTIVATION_LEN if short).
+ * y: n_tok x rows f32, overwritten (zero-fill semantics of stream.rs:41),
+ * or accumulated into with EMU_MV_ACCUMULATE.  n_tok 1..8. */
+enum { EMU_MV_ACCUMULATE = 1u };
+int emu_qmatvec(emu_ctx *ctx, int encoding, const void *d_w, size_t w_len, uint32_t rows,
+                uint32_t cols, const float *d_x, size_t x_len, uint32_t n_tok, float *d_y,
+                uint32_t flags);
+
+/* Fused forms used by the decode step (no separate reference entry point;
+ * each equals a composition of reference calls):
+ *  - gain != NULL: x is RMS-normalised with gain and eps first
+ *    (spm-smol-ops/src/norm.rs:12-32 pre_norm, spm-qwen3-slice/src/math.rs:1-10);
+ *  - d_w_up != NULL: SwiGLU pair, y = silu(W x) * (W_up x)
+ *    (spm-batch/src/inner.rs:103-107, spm-qwen3-slice/src/model.rs:93-116). */
+int emu_qmatvec_fused(emu_ctx *ctx, int encoding, const void *d_w, const void *d_w_up,
+                      uint32_t rows, uint32_t cols, const float *d_x, uint32_t n_tok,
+                      const float *d_gain, float eps, float *d_y, uint32_t flags);
+
+/* ---- int8-activation mode (integer block dots) -------------------------- */
+/* No reference counterpart: the reference multiplies f32 activations only.
+ * Quantize x (n_tok x cols, cols % 32 == 0) per 32 columns: s = amax/127,
+ * q = roundf(x * (1/s)), clamped to [-127,127]. */
+int emu_quantize_act(emu_ctx *ctx, const float *d_x, uint32_t n_tok, uint32_t cols,
+                     int8_t *d_q, float *d_scales);
+/* Exact int32 sums of (weight code) * q over each scale sub-block (16 columns
+ * for Q6_K/Q2_K, 32 for Q8_0/Q5_K); out is n_tok x rows x (cols/sub). */
+int emu_block_dots(emu_ctx *ctx, int encoding, const void *d_w, size_t w_len, uint32_t rows,
+                   uint32_t cols, const int8_t *d_q, uint32_t n_tok, int32_t *d_out);
+/* y = W x with x given as int8 blocks + scales (the integer-dot matvec). */
+int emu_qmatvec_i8(emu_ctx *ctx, int encoding, const void *d_w, size_t w_len, uint32_t rows,
+                   uint32_t cols, const int8_t *d_q, const float *d_scales, uint32_t n_tok,
+                   float *d_y);
+
+/* ---- norms, RoPE, attention, router, selection -------------------------- */
+/* out[r] = x[r] * (1/sqrt(mean(x[r]^2) + eps)) * gain, for n_rows rows of width
+ * (spm-smol-ops/src/norm.rs:12-21; spm-qwen3-slice/src/math.rs:1-10). */
+int emu_rms_norm(emu_ctx *ctx, const float *d_x, const float *d_gain, uint32_t n_rows,
+                 uint32_t width, float eps, float *d_out);
+
+/* RoPE styles. */
+enum {
+    EMU_ROPE_NEOX = 0,       /* halves: spm-qwen3-slice/src/attention.rs:11-25 and
+                                spm-ops/src/attention.rs:20-32 */
+    EMU_ROPE_INTERLEAVED = 1 /* adjacent pairs: spm-granite-moe/src/attention.rs:12-26 */
+};
+/* Host-built cos/sin table (glibc powf/sinf/cosf, the reference's libm):
+ * d_table[pos][i] = (cos, sin) of pos / theta^(2i/head_dim), pos < positions.
+ * Built on the host and uploaded; bytes = positions * head_dim/2 * 8. */
+int emu_rope_table(emu_ctx *ctx, uint32_t positions, uint32_t head_dim, float theta,
+                   float *d_table);
+/* rotate_at (spm-kv/src/attend.rs:13-19): rotate n_tok tokens of `heads` heads
+ * in place, token t at position d_positions[t]. */
+int emu_rope(emu_ctx *ctx, float *d_x, uint32_t n_tok, uint32_t heads, uint32_t head_dim,
+             const uint32_t *d_positions, const float *d_table, uint32_t table_positions,
+             int style);
+
+/* attend_cached (spm-kv/src/attend.rs:75-94) for one token over a cached
+ * prefix of `positions` rows.  keys/values: f32 or f16 (kv_f16 != 0) rows of
+ * kv_heads*head_dim; score = dot * scale; softmax; weighted sum of values. */
+int emu_attend_cached(emu_ctx *ctx, const float *d_q, const void *d_keys, const void *d_values,
+                      int kv_f16, uint32_t positions, uint32_t heads, uint32_t kv_heads,
+                      uint32_t head_dim, float scale, float *d_out);
+
+/* moe::route (spm-granite-moe/src/moe.rs:17-35): softmax over n_experts
+ * logits per token, top-k by (prob desc, id asc), weights renormalised by the
+ * selected sum.  ids/weights are n_tok x k. */
+int emu_route(emu_ctx *ctx, const float *d_logits, uint32_t n_tok, uint32_t n_experts,
+              uint32_t k, int32_t *d_ids, float *d_weights);
+
+/* Greedy selection over n_rows rows of width: tie_last 0 = lowest index of the
+ * maximum (top_k, spm-qwen3-slice/src/math.rs:38-48); 1 = last index
+ * (max_by(partial_cmp), spm-batch/tests/batching.rs:111-123). */
+int emu_argmax(emu_ctx *ctx, const float *d_x, uint32_t n_rows, uint32_t width, int tie_last,
+               int32_t *d_out);
+
+/* ---- dense decoder model and decode step (serve API) -------------------- */
+enum { EMU_STYLE_QWEN3 = 0, EMU_STYLE_SMOL = 1 };
+
+typedef struct emu_model_config {
+    uint32_t hidden, heads, kv_heads, head_dim, ffn, vocab, layers;
+    float rope_theta, eps;
+    int32_t style;    /* EMU_STYLE_*: QK-norm + top_k greedy (Qwen3) or the
+                         spm-batch SmolLM2 path (max_by greedy) */
+    int32_t encoding; /* every linear, the embedding and the output matrix */
+    int32_t tied;     /* logits from the embedding matrix (SmolLM2) */
+    int32_t qk_norm;  /* per-head RMSNorm of q and k before RoPE (Qwen3) */
+} emu_model_config;
+
+/* Tensor kinds addressable inside a model. */
+enum {
+    EMU_T_LAYER = 0,    /* layer's q,k,v,o,gate,up,down blocks back to back (consume order) */
+    EMU_T_EMBED = 1,    /* vocab x hidden */
+    EMU_T_OUTPUT = 2,   /* vocab x hidden (absent when tied) */
+    EMU_T_ATTN_NORM = 3, EMU_T_FFN_NORM = 4, EMU_T_Q_NORM = 5, EMU_T_K_NORM = 6,
+    EMU_T_OUT_NORM = 7  /* f32 gains */
+};
+
+int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_model **out);
+int emu_model_destroy(emu_model *model);
+/* Device address and size of a tensor inside the model's HBM residency (for
+ * uploading real weights or reading them back).  layer is ignored for
+ * model-wide tensors. */
+int emu_model_tensor(emu_model *model, int kind, uint32_t layer, void **d_ptr, size_t *bytes);
+/* Seeded synthetic weights: every quantized tensor from N(0, 0.02) draws,
+ * quantized on the device; gains 1.0. */
+int emu_model_synth(emu_model *model, uint64_t seed);
+/* Algorithmic weight bytes one decode step reads (all linears + output rows). */
+int emu_model_weight_bytes(const emu_model *model, uint64_t *bytes);
+
+/* A set of clients (spm-batch/src/session.rs:13-38 Client, :46-79 Scratch):
+ * per-client KV caches of `context` positions (f16 when kv_f16, else f32). */
+int emu_session_create(emu_model *model, uint32_t n_clients, uint32_t context, int kv_f16,
+                       emu_session **out);
+int emu_session_destroy(emu_session *s);
+int emu_session_reset(emu_session *s);
+/* decode_step (spm-batch/src/step.rs:19-39): feed h_tokens[c] to client c at
+ * its current position, advance every position by one, and greedily select
+ * each client's next token.  h_next may be NULL.  d_logits, when non-NULL,
+ * receives n_clients x vocab logits. */
+int emu_decode_step(emu_session *s, const uint32_t *h_tokens, uint32_t *h_next, float *d_logits);
+/* Greedy generation: feed h_prompt (n_clients x prompt_len, one token per step
+ * as examples/serve-demo.rs:62-91 does), then produce `steps` tokens per
+ * client into h_out (n_clients x steps).  The loop is device-resident: token
+ * selection feeds the next step without host round trips. */
+int emu_generate(emu_session *s, const uint32_t *h_prompt, uint32_t prompt_len, uint32_t steps,
+                 uint32_t *h_out);
+/* Time `steps` greedy steps (after the caller's warmup) with events around the
+ * region; ms receives the elapsed time. */
+int emu_time_decode(emu_session *s, uint32_t steps, float *ms);
+/* Current position (tokens consumed) of every client. */
+int emu_session_positions(emu_session *s, uint32_t *h_positions);
+/* Copy a client's cached K or V rows for one layer (positions x kv_width f32). */
+int emu_session_read_kv(emu_session *s, uint32_t client, uint32_t layer, int which_v,
+                        float *h_out, uint32_t positions);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* EMUHIP_H */

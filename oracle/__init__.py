@@ -1,0 +1,236 @@
+"""Python binding of the CPU oracle (liboracle.so) -- TEST INFRASTRUCTURE ONLY.
+
+The oracle restates the reference's Rust CPU arithmetic in C (oracle.c) and is
+the checker the HIP path is compared against.  Only tests, the smoke entry
+point and the benchmark's CPU-baseline leg use it; the product never does.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "liboracle.so"
+
+OR_F32, OR_F16, OR_Q8_0, OR_Q2_K, OR_Q5_K, OR_Q6_K = 0, 1, 8, 10, 13, 14
+STYLE_QWEN3, STYLE_SMOL = 0, 1
+
+
+class DenseCfg(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_uint32), ("heads", C.c_uint32), ("kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32), ("ffn", C.c_uint32), ("vocab", C.c_uint32),
+        ("layers", C.c_uint32), ("context", C.c_uint32), ("rope_theta", C.c_float),
+        ("eps", C.c_float), ("style", C.c_int32), ("dtype", C.c_int32), ("kv_f16", C.c_int32),
+        ("tied", C.c_int32), ("qk_norm", C.c_int32),
+    ]
+
+
+class DenseWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in
+                ("layers", "embed", "output", "attn_norm", "ffn_norm", "q_norm", "k_norm", "out_norm")]
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB
+
+
+_lib = None
+
+
+def load() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        lib = C.CDLL(str(LIB))
+        P, U, I, F, SZ = C.c_void_p, C.c_uint32, C.c_int, C.c_float, C.c_size_t
+        sig = {
+            "or_f16_to_f32": ([C.c_uint16], F),
+            "or_f32_to_f16": ([F], C.c_uint16),
+            "or_decode": ([I, P, SZ, P], I),
+            "or_decode_q6_k": ([P, SZ, P], I),
+            "or_decode_q5_k": ([P, SZ, P], I),
+            "or_decode_q8_0": ([P, SZ, P], I),
+            "or_decode_q2_k": ([P, SZ, P], I),
+            "or_matvec_m1": ([P, U, U, P, P], None),
+            "or_matvec_m2": ([P, U, U, P, U, P], None),
+            "or_qmatvec": ([I, P, U, U, P, U, P, I], I),
+            "or_quantize_act_q8": ([P, U, P, P], None),
+            "or_block_dots": ([I, P, U, U, P, U, P], I),
+            "or_rms_norm": ([P, P, U, F, P], None),
+            "or_rope_qwen3": ([P, U, U, F], None),
+            "or_rope_fma": ([P, U, U, F], None),
+            "or_rope_interleaved": ([P, U, U, F], None),
+            "or_softmax_div": ([P, U], None),
+            "or_softmax_recip": ([P, U], None),
+            "or_silu": ([F], F),
+            "or_top_k": ([P, U, U, P, P], None),
+            "or_route": ([P, U, U, P, P], None),
+            "or_attend": ([P, P, P, U, U, U, U, I, F, P], None),
+            "or_dense_layer_bytes": ([C.POINTER(DenseCfg)], SZ),
+            "or_dense_step": ([C.POINTER(DenseCfg), C.POINTER(DenseWeights), P, P, P, P, U, P, U], I),
+            "or_argmax": ([P, U, I], U),
+        }
+        for name, (args, res) in sig.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = lib
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+BLOCK = {OR_Q8_0: (32, 34), OR_Q2_K: (256, 84), OR_Q5_K: (256, 176), OR_Q6_K: (256, 210), OR_F32: (1, 4)}
+
+
+def decode(dtype: int, data) -> np.ndarray:
+    raw = np.ascontiguousarray(np.frombuffer(bytes(data), np.uint8) if not isinstance(data, np.ndarray)
+                               else data.view(np.uint8).reshape(-1))
+    e, b = BLOCK[dtype]
+    out = np.empty(max(raw.size // b * e, 1), np.float32)
+    st = load().or_decode(dtype, _p(raw), raw.size, _p(out))
+    if st != 0:
+        raise ValueError(f"oracle decode failed ({st}): partial block")
+    return out[: raw.size // b * e]
+
+
+def matvec_m1(w: np.ndarray, x: np.ndarray) -> np.ndarray:
+    w = np.ascontiguousarray(w, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(w.shape[0], np.float32)
+    load().or_matvec_m1(_p(w), w.shape[0], w.shape[1], _p(x), _p(y))
+    return y
+
+
+def matvec_m2(w: np.ndarray, x: np.ndarray, positions: int) -> np.ndarray:
+    w = np.ascontiguousarray(w, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(w.shape[0] * positions, np.float32)
+    load().or_matvec_m2(_p(w), w.shape[0], w.shape[1], _p(x), positions, _p(y))
+    return y
+
+
+def qmatvec(dtype: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray, n_tok: int, mode: int = 1) -> np.ndarray:
+    w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    y = np.empty(rows * n_tok, np.float32)
+    st = load().or_qmatvec(dtype, _p(w), rows, cols, _p(x), n_tok, _p(y), mode)
+    if st != 0:
+        raise ValueError(f"oracle qmatvec failed ({st})")
+    return y
+
+
+def quantize_act(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    q = np.empty(x.size, np.int8)
+    s = np.empty(x.size // 32, np.float32)
+    load().or_quantize_act_q8(_p(x), x.size, _p(q), _p(s))
+    return q, s
+
+
+def block_dots(dtype: int, w: np.ndarray, rows: int, cols: int, xq: np.ndarray, n_tok: int) -> np.ndarray:
+    sub = 16 if dtype in (OR_Q6_K, OR_Q2_K) else 32
+    w = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
+    xq = np.ascontiguousarray(xq, np.int8).reshape(-1)
+    out = np.empty(n_tok * rows * (cols // sub), np.int32)
+    st = load().or_block_dots(dtype, _p(w), rows, cols, _p(xq), n_tok, _p(out))
+    if st != 0:
+        raise ValueError(f"oracle block_dots failed ({st})")
+    return out
+
+
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    y = np.empty_like(x)
+    load().or_rms_norm(_p(x), _p(w), x.size, eps, _p(y))
+    return y
+
+
+def rope(kind: str, head: np.ndarray, position: int, theta: float) -> np.ndarray:
+    h = np.array(head, np.float32, copy=True)
+    fn = {"qwen3": load().or_rope_qwen3, "fma": load().or_rope_fma,
+          "interleaved": load().or_rope_interleaved}[kind]
+    fn(_p(h), h.size, position, theta)
+    return h
+
+
+def softmax(v: np.ndarray, recip: bool = False) -> np.ndarray:
+    v = np.array(v, np.float32, copy=True)
+    (load().or_softmax_recip if recip else load().or_softmax_div)(_p(v), v.size)
+    return v
+
+
+def silu(x: float) -> float:
+    return load().or_silu(x)
+
+
+def top_k(v: np.ndarray, k: int) -> list[tuple[int, float]]:
+    v = np.ascontiguousarray(v, np.float32)
+    idx = np.empty(k, np.uint32)
+    val = np.empty(k, np.float32)
+    load().or_top_k(_p(v), v.size, k, _p(idx), _p(val))
+    return [(int(i), float(x)) for i, x in zip(idx, val)]
+
+
+def route(logits: np.ndarray, k: int) -> tuple[np.ndarray, np.ndarray]:
+    logits = np.ascontiguousarray(logits, np.float32)
+    ids = np.empty(k, np.uint32)
+    w = np.empty(k, np.float32)
+    load().or_route(_p(logits), logits.size, k, _p(ids), _p(w))
+    return ids, w
+
+
+def attend(q, keys, values, positions, heads, kv_heads, hd, variant, c=0.0) -> np.ndarray:
+    q = np.ascontiguousarray(q, np.float32)
+    keys = np.ascontiguousarray(keys, np.float32)
+    values = np.ascontiguousarray(values, np.float32)
+    out = np.empty(heads * hd, np.float32)
+    load().or_attend(_p(q), _p(keys), _p(values), positions, heads, kv_heads, hd, variant, c, _p(out))
+    return out
+
+
+def argmax(v: np.ndarray, tie_last: bool) -> int:
+    v = np.ascontiguousarray(v, np.float32)
+    return int(load().or_argmax(_p(v), v.size, int(tie_last)))
+
+
+class DenseOracle:
+    """Reference decode steps for a dense decoder (or_dense_step)."""
+
+    def __init__(self, cfg: DenseCfg, weights: dict, n_clients: int):
+        self.cfg = cfg
+        self.w = {k: np.ascontiguousarray(v) for k, v in weights.items()}
+        self.ws = DenseWeights(*[_p(self.w[k]) for k in
+                                 ("layers", "embed", "output", "attn_norm", "ffn_norm", "q_norm", "k_norm",
+                                  "out_norm")])
+        kw = cfg.kv_heads * cfg.head_dim
+        self.n = n_clients
+        self.k = np.zeros(n_clients * cfg.layers * cfg.context * kw, np.float32)
+        self.v = np.zeros_like(self.k)
+        self.pos = np.zeros(n_clients, np.uint32)
+
+    def step(self, tokens, layers_limit: int = 0) -> np.ndarray:
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        logits = np.empty(self.n * self.cfg.vocab, np.float32)
+        st = load().or_dense_step(C.byref(self.cfg), C.byref(self.ws), _p(self.k), _p(self.v), _p(self.pos),
+                                  _p(toks), self.n, _p(logits), layers_limit)
+        if st != 0:
+            raise ValueError(f"oracle dense step failed ({st})")
+        self.pos += 1
+        return logits.reshape(self.n, self.cfg.vocab)
+
+    def cache(self, client: int, layer: int, values: bool) -> np.ndarray:
+        c = self.cfg
+        kw = c.kv_heads * c.head_dim
+        buf = self.v if values else self.k
+        base = (client * c.layers + layer) * c.context * kw
+        return buf[base: base + c.context * kw].reshape(c.context, kw)

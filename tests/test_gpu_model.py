@@ -1,0 +1,117 @@
+"""Decode-step parity: the device-resident decoder against the oracle.
+
+Bars (stated per the target): logits within ||gpu - ref||_inf <= 1e-3 *
+||ref||_inf per step; greedy tokens identical over 256 decode steps; the fp16
+KV cache holds exactly the oracle's fp16-rounded keys/values to within the
+logit tolerance propagated through one layer (checked at 1e-3 relative).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from emufpga_amd import _lib
+from emufpga_amd.serve import DenseConfig, Model, Session
+
+pytestmark = pytest.mark.gpu
+
+SMALL_QWEN3 = DenseConfig(hidden=512, heads=4, kv_heads=2, head_dim=128, ffn=1024, vocab=1000, layers=3,
+                          rope_theta=1e6, eps=1e-6, style=_lib.EMU_STYLE_QWEN3, encoding=_lib.Q6_K, tied=False,
+                          qk_norm=True)
+SMALL_SMOL = DenseConfig(hidden=576, heads=9, kv_heads=3, head_dim=64, ffn=1536, vocab=2048, layers=3,
+                         rope_theta=1e5, eps=1e-5, style=_lib.EMU_STYLE_SMOL, encoding=_lib.Q8_0, tied=True,
+                         qk_norm=False)
+
+
+def oracle_for(model: Model, context: int, kv_f16: bool, n_clients: int) -> oracle.DenseOracle:
+    c = model.cfg
+    cfg = oracle.DenseCfg(hidden=c.hidden, heads=c.heads, kv_heads=c.kv_heads, head_dim=c.head_dim, ffn=c.ffn,
+                          vocab=c.vocab, layers=c.layers, context=context, rope_theta=c.rope_theta, eps=c.eps,
+                          style=c.style, dtype=c.encoding, kv_f16=int(kv_f16), tied=int(c.tied),
+                          qk_norm=int(c.qk_norm))
+    return oracle.DenseOracle(cfg, model.host_weights(), n_clients)
+
+
+def rel_inf(a, b):
+    return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+
+
+@pytest.mark.parametrize("cfg", [SMALL_QWEN3, SMALL_SMOL], ids=["qwen3", "smol"])
+def test_decode_steps_match_oracle(ctx, cfg):
+    model = Model(ctx, cfg)
+    model.synth(1234)
+    context = 300  # > one 256-position attention chunk: exercises the split merge
+    sess = Session(model, 2, context, kv_f16=True)
+    ref = oracle_for(model, context, True, 2)
+    rng = np.random.default_rng(0)
+    worst = 0.0
+    for step in range(270):
+        toks = rng.integers(0, cfg.vocab, size=2).astype(np.uint32)
+        nxt, logits = sess.decode_step(toks, want_logits=True)
+        r = ref.step(toks)
+        if step % 9 == 0 or step > 255:
+            for c in range(2):
+                worst = max(worst, rel_inf(logits[c], r[c]))
+                tie_last = cfg.style == _lib.EMU_STYLE_SMOL
+                assert int(nxt[c]) == int(np.argmax(logits[c])) if not tie_last else True
+    assert worst <= 1e-3, worst
+    assert list(sess.positions()) == [270, 270]
+    kv = sess.read_kv(1, cfg.layers - 1, values=False, positions=270)
+    rk = ref.cache(1, cfg.layers - 1, values=False)[:270]
+    assert np.max(np.abs(kv - rk)) <= 1e-3 * np.max(np.abs(rk))
+
+
+@pytest.mark.parametrize("cfg", [SMALL_QWEN3, SMALL_SMOL], ids=["qwen3", "smol"])
+def test_greedy_tokens_identical_over_256_steps(ctx, cfg):
+    model = Model(ctx, cfg)
+    model.synth(99)
+    prompt_len, steps = 8, 256
+    context = prompt_len + steps
+    sess = Session(model, 1, context, kv_f16=True)
+    rng = np.random.default_rng(1)
+    prompt = rng.integers(0, cfg.vocab, size=(1, prompt_len)).astype(np.uint32)
+    got = sess.generate(prompt, steps)[0]
+    ref = oracle_for(model, context, True, 1)
+    tie_last = cfg.style == _lib.EMU_STYLE_SMOL
+    toks = []
+    for t in range(prompt_len):
+        logits = ref.step(prompt[:, t])
+    nxt = oracle.argmax(logits[0], tie_last)
+    toks.append(nxt)
+    for _ in range(steps - 1):
+        logits = ref.step([nxt])
+        nxt = oracle.argmax(logits[0], tie_last)
+        toks.append(nxt)
+    assert list(got) == toks
+
+
+def test_batched_client_gets_what_it_would_alone(ctx):  # spm-batch/tests/batching.rs:128-145
+    model = Model(ctx, SMALL_QWEN3)
+    model.synth(7)
+    prompts = np.array([[1, 2, 3, 4], [9, 8, 7, 6], [5, 5, 5, 5]], np.uint32)
+    together = Session(model, 3, 64).generate(prompts, 20)
+    for c in range(3):
+        alone = Session(model, 1, 64).generate(prompts[c:c + 1], 20)
+        assert np.array_equal(alone[0], together[c])
+
+
+def test_context_full_is_an_error(ctx):  # spm-kv/src/cache.rs:50-54
+    model = Model(ctx, SMALL_SMOL)
+    model.synth(3)
+    sess = Session(model, 1, 10)
+    with pytest.raises(_lib.ContextFull):
+        sess.generate(np.zeros((1, 5), np.uint32), 7)
+    for _ in range(10):
+        sess.decode_step([1])
+    with pytest.raises(_lib.ContextFull):
+        sess.decode_step([1])
+
+
+def test_generate_is_deterministic_and_replays(ctx):
+    model = Model(ctx, SMALL_QWEN3)
+    model.synth(11)
+    sess = Session(model, 2, 128)
+    prompts = np.array([[3, 1, 4, 1, 5], [2, 7, 1, 8, 2]], np.uint32)
+    a = sess.generate(prompts, 40)
+    sess.reset()
+    b = sess.generate(prompts, 40)
+    assert np.array_equal(a, b)

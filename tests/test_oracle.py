@@ -1,0 +1,319 @@
+"""Pins the CPU oracle (CPU only, no GPU).
+
+Each check is independent of the oracle's own code: the reference's own
+known-answer tests (cited), closed forms computed exactly in float64, an
+independent numpy restatement (tests/npref.py), brute force on small inputs,
+and invariants.  A mistake planted in the oracle (dropped term, swapped
+nibble, wrong scale index, wrong tie order) fails at least one of these.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from tests import npref
+
+Q6, Q5, Q8, Q2 = oracle.OR_Q6_K, oracle.OR_Q5_K, oracle.OR_Q8_0, oracle.OR_Q2_K
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+# ---- f16 ----------------------------------------------------------------
+
+def test_f16_exhaustive_matches_ieee_half():
+    lib = oracle.load()
+    codes = np.arange(65536, dtype=np.uint16)
+    ours = np.array([lib.or_f16_to_f32(int(c)) for c in codes], np.float32)
+    ref = codes.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(bits(ours[~nan]), bits(ref[~nan]))
+    # NaN payload kept (tensor.rs:94): fraction shifted into the f32 mantissa.
+    # Only quiet NaNs survive the ctypes float -> double round trip unchanged.
+    assert np.all(np.isnan(ours[nan]))
+    quiet = nan & ((codes & 0x200) != 0)
+    assert np.array_equal(bits(ours[quiet]) & 0x7FFFFF, (codes[quiet].astype(np.uint32) & 0x3FF) << 13)
+
+
+def test_f32_to_f16_round_nearest_even():
+    lib = oracle.load()
+    rng = np.random.default_rng(1)
+    xs = np.concatenate([
+        rng.normal(0, 1, 4000), rng.normal(0, 1e-5, 2000), rng.normal(0, 7e4, 500),
+        [0.0, -0.0, 65504.0, 65520.0, 65519.99, 6e-8, 2.98e-8, 5.96e-8, np.inf, -np.inf],
+        (np.arange(1, 2048) * 2.0 ** -24),  # subnormal grid and half-way points
+        (np.arange(1, 2048) * 2.0 ** -25),
+    ]).astype(np.float32)
+    ours = np.array([lib.or_f32_to_f16(float(x)) for x in xs], np.uint16)
+    ref = xs.astype(np.float16).view(np.uint16)
+    assert np.array_equal(ours, ref)
+
+
+# ---- decoders: reference KATs (spm-gguf/tests/decode.rs) -----------------
+
+def test_q6_k_zero_code_with_unit_scale_is_minus_32():  # decode.rs:8-14
+    block = np.zeros(210, np.uint8)
+    block[192:208] = 1
+    block[208:210] = np.frombuffer(np.uint16(0x3C00).tobytes(), np.uint8)
+    assert np.array_equal(oracle.decode(Q6, block), np.full(256, -32.0, np.float32))
+
+
+def test_q6_k_lane_bit_packing_matches_reference_layout():  # decode.rs:16-28
+    block = np.zeros(210, np.uint8)
+    block[192:208] = 1
+    block[208:210] = np.frombuffer(np.uint16(0x4000).tobytes(), np.uint8)
+    block[0], block[32], block[128] = 0xA5, 0xC7, 0b11_10_01_00
+    d = oracle.decode(Q6, block)
+    assert np.array_equal(bits(d[[0, 32, 64, 96]]), bits([-54.0, -18.0, 20.0, 56.0]))
+
+
+def test_q6_k_rejects_partial_block():  # decode.rs:30-33
+    with pytest.raises(ValueError):
+        oracle.decode(Q6, np.zeros(209, np.uint8))
+
+
+def test_q5_k_known_low_nibbles_and_rejects_partial_block():  # decode.rs:35-46
+    block = np.zeros(176, np.uint8)
+    block[0:2] = np.frombuffer(np.uint16(0x3C00).tobytes(), np.uint8)
+    block[4] = 1
+    block[5] = 1
+    block[48:80] = 0x32
+    d = oracle.decode(Q5, block)
+    assert np.array_equal(d[:32], np.full(32, 2.0, np.float32))
+    assert np.array_equal(d[32:64], np.full(32, 3.0, np.float32))
+    with pytest.raises(ValueError):
+        oracle.decode(Q5, block[:175])
+
+
+def test_q8_0_signed_values_and_rejects_partial_block():  # decode.rs:48-58
+    block = np.zeros(34, np.uint8)
+    block[0:2] = np.frombuffer(np.uint16(0x3800).tobytes(), np.uint8)
+    block[2] = 4
+    block[3] = np.uint8(np.int8(-6).view(np.uint8))
+    d = oracle.decode(Q8, block)
+    assert abs(d[0] - 2.0) < np.finfo(np.float32).eps
+    assert abs(d[1] + 3.0) < np.finfo(np.float32).eps
+    with pytest.raises(ValueError):
+        oracle.decode(Q8, block[:33])
+
+
+def test_q6_pipeline_fixture_matches_independent_decoder():  # q6-pipeline/tests/pipeline.rs:22-35
+    raw = npref.q6_pipeline_fixture(3)
+    assert np.array_equal(bits(oracle.decode(Q6, raw)), bits(npref.decode_q6_k(raw)))
+
+
+@pytest.mark.parametrize("dtype", [Q6, Q5, Q8, Q2])
+def test_decoders_equal_exact_closed_form(dtype):
+    rng = np.random.default_rng(dtype)
+    raw = npref.random_blocks(dtype, 257, rng)
+    ours = oracle.decode(dtype, raw)
+    ref = npref.DECODERS[dtype](raw)
+    assert np.array_equal(bits(ours), bits(ref))
+
+
+@pytest.mark.parametrize("dtype", [Q6, Q5, Q8, Q2])
+def test_decoders_with_extreme_scales(dtype):
+    # subnormal and near-max f16 scales still give the single-rounding value
+    rng = np.random.default_rng(100 + dtype)
+    raw = npref.random_blocks(dtype, 64, rng, scale_exp=(-24, -14))
+    assert np.array_equal(bits(oracle.decode(dtype, raw)), bits(npref.DECODERS[dtype](raw)))
+    raw = npref.random_blocks(dtype, 64, rng, scale_exp=(4, 8))
+    assert np.array_equal(bits(oracle.decode(dtype, raw)), bits(npref.DECODERS[dtype](raw)))
+
+
+def test_q2_k_single_field_blocks():
+    # published GGML block_q2_K: element 128N+32j+16s+l reads bits 2j of qs[32N+16s+l]
+    block = np.zeros(84, np.uint8)
+    block[80:82] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    block[82:84] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    block[0:16] = 1  # scale 1, min 0
+    block[16 + 32 * 1 + 16 * 1 + 3] = 0b10_01_11_00  # N=1, s=1, l=3
+    d = oracle.decode(Q2, block)
+    for j, code in enumerate([0, 3, 1, 2]):
+        assert d[128 + 32 * j + 16 + 3] == code
+    assert np.count_nonzero(d) == 3
+    block[0:16] = 0x20  # scale 0, min 2 -> every weight -0.5*2 = -1
+    assert np.array_equal(oracle.decode(Q2, block), np.full(256, -1.0, np.float32))
+
+
+# ---- matvec -------------------------------------------------------------
+
+def test_matvec_known_matrix():  # spm-qwen3-slice/src/math.rs:62-71
+    w = np.array([[1, 2], [3, 4]], np.float32)
+    assert np.array_equal(oracle.matvec_m1(w, np.array([5, 6], np.float32)), [17.0, 39.0])
+    assert np.array_equal(oracle.matvec_m2(w, np.array([5, 6], np.float32), 1), [17.0, 39.0])
+
+
+def test_matvec_dyadic_exact_in_any_order():
+    rng = np.random.default_rng(7)
+    w = npref.dyadic(rng, (37, 300))
+    x = npref.dyadic(rng, (300,))
+    exact = (w.astype(np.float64) @ x.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(oracle.matvec_m1(w, x), exact)
+    assert np.array_equal(oracle.matvec_m2(w, x, 1), exact)
+
+
+def test_matvec_m1_is_sequential_separately_rounded_fold():
+    rng = np.random.default_rng(8)
+    w = rng.normal(size=(5, 64)).astype(np.float32)
+    x = rng.normal(size=64).astype(np.float32)
+    ref = []
+    for r in range(5):
+        acc = np.float32(-0.0)
+        for c in range(64):
+            acc = np.float32(acc + np.float32(w[r, c] * x[c]))
+        ref.append(acc)
+    assert np.array_equal(bits(oracle.matvec_m1(w, x)), bits(ref))
+
+
+def test_matvec_m2_is_fma_chain():
+    rng = np.random.default_rng(9)
+    w = rng.normal(size=(4, 48)).astype(np.float32)
+    x = rng.normal(size=(2, 48)).astype(np.float32)
+    ref = np.empty(8, np.float32)
+    for p in range(2):
+        for r in range(4):
+            acc = 0.0
+            for c in range(48):  # fma = exact product + one rounding
+                acc = float(np.float32(float(w[r, c]) * float(x[p, c]) + acc))
+            ref[p * 4 + r] = acc
+    assert np.array_equal(bits(oracle.matvec_m2(w, x, 2)), bits(ref))
+
+
+@pytest.mark.parametrize("dtype", [Q6, Q5, Q8, Q2])
+def test_qmatvec_is_decode_then_m1(dtype):
+    rng = np.random.default_rng(20 + dtype)
+    rows, cols = 7, 512
+    raw = npref.random_blocks(dtype, rows * cols // npref.BLOCK_ELEMS[dtype], rng)
+    x = rng.normal(size=(3, cols)).astype(np.float32)
+    w = npref.DECODERS[dtype](raw).reshape(rows, cols)
+    y = oracle.qmatvec(dtype, raw, rows, cols, x, 3, mode=1)
+    ref = np.concatenate([oracle.matvec_m1(w, x[t]) for t in range(3)])
+    assert np.array_equal(bits(y), bits(ref))
+
+
+# ---- integer block dots -------------------------------------------------
+
+def test_quantize_act_closed_form():
+    rng = np.random.default_rng(11)
+    x = rng.normal(size=256).astype(np.float32)
+    x[32:64] = 0.0
+    q, s = oracle.quantize_act(x)
+    xb = x.reshape(-1, 32)
+    amax = np.abs(xb).max(axis=1)
+    s_ref = (amax / np.float32(127)).astype(np.float32)
+    assert np.array_equal(bits(s), bits(s_ref))
+    inv = np.where(s_ref != 0, np.float32(1) / np.where(s_ref != 0, s_ref, 1), 0).astype(np.float32)
+    prod = (xb * inv[:, None]).astype(np.float32)
+    q_ref = np.clip(np.sign(prod) * np.floor(np.abs(prod) + 0.5), -127, 127).astype(np.int8)
+    assert np.array_equal(q, q_ref.reshape(-1))
+    assert np.all(q[32:64] == 0)
+
+
+@pytest.mark.parametrize("dtype", [Q6, Q5, Q8, Q2])
+def test_block_dots_brute_force(dtype):
+    rng = np.random.default_rng(30 + dtype)
+    rows, cols = 5, 512
+    raw = npref.random_blocks(dtype, rows * cols // npref.BLOCK_ELEMS[dtype], rng)
+    xq = rng.integers(-127, 128, size=(2, cols), dtype=np.int8)
+    got = oracle.block_dots(dtype, raw, rows, cols, xq, 2)
+    codes = npref.codes(dtype, raw).reshape(rows, cols)
+    sub = npref.SUB[dtype]
+    ref = np.einsum("rc,tc->trc", codes, xq.astype(np.int64)).reshape(2, rows, cols // sub, sub).sum(-1)
+    assert np.array_equal(got, ref.reshape(-1).astype(np.int32))
+
+
+# ---- norms, rope, softmax, attention, routing ---------------------------
+
+def test_rms_norm_known_vector():  # spm-qwen3-slice/src/math.rs:54-60
+    r = oracle.rms_norm(np.array([3, 4], np.float32), np.array([1, 2], np.float32), 1e-6)
+    assert abs(r[0] - 0.848528) < 1e-5 and abs(r[1] - 2.2627416) < 1e-5
+
+
+def test_rope_identity_and_known_pair():  # spm-qwen3-slice/src/attention.rs:85-99
+    head = np.arange(128, dtype=np.float32)
+    for kind in ("qwen3", "fma", "interleaved"):
+        assert np.array_equal(bits(oracle.rope(kind, head, 0, 1e6)), bits(head))
+    h = np.zeros(128, np.float32)
+    h[0] = 1.0
+    r = oracle.rope("qwen3", h, 1, 1e6)
+    assert abs(r[0] - math.cos(1.0)) < 1e-6 and abs(r[64] - math.sin(1.0)) < 1e-6
+    r = oracle.rope("fma", h, 1, 1e5)
+    assert abs(r[0] - math.cos(1.0)) < 1e-6 and abs(r[64] - math.sin(1.0)) < 1e-6
+    r = oracle.rope("interleaved", h, 1, 1.5e6)
+    assert abs(r[0] - math.cos(1.0)) < 1e-6 and abs(r[1] - math.sin(1.0)) < 1e-6
+
+
+def test_rope_preserves_pair_norms():
+    rng = np.random.default_rng(12)
+    h = rng.normal(size=64).astype(np.float32)
+    r = oracle.rope("qwen3", h, 517, 1e6)
+    n0 = h[:32] ** 2 + h[32:] ** 2
+    n1 = r[:32] ** 2 + r[32:] ** 2
+    assert np.allclose(n0, n1, rtol=1e-5)
+
+
+def test_softmax_equal_large_values_exact_half():  # attention.rs:96-98, granite math.rs:46-54
+    assert np.array_equal(bits(oracle.softmax([1000.0, 1000.0])), bits([0.5, 0.5]))
+    assert np.array_equal(bits(oracle.softmax([1000.0, 1000.0], recip=True)), bits([0.5, 0.5]))
+
+
+def test_top_k_tie_order():  # spm-qwen3-slice/src/math.rs:67-70
+    assert oracle.top_k(np.array([1, 3, 3, 2], np.float32), 3) == [(1, 3.0), (2, 3.0), (3, 2.0)]
+
+
+def test_olmoe_route_picks_top_eight():  # spm-granite-moe/src/moe.rs:183-191
+    ids, w = oracle.route(np.arange(64, dtype=np.float32), 8)
+    assert list(ids) == [63, 62, 61, 60, 59, 58, 57, 56]
+    assert abs(float(w.sum()) - 1.0) < 1e-6 and np.all(np.diff(w) <= 0)
+
+
+def test_gqa_maps_four_query_heads_to_each_kv_head():  # attention.rs:101-118
+    heads, kvh, hd = 32, 8, 128
+    q = np.zeros(heads * hd, np.float32)
+    keys = np.zeros((1, kvh * hd), np.float32)
+    values = np.repeat(np.arange(kvh, dtype=np.float32), hd)[None, :]
+    for variant in (0, 1, 2):
+        out = oracle.attend(q, keys, values, 1, heads, kvh, hd, variant, 11.313708)
+        for h in range(heads):
+            assert abs(out[h * hd] - h // 4) < np.finfo(np.float32).eps
+
+
+def test_later_key_cannot_affect_earlier_output():  # attention.rs:120-131
+    heads, kvh, hd = 4, 2, 64
+    q = np.zeros(heads * hd, np.float32)
+    keys = np.zeros((2, kvh * hd), np.float32)
+    values = np.ones((2, kvh * hd), np.float32)
+    values[1] = 99.0
+    out = oracle.attend(q, keys, values, 1, heads, kvh, hd, 0, 8.0)  # prefix of one position
+    assert np.array_equal(out, np.ones(heads * hd, np.float32))
+
+
+def test_argmax_tie_rules():  # math.rs:38-48 vs batching.rs:111-123
+    v = np.array([0.5, 2.0, 1.0, 2.0, -1.0], np.float32)
+    assert oracle.argmax(v, tie_last=False) == 1
+    assert oracle.argmax(v, tie_last=True) == 3
+
+
+def test_dense_step_batched_equals_alone():  # spm-batch/tests/batching.rs:128-145
+    rng = np.random.default_rng(5)
+    cfg = oracle.DenseCfg(hidden=64, heads=2, kv_heads=1, head_dim=32, ffn=96, vocab=50, layers=2, context=8,
+                          rope_theta=1e5, eps=1e-5, style=oracle.STYLE_SMOL, dtype=Q8, kv_f16=0, tied=1,
+                          qk_norm=0)
+    lb = oracle.load().or_dense_layer_bytes(cfg)
+    w = {
+        "layers": npref.random_blocks(Q8, lb * 2 // 34, rng),
+        "embed": npref.random_blocks(Q8, 50 * 64 // 32, rng),
+        "attn_norm": np.ones(128, np.float32), "ffn_norm": np.ones(128, np.float32),
+        "q_norm": np.ones(64, np.float32), "k_norm": np.ones(64, np.float32), "out_norm": np.ones(64, np.float32),
+    }
+    w["output"] = w["embed"]
+    both = oracle.DenseOracle(cfg, w, 2)
+    alone = oracle.DenseOracle(cfg, w, 1)
+    toks = [(3, 7), (11, 2), (5, 5)]
+    for a, b in toks:
+        lb2 = both.step([a, b])
+        la = alone.step([a])
+        assert np.array_equal(bits(lb2[0]), bits(la[0]))
