@@ -42,13 +42,15 @@ struct AttnArgs {
 
 template <int HD> __device__ __forceinline__ float rotate_pair_first(float l, float r, float2 cs, int fma_form)
 {
-    if (fma_form) return __builtin_fmaf(l, cs.x, -__fmul_rn(r, cs.y));
-    return __fsub_rn(__fmul_rn(l, cs.x), __fmul_rn(r, cs.y));
+#pragma clang fp contract(off)
+    if (fma_form) return __builtin_fmaf(l, cs.x, -(r * cs.y));
+    return l * cs.x - r * cs.y;
 }
 template <int HD> __device__ __forceinline__ float rotate_pair_second(float l, float r, float2 cs, int fma_form)
 {
-    if (fma_form) return __builtin_fmaf(l, cs.y, __fmul_rn(r, cs.x));
-    return __fadd_rn(__fmul_rn(r, cs.x), __fmul_rn(l, cs.y));
+#pragma clang fp contract(off)
+    if (fma_form) return __builtin_fmaf(l, cs.y, r * cs.x);
+    return r * cs.x + l * cs.y;
 }
 
 // Norm + rotate one head of HD values held in LDS by the first HD/2 threads of

@@ -92,10 +92,23 @@ struct Grp {
     float mul, add;
 };
 
-// Exact weight i (0..7) of a group.
+// Weight i (0..7) of a group for the matvec: one fma, exact value.  For the
+// biased formats (Q6_K, Q8_0) a zero weight comes out +0.0 where the
+// reference's d*sc*(q-32) may give -0.0; the sign of a zero weight cannot
+// change a dot product, so the matvec keeps the single instruction.
 __device__ __forceinline__ float grp_weight(const Grp &g, int i)
 {
     return __builtin_fmaf(byte_f(i < 4 ? g.q0 : g.q1, i & 3), g.mul, g.add);
+}
+
+// Weight i with the reference's exact bits, signed zeros included:
+// Q6_K d*sc*(q-32) and Q8_0 d*i8 as (code - BIAS) * mul; Q5_K / Q2_K
+// d*sc*q - dmin*m as one fma of the exact product and the exact min term.
+template <int BIAS> __device__ __forceinline__ float grp_weight_exact(const Grp &g, int i)
+{
+    const float b = byte_f(i < 4 ? g.q0 : g.q1, i & 3);
+    if (BIAS) return __fmul_rn(__fsub_rn(b, (float)BIAS), g.mul);
+    return __builtin_fmaf(b, g.mul, g.add);
 }
 
 // Code i (0..7) of a group minus the format's bias: the signed integer the

@@ -263,7 +263,7 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint8_t *embed, s
     for (int g = 0; g < F::G; ++g) {
         const Grp gp = F::group(raw, sub, g);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) out[F::col(sub, g) + i] = grp_weight(gp, i);
+        for (int i = 0; i < 8; ++i) out[F::col(sub, g) + i] = grp_weight_exact<F::BIAS>(gp, i);
     }
 }
 

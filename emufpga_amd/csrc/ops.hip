@@ -46,6 +46,7 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(float *x, int n_tok, int
                                                         const uint32_t *positions, const float2 *table,
                                                         int table_positions, int style)
 {
+#pragma clang fp contract(off)
     const int half = hd / 2;
     const size_t id = (size_t)blockIdx.x * kThreads + threadIdx.x;
     if (id >= (size_t)n_tok * heads * half) return;
@@ -59,8 +60,8 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(float *x, int n_tok, int
     const int a = style == EMU_ROPE_NEOX ? i : 2 * i;
     const int b = style == EMU_ROPE_NEOX ? i + half : 2 * i + 1;
     const float l = head[a], r = head[b];
-    head[a] = __fsub_rn(__fmul_rn(l, cs.x), __fmul_rn(r, cs.y));
-    head[b] = __fadd_rn(__fmul_rn(r, cs.x), __fmul_rn(l, cs.y));
+    head[a] = l * cs.x - r * cs.y;
+    head[b] = r * cs.x + l * cs.y;
 }
 
 // attend_cached (spm-kv/src/attend.rs:37-94): one workgroup per query head.

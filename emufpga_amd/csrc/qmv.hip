@@ -182,7 +182,7 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(const uint8_t *src, s
         const Grp gp = F::group(raw, sub, g);
         float w[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) w[i] = grp_weight(gp, i);
+        for (int i = 0; i < 8; ++i) w[i] = grp_weight_exact<F::BIAS>(gp, i);
         float4 *dst = reinterpret_cast<float4 *>(out + blk * F::BE + F::col(sub, g));
         dst[0] = make_float4(w[0], w[1], w[2], w[3]);
         dst[1] = make_float4(w[4], w[5], w[6], w[7]);

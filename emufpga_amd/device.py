@@ -2,6 +2,7 @@
 from __future__ import annotations
 
 import ctypes as C
+import sys
 
 import numpy as np
 
@@ -19,10 +20,15 @@ class Context:
         self.h = h
         self._live = True
 
+    @property
+    def live(self) -> bool:
+        return self._live
+
     def close(self) -> None:
+        """Destroy the context; buffers, models and sessions made from it become inert."""
         if self._live:
-            self.lib.emu_ctx_destroy(self.h)
             self._live = False
+            self.lib.emu_ctx_destroy(self.h)
 
     def __enter__(self):
         return self
@@ -30,11 +36,12 @@ class Context:
     def __exit__(self, *exc):
         self.close()
 
-    def __del__(self):  # pragma: no cover - interpreter teardown
-        try:
-            self.close()
-        except Exception:
-            pass
+    def __del__(self):  # pragma: no cover - never call into HIP during interpreter teardown
+        if not sys.is_finalizing():
+            try:
+                self.close()
+            except Exception:
+                pass
 
     def check(self, status: int, what: str) -> None:
         check(status, what, self.h)
@@ -86,15 +93,16 @@ class DeviceBuffer:
         return self.ptr.value
 
     def free(self) -> None:
-        if self.ptr is not None and self.ptr.value:
+        if self.ptr is not None and self.ptr.value and self.ctx.live:
             self.ctx.lib.emu_free(self.ctx.h, self.ptr)
-            self.ptr = None
+        self.ptr = None
 
     def __del__(self):  # pragma: no cover
-        try:
-            self.free()
-        except Exception:
-            pass
+        if not sys.is_finalizing():
+            try:
+                self.free()
+            except Exception:
+                pass
 
     def write(self, arr: np.ndarray, offset: int = 0) -> None:
         arr = np.ascontiguousarray(arr)

@@ -9,6 +9,7 @@ own position with its own KV cache (Client, src/session.rs:13-38), and
 from __future__ import annotations
 
 import ctypes as C
+import sys
 from dataclasses import dataclass
 
 import numpy as np
@@ -67,15 +68,16 @@ class Model:
         self.h = h
 
     def close(self) -> None:
-        if self.h is not None:
+        if self.h is not None and self.ctx.live:
             self.ctx.lib.emu_model_destroy(self.h)
-            self.h = None
+        self.h = None
 
     def __del__(self):  # pragma: no cover
-        try:
-            self.close()
-        except Exception:
-            pass
+        if not sys.is_finalizing():
+            try:
+                self.close()
+            except Exception:
+                pass
 
     def synth(self, seed: int) -> None:
         self.ctx.check(self.ctx.lib.emu_model_synth(self.h, seed), "emu_model_synth")
@@ -135,15 +137,16 @@ class Session:
         self.h = h
 
     def close(self) -> None:
-        if self.h is not None:
+        if self.h is not None and self.ctx.live:
             self.ctx.lib.emu_session_destroy(self.h)
-            self.h = None
+        self.h = None
 
     def __del__(self):  # pragma: no cover
-        try:
-            self.close()
-        except Exception:
-            pass
+        if not sys.is_finalizing():
+            try:
+                self.close()
+            except Exception:
+                pass
 
     def reset(self) -> None:
         self.ctx.check(self.ctx.lib.emu_session_reset(self.h), "emu_session_reset")
