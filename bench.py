@@ -128,6 +128,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-batch8", action="store_true")
     ap.add_argument("--roofline-rounds", type=int, default=8)
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only time the dominant kernel (the fused gate|up matvec over all layers); for profiling")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (the decode path is "
@@ -143,6 +145,13 @@ def main() -> int:
     model.synth(20260101)
     weight_bytes = model.weight_bytes()
     log(f"synthesised {weight_bytes / 1e9:.3f} GB of Q6_K weights in {time.perf_counter() - t0:.1f} s")
+
+    if args.kernel_only:
+        ku_ms, ku_bytes, launches = time_gate_up(ctx, model, args.roofline_rounds)
+        achieved = ku_bytes / (ku_ms / 1e3) / 1e9
+        print(json.dumps({"kernel": "gate_up", "avg_launch_us": round(ku_ms * 1e3, 3), "launches": launches,
+                          "achieved_gbs": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4)}), flush=True)
+        return 0
 
     rng = np.random.default_rng(42)
     results = {}

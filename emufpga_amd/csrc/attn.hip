@@ -1,27 +1,37 @@
 // attn.hip -- fused decode attention for the decode step.
 //
-// One workgroup per (context chunk, kv head, client).  Each workgroup
-//   1. rebuilds the rotated queries of its GQ = heads/kv_heads query heads from
-//      the projection output (per-head RMSNorm when the model has QK-norm, then
-//      RoPE from the host-built table: spm-qwen3-slice/src/attention.rs:27-34);
-//   2. if its chunk holds the new position, rotates the new key, rounds key and
-//      value to the cache type and appends them (KvCache::append,
-//      spm-kv/src/cache.rs:49-58) -- the same values it then attends with;
-//   3. scores its chunk's positions (one position per thread, the query heads
-//      broadcast from LDS), takes the chunk max and exp-sum, and accumulates
-//      the un-normalised weighted values (head lanes x position halves);
-//   4. writes (max, sum, partial) per query head; the last workgroup of the
-//      (client, kv head) to finish merges every chunk (flash-decoding) and
-//      resets the arrival counter for the next step.
+// One workgroup (4 wavefronts) per (64-position context chunk, kv head,
+// client).  Each workgroup
+//   1. rebuilds the rotated queries of its GQ = heads/kv_heads query heads
+//      from the projection output, one head per wavefront: per-head RMSNorm
+//      when the model has QK-norm, then RoPE from the host-built table
+//      (spm-qwen3-slice/src/attention.rs:27-34, spm-kv/src/attend.rs:13-19);
+//   2. if its chunk holds the new position, also rotates the new key, rounds
+//      key and value to the cache type and appends them (KvCache::append,
+//      spm-kv/src/cache.rs:49-58) -- and attends with exactly those values;
+//   3. scores its 64 positions: wavefront w takes 16 of them, lanes split the
+//      head dimension, so every K and V row is one coalesced load per lane and
+//      all 32 of a lane's loads are in flight at once; the per-lane partial
+//      dots of (position, head) pairs are combined by a butterfly
+//      reduce-scatter across the wavefront (one shuffle per pair);
+//   4. softmax per head over the chunk (max, exp, sum), weighted values,
+//      wavefronts merged through LDS;
+//   5. writes (max, sum, unnormalised output) per query head; the last
+//      workgroup of the (client, kv head) to finish merges all chunks
+//      (flash-decoding) and resets the arrival counter for the next step.
 // Cache layout: [client][layer][kv_head][context][head_dim], f16 or f32.
 #include "internal.hpp"
 
 #include <math.h>
+#include <type_traits>
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kChunk = 256; // positions per workgroup: one per thread
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * EMU_WAVE;
+constexpr int kPP = 16;              // positions per wavefront
+constexpr int kChunk = kWaves * kPP; // positions per workgroup
+constexpr int kMergeChunks = 256;    // chunk weights kept in LDS by the merge
 
 struct AttnArgs {
     const float *qkv;       // [client][q_width + 2*kv_width]
@@ -30,9 +40,10 @@ struct AttnArgs {
     const float2 *rope;     // [context][hd/2] (cos, sin)
     const float *q_norm, *k_norm; // per-layer gains or null
     float eps;
-    float score_mul;        // score = dot * score_mul (or / score_div)
-    float score_div;        // > 0 selects division
+    float score_mul;        // score = dot * score_mul, or dot / score_div when score_div > 0
+    float score_div;
     int rope_fma;           // spm-ops form: fma(x, cos, -(y*sin))
+    int interleaved;        // adjacent-pair RoPE (spm-granite-moe/src/attention.rs:12-26)
     int heads, kv_heads, layers, layer, context;
     float *partial;         // [client][head][max_chunks][hd + 2]
     uint32_t *counters;     // [client][kv_head]
@@ -40,262 +51,379 @@ struct AttnArgs {
     float *out;             // [client][heads * hd]
 };
 
-template <int HD> __device__ __forceinline__ float rotate_pair_first(float l, float r, float2 cs, int fma_form)
+__device__ __forceinline__ float wave_max(float v)
 {
-#pragma clang fp contract(off)
-    if (fma_form) return __builtin_fmaf(l, cs.x, -(r * cs.y));
-    return l * cs.x - r * cs.y;
-}
-template <int HD> __device__ __forceinline__ float rotate_pair_second(float l, float r, float2 cs, int fma_form)
-{
-#pragma clang fp contract(off)
-    if (fma_form) return __builtin_fmaf(l, cs.y, r * cs.x);
-    return r * cs.x + l * cs.y;
-}
-
-// Norm + rotate one head of HD values held in LDS by the first HD/2 threads of
-// a wave-aligned group.  src/dst may alias.
-template <int HD>
-__device__ void prep_head(const float *src, float *dst, const float *gain, float eps, float2 const *rope_row,
-                          int fma_form, int tid, float *red)
-{
-    // Sum of squares over the head (threads 0..HD-1 of this call each own one).
-    float v = tid < HD ? src[tid] : 0.0f;
-    float s = v * v;
-    s = wave_sum(s);
-    if (HD > 64) {
-        if ((tid & 63) == 0 && tid < HD) red[tid >> 6] = s;
-        __syncthreads();
-        s = 0.0f;
 #pragma unroll
-        for (int i = 0; i < HD / 64; ++i) s += red[i];
-        __syncthreads();
-    }
-    float scale = 1.0f;
-    if (gain) scale = 1.0f / sqrtf(s / (float)HD + eps);
-    const float nv = gain && tid < HD ? __fmul_rn(__fmul_rn(v, scale), gain[tid]) : v;
-    __syncthreads();
-    if (tid < HD) dst[tid] = nv;
-    __syncthreads();
-    if (tid < HD / 2) {
-        const float2 cs = rope_row[tid];
-        const float l = dst[tid], r = dst[tid + HD / 2];
-        const float a = rotate_pair_first<HD>(l, r, cs, fma_form);
-        const float b = rotate_pair_second<HD>(l, r, cs, fma_form);
-        dst[tid] = a;
-        dst[tid + HD / 2] = b;
-    }
-    __syncthreads();
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, EMU_WAVE));
+    return v;
 }
 
-template <int HD, bool F16>
+// Rotation of one pair, with the reference's roundings: separate products and
+// sum (spm-qwen3-slice/src/attention.rs:22-23) or the fma form of
+// spm-ops/src/attention.rs:29-30.
+__device__ __forceinline__ void rotate(float &l, float &r, float2 cs, int fma_form)
+{
+#pragma clang fp contract(off)
+    float a, b;
+    if (fma_form) {
+        a = __builtin_fmaf(l, cs.x, -(r * cs.y));
+        b = __builtin_fmaf(l, cs.y, r * cs.x);
+    } else {
+        a = l * cs.x - r * cs.y;
+        b = r * cs.x + l * cs.y;
+    }
+    l = a;
+    r = b;
+}
+
+// One wavefront: RMSNorm (optional) + RoPE of one head of HD values from
+// global memory into dst (LDS).  Lanes own rotation pairs.
+template <int HD>
+__device__ __forceinline__ void prep_head(const float *src, float *dst, const float *gain, float eps,
+                                          const float2 *rope_row, int fma_form, int interleaved, int lane)
+{
+    constexpr int NP = HD / 2;
+    constexpr int PPL = (NP + EMU_WAVE - 1) / EMU_WAVE;
+    float a[PPL], b[PPL];
+    int ia[PPL], ib[PPL];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) {
+        const int i = lane + EMU_WAVE * j;
+        const bool act = i < NP;
+        ia[j] = interleaved ? 2 * i : i;
+        ib[j] = interleaved ? 2 * i + 1 : i + NP;
+        a[j] = act ? src[ia[j]] : 0.0f;
+        b[j] = act ? src[ib[j]] : 0.0f;
+        ss = __builtin_fmaf(a[j], a[j], ss);
+        ss = __builtin_fmaf(b[j], b[j], ss);
+    }
+    if (gain) {
+        const float scale = 1.0f / sqrtf(wave_sum(ss) / (float)HD + eps);
+#pragma unroll
+        for (int j = 0; j < PPL; ++j) {
+            if (lane + EMU_WAVE * j < NP) {
+                a[j] = __fmul_rn(__fmul_rn(a[j], scale), gain[ia[j]]);
+                b[j] = __fmul_rn(__fmul_rn(b[j], scale), gain[ib[j]]);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) {
+        const int i = lane + EMU_WAVE * j;
+        if (i < NP) {
+            rotate(a[j], b[j], rope_row[i], fma_form);
+            dst[ia[j]] = a[j];
+            dst[ib[j]] = b[j];
+        }
+    }
+}
+
+// Butterfly reduce-scatter of N (<= 64, power of two) per-lane values:
+// afterwards lane l holds the wavefront-wide sum of value (l >> log2(64/N)).
+// Each step halves the values a lane keeps, trading the other half with the
+// partner lane `OFF` away; once one value is left, plain xor-sums finish.
+template <int N, int OFF>
+__device__ __forceinline__ void reduce_scatter_step(float *v, int lane)
+{
+    if constexpr (OFF > 0) {
+        if constexpr (N > 1) {
+            constexpr int H = N / 2;
+            const bool up = (lane & OFF) != 0;
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                const float keep = up ? v[i + H] : v[i];
+                const float send = up ? v[i] : v[i + H];
+                v[i] = keep + __shfl_xor(send, OFF, EMU_WAVE);
+            }
+            reduce_scatter_step<H, OFF / 2>(v, lane);
+        } else {
+            v[0] += __shfl_xor(v[0], OFF, EMU_WAVE);
+            reduce_scatter_step<1, OFF / 2>(v, lane);
+        }
+    }
+}
+
+template <int NV>
+__device__ __forceinline__ float reduce_scatter(float (&v)[NV], int lane)
+{
+    reduce_scatter_step<NV, 32>(v, lane);
+    return v[0];
+}
+
+template <class T, int N> struct VecLoad;
+template <> struct VecLoad<__half, 1> { using type = uint16_t; };
+template <> struct VecLoad<__half, 2> { using type = uint32_t; };
+template <> struct VecLoad<__half, 4> { using type = uint2; };
+template <> struct VecLoad<float, 1> { using type = float; };
+template <> struct VecLoad<float, 2> { using type = float2; };
+template <> struct VecLoad<float, 4> { using type = float4; };
+
+template <int EPL, bool F16, class V>
+__device__ __forceinline__ void unpack_row(const V &raw, float (&out)[EPL])
+{
+    if constexpr (F16) {
+        const uint16_t *h = reinterpret_cast<const uint16_t *>(&raw);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) out[e] = __half2float(__ushort_as_half(h[e]));
+    } else {
+        const float *f = reinterpret_cast<const float *>(&raw);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) out[e] = f[e];
+    }
+}
+
+template <int HD, bool F16, int GQP>
 __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
 {
     using kv_t = typename std::conditional<F16, __half, float>::type;
+    constexpr int EPL = HD / EMU_WAVE;          // head elements per lane
+    constexpr int GH = GQP < 4 ? GQP : 4;       // heads per scoring pass
+    constexpr int NV = kPP * GH;                // values per reduce-scatter
+    using vec_t = typename VecLoad<kv_t, EPL>::type;
+
     const int chunk = blockIdx.x, kvh = blockIdx.y, client = blockIdx.z;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & (EMU_WAVE - 1), w = tid / EMU_WAVE;
     const int pos = (int)a.positions[client];
     const int n = pos + 1;
     const int n_chunks = (n + kChunk - 1) / kChunk;
     if (chunk >= n_chunks) return; // uniform per workgroup
     const int GQ = a.heads / a.kv_heads;
 
-    __shared__ float q_s[8][HD];      // GQ <= 8
+    __shared__ float q_s[GQP][HD];
     __shared__ float knew[HD], vnew[HD];
-    __shared__ float sc[8][kChunk];
-    __shared__ float red[8];
-    __shared__ float accs[2][8][HD];
+    __shared__ float sc[GQP][kChunk];
+    __shared__ float mh[GQP], lh[GQP];
+    __shared__ float accs[kWaves][GQP][HD];
+    __shared__ uint32_t arrived;
 
     const int qw = a.heads * HD, kw = a.kv_heads * HD;
     const float *row = a.qkv + (size_t)client * (qw + 2 * kw);
     const float2 *rope_row = a.rope + (size_t)pos * (HD / 2);
     const float *qn = a.q_norm ? a.q_norm + (size_t)a.layer * HD : nullptr;
     const float *kn = a.k_norm ? a.k_norm + (size_t)a.layer * HD : nullptr;
-
-    for (int g = 0; g < GQ; ++g) {
-        const int head = kvh * GQ + g;
-        if (tid < HD) q_s[g][tid] = row[head * HD + tid];
-        __syncthreads();
-        prep_head<HD>(q_s[g], q_s[g], qn, a.eps, rope_row, a.rope_fma, tid, red);
-    }
-
-    const size_t cache_base = (((size_t)client * a.layers + a.layer) * a.kv_heads + kvh) * (size_t)a.context * HD;
+    const size_t cache_base =
+        (((size_t)client * a.layers + a.layer) * a.kv_heads + kvh) * (size_t)a.context * HD;
     kv_t *kc = static_cast<kv_t *>(a.k_cache) + cache_base;
     kv_t *vc = static_cast<kv_t *>(a.v_cache) + cache_base;
     const int p0 = chunk * kChunk;
     const bool owner = pos >= p0 && pos < p0 + kChunk;
-    if (owner) {
-        if (tid < HD) knew[tid] = row[qw + kvh * HD + tid];
-        __syncthreads();
-        prep_head<HD>(knew, knew, kn, a.eps, rope_row, a.rope_fma, tid, red);
-        if (tid < HD) {
-            const float kv = knew[tid];
-            const float vv = row[qw + kw + kvh * HD + tid];
-            kv_t kq, vq;
-            if constexpr (F16) {
-                kq = (kv_t)__float2half_rn(kv);
-                vq = (kv_t)__float2half_rn(vv);
-            } else {
-                kq = (kv_t)kv;
-                vq = (kv_t)vv;
-            }
-            kc[(size_t)pos * HD + tid] = kq;
-            vc[(size_t)pos * HD + tid] = vq;
-            knew[tid] = (float)kq; // attend with the cached (rounded) values
-            vnew[tid] = (float)vq;
+
+    // This wavefront's 16 positions: issue every K and V row load now.
+    const int pw = p0 + w * kPP;
+    vec_t kr[kPP], vr[kPP];
+#pragma unroll
+    for (int pp = 0; pp < kPP; ++pp) {
+        const int p = pw + pp;
+        if (p < n && p != pos) {
+            kr[pp] = *reinterpret_cast<const vec_t *>(kc + (size_t)p * HD + lane * EPL);
+            vr[pp] = *reinterpret_cast<const vec_t *>(vc + (size_t)p * HD + lane * EPL);
+        } else {
+            kr[pp] = vec_t{};
+            vr[pp] = vec_t{};
         }
-        __syncthreads();
     }
 
-    // Scores: thread per position.
-    const int p = p0 + tid;
-    const bool live = p < n;
-    float s[8];
-#pragma unroll
-    for (int g = 0; g < 8; ++g) s[g] = -INFINITY;
-    if (live) {
-        float dot[8];
-#pragma unroll
-        for (int g = 0; g < 8; ++g) dot[g] = 0.0f;
-        if (p == pos) {
-            for (int i = 0; i < HD; ++i) {
-                const float kv = knew[i];
-#pragma unroll
-                for (int g = 0; g < 8; ++g)
-                    if (g < GQ) dot[g] = __builtin_fmaf(q_s[g][i], kv, dot[g]);
-            }
-        } else {
-            const kv_t *kr = kc + (size_t)p * HD;
-            for (int i = 0; i < HD; i += 8) {
-                float kv[8];
-                if constexpr (F16) {
-                    const uint4 raw = *reinterpret_cast<const uint4 *>(kr + i);
-                    const __half2 *h2 = reinterpret_cast<const __half2 *>(&raw);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const float2 f = __half22float2(h2[j]);
-                        kv[2 * j] = f.x;
-                        kv[2 * j + 1] = f.y;
-                    }
-                } else {
-                    const float4 x0 = *reinterpret_cast<const float4 *>(kr + i);
-                    const float4 x1 = *reinterpret_cast<const float4 *>(kr + i + 4);
-                    kv[0] = x0.x; kv[1] = x0.y; kv[2] = x0.z; kv[3] = x0.w;
-                    kv[4] = x1.x; kv[5] = x1.y; kv[6] = x1.z; kv[7] = x1.w;
-                }
-#pragma unroll
-                for (int g = 0; g < 8; ++g)
-                    if (g < GQ)
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) dot[g] = __builtin_fmaf(q_s[g][i + j], kv[j], dot[g]);
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < 8; ++g)
-            if (g < GQ) s[g] = a.score_div > 0.0f ? dot[g] / a.score_div : dot[g] * a.score_mul;
+    // 1-2. Rotated queries (and the new key) into LDS: item i on wavefront i % 4.
+    const int items = GQ + (owner ? 1 : 0);
+    for (int it = w; it < items; it += kWaves) {
+        if (it < GQ)
+            prep_head<HD>(row + (kvh * GQ + it) * HD, q_s[it], qn, a.eps, rope_row, a.rope_fma, a.interleaved,
+                          lane);
+        else
+            prep_head<HD>(row + qw + kvh * HD, knew, kn, a.eps, rope_row, a.rope_fma, a.interleaved, lane);
     }
-    // Chunk max and exp per head.
-    float m[8];
-#pragma unroll
-    for (int g = 0; g < 8; ++g) {
-        if (g >= GQ) break;
-        float v = s[g];
-        for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-        if ((tid & 63) == 0) red[tid >> 6] = v;
-        __syncthreads();
-        m[g] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        __syncthreads();
-        sc[g][tid] = live ? expf(s[g] - m[g]) : 0.0f;
+    for (int g = GQ + w; g < GQP; g += kWaves)
+        for (int e = lane; e < HD; e += EMU_WAVE) q_s[g][e] = 0.0f;
+    __syncthreads();
+    if (owner && tid < HD) {
+        const float kv = knew[tid];
+        const float vv = row[qw + kw + kvh * HD + tid];
+        kv_t kq, vq;
+        if constexpr (F16) {
+            kq = __float2half_rn(kv);
+            vq = __float2half_rn(vv);
+        } else {
+            kq = kv;
+            vq = vv;
+        }
+        kc[(size_t)pos * HD + tid] = kq;
+        vc[(size_t)pos * HD + tid] = vq;
+        knew[tid] = (float)kq; // attend with the cached (rounded) values
+        vnew[tid] = (float)vq;
     }
     __syncthreads();
-    float l[8];
-#pragma unroll
-    for (int g = 0; g < 8; ++g) {
-        if (g >= GQ) break;
-        float v = wave_sum(sc[g][tid]);
-        if ((tid & 63) == 0) red[tid >> 6] = v;
-        __syncthreads();
-        l[g] = (red[0] + red[1]) + (red[2] + red[3]);
-        __syncthreads();
-    }
 
-    // Weighted values: thread = (lane d, half of the chunk's positions).
-    const int cnt = min(kChunk, n - p0);
-    for (int d0 = 0; d0 < HD; d0 += kThreads / 2) {
-        const int d = d0 + (tid % (kThreads / 2));
-        const int halfsel = tid / (kThreads / 2);
-        float acc[8];
+    // 3. Scores.
+    float qreg[GQP][EPL];
 #pragma unroll
-        for (int g = 0; g < 8; ++g) acc[g] = 0.0f;
-        if (d < HD) {
-            for (int i = halfsel; i < cnt; i += 2) {
-                const int pp = p0 + i;
-                const float vv = pp == pos ? vnew[d] : (float)vc[(size_t)pp * HD + d];
+    for (int g = 0; g < GQP; ++g)
 #pragma unroll
-                for (int g = 0; g < 8; ++g)
-                    if (g < GQ) acc[g] = __builtin_fmaf(sc[g][i], vv, acc[g]);
-            }
+        for (int e = 0; e < EPL; ++e) qreg[g][e] = q_s[g][lane * EPL + e];
+    float kf[kPP][EPL];
 #pragma unroll
-            for (int g = 0; g < 8; ++g)
-                if (g < GQ) accs[halfsel][g][d] = acc[g];
+    for (int pp = 0; pp < kPP; ++pp) {
+        if (pw + pp == pos) {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) kf[pp][e] = knew[lane * EPL + e];
+        } else {
+            unpack_row<EPL, F16>(kr[pp], kf[pp]);
         }
-        __syncthreads();
-        if (halfsel == 0 && d < HD) {
-#pragma unroll
-            for (int g = 0; g < 8; ++g)
-                if (g < GQ) accs[0][g][d] = accs[0][g][d] + accs[1][g][d];
-        }
-        __syncthreads();
     }
+    constexpr int SHIFT = NV >= 64 ? 0 : (NV == 32 ? 1 : 2);
+#pragma unroll
+    for (int pass = 0; pass < GQP / GH; ++pass) {
+        float v[NV];
+#pragma unroll
+        for (int pp = 0; pp < kPP; ++pp)
+#pragma unroll
+            for (int gh = 0; gh < GH; ++gh) {
+                float d = 0.0f;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) d = __builtin_fmaf(qreg[pass * GH + gh][e], kf[pp][e], d);
+                v[pp * GH + gh] = d;
+            }
+        const float dot = reduce_scatter<NV>(v, lane);
+        if ((lane & ((1 << SHIFT) - 1)) == 0) {
+            const int idx = lane >> SHIFT;
+            const int pp = idx / GH, g = pass * GH + idx % GH;
+            const int p = pw + pp;
+            const float s = a.score_div > 0.0f ? dot / a.score_div : dot * a.score_mul;
+            sc[g][w * kPP + pp] = p < n ? s : -INFINITY;
+        }
+    }
+    __syncthreads();
+
+    // 4. Softmax over the chunk, one head per wavefront.
+    for (int g = w; g < GQ; g += kWaves) {
+        const float s = sc[g][lane];
+        const float m = wave_max(s);
+        const float e = s == -INFINITY ? 0.0f : expf(s - m);
+        const float l = wave_sum(e);
+        sc[g][lane] = e;
+        if (lane == 0) {
+            mh[g] = m;
+            lh[g] = l;
+        }
+    }
+    __syncthreads();
+
+    float acc[GQP][EPL];
+#pragma unroll
+    for (int g = 0; g < GQP; ++g)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
+#pragma unroll
+    for (int pp = 0; pp < kPP; ++pp) {
+        const int p = pw + pp;
+        float vf[EPL];
+        if (p == pos) {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) vf[e] = vnew[lane * EPL + e];
+        } else {
+            unpack_row<EPL, F16>(vr[pp], vf);
+        }
+#pragma unroll
+        for (int g = 0; g < GQP; ++g) {
+            if (g < GQ) {
+                const float wgt = sc[g][w * kPP + pp];
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) acc[g][e] = __builtin_fmaf(wgt, vf[e], acc[g][e]);
+            }
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < GQP; ++g)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) accs[w][g][lane * EPL + e] = acc[g][e];
+    __syncthreads();
 
     float *outp = a.out + (size_t)client * qw;
     if (n_chunks == 1) {
         for (int idx = tid; idx < GQ * HD; idx += kThreads) {
             const int g = idx / HD, d = idx % HD;
-            outp[(kvh * GQ + g) * HD + d] = accs[0][g][d] / l[g];
+            const float o = (accs[0][g][d] + accs[1][g][d]) + (accs[2][g][d] + accs[3][g][d]);
+            outp[(kvh * GQ + g) * HD + d] = o / lh[g];
         }
         return;
     }
-    // Partial for the merge.
+    // 5. Partial for the merge.
     for (int idx = tid; idx < GQ * (HD + 2); idx += kThreads) {
         const int g = idx / (HD + 2), j = idx % (HD + 2);
         const int head = kvh * GQ + g;
         float *pp = a.partial + (((size_t)client * a.heads + head) * a.max_chunks + chunk) * (HD + 2);
-        pp[j] = j < HD ? accs[0][g][j] : (j == HD ? m[g] : l[g]);
+        float val;
+        if (j < HD)
+            val = (accs[0][g][j] + accs[1][g][j]) + (accs[2][g][j] + accs[3][g][j]);
+        else
+            val = j == HD ? mh[g] : lh[g];
+        pp[j] = val;
     }
     __threadfence();
     __syncthreads();
-    __shared__ uint32_t arrived;
     if (tid == 0) arrived = atomicAdd(a.counters + (size_t)client * a.kv_heads + kvh, 1u);
     __syncthreads();
     if (arrived != (uint32_t)(n_chunks - 1)) return;
     __threadfence();
+    // Merge: one wavefront per head reads every chunk's (max, sum) in
+    // parallel and leaves each chunk's weight exp(m_c - M) / L in LDS (chunks
+    // past the LDS table are recomputed); then head lanes sum the outputs.
+    __shared__ float fw[GQP][kMergeChunks];
+    for (int g = w; g < GQ; g += kWaves) {
+        const float *pb = a.partial + ((size_t)client * a.heads + kvh * GQ + g) * a.max_chunks * (HD + 2);
+        float m = -INFINITY;
+        for (int c = lane; c < n_chunks; c += EMU_WAVE) m = fmaxf(m, __builtin_nontemporal_load(pb + c * (HD + 2) + HD));
+        const float M = wave_max(m);
+        float l = 0.0f;
+        for (int c = lane; c < n_chunks; c += EMU_WAVE) {
+            const float *pc = pb + c * (HD + 2);
+            l = __builtin_fmaf(__builtin_nontemporal_load(pc + HD + 1), expf(__builtin_nontemporal_load(pc + HD) - M), l);
+        }
+        const float L = wave_sum(l);
+        for (int c = lane; c < n_chunks && c < kMergeChunks; c += EMU_WAVE)
+            fw[g][c] = expf(__builtin_nontemporal_load(pb + c * (HD + 2) + HD) - M) / L;
+        if (lane == 0) {
+            mh[g] = M;
+            lh[g] = L;
+        }
+    }
+    __syncthreads();
     for (int idx = tid; idx < GQ * HD; idx += kThreads) {
         const int g = idx / HD, d = idx % HD;
         const int head = kvh * GQ + g;
         const float *pb = a.partial + ((size_t)client * a.heads + head) * a.max_chunks * (HD + 2);
-        float M = -INFINITY;
-        for (int c = 0; c < n_chunks; ++c) M = fmaxf(M, __builtin_nontemporal_load(pb + c * (HD + 2) + HD));
-        float L = 0.0f, O = 0.0f;
+        float O = 0.0f;
+#pragma unroll 8
         for (int c = 0; c < n_chunks; ++c) {
-            const float *pc = pb + c * (HD + 2);
-            const float f = expf(__builtin_nontemporal_load(pc + HD) - M);
-            L = __builtin_fmaf(__builtin_nontemporal_load(pc + HD + 1), f, L);
-            O = __builtin_fmaf(__builtin_nontemporal_load(pc + d), f, O);
+            const float f = c < kMergeChunks ? fw[g][c]
+                                              : expf(__builtin_nontemporal_load(pb + c * (HD + 2) + HD) - mh[g]) / lh[g];
+            O = __builtin_fmaf(__builtin_nontemporal_load(pb + c * (HD + 2) + d), f, O);
         }
-        outp[head * HD + d] = O / L;
+        outp[head * HD + d] = O;
     }
     if (tid == 0) atomicExch(a.counters + (size_t)client * a.kv_heads + kvh, 0u);
 }
 
-} // namespace
+template <int HD, bool F16>
+void launch_hd(const AttnArgs &a, dim3 grid, hipStream_t stream, int gq)
+{
+    if (gq <= 1)
+        hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 1>), grid, dim3(kThreads), 0, stream, a);
+    else if (gq <= 2)
+        hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 2>), grid, dim3(kThreads), 0, stream, a);
+    else if (gq <= 4)
+        hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 4>), grid, dim3(kThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 8>), grid, dim3(kThreads), 0, stream, a);
+}
 
+} // namespace
 
 int emu_attn_max_chunks(int context) { return (context + kChunk - 1) / kChunk; }
 
 int emu_launch_attn(emu_ctx *ctx, const EmuAttnLaunch &l)
 {
-    if (l.heads % l.kv_heads != 0 || l.heads / l.kv_heads > 8) return EMU_E_CONFIG;
+    if (l.kv_heads <= 0 || l.heads % l.kv_heads != 0 || l.heads / l.kv_heads > 8) return EMU_E_CONFIG;
     AttnArgs a{};
     a.qkv = l.qkv;
     a.k_cache = l.k_cache;
@@ -308,6 +436,7 @@ int emu_launch_attn(emu_ctx *ctx, const EmuAttnLaunch &l)
     a.score_mul = l.score_mul;
     a.score_div = l.score_div;
     a.rope_fma = l.rope_fma;
+    a.interleaved = l.interleaved;
     a.heads = l.heads;
     a.kv_heads = l.kv_heads;
     a.layers = l.layers;
@@ -317,21 +446,17 @@ int emu_launch_attn(emu_ctx *ctx, const EmuAttnLaunch &l)
     a.counters = l.counters;
     a.max_chunks = emu_attn_max_chunks(l.context);
     a.out = l.out;
-    dim3 grid(a.max_chunks, l.kv_heads, l.clients);
-#define EMU_ATTN_CASE(HD)                                                                              \
-    case HD:                                                                                           \
-        if (l.kv_f16)                                                                                  \
-            hipLaunchKernelGGL((attn_decode_kernel<HD, true>), grid, dim3(kThreads), 0, ctx->stream, a); \
-        else                                                                                           \
-            hipLaunchKernelGGL((attn_decode_kernel<HD, false>), grid, dim3(kThreads), 0, ctx->stream, a); \
-        break;
-    switch (l.head_dim) {
-        EMU_ATTN_CASE(64)
-        EMU_ATTN_CASE(128)
-        EMU_ATTN_CASE(256)
+    const dim3 grid(a.max_chunks, l.kv_heads, l.clients);
+    const int gq = l.heads / l.kv_heads;
+    switch (l.head_dim * 2 + (l.kv_f16 ? 1 : 0)) {
+    case 128: launch_hd<64, false>(a, grid, ctx->stream, gq); break;
+    case 129: launch_hd<64, true>(a, grid, ctx->stream, gq); break;
+    case 256: launch_hd<128, false>(a, grid, ctx->stream, gq); break;
+    case 257: launch_hd<128, true>(a, grid, ctx->stream, gq); break;
+    case 512: launch_hd<256, false>(a, grid, ctx->stream, gq); break;
+    case 513: launch_hd<256, true>(a, grid, ctx->stream, gq); break;
     default: return EMU_E_CONFIG;
     }
-#undef EMU_ATTN_CASE
     EMU_LAUNCH_CHECK(ctx);
     return EMU_OK;
 }

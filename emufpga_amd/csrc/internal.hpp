@@ -72,6 +72,16 @@ __device__ __forceinline__ float h2f(uint16_t bits)
     return __half2float(__ushort_as_half(bits));
 }
 
+// A pointer every lane of the wavefront holds: read into scalar registers so
+// memory instructions take it as their scalar base.
+__device__ __forceinline__ const uint8_t *uniform_ptr(const uint8_t *p)
+{
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const uint8_t *>(((uint64_t)hi << 32) | lo);
+}
+
 // Byte i of w as a float: the backend selects v_cvt_f32_ubyte{0..3}.
 __device__ __forceinline__ float byte_f(uint32_t w, int i)
 {
@@ -130,15 +140,18 @@ struct FmtQ6K {
         uint2 a, b, c, s;
         uint32_t d;
     };
-    __device__ __forceinline__ static void load(const uint8_t *blk, int sub, Raw &r)
+    // Block at base + off; unsigned 32-bit offsets let a wave-uniform base
+    // stay in scalar registers.
+    __device__ __forceinline__ static void load(const uint8_t *base, uint32_t off, int sub, Raw &r)
     {
-        const int h = sub >> 2, l8 = sub & 3;
-        r.a = ld8(blk + 64 * h + 8 * l8);
-        r.b = ld8(blk + 64 * h + 32 + 8 * l8);
-        r.c = ld8(blk + 128 + 32 * h + 8 * l8);
-        r.s = ld8(blk + 192 + 8 * h);
-        r.d = ld2(blk + 208);
+        const uint32_t h = (uint32_t)sub >> 2, l8 = (uint32_t)sub & 3u;
+        r.a = ld8(base + (off + 64u * h + 8u * l8));
+        r.b = ld8(base + (off + 64u * h + 32u + 8u * l8));
+        r.c = ld8(base + (off + 128u + 32u * h + 8u * l8));
+        r.s = ld8(base + (off + 192u + 8u * h));
+        r.d = ld2(base + (off + 208u));
     }
+    __device__ __forceinline__ static void load(const uint8_t *blk, int sub, Raw &r) { load(blk, 0u, sub, r); }
     __device__ __forceinline__ static int col(int sub, int g)
     {
         return 128 * (sub >> 2) + 32 * g + 8 * (sub & 3);
@@ -170,11 +183,12 @@ struct FmtQ8_0 {
         uint4 v;
         uint32_t d;
     };
-    __device__ __forceinline__ static void load(const uint8_t *blk, int sub, Raw &r)
+    __device__ __forceinline__ static void load(const uint8_t *base, uint32_t off, int sub, Raw &r)
     {
-        r.v = ld16(blk + 2 + 16 * sub);
-        r.d = ld2(blk);
+        r.v = ld16(base + (off + 2u + 16u * (uint32_t)sub));
+        r.d = ld2(base + off);
     }
+    __device__ __forceinline__ static void load(const uint8_t *blk, int sub, Raw &r) { load(blk, 0u, sub, r); }
     __device__ __forceinline__ static int col(int sub, int g) { return 16 * sub + 8 * g; }
     __device__ __forceinline__ static Grp group(const Raw &r, int, int gi)
     {
@@ -200,16 +214,17 @@ struct FmtQ5K {
         uint4 qs, qh;
         uint32_t s0, s1, s2, dd;
     };
-    __device__ __forceinline__ static void load(const uint8_t *blk, int sub, Raw &r)
+    __device__ __forceinline__ static void load(const uint8_t *base, uint32_t off, int sub, Raw &r)
     {
-        const int g = sub >> 1, l16 = sub & 1;
-        r.qs = ld16(blk + 48 + 32 * g + 16 * l16);
-        r.qh = ld16(blk + 16 + 16 * l16);
-        r.dd = ld4(blk);
-        r.s0 = ld4(blk + 4);
-        r.s1 = ld4(blk + 8);
-        r.s2 = ld4(blk + 12);
+        const uint32_t g = (uint32_t)sub >> 1, l16 = (uint32_t)sub & 1u;
+        r.qs = ld16(base + (off + 48u + 32u * g + 16u * l16));
+        r.qh = ld16(base + (off + 16u + 16u * l16));
+        r.dd = ld4(base + off);
+        r.s0 = ld4(base + (off + 4u));
+        r.s1 = ld4(base + (off + 8u));
+        r.s2 = ld4(base + (off + 12u));
     }
+    __device__ __forceinline__ static void load(const uint8_t *blk, int sub, Raw &r) { load(blk, 0u, sub, r); }
     __device__ __forceinline__ static int col(int sub, int gi)
     {
         return 64 * (sub >> 1) + 32 * (gi >> 1) + 16 * (sub & 1) + 8 * (gi & 1);
@@ -257,13 +272,14 @@ struct FmtQ2K {
         uint2 qs, sc;
         uint32_t dd;
     };
-    __device__ __forceinline__ static void load(const uint8_t *blk, int sub, Raw &r)
+    __device__ __forceinline__ static void load(const uint8_t *base, uint32_t off, int sub, Raw &r)
     {
-        const int N = sub >> 2, s = (sub >> 1) & 1, l8 = sub & 1;
-        r.qs = ld8(blk + 16 + 32 * N + 16 * s + 8 * l8);
-        r.sc = ld8(blk + 8 * N);
-        r.dd = ld4(blk + 80);
+        const uint32_t N = (uint32_t)sub >> 2, s = ((uint32_t)sub >> 1) & 1u, l8 = (uint32_t)sub & 1u;
+        r.qs = ld8(base + (off + 16u + 32u * N + 16u * s + 8u * l8));
+        r.sc = ld8(base + (off + 8u * N));
+        r.dd = ld4(base + (off + 80u));
     }
+    __device__ __forceinline__ static void load(const uint8_t *blk, int sub, Raw &r) { load(blk, 0u, sub, r); }
     __device__ __forceinline__ static int col(int sub, int j)
     {
         return 128 * (sub >> 2) + 32 * j + 16 * ((sub >> 1) & 1) + 8 * (sub & 1);
@@ -279,6 +295,35 @@ struct FmtQ2K {
         return g;
     }
 };
+
+// ------------------------------------------------------ greedy selection --
+// Rust f32::total_cmp as an order-preserving unsigned key.
+__device__ __forceinline__ uint32_t emu_total_key(float f)
+{
+    int32_t i = __float_as_int(f);
+    i ^= (int32_t)(((uint32_t)(i >> 31)) >> 1);
+    return (uint32_t)i ^ 0x80000000u;
+}
+
+// 64-bit selection key, larger is better.  tie_last == 0: greatest value in
+// total order, lowest index on ties (top_k, spm-qwen3-slice/src/math.rs:38-48);
+// tie_last == 1: greatest value with -0 == +0, last index on ties
+// (max_by(partial_cmp), spm-batch/tests/batching.rs:111-123).  Key 0 is
+// below every real key.
+__device__ __forceinline__ uint64_t emu_select_key(float v, uint32_t idx, int tie_last)
+{
+    if (tie_last) {
+        if (v == 0.0f) v = 0.0f;
+        return ((uint64_t)emu_total_key(v) << 32) | idx;
+    }
+    return ((uint64_t)emu_total_key(v) << 32) | (0xffffffffu - idx);
+}
+
+__device__ __forceinline__ uint32_t emu_key_index(uint64_t k, int tie_last)
+{
+    const uint32_t lo = (uint32_t)k;
+    return tie_last ? lo : 0xffffffffu - lo;
+}
 
 // ------------------------------------------------------------ reductions --
 
@@ -301,9 +346,14 @@ struct QmvArgs {
     float eps;
     float *y;              // n_tok x rows
     int accumulate;
+    uint64_t *keys;        // optional greedy-selection keys: keys[t * key_stride + wave]
+    int key_stride;
+    int tie_last;
 };
 
-int emu_launch_qmv(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok);
+// Launch a quantized matvec; *key_slots (optional) receives how many key
+// slots per token the launch writes when a.keys is set.
+int emu_launch_qmv(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int *key_slots = nullptr);
 int emu_row_bytes(int encoding, uint32_t cols, size_t *row_bytes);
 
 // Fused decode attention of one layer for every client (attn.hip).
@@ -314,7 +364,7 @@ struct EmuAttnLaunch {
     const float *rope;
     const float *q_norm, *k_norm;
     float eps, score_mul, score_div;
-    int rope_fma, heads, kv_heads, head_dim, layers, layer, context, clients, kv_f16;
+    int rope_fma, interleaved, heads, kv_heads, head_dim, layers, layer, context, clients, kv_f16;
     float *partial;
     uint32_t *counters;
     float *out;

@@ -18,6 +18,7 @@
 #include "internal.hpp"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 #include <vector>
 
@@ -53,6 +54,8 @@ struct emu_session {
     size_t kv_bytes = 0;
     uint32_t *positions = nullptr, *tokens = nullptr, *steps = nullptr, *prompt = nullptr,
              *hist = nullptr, *ctrl = nullptr, *last = nullptr, *counters = nullptr;
+    uint64_t *keys = nullptr; // per-client greedy-selection keys written by the output matvec
+    uint32_t key_stride = 0;
     float *state = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr,
           *partial = nullptr, *rope = nullptr;
     std::vector<uint32_t> host_pos;
@@ -267,35 +270,22 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint8_t *embed, s
     }
 }
 
-__device__ __forceinline__ uint32_t total_key_u(float f)
-{
-    int32_t i = __float_as_int(f);
-    i ^= (int32_t)(((uint32_t)(i >> 31)) >> 1);
-    return (uint32_t)i ^ 0x80000000u;
-}
-
-// Greedy select + advance, one workgroup per client.
+// Greedy select + advance, one workgroup per client, over the selection keys
+// the output matvec left per wavefront (key_slots of them per client).
 // ctrl[0] = prompt length (0: every step is a free-running decode step),
 // ctrl[1] = capacity of the generated-token history per client.
-__global__ __launch_bounds__(1024) void finalize_kernel(const float *logits, int vocab, int tie_last,
-                                                        const uint32_t *prompt, int prompt_stride,
+__global__ __launch_bounds__(1024) void finalize_kernel(const uint64_t *keys, int key_stride, int key_slots,
+                                                        int tie_last, const uint32_t *prompt, int prompt_stride,
                                                         uint32_t *hist, const uint32_t *ctrl,
                                                         uint32_t *tokens, uint32_t *positions,
                                                         uint32_t *steps, uint32_t *last)
 {
     __shared__ uint64_t red[16];
     const int c = blockIdx.x;
-    const float *lr = logits + (size_t)c * vocab;
+    const uint64_t *kr = keys + (size_t)c * key_stride;
     uint64_t best = 0;
-    for (int i = threadIdx.x; i < vocab; i += blockDim.x) {
-        float v = lr[i];
-        uint64_t k;
-        if (tie_last) {
-            if (v == 0.0f) v = 0.0f;
-            k = ((uint64_t)total_key_u(v) << 32) | (uint32_t)i;
-        } else {
-            k = ((uint64_t)total_key_u(v) << 32) | (0xffffffffu - (uint32_t)i);
-        }
+    for (int i = threadIdx.x; i < key_slots; i += blockDim.x) {
+        const uint64_t k = kr[i];
         best = k > best ? k : best;
     }
 #pragma unroll
@@ -379,6 +369,7 @@ int run_step(emu_session *s)
         al.score_mul = smol ? 1.0f / sqrtf((float)hd) : 0.0f;
         al.score_div = smol ? 0.0f : sqrtf((float)hd);
         al.rope_fma = smol;
+        al.interleaved = 0;
         al.heads = (int)c.heads;
         al.kv_heads = (int)c.kv_heads;
         al.head_dim = (int)hd;
@@ -437,8 +428,13 @@ int run_step(emu_session *s)
     out.gain = reinterpret_cast<const float *>(m->base + m->off_out_norm);
     out.eps = c.eps;
     out.y = s->logits;
-    if ((st = emu_launch_qmv(ctx, c.encoding, out, n)) != EMU_OK) return st;
-    hipLaunchKernelGGL(finalize_kernel, dim3(s->n), dim3(1024), 0, ctx->stream, s->logits, (int)c.vocab,
+    out.keys = s->keys;
+    out.key_stride = (int)s->key_stride;
+    out.tie_last = smol ? 1 : 0;
+    int slots = 0;
+    if ((st = emu_launch_qmv(ctx, c.encoding, out, n, &slots)) != EMU_OK) return st;
+    if (slots <= 0 || slots > (int)s->key_stride) return EMU_E_CONFIG;
+    hipLaunchKernelGGL(finalize_kernel, dim3(s->n), dim3(1024), 0, ctx->stream, s->keys, (int)s->key_stride, slots,
                        smol ? 1 : 0, s->prompt, (int)s->context, s->hist, s->ctrl, s->tokens, s->positions,
                        s->steps, s->last);
     EMU_LAUNCH_CHECK(ctx);
@@ -467,12 +463,31 @@ int ensure_graph(emu_session *s)
     return EMU_OK;
 }
 
+// EMU_GRAPH=0 launches the step's kernels directly instead of replaying the
+// captured graph (same kernels, same order; for profilers that cannot trace
+// graph launches, and to measure what the graph saves).
+bool graphs_enabled()
+{
+    static const bool on = [] {
+        const char *v = getenv("EMU_GRAPH");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
+
 int launch_steps(emu_session *s, uint32_t count)
 {
-    int st = ensure_graph(s);
-    if (st != EMU_OK) return st;
     emu_ctx *ctx = s->m->ctx;
-    for (uint32_t i = 0; i < count; ++i) EMU_HIP(ctx, hipGraphLaunch(s->exec, ctx->stream));
+    if (!graphs_enabled()) {
+        for (uint32_t i = 0; i < count; ++i) {
+            const int st = run_step(s);
+            if (st != EMU_OK) return st;
+        }
+    } else {
+        int st = ensure_graph(s);
+        if (st != EMU_OK) return st;
+        for (uint32_t i = 0; i < count; ++i) EMU_HIP(ctx, hipGraphLaunch(s->exec, ctx->stream));
+    }
     for (auto &p : s->host_pos) p += count;
     return EMU_OK;
 }
@@ -658,6 +673,8 @@ extern "C" int emu_session_create(emu_model *m, uint32_t n_clients, uint32_t con
     alloc((void **)&s->attn, sizeof(float) * n_clients * QW);
     alloc((void **)&s->act, sizeof(float) * n_clients * c.ffn);
     alloc((void **)&s->logits, sizeof(float) * n_clients * c.vocab);
+    s->key_stride = c.vocab + 8; // >= key slots of any output-matvec launch shape
+    alloc((void **)&s->keys, sizeof(uint64_t) * n_clients * s->key_stride);
     alloc((void **)&s->partial, sizeof(float) * n_clients * c.heads * chunks * (c.head_dim + 2));
     alloc((void **)&s->rope, sizeof(float) * (size_t)context * c.head_dim);
     if (st == EMU_OK) {
@@ -682,7 +699,8 @@ extern "C" int emu_session_destroy(emu_session *s)
     if (s->exec) (void)hipGraphExecDestroy(s->exec);
     if (s->graph) (void)hipGraphDestroy(s->graph);
     void *ptrs[] = {s->k_cache, s->v_cache, s->positions, s->tokens, s->steps, s->last, s->prompt, s->hist,
-                    s->ctrl, s->counters, s->state, s->qkv, s->attn, s->act, s->logits, s->partial, s->rope};
+                    s->ctrl, s->counters, s->state, s->qkv, s->attn, s->act, s->logits, s->keys, s->partial,
+                    s->rope};
     for (void *p : ptrs) emu_free(ctx, p);
     delete s;
     return EMU_OK;
@@ -754,7 +772,7 @@ extern "C" int emu_time_decode(emu_session *s, uint32_t steps, float *ms)
     if (st != EMU_OK) return st;
     emu_ctx *ctx = s->m->ctx;
     if ((st = set_ctrl(s, 0, 0)) != EMU_OK) return st;
-    if ((st = ensure_graph(s)) != EMU_OK) return st;
+    if (graphs_enabled() && (st = ensure_graph(s)) != EMU_OK) return st;
     if ((st = emu_ctx_sync(ctx)) != EMU_OK) return st;
     if ((st = emu_event_record(ctx, 14)) != EMU_OK) return st;
     if ((st = launch_steps(s, steps)) != EMU_OK) return st;

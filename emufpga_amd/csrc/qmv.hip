@@ -13,6 +13,7 @@
 #include "internal.hpp"
 
 #include <math.h>
+#include <stdlib.h>
 
 namespace {
 
@@ -113,6 +114,21 @@ __global__ __launch_bounds__(kThreads) void qmv_kernel(QmvArgs a)
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[k][t] = wave_sum(acc[k][t]) * scale[t];
 
+    if (!DUAL && a.keys && lane == 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            uint64_t best = 0;
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+                if (r0 + k < a.rows) {
+                    const uint64_t key = emu_select_key(acc[k][t], (uint32_t)(r0 + k), a.tie_last);
+                    best = key > best ? key : best;
+                }
+            }
+            a.keys[(size_t)t * a.key_stride + wave] = best;
+        }
+    }
+
 #pragma unroll
     for (int k = 0; k < R; ++k) {
         const int row = r0 + k;
@@ -150,9 +166,253 @@ int launch_nt(emu_ctx *ctx, const QmvArgs &a)
     return EMU_OK;
 }
 
-template <class F>
-int launch_fmt(emu_ctx *ctx, const QmvArgs &a, int n_tok)
+// ---- batch-1 matvec: persistent, software-pipelined, activations in LDS ----
+// LDS slot of column c (4 pad floats per 128 columns) and of 8-column group
+// q's sum (4 pad floats per 32 groups); 16-byte alignment of 4-column runs
+// is kept.
+__host__ __device__ constexpr int px(int c) { return c + 4 * (c >> 7); }
+__host__ __device__ constexpr int pg(int q) { return q + 4 * (q >> 5); }
+__host__ __device__ constexpr int lds_x_floats(int cols) { return px(cols) + 4; }
+__host__ __device__ constexpr int lds_g_floats(int cols) { return pg(cols / 8) + 4; }
+
+// The workgroup stages x (RMS-normalised as (x*s)*gain when requested, the
+// reference's order) in LDS once.  Each wavefront then walks its row groups
+// (R rows, or R gate/up row pairs) as a flat list of items (row group x unit
+// iteration) and issues the next item's block loads before the current
+// item's arithmetic, so two items of loads are in flight per wave.  R is
+// chosen per launch: large for tall matrices (fewer activation reads per
+// weight), small for short ones (enough wavefronts to fill every CU).  With a
+// key buffer the epilogue also tracks the wave's greedy-selection key.
+template <class F, int R, bool DUAL, bool NORM>
+__global__ __launch_bounds__(kThreads) void qmv_pipe_kernel(QmvArgs a, int total_waves)
 {
+    constexpr int NR = DUAL ? 2 * R : R;
+    constexpr int G = F::G;
+    extern __shared__ float xs[];
+    __shared__ float red[kThreads / EMU_WAVE];
+    const int tid = threadIdx.x, lane = tid & (EMU_WAVE - 1), wv = tid / EMU_WAVE;
+
+    // Padded LDS layout: column c lives at px(c), 8-column group q's sum at
+    // xg[pg(q)].  Lane units sit 32 columns apart except for their 8-column
+    // slot, so without padding 16 lanes would share each bank group.
+    float *xg = xs + lds_x_floats(a.cols);
+    float ss = 0.0f;
+    for (int c = tid * 4; c < a.cols; c += kThreads * 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(a.x + c);
+        if (NORM) ss = __builtin_fmaf(v.w, v.w, __builtin_fmaf(v.z, v.z, __builtin_fmaf(v.y, v.y, __builtin_fmaf(v.x, v.x, ss))));
+        *reinterpret_cast<float4 *>(xs + px(c)) = v;
+    }
+    if (NORM) {
+        ss = wave_sum(ss);
+        if (lane == 0) red[wv] = ss;
+        __syncthreads();
+        const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+        const float scale = 1.0f / sqrtf(tot / (float)a.cols + a.eps);
+        for (int c = tid * 4; c < a.cols; c += kThreads * 4) {
+            float4 v = *reinterpret_cast<float4 *>(xs + px(c));
+            const float4 g = *reinterpret_cast<const float4 *>(a.gain + c);
+            v.x = __fmul_rn(__fmul_rn(v.x, scale), g.x);
+            v.y = __fmul_rn(__fmul_rn(v.y, scale), g.y);
+            v.z = __fmul_rn(__fmul_rn(v.z, scale), g.z);
+            v.w = __fmul_rn(__fmul_rn(v.w, scale), g.w);
+            *reinterpret_cast<float4 *>(xs + px(c)) = v;
+        }
+    }
+    __syncthreads();
+    for (int q = tid; q < a.cols / 8; q += kThreads) {
+        const float *p = xs + px(8 * q);
+        xg[pg(q)] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    }
+    __syncthreads();
+
+    const int gw = blockIdx.x * (kThreads / EMU_WAVE) + wv;
+    const int n_rg = (a.rows + R - 1) / R;
+    const int U = a.nb * F::UPB;
+    const int iters = (U + EMU_WAVE - 1) / EMU_WAVE;
+    const int my_rg = gw < n_rg ? (n_rg - 1 - gw) / total_waves + 1 : 0;
+    const int items = my_rg * iters;
+
+    // One item's loads: the R (or 2R) rows' unit bytes and, for the first item
+    // of a row group, the residual the epilogue adds to (so the epilogue never
+    // waits on a load issued behind the prefetch).  Row bases are
+    // wave-uniform: they stay in scalar registers and each lane addresses its
+    // unit with a 32-bit offset.
+    struct Buf {
+        typename F::Raw raw[NR];
+        float resid;
+    };
+    auto load_item = [&](int it, Buf &dst) {
+        const int rg = gw + (it / iters) * total_waves;
+        const int ui = it % iters;
+        int u = lane + EMU_WAVE * ui;
+        u = u < U ? u : U - 1; // in-bounds duplicate; its contribution is masked
+        const int blk = u / F::UPB, sub = u % F::UPB;
+        const uint32_t off = (uint32_t)blk * F::BB;
+#pragma unroll
+        for (int k = 0; k < NR; ++k) {
+            int row = rg * R + (k % R);
+            row = row < a.rows ? row : a.rows - 1;
+            const uint8_t *base = (DUAL && k >= R) ? a.w_up : a.w;
+            row = __builtin_amdgcn_readfirstlane(row);
+            F::load(base + (size_t)row * a.row_bytes, off, sub, dst.raw[k]);
+        }
+        if (a.accumulate && ui == 0) {
+            int row = rg * R + (lane < R ? lane : R - 1);
+            row = row < a.rows ? row : a.rows - 1;
+            dst.resid = a.y[row];
+        }
+    };
+
+    float acc[NR];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) acc[k] = 0.0f;
+    uint64_t best = 0;
+    float resid = 0.0f;
+
+    // w_i = code_i * mul + add, so a group adds mul * sum(code_i x_i) + add * sum(x_i).
+    auto process = [&](int it, const Buf &buf) {
+        const typename F::Raw(&cur)[NR] = buf.raw;
+        const int ui = it % iters;
+        if (a.accumulate && ui == 0) resid = buf.resid;
+        const int u = lane + EMU_WAVE * ui;
+        if (u < U) {
+            const int blk = u / F::UPB, sub = u % F::UPB;
+            const int c0 = blk * F::BE;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const int col = c0 + F::col(sub, g);
+                const float4 x0 = *reinterpret_cast<const float4 *>(xs + px(col));
+                const float4 x1 = *reinterpret_cast<const float4 *>(xs + px(col) + 4);
+                const float xsum = xg[pg(col / 8)];
+                const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                for (int k = 0; k < NR; ++k) {
+                    const Grp gp = F::group(cur[k], sub, g);
+                    float t = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) t = __builtin_fmaf(byte_f(i < 4 ? gp.q0 : gp.q1, i & 3), xv[i], t);
+                    if (F::BIAS) // add == -BIAS * mul: mul * (t - BIAS * xsum)
+                        acc[k] = __builtin_fmaf(gp.mul, __builtin_fmaf(-(float)F::BIAS, xsum, t), acc[k]);
+                    else
+                        acc[k] = __builtin_fmaf(gp.add, xsum, __builtin_fmaf(gp.mul, t, acc[k]));
+                }
+            }
+        }
+        if (ui == iters - 1) {
+            const int rg = gw + (it / iters) * total_waves;
+            float v[NR];
+#pragma unroll
+            for (int k = 0; k < NR; ++k) {
+                v[k] = wave_sum(acc[k]);
+                acc[k] = 0.0f;
+            }
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+                const int row = rg * R + k;
+                float val = v[k];
+                if (DUAL) val = (val / (1.0f + expf(-val))) * v[k + R];
+                if (row < a.rows) {
+                    if (lane == k) a.y[row] = a.accumulate ? resid + val : val;
+                    if (a.keys) {
+                        const uint64_t key = emu_select_key(val, (uint32_t)row, a.tie_last);
+                        best = key > best ? key : best;
+                    }
+                }
+            }
+        }
+    };
+
+    // Two buffers in turn: item it+1's loads are in flight during item it.
+    // The prefetch is unconditional (clamped to the last item) so the
+    // compiler's wait counts never have to cover a maybe-issued load.
+    if (items > 0) {
+        const int last = items - 1;
+        Buf b0, b1;
+        load_item(0, b0);
+        for (int it = 0; it < items; it += 2) {
+            load_item(it + 1 < last ? it + 1 : last, b1);
+            process(it, b0);
+            load_item(it + 2 < last ? it + 2 : last, b0);
+            if (it + 1 < items) process(it + 1, b1);
+        }
+    }
+    if (a.keys && lane == 0) a.keys[gw] = best;
+}
+
+template <class F, int R>
+void launch_pipe_r(emu_ctx *ctx, const QmvArgs &a, int blocks, int total_waves, size_t lds)
+{
+    const bool dual = a.w_up != nullptr, norm = a.gain != nullptr;
+    if (dual && norm)
+        hipLaunchKernelGGL((qmv_pipe_kernel<F, R, true, true>), dim3(blocks), dim3(kThreads), lds, ctx->stream, a, total_waves);
+    else if (dual)
+        hipLaunchKernelGGL((qmv_pipe_kernel<F, R, true, false>), dim3(blocks), dim3(kThreads), lds, ctx->stream, a, total_waves);
+    else if (norm)
+        hipLaunchKernelGGL((qmv_pipe_kernel<F, R, false, true>), dim3(blocks), dim3(kThreads), lds, ctx->stream, a, total_waves);
+    else
+        hipLaunchKernelGGL((qmv_pipe_kernel<F, R, false, false>), dim3(blocks), dim3(kThreads), lds, ctx->stream, a, total_waves);
+}
+
+template <class F>
+int launch_pipe(emu_ctx *ctx, const QmvArgs &a, int *key_slots)
+{
+    const bool dual = a.w_up != nullptr;
+    const int waves_per_block = kThreads / EMU_WAVE;
+    const int cus = ctx->cus > 0 ? ctx->cus : 256;
+    const int max_blocks = cus * 4;               // 16 wavefronts per CU resident
+    const int want_waves = max_blocks * waves_per_block;
+    // Largest R (rows sharing each activation read) that still gives every
+    // CU its full complement of wavefronts; gate/up pairs count double.
+    int R = dual ? 2 : 4;
+    while (R > 1 && (a.rows + R - 1) / R < want_waves) R /= 2;
+    if (const char *force = getenv("EMU_QMV_R")) { // fixed rows per wave, for tuning sweeps
+        const int f = atoi(force);
+        if (f == 1 || f == 2 || (f == 4 && !dual)) R = f;
+    }
+    const int n_rg = (a.rows + R - 1) / R;
+    int blocks = (n_rg + waves_per_block - 1) / waves_per_block;
+    blocks = blocks < max_blocks ? blocks : max_blocks;
+    const int total_waves = blocks * waves_per_block;
+    const size_t lds = sizeof(float) * (size_t)(lds_x_floats(a.cols) + lds_g_floats(a.cols));
+    switch (R) {
+    case 4: launch_pipe_r<F, 4>(ctx, a, blocks, total_waves, lds); break;
+    case 2: launch_pipe_r<F, 2>(ctx, a, blocks, total_waves, lds); break;
+    default: launch_pipe_r<F, 1>(ctx, a, blocks, total_waves, lds); break;
+    }
+    EMU_LAUNCH_CHECK(ctx);
+    if (key_slots) *key_slots = total_waves;
+    return EMU_OK;
+}
+
+constexpr int kPipeMaxCols = 12288; // padded activations + group sums fit in 58 KB of LDS
+
+// EMU_QMV_PIPE=0 routes batch-1 matvecs to the row-per-wave kernel instead
+// (for comparing the two).
+bool pipe_disabled()
+{
+    static const bool off = [] {
+        const char *v = getenv("EMU_QMV_PIPE");
+        return v && v[0] == '0';
+    }();
+    return off;
+}
+
+template <class F>
+int launch_fmt(emu_ctx *ctx, const QmvArgs &a, int n_tok, int *key_slots)
+{
+    if (n_tok == 1 && a.cols <= kPipeMaxCols && a.cols % 4 == 0 && !pipe_disabled())
+        return launch_pipe<F>(ctx, a, key_slots);
+    if (a.keys && a.w_up) return EMU_E_ARG; // keys select among plain matvec rows
+    if (key_slots) {
+        const bool dual = a.w_up != nullptr;
+        int R = 1;
+        switch (n_tok) {
+        case 1: R = dual ? rows_per_wave<1, true>() : rows_per_wave<1, false>(); break;
+        case 2: case 3: case 4: R = rows_per_wave<2, false>(); break;
+        default: R = rows_per_wave<8, false>(); break;
+        }
+        *key_slots = (a.rows + R - 1) / R;
+    }
     switch (n_tok) {
     case 1: return launch_nt<F, 1>(ctx, a);
     case 2: return launch_nt<F, 2>(ctx, a);
@@ -350,14 +610,14 @@ int emu_row_bytes(int encoding, uint32_t cols, size_t *row_bytes)
     return EMU_OK;
 }
 
-int emu_launch_qmv(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok)
+int emu_launch_qmv(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int *key_slots)
 {
     if (a.rows == 0 || n_tok == 0) return EMU_OK;
     switch (encoding) {
-    case EMU_ENC_Q6_K: return launch_fmt<FmtQ6K>(ctx, a, n_tok);
-    case EMU_ENC_Q8_0: return launch_fmt<FmtQ8_0>(ctx, a, n_tok);
-    case EMU_ENC_Q5_K: return launch_fmt<FmtQ5K>(ctx, a, n_tok);
-    case EMU_ENC_Q2_K: return launch_fmt<FmtQ2K>(ctx, a, n_tok);
+    case EMU_ENC_Q6_K: return launch_fmt<FmtQ6K>(ctx, a, n_tok, key_slots);
+    case EMU_ENC_Q8_0: return launch_fmt<FmtQ8_0>(ctx, a, n_tok, key_slots);
+    case EMU_ENC_Q5_K: return launch_fmt<FmtQ5K>(ctx, a, n_tok, key_slots);
+    case EMU_ENC_Q2_K: return launch_fmt<FmtQ2K>(ctx, a, n_tok, key_slots);
     default: return EMU_E_UNSUPPORTED;
     }
 }

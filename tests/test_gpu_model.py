@@ -84,6 +84,37 @@ def test_greedy_tokens_identical_over_256_steps(ctx, cfg):
     assert list(got) == toks
 
 
+ATTN_SHAPES = [
+    # (heads, kv_heads, head_dim, style): group sizes 8, 1, 3 and 2; head dims 64, 256, 128
+    (8, 1, 64, _lib.EMU_STYLE_QWEN3),
+    (2, 2, 256, _lib.EMU_STYLE_QWEN3),
+    (6, 2, 128, _lib.EMU_STYLE_SMOL),
+    (4, 2, 256, _lib.EMU_STYLE_SMOL),
+]
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim,style", ATTN_SHAPES)
+def test_attention_shapes_match_oracle(ctx, heads, kv_heads, head_dim, style):
+    smol = style == _lib.EMU_STYLE_SMOL
+    cfg = DenseConfig(hidden=512, heads=heads, kv_heads=kv_heads, head_dim=head_dim, ffn=768, vocab=600,
+                      layers=2, rope_theta=1e5 if smol else 1e6, eps=1e-5 if smol else 1e-6, style=style,
+                      encoding=_lib.Q8_0 if smol else _lib.Q6_K, tied=smol, qk_norm=not smol)
+    model = Model(ctx, cfg)
+    model.synth(heads * 1000 + head_dim)
+    context = 140
+    sess = Session(model, 2, context, kv_f16=True)
+    ref = oracle_for(model, context, True, 2)
+    rng = np.random.default_rng(heads + head_dim)
+    worst = 0.0
+    for step in range(context):
+        toks = rng.integers(0, cfg.vocab, size=2).astype(np.uint32)
+        _, logits = sess.decode_step(toks, want_logits=True)
+        r = ref.step(toks)
+        if step % 7 == 0 or step >= context - 3:
+            worst = max(worst, rel_inf(logits[0], r[0]), rel_inf(logits[1], r[1]))
+    assert worst <= 1e-3, worst
+
+
 def test_batched_client_gets_what_it_would_alone(ctx):  # spm-batch/tests/batching.rs:128-145
     model = Model(ctx, SMALL_QWEN3)
     model.synth(7)
