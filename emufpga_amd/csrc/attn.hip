@@ -209,19 +209,20 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     const int p0 = chunk * kChunk;
     const bool owner = pos >= p0 && pos < p0 + kChunk;
 
-    // This wavefront's 16 positions: issue every K and V row load now.
+    // This wavefront's 16 positions: issue every K and V row load now, with no
+    // branch around them (a branch per load serialises them behind waits).
+    // Positions past the context read row `pos - 1` or row 0 (always inside
+    // the cache) and are masked after the loads; the new position's row is
+    // being written by its owner and is replaced by the owner's values.
     const int pw = p0 + w * kPP;
+    const int safe_row = pos > 0 ? pos - 1 : 0;
     vec_t kr[kPP], vr[kPP];
 #pragma unroll
     for (int pp = 0; pp < kPP; ++pp) {
         const int p = pw + pp;
-        if (p < n && p != pos) {
-            kr[pp] = *reinterpret_cast<const vec_t *>(kc + (size_t)p * HD + lane * EPL);
-            vr[pp] = *reinterpret_cast<const vec_t *>(vc + (size_t)p * HD + lane * EPL);
-        } else {
-            kr[pp] = vec_t{};
-            vr[pp] = vec_t{};
-        }
+        const int r = (p < n && p != pos) ? p : safe_row;
+        kr[pp] = *reinterpret_cast<const vec_t *>(kc + (size_t)r * HD + lane * EPL);
+        vr[pp] = *reinterpret_cast<const vec_t *>(vc + (size_t)r * HD + lane * EPL);
     }
 
     // 1-2. Rotated queries (and the new key) into LDS: item i on wavefront i % 4.
@@ -263,11 +264,10 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     float kf[kPP][EPL];
 #pragma unroll
     for (int pp = 0; pp < kPP; ++pp) {
+        unpack_row<EPL, F16>(kr[pp], kf[pp]);
         if (pw + pp == pos) {
 #pragma unroll
             for (int e = 0; e < EPL; ++e) kf[pp][e] = knew[lane * EPL + e];
-        } else {
-            unpack_row<EPL, F16>(kr[pp], kf[pp]);
         }
     }
     constexpr int SHIFT = NV >= 64 ? 0 : (NV == 32 ? 1 : 2);
@@ -317,11 +317,13 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     for (int pp = 0; pp < kPP; ++pp) {
         const int p = pw + pp;
         float vf[EPL];
+        unpack_row<EPL, F16>(vr[pp], vf);
         if (p == pos) {
 #pragma unroll
             for (int e = 0; e < EPL; ++e) vf[e] = vnew[lane * EPL + e];
-        } else {
-            unpack_row<EPL, F16>(vr[pp], vf);
+        } else if (p >= n) { // stand-in row: zero, so that its zero weight cannot meet a NaN
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) vf[e] = 0.0f;
         }
 #pragma unroll
         for (int g = 0; g < GQP; ++g) {

@@ -355,6 +355,10 @@ struct QmvArgs {
 // slots per token the launch writes when a.keys is set.
 int emu_launch_qmv(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int *key_slots = nullptr);
 int emu_row_bytes(int encoding, uint32_t cols, size_t *row_bytes);
+// Batch-1 integer-limb matvec (limb.hip): shapes and formats it covers, and
+// its launcher (EMU_E_UNSUPPORTED for anything else).
+bool emu_limb_supports(int encoding, int cols);
+int emu_launch_limb(emu_ctx *ctx, int encoding, const QmvArgs &a, int *key_slots);
 
 // Fused decode attention of one layer for every client (attn.hip).
 struct EmuAttnLaunch {

@@ -1,0 +1,403 @@
+// limb.hip -- batch-1 quantized matvec on integer dot products.
+//
+// The weight codes of a GGUF K-quant are small integers; the activations are
+// f32.  Instead of converting every code to float (one convert and one fma
+// per weight), the activation vector is re-expressed once per launch as
+// integers: each 16-column sub-block gets a power-of-two scale s and three
+// signed 7-bit limbs per column,
+//
+//     x ~= s * (16384 * L0 + 128 * L1 + L2),    |L0|, |L1|, |L2| <= 64,
+//
+// exact to 2^-20 of the sub-block's largest |x| (the residual of the third
+// limb), i.e. as fine as the rounding of an f32 dot over a few thousand
+// terms.  A sub-block's dot with the codes is then three v_dot4_i32_i8 chains
+// (four weights per instruction) combined exactly in int32, so the float work
+// is one convert and one fma per 16 weights.
+//
+// Layout of the work: a wavefront covers 4096 columns of a row, lane l owning
+// the 64 columns of unit l (for Q6_K: the (half, 16-column slot) quarter of a
+// 256-column block, i.e. 16 bytes of ql low nibbles, 16 of ql high nibbles,
+// 16 of qh and the block's scales -- three dwordx4 loads per row).  The lane
+// keeps its 64 columns' limbs in registers for the whole launch, so a row
+// costs only its weight bytes.  Waves are persistent: row-group g handles rows
+// g, g + G, g + 2G, ... (G row-groups in the grid) with the next D rows'
+// loads in flight while the current ones are reduced (DPP wave sums).  Rows
+// of 4096*S columns use S wavefronts per row-group, whose partial sums meet in
+// LDS in a fixed order (deterministic results).
+//
+// Prologue (per workgroup, overlapped with the first rows' loads): x is read,
+// optionally RMS-normalised as (x * scale) * gain with
+// scale = 1 / sqrt(mean(x^2) + eps), and split into limbs in LDS.  A
+// sub-block holding an inf or NaN gets a NaN scale, so every row it meets
+// comes out NaN; sub-blocks whose largest |x| is below 2^-107 have subnormal
+// scales and lose precision (as f32 products of such values do).
+#include "internal.hpp"
+
+#include <math.h>
+#include <stdlib.h>
+
+namespace {
+
+struct LimbRec { // one 16-column sub-block, 64 bytes
+    uint4 l0, l1, l2; // limbs, one byte per column
+    float s;          // power-of-two scale (NaN when the sub-block holds a non-finite value)
+    int sum;          // sum over the columns of 16384*L0 + 128*L1 + L2
+    int pad[2];
+};
+static_assert(sizeof(LimbRec) == 64, "LimbRec layout");
+
+// A lane's four sub-blocks: limbs, scales and the format's bias term.
+struct Limbs {
+    uint4 l[4][3];
+    float s[4];
+    int c[4];
+};
+
+__device__ __forceinline__ int comp(const uint4 &v, int i)
+{
+    return (int)(i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w);
+}
+
+// Wave-wide sum by DPP row operations; the total is valid in lane 63.
+#define EMU_DPP(v, ctrl, rm) __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, rm, 0xf, false))
+__device__ __forceinline__ float wave_sum63(float v)
+{
+    v += EMU_DPP(v, 0xb1, 0xf);  // quad_perm [1,0,3,2]
+    v += EMU_DPP(v, 0x4e, 0xf);  // quad_perm [2,3,0,1]
+    v += EMU_DPP(v, 0x141, 0xf); // row_half_mirror
+    v += EMU_DPP(v, 0x140, 0xf); // row_mirror
+    v += EMU_DPP(v, 0x142, 0xa); // row_bcast:15 into rows 1 and 3
+    v += EMU_DPP(v, 0x143, 0xc); // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+// Q6_K (210-byte blocks of 256: ql[128], qh[64], int8 scales[16], f16 d).
+// Column 128h + 32j + 16m + i of a block has code
+//   (ql[64h + 32(j&1) + 16m + i] >> 4(j>>1) & 15) | (qh[32h + 16m + i] >> 2j & 3) << 4
+// and weight d * scales[8h + 2j + m] * (code - 32).  Unit (blk, h, m) owns
+// the four sub-blocks j = 0..3.
+struct LimbQ6K {
+    struct Raw {
+        uint4 a, b, q; // ql[64h+16m..], ql[64h+32+16m..], qh[32h+16m..]
+        uint2 sc;      // scales[8h .. 8h+8]
+        uint32_t d;
+    };
+    __device__ static __forceinline__ void load(const uint8_t *row, int unit, Raw &r)
+    {
+        const uint32_t blk = (uint32_t)unit >> 2, h = ((uint32_t)unit >> 1) & 1u, m = (uint32_t)unit & 1u;
+        const uint32_t off = blk * 210u;
+        r.a = ld16(row + (off + 64u * h + 16u * m));
+        r.b = ld16(row + (off + 64u * h + 32u + 16u * m));
+        r.q = ld16(row + (off + 128u + 32u * h + 16u * m));
+        r.sc = ld8(row + (off + 192u + 8u * h));
+        r.d = ld2(row + (off + 208u));
+    }
+    __device__ static __forceinline__ int sub_block(int unit, int j)
+    {
+        return 16 * (unit >> 2) + 8 * ((unit >> 1) & 1) + 2 * j + (unit & 1);
+    }
+    // The codes are biased by 32: start each sub-block's last chain at -32 * sum.
+    __device__ static __forceinline__ int bias(int sum) { return (int)(0u - 32u * (uint32_t)sum); }
+    __device__ static __forceinline__ uint32_t code(const Raw &r, int j, int i)
+    {
+        const uint32_t A = (uint32_t)comp(r.a, i), B = (uint32_t)comp(r.b, i), Q = (uint32_t)comp(r.q, i);
+        switch (j) {
+        case 0: return (A & 0x0f0f0f0fu) | ((Q << 4) & 0x30303030u);
+        case 1: return (B & 0x0f0f0f0fu) | ((Q << 2) & 0x30303030u);
+        case 2: return ((A >> 4) & 0x0f0f0f0fu) | (Q & 0x30303030u);
+        default: return ((B >> 4) & 0x0f0f0f0fu) | ((Q >> 2) & 0x30303030u);
+        }
+    }
+    __device__ static __forceinline__ float dot(const Raw &r, const Limbs &L, int unit)
+    {
+        const int m = unit & 1;
+        const float d = h2f((uint16_t)r.d);
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int a0 = 0, a1 = 0, a2 = L.c[j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int q = (int)code(r, j, i);
+                a0 = __builtin_amdgcn_sdot4(q, comp(L.l[j][0], i), a0, false);
+                a1 = __builtin_amdgcn_sdot4(q, comp(L.l[j][1], i), a1, false);
+                a2 = __builtin_amdgcn_sdot4(q, comp(L.l[j][2], i), a2, false);
+            }
+            // |result| < 2^31 by the limb bounds; unsigned arithmetic keeps the
+            // intermediate sums well defined.
+            const int t = (int)(((uint32_t)a0 << 14) + ((uint32_t)a1 << 7) + (uint32_t)a2);
+            const uint32_t sw = j < 2 ? r.sc.x : r.sc.y;
+            const float sc = (float)(int)__builtin_amdgcn_sbfe(sw, 8u * (uint32_t)(m + 2 * (j & 1)), 8u);
+            // d folded in before t: t * s alone (a sum of codes times x) can
+            // overflow where the dot itself does not.
+            acc = __builtin_fmaf((float)t, (sc * d) * L.s[j], acc);
+        }
+        return acc;
+    }
+};
+
+template <int S> struct LimbShape {
+    static constexpr int W = S == 1 ? 8 : 4 * S; // wavefronts per workgroup
+    static constexpr int RG = W / S;             // row-groups per workgroup
+    static constexpr int T = EMU_WAVE * W;
+    static constexpr int NSB = 256 * S;          // 16-column sub-blocks per row
+    static constexpr int G = T / NSB;            // prologue threads per sub-block
+    static constexpr int CPT = 16 / G;           // prologue columns per thread
+    static_assert(G * NSB == T && (G == 1 || G == 2 || G == 4), "prologue mapping");
+};
+
+// Split this thread's CPT columns (already normalised) into limbs; the G
+// threads of a sub-block are neighbouring lanes.
+template <int G, int CPT>
+__device__ __forceinline__ void make_limbs(const float (&xv)[CPT], LimbRec *rec, int sb, int part)
+{
+    float amax = 0.0f;
+    int bad = 0; // an inf or NaN in the sub-block (fmaxf alone would drop a NaN)
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+        amax = fmaxf(amax, fabsf(xv[k]));
+        bad |= !(fabsf(xv[k]) <= 3.402823466e38f);
+    }
+    if (G >= 2) {
+        amax = fmaxf(amax, __shfl_xor(amax, 1, EMU_WAVE));
+        bad |= __shfl_xor(bad, 1, EMU_WAVE);
+    }
+    if (G >= 4) {
+        amax = fmaxf(amax, __shfl_xor(amax, 2, EMU_WAVE));
+        bad |= __shfl_xor(bad, 2, EMU_WAVE);
+    }
+    const bool finite = !bad;
+    int e = 0;
+    (void)frexpf(finite ? amax : 0.0f, &e);      // amax < 2^e, so |x| * 2^(6-e) < 64
+    uint32_t p0[CPT / 4], p1[CPT / 4], p2[CPT / 4];
+    int sum = 0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+        const float v = finite ? ldexpf(xv[k], 6 - e) : 0.0f; // exact
+        const float f0 = rintf(v);
+        const float r1 = (v - f0) * 128.0f; // exact
+        const float f1 = rintf(r1);
+        const float f2 = rintf((r1 - f1) * 128.0f);
+        const int i0 = (int)f0, i1 = (int)f1, i2 = (int)f2;
+        sum += i0 * 16384 + i1 * 128 + i2;
+        const uint32_t b = ((uint32_t)i0 & 0xffu) | ((uint32_t)i1 & 0xffu) << 8 | ((uint32_t)i2 & 0xffu) << 16;
+        const int sh = 8 * (k & 3);
+        if ((k & 3) == 0) p0[k >> 2] = p1[k >> 2] = p2[k >> 2] = 0u;
+        p0[k >> 2] |= (b & 0xffu) << sh;
+        p1[k >> 2] |= ((b >> 8) & 0xffu) << sh;
+        p2[k >> 2] |= ((b >> 16) & 0xffu) << sh;
+    }
+    if (G >= 2) sum += __shfl_xor(sum, 1, EMU_WAVE);
+    if (G >= 4) sum += __shfl_xor(sum, 2, EMU_WAVE);
+    uint32_t *d0 = reinterpret_cast<uint32_t *>(&rec[sb].l0);
+    uint32_t *d1 = reinterpret_cast<uint32_t *>(&rec[sb].l1);
+    uint32_t *d2 = reinterpret_cast<uint32_t *>(&rec[sb].l2);
+#pragma unroll
+    for (int k = 0; k < CPT / 4; ++k) {
+        d0[part * (CPT / 4) + k] = p0[k];
+        d1[part * (CPT / 4) + k] = p1[k];
+        d2[part * (CPT / 4) + k] = p2[k];
+    }
+    if (part == 0) {
+        rec[sb].s = finite ? ldexpf(1.0f, e - 20) : __int_as_float(0x7fc00000);
+        rec[sb].sum = sum;
+    }
+}
+
+template <class LF, int S, int D, bool DUAL, bool NORM, bool ACC>
+__global__ __launch_bounds__(EMU_WAVE * LimbShape<S>::W) void qmv_limb_kernel(QmvArgs a, int rounds)
+{
+    using SH = LimbShape<S>;
+    constexpr int NR = DUAL ? 2 : 1;
+    __shared__ LimbRec rec[SH::NSB];
+    __shared__ float red[SH::W];
+    __shared__ float part[2][SH::RG][S][D][NR];
+
+    const int tid = threadIdx.x, lane = tid & (EMU_WAVE - 1), wv = tid / EMU_WAVE;
+    const int rg = wv / S, sl = wv % S;
+    const int grg = blockIdx.x * SH::RG + rg, total_rg = gridDim.x * SH::RG;
+    const int unit = sl * EMU_WAVE + lane;
+
+    struct Slot {
+        typename LF::Raw raw[NR];
+        float resid;
+    };
+    auto load_slot = [&](int k, int d, Slot &s) {
+        int row = grg + (k * D + d) * total_rg;
+        row = row < a.rows ? row : a.rows - 1;
+        row = __builtin_amdgcn_readfirstlane(row);
+#pragma unroll
+        for (int n = 0; n < NR; ++n) LF::load((n ? a.w_up : a.w) + (size_t)row * a.row_bytes, unit, s.raw[n]);
+        if (ACC) s.resid = a.y[row];
+    };
+
+    // First rows' loads go out before the prologue, which hides under them.
+    Slot buf[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_slot(0, d, buf[d]);
+
+    {
+        const int sb = tid / SH::G, pi = tid % SH::G;
+        const int c0 = 16 * sb + SH::CPT * pi;
+        float xv[SH::CPT], gv[SH::CPT];
+#pragma unroll
+        for (int k = 0; k < SH::CPT; k += 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(a.x + c0 + k);
+            xv[k] = v.x; xv[k + 1] = v.y; xv[k + 2] = v.z; xv[k + 3] = v.w;
+            if (NORM) {
+                const float4 g = *reinterpret_cast<const float4 *>(a.gain + c0 + k);
+                gv[k] = g.x; gv[k + 1] = g.y; gv[k + 2] = g.z; gv[k + 3] = g.w;
+            }
+        }
+        if (NORM) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < SH::CPT; ++k) ss = __builtin_fmaf(xv[k], xv[k], ss);
+            ss = wave_sum63(ss);
+            if (lane == EMU_WAVE - 1) red[wv] = ss;
+            __syncthreads();
+            float tot = 0.0f;
+#pragma unroll
+            for (int k = 0; k < SH::W; ++k) tot += red[k];
+            const float scale = 1.0f / sqrtf(tot / (float)a.cols + a.eps);
+#pragma unroll
+            for (int k = 0; k < SH::CPT; ++k) xv[k] = __fmul_rn(__fmul_rn(xv[k], scale), gv[k]);
+        }
+        make_limbs<SH::G, SH::CPT>(xv, rec, sb, pi);
+    }
+    __syncthreads();
+    Limbs L;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const LimbRec &r = rec[LF::sub_block(unit, j)];
+        L.l[j][0] = r.l0;
+        L.l[j][1] = r.l1;
+        L.l[j][2] = r.l2;
+        L.s[j] = r.s;
+        L.c[j] = LF::bias(r.sum);
+    }
+
+    uint64_t best = 0;
+    auto finish = [&](int row, const float (&p)[NR], float resid) {
+        float val = p[0];
+        if (DUAL) val = (val / (1.0f + expf(-val))) * p[1];
+        if (row < a.rows) {
+            a.y[row] = ACC ? resid + val : val;
+            if (a.keys) {
+                const uint64_t key = emu_select_key(val, (uint32_t)row, a.tie_last);
+                best = key > best ? key : best;
+            }
+        }
+    };
+
+    for (int k = 0; k < rounds; ++k) {
+        float resid[D]; // this round's residuals (the slots are refilled below)
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            float p[NR];
+#pragma unroll
+            for (int n = 0; n < NR; ++n) p[n] = wave_sum63(LF::dot(buf[d].raw[n], L, unit));
+            resid[d] = ACC ? buf[d].resid : 0.0f;
+            if (k + 1 < rounds) load_slot(k + 1, d, buf[d]);
+            if (S == 1) {
+                if (lane == EMU_WAVE - 1) finish(grg + (k * D + d) * total_rg, p, resid[d]);
+            } else if (lane == EMU_WAVE - 1) {
+#pragma unroll
+                for (int n = 0; n < NR; ++n) part[k & 1][rg][sl][d][n] = p[n];
+            }
+        }
+        if (S > 1) {
+            // Double-buffered by round parity: one barrier per round suffices.
+            __syncthreads();
+            if (sl == 0 && lane == EMU_WAVE - 1) {
+#pragma unroll
+                for (int d = 0; d < D; ++d) {
+                    float p[NR];
+#pragma unroll
+                    for (int n = 0; n < NR; ++n) {
+                        float t = part[k & 1][rg][0][d][n];
+#pragma unroll
+                        for (int s = 1; s < S; ++s) t += part[k & 1][rg][s][d][n];
+                        p[n] = t;
+                    }
+                    finish(grg + (k * D + d) * total_rg, p, resid[d]);
+                }
+            }
+        }
+    }
+    if (a.keys && sl == 0 && lane == EMU_WAVE - 1) a.keys[grg] = best;
+}
+
+constexpr int kLimbD = 2;
+
+template <class LF, int S, bool DUAL, bool NORM, bool ACC>
+void launch_limb_cfg(emu_ctx *ctx, const QmvArgs &a, int blocks)
+{
+    using SH = LimbShape<S>;
+    const int total_rg = blocks * SH::RG;
+    const int rounds = (a.rows + total_rg * kLimbD - 1) / (total_rg * kLimbD);
+    hipLaunchKernelGGL((qmv_limb_kernel<LF, S, kLimbD, DUAL, NORM, ACC>), dim3(blocks), dim3(SH::T), 0, ctx->stream,
+                       a, rounds);
+}
+
+template <class LF, int S>
+int launch_limb_s(emu_ctx *ctx, const QmvArgs &a, int *key_slots)
+{
+    const bool dual = a.w_up != nullptr, norm = a.gain != nullptr, acc = a.accumulate != 0;
+    if (dual && acc) return EMU_E_ARG; // the fused entry point never asks for this
+    const int cus = ctx->cus > 0 ? ctx->cus : 256;
+    // Workgroups per CU: two for single matrices of 4096 columns, one when a
+    // gate/up pair or a split row needs the registers.
+    int per_cu = (S == 1 && !dual) ? 2 : 1;
+    if (const char *v = getenv("EMU_LIMB_BPC")) { // sweep override
+        const int f = atoi(v);
+        if (f >= 1 && f <= 4) per_cu = f;
+    }
+    // No more row-groups than rows (a key slot per row-group must fit the
+    // caller's key stride, which holds rows + 8).
+    const int need = (a.rows + LimbShape<S>::RG - 1) / LimbShape<S>::RG;
+    const int blocks = cus * per_cu < need ? cus * per_cu : need;
+    if (a.keys && blocks * LimbShape<S>::RG > a.key_stride) return EMU_E_CONFIG;
+    if (dual) {
+        if (norm) launch_limb_cfg<LF, S, true, true, false>(ctx, a, blocks);
+        else launch_limb_cfg<LF, S, true, false, false>(ctx, a, blocks);
+    } else if (acc) {
+        if (norm) launch_limb_cfg<LF, S, false, true, true>(ctx, a, blocks);
+        else launch_limb_cfg<LF, S, false, false, true>(ctx, a, blocks);
+    } else {
+        if (norm) launch_limb_cfg<LF, S, false, true, false>(ctx, a, blocks);
+        else launch_limb_cfg<LF, S, false, false, false>(ctx, a, blocks);
+    }
+    EMU_LAUNCH_CHECK(ctx);
+    if (key_slots) *key_slots = blocks * LimbShape<S>::RG;
+    return EMU_OK;
+}
+
+bool limb_disabled()
+{
+    static const bool off = [] {
+        const char *v = getenv("EMU_QMV_LIMB");
+        return v && v[0] == '0';
+    }();
+    return off;
+}
+
+} // namespace
+
+bool emu_limb_supports(int encoding, int cols)
+{
+    if (limb_disabled()) return false;
+    if (encoding != EMU_ENC_Q6_K) return false;
+    return cols == 4096 || cols == 12288;
+}
+
+int emu_launch_limb(emu_ctx *ctx, int encoding, const QmvArgs &a, int *key_slots)
+{
+    if (!emu_limb_supports(encoding, a.cols)) return EMU_E_UNSUPPORTED;
+    if (a.rows <= 0) return EMU_E_ARG;
+    switch (a.cols) {
+    case 4096: return launch_limb_s<LimbQ6K, 1>(ctx, a, key_slots);
+    case 12288: return launch_limb_s<LimbQ6K, 3>(ctx, a, key_slots);
+    default: return EMU_E_UNSUPPORTED;
+    }
+}

@@ -373,6 +373,7 @@ int launch_pipe(emu_ctx *ctx, const QmvArgs &a, int *key_slots)
     int blocks = (n_rg + waves_per_block - 1) / waves_per_block;
     blocks = blocks < max_blocks ? blocks : max_blocks;
     const int total_waves = blocks * waves_per_block;
+    if (a.keys && total_waves > a.key_stride) return EMU_E_CONFIG; // key slot per wave
     const size_t lds = sizeof(float) * (size_t)(lds_x_floats(a.cols) + lds_g_floats(a.cols));
     switch (R) {
     case 4: launch_pipe_r<F, 4>(ctx, a, blocks, total_waves, lds); break;
@@ -412,6 +413,7 @@ int launch_fmt(emu_ctx *ctx, const QmvArgs &a, int n_tok, int *key_slots)
         default: R = rows_per_wave<8, false>(); break;
         }
         *key_slots = (a.rows + R - 1) / R;
+        if (a.keys && *key_slots > a.key_stride) return EMU_E_CONFIG;
     }
     switch (n_tok) {
     case 1: return launch_nt<F, 1>(ctx, a);
@@ -613,6 +615,8 @@ int emu_row_bytes(int encoding, uint32_t cols, size_t *row_bytes)
 int emu_launch_qmv(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int *key_slots)
 {
     if (a.rows == 0 || n_tok == 0) return EMU_OK;
+    if (n_tok == 1 && emu_limb_supports(encoding, a.cols) && !(a.w_up && a.accumulate))
+        return emu_launch_limb(ctx, encoding, a, key_slots);
     switch (encoding) {
     case EMU_ENC_Q6_K: return launch_fmt<FmtQ6K>(ctx, a, n_tok, key_slots);
     case EMU_ENC_Q8_0: return launch_fmt<FmtQ8_0>(ctx, a, n_tok, key_slots);

@@ -84,6 +84,30 @@ def test_greedy_tokens_identical_over_256_steps(ctx, cfg):
     assert list(got) == toks
 
 
+# Qwen3-8B widths (the 4096- and 12288-column integer-limb matvecs at batch 1)
+# with two layers and a short vocabulary, so the oracle keeps up.
+WIDE_QWEN3 = DenseConfig(hidden=4096, heads=32, kv_heads=8, head_dim=128, ffn=12288, vocab=3000, layers=2,
+                         rope_theta=1e6, eps=1e-6, style=_lib.EMU_STYLE_QWEN3, encoding=_lib.Q6_K, tied=False,
+                         qk_norm=True)
+
+
+def test_qwen3_width_decode_matches_oracle(ctx):
+    model = Model(ctx, WIDE_QWEN3)
+    model.synth(4321)
+    steps, context = 12, 80
+    sess = Session(model, 1, context, kv_f16=True)
+    ref = oracle_for(model, context, True, 1)
+    rng = np.random.default_rng(5)
+    worst = 0.0
+    for step in range(steps):
+        toks = rng.integers(0, WIDE_QWEN3.vocab, size=1).astype(np.uint32)
+        nxt, logits = sess.decode_step(toks, want_logits=True)
+        r = ref.step(toks)
+        worst = max(worst, rel_inf(logits[0], r[0]))
+        assert int(nxt[0]) == oracle.argmax(r[0], False), step
+    assert worst <= 1e-3, worst
+
+
 ATTN_SHAPES = [
     # (heads, kv_heads, head_dim, style): group sizes 8, 1, 3 and 2; head dims 64, 256, 128
     (8, 1, 64, _lib.EMU_STYLE_QWEN3),
