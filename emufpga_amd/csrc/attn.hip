@@ -19,6 +19,8 @@
 //   5. writes (max, sum, unnormalised output) per query head; the last
 //      workgroup of the (client, kv head) to finish merges all chunks
 //      (flash-decoding) and resets the arrival counter for the next step.
+//      The hand-off uses agent-scope atomic stores/loads and a relaxed
+//      counter rather than an L2 write-back fence.
 // Cache layout: [client][layer][kv_head][context][head_dim], f16 or f32.
 #include "internal.hpp"
 
@@ -31,7 +33,7 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * EMU_WAVE;
 constexpr int kPP = 16;              // positions per wavefront
 constexpr int kChunk = kWaves * kPP; // positions per workgroup
-constexpr int kMergeChunks = 256;    // chunk weights kept in LDS by the merge
+constexpr int kMergeBatch = 16;      // chunks whose partials the merge loads at once
 
 struct AttnArgs {
     const float *qkv;       // [client][q_width + 2*kv_width]
@@ -84,35 +86,44 @@ __device__ __forceinline__ void prep_head(const float *src, float *dst, const fl
 {
     constexpr int NP = HD / 2;
     constexpr int PPL = (NP + EMU_WAVE - 1) / EMU_WAVE;
-    float a[PPL], b[PPL];
+    float a[PPL], b[PPL], ga[PPL], gb[PPL];
+    float2 cs[PPL];
     int ia[PPL], ib[PPL];
-    float ss = 0.0f;
+    // Every load (values, gains, rotation table) first: one round trip.
 #pragma unroll
     for (int j = 0; j < PPL; ++j) {
         const int i = lane + EMU_WAVE * j;
-        const bool act = i < NP;
-        ia[j] = interleaved ? 2 * i : i;
-        ib[j] = interleaved ? 2 * i + 1 : i + NP;
-        a[j] = act ? src[ia[j]] : 0.0f;
-        b[j] = act ? src[ib[j]] : 0.0f;
-        ss = __builtin_fmaf(a[j], a[j], ss);
-        ss = __builtin_fmaf(b[j], b[j], ss);
+        const int ic = i < NP ? i : NP - 1; // in-bounds stand-in for idle lanes
+        ia[j] = interleaved ? 2 * ic : ic;
+        ib[j] = interleaved ? 2 * ic + 1 : ic + NP;
+        a[j] = src[ia[j]];
+        b[j] = src[ib[j]];
+        cs[j] = rope_row[ic];
+        if (gain) {
+            ga[j] = gain[ia[j]];
+            gb[j] = gain[ib[j]];
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) {
+        if (lane + EMU_WAVE * j < NP) {
+            ss = __builtin_fmaf(a[j], a[j], ss);
+            ss = __builtin_fmaf(b[j], b[j], ss);
+        }
     }
     if (gain) {
         const float scale = 1.0f / sqrtf(wave_sum(ss) / (float)HD + eps);
 #pragma unroll
         for (int j = 0; j < PPL; ++j) {
-            if (lane + EMU_WAVE * j < NP) {
-                a[j] = __fmul_rn(__fmul_rn(a[j], scale), gain[ia[j]]);
-                b[j] = __fmul_rn(__fmul_rn(b[j], scale), gain[ib[j]]);
-            }
+            a[j] = __fmul_rn(__fmul_rn(a[j], scale), ga[j]);
+            b[j] = __fmul_rn(__fmul_rn(b[j], scale), gb[j]);
         }
     }
 #pragma unroll
     for (int j = 0; j < PPL; ++j) {
-        const int i = lane + EMU_WAVE * j;
-        if (i < NP) {
-            rotate(a[j], b[j], rope_row[i], fma_form);
+        rotate(a[j], b[j], cs[j], fma_form);
+        if (lane + EMU_WAVE * j < NP) {
             dst[ia[j]] = a[j];
             dst[ib[j]] = b[j];
         }
@@ -349,7 +360,11 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
         }
         return;
     }
-    // 5. Partial for the merge.
+    // 5. Partial for the merge.  The hand-off between workgroups uses
+    // agent-scope atomic stores and loads (written through to, and read from,
+    // the device-coherent level) and a relaxed arrival counter, with every
+    // store completed (s_waitcnt) before the counter moves: no L2 write-back
+    // fence, which costs several microseconds per workgroup on this part.
     for (int idx = tid; idx < GQ * (HD + 2); idx += kThreads) {
         const int g = idx / (HD + 2), j = idx % (HD + 2);
         const int head = kvh * GQ + g;
@@ -359,51 +374,52 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
             val = (accs[0][g][j] + accs[1][g][j]) + (accs[2][g][j] + accs[3][g][j]);
         else
             val = j == HD ? mh[g] : lh[g];
-        pp[j] = val;
+        __hip_atomic_store(pp + j, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    __threadfence();
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (tid == 0) arrived = atomicAdd(a.counters + (size_t)client * a.kv_heads + kvh, 1u);
+    uint32_t *counter = a.counters + (size_t)client * a.kv_heads + kvh;
+    if (tid == 0) arrived = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (arrived != (uint32_t)(n_chunks - 1)) return;
-    __threadfence();
-    // Merge: one wavefront per head reads every chunk's (max, sum) in
-    // parallel and leaves each chunk's weight exp(m_c - M) / L in LDS (chunks
-    // past the LDS table are recomputed); then head lanes sum the outputs.
-    __shared__ float fw[GQP][kMergeChunks];
-    for (int g = w; g < GQ; g += kWaves) {
-        const float *pb = a.partial + ((size_t)client * a.heads + kvh * GQ + g) * a.max_chunks * (HD + 2);
-        float m = -INFINITY;
-        for (int c = lane; c < n_chunks; c += EMU_WAVE) m = fmaxf(m, __builtin_nontemporal_load(pb + c * (HD + 2) + HD));
-        const float M = wave_max(m);
-        float l = 0.0f;
-        for (int c = lane; c < n_chunks; c += EMU_WAVE) {
-            const float *pc = pb + c * (HD + 2);
-            l = __builtin_fmaf(__builtin_nontemporal_load(pc + HD + 1), expf(__builtin_nontemporal_load(pc + HD) - M), l);
-        }
-        const float L = wave_sum(l);
-        for (int c = lane; c < n_chunks && c < kMergeChunks; c += EMU_WAVE)
-            fw[g][c] = expf(__builtin_nontemporal_load(pb + c * (HD + 2) + HD) - M) / L;
-        if (lane == 0) {
-            mh[g] = M;
-            lh[g] = L;
-        }
-    }
-    __syncthreads();
+    // Merge (last workgroup to arrive): thread per (head, dim); each batch of
+    // kMergeBatch chunks is loaded at once and folded into a running
+    // (max, sum, output) -- one memory round trip per batch.
     for (int idx = tid; idx < GQ * HD; idx += kThreads) {
         const int g = idx / HD, d = idx % HD;
         const int head = kvh * GQ + g;
         const float *pb = a.partial + ((size_t)client * a.heads + head) * a.max_chunks * (HD + 2);
-        float O = 0.0f;
-#pragma unroll 8
-        for (int c = 0; c < n_chunks; ++c) {
-            const float f = c < kMergeChunks ? fw[g][c]
-                                              : expf(__builtin_nontemporal_load(pb + c * (HD + 2) + HD) - mh[g]) / lh[g];
-            O = __builtin_fmaf(__builtin_nontemporal_load(pb + c * (HD + 2) + d), f, O);
+        float M = -INFINITY, L = 0.0f, O = 0.0f;
+        for (int c0 = 0; c0 < n_chunks; c0 += kMergeBatch) {
+            float m[kMergeBatch], l[kMergeBatch], o[kMergeBatch];
+#pragma unroll
+            for (int i = 0; i < kMergeBatch; ++i) {
+                const int c = c0 + i < n_chunks ? c0 + i : n_chunks - 1;
+                const float *pc = pb + (size_t)c * (HD + 2);
+                m[i] = __hip_atomic_load(pc + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                l[i] = __hip_atomic_load(pc + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                o[i] = __hip_atomic_load(pc + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            float bm = M;
+#pragma unroll
+            for (int i = 0; i < kMergeBatch; ++i)
+                if (c0 + i < n_chunks) bm = fmaxf(bm, m[i]);
+            const float r = expf(M - bm); // 0 on the first batch (M = -inf)
+            L *= r;
+            O *= r;
+#pragma unroll
+            for (int i = 0; i < kMergeBatch; ++i) {
+                if (c0 + i < n_chunks) {
+                    const float f = expf(m[i] - bm);
+                    L = __builtin_fmaf(l[i], f, L);
+                    O = __builtin_fmaf(o[i], f, O);
+                }
+            }
+            M = bm;
         }
-        outp[head * HD + d] = O;
+        outp[head * HD + d] = O / L;
     }
-    if (tid == 0) atomicExch(a.counters + (size_t)client * a.kv_heads + kvh, 0u);
+    if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int HD, bool F16>

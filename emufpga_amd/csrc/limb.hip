@@ -346,9 +346,9 @@ int launch_limb_s(emu_ctx *ctx, const QmvArgs &a, int *key_slots)
     const bool dual = a.w_up != nullptr, norm = a.gain != nullptr, acc = a.accumulate != 0;
     if (dual && acc) return EMU_E_ARG; // the fused entry point never asks for this
     const int cus = ctx->cus > 0 ? ctx->cus : 256;
-    // Workgroups per CU: two for single matrices of 4096 columns, one when a
-    // gate/up pair or a split row needs the registers.
-    int per_cu = (S == 1 && !dual) ? 2 : 1;
+    // One workgroup per CU: measured fastest for every decode shape (more
+    // resident waves only add contention for the same HBM stream).
+    int per_cu = 1;
     if (const char *v = getenv("EMU_LIMB_BPC")) { // sweep override
         const int f = atoi(v);
         if (f >= 1 && f <= 4) per_cu = f;
