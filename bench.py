@@ -8,10 +8,12 @@ resident in HBM.  Prints one JSON line (see the repository's bench contract).
   value     batch-1 decode tokens/s after a 512-token prompt (fp16 KV)
   batch8    the same model with 8 clients (aggregate tokens/s)
   roofline  the dominant kernel: the fused gate|up Q6_K matvec (RMSNorm +
-            SwiGLU epilogue), 2 x 12288 x 4096 weights = 82,575,360 B per
-            launch, timed with HIP events on the library's stream while it
-            walks all 36 layers (6.2 GB of distinct weights, so nothing is
-            served from the 256 MB Infinity Cache)
+            SwiGLU epilogue, integer-limb dot products), 2 x 12288 x 4096
+            weights = 82,575,360 B per launch, timed with HIP events on the
+            library's stream while it walks all 36 layers (6.2 GB of distinct
+            weights, so nothing is served from the 256 MB Infinity Cache);
+            `traffic` is the HBM bytes per launch that the committed PMC
+            summary (profiles/qmv_limb_gate_up_qwen3_8b_pmc.txt) measured
   cpu_baseline  the oracle (C restatement of the reference CPU path), one
             thread, one token through 1 and 4 layers + output, extrapolated
 """
@@ -36,6 +38,21 @@ from emufpga_amd.serve import QWEN3_8B_Q6K, Model, Session  # noqa: E402
 
 METRIC = "decode tok/s at batch 1 and 8; achieved HBM GB/s vs 8 TB/s peak"
 HBM_PEAK_GBS = 8000.0
+KERNEL = "qmv_limb_kernel<LimbQ6K, S=1, D=2, dual, norm> (fused gate|up, 2 x 12288 x 4096 Q6_K)"
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "qmv_limb_gate_up_qwen3_8b_pmc.txt")
+COPY_BYTES = 256 << 20  # calibration copy for the PMC byte counters
+
+
+def measured_traffic():
+    """HBM bytes per gate|up launch from the committed PMC summary, if any."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def log(msg: str) -> None:
@@ -78,43 +95,57 @@ def time_gate_up(ctx: Context, model: Model, rounds: int) -> tuple[float, int, i
     return ms, algo, rounds * len(bases)
 
 
-def cpu_baseline(model: Model) -> dict:
+def cpu_baseline(model: Model, budget_s: float = 40.0) -> dict:
+    """One batch-1 token through the oracle (single-threaded C restatement of
+    the reference CPU path): the whole model when a one-layer probe says it
+    fits the time budget, else 1 and 4 layers extrapolated."""
     import oracle
 
     cfg = model.cfg
-    n_layers = 4
-    w = {
-        "layers": np.concatenate([model.read_tensor(_lib.EMU_T_LAYER, l) for l in range(n_layers)]),
-        "embed": model.read_tensor(_lib.EMU_T_EMBED),
-        "output": model.read_tensor(_lib.EMU_T_OUTPUT),
-        "attn_norm": model.read_tensor(_lib.EMU_T_ATTN_NORM, dtype=np.float32),
-        "ffn_norm": model.read_tensor(_lib.EMU_T_FFN_NORM, dtype=np.float32),
-        "q_norm": model.read_tensor(_lib.EMU_T_Q_NORM, dtype=np.float32),
-        "k_norm": model.read_tensor(_lib.EMU_T_K_NORM, dtype=np.float32),
-        "out_norm": model.read_tensor(_lib.EMU_T_OUT_NORM, dtype=np.float32),
-    }
+
+    def weights(n_layers):
+        return {
+            "layers": np.concatenate([model.read_tensor(_lib.EMU_T_LAYER, l) for l in range(n_layers)]),
+            "embed": model.read_tensor(_lib.EMU_T_EMBED),
+            "output": model.read_tensor(_lib.EMU_T_OUTPUT),
+            "attn_norm": model.read_tensor(_lib.EMU_T_ATTN_NORM, dtype=np.float32),
+            "ffn_norm": model.read_tensor(_lib.EMU_T_FFN_NORM, dtype=np.float32),
+            "q_norm": model.read_tensor(_lib.EMU_T_Q_NORM, dtype=np.float32),
+            "k_norm": model.read_tensor(_lib.EMU_T_K_NORM, dtype=np.float32),
+            "out_norm": model.read_tensor(_lib.EMU_T_OUT_NORM, dtype=np.float32),
+        }
+
     ocfg = oracle.DenseCfg(hidden=cfg.hidden, heads=cfg.heads, kv_heads=cfg.kv_heads, head_dim=cfg.head_dim,
                            ffn=cfg.ffn, vocab=cfg.vocab, layers=cfg.layers, context=4, rope_theta=cfg.rope_theta,
                            eps=cfg.eps, style=cfg.style, dtype=cfg.encoding, kv_f16=1, tied=0, qk_norm=1)
-    times = {}
-    for limit in (1, n_layers):
+
+    def timed(w, limit):
         orc = oracle.DenseOracle(ocfg, w, 1)
         t0 = time.perf_counter()
         orc.step([17], layers_limit=limit)
-        times[limit] = time.perf_counter() - t0
-        log(f"cpu oracle: {limit} layer(s) + output in {times[limit]:.2f} s")
-    per_layer = (times[n_layers] - times[1]) / (n_layers - 1)
-    full = times[1] + (cfg.layers - 1) * per_layer
-    weight_bytes = model.weight_bytes()
+        dt = time.perf_counter() - t0
+        log(f"cpu oracle: {limit} layer(s) + output in {dt:.2f} s")
+        return dt
+
+    w4 = weights(4)
+    t1, t4 = timed(w4, 1), timed(w4, 4)
+    per_layer = (t4 - t1) / 3
+    estimate = t1 + (cfg.layers - 1) * per_layer
+    if estimate <= budget_s:
+        del w4
+        full = timed(weights(cfg.layers), cfg.layers)
+        how = f"the whole {cfg.layers}-layer model timed: {full:.2f} s/token"
+    else:
+        full = estimate
+        how = f"1 and 4 layers timed, per-layer {per_layer:.3f} s extrapolated to {cfg.layers} layers: {full:.2f} s/token"
     return {
         "value": round(1.0 / full, 5),
         "unit": "tok/s",
         "cores": 1,
         "kind": "port",
-        "sample": (f"one batch-1 token at position 0 through the embedding, 1 and {n_layers} layers and the "
-                   f"151936-row output (single-threaded C restatement of the reference CPU path); per-layer time "
-                   f"({per_layer:.3f} s) extrapolated to {cfg.layers} layers: {full:.2f} s/token"),
-        "algorithmic_gbs": round(weight_bytes / full / 1e9, 3),
+        "sample": ("one batch-1 token at position 0 through the embedding, the layers and the 151936-row output on "
+                   "the single-threaded C restatement of the reference CPU path; " + how),
+        "algorithmic_gbs": round(model.weight_bytes() / full / 1e9, 3),
     }
 
 
@@ -149,8 +180,14 @@ def main() -> int:
     if args.kernel_only:
         ku_ms, ku_bytes, launches = time_gate_up(ctx, model, args.roofline_rounds)
         achieved = ku_bytes / (ku_ms / 1e3) / 1e9
-        print(json.dumps({"kernel": "gate_up", "avg_launch_us": round(ku_ms * 1e3, 3), "launches": launches,
-                          "achieved_gbs": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4)}), flush=True)
+        # One device-to-device copy of known size: its counter readings
+        # calibrate the PMC byte counters (reads COPY_BYTES, writes COPY_BYTES).
+        src, dst = ctx.alloc(COPY_BYTES), ctx.alloc(COPY_BYTES)
+        ctx.check(ctx.lib.emu_memcpy_dtod(ctx.h, dst.ptr, src.ptr, COPY_BYTES), "calibration copy")
+        ctx.sync()
+        print(json.dumps({"kernel": KERNEL, "avg_launch_us": round(ku_ms * 1e3, 3), "launches": launches,
+                          "achieved_gbs": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4),
+                          "calibration_copy_bytes": COPY_BYTES}), flush=True)
         return 0
 
     rng = np.random.default_rng(42)
@@ -192,7 +229,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "i8xi8->i32 dots + f32",
         "data": "synthetic",
         "config": {
             "workload": (f"Qwen3-8B-shaped dense decoder, Q6_K weights (seeded N(0,0.02) synthetic), batch 1, "
@@ -205,13 +242,13 @@ def main() -> int:
         "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
         "weight_bytes_per_step": weight_bytes,
         "roofline": {
-            "kernel": "qmv_kernel<FmtQ6K,1,dual,norm> (fused gate|up, 12288x4096 pair)",
+            "kernel": KERNEL,
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "avg_launch_us": round(ku_ms * 1e3, 3),
             "algorithmic_bytes_per_launch": ku_bytes,
         },
