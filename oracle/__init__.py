@@ -29,6 +29,15 @@ class DenseCfg(C.Structure):
     ]
 
 
+class MoeDesc(C.Structure):
+    _fields_ = [("enc_gate_up", C.c_int32), ("enc_down", C.c_int32), ("gate", C.c_void_p), ("up", C.c_void_p),
+                ("down", C.c_void_p), ("down_scale", C.c_void_p), ("n_experts", C.c_uint32),
+                ("width", C.c_uint32), ("ff", C.c_uint32), ("k", C.c_uint32), ("act", C.c_int32)]
+
+
+OR_ACT_SILU, OR_ACT_GELU_TANH = 0, 1
+
+
 class DenseWeights(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in
                 ("layers", "embed", "output", "attn_norm", "ffn_norm", "q_norm", "k_norm", "out_norm")]
@@ -75,6 +84,8 @@ def load() -> C.CDLL:
             "or_dense_layer_bytes": ([C.POINTER(DenseCfg)], SZ),
             "or_dense_step": ([C.POINTER(DenseCfg), C.POINTER(DenseWeights), P, P, P, P, U, P, U], I),
             "or_argmax": ([P, U, I], U),
+            "or_gelu_tanh": ([F], F),
+            "or_moe_ffn": ([C.POINTER(MoeDesc), P, U, P, P, P], I),
         }
         for name, (args, res) in sig.items():
             fn = getattr(lib, name)
@@ -167,6 +178,28 @@ def softmax(v: np.ndarray, recip: bool = False) -> np.ndarray:
     v = np.array(v, np.float32, copy=True)
     (load().or_softmax_recip if recip else load().or_softmax_div)(_p(v), v.size)
     return v
+
+
+def gelu_tanh(x: float) -> float:
+    return float(load().or_gelu_tanh(x))
+
+
+def moe_ffn(enc_gate_up: int, enc_down: int, gate, up, down, down_scale, n_experts: int, width: int, ff: int,
+            k: int, act: int, x: np.ndarray, ids: np.ndarray, weights: np.ndarray) -> np.ndarray:
+    """Selected-expert FFN (moe::run after routing); x is n_tok x width."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, width)
+    n_tok = x.shape[0]
+    ids = np.ascontiguousarray(ids, np.uint32).reshape(n_tok, k)
+    weights = np.ascontiguousarray(weights, np.float32).reshape(n_tok, k)
+    bufs = [np.ascontiguousarray(a).view(np.uint8) if a is not None else None for a in (gate, up, down)]
+    sc = np.ascontiguousarray(down_scale, np.float32) if down_scale is not None else None
+    d = MoeDesc(enc_gate_up, enc_down, *[b.ctypes.data if b is not None else None for b in bufs],
+                sc.ctypes.data if sc is not None else None, n_experts, width, ff, k, act)
+    out = np.empty((n_tok, width), np.float32)
+    st = load().or_moe_ffn(C.byref(d), _p(x), n_tok, _p(ids), _p(weights), _p(out))
+    if st != 0:
+        raise ValueError(f"oracle moe_ffn failed ({st})")
+    return out
 
 
 def silu(x: float) -> float:

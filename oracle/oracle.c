@@ -490,6 +490,19 @@ float or_silu(float x)
     return x / den;
 }
 
+/* spm-granite-moe/src/gemma_smoke.rs:88-90 */
+float or_gelu_tanh(float v)
+{
+    float inner = 0.044715f * v;
+    inner = inner * v;
+    inner = 1.0f + inner;
+    float arg = 0.7978846f * v;
+    arg = arg * inner;
+    float t = tanhf(arg);
+    float half = 0.5f * v;
+    return half * (1.0f + t);
+}
+
 /* Rust f32::total_cmp key. */
 static int32_t total_key(float f)
 {
@@ -746,4 +759,80 @@ int or_dense_step(const or_dense_cfg *cfg, const or_dense_weights *w, float *kv_
     }
     free(buf);
     return 0;
+}
+
+/* Selected-expert FFN: spm-granite-moe/src/moe.rs:37-159 (expert_tokens,
+ * activate, accumulate, process_expert, run) and the Gemma expert form of
+ * gemma_smoke.rs:92-139 (fused gate|up rows, gelu, per-expert down scale).
+ * Experts run in ascending id (the BTreeSet of moe.rs:134); each projects the
+ * tokens routed to it in token order with M1 (weights.rs:41-55 ->
+ * math::matvec); output[t] starts at +0.0 and gets lane * weight[slot] added
+ * per expert (moe.rs:58-75). */
+int or_moe_ffn(const or_moe_desc *d, const float *x, uint32_t n_tok, const uint32_t *ids,
+               const float *weights, float *out)
+{
+    uint32_t be_in, bb_in, be_ff, bb_ff;
+    if (or_block_layout(d->enc_gate_up, &be_in, &bb_in) != 0 || or_block_layout(d->enc_down, &be_ff, &bb_ff) != 0)
+        return -2;
+    if (d->width % be_in != 0 || d->ff % be_ff != 0)
+        return -3;
+    const size_t rb_in = (size_t)(d->width / be_in) * bb_in, rb_ff = (size_t)(d->ff / be_ff) * bb_ff;
+    const uint32_t W = d->width, FF = d->ff, K = d->k;
+    float *xs = (float *)malloc(sizeof(float) * (size_t)n_tok * W);
+    float *g = (float *)malloc(sizeof(float) * (size_t)n_tok * FF);
+    float *u = (float *)malloc(sizeof(float) * (size_t)n_tok * FF);
+    float *dn = (float *)malloc(sizeof(float) * (size_t)n_tok * W);
+    uint32_t *tok = (uint32_t *)malloc(sizeof(uint32_t) * (n_tok ? n_tok : 1));
+    int st = 0;
+    for (size_t i = 0; i < (size_t)n_tok * W; ++i)
+        out[i] = 0.0f;
+    for (uint32_t e = 0; e < d->n_experts && st == 0; ++e) {
+        uint32_t cnt = 0;
+        for (uint32_t t = 0; t < n_tok; ++t)
+            for (uint32_t s = 0; s < K; ++s)
+                if (ids[(size_t)t * K + s] == e) {
+                    tok[cnt++] = t;
+                    break;
+                }
+        if (cnt == 0)
+            continue;
+        for (uint32_t i = 0; i < cnt; ++i)
+            memcpy(xs + (size_t)i * W, x + (size_t)tok[i] * W, sizeof(float) * W);
+        const uint8_t *gw, *uw;
+        if (d->up) {
+            gw = d->gate + (size_t)e * FF * rb_in;
+            uw = d->up + (size_t)e * FF * rb_in;
+        } else {
+            gw = d->gate + (size_t)e * 2 * FF * rb_in;
+            uw = gw + (size_t)FF * rb_in;
+        }
+        st |= or_qmatvec(d->enc_gate_up, gw, FF, W, xs, cnt, g, 1);
+        st |= or_qmatvec(d->enc_gate_up, uw, FF, W, xs, cnt, u, 1);
+        for (size_t i = 0; i < (size_t)cnt * FF; ++i) {
+            float a = d->act == OR_ACT_GELU_TANH ? or_gelu_tanh(g[i]) : or_silu(g[i]);
+            g[i] = a * u[i];
+        }
+        st |= or_qmatvec(d->enc_down, d->down + (size_t)e * W * rb_ff, W, FF, g, cnt, dn, 1);
+        for (uint32_t i = 0; i < cnt; ++i) {
+            const uint32_t t = tok[i];
+            uint32_t slot = 0;
+            while (ids[(size_t)t * K + slot] != e)
+                ++slot;
+            const float w = weights[(size_t)t * K + slot];
+            const float sc = d->down_scale ? d->down_scale[e] : 1.0f;
+            for (uint32_t c = 0; c < W; ++c) {
+                float v = dn[(size_t)i * W + c];
+                if (d->down_scale)
+                    v = v * sc;
+                float p = v * w;
+                out[(size_t)t * W + c] = out[(size_t)t * W + c] + p;
+            }
+        }
+    }
+    free(xs);
+    free(g);
+    free(u);
+    free(dn);
+    free(tok);
+    return st ? -1 : 0;
 }

@@ -39,6 +39,13 @@
  *   or_dense_step        composition only; pinned through its parts and the
  *                        batched == alone property (spm-batch/tests/
  *                        batching.rs:128-145).
+ *   or_gelu_tanh         closed form in float64 (error bound), gelu(0) = 0,
+ *                        odd-part identity gelu(v) - gelu(-v) = v.
+ *   or_moe_ffn           composition of or_qmatvec / or_silu / or_gelu_tanh;
+ *                        pinned by the reference's expert-order test
+ *                        (moe.rs:166-185: ascending ids), a one-expert case
+ *                        equal to a plain SwiGLU FFN, and weights summing the
+ *                        same expert twice == that expert's output.
  */
 #ifndef EMUFPGA_ORACLE_H
 #define EMUFPGA_ORACLE_H
@@ -108,6 +115,25 @@ void or_route(const float *logits, uint32_t n_experts, uint32_t k, uint32_t *ids
  * variant 2: granite attend (score = dot * c, softmax divide, sum v*score). */
 void or_attend(const float *q, const float *keys, const float *values, uint32_t positions,
                uint32_t heads, uint32_t kv_heads, uint32_t hd, int variant, float c, float *out);
+
+/* gelu with the tanh approximation, spm-granite-moe/src/gemma_smoke.rs:88-90,
+ * evaluated left to right: (0.5*v) * (1 + tanh((0.7978846*v) * (1 + (0.044715*v)*v))). */
+float or_gelu_tanh(float v);
+
+/* ---- selected-expert FFN of one MoE layer ------------------------------- */
+enum { OR_ACT_SILU = 0, OR_ACT_GELU_TANH = 1 };
+typedef struct {
+    int32_t enc_gate_up, enc_down;
+    const uint8_t *gate;      /* n_experts x ff x width blocks (or fused, see up) */
+    const uint8_t *up;        /* same layout; NULL: gate holds per expert 2*ff rows, gate then up */
+    const uint8_t *down;      /* n_experts x width x ff blocks */
+    const float *down_scale;  /* per-expert output scale (gemma_smoke.rs:129-137) or NULL */
+    uint32_t n_experts, width, ff, k;
+    int32_t act;              /* OR_ACT_* */
+} or_moe_desc;
+/* moe::run after routing: ids/weights are n_tok x k (or_route's output). */
+int or_moe_ffn(const or_moe_desc *d, const float *x, uint32_t n_tok, const uint32_t *ids,
+               const float *weights, float *out);
 
 /* ---- dense decoder (one decode step for n clients) ---------------------- */
 enum { OR_STYLE_QWEN3 = 0, OR_STYLE_SMOL = 1 };

@@ -146,3 +146,36 @@ def q6_pipeline_fixture(blocks: int) -> np.ndarray:
 def dyadic(rng: np.random.Generator, shape, lo=-8, hi=8, denom=16) -> np.ndarray:
     """Multiples of 1/denom: sums and products of these stay exact in f32 at test sizes."""
     return (rng.integers(lo, hi + 1, size=shape) / denom).astype(np.float32)
+
+
+def gelu_tanh_f64(v):
+    v = np.asarray(v, np.float64)
+    return 0.5 * v * (1.0 + np.tanh(0.7978846 * v * (1.0 + 0.044715 * v * v)))
+
+
+def silu_f64(v):
+    v = np.asarray(v, np.float64)
+    return v / (1.0 + np.exp(-v))
+
+
+def moe_ffn_f64(enc_in, enc_down, gate, up, down, down_scale, n_experts, width, ff, k, gelu, x, ids, weights):
+    """The selected-expert FFN in float64 from this module's own decoders:
+    out[t] = sum over the token's slots of w * down_e(act(gate_e x) * up_e x) (* scale_e)."""
+    dec_in, dec_dn = DECODERS[enc_in], DECODERS[enc_down]
+    g_all = dec_in(gate).astype(np.float64)
+    g_all = g_all.reshape(n_experts, (1 if up is not None else 2) * ff, width)
+    u_all = dec_in(up).astype(np.float64).reshape(n_experts, ff, width) if up is not None else g_all[:, ff:]
+    g_all = g_all[:, :ff]
+    d_all = dec_dn(down).astype(np.float64).reshape(n_experts, width, ff)
+    x = np.asarray(x, np.float64).reshape(-1, width)
+    out = np.zeros_like(x)
+    act = gelu_tanh_f64 if gelu else silu_f64
+    for t in range(x.shape[0]):
+        for s in range(k):
+            e = int(ids[t][s])
+            h = act(g_all[e] @ x[t]) * (u_all[e] @ x[t])
+            v = d_all[e] @ h
+            if down_scale is not None:
+                v = v * float(down_scale[e])
+            out[t] += float(weights[t][s]) * v
+    return out

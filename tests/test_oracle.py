@@ -317,3 +317,76 @@ def test_dense_step_batched_equals_alone():  # spm-batch/tests/batching.rs:128-1
         lb2 = both.step([a, b])
         la = alone.step([a])
         assert np.array_equal(bits(lb2[0]), bits(la[0]))
+
+
+def test_gelu_tanh_closed_form_and_odd_part():  # spm-granite-moe/src/gemma_smoke.rs:88-90
+    v = np.linspace(-8, 8, 2001).astype(np.float32)
+    got = np.array([oracle.gelu_tanh(float(a)) for a in v], np.float64)
+    ref = npref.gelu_tanh_f64(v)
+    # f32 evaluation: a few ulp relative, plus the cancellation of 1 + tanh(..) for v < 0,
+    # worth at most one ulp of 1.0 times 0.5|v|
+    assert np.all(np.abs(got - ref) <= 4e-7 * np.abs(ref) + 6e-8 * np.abs(v) + 1e-30)
+    assert oracle.gelu_tanh(0.0) == 0.0
+    # tanh is odd: gelu(v) - gelu(-v) == v in exact arithmetic
+    odd = np.array([oracle.gelu_tanh(float(a)) - oracle.gelu_tanh(float(-a)) for a in v], np.float64)
+    assert np.all(np.abs(odd - v) <= 2e-7 * np.maximum(np.abs(v), 1.0))
+
+
+def _moe_case(rng, enc_in, enc_down, n_experts, width, ff, fused):
+    n_in = n_experts * (2 if fused else 1) * ff * width // npref.BLOCK_ELEMS[enc_in]
+    gate = npref.random_blocks(enc_in, n_in, rng)
+    up = None if fused else npref.random_blocks(enc_in, n_in, rng)
+    down = npref.random_blocks(enc_down, n_experts * width * ff // npref.BLOCK_ELEMS[enc_down], rng)
+    return gate, up, down
+
+
+@pytest.mark.parametrize("enc_in,enc_down,fused,gelu", [(oracle.OR_Q6_K, oracle.OR_Q6_K, False, False),
+                                                        (oracle.OR_Q2_K, oracle.OR_Q2_K, False, False),
+                                                        (oracle.OR_Q5_K, oracle.OR_Q8_0, True, True)])
+def test_moe_ffn_against_float64_composition(enc_in, enc_down, fused, gelu):
+    """moe::run (moe.rs:37-159) against an independent float64 restatement
+    built from numpy decoders: per-token weighted sum of the routed experts."""
+    rng = np.random.default_rng(enc_in * 7 + enc_down)
+    E, W, FF, K, T = 6, 256, 256 if enc_down != oracle.OR_Q8_0 else 64, 3, 4
+    gate, up, down = _moe_case(rng, enc_in, enc_down, E, W, FF, fused)
+    x = rng.normal(size=(T, W)).astype(np.float32)
+    logits = rng.normal(size=(T, E)).astype(np.float32)
+    ids, wts = zip(*[oracle.route(logits[t], K) for t in range(T)])
+    ids, wts = np.array(ids), np.array(wts)
+    scale = rng.uniform(0.5, 2.0, E).astype(np.float32) if fused else None
+    act = oracle.OR_ACT_GELU_TANH if gelu else oracle.OR_ACT_SILU
+    got = oracle.moe_ffn(enc_in, enc_down, gate, up, down, scale, E, W, FF, K, act, x, ids, wts)
+    ref = npref.moe_ffn_f64(enc_in, enc_down, gate, up, down, scale, E, W, FF, K, gelu, x, ids, wts)
+    assert np.max(np.abs(got - ref)) <= 1e-4 * np.max(np.abs(ref))
+
+
+def test_moe_ffn_single_expert_is_plain_swiglu_ffn():
+    rng = np.random.default_rng(5)
+    E, W, FF = 3, 256, 512
+    gate, up, down = _moe_case(rng, oracle.OR_Q6_K, oracle.OR_Q6_K, E, W, FF, False)
+    x = rng.normal(size=(2, W)).astype(np.float32)
+    ids, wts = np.array([[1], [2]]), np.ones((2, 1), np.float32)
+    got = oracle.moe_ffn(oracle.OR_Q6_K, oracle.OR_Q6_K, gate, up, down, None, E, W, FF, 1, oracle.OR_ACT_SILU,
+                         x, ids, wts)
+    rb_in, rb_dn = W // 256 * 210, FF // 256 * 210
+    for t, e in enumerate([1, 2]):
+        g = oracle.qmatvec(oracle.OR_Q6_K, gate[e * FF * rb_in:(e + 1) * FF * rb_in], FF, W, x[t], 1)
+        u = oracle.qmatvec(oracle.OR_Q6_K, up[e * FF * rb_in:(e + 1) * FF * rb_in], FF, W, x[t], 1)
+        h = (np.array([oracle.silu(float(a)) for a in g], np.float32) * u).astype(np.float32)
+        y = oracle.qmatvec(oracle.OR_Q6_K, down[e * W * rb_dn:(e + 1) * W * rb_dn], W, FF, h, 1)
+        assert np.array_equal(got[t], y)  # 0.0 + y * 1.0 == y
+
+
+def test_moe_ffn_sums_experts_in_ascending_id_order():  # moe.rs:166-185
+    """out = ((0 + v_lo * w_lo) + v_hi * w_hi) whatever order the route lists them in."""
+    rng = np.random.default_rng(6)
+    E, W, FF = 4, 256, 256
+    gate, up, down = _moe_case(rng, oracle.OR_Q6_K, oracle.OR_Q6_K, E, W, FF, False)
+    x = rng.normal(size=(1, W)).astype(np.float32)
+    w = np.array([[0.3, 0.7]], np.float32)
+    a = oracle.moe_ffn(oracle.OR_Q6_K, oracle.OR_Q6_K, gate, up, down, None, E, W, FF, 2, oracle.OR_ACT_SILU,
+                       x, np.array([[3, 0]]), w)
+    one = [oracle.moe_ffn(oracle.OR_Q6_K, oracle.OR_Q6_K, gate, up, down, None, E, W, FF, 1, oracle.OR_ACT_SILU,
+                          x, np.array([[e]]), np.ones((1, 1), np.float32))[0] for e in (0, 3)]
+    want = (np.float32(0.0) + one[0] * w[0, 1]).astype(np.float32) + (one[1] * w[0, 0]).astype(np.float32)
+    assert np.array_equal(a[0], want.astype(np.float32))
