@@ -105,6 +105,17 @@ _ERRORS = {
 }
 
 
+EMU_ACT_SILU, EMU_ACT_GELU_TANH = 0, 1
+
+
+class MoeDesc(C.Structure):
+    _fields_ = [
+        ("enc_gate_up", C.c_int32), ("enc_down", C.c_int32), ("d_gate", C.c_void_p), ("d_up", C.c_void_p),
+        ("d_down", C.c_void_p), ("d_down_scale", C.c_void_p), ("n_experts", C.c_uint32),
+        ("width", C.c_uint32), ("ff", C.c_uint32), ("k", C.c_uint32), ("act", C.c_int32),
+    ]
+
+
 class ModelConfig(C.Structure):
     _fields_ = [
         ("hidden", C.c_uint32), ("heads", C.c_uint32), ("kv_heads", C.c_uint32),
@@ -152,6 +163,8 @@ SIGNATURES = {
     "emu_attend_cached": [P, P, P, P, I, U32, U32, U32, U32, F, P],
     "emu_route": [P, P, U32, U32, U32, P, P],
     "emu_argmax": [P, P, U32, U32, I, P],
+    "emu_moe_workspace_bytes": [U32, U32, U32, U32],
+    "emu_moe_ffn": [P, C.POINTER(MoeDesc), P, U32, P, P, P, SZ, P],
     "emu_model_create": [P, C.POINTER(ModelConfig), C.POINTER(P)],
     "emu_model_destroy": [P],
     "emu_model_tensor": [P, I, U32, C.POINTER(P), C.POINTER(SZ)],
@@ -166,7 +179,7 @@ SIGNATURES = {
     "emu_session_positions": [P, P],
     "emu_session_read_kv": [P, U32, U32, I, P, U32],
 }
-_RESTYPE = {"emu_strerror": C.c_char_p, "emu_last_error": C.c_char_p}
+_RESTYPE = {"emu_strerror": C.c_char_p, "emu_last_error": C.c_char_p, "emu_moe_workspace_bytes": C.c_size_t}
 
 _lib = None
 

@@ -1,0 +1,295 @@
+// moe.hip -- selected-expert FFN of one MoE layer (moe::run,
+// spm-granite-moe/src/moe.rs:37-159; the Gemma expert form of
+// gemma_smoke.rs:92-139).
+//
+// After routing (emu_route: ids and weights, n_tok x k), three launches:
+//   1. gate|up: grid (expert, 16-row tile).  A wavefront finds the tokens
+//      routed to its expert with one ballot over the n_tok*k routing table
+//      (token order, as expert_tokens does), streams each gate and up row once
+//      for all of them, and writes act(gate) * up per (token, slot);
+//   2. down: grid (expert, 16-row tile) over the hidden rows, reading the
+//      activations of the expert's tokens, times the expert's optional output
+//      scale, into a per-(token, slot) contribution;
+//   3. combine: per token, output = +0.0 plus contribution * weight added in
+//      ascending expert id (accumulate, moe.rs:58-75, with the experts visited
+//      in BTreeSet order), each product rounded before the add.
+// Experts nobody chose cost one ballot per wavefront.  Weights are read once
+// per step however many tokens share an expert (the reference's batch reuse).
+#include "internal.hpp"
+
+#include <math.h>
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowsPerWave = 4;
+constexpr int kRowsPerBlock = kRowsPerWave * (kThreads / EMU_WAVE);
+constexpr int kMaxTok = 8;
+
+struct MoeArgs {
+    const uint8_t *gate, *up, *down; // up == nullptr: gate holds 2*ff rows per expert (gate, then up)
+    const float *down_scale;         // per expert, or null
+    size_t rb_in, rb_ff;             // row bytes of gate/up rows (width cols) and down rows (ff cols)
+    int nb_in, nb_ff;                // blocks per row
+    int n_experts, width, ff, k, n_tok, act;
+    const float *x;                  // n_tok x width
+    const int32_t *ids;              // n_tok x k
+    const float *weights;            // n_tok x k
+    float *act_buf;                  // (n_tok*k) x ff
+    float *contrib;                  // (n_tok*k) x width
+    float *out;                      // n_tok x width
+};
+
+__device__ __forceinline__ void load8(const float *p, float v[8])
+{
+    const float4 a = *reinterpret_cast<const float4 *>(p);
+    const float4 b = *reinterpret_cast<const float4 *>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+// The routing-table entries (t*k + slot) that chose expert e, ascending
+// (token order); at most kMaxTok of them, since a token picks an expert once.
+__device__ __forceinline__ int expert_slots(const MoeArgs &a, int e, int lane, int (&slot)[kMaxTok])
+{
+    const int nk = a.n_tok * a.k;
+    const bool hit = lane < nk && a.ids[lane] == e;
+    uint64_t m = __ballot(hit);
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxTok; ++i) {
+        slot[i] = m ? __ffsll((unsigned long long)m) - 1 : 0;
+        cnt += m ? 1 : 0;
+        m &= m - 1;
+    }
+    return cnt;
+}
+
+// gelu, tanh form (gemma_smoke.rs:88-90), left to right, no contraction.
+__device__ __forceinline__ float gelu_tanh(float v)
+{
+#pragma clang fp contract(off)
+    float inner = 0.044715f * v;
+    inner = inner * v;
+    inner = 1.0f + inner;
+    float arg = 0.7978846f * v;
+    arg = arg * inner;
+    const float t = tanhf(arg);
+    const float half = 0.5f * v;
+    return half * (1.0f + t);
+}
+
+template <int ACT> __device__ __forceinline__ float activate(float g, float u)
+{
+#pragma clang fp contract(off)
+    if (ACT == EMU_ACT_GELU_TANH) return gelu_tanh(g) * u;
+    return (g / (1.0f + expf(-g))) * u; // moe.rs:46-56
+}
+
+// One row of one expert matrix against the cnt routed input vectors
+// (in[slot[t] * in_stride + c]); per-lane partial sums, not yet reduced.
+template <class F>
+__device__ __forceinline__ void row_dots(const uint8_t *row, int nb, const float *in, int in_stride,
+                                         const int (&slot)[kMaxTok], int cnt, int lane, float (&acc)[kMaxTok])
+{
+    const int U = nb * F::UPB;
+    for (int u = lane; u < U; u += EMU_WAVE) {
+        const int blk = u / F::UPB, sub = u % F::UPB;
+        typename F::Raw raw;
+        F::load(row, (uint32_t)blk * F::BB, sub, raw);
+        const int c0 = blk * F::BE;
+#pragma unroll
+        for (int g = 0; g < F::G; ++g) {
+            const Grp gp = F::group(raw, sub, g);
+            float w[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w[i] = grp_weight(gp, i);
+            const int col = c0 + F::col(sub, g);
+#pragma unroll
+            for (int t = 0; t < kMaxTok; ++t) {
+                if (t < cnt) {
+                    float xv[8];
+                    load8(in + (size_t)slot[t] * in_stride + col, xv);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[t] = __builtin_fmaf(w[i], xv[i], acc[t]);
+                }
+            }
+        }
+    }
+}
+
+template <class F, int ACT>
+__global__ __launch_bounds__(kThreads) void moe_up_kernel(MoeArgs a)
+{
+    const int e = blockIdx.x;
+    const int lane = threadIdx.x & (EMU_WAVE - 1), wv = threadIdx.x / EMU_WAVE;
+    int slot[kMaxTok];
+    const int cnt = expert_slots(a, e, lane, slot);
+    if (cnt == 0) return; // uniform: the ballot is the same in every wavefront
+    // Token rows of x: slot / k is the token.
+    int tok[kMaxTok];
+#pragma unroll
+    for (int t = 0; t < kMaxTok; ++t) tok[t] = slot[t] / a.k;
+    const size_t per = (size_t)(a.up ? 1 : 2) * a.ff;
+    for (int i = 0; i < kRowsPerWave; ++i) {
+        const int r = blockIdx.y * kRowsPerBlock + wv * kRowsPerWave + i;
+        if (r >= a.ff) break;
+        const uint8_t *grow = a.gate + ((size_t)e * per + r) * a.rb_in;
+        const uint8_t *urow = a.up ? a.up + ((size_t)e * a.ff + r) * a.rb_in
+                                   : a.gate + ((size_t)e * per + a.ff + r) * a.rb_in;
+        float ag[kMaxTok], au[kMaxTok];
+#pragma unroll
+        for (int t = 0; t < kMaxTok; ++t) ag[t] = au[t] = 0.0f;
+        row_dots<F>(grow, a.nb_in, a.x, a.width, tok, cnt, lane, ag);
+        row_dots<F>(urow, a.nb_in, a.x, a.width, tok, cnt, lane, au);
+#pragma unroll
+        for (int t = 0; t < kMaxTok; ++t) {
+            if (t < cnt) {
+                const float g = wave_sum(ag[t]), u = wave_sum(au[t]);
+                if (lane == 0) a.act_buf[(size_t)slot[t] * a.ff + r] = activate<ACT>(g, u);
+            }
+        }
+    }
+}
+
+template <class F>
+__global__ __launch_bounds__(kThreads) void moe_down_kernel(MoeArgs a)
+{
+    const int e = blockIdx.x;
+    const int lane = threadIdx.x & (EMU_WAVE - 1), wv = threadIdx.x / EMU_WAVE;
+    int slot[kMaxTok];
+    const int cnt = expert_slots(a, e, lane, slot);
+    if (cnt == 0) return;
+    const float scale = a.down_scale ? a.down_scale[e] : 1.0f;
+    for (int i = 0; i < kRowsPerWave; ++i) {
+        const int r = blockIdx.y * kRowsPerBlock + wv * kRowsPerWave + i;
+        if (r >= a.width) break;
+        const uint8_t *row = a.down + ((size_t)e * a.width + r) * a.rb_ff;
+        float acc[kMaxTok];
+#pragma unroll
+        for (int t = 0; t < kMaxTok; ++t) acc[t] = 0.0f;
+        row_dots<F>(row, a.nb_ff, a.act_buf, a.ff, slot, cnt, lane, acc);
+#pragma unroll
+        for (int t = 0; t < kMaxTok; ++t) {
+            if (t < cnt) {
+                float v = wave_sum(acc[t]);
+                if (a.down_scale) v = __fmul_rn(v, scale); // gemma_smoke.rs:129-137
+                if (lane == 0) a.contrib[(size_t)slot[t] * a.width + r] = v;
+            }
+        }
+    }
+}
+
+// Per token: sum over its slots in ascending expert id, from +0.0.
+__global__ __launch_bounds__(kThreads) void moe_combine_kernel(MoeArgs a)
+{
+    const int t = blockIdx.x;
+    int order[kMaxTok];
+    int n = 0;
+    // Selection of the token's slots by expert id (k <= 8; ids are distinct).
+    int prev = -1;
+    for (int i = 0; i < a.k; ++i) {
+        int best = -1, best_id = 0x7fffffff;
+        for (int s = 0; s < a.k; ++s) {
+            const int id = a.ids[t * a.k + s];
+            if (id > prev && id < best_id && id < a.n_experts) {
+                best = s;
+                best_id = id;
+            }
+        }
+        if (best < 0) break;
+        order[n++] = best;
+        prev = best_id;
+    }
+    for (int c = threadIdx.x; c < a.width; c += kThreads) {
+        float sum = 0.0f;
+        for (int i = 0; i < n; ++i) {
+            const int s = t * a.k + order[i];
+            sum = __fadd_rn(sum, __fmul_rn(a.contrib[(size_t)s * a.width + c], a.weights[s]));
+        }
+        a.out[(size_t)t * a.width + c] = sum;
+    }
+}
+
+template <class F> void launch_up(emu_ctx *ctx, const MoeArgs &a)
+{
+    const dim3 grid(a.n_experts, (a.ff + kRowsPerBlock - 1) / kRowsPerBlock);
+    if (a.act == EMU_ACT_GELU_TANH)
+        hipLaunchKernelGGL((moe_up_kernel<F, EMU_ACT_GELU_TANH>), grid, dim3(kThreads), 0, ctx->stream, a);
+    else
+        hipLaunchKernelGGL((moe_up_kernel<F, EMU_ACT_SILU>), grid, dim3(kThreads), 0, ctx->stream, a);
+}
+
+template <class F> void launch_down(emu_ctx *ctx, const MoeArgs &a)
+{
+    const dim3 grid(a.n_experts, (a.width + kRowsPerBlock - 1) / kRowsPerBlock);
+    hipLaunchKernelGGL(moe_down_kernel<F>, grid, dim3(kThreads), 0, ctx->stream, a);
+}
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+} // namespace
+
+extern "C" size_t emu_moe_workspace_bytes(uint32_t n_tok, uint32_t k, uint32_t width, uint32_t ff)
+{
+    const size_t slots = (size_t)n_tok * k;
+    return align256(sizeof(float) * slots * ff) + align256(sizeof(float) * slots * width);
+}
+
+extern "C" int emu_moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok,
+                           const int32_t *d_ids, const float *d_weights, void *d_workspace, size_t workspace_bytes,
+                           float *d_out)
+{
+    if (!ctx || !d || !d_x || !d_ids || !d_weights || !d_out || !d->d_gate || !d->d_down) return EMU_E_ARG;
+    if (n_tok == 0) return EMU_OK;
+    if (n_tok > kMaxTok || d->k == 0 || d->k > 8 || d->n_experts == 0 || d->k > d->n_experts) return EMU_E_ARG;
+    if (d->act != EMU_ACT_SILU && d->act != EMU_ACT_GELU_TANH) return EMU_E_ARG;
+    uint32_t be_in = 0, bb_in = 0, be_ff = 0, bb_ff = 0;
+    int st = emu_block_layout(d->enc_gate_up, &be_in, &bb_in);
+    if (st == EMU_OK) st = emu_block_layout(d->enc_down, &be_ff, &bb_ff);
+    if (st != EMU_OK) return st;
+    if (d->width == 0 || d->ff == 0 || d->width % be_in != 0 || d->ff % be_ff != 0) return EMU_E_SHORT;
+    if (d->width % 8 != 0 || d->ff % 8 != 0) return EMU_E_SHAPE; // 8-column activation groups
+    if (!d_workspace || workspace_bytes < emu_moe_workspace_bytes(n_tok, d->k, d->width, d->ff)) return EMU_E_ARG;
+    MoeArgs a{};
+    a.gate = static_cast<const uint8_t *>(d->d_gate);
+    a.up = static_cast<const uint8_t *>(d->d_up);
+    a.down = static_cast<const uint8_t *>(d->d_down);
+    a.down_scale = d->d_down_scale;
+    a.nb_in = (int)(d->width / be_in);
+    a.nb_ff = (int)(d->ff / be_ff);
+    a.rb_in = (size_t)a.nb_in * bb_in;
+    a.rb_ff = (size_t)a.nb_ff * bb_ff;
+    a.n_experts = (int)d->n_experts;
+    a.width = (int)d->width;
+    a.ff = (int)d->ff;
+    a.k = (int)d->k;
+    a.n_tok = (int)n_tok;
+    a.act = d->act;
+    a.x = d_x;
+    a.ids = d_ids;
+    a.weights = d_weights;
+    a.act_buf = static_cast<float *>(d_workspace);
+    a.contrib = reinterpret_cast<float *>(static_cast<uint8_t *>(d_workspace) +
+                                          align256(sizeof(float) * (size_t)n_tok * d->k * d->ff));
+    a.out = d_out;
+    switch (d->enc_gate_up) {
+    case EMU_ENC_Q6_K: launch_up<FmtQ6K>(ctx, a); break;
+    case EMU_ENC_Q8_0: launch_up<FmtQ8_0>(ctx, a); break;
+    case EMU_ENC_Q5_K: launch_up<FmtQ5K>(ctx, a); break;
+    case EMU_ENC_Q2_K: launch_up<FmtQ2K>(ctx, a); break;
+    default: return EMU_E_UNSUPPORTED;
+    }
+    EMU_LAUNCH_CHECK(ctx);
+    switch (d->enc_down) {
+    case EMU_ENC_Q6_K: launch_down<FmtQ6K>(ctx, a); break;
+    case EMU_ENC_Q8_0: launch_down<FmtQ8_0>(ctx, a); break;
+    case EMU_ENC_Q5_K: launch_down<FmtQ5K>(ctx, a); break;
+    case EMU_ENC_Q2_K: launch_down<FmtQ2K>(ctx, a); break;
+    default: return EMU_E_UNSUPPORTED;
+    }
+    EMU_LAUNCH_CHECK(ctx);
+    hipLaunchKernelGGL(moe_combine_kernel, dim3(n_tok), dim3(kThreads), 0, ctx->stream, a);
+    EMU_LAUNCH_CHECK(ctx);
+    return EMU_OK;
+}

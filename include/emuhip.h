@@ -178,6 +178,32 @@ int emu_attend_cached(emu_ctx *ctx, const float *d_q, const void *d_keys, const 
 int emu_route(emu_ctx *ctx, const float *d_logits, uint32_t n_tok, uint32_t n_experts,
               uint32_t k, int32_t *d_ids, float *d_weights);
 
+/* Selected-expert FFN of one MoE layer for n_tok (<= 8) tokens after routing:
+ * moe::run (spm-granite-moe/src/moe.rs:37-159: expert_tokens, activate,
+ * process_expert, accumulate) with weights::project_expert
+ * (weights.rs:41-55), and the Gemma expert form (gemma_smoke.rs:92-139: one
+ * fused gate|up matrix per expert, gelu, a per-expert down scale).
+ * For token t: out[t] = +0.0, then for its slots in ascending expert id,
+ * out[t] += down_e(act(gate_e x_t) * up_e x_t) (* down_scale[e]) * weight.
+ * Expert tensors are expert-major GGUF blocks: gate/up n_experts x ff rows of
+ * width columns (d_up NULL: d_gate holds 2*ff rows per expert, gate rows
+ * then up rows); down n_experts x width rows of ff columns.  ids/weights are
+ * n_tok x k as emu_route writes them (distinct ids per token).  The
+ * workspace holds n_tok*k activation rows and contributions
+ * (emu_moe_workspace_bytes). */
+enum { EMU_ACT_SILU = 0, EMU_ACT_GELU_TANH = 1 };
+typedef struct emu_moe_desc {
+    int32_t enc_gate_up, enc_down;
+    const void *d_gate, *d_up, *d_down;
+    const float *d_down_scale; /* per-expert output scale or NULL */
+    uint32_t n_experts, width, ff, k;
+    int32_t act;               /* EMU_ACT_* */
+} emu_moe_desc;
+size_t emu_moe_workspace_bytes(uint32_t n_tok, uint32_t k, uint32_t width, uint32_t ff);
+int emu_moe_ffn(emu_ctx *ctx, const emu_moe_desc *desc, const float *d_x, uint32_t n_tok,
+                const int32_t *d_ids, const float *d_weights, void *d_workspace, size_t workspace_bytes,
+                float *d_out);
+
 /* Greedy selection over n_rows rows of width: tie_last 0 = lowest index of the
  * maximum (top_k, spm-qwen3-slice/src/math.rs:38-48); 1 = last index
  * (max_by(partial_cmp), spm-batch/tests/batching.rs:111-123). */
