@@ -203,7 +203,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
 
     __shared__ float q_s[GQP][HD];
     __shared__ float knew[HD], vnew[HD];
-    __shared__ float sc[GQP][kChunk];
+    __shared__ __align__(16) float sc[GQP][kChunk];
     __shared__ float mh[GQP], lh[GQP];
     __shared__ float accs[kWaves][GQP][HD];
     __shared__ uint32_t arrived;
@@ -272,14 +272,18 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     for (int g = 0; g < GQP; ++g)
 #pragma unroll
         for (int e = 0; e < EPL; ++e) qreg[g][e] = q_s[g][lane * EPL + e];
+    // Branch-free: a branch per position puts each LDS read behind its own
+    // wait.  The new key is read once and selected where its position is.
+    float kfresh[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) kfresh[e] = knew[lane * EPL + e];
     float kf[kPP][EPL];
 #pragma unroll
     for (int pp = 0; pp < kPP; ++pp) {
         unpack_row<EPL, F16>(kr[pp], kf[pp]);
-        if (pw + pp == pos) {
+        const bool is_new = pw + pp == pos;
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) kf[pp][e] = knew[lane * EPL + e];
-        }
+        for (int e = 0; e < EPL; ++e) kf[pp][e] = is_new ? kfresh[e] : kf[pp][e];
     }
     constexpr int SHIFT = NV >= 64 ? 0 : (NV == 32 ? 1 : 2);
 #pragma unroll
@@ -319,6 +323,21 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     }
     __syncthreads();
 
+    // Weighted values, branch-free: every head's 16 weights of this
+    // wavefront's positions come in with four 16-byte LDS reads, the new value
+    // is read once and selected, and all GQP heads accumulate (the rows past
+    // GQ hold zero queries' scores and are never written out).
+    float wgt[GQP][kPP];
+#pragma unroll
+    for (int g = 0; g < GQP; ++g)
+#pragma unroll
+        for (int q4 = 0; q4 < kPP / 4; ++q4) {
+            const float4 v4 = *reinterpret_cast<const float4 *>(&sc[g][w * kPP + 4 * q4]);
+            wgt[g][4 * q4] = v4.x; wgt[g][4 * q4 + 1] = v4.y; wgt[g][4 * q4 + 2] = v4.z; wgt[g][4 * q4 + 3] = v4.w;
+        }
+    float vn[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) vn[e] = vnew[lane * EPL + e];
     float acc[GQP][EPL];
 #pragma unroll
     for (int g = 0; g < GQP; ++g)
@@ -329,21 +348,14 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
         const int p = pw + pp;
         float vf[EPL];
         unpack_row<EPL, F16>(vr[pp], vf);
-        if (p == pos) {
+        // the new position takes the appended value; stand-in rows past the
+        // context are zeroed so that their zero weight cannot meet a NaN
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) vf[e] = vnew[lane * EPL + e];
-        } else if (p >= n) { // stand-in row: zero, so that its zero weight cannot meet a NaN
+        for (int e = 0; e < EPL; ++e) vf[e] = p == pos ? vn[e] : (p >= n ? 0.0f : vf[e]);
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) vf[e] = 0.0f;
-        }
+        for (int g = 0; g < GQP; ++g)
 #pragma unroll
-        for (int g = 0; g < GQP; ++g) {
-            if (g < GQ) {
-                const float wgt = sc[g][w * kPP + pp];
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) acc[g][e] = __builtin_fmaf(wgt, vf[e], acc[g][e]);
-            }
-        }
+            for (int e = 0; e < EPL; ++e) acc[g][e] = __builtin_fmaf(wgt[g][pp], vf[e], acc[g][e]);
     }
 #pragma unroll
     for (int g = 0; g < GQP; ++g)
@@ -382,43 +394,61 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     if (tid == 0) arrived = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (arrived != (uint32_t)(n_chunks - 1)) return;
-    // Merge (last workgroup to arrive): thread per (head, dim); each batch of
-    // kMergeBatch chunks is loaded at once and folded into a running
-    // (max, sum, output) -- one memory round trip per batch.
-    for (int idx = tid; idx < GQ * HD; idx += kThreads) {
-        const int g = idx / HD, d = idx % HD;
-        const int head = kvh * GQ + g;
-        const float *pb = a.partial + ((size_t)client * a.heads + head) * a.max_chunks * (HD + 2);
-        float M = -INFINITY, L = 0.0f, O = 0.0f;
-        for (int c0 = 0; c0 < n_chunks; c0 += kMergeBatch) {
-            float m[kMergeBatch], l[kMergeBatch], o[kMergeBatch];
+    // Merge (last workgroup to arrive): each thread owns NI (head, dim)
+    // outputs, and every batch of MB chunks' (max, sum, output) values for
+    // all of them is loaded at once and folded into running (M, L, O): one
+    // memory round trip per batch for the whole thread.
+    constexpr int NI = (GQP * HD + kThreads - 1) / kThreads;
+    constexpr int MB = NI <= 2 ? kMergeBatch : 32 / NI;
+    float M[NI], L[NI], O[NI];
+    const float *pb[NI];
+    int head_of[NI], dim_of[NI];
+    bool live[NI];
 #pragma unroll
-            for (int i = 0; i < kMergeBatch; ++i) {
-                const int c = c0 + i < n_chunks ? c0 + i : n_chunks - 1;
-                const float *pc = pb + (size_t)c * (HD + 2);
-                m[i] = __hip_atomic_load(pc + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                l[i] = __hip_atomic_load(pc + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                o[i] = __hip_atomic_load(pc + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            float bm = M;
-#pragma unroll
-            for (int i = 0; i < kMergeBatch; ++i)
-                if (c0 + i < n_chunks) bm = fmaxf(bm, m[i]);
-            const float r = expf(M - bm); // 0 on the first batch (M = -inf)
-            L *= r;
-            O *= r;
-#pragma unroll
-            for (int i = 0; i < kMergeBatch; ++i) {
-                if (c0 + i < n_chunks) {
-                    const float f = expf(m[i] - bm);
-                    L = __builtin_fmaf(l[i], f, L);
-                    O = __builtin_fmaf(o[i], f, O);
-                }
-            }
-            M = bm;
-        }
-        outp[head * HD + d] = O / L;
+    for (int i = 0; i < NI; ++i) {
+        const int idx = tid + i * kThreads;
+        live[i] = idx < GQ * HD;
+        const int ic = live[i] ? idx : 0; // in-bounds stand-in
+        head_of[i] = kvh * GQ + ic / HD;
+        dim_of[i] = ic % HD;
+        pb[i] = a.partial + ((size_t)client * a.heads + head_of[i]) * a.max_chunks * (HD + 2);
+        M[i] = -INFINITY;
+        L[i] = 0.0f;
+        O[i] = 0.0f;
     }
+    for (int c0 = 0; c0 < n_chunks; c0 += MB) {
+        float m[NI][MB], l[NI][MB], o[NI][MB];
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int j = 0; j < MB; ++j) {
+                const int c = c0 + j < n_chunks ? c0 + j : n_chunks - 1;
+                const float *pc = pb[i] + (size_t)c * (HD + 2);
+                m[i][j] = __hip_atomic_load(pc + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                l[i][j] = __hip_atomic_load(pc + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                o[i][j] = __hip_atomic_load(pc + dim_of[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            float bm = M[i];
+#pragma unroll
+            for (int j = 0; j < MB; ++j)
+                if (c0 + j < n_chunks) bm = fmaxf(bm, m[i][j]);
+            const float r = expf(M[i] - bm); // 0 on the first batch (M = -inf)
+            L[i] *= r;
+            O[i] *= r;
+#pragma unroll
+            for (int j = 0; j < MB; ++j) {
+                const float f = c0 + j < n_chunks ? expf(m[i][j] - bm) : 0.0f;
+                L[i] = __builtin_fmaf(l[i][j], f, L[i]);
+                O[i] = __builtin_fmaf(o[i][j], f, O[i]);
+            }
+            M[i] = bm;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+        if (live[i]) outp[head_of[i] * HD + dim_of[i]] = O[i] / L[i];
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
