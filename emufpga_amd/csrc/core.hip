@@ -78,6 +78,7 @@ extern "C" int emu_ctx_destroy(emu_ctx *ctx)
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     for (auto &ev : ctx->events)
         if (ev) (void)hipEventDestroy(ev);
+    if (ctx->mfma_ws) (void)hipFree(ctx->mfma_ws);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return EMU_OK;

@@ -26,6 +26,8 @@ struct emu_ctx {
     int cus = 0;
     char arch[64] = {0};
     char last_error[256] = {0};
+    void *mfma_ws = nullptr; // multi-token matvec workspace (mfma.hip), grown on demand
+    size_t mfma_ws_bytes = 0;
 };
 
 int emu_hip_fail(emu_ctx *ctx, hipError_t e, const char *what);
@@ -359,6 +361,13 @@ int emu_row_bytes(int encoding, uint32_t cols, size_t *row_bytes);
 // its launcher (EMU_E_UNSUPPORTED for anything else).
 bool emu_limb_supports(int encoding, int cols);
 int emu_launch_limb(emu_ctx *ctx, int encoding, const QmvArgs &a, int *key_slots);
+// Multi-token (2..8) matvec on the int8 matrix cores (mfma.hip).  Its
+// workspace lives in the context and grows on demand (hipMalloc); callers
+// that capture graphs reserve it beforehand with emu_mfma_reserve.
+bool emu_mfma_supports(int encoding, int cols, int n_tok);
+size_t emu_mfma_workspace_bytes(int rows, int cols, int nmat);
+int emu_mfma_reserve(emu_ctx *ctx, size_t bytes);
+int emu_launch_mfma(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int *key_slots);
 
 // Fused decode attention of one layer for every client (attn.hip).
 struct EmuAttnLaunch {

@@ -1,0 +1,395 @@
+// mfma.hip -- quantized matvec for 2..8 tokens on the int8 matrix cores.
+//
+// The activations are carried as in the batch-1 limb kernel: per token and
+// 16-column sub-block, x ~= s * (16384*L0 + 128*L1 + L2) with |L| <= 64 and
+// s a power of two (exact to 2^-20 of the sub-block's largest |x|).  A Q6_K
+// sub-block is 16 columns, which is exactly the K of v_mfma_i32_32x32x16_i8,
+// so one instruction forms every (token, limb) x (weight row) integer dot of
+// one sub-block for 32 weight rows:
+//
+//     A (32 x 16, int8) = the limbs: M row i = 8 * limb + token (rows 24..31 zero)
+//     B (16 x 32, int8) = the weight codes minus 32 of 32 consecutive rows
+//     D (32 x 32, int32): lane l, register r holds row i = 8*(r/4) + 4*(l/32) + r%4
+//                         of weight row l % 32, i.e. limb r/4 of token 4*(l/32) + r%4
+//
+// so each lane finds the three limb sums of its (row, token) pairs in its own
+// registers and combines them exactly, t = (D0 << 14) + (D1 << 7) + D2, before
+// the one float step per sub-block, acc = fma(t, (sc * d) * s, acc), the same
+// step as the batch-1 kernel.
+//
+// Work split: a workgroup owns 32 weight rows of one matrix and a 2048-column
+// slice (eight 256-column blocks, one per wavefront); the eight wavefronts'
+// sums meet in LDS in a fixed order and the slice's partial sum is written to
+// a workspace.  A finishing pass adds the slices' partials in slice order and
+// applies the epilogue (residual accumulate, SwiGLU of a gate/up pair, greedy
+// selection keys).  Everything is deterministic.
+//
+// Three kernels:
+//   mfma_prep_kernel   x (optionally RMS-normalised) -> A operands + scales
+//   qmv_mfma_kernel    A operands x weight codes -> per-slice partial sums
+//   mfma_finish_kernel partial sums -> y
+#include "internal.hpp"
+
+#include <math.h>
+#include <stdlib.h>
+
+namespace {
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kMaxTok = 8;          // tokens per tile (A rows 8 * limb + token)
+constexpr int kTileRows = 32;       // weight rows per tile (MFMA N)
+constexpr int kWaves = 8;           // wavefronts per workgroup, one 256-column block each
+constexpr int kSlice = kWaves * 256; // columns per workgroup
+constexpr int kSbBytes = 2 * 24 * 8; // A-operand bytes per 16-column sub-block
+constexpr int kPrepThreads = 256;
+constexpr int kFinishThreads = 256;
+
+struct PrepArgs {
+    const float *x; // n_tok x cols
+    const float *gain;
+    float eps;
+    int cols, n_tok;
+    uint8_t *xa; // cols/16 x kSbBytes
+    float *xs;   // cols/16 x kMaxTok
+};
+
+// A-operand layout: sub-block sb, half kh (columns 8kh..8kh+7 of the
+// sub-block), limb, token -> 8 bytes at xa + sb*kSbBytes + (kh*24 + 8*limb + token)*8.
+__global__ __launch_bounds__(kPrepThreads) void mfma_prep_kernel(PrepArgs a)
+{
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float *x = a.x + (size_t)t * a.cols;
+    __shared__ float red[kPrepThreads / EMU_WAVE];
+    float scale = 1.0f;
+    if (a.gain) {
+        float ss = 0.0f;
+        for (int c = 4 * tid; c < a.cols; c += 4 * kPrepThreads) {
+            const float4 v = *reinterpret_cast<const float4 *>(x + c);
+            ss = __builtin_fmaf(v.x, v.x, ss);
+            ss = __builtin_fmaf(v.y, v.y, ss);
+            ss = __builtin_fmaf(v.z, v.z, ss);
+            ss = __builtin_fmaf(v.w, v.w, ss);
+        }
+        ss = wave_sum(ss);
+        if ((tid & (EMU_WAVE - 1)) == 0) red[tid / EMU_WAVE] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kPrepThreads / EMU_WAVE; ++k) tot += red[k];
+        scale = 1.0f / sqrtf(tot / (float)a.cols + a.eps);
+    }
+    // Thread pair (2m, 2m+1) holds the two 8-column halves of one sub-block.
+    for (int p = tid; p < a.cols / 8; p += kPrepThreads) {
+        const int sb = p >> 1, kh = p & 1, c0 = 8 * p;
+        float v[8];
+        const float4 x0 = *reinterpret_cast<const float4 *>(x + c0);
+        const float4 x1 = *reinterpret_cast<const float4 *>(x + c0 + 4);
+        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+        v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+        if (a.gain) {
+            const float4 g0 = *reinterpret_cast<const float4 *>(a.gain + c0);
+            const float4 g1 = *reinterpret_cast<const float4 *>(a.gain + c0 + 4);
+            const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = __fmul_rn(__fmul_rn(v[k], scale), g[k]);
+        }
+        float amax = 0.0f;
+        int bad = 0; // an inf or NaN (fmaxf alone would drop a NaN)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            amax = fmaxf(amax, fabsf(v[k]));
+            bad |= !(fabsf(v[k]) <= 3.402823466e38f);
+        }
+        amax = fmaxf(amax, __shfl_xor(amax, 1, EMU_WAVE));
+        bad |= __shfl_xor(bad, 1, EMU_WAVE);
+        const bool finite = !bad;
+        int e = 0;
+        (void)frexpf(finite ? amax : 0.0f, &e); // amax < 2^e, so |x| * 2^(6-e) < 64
+        uint32_t lo[3] = {0u, 0u, 0u}, hi[3] = {0u, 0u, 0u};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float s = finite ? ldexpf(v[k], 6 - e) : 0.0f; // exact
+            const float f0 = rintf(s);
+            const float r1 = (s - f0) * 128.0f; // exact
+            const float f1 = rintf(r1);
+            const float f2 = rintf((r1 - f1) * 128.0f);
+            const uint32_t b[3] = {(uint32_t)(int)f0 & 0xffu, (uint32_t)(int)f1 & 0xffu, (uint32_t)(int)f2 & 0xffu};
+#pragma unroll
+            for (int l = 0; l < 3; ++l) {
+                if (k < 4) lo[l] |= b[l] << (8 * k);
+                else hi[l] |= b[l] << (8 * (k - 4));
+            }
+        }
+        uint8_t *dst = a.xa + (size_t)sb * kSbBytes + (size_t)(kh * 24 + t) * 8;
+#pragma unroll
+        for (int l = 0; l < 3; ++l) *reinterpret_cast<uint2 *>(dst + 64 * l) = make_uint2(lo[l], hi[l]);
+        if (kh == 0) a.xs[(size_t)sb * kMaxTok + t] = finite ? ldexpf(1.0f, e - 20) : __int_as_float(0x7fc00000);
+    }
+}
+
+struct MfmaArgs {
+    const uint8_t *w[2]; // one matrix, or the gate/up pair
+    int nmat;
+    size_t row_bytes;
+    int rows, cols, n_tok;
+    const uint8_t *xa;
+    const float *xs;
+    float *part; // [cols/kSlice][nmat][kMaxTok][rows]
+};
+
+// Q6_K codes of 8 columns (two dwords) minus 32, as int8: sub-block
+// (h, q, p) takes the nibble q>>1 of the ql bytes and bits 2q..2q+1 of the qh
+// bytes.  (c | 0x80) - 0x20 never borrows across bytes; ^ 0x80 restores the sign.
+__device__ __forceinline__ uint32_t code_m32(uint32_t ql, uint32_t qh, int q)
+{
+    uint32_t c;
+    switch (q) {
+    case 0: c = (ql & 0x0f0f0f0fu) | ((qh << 4) & 0x30303030u); break;
+    case 1: c = (ql & 0x0f0f0f0fu) | ((qh << 2) & 0x30303030u); break;
+    case 2: c = ((ql >> 4) & 0x0f0f0f0fu) | (qh & 0x30303030u); break;
+    default: c = ((ql >> 4) & 0x0f0f0f0fu) | ((qh >> 2) & 0x30303030u); break;
+    }
+    return ((c | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+}
+
+__global__ __launch_bounds__(EMU_WAVE * kWaves) void qmv_mfma_kernel(MfmaArgs a)
+{
+    const int nks = a.cols / kSlice, nrt = (a.rows + kTileRows - 1) / kTileRows;
+    int u = blockIdx.x;
+    const int ks = u % nks;
+    u /= nks;
+    const int rt = u % nrt, mat = u / nrt;
+    const int tid = threadIdx.x, lane = tid & (EMU_WAVE - 1), w = tid / EMU_WAVE;
+    const int j = lane & 31, kh = lane >> 5;
+    const int cb = ks * kWaves + w; // this wavefront's 256-column block
+    const int row = rt * kTileRows + j;
+    const int rl = row < a.rows ? row : a.rows - 1; // a valid row; never stored
+    const uint8_t *bp = a.w[mat] + (size_t)rl * a.row_bytes + (size_t)cb * 210;
+
+    // This lane's weight bytes: columns 8kh..8kh+7 of each of the block's 16
+    // sub-blocks (h, q, p) = 128h + 32q + 16p + ...
+    uint2 ql[2][2][2], qh[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            ql[h][0][p] = ld8(bp + 64 * h + 16 * p + 8 * kh);
+            ql[h][1][p] = ld8(bp + 64 * h + 32 + 16 * p + 8 * kh);
+            qh[h][p] = ld8(bp + 128 + 32 * h + 16 * p + 8 * kh);
+        }
+    const uint4 scv = ld16(bp + 192);
+    const float d = h2f(ld2(bp + 208));
+
+    // A operands: M row i = lane % 32 (limb i / 8, token i % 8).
+    const int i = j;
+    const bool live = i < 24 && (i & 7) < a.n_tok;
+    const uint8_t *ap = a.xa + (size_t)cb * 16 * kSbBytes + (size_t)(kh * 24 + (live ? i : 0)) * 8;
+    const float *sp = a.xs + (size_t)cb * 16 * kMaxTok + 4 * kh;
+
+    long av[16];
+#pragma unroll
+    for (int sb = 0; sb < 16; ++sb) av[sb] = live ? *reinterpret_cast<const long *>(ap + sb * kSbBytes) : 0;
+
+    // Sub-block sb = 8h + 2q + p: its codes, one MFMA, then the float step.
+    // Software-pipelined by hand (the next sub-block's MFMA goes out before
+    // this one's float step; scales are loaded two sub-blocks ahead) with a
+    // scheduling barrier per step, so only two accumulator tiles are live.
+    auto mma = [&](int sb) {
+        const int h = sb >> 3, q = (sb >> 1) & 3, p = sb & 1;
+        const uint2 lq = ql[h][q & 1][p], hq = qh[h][p];
+        const uint32_t c0 = code_m32(lq.x, hq.x, q), c1 = code_m32(lq.y, hq.y, q);
+        const long bv = (long)(((uint64_t)c1 << 32) | c0);
+        v16i D = {};
+        return __builtin_amdgcn_mfma_i32_32x32x16_i8(av[sb], bv, D, 0, 0, 0);
+    };
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto epi = [&](int sb, const v16i &D, const float4 &s4) {
+        const uint32_t sw = sb < 4 ? scv.x : sb < 8 ? scv.y : sb < 12 ? scv.z : scv.w;
+        const float scd = (float)(int)__builtin_amdgcn_sbfe(sw, 8u * (uint32_t)(sb & 3), 8u) * d;
+        const float s[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            // |t| < 2^30 by the limb bounds; unsigned arithmetic keeps the
+            // intermediate sums well defined.
+            const uint32_t t1 = ((uint32_t)D[r] << 7) + (uint32_t)D[r + 4];
+            const int t = (int)((t1 << 7) + (uint32_t)D[r + 8]);
+            acc[r] = __builtin_fmaf((float)t, scd * s[r], acc[r]);
+        }
+    };
+    auto sload = [&](int sb) { return *reinterpret_cast<const float4 *>(sp + sb * kMaxTok); };
+    float4 sv[16];
+    sv[0] = sload(0);
+    sv[1] = sload(1);
+    v16i cur = mma(0);
+#pragma unroll
+    for (int sb = 0; sb < 16; ++sb) {
+        if (sb + 2 < 16) sv[sb + 2] = sload(sb + 2);
+        v16i next;
+        if (sb + 1 < 16) next = mma(sb + 1);
+        epi(sb, cur, sv[sb]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (sb + 1 < 16) cur = next;
+    }
+
+    __shared__ float red[kWaves][kMaxTok][kTileRows];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[w][4 * kh + r][j] = acc[r];
+    __syncthreads();
+    if (tid < kMaxTok * kTileRows) {
+        const int t = tid / kTileRows, jj = tid % kTileRows, orow = rt * kTileRows + jj;
+        if (t < a.n_tok && orow < a.rows) {
+            float v = red[0][t][jj];
+#pragma unroll
+            for (int k = 1; k < kWaves; ++k) v += red[k][t][jj];
+            a.part[(((size_t)ks * a.nmat + mat) * kMaxTok + t) * a.rows + orow] = v;
+        }
+    }
+}
+
+struct FinishArgs {
+    const float *part;
+    int nks, nmat, rows;
+    float *y; // n_tok x rows
+    int accumulate;
+    uint64_t *keys;
+    int key_stride, tie_last;
+};
+
+__global__ __launch_bounds__(kFinishThreads) void mfma_finish_kernel(FinishArgs a)
+{
+    const int t = blockIdx.y, row = blockIdx.x * kFinishThreads + threadIdx.x;
+    const bool ok = row < a.rows;
+    float v = 0.0f;
+    if (ok) {
+        const size_t stride = (size_t)a.nmat * kMaxTok * a.rows;
+        const float *p = a.part + (size_t)t * a.rows + row;
+        v = p[0];
+        for (int k = 1; k < a.nks; ++k) v += p[k * stride];
+        if (a.nmat == 2) {
+            const float *pu = p + (size_t)kMaxTok * a.rows;
+            float up = pu[0];
+            for (int k = 1; k < a.nks; ++k) up += pu[k * stride];
+            v = (v / (1.0f + expf(-v))) * up;
+        }
+        float *dst = a.y + (size_t)t * a.rows + row;
+        *dst = a.accumulate ? *dst + v : v;
+    }
+    if (a.keys) {
+        __shared__ uint64_t best[kFinishThreads / EMU_WAVE];
+        uint64_t k = ok ? emu_select_key(v, (uint32_t)row, a.tie_last) : 0;
+#pragma unroll
+        for (int o = EMU_WAVE / 2; o >= 1; o >>= 1) {
+            const uint64_t other = __shfl_xor(k, o, EMU_WAVE);
+            k = other > k ? other : k;
+        }
+        if ((threadIdx.x & (EMU_WAVE - 1)) == 0) best[threadIdx.x / EMU_WAVE] = k;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint64_t m = best[0];
+#pragma unroll
+            for (int w = 1; w < kFinishThreads / EMU_WAVE; ++w) m = best[w] > m ? best[w] : m;
+            a.keys[(size_t)t * a.key_stride + blockIdx.x] = m;
+        }
+    }
+}
+
+bool mfma_disabled()
+{
+    static const bool off = [] {
+        const char *v = getenv("EMU_QMV_MFMA");
+        return v && v[0] == '0';
+    }();
+    return off;
+}
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+} // namespace
+
+size_t emu_mfma_workspace_bytes(int rows, int cols, int nmat)
+{
+    const size_t nsb = (size_t)cols / 16, nks = (size_t)cols / kSlice;
+    return align256(nsb * kSbBytes) + align256(nsb * kMaxTok * sizeof(float)) +
+           align256(nks * nmat * kMaxTok * (size_t)rows * sizeof(float));
+}
+
+int emu_mfma_reserve(emu_ctx *ctx, size_t bytes)
+{
+    if (bytes <= ctx->mfma_ws_bytes) return EMU_OK;
+    if (ctx->mfma_ws) {
+        EMU_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        EMU_HIP(ctx, hipFree(ctx->mfma_ws));
+        ctx->mfma_ws = nullptr;
+        ctx->mfma_ws_bytes = 0;
+    }
+    EMU_HIP(ctx, hipMalloc(&ctx->mfma_ws, bytes));
+    ctx->mfma_ws_bytes = bytes;
+    return EMU_OK;
+}
+
+bool emu_mfma_supports(int encoding, int cols, int n_tok)
+{
+    if (mfma_disabled()) return false;
+    return encoding == EMU_ENC_Q6_K && n_tok >= 2 && n_tok <= kMaxTok && cols > 0 && cols % kSlice == 0;
+}
+
+int emu_launch_mfma(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int *key_slots)
+{
+    if (!emu_mfma_supports(encoding, a.cols, n_tok)) return EMU_E_UNSUPPORTED;
+    if (a.rows <= 0) return EMU_E_ARG;
+    const int nmat = a.w_up ? 2 : 1;
+    if (nmat == 2 && a.accumulate) return EMU_E_ARG; // the fused entry point never asks for this
+    const int nks = a.cols / kSlice, nrt = (a.rows + kTileRows - 1) / kTileRows;
+    const int gx = (a.rows + kFinishThreads - 1) / kFinishThreads;
+    if (a.keys && gx > a.key_stride) return EMU_E_CONFIG;
+    int st = emu_mfma_reserve(ctx, emu_mfma_workspace_bytes(a.rows, a.cols, nmat));
+    if (st != EMU_OK) return st;
+    const size_t nsb = (size_t)a.cols / 16;
+    uint8_t *ws = static_cast<uint8_t *>(ctx->mfma_ws);
+    uint8_t *xa = ws;
+    float *xs = reinterpret_cast<float *>(ws + align256(nsb * kSbBytes));
+    float *part = reinterpret_cast<float *>(ws + align256(nsb * kSbBytes) + align256(nsb * kMaxTok * sizeof(float)));
+
+    PrepArgs pa{};
+    pa.x = a.x;
+    pa.gain = a.gain;
+    pa.eps = a.eps;
+    pa.cols = a.cols;
+    pa.n_tok = n_tok;
+    pa.xa = xa;
+    pa.xs = xs;
+    hipLaunchKernelGGL(mfma_prep_kernel, dim3(n_tok), dim3(kPrepThreads), 0, ctx->stream, pa);
+    EMU_LAUNCH_CHECK(ctx);
+
+    MfmaArgs ma{};
+    ma.w[0] = a.w;
+    ma.w[1] = a.w_up;
+    ma.nmat = nmat;
+    ma.row_bytes = a.row_bytes;
+    ma.rows = a.rows;
+    ma.cols = a.cols;
+    ma.n_tok = n_tok;
+    ma.xa = xa;
+    ma.xs = xs;
+    ma.part = part;
+    hipLaunchKernelGGL(qmv_mfma_kernel, dim3((unsigned)(nks * nrt * nmat)), dim3(EMU_WAVE * kWaves), 0,
+                       ctx->stream, ma);
+    EMU_LAUNCH_CHECK(ctx);
+
+    FinishArgs fa{};
+    fa.part = part;
+    fa.nks = nks;
+    fa.nmat = nmat;
+    fa.rows = a.rows;
+    fa.y = a.y;
+    fa.accumulate = a.accumulate;
+    fa.keys = a.keys;
+    fa.key_stride = a.key_stride;
+    fa.tie_last = a.tie_last;
+    hipLaunchKernelGGL(mfma_finish_kernel, dim3((unsigned)gx, (unsigned)n_tok), dim3(kFinishThreads), 0,
+                       ctx->stream, fa);
+    EMU_LAUNCH_CHECK(ctx);
+    if (key_slots) *key_slots = gx;
+    return EMU_OK;
+}

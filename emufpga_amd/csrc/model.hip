@@ -683,6 +683,22 @@ extern "C" int emu_session_create(emu_model *m, uint32_t n_clients, uint32_t con
         st = emu_memcpy_htod(ctx, s->rope, table.data(), table.size() * sizeof(float));
     }
     if (st == EMU_OK) st = emu_memset(ctx, s->counters, 0, sizeof(uint32_t) * n_clients * c.kv_heads);
+    if (st == EMU_OK) {
+        // The multi-token matvec's workspace must exist before the step is
+        // captured into a graph: size it for every matvec of the step.
+        const int shapes[5][3] = {{(int)(QW + 2 * KW), (int)c.hidden, 1},
+                                  {(int)c.hidden, (int)QW, 1},
+                                  {(int)c.ffn, (int)c.hidden, 2},
+                                  {(int)c.hidden, (int)c.ffn, 1},
+                                  {(int)c.vocab, (int)c.hidden, 1}};
+        size_t ws = 0;
+        for (const auto &sh : shapes)
+            if (emu_mfma_supports(c.encoding, sh[1], (int)n_clients)) {
+                const size_t b = emu_mfma_workspace_bytes(sh[0], sh[1], sh[2]);
+                ws = b > ws ? b : ws;
+            }
+        if (ws) st = emu_mfma_reserve(ctx, ws);
+    }
     if (st == EMU_OK) st = emu_session_reset(s);
     if (st != EMU_OK) {
         emu_session_destroy(s);

@@ -617,6 +617,8 @@ int emu_launch_qmv(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int 
     if (a.rows == 0 || n_tok == 0) return EMU_OK;
     if (n_tok == 1 && emu_limb_supports(encoding, a.cols) && !(a.w_up && a.accumulate))
         return emu_launch_limb(ctx, encoding, a, key_slots);
+    if (emu_mfma_supports(encoding, a.cols, n_tok) && !(a.w_up && a.accumulate))
+        return emu_launch_mfma(ctx, encoding, a, n_tok, key_slots);
     switch (encoding) {
     case EMU_ENC_Q6_K: return launch_fmt<FmtQ6K>(ctx, a, n_tok, key_slots);
     case EMU_ENC_Q8_0: return launch_fmt<FmtQ8_0>(ctx, a, n_tok, key_slots);
