@@ -368,6 +368,28 @@ bool emu_mfma_supports(int encoding, int cols, int n_tok);
 size_t emu_mfma_workspace_bytes(int rows, int cols, int nmat);
 int emu_mfma_reserve(emu_ctx *ctx, size_t bytes);
 int emu_launch_mfma(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int *key_slots);
+// The chained form used by the decode step: link (the producing matvec's
+// partial sums -> its epilogue -> the next matvec's A operands), matvec
+// (A operands -> partial sums), ... with one workspace sized for operands of
+// up to cols_cap columns plus the largest partial-sum set
+// (emu_mfma_chain_bytes).  Modes of the link: 0 input x, 1 residual add into
+// h, 2 SwiGLU of a gate/up pair, 3 plain sums written to h.
+struct EmuMfmaLink {
+    int mode;
+    bool from_part; // the partial sums of the last matvec (modes 1-3)
+    int part_nks, part_nmat;
+    float *h;
+    const float *x;
+    int cols, cols_cap, n_tok;
+    const float *gain;
+    float eps;
+    bool limbs; // write the next matvec's A operands
+};
+size_t emu_mfma_chain_bytes(int cols_cap, size_t max_part_bytes);
+size_t emu_mfma_part_bytes(int rows, int cols, int nmat);
+int emu_mfma_link(emu_ctx *ctx, const EmuMfmaLink &l);
+int emu_mfma_matvec(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int *part_nks);
+int emu_mfma_finish(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int *key_slots);
 
 // Fused decode attention of one layer for every client (attn.hip).
 struct EmuAttnLaunch {

@@ -24,10 +24,14 @@
 // applies the epilogue (residual accumulate, SwiGLU of a gate/up pair, greedy
 // selection keys).  Everything is deterministic.
 //
-// Three kernels:
-//   mfma_prep_kernel   x (optionally RMS-normalised) -> A operands + scales
+// Kernels:
+//   mfma_link_kernel   the producing matvec's partial sums (or a given x) ->
+//                      its epilogue (residual add, SwiGLU) -> optional RMS
+//                      norm -> the next matvec's A operands and scales
 //   qmv_mfma_kernel    A operands x weight codes -> per-slice partial sums
-//   mfma_finish_kernel partial sums -> y
+//   mfma_finish_kernel partial sums -> y (residual accumulate, SwiGLU, keys)
+// A decode step chains them as link, matvec, link, matvec, ... so each
+// matvec costs one small kernel besides its own.
 #include "internal.hpp"
 
 #include <math.h>
@@ -37,79 +41,140 @@ namespace {
 
 typedef int v16i __attribute__((ext_vector_type(16)));
 
+__device__ __forceinline__ void ld8f(const float *p, float (&v)[8])
+{
+    const float4 a = *reinterpret_cast<const float4 *>(p);
+    const float4 b = *reinterpret_cast<const float4 *>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
 constexpr int kMaxTok = 8;          // tokens per tile (A rows 8 * limb + token)
 constexpr int kTileRows = 32;       // weight rows per tile (MFMA N)
 constexpr int kWaves = 8;           // wavefronts per workgroup, one 256-column block each
 constexpr int kSlice = kWaves * 256; // columns per workgroup
 constexpr int kSbBytes = 2 * 24 * 8; // A-operand bytes per 16-column sub-block
-constexpr int kPrepThreads = 256;
 constexpr int kFinishThreads = 256;
 
-struct PrepArgs {
-    const float *x; // n_tok x cols
-    const float *gain;
-    float eps;
+// One token's activation vector, finished from the producing matvec's
+// partial sums (or taken as given) and turned into the next matvec's A
+// operands.  Modes: the producing matvec's epilogue.
+enum LinkMode { kLinkInput = 0, kLinkResid = 1, kLinkSwiglu = 2, kLinkPlain = 3 };
+
+struct LinkArgs {
+    const float *part; // [nks][nmat][kMaxTok][cols] partial sums, or null (kLinkInput)
+    int nks, nmat, mode;
+    float *h;       // kLinkResid: residual stream, updated in place; kLinkPlain: output
+    const float *x; // kLinkInput: the activations
     int cols, n_tok;
-    uint8_t *xa; // cols/16 x kSbBytes
-    float *xs;   // cols/16 x kMaxTok
+    const float *gain; // RMS gain of the next matvec's input, or null
+    float eps;
+    uint8_t *xa; // A operands (null: none wanted)
+    float *xs;
 };
 
 // A-operand layout: sub-block sb, half kh (columns 8kh..8kh+7 of the
 // sub-block), limb, token -> 8 bytes at xa + sb*kSbBytes + (kh*24 + 8*limb + token)*8.
-__global__ __launch_bounds__(kPrepThreads) void mfma_prep_kernel(PrepArgs a)
+// Thread pair (2m, 2m+1) holds the two 8-column halves of one sub-block;
+// a thread owns up to kLinkPairs such 8-column pieces.
+constexpr int kLinkThreads = 512;
+constexpr int kLinkPairs = 3; // columns per token up to 8 * kLinkThreads * kLinkPairs = 12288
+
+__global__ __launch_bounds__(kLinkThreads) void mfma_link_kernel(LinkArgs a)
 {
     const int t = blockIdx.x, tid = threadIdx.x;
-    const float *x = a.x + (size_t)t * a.cols;
-    __shared__ float red[kPrepThreads / EMU_WAVE];
+    const int npairs = a.cols / 8;
+    float v[kLinkPairs][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kLinkPairs; ++k) {
+        const int p = tid + k * kLinkThreads;
+        if (p >= npairs) break;
+        const int c0 = 8 * p;
+        if (a.mode == kLinkInput) {
+            ld8f(a.x + (size_t)t * a.cols + c0, v[k]);
+        } else {
+            // Slices added in slice order (the finishing pass's order).
+            const size_t stride = (size_t)a.nmat * kMaxTok * a.cols;
+            const float *pp = a.part + (size_t)t * a.cols + c0;
+            ld8f(pp, v[k]);
+            for (int ks = 1; ks < a.nks; ++ks) {
+                float q[8];
+                ld8f(pp + ks * stride, q);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[k][e] += q[e];
+            }
+            if (a.mode == kLinkSwiglu) {
+                const float *pu = pp + (size_t)kMaxTok * a.cols;
+                float u[8];
+                ld8f(pu, u);
+                for (int ks = 1; ks < a.nks; ++ks) {
+                    float q[8];
+                    ld8f(pu + ks * stride, q);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) u[e] += q[e];
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[k][e] = (v[k][e] / (1.0f + expf(-v[k][e]))) * u[e];
+            }
+            if (a.mode == kLinkResid || a.mode == kLinkPlain) {
+                float *hp = a.h + (size_t)t * a.cols + c0;
+                if (a.mode == kLinkResid) {
+                    float hv[8];
+                    ld8f(hp, hv);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[k][e] = hv[e] + v[k][e];
+                }
+                *reinterpret_cast<float4 *>(hp) = make_float4(v[k][0], v[k][1], v[k][2], v[k][3]);
+                *reinterpret_cast<float4 *>(hp + 4) = make_float4(v[k][4], v[k][5], v[k][6], v[k][7]);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(v[k][e], v[k][e], ss);
+    }
+    if (!a.xa) return; // uniform
     float scale = 1.0f;
     if (a.gain) {
-        float ss = 0.0f;
-        for (int c = 4 * tid; c < a.cols; c += 4 * kPrepThreads) {
-            const float4 v = *reinterpret_cast<const float4 *>(x + c);
-            ss = __builtin_fmaf(v.x, v.x, ss);
-            ss = __builtin_fmaf(v.y, v.y, ss);
-            ss = __builtin_fmaf(v.z, v.z, ss);
-            ss = __builtin_fmaf(v.w, v.w, ss);
-        }
+        __shared__ float red[kLinkThreads / EMU_WAVE];
         ss = wave_sum(ss);
         if ((tid & (EMU_WAVE - 1)) == 0) red[tid / EMU_WAVE] = ss;
         __syncthreads();
         float tot = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kPrepThreads / EMU_WAVE; ++k) tot += red[k];
+        for (int k = 0; k < kLinkThreads / EMU_WAVE; ++k) tot += red[k];
         scale = 1.0f / sqrtf(tot / (float)a.cols + a.eps);
     }
-    // Thread pair (2m, 2m+1) holds the two 8-column halves of one sub-block.
-    for (int p = tid; p < a.cols / 8; p += kPrepThreads) {
-        const int sb = p >> 1, kh = p & 1, c0 = 8 * p;
-        float v[8];
-        const float4 x0 = *reinterpret_cast<const float4 *>(x + c0);
-        const float4 x1 = *reinterpret_cast<const float4 *>(x + c0 + 4);
-        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
-        v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
-        if (a.gain) {
-            const float4 g0 = *reinterpret_cast<const float4 *>(a.gain + c0);
-            const float4 g1 = *reinterpret_cast<const float4 *>(a.gain + c0 + 4);
-            const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = __fmul_rn(__fmul_rn(v[k], scale), g[k]);
+    for (int k = 0; k < kLinkPairs; ++k) {
+        const int p = tid + k * kLinkThreads;
+        if (p >= npairs) break; // pairs (2m, 2m+1) stop together: npairs is even
+        const int sb = p >> 1, kh = p & 1, c0 = 8 * p;
+        float w[8];
+        if (a.gain) {
+            float g[8];
+            ld8f(a.gain + c0, g);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) w[e] = __fmul_rn(__fmul_rn(v[k][e], scale), g[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) w[e] = v[k][e];
         }
         float amax = 0.0f;
         int bad = 0; // an inf or NaN (fmaxf alone would drop a NaN)
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            amax = fmaxf(amax, fabsf(v[k]));
-            bad |= !(fabsf(v[k]) <= 3.402823466e38f);
+        for (int e = 0; e < 8; ++e) {
+            amax = fmaxf(amax, fabsf(w[e]));
+            bad |= !(fabsf(w[e]) <= 3.402823466e38f);
         }
         amax = fmaxf(amax, __shfl_xor(amax, 1, EMU_WAVE));
         bad |= __shfl_xor(bad, 1, EMU_WAVE);
         const bool finite = !bad;
-        int e = 0;
-        (void)frexpf(finite ? amax : 0.0f, &e); // amax < 2^e, so |x| * 2^(6-e) < 64
+        int e2 = 0;
+        (void)frexpf(finite ? amax : 0.0f, &e2); // amax < 2^e2, so |x| * 2^(6-e2) < 64
         uint32_t lo[3] = {0u, 0u, 0u}, hi[3] = {0u, 0u, 0u};
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const float s = finite ? ldexpf(v[k], 6 - e) : 0.0f; // exact
+        for (int e = 0; e < 8; ++e) {
+            const float s = finite ? ldexpf(w[e], 6 - e2) : 0.0f; // exact
             const float f0 = rintf(s);
             const float r1 = (s - f0) * 128.0f; // exact
             const float f1 = rintf(r1);
@@ -117,14 +182,14 @@ __global__ __launch_bounds__(kPrepThreads) void mfma_prep_kernel(PrepArgs a)
             const uint32_t b[3] = {(uint32_t)(int)f0 & 0xffu, (uint32_t)(int)f1 & 0xffu, (uint32_t)(int)f2 & 0xffu};
 #pragma unroll
             for (int l = 0; l < 3; ++l) {
-                if (k < 4) lo[l] |= b[l] << (8 * k);
-                else hi[l] |= b[l] << (8 * (k - 4));
+                if (e < 4) lo[l] |= b[l] << (8 * e);
+                else hi[l] |= b[l] << (8 * (e - 4));
             }
         }
         uint8_t *dst = a.xa + (size_t)sb * kSbBytes + (size_t)(kh * 24 + t) * 8;
 #pragma unroll
         for (int l = 0; l < 3; ++l) *reinterpret_cast<uint2 *>(dst + 64 * l) = make_uint2(lo[l], hi[l]);
-        if (kh == 0) a.xs[(size_t)sb * kMaxTok + t] = finite ? ldexpf(1.0f, e - 20) : __int_as_float(0x7fc00000);
+        if (kh == 0) a.xs[(size_t)sb * kMaxTok + t] = finite ? ldexpf(1.0f, e2 - 20) : __int_as_float(0x7fc00000);
     }
 }
 
@@ -305,14 +370,47 @@ bool mfma_disabled()
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
+// Workspace: A operands and scales for up to cols_cap columns, then the
+// partial sums.
+struct Ws {
+    uint8_t *xa;
+    float *xs, *part;
+    size_t part_bytes;
+};
+size_t operand_bytes(int cols_cap)
+{
+    const size_t nsb = (size_t)cols_cap / 16;
+    return align256(nsb * kSbBytes) + align256(nsb * kMaxTok * sizeof(float));
+}
+Ws workspace(emu_ctx *ctx, int cols_cap)
+{
+    const size_t nsb = (size_t)cols_cap / 16;
+    uint8_t *base = static_cast<uint8_t *>(ctx->mfma_ws);
+    Ws w;
+    w.xa = base;
+    w.xs = reinterpret_cast<float *>(base + align256(nsb * kSbBytes));
+    w.part = reinterpret_cast<float *>(base + operand_bytes(cols_cap));
+    w.part_bytes = ctx->mfma_ws_bytes > operand_bytes(cols_cap) ? ctx->mfma_ws_bytes - operand_bytes(cols_cap) : 0;
+    return w;
+}
+size_t part_bytes(int rows, int cols, int nmat)
+{
+    return (size_t)(cols / kSlice) * nmat * kMaxTok * (size_t)rows * sizeof(float);
+}
+
 } // namespace
 
 size_t emu_mfma_workspace_bytes(int rows, int cols, int nmat)
 {
-    const size_t nsb = (size_t)cols / 16, nks = (size_t)cols / kSlice;
-    return align256(nsb * kSbBytes) + align256(nsb * kMaxTok * sizeof(float)) +
-           align256(nks * nmat * kMaxTok * (size_t)rows * sizeof(float));
+    return operand_bytes(cols) + align256(part_bytes(rows, cols, nmat));
 }
+
+size_t emu_mfma_chain_bytes(int cols_cap, size_t max_part_bytes)
+{
+    return operand_bytes(cols_cap) + align256(max_part_bytes);
+}
+
+size_t emu_mfma_part_bytes(int rows, int cols, int nmat) { return part_bytes(rows, cols, nmat); }
 
 int emu_mfma_reserve(emu_ctx *ctx, size_t bytes)
 {
@@ -331,7 +429,83 @@ int emu_mfma_reserve(emu_ctx *ctx, size_t bytes)
 bool emu_mfma_supports(int encoding, int cols, int n_tok)
 {
     if (mfma_disabled()) return false;
-    return encoding == EMU_ENC_Q6_K && n_tok >= 2 && n_tok <= kMaxTok && cols > 0 && cols % kSlice == 0;
+    return encoding == EMU_ENC_Q6_K && n_tok >= 2 && n_tok <= kMaxTok && cols > 0 && cols % kSlice == 0 &&
+           cols <= 8 * kLinkThreads * kLinkPairs;
+}
+
+int emu_mfma_link(emu_ctx *ctx, const EmuMfmaLink &l)
+{
+    if (l.n_tok < 1 || l.n_tok > kMaxTok || l.cols <= 0 || l.cols % 16 != 0 || l.cols > l.cols_cap ||
+        l.cols > 8 * kLinkThreads * kLinkPairs)
+        return EMU_E_CONFIG;
+    const Ws w = workspace(ctx, l.cols_cap);
+    if (!ctx->mfma_ws || (l.limbs && ctx->mfma_ws_bytes < operand_bytes(l.cols_cap))) return EMU_E_CONFIG;
+    LinkArgs a{};
+    a.part = l.from_part ? w.part : nullptr;
+    a.nks = l.from_part ? l.part_nks : 0;
+    a.nmat = l.part_nmat;
+    a.mode = l.mode;
+    a.h = l.h;
+    a.x = l.x;
+    a.cols = l.cols;
+    a.n_tok = l.n_tok;
+    a.gain = l.gain;
+    a.eps = l.eps;
+    a.xa = l.limbs ? w.xa : nullptr;
+    a.xs = l.limbs ? w.xs : nullptr;
+    if (l.from_part && (size_t)a.nks * a.nmat * kMaxTok * (size_t)l.cols * sizeof(float) > w.part_bytes)
+        return EMU_E_CONFIG;
+    hipLaunchKernelGGL(mfma_link_kernel, dim3(l.n_tok), dim3(kLinkThreads), 0, ctx->stream, a);
+    EMU_LAUNCH_CHECK(ctx);
+    return EMU_OK;
+}
+
+int emu_mfma_matvec(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int *part_nks)
+{
+    if (!emu_mfma_supports(EMU_ENC_Q6_K, q.cols, n_tok) || q.cols > cols_cap || q.rows <= 0) return EMU_E_CONFIG;
+    const int nmat = q.w_up ? 2 : 1;
+    const Ws w = workspace(ctx, cols_cap);
+    if (!ctx->mfma_ws || part_bytes(q.rows, q.cols, nmat) > w.part_bytes) return EMU_E_CONFIG;
+    MfmaArgs ma{};
+    ma.w[0] = q.w;
+    ma.w[1] = q.w_up;
+    ma.nmat = nmat;
+    ma.row_bytes = q.row_bytes;
+    ma.rows = q.rows;
+    ma.cols = q.cols;
+    ma.n_tok = n_tok;
+    ma.xa = w.xa;
+    ma.xs = w.xs;
+    ma.part = w.part;
+    const int nks = q.cols / kSlice, nrt = (q.rows + kTileRows - 1) / kTileRows;
+    hipLaunchKernelGGL(qmv_mfma_kernel, dim3((unsigned)(nks * nrt * nmat)), dim3(EMU_WAVE * kWaves), 0,
+                       ctx->stream, ma);
+    EMU_LAUNCH_CHECK(ctx);
+    if (part_nks) *part_nks = nks;
+    return EMU_OK;
+}
+
+int emu_mfma_finish(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int *key_slots)
+{
+    const int nmat = q.w_up ? 2 : 1;
+    const int gx = (q.rows + kFinishThreads - 1) / kFinishThreads;
+    if (q.keys && gx > q.key_stride) return EMU_E_CONFIG;
+    const Ws w = workspace(ctx, cols_cap);
+    FinishArgs fa{};
+    fa.part = w.part;
+    fa.nks = q.cols / kSlice;
+    fa.nmat = nmat;
+    fa.rows = q.rows;
+    fa.y = q.y;
+    fa.accumulate = q.accumulate;
+    fa.keys = q.keys;
+    fa.key_stride = q.key_stride;
+    fa.tie_last = q.tie_last;
+    hipLaunchKernelGGL(mfma_finish_kernel, dim3((unsigned)gx, (unsigned)n_tok), dim3(kFinishThreads), 0,
+                       ctx->stream, fa);
+    EMU_LAUNCH_CHECK(ctx);
+    if (key_slots) *key_slots = gx;
+    return EMU_OK;
 }
 
 int emu_launch_mfma(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int *key_slots)
@@ -340,56 +514,20 @@ int emu_launch_mfma(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int
     if (a.rows <= 0) return EMU_E_ARG;
     const int nmat = a.w_up ? 2 : 1;
     if (nmat == 2 && a.accumulate) return EMU_E_ARG; // the fused entry point never asks for this
-    const int nks = a.cols / kSlice, nrt = (a.rows + kTileRows - 1) / kTileRows;
     const int gx = (a.rows + kFinishThreads - 1) / kFinishThreads;
     if (a.keys && gx > a.key_stride) return EMU_E_CONFIG;
     int st = emu_mfma_reserve(ctx, emu_mfma_workspace_bytes(a.rows, a.cols, nmat));
     if (st != EMU_OK) return st;
-    const size_t nsb = (size_t)a.cols / 16;
-    uint8_t *ws = static_cast<uint8_t *>(ctx->mfma_ws);
-    uint8_t *xa = ws;
-    float *xs = reinterpret_cast<float *>(ws + align256(nsb * kSbBytes));
-    float *part = reinterpret_cast<float *>(ws + align256(nsb * kSbBytes) + align256(nsb * kMaxTok * sizeof(float)));
-
-    PrepArgs pa{};
-    pa.x = a.x;
-    pa.gain = a.gain;
-    pa.eps = a.eps;
-    pa.cols = a.cols;
-    pa.n_tok = n_tok;
-    pa.xa = xa;
-    pa.xs = xs;
-    hipLaunchKernelGGL(mfma_prep_kernel, dim3(n_tok), dim3(kPrepThreads), 0, ctx->stream, pa);
-    EMU_LAUNCH_CHECK(ctx);
-
-    MfmaArgs ma{};
-    ma.w[0] = a.w;
-    ma.w[1] = a.w_up;
-    ma.nmat = nmat;
-    ma.row_bytes = a.row_bytes;
-    ma.rows = a.rows;
-    ma.cols = a.cols;
-    ma.n_tok = n_tok;
-    ma.xa = xa;
-    ma.xs = xs;
-    ma.part = part;
-    hipLaunchKernelGGL(qmv_mfma_kernel, dim3((unsigned)(nks * nrt * nmat)), dim3(EMU_WAVE * kWaves), 0,
-                       ctx->stream, ma);
-    EMU_LAUNCH_CHECK(ctx);
-
-    FinishArgs fa{};
-    fa.part = part;
-    fa.nks = nks;
-    fa.nmat = nmat;
-    fa.rows = a.rows;
-    fa.y = a.y;
-    fa.accumulate = a.accumulate;
-    fa.keys = a.keys;
-    fa.key_stride = a.key_stride;
-    fa.tie_last = a.tie_last;
-    hipLaunchKernelGGL(mfma_finish_kernel, dim3((unsigned)gx, (unsigned)n_tok), dim3(kFinishThreads), 0,
-                       ctx->stream, fa);
-    EMU_LAUNCH_CHECK(ctx);
-    if (key_slots) *key_slots = gx;
-    return EMU_OK;
+    EmuMfmaLink l{};
+    l.mode = kLinkInput;
+    l.x = a.x;
+    l.cols = a.cols;
+    l.cols_cap = a.cols;
+    l.n_tok = n_tok;
+    l.gain = a.gain;
+    l.eps = a.eps;
+    l.limbs = true;
+    if ((st = emu_mfma_link(ctx, l)) != EMU_OK) return st;
+    if ((st = emu_mfma_matvec(ctx, a, n_tok, a.cols, nullptr)) != EMU_OK) return st;
+    return emu_mfma_finish(ctx, a, n_tok, a.cols, key_slots);
 }

@@ -20,6 +20,8 @@
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
+
+#include <algorithm>
 #include <vector>
 
 int emu_build_rope_table(uint32_t positions, uint32_t head_dim, float theta, int fma_form,
@@ -324,6 +326,154 @@ int launch_embed(emu_ctx *ctx, const emu_model *m, const uint32_t *tokens, float
     return EMU_OK;
 }
 
+EmuAttnLaunch layer_attn(emu_session *s, uint32_t layer)
+{
+    const emu_model *m = s->m;
+    const emu_model_config &c = m->cfg;
+    const uint32_t hd = c.head_dim;
+    const int smol = c.style == EMU_STYLE_SMOL;
+    EmuAttnLaunch al{};
+    al.qkv = s->qkv;
+    al.k_cache = s->k_cache;
+    al.v_cache = s->v_cache;
+    al.positions = s->positions;
+    al.rope = s->rope;
+    al.q_norm = c.qk_norm ? reinterpret_cast<const float *>(m->base + m->off_q_norm) : nullptr;
+    al.k_norm = c.qk_norm ? reinterpret_cast<const float *>(m->base + m->off_k_norm) : nullptr;
+    al.eps = c.eps;
+    al.score_mul = smol ? 1.0f / sqrtf((float)hd) : 0.0f;
+    al.score_div = smol ? 0.0f : sqrtf((float)hd);
+    al.rope_fma = smol;
+    al.interleaved = 0;
+    al.heads = (int)c.heads;
+    al.kv_heads = (int)c.kv_heads;
+    al.head_dim = (int)hd;
+    al.layers = (int)c.layers;
+    al.layer = (int)layer;
+    al.context = (int)s->context;
+    al.clients = (int)s->n;
+    al.kv_f16 = s->kv_f16;
+    al.partial = s->partial;
+    al.counters = s->counters;
+    al.out = s->attn;
+    return al;
+}
+
+int launch_finalize(emu_session *s, int slots)
+{
+    emu_ctx *ctx = s->m->ctx;
+    const int smol = s->m->cfg.style == EMU_STYLE_SMOL;
+    if (slots <= 0 || slots > (int)s->key_stride) return EMU_E_CONFIG;
+    hipLaunchKernelGGL(finalize_kernel, dim3(s->n), dim3(1024), 0, ctx->stream, s->keys, (int)s->key_stride, slots,
+                       smol ? 1 : 0, s->prompt, (int)s->context, s->hist, s->ctrl, s->tokens, s->positions,
+                       s->steps, s->last);
+    EMU_LAUNCH_CHECK(ctx);
+    return EMU_OK;
+}
+
+// Whether the step's matvecs take the chained multi-token form (mfma.hip):
+// several clients, Q6_K, and every matvec's columns a multiple of its slice.
+bool mfma_chain(const emu_model *m, uint32_t n)
+{
+    const emu_model_config &c = m->cfg;
+    const int QW = (int)(c.heads * c.head_dim), KW = (int)(c.kv_heads * c.head_dim);
+    return n >= 2 && emu_mfma_supports(c.encoding, (int)c.hidden, (int)n) &&
+           emu_mfma_supports(c.encoding, QW, (int)n) && emu_mfma_supports(c.encoding, (int)c.ffn, (int)n) &&
+           (QW + 2 * KW) % 16 == 0 && (QW + 2 * KW) <= (int)c.ffn;
+}
+
+// Workspace of the chained form: operands of up to the widest input, and the
+// largest matvec's partial sums.
+size_t mfma_chain_bytes(const emu_model *m)
+{
+    const emu_model_config &c = m->cfg;
+    const int H = (int)c.hidden, QW = (int)(c.heads * c.head_dim), KW = (int)(c.kv_heads * c.head_dim),
+              F = (int)c.ffn;
+    const int cap = std::max(H, std::max(QW, F));
+    size_t part = emu_mfma_part_bytes(QW + 2 * KW, H, 1);
+    part = std::max(part, emu_mfma_part_bytes(H, QW, 1));
+    part = std::max(part, emu_mfma_part_bytes(F, H, 2));
+    part = std::max(part, emu_mfma_part_bytes(H, F, 1));
+    part = std::max(part, emu_mfma_part_bytes((int)c.vocab, H, 1));
+    return emu_mfma_chain_bytes(cap, part);
+}
+
+// The layers, output matvec and selection of a multi-token step, chained:
+// each link kernel finishes the previous matvec (residual add / SwiGLU /
+// q|k|v sums) and prepares the next one's operands, RMS norm included.
+int run_chain(emu_session *s)
+{
+    emu_model *m = s->m;
+    emu_ctx *ctx = m->ctx;
+    const emu_model_config &c = m->cfg;
+    const int H = (int)c.hidden, QW = (int)(c.heads * c.head_dim), KW = (int)(c.kv_heads * c.head_dim),
+              F = (int)c.ffn;
+    const int n = (int)s->n, cap = std::max(H, std::max(QW, F));
+    uint32_t be = 0, bb = 0;
+    emu_block_layout(c.encoding, &be, &bb);
+    const float *attn_norm = reinterpret_cast<const float *>(m->base + m->off_attn_norm);
+    const float *ffn_norm = reinterpret_cast<const float *>(m->base + m->off_ffn_norm);
+    const float *out_norm = reinterpret_cast<const float *>(m->base + m->off_out_norm);
+    int st = EMU_OK;
+    auto link = [&](int mode, int nks, int nmat, float *h, const float *x, int cols, const float *gain, bool limbs) {
+        EmuMfmaLink l{};
+        l.mode = mode;
+        l.from_part = mode != 0;
+        l.part_nks = nks;
+        l.part_nmat = nmat;
+        l.h = h;
+        l.x = x;
+        l.cols = cols;
+        l.cols_cap = cap;
+        l.n_tok = n;
+        l.gain = gain;
+        l.eps = c.eps;
+        l.limbs = limbs;
+        return emu_mfma_link(ctx, l);
+    };
+    auto matvec = [&](const uint8_t *w, const uint8_t *w_up, size_t rb, int rows, int cols, int *nks) {
+        QmvArgs q{};
+        q.w = w;
+        q.w_up = w_up;
+        q.row_bytes = rb;
+        q.rows = rows;
+        q.cols = cols;
+        q.nb = cols / (int)be;
+        return emu_mfma_matvec(ctx, q, n, cap, nks);
+    };
+    // the first layer's q|k|v input: the embeddings, normalised
+    if ((st = link(0, 0, 1, nullptr, s->state, H, attn_norm, true)) != EMU_OK) return st;
+    for (uint32_t layer = 0; layer < c.layers; ++layer) {
+        const uint8_t *lw = m->base + m->off_layers + (size_t)layer * m->layer_bytes;
+        int nks = 0;
+        if ((st = matvec(lw + m->off_q, nullptr, m->rb_h, QW + 2 * KW, H, &nks)) != EMU_OK) return st;
+        if ((st = link(3, nks, 1, s->qkv, nullptr, QW + 2 * KW, nullptr, false)) != EMU_OK) return st;
+        if ((st = emu_launch_attn(ctx, layer_attn(s, layer))) != EMU_OK) return st;
+        if ((st = link(0, 0, 1, nullptr, s->attn, QW, nullptr, true)) != EMU_OK) return st;
+        if ((st = matvec(lw + m->off_o, nullptr, m->rb_q, H, QW, &nks)) != EMU_OK) return st;
+        if ((st = link(1, nks, 1, s->state, nullptr, H, ffn_norm + (size_t)layer * H, true)) != EMU_OK) return st;
+        if ((st = matvec(lw + m->off_g, lw + m->off_u, m->rb_h, F, H, &nks)) != EMU_OK) return st;
+        if ((st = link(2, nks, 2, nullptr, nullptr, F, nullptr, true)) != EMU_OK) return st;
+        if ((st = matvec(lw + m->off_d, nullptr, m->rb_f, H, F, &nks)) != EMU_OK) return st;
+        const float *next = layer + 1 < c.layers ? attn_norm + (size_t)(layer + 1) * H : out_norm;
+        if ((st = link(1, nks, 1, s->state, nullptr, H, next, true)) != EMU_OK) return st;
+    }
+    QmvArgs out{};
+    out.w = m->base + (c.tied ? m->off_embed : m->off_output);
+    out.row_bytes = m->rb_h;
+    out.rows = (int)c.vocab;
+    out.cols = H;
+    out.nb = H / (int)be;
+    out.y = s->logits;
+    out.keys = s->keys;
+    out.key_stride = (int)s->key_stride;
+    out.tie_last = c.style == EMU_STYLE_SMOL ? 1 : 0;
+    if ((st = emu_mfma_matvec(ctx, out, n, cap, nullptr)) != EMU_OK) return st;
+    int slots = 0;
+    if ((st = emu_mfma_finish(ctx, out, n, cap, &slots)) != EMU_OK) return st;
+    return launch_finalize(s, slots);
+}
+
 int run_step(emu_session *s)
 {
     emu_model *m = s->m;
@@ -340,6 +490,7 @@ int run_step(emu_session *s)
     default: return EMU_E_UNSUPPORTED;
     }
     if (st != EMU_OK) return st;
+    if (mfma_chain(m, s->n)) return run_chain(s);
     uint32_t be = 0, bb = 0;
     emu_block_layout(c.encoding, &be, &bb);
     const int smol = c.style == EMU_STYLE_SMOL;
@@ -357,31 +508,7 @@ int run_step(emu_session *s)
         a.eps = c.eps;
         a.y = s->qkv;
         if ((st = emu_launch_qmv(ctx, c.encoding, a, n)) != EMU_OK) return st;
-        EmuAttnLaunch al{};
-        al.qkv = s->qkv;
-        al.k_cache = s->k_cache;
-        al.v_cache = s->v_cache;
-        al.positions = s->positions;
-        al.rope = s->rope;
-        al.q_norm = c.qk_norm ? reinterpret_cast<const float *>(m->base + m->off_q_norm) : nullptr;
-        al.k_norm = c.qk_norm ? reinterpret_cast<const float *>(m->base + m->off_k_norm) : nullptr;
-        al.eps = c.eps;
-        al.score_mul = smol ? 1.0f / sqrtf((float)hd) : 0.0f;
-        al.score_div = smol ? 0.0f : sqrtf((float)hd);
-        al.rope_fma = smol;
-        al.interleaved = 0;
-        al.heads = (int)c.heads;
-        al.kv_heads = (int)c.kv_heads;
-        al.head_dim = (int)hd;
-        al.layers = (int)c.layers;
-        al.layer = (int)layer;
-        al.context = (int)s->context;
-        al.clients = n;
-        al.kv_f16 = s->kv_f16;
-        al.partial = s->partial;
-        al.counters = s->counters;
-        al.out = s->attn;
-        if ((st = emu_launch_attn(ctx, al)) != EMU_OK) return st;
+        if ((st = emu_launch_attn(ctx, layer_attn(s, layer))) != EMU_OK) return st;
         // o projection + residual.
         QmvArgs o{};
         o.w = lw + m->off_o;
@@ -433,12 +560,7 @@ int run_step(emu_session *s)
     out.tie_last = smol ? 1 : 0;
     int slots = 0;
     if ((st = emu_launch_qmv(ctx, c.encoding, out, n, &slots)) != EMU_OK) return st;
-    if (slots <= 0 || slots > (int)s->key_stride) return EMU_E_CONFIG;
-    hipLaunchKernelGGL(finalize_kernel, dim3(s->n), dim3(1024), 0, ctx->stream, s->keys, (int)s->key_stride, slots,
-                       smol ? 1 : 0, s->prompt, (int)s->context, s->hist, s->ctrl, s->tokens, s->positions,
-                       s->steps, s->last);
-    EMU_LAUNCH_CHECK(ctx);
-    return EMU_OK;
+    return launch_finalize(s, slots);
 }
 
 int ensure_graph(emu_session *s)
@@ -691,7 +813,7 @@ extern "C" int emu_session_create(emu_model *m, uint32_t n_clients, uint32_t con
                                   {(int)c.ffn, (int)c.hidden, 2},
                                   {(int)c.hidden, (int)c.ffn, 1},
                                   {(int)c.vocab, (int)c.hidden, 1}};
-        size_t ws = 0;
+        size_t ws = mfma_chain(m, n_clients) ? mfma_chain_bytes(m) : 0;
         for (const auto &sh : shapes)
             if (emu_mfma_supports(c.encoding, sh[1], (int)n_clients)) {
                 const size_t b = emu_mfma_workspace_bytes(sh[0], sh[1], sh[2]);

@@ -108,6 +108,26 @@ def test_qwen3_width_decode_matches_oracle(ctx):
     assert worst <= 1e-3, worst
 
 
+def test_qwen3_width_batched_decode_matches_oracle(ctx):
+    """Several clients at Qwen3-8B widths: the chained multi-token matvecs
+    (int8 matrix cores) against the oracle, per client."""
+    model = Model(ctx, WIDE_QWEN3)
+    model.synth(4322)
+    steps, context, n = 10, 80, 4
+    sess = Session(model, n, context, kv_f16=True)
+    ref = oracle_for(model, context, True, n)
+    rng = np.random.default_rng(6)
+    worst = 0.0
+    for step in range(steps):
+        toks = rng.integers(0, WIDE_QWEN3.vocab, size=n).astype(np.uint32)
+        nxt, logits = sess.decode_step(toks, want_logits=True)
+        r = ref.step(toks)
+        for c in range(n):
+            worst = max(worst, rel_inf(logits[c], r[c]))
+            assert int(nxt[c]) == oracle.argmax(r[c], False), (step, c)
+    assert worst <= 1e-3, worst
+
+
 ATTN_SHAPES = [
     # (heads, kv_heads, head_dim, style): group sizes 8, 1, 3 and 2; head dims 64, 256, 128
     (8, 1, 64, _lib.EMU_STYLE_QWEN3),
