@@ -203,75 +203,94 @@ struct MfmaArgs {
     float *part; // [cols/kSlice][nmat][kMaxTok][rows]
 };
 
-// Q6_K codes of 8 columns (two dwords) minus 32, as int8: sub-block
-// (h, q, p) takes the nibble q>>1 of the ql bytes and bits 2q..2q+1 of the qh
-// bytes.  (c | 0x80) - 0x20 never borrows across bytes; ^ 0x80 restores the sign.
-__device__ __forceinline__ uint32_t code_m32(uint32_t ql, uint32_t qh, int q)
+// Q6_K codes (0..63) of 8 columns, two dwords: sub-block (h, q, p) takes
+// the nibble q>>1 of the ql bytes and bits 2q..2q+1 of the qh bytes.
+__device__ __forceinline__ uint32_t code8(uint32_t ql, uint32_t qh, int q)
 {
-    uint32_t c;
     switch (q) {
-    case 0: c = (ql & 0x0f0f0f0fu) | ((qh << 4) & 0x30303030u); break;
-    case 1: c = (ql & 0x0f0f0f0fu) | ((qh << 2) & 0x30303030u); break;
-    case 2: c = ((ql >> 4) & 0x0f0f0f0fu) | (qh & 0x30303030u); break;
-    default: c = ((ql >> 4) & 0x0f0f0f0fu) | ((qh >> 2) & 0x30303030u); break;
+    case 0: return (ql & 0x0f0f0f0fu) | ((qh << 4) & 0x30303030u);
+    case 1: return (ql & 0x0f0f0f0fu) | ((qh << 2) & 0x30303030u);
+    case 2: return ((ql >> 4) & 0x0f0f0f0fu) | (qh & 0x30303030u);
+    default: return ((ql >> 4) & 0x0f0f0f0fu) | ((qh >> 2) & 0x30303030u);
     }
-    return ((c | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
 }
 
-__global__ __launch_bounds__(EMU_WAVE * kWaves) void qmv_mfma_kernel(MfmaArgs a)
+// One unit of work: 32 weight rows of one matrix x one 2048-column slice.
+// A lane holds, for its row (lane % 32) and column half kh = lane / 32 of
+// each 16-column sub-block of its wavefront's 256-column block, the weight
+// bytes and the A operands (limbs of M row lane % 32).
+struct Unit {
+    uint2 ql[2][2][2], qh[2][2];
+    uint4 sc;
+    uint32_t d;
+    long av[16];
+    int ks, rt, mat;
+};
+
+// One unit per workgroup (two workgroups fit per CU, which hides the
+// load latency better than one persistent double-buffered workgroup).
+// The unit's per-token scales are staged in LDS while the weights load.
+__global__ __launch_bounds__(EMU_WAVE * kWaves, 2) void qmv_mfma_kernel(MfmaArgs a, int units)
 {
     const int nks = a.cols / kSlice, nrt = (a.rows + kTileRows - 1) / kTileRows;
-    int u = blockIdx.x;
-    const int ks = u % nks;
-    u /= nks;
-    const int rt = u % nrt, mat = u / nrt;
     const int tid = threadIdx.x, lane = tid & (EMU_WAVE - 1), w = tid / EMU_WAVE;
     const int j = lane & 31, kh = lane >> 5;
-    const int cb = ks * kWaves + w; // this wavefront's 256-column block
-    const int row = rt * kTileRows + j;
-    const int rl = row < a.rows ? row : a.rows - 1; // a valid row; never stored
-    const uint8_t *bp = a.w[mat] + (size_t)rl * a.row_bytes + (size_t)cb * 210;
+    const bool live = j < 24 && (j & 7) < a.n_tok; // A row j: limb j / 8 of token j % 8
+    __shared__ __align__(16) float xs[kSlice / 16 * kMaxTok];
+    __shared__ float red[kWaves][kMaxTok][kTileRows];
 
-    // This lane's weight bytes: columns 8kh..8kh+7 of each of the block's 16
-    // sub-blocks (h, q, p) = 128h + 32q + 16p + ...
-    uint2 ql[2][2][2], qh[2][2];
+    Unit b;
+    {
+        const int u = blockIdx.x;
+        b.ks = u % nks;
+        const int v = u / nks;
+        b.rt = v % nrt;
+        b.mat = v / nrt;
+        const int cb = b.ks * kWaves + w; // this wavefront's 256-column block
+        int row = b.rt * kTileRows + j;
+        row = row < a.rows ? row : a.rows - 1; // a valid row; never stored
+        const uint8_t *bp = a.w[b.mat] + (size_t)row * a.row_bytes + (size_t)cb * 210;
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            ql[h][0][p] = ld8(bp + 64 * h + 16 * p + 8 * kh);
-            ql[h][1][p] = ld8(bp + 64 * h + 32 + 16 * p + 8 * kh);
-            qh[h][p] = ld8(bp + 128 + 32 * h + 16 * p + 8 * kh);
-        }
-    const uint4 scv = ld16(bp + 192);
-    const float d = h2f(ld2(bp + 208));
-
-    // A operands: M row i = lane % 32 (limb i / 8, token i % 8).
-    const int i = j;
-    const bool live = i < 24 && (i & 7) < a.n_tok;
-    const uint8_t *ap = a.xa + (size_t)cb * 16 * kSbBytes + (size_t)(kh * 24 + (live ? i : 0)) * 8;
-    const float *sp = a.xs + (size_t)cb * 16 * kMaxTok + 4 * kh;
-
-    long av[16];
+            for (int p = 0; p < 2; ++p) {
+                b.ql[h][0][p] = ld8(bp + 64 * h + 16 * p + 8 * kh);
+                b.ql[h][1][p] = ld8(bp + 64 * h + 32 + 16 * p + 8 * kh);
+                b.qh[h][p] = ld8(bp + 128 + 32 * h + 16 * p + 8 * kh);
+            }
+        b.sc = ld16(bp + 192);
+        b.d = ld2(bp + 208);
+        const uint8_t *ap = a.xa + (size_t)cb * 16 * kSbBytes + (size_t)(kh * 24 + (live ? j : 0)) * 8;
 #pragma unroll
-    for (int sb = 0; sb < 16; ++sb) av[sb] = live ? *reinterpret_cast<const long *>(ap + sb * kSbBytes) : 0;
+        for (int sb = 0; sb < 16; ++sb) b.av[sb] = live ? *reinterpret_cast<const long *>(ap + sb * kSbBytes) : 0;
+    }
+    {
+        const float4 *src = reinterpret_cast<const float4 *>(a.xs + (size_t)b.ks * (kSlice / 16) * kMaxTok);
+        for (int i = tid; i < kSlice / 16 * kMaxTok / 4; i += EMU_WAVE * kWaves)
+            reinterpret_cast<float4 *>(xs)[i] = src[i];
+    }
+    __syncthreads();
 
-    // Sub-block sb = 8h + 2q + p: its codes, one MFMA, then the float step.
-    // Software-pipelined by hand (the next sub-block's MFMA goes out before
-    // this one's float step; scales are loaded two sub-blocks ahead) with a
-    // scheduling barrier per step, so only two accumulator tiles are live.
+    // Sub-block sb = 8h + 2q + p: D = A x codes + A x (-32), then the float
+    // step.  Software-pipelined by hand (the next sub-block's MFMAs go out
+    // before this one's float step) with a scheduling barrier per step, so
+    // only two accumulator tiles are live.
+    const long neg32 = (long)0xe0e0e0e0e0e0e0e0ull;
+    const float d = h2f((uint16_t)b.d);
+    const float *sp = xs + (size_t)w * 16 * kMaxTok + 4 * kh;
     auto mma = [&](int sb) {
         const int h = sb >> 3, q = (sb >> 1) & 3, p = sb & 1;
-        const uint2 lq = ql[h][q & 1][p], hq = qh[h][p];
-        const uint32_t c0 = code_m32(lq.x, hq.x, q), c1 = code_m32(lq.y, hq.y, q);
-        const long bv = (long)(((uint64_t)c1 << 32) | c0);
+        const uint2 lq = b.ql[h][q & 1][p], hq = b.qh[h][p];
+        const long bv = (long)(((uint64_t)code8(lq.y, hq.y, q) << 32) | code8(lq.x, hq.x, q));
         v16i D = {};
-        return __builtin_amdgcn_mfma_i32_32x32x16_i8(av[sb], bv, D, 0, 0, 0);
+        D = __builtin_amdgcn_mfma_i32_32x32x16_i8(b.av[sb], bv, D, 0, 0, 0);
+        return __builtin_amdgcn_mfma_i32_32x32x16_i8(b.av[sb], neg32, D, 0, 0, 0);
     };
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto epi = [&](int sb, const v16i &D, const float4 &s4) {
-        const uint32_t sw = sb < 4 ? scv.x : sb < 8 ? scv.y : sb < 12 ? scv.z : scv.w;
+    auto epi = [&](int sb, const v16i &D) {
+        const uint32_t sw = sb < 4 ? b.sc.x : sb < 8 ? b.sc.y : sb < 12 ? b.sc.z : b.sc.w;
         const float scd = (float)(int)__builtin_amdgcn_sbfe(sw, 8u * (uint32_t)(sb & 3), 8u) * d;
+        const float4 s4 = *reinterpret_cast<const float4 *>(sp + sb * kMaxTok);
         const float s[4] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -282,32 +301,27 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves) void qmv_mfma_kernel(MfmaArgs a)
             acc[r] = __builtin_fmaf((float)t, scd * s[r], acc[r]);
         }
     };
-    auto sload = [&](int sb) { return *reinterpret_cast<const float4 *>(sp + sb * kMaxTok); };
-    float4 sv[16];
-    sv[0] = sload(0);
-    sv[1] = sload(1);
     v16i cur = mma(0);
 #pragma unroll
     for (int sb = 0; sb < 16; ++sb) {
-        if (sb + 2 < 16) sv[sb + 2] = sload(sb + 2);
         v16i next;
         if (sb + 1 < 16) next = mma(sb + 1);
-        epi(sb, cur, sv[sb]);
+        epi(sb, cur);
         __builtin_amdgcn_sched_barrier(0);
         if (sb + 1 < 16) cur = next;
     }
 
-    __shared__ float red[kWaves][kMaxTok][kTileRows];
+    // The eight wavefronts' sums meet in LDS in a fixed order.
 #pragma unroll
     for (int r = 0; r < 4; ++r) red[w][4 * kh + r][j] = acc[r];
     __syncthreads();
     if (tid < kMaxTok * kTileRows) {
-        const int t = tid / kTileRows, jj = tid % kTileRows, orow = rt * kTileRows + jj;
+        const int t = tid / kTileRows, jj = tid % kTileRows, orow = b.rt * kTileRows + jj;
         if (t < a.n_tok && orow < a.rows) {
             float v = red[0][t][jj];
 #pragma unroll
             for (int k = 1; k < kWaves; ++k) v += red[k][t][jj];
-            a.part[(((size_t)ks * a.nmat + mat) * kMaxTok + t) * a.rows + orow] = v;
+            a.part[(((size_t)b.ks * a.nmat + b.mat) * kMaxTok + t) * a.rows + orow] = v;
         }
     }
 }
@@ -478,8 +492,8 @@ int emu_mfma_matvec(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int
     ma.xs = w.xs;
     ma.part = w.part;
     const int nks = q.cols / kSlice, nrt = (q.rows + kTileRows - 1) / kTileRows;
-    hipLaunchKernelGGL(qmv_mfma_kernel, dim3((unsigned)(nks * nrt * nmat)), dim3(EMU_WAVE * kWaves), 0,
-                       ctx->stream, ma);
+    const int units = nks * nrt * nmat;
+    hipLaunchKernelGGL(qmv_mfma_kernel, dim3((unsigned)units), dim3(EMU_WAVE * kWaves), 0, ctx->stream, ma, units);
     EMU_LAUNCH_CHECK(ctx);
     if (part_nks) *part_nks = nks;
     return EMU_OK;
