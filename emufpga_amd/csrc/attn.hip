@@ -193,7 +193,10 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     constexpr int NV = kPP * GH;                // values per reduce-scatter
     using vec_t = typename VecLoad<kv_t, EPL>::type;
 
-    const int chunk = blockIdx.x, kvh = blockIdx.y, client = blockIdx.z;
+    // Grid: x = (kv head, client), y = chunk.  Workgroups are dispatched x
+    // first, so every client's low chunks (the ones a context uses) go out
+    // before the idle high chunks, which exit at once.
+    const int kvh = blockIdx.x % a.kv_heads, client = blockIdx.x / a.kv_heads, chunk = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & (EMU_WAVE - 1), w = tid / EMU_WAVE;
     const int pos = (int)a.positions[client];
     const int n = pos + 1;
@@ -494,7 +497,7 @@ int emu_launch_attn(emu_ctx *ctx, const EmuAttnLaunch &l)
     a.counters = l.counters;
     a.max_chunks = emu_attn_max_chunks(l.context);
     a.out = l.out;
-    const dim3 grid(a.max_chunks, l.kv_heads, l.clients);
+    const dim3 grid(l.kv_heads * l.clients, a.max_chunks);
     const int gq = l.heads / l.kv_heads;
     switch (l.head_dim * 2 + (l.kv_f16 ? 1 : 0)) {
     case 128: launch_hd<64, false>(a, grid, ctx->stream, gq); break;
