@@ -36,7 +36,10 @@ constexpr int kChunk = kWaves * kPP; // positions per workgroup
 constexpr int kMergeBatch = 16;      // chunks whose partials the merge loads at once
 
 struct AttnArgs {
-    const float *qkv;       // [client][q_width + 2*kv_width]
+    const float *qkv;       // [client][q_width + 2*kv_width], or the sum of qkv_slices such arrays
+    int qkv_slices;         // partial-sum slices to add (>= 1)
+    int qkv_client_stride;  // floats between clients
+    size_t qkv_slice_stride; // floats between slices
     void *k_cache, *v_cache;
     const uint32_t *positions;
     const float2 *rope;     // [context][hd/2] (cos, sin)
@@ -51,7 +54,46 @@ struct AttnArgs {
     uint32_t *counters;     // [client][kv_head]
     int max_chunks;
     float *out;             // [client][heads * hd]
+    uint8_t *xa;            // optional: the output as the multi-token matvec's A operands
+    float *xs;              //           and their scales (token = client)
 };
+
+// A value of q|k|v: the sum of its partial-sum slices, in slice order.
+__device__ __forceinline__ float qkv_at(const float *p, int ns, size_t stride)
+{
+    float v = p[0];
+    for (int s = 1; s < ns; ++s) v += p[s * stride];
+    return v;
+}
+
+// One column of the output written as the multi-token matvec's A operands:
+// three 7-bit limbs under the 16-column sub-block's power-of-two scale (the
+// link kernel's split, bit for bit).  The 16 lanes of a sub-block are
+// neighbours and all call this together.
+__device__ __forceinline__ void emit_limbs(float v, int col, int t, uint8_t *xa, float *xs)
+{
+    float amax = fabsf(v);
+    int bad = !(fabsf(v) <= 3.402823466e38f);
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, o, EMU_WAVE));
+        bad |= __shfl_xor(bad, o, EMU_WAVE);
+    }
+    const bool finite = !bad;
+    int e = 0;
+    (void)frexpf(finite ? amax : 0.0f, &e);
+    const float s = finite ? ldexpf(v, 6 - e) : 0.0f;
+    const float f0 = rintf(s);
+    const float r1 = (s - f0) * 128.0f;
+    const float f1 = rintf(r1);
+    const float f2 = rintf((r1 - f1) * 128.0f);
+    const int sb = col >> 4, kh = (col >> 3) & 1;
+    uint8_t *dst = xa + (size_t)sb * 384 + (size_t)(kh * 24 + t) * 8 + (col & 7);
+    dst[0] = (uint8_t)(int)f0;
+    dst[64] = (uint8_t)(int)f1;
+    dst[128] = (uint8_t)(int)f2;
+    if ((col & 15) == 0) xs[(size_t)sb * 8 + t] = finite ? ldexpf(1.0f, e - 20) : __int_as_float(0x7fc00000);
+}
 
 __device__ __forceinline__ float wave_max(float v)
 {
@@ -81,8 +123,8 @@ __device__ __forceinline__ void rotate(float &l, float &r, float2 cs, int fma_fo
 // One wavefront: RMSNorm (optional) + RoPE of one head of HD values from
 // global memory into dst (LDS).  Lanes own rotation pairs.
 template <int HD>
-__device__ __forceinline__ void prep_head(const float *src, float *dst, const float *gain, float eps,
-                                          const float2 *rope_row, int fma_form, int interleaved, int lane)
+__device__ __forceinline__ void prep_head(const float *src, int ns, size_t sstride, float *dst, const float *gain,
+                                          float eps, const float2 *rope_row, int fma_form, int interleaved, int lane)
 {
     constexpr int NP = HD / 2;
     constexpr int PPL = (NP + EMU_WAVE - 1) / EMU_WAVE;
@@ -96,8 +138,8 @@ __device__ __forceinline__ void prep_head(const float *src, float *dst, const fl
         const int ic = i < NP ? i : NP - 1; // in-bounds stand-in for idle lanes
         ia[j] = interleaved ? 2 * ic : ic;
         ib[j] = interleaved ? 2 * ic + 1 : ic + NP;
-        a[j] = src[ia[j]];
-        b[j] = src[ib[j]];
+        a[j] = qkv_at(src + ia[j], ns, sstride);
+        b[j] = qkv_at(src + ib[j], ns, sstride);
         cs[j] = rope_row[ic];
         if (gain) {
             ga[j] = gain[ia[j]];
@@ -212,7 +254,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     __shared__ uint32_t arrived;
 
     const int qw = a.heads * HD, kw = a.kv_heads * HD;
-    const float *row = a.qkv + (size_t)client * (qw + 2 * kw);
+    const float *row = a.qkv + (size_t)client * a.qkv_client_stride;
     const float2 *rope_row = a.rope + (size_t)pos * (HD / 2);
     const float *qn = a.q_norm ? a.q_norm + (size_t)a.layer * HD : nullptr;
     const float *kn = a.k_norm ? a.k_norm + (size_t)a.layer * HD : nullptr;
@@ -243,17 +285,19 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     const int items = GQ + (owner ? 1 : 0);
     for (int it = w; it < items; it += kWaves) {
         if (it < GQ)
-            prep_head<HD>(row + (kvh * GQ + it) * HD, q_s[it], qn, a.eps, rope_row, a.rope_fma, a.interleaved,
+            prep_head<HD>(row + (kvh * GQ + it) * HD, a.qkv_slices, a.qkv_slice_stride, q_s[it], qn, a.eps,
+                          rope_row, a.rope_fma, a.interleaved,
                           lane);
         else
-            prep_head<HD>(row + qw + kvh * HD, knew, kn, a.eps, rope_row, a.rope_fma, a.interleaved, lane);
+            prep_head<HD>(row + qw + kvh * HD, a.qkv_slices, a.qkv_slice_stride, knew, kn, a.eps, rope_row,
+                          a.rope_fma, a.interleaved, lane);
     }
     for (int g = GQ + w; g < GQP; g += kWaves)
         for (int e = lane; e < HD; e += EMU_WAVE) q_s[g][e] = 0.0f;
     __syncthreads();
     if (owner && tid < HD) {
         const float kv = knew[tid];
-        const float vv = row[qw + kw + kvh * HD + tid];
+        const float vv = qkv_at(row + qw + kw + kvh * HD + tid, a.qkv_slices, a.qkv_slice_stride);
         kv_t kq, vq;
         if constexpr (F16) {
             kq = __float2half_rn(kv);
@@ -371,7 +415,9 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
         for (int idx = tid; idx < GQ * HD; idx += kThreads) {
             const int g = idx / HD, d = idx % HD;
             const float o = (accs[0][g][d] + accs[1][g][d]) + (accs[2][g][d] + accs[3][g][d]);
-            outp[(kvh * GQ + g) * HD + d] = o / lh[g];
+            const float r = o / lh[g];
+            outp[(kvh * GQ + g) * HD + d] = r;
+            if (a.xa) emit_limbs(r, (kvh * GQ + g) * HD + d, client, a.xa, a.xs);
         }
         return;
     }
@@ -451,7 +497,11 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     }
 #pragma unroll
     for (int i = 0; i < NI; ++i)
-        if (live[i]) outp[head_of[i] * HD + dim_of[i]] = O[i] / L[i];
+        if (live[i]) {
+            const float r = O[i] / L[i];
+            outp[head_of[i] * HD + dim_of[i]] = r;
+            if (a.xa) emit_limbs(r, head_of[i] * HD + dim_of[i], client, a.xa, a.xs); // whole 16-lane groups
+        }
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -497,6 +547,12 @@ int emu_launch_attn(emu_ctx *ctx, const EmuAttnLaunch &l)
     a.counters = l.counters;
     a.max_chunks = emu_attn_max_chunks(l.context);
     a.out = l.out;
+    a.qkv_slices = l.qkv_slices > 0 ? l.qkv_slices : 1;
+    a.qkv_client_stride = l.qkv_client_stride > 0 ? l.qkv_client_stride : (l.heads + 2 * l.kv_heads) * l.head_dim;
+    a.qkv_slice_stride = l.qkv_slice_stride;
+    a.xa = l.xa;
+    a.xs = l.xs;
+    if (a.xa && (l.clients > 8 || (l.heads * l.head_dim) % 16 != 0)) return EMU_E_CONFIG;
     const dim3 grid(l.kv_heads * l.clients, a.max_chunks);
     const int gq = l.heads / l.kv_heads;
     switch (l.head_dim * 2 + (l.kv_f16 ? 1 : 0)) {

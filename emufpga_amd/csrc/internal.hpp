@@ -390,6 +390,9 @@ size_t emu_mfma_part_bytes(int rows, int cols, int nmat);
 int emu_mfma_link(emu_ctx *ctx, const EmuMfmaLink &l);
 int emu_mfma_matvec(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int *part_nks);
 int emu_mfma_finish(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int *key_slots);
+// The chained form's buffers: A operands + scales, and the partial sums
+// (layout [slice][matrix][8 tokens][rows]).
+void emu_mfma_buffers(emu_ctx *ctx, int cols_cap, uint8_t **xa, float **xs, float **part);
 
 // Fused decode attention of one layer for every client (attn.hip).
 struct EmuAttnLaunch {
@@ -403,6 +406,13 @@ struct EmuAttnLaunch {
     float *partial;
     uint32_t *counters;
     float *out;
+    // Optional: q|k|v as the sum of qkv_slices partial-sum arrays (client
+    // stride and slice stride in floats; 0 = one plain array), and the output
+    // also written as the multi-token matvec's A operands (mfma.hip layout).
+    int qkv_slices, qkv_client_stride;
+    size_t qkv_slice_stride;
+    uint8_t *xa;
+    float *xs;
 };
 int emu_launch_attn(emu_ctx *ctx, const EmuAttnLaunch &l);
 int emu_attn_max_chunks(int context);

@@ -84,8 +84,16 @@ __global__ __launch_bounds__(kLinkThreads) void mfma_link_kernel(LinkArgs a)
 {
     const int t = blockIdx.x, tid = threadIdx.x;
     const int npairs = a.cols / 8;
-    float v[kLinkPairs][8];
+    float v[kLinkPairs][8], gn[kLinkPairs][8];
     float ss = 0.0f;
+    // The gain goes out with the first loads (it does not depend on them).
+    if (a.gain && a.xa) {
+#pragma unroll
+        for (int k = 0; k < kLinkPairs; ++k) {
+            const int p = tid + k * kLinkThreads;
+            if (p < npairs) ld8f(a.gain + 8 * p, gn[k]);
+        }
+    }
 #pragma unroll
     for (int k = 0; k < kLinkPairs; ++k) {
         const int p = tid + k * kLinkThreads;
@@ -148,13 +156,11 @@ __global__ __launch_bounds__(kLinkThreads) void mfma_link_kernel(LinkArgs a)
     for (int k = 0; k < kLinkPairs; ++k) {
         const int p = tid + k * kLinkThreads;
         if (p >= npairs) break; // pairs (2m, 2m+1) stop together: npairs is even
-        const int sb = p >> 1, kh = p & 1, c0 = 8 * p;
+        const int sb = p >> 1, kh = p & 1;
         float w[8];
         if (a.gain) {
-            float g[8];
-            ld8f(a.gain + c0, g);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) w[e] = __fmul_rn(__fmul_rn(v[k][e], scale), g[e]);
+            for (int e = 0; e < 8; ++e) w[e] = __fmul_rn(__fmul_rn(v[k][e], scale), gn[k][e]);
         } else {
 #pragma unroll
             for (int e = 0; e < 8; ++e) w[e] = v[k][e];
@@ -520,6 +526,14 @@ int emu_mfma_finish(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int
     EMU_LAUNCH_CHECK(ctx);
     if (key_slots) *key_slots = gx;
     return EMU_OK;
+}
+
+void emu_mfma_buffers(emu_ctx *ctx, int cols_cap, uint8_t **xa, float **xs, float **part)
+{
+    const Ws w = workspace(ctx, cols_cap);
+    *xa = w.xa;
+    *xs = w.xs;
+    *part = w.part;
 }
 
 int emu_launch_mfma(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int *key_slots)

@@ -441,15 +441,25 @@ int run_chain(emu_session *s)
         q.nb = cols / (int)be;
         return emu_mfma_matvec(ctx, q, n, cap, nks);
     };
+    uint8_t *xa = nullptr;
+    float *xs = nullptr, *part = nullptr;
+    emu_mfma_buffers(ctx, cap, &xa, &xs, &part);
     // the first layer's q|k|v input: the embeddings, normalised
     if ((st = link(0, 0, 1, nullptr, s->state, H, attn_norm, true)) != EMU_OK) return st;
     for (uint32_t layer = 0; layer < c.layers; ++layer) {
         const uint8_t *lw = m->base + m->off_layers + (size_t)layer * m->layer_bytes;
         int nks = 0;
         if ((st = matvec(lw + m->off_q, nullptr, m->rb_h, QW + 2 * KW, H, &nks)) != EMU_OK) return st;
-        if ((st = link(3, nks, 1, s->qkv, nullptr, QW + 2 * KW, nullptr, false)) != EMU_OK) return st;
-        if ((st = emu_launch_attn(ctx, layer_attn(s, layer))) != EMU_OK) return st;
-        if ((st = link(0, 0, 1, nullptr, s->attn, QW, nullptr, true)) != EMU_OK) return st;
+        // Attention adds the q|k|v slices itself and writes the o
+        // projection's operands: no link kernel on either side of it.
+        EmuAttnLaunch al = layer_attn(s, layer);
+        al.qkv = part;
+        al.qkv_slices = nks;
+        al.qkv_client_stride = QW + 2 * KW;
+        al.qkv_slice_stride = (size_t)8 * (QW + 2 * KW);
+        al.xa = xa;
+        al.xs = xs;
+        if ((st = emu_launch_attn(ctx, al)) != EMU_OK) return st;
         if ((st = matvec(lw + m->off_o, nullptr, m->rb_q, H, QW, &nks)) != EMU_OK) return st;
         if ((st = link(1, nks, 1, s->state, nullptr, H, ffn_norm + (size_t)layer * H, true)) != EMU_OK) return st;
         if ((st = matvec(lw + m->off_g, lw + m->off_u, m->rb_h, F, H, &nks)) != EMU_OK) return st;
