@@ -17,8 +17,8 @@
 // the one float step per sub-block, acc = fma(t, (sc * d) * s, acc), the same
 // step as the batch-1 kernel.
 //
-// Work split: a workgroup owns 32 weight rows of one matrix and a 2048-column
-// slice (eight 256-column blocks, one per wavefront); the eight wavefronts'
+// Work split: a workgroup owns 32 weight rows of one matrix and a 1024-column
+// slice (four 256-column blocks, one per wavefront); the four wavefronts'
 // sums meet in LDS in a fixed order and the slice's partial sum is written to
 // a workspace.  A finishing pass adds the slices' partials in slice order and
 // applies the epilogue (residual accumulate, SwiGLU of a gate/up pair, greedy
@@ -51,9 +51,10 @@ __device__ __forceinline__ void ld8f(const float *p, float (&v)[8])
 
 constexpr int kMaxTok = 8;          // tokens per tile (A rows 8 * limb + token)
 constexpr int kTileRows = 32;       // weight rows per tile (MFMA N)
-constexpr int kWaves = 8;           // wavefronts per workgroup, one 256-column block each
+constexpr int kWaves = 4;           // wavefronts per workgroup, one 256-column block each
 constexpr int kSlice = kWaves * 256; // columns per workgroup
 constexpr int kSbBytes = 2 * 24 * 8; // A-operand bytes per 16-column sub-block
+constexpr int kRowStride = 232;      // LDS bytes per staged weight row: 58 dwords, so 32 rows hit distinct banks
 constexpr int kFinishThreads = 256;
 
 // One token's activation vector, finished from the producing matvec's
@@ -221,7 +222,7 @@ __device__ __forceinline__ uint32_t code8(uint32_t ql, uint32_t qh, int q)
     }
 }
 
-// One unit of work: 32 weight rows of one matrix x one 2048-column slice.
+// One unit of work: 32 weight rows of one matrix x one 1024-column slice.
 // A lane holds, for its row (lane % 32) and column half kh = lane / 32 of
 // each 16-column sub-block of its wavefront's 256-column block, the weight
 // bytes and the A operands (limbs of M row lane % 32).
@@ -233,10 +234,14 @@ struct Unit {
     int ks, rt, mat;
 };
 
-// One unit per workgroup (two workgroups fit per CU, which hides the
-// load latency better than one persistent double-buffered workgroup).
-// The unit's per-token scales are staged in LDS while the weights load.
-__global__ __launch_bounds__(EMU_WAVE * kWaves, 2) void qmv_mfma_kernel(MfmaArgs a, int units)
+// One unit per workgroup (four fit per CU; they drift out of step, so one
+// loads while another computes).  The weight bytes are fetched coalesced --
+// four rows per instruction, 16 bytes per lane -- into the wavefront's own
+// LDS rows and read back in the MFMA operand layout (fetching that layout
+// directly, 8 bytes from each of 32 rows per instruction, streams at about
+// two thirds of the rate).  The unit's per-token scales are staged in LDS
+// while the weights load.
+__global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs a, int units)
 {
     const int nks = a.cols / kSlice, nrt = (a.rows + kTileRows - 1) / kTileRows;
     const int tid = threadIdx.x, lane = tid & (EMU_WAVE - 1), w = tid / EMU_WAVE;
@@ -246,6 +251,7 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 2) void qmv_mfma_kernel(MfmaArgs
     __shared__ float red[kWaves][kMaxTok][kTileRows];
 
     Unit b;
+    __shared__ __align__(16) uint8_t wl[kWaves][kTileRows * kRowStride];
     {
         const int u = blockIdx.x;
         b.ks = u % nks;
@@ -253,19 +259,43 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 2) void qmv_mfma_kernel(MfmaArgs
         b.rt = v % nrt;
         b.mat = v / nrt;
         const int cb = b.ks * kWaves + w; // this wavefront's 256-column block
-        int row = b.rt * kTileRows + j;
-        row = row < a.rows ? row : a.rows - 1; // a valid row; never stored
-        const uint8_t *bp = a.w[b.mat] + (size_t)row * a.row_bytes + (size_t)cb * 210;
+        // Coalesced: instruction k covers rows 4k..4k+3 of the tile, 16 lanes
+        // per row (13 x 16 bytes + the 2-byte d), into this wavefront's LDS rows.
+        const int r4 = lane >> 4, c16 = lane & 15;
+        uint4 raw[8];
+        uint16_t dd[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            int row = b.rt * kTileRows + 4 * k + r4;
+            row = row < a.rows ? row : a.rows - 1; // a valid row; never stored
+            const uint8_t *bp = a.w[b.mat] + (size_t)row * a.row_bytes + (size_t)cb * 210;
+            if (c16 < 13) raw[k] = ld16(bp + 16 * c16);
+            else if (c16 == 13) dd[k] = ld2(bp + 208);
+        }
+        uint8_t *mine = wl[w];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            uint8_t *rp = mine + (4 * k + r4) * kRowStride;
+            if (c16 < 13) {
+                *reinterpret_cast<uint2 *>(rp + 16 * c16) = make_uint2(raw[k].x, raw[k].y);
+                *reinterpret_cast<uint2 *>(rp + 16 * c16 + 8) = make_uint2(raw[k].z, raw[k].w);
+            } else if (c16 == 13) {
+                *reinterpret_cast<uint16_t *>(rp + 208) = dd[k];
+            }
+        }
+        __builtin_amdgcn_wave_barrier(); // LDS accesses of one wavefront complete in order
+        const uint8_t *bp = mine + j * kRowStride;
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
-                b.ql[h][0][p] = ld8(bp + 64 * h + 16 * p + 8 * kh);
-                b.ql[h][1][p] = ld8(bp + 64 * h + 32 + 16 * p + 8 * kh);
-                b.qh[h][p] = ld8(bp + 128 + 32 * h + 16 * p + 8 * kh);
+                b.ql[h][0][p] = *reinterpret_cast<const uint2 *>(bp + 64 * h + 16 * p + 8 * kh);
+                b.ql[h][1][p] = *reinterpret_cast<const uint2 *>(bp + 64 * h + 32 + 16 * p + 8 * kh);
+                b.qh[h][p] = *reinterpret_cast<const uint2 *>(bp + 128 + 32 * h + 16 * p + 8 * kh);
             }
-        b.sc = ld16(bp + 192);
-        b.d = ld2(bp + 208);
+        const uint2 s0 = *reinterpret_cast<const uint2 *>(bp + 192), s1 = *reinterpret_cast<const uint2 *>(bp + 200);
+        b.sc = make_uint4(s0.x, s0.y, s1.x, s1.y);
+        b.d = *reinterpret_cast<const uint16_t *>(bp + 208);
         const uint8_t *ap = a.xa + (size_t)cb * 16 * kSbBytes + (size_t)(kh * 24 + (live ? j : 0)) * 8;
 #pragma unroll
         for (int sb = 0; sb < 16; ++sb) b.av[sb] = live ? *reinterpret_cast<const long *>(ap + sb * kSbBytes) : 0;
@@ -317,7 +347,7 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 2) void qmv_mfma_kernel(MfmaArgs
         if (sb + 1 < 16) cur = next;
     }
 
-    // The eight wavefronts' sums meet in LDS in a fixed order.
+    // The four wavefronts' sums meet in LDS in a fixed order.
 #pragma unroll
     for (int r = 0; r < 4; ++r) red[w][4 * kh + r][j] = acc[r];
     __syncthreads();
