@@ -58,9 +58,19 @@ struct AttnArgs {
     float *xs;              //           and their scales (token = client)
 };
 
-// A value of q|k|v: the sum of its partial-sum slices, in slice order.
+// A value of q|k|v: the sum of its partial-sum slices, in slice order.  Up
+// to four slices, every load goes out before the first add.
 __device__ __forceinline__ float qkv_at(const float *p, int ns, size_t stride)
 {
+    if (ns <= 4) {
+        float q[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) q[s] = p[(s < ns ? s : 0) * stride];
+        float v = q[0];
+#pragma unroll
+        for (int s = 1; s < 4; ++s) v = s < ns ? v + q[s] : v;
+        return v;
+    }
     float v = p[0];
     for (int s = 1; s < ns; ++s) v += p[s * stride];
     return v;

@@ -77,10 +77,32 @@ struct LinkArgs {
 // A-operand layout: sub-block sb, half kh (columns 8kh..8kh+7 of the
 // sub-block), limb, token -> 8 bytes at xa + sb*kSbBytes + (kh*24 + 8*limb + token)*8.
 // Thread pair (2m, 2m+1) holds the two 8-column halves of one sub-block;
-// a thread owns up to kLinkPairs such 8-column pieces.
+// a thread owns up to kLinkPairs such 8-column pieces.  With an RMS norm one
+// workgroup covers a token's row (the norm needs its sum of squares);
+// without one, gridDim.y workgroups share it.
+constexpr int kMaxSlices = 12; // input columns / slice width, at most
+
+// Sum of n (<= MAXS) slices' 8 partial sums, in slice order, with every
+// load issued before the first add (slices past n read slice 0 and are
+// dropped), so the sum costs one memory round trip.
+template <int MAXS>
+__device__ __forceinline__ void slice_sum(const float *p, size_t stride, int n, float (&v)[8])
+{
+    float q[MAXS][8];
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) ld8f(p + (s < n ? s : 0) * stride, q[s]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = q[0][e];
+#pragma unroll
+    for (int s = 1; s < MAXS; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = s < n ? v[e] + q[s][e] : v[e];
+}
+
 constexpr int kLinkThreads = 512;
 constexpr int kLinkPairs = 3; // columns per token up to 8 * kLinkThreads * kLinkPairs = 12288
 
+template <int MAXS>
 __global__ __launch_bounds__(kLinkThreads) void mfma_link_kernel(LinkArgs a)
 {
     const int t = blockIdx.x, tid = threadIdx.x;
@@ -91,13 +113,13 @@ __global__ __launch_bounds__(kLinkThreads) void mfma_link_kernel(LinkArgs a)
     if (a.gain && a.xa) {
 #pragma unroll
         for (int k = 0; k < kLinkPairs; ++k) {
-            const int p = tid + k * kLinkThreads;
+            const int p = (blockIdx.y + k * gridDim.y) * kLinkThreads + tid;
             if (p < npairs) ld8f(a.gain + 8 * p, gn[k]);
         }
     }
 #pragma unroll
     for (int k = 0; k < kLinkPairs; ++k) {
-        const int p = tid + k * kLinkThreads;
+        const int p = (blockIdx.y + k * gridDim.y) * kLinkThreads + tid;
         if (p >= npairs) break;
         const int c0 = 8 * p;
         if (a.mode == kLinkInput) {
@@ -106,23 +128,11 @@ __global__ __launch_bounds__(kLinkThreads) void mfma_link_kernel(LinkArgs a)
             // Slices added in slice order (the finishing pass's order).
             const size_t stride = (size_t)a.nmat * kMaxTok * a.cols;
             const float *pp = a.part + (size_t)t * a.cols + c0;
-            ld8f(pp, v[k]);
-            for (int ks = 1; ks < a.nks; ++ks) {
-                float q[8];
-                ld8f(pp + ks * stride, q);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[k][e] += q[e];
-            }
+            slice_sum<MAXS>(pp, stride, a.nks, v[k]);
             if (a.mode == kLinkSwiglu) {
                 const float *pu = pp + (size_t)kMaxTok * a.cols;
                 float u[8];
-                ld8f(pu, u);
-                for (int ks = 1; ks < a.nks; ++ks) {
-                    float q[8];
-                    ld8f(pu + ks * stride, q);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) u[e] += q[e];
-                }
+                slice_sum<MAXS>(pu, stride, a.nks, u);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[k][e] = (v[k][e] / (1.0f + expf(-v[k][e]))) * u[e];
             }
@@ -155,7 +165,7 @@ __global__ __launch_bounds__(kLinkThreads) void mfma_link_kernel(LinkArgs a)
     }
 #pragma unroll
     for (int k = 0; k < kLinkPairs; ++k) {
-        const int p = tid + k * kLinkThreads;
+        const int p = (blockIdx.y + k * gridDim.y) * kLinkThreads + tid;
         if (p >= npairs) break; // pairs (2m, 2m+1) stop together: npairs is even
         const int sb = p >> 1, kh = p & 1;
         float w[8];
@@ -480,6 +490,7 @@ bool emu_mfma_supports(int encoding, int cols, int n_tok)
 {
     if (mfma_disabled()) return false;
     return encoding == EMU_ENC_Q6_K && n_tok >= 2 && n_tok <= kMaxTok && cols > 0 && cols % kSlice == 0 &&
+           cols / kSlice <= kMaxSlices &&
            cols <= 8 * kLinkThreads * kLinkPairs;
 }
 
@@ -505,7 +516,12 @@ int emu_mfma_link(emu_ctx *ctx, const EmuMfmaLink &l)
     a.xs = l.limbs ? w.xs : nullptr;
     if (l.from_part && (size_t)a.nks * a.nmat * kMaxTok * (size_t)l.cols * sizeof(float) > w.part_bytes)
         return EMU_E_CONFIG;
-    hipLaunchKernelGGL(mfma_link_kernel, dim3(l.n_tok), dim3(kLinkThreads), 0, ctx->stream, a);
+    // Without a norm there is no row-wide sum: one workgroup per 4096 columns.
+    const int gy = a.gain ? 1 : (l.cols / 8 + kLinkThreads - 1) / kLinkThreads;
+    if (a.nks <= 4)
+        hipLaunchKernelGGL(mfma_link_kernel<4>, dim3(l.n_tok, gy), dim3(kLinkThreads), 0, ctx->stream, a);
+    else
+        hipLaunchKernelGGL(mfma_link_kernel<kMaxSlices>, dim3(l.n_tok, gy), dim3(kLinkThreads), 0, ctx->stream, a);
     EMU_LAUNCH_CHECK(ctx);
     return EMU_OK;
 }
