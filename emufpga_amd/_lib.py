@@ -32,6 +32,7 @@ EMU_ROPE_NEOX = 0
 EMU_ROPE_INTERLEAVED = 1
 EMU_STYLE_QWEN3 = 0
 EMU_STYLE_SMOL = 1
+EMU_STYLE_GRANITE = 2
 (EMU_T_LAYER, EMU_T_EMBED, EMU_T_OUTPUT, EMU_T_ATTN_NORM, EMU_T_FFN_NORM, EMU_T_Q_NORM,
  EMU_T_K_NORM, EMU_T_OUT_NORM) = range(8)
 
@@ -122,7 +123,9 @@ class ModelConfig(C.Structure):
         ("head_dim", C.c_uint32), ("ffn", C.c_uint32), ("vocab", C.c_uint32),
         ("layers", C.c_uint32), ("rope_theta", C.c_float), ("eps", C.c_float),
         ("style", C.c_int32), ("encoding", C.c_int32), ("tied", C.c_int32),
-        ("qk_norm", C.c_int32),
+        ("qk_norm", C.c_int32), ("n_experts", C.c_uint32), ("experts_used", C.c_uint32),
+        ("expert_ff", C.c_uint32), ("expert_encoding", C.c_int32), ("embed_scale", C.c_float),
+        ("residual_scale", C.c_float), ("logit_div", C.c_float), ("score_mul", C.c_float),
     ]
 
 

@@ -351,7 +351,18 @@ struct QmvArgs {
     uint64_t *keys;        // optional greedy-selection keys: keys[t * key_stride + wave]
     int key_stride;
     int tie_last;
+    float acc_scale;       // accumulate as y + v * acc_scale (0: y + v)
+    float out_div;         // results divided by this before store and keys (0: none)
 };
+
+// A matvec result's epilogue: divided by out_div (when set), then added to
+// the residual as r + v * s with two roundings (the reference's add_scaled,
+// spm-granite-moe/src/math.rs:31-33), or r + v when s is 0.
+__device__ __forceinline__ float emu_out_div(float v, float d) { return d != 0.0f ? v / d : v; }
+__device__ __forceinline__ float emu_resid_add(float r, float v, float s)
+{
+    return s != 0.0f ? r + __fmul_rn(v, s) : r + v;
+}
 
 // Launch a quantized matvec; *key_slots (optional) receives how many key
 // slots per token the launch writes when a.keys is set.

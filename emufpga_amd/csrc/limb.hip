@@ -281,8 +281,9 @@ __global__ __launch_bounds__(EMU_WAVE * LimbShape<S>::W) void qmv_limb_kernel(Qm
     auto finish = [&](int row, const float (&p)[NR], float resid) {
         float val = p[0];
         if (DUAL) val = (val / (1.0f + expf(-val))) * p[1];
+        val = emu_out_div(val, a.out_div);
         if (row < a.rows) {
-            a.y[row] = ACC ? resid + val : val;
+            a.y[row] = ACC ? emu_resid_add(resid, val, a.acc_scale) : val;
             if (a.keys) {
                 const uint64_t key = emu_select_key(val, (uint32_t)row, a.tie_last);
                 best = key > best ? key : best;

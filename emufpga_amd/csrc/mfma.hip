@@ -377,6 +377,7 @@ struct FinishArgs {
     int nks, nmat, rows;
     float *y; // n_tok x rows
     int accumulate;
+    float acc_scale, out_div;
     uint64_t *keys;
     int key_stride, tie_last;
 };
@@ -397,8 +398,9 @@ __global__ __launch_bounds__(kFinishThreads) void mfma_finish_kernel(FinishArgs 
             for (int k = 1; k < a.nks; ++k) up += pu[k * stride];
             v = (v / (1.0f + expf(-v))) * up;
         }
+        v = emu_out_div(v, a.out_div);
         float *dst = a.y + (size_t)t * a.rows + row;
-        *dst = a.accumulate ? *dst + v : v;
+        *dst = a.accumulate ? emu_resid_add(*dst, v, a.acc_scale) : v;
     }
     if (a.keys) {
         __shared__ uint64_t best[kFinishThreads / EMU_WAVE];
@@ -564,6 +566,8 @@ int emu_mfma_finish(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int
     fa.rows = q.rows;
     fa.y = q.y;
     fa.accumulate = q.accumulate;
+    fa.acc_scale = q.acc_scale;
+    fa.out_div = q.out_div;
     fa.keys = q.keys;
     fa.key_stride = q.key_stride;
     fa.tie_last = q.tie_last;

@@ -46,6 +46,10 @@ struct emu_model {
     size_t off_layers = 0, off_embed = 0, off_output = 0, off_attn_norm = 0, off_ffn_norm = 0,
            off_q_norm = 0, off_k_norm = 0, off_out_norm = 0;
     size_t embed_bytes = 0;
+    // Mixture-of-experts layers: router (f32) and gate/up/down experts,
+    // expert-major (spm-granite-moe/src/weights.rs:57-73), after q, k, v, o.
+    size_t off_r = 0, off_ge = 0, off_ue = 0, off_de = 0, rb_he = 0, rb_fe = 0;
+    bool moe() const { return cfg.style == EMU_STYLE_GRANITE; }
 };
 
 struct emu_session {
@@ -60,6 +64,12 @@ struct emu_session {
     uint32_t key_stride = 0;
     float *state = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits = nullptr,
           *partial = nullptr, *rope = nullptr;
+    // mixture-of-experts scratch: normalised input, router logits, routes,
+    // expert output, and the selected-expert FFN's workspace
+    float *xn = nullptr, *rlog = nullptr, *rwts = nullptr, *moe_out = nullptr;
+    int32_t *rids = nullptr;
+    void *moe_ws = nullptr;
+    size_t moe_ws_bytes = 0;
     std::vector<uint32_t> host_pos;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -249,11 +259,45 @@ int synth_tensor(emu_ctx *ctx, int enc, uint8_t *dst, size_t bytes, uint64_t see
     return EMU_OK;
 }
 
+__global__ __launch_bounds__(kThreads) void synth_f32_kernel(float *dst, size_t n, uint64_t seed, uint64_t stream,
+                                                             float sd)
+{
+    const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) dst[i] = gauss(seed, stream, i, sd);
+}
+
 // --------------------------------------------------------- step kernels --
+// Router logits of every client (spm-granite-moe/src/moe.rs:132-138, an M1
+// matvec of the f32 router): one wavefront per (expert, client).
+__global__ __launch_bounds__(EMU_WAVE) void router_kernel(const float *w, const float *x, int width, int experts,
+                                                           float *logits)
+{
+    const int e = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
+    const float *row = w + (size_t)e * width;
+    const float *xc = x + (size_t)c * width;
+    float acc = 0.0f;
+    for (int i = 4 * lane; i < width; i += 4 * EMU_WAVE) {
+        const float4 a = *reinterpret_cast<const float4 *>(row + i);
+        const float4 b = *reinterpret_cast<const float4 *>(xc + i);
+        acc = __builtin_fmaf(a.x, b.x, acc);
+        acc = __builtin_fmaf(a.y, b.y, acc);
+        acc = __builtin_fmaf(a.z, b.z, acc);
+        acc = __builtin_fmaf(a.w, b.w, acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) logits[(size_t)c * experts + e] = acc;
+}
+
+// state += v * s with two roundings (add_scaled, spm-granite-moe/src/math.rs:31-33).
+__global__ __launch_bounds__(kThreads) void add_scaled_kernel(float *state, const float *v, size_t n, float s)
+{
+    const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) state[i] = emu_resid_add(state[i], v[i], s);
+}
 // Embedding row of tokens[c]: a unit-per-thread decode of one row.
 template <class F>
 __global__ __launch_bounds__(kThreads) void embed_kernel(const uint8_t *embed, size_t row_bytes, int hidden,
-                                                         const uint32_t *tokens, float *state)
+                                                         const uint32_t *tokens, float *state, float scale)
 {
     const int c = blockIdx.y;
     const int u = blockIdx.x * kThreads + threadIdx.x;
@@ -268,7 +312,10 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const uint8_t *embed, s
     for (int g = 0; g < F::G; ++g) {
         const Grp gp = F::group(raw, sub, g);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) out[F::col(sub, g) + i] = grp_weight_exact<F::BIAS>(gp, i);
+        for (int i = 0; i < 8; ++i) {
+            const float v = grp_weight_exact<F::BIAS>(gp, i);
+            out[F::col(sub, g) + i] = scale != 0.0f ? v * scale : v; // model.rs:196-213: value * 12.0
+        }
     }
 }
 
@@ -321,7 +368,7 @@ int launch_embed(emu_ctx *ctx, const emu_model *m, const uint32_t *tokens, float
     const int units = (int)(m->cfg.hidden / F::BE * F::UPB);
     dim3 grid((units + kThreads - 1) / kThreads, n);
     hipLaunchKernelGGL(embed_kernel<F>, grid, dim3(kThreads), 0, ctx->stream, m->base + m->off_embed,
-                       m->rb_h, (int)m->cfg.hidden, tokens, state);
+                       m->rb_h, (int)m->cfg.hidden, tokens, state, m->cfg.embed_scale);
     EMU_LAUNCH_CHECK(ctx);
     return EMU_OK;
 }
@@ -345,6 +392,11 @@ EmuAttnLaunch layer_attn(emu_session *s, uint32_t layer)
     al.score_div = smol ? 0.0f : sqrtf((float)hd);
     al.rope_fma = smol;
     al.interleaved = 0;
+    if (m->moe()) { // spm-granite-moe/src/attention.rs:12-26, 40-46
+        al.score_mul = c.score_mul != 0.0f ? c.score_mul : 1.0f / sqrtf((float)hd);
+        al.score_div = 0.0f;
+        al.interleaved = 1;
+    }
     al.heads = (int)c.heads;
     al.kv_heads = (int)c.kv_heads;
     al.head_dim = (int)hd;
@@ -377,7 +429,7 @@ bool mfma_chain(const emu_model *m, uint32_t n)
 {
     const emu_model_config &c = m->cfg;
     const int QW = (int)(c.heads * c.head_dim), KW = (int)(c.kv_heads * c.head_dim);
-    return n >= 2 && emu_mfma_supports(c.encoding, (int)c.hidden, (int)n) &&
+    return !m->moe() && n >= 2 && emu_mfma_supports(c.encoding, (int)c.hidden, (int)n) &&
            emu_mfma_supports(c.encoding, QW, (int)n) && emu_mfma_supports(c.encoding, (int)c.ffn, (int)n) &&
            (QW + 2 * KW) % 16 == 0 && (QW + 2 * KW) <= (int)c.ffn;
 }
@@ -484,6 +536,94 @@ int run_chain(emu_session *s)
     return launch_finalize(s, slots);
 }
 
+// The layers, output matvec and selection of a mixture-of-experts step
+// (spm-granite-moe/src/model.rs:330-411): attention as in the dense step but
+// with adjacent-pair RoPE and score * score_mul, residual adds r + v * 0.22,
+// then per layer RMSNorm, the f32 router, top-k routing and the selected
+// experts, and logits from the tied embedding divided by logit_div.
+int run_moe(emu_session *s)
+{
+    emu_model *m = s->m;
+    emu_ctx *ctx = m->ctx;
+    const emu_model_config &c = m->cfg;
+    const uint32_t H = c.hidden, QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim;
+    const uint32_t E = c.n_experts, K = c.experts_used;
+    const int n = (int)s->n;
+    uint32_t be = 0, bb = 0;
+    emu_block_layout(c.encoding, &be, &bb);
+    const float *attn_norm = reinterpret_cast<const float *>(m->base + m->off_attn_norm);
+    const float *ffn_norm = reinterpret_cast<const float *>(m->base + m->off_ffn_norm);
+    int st = EMU_OK;
+    for (uint32_t layer = 0; layer < c.layers; ++layer) {
+        const uint8_t *lw = m->base + m->off_layers + (size_t)layer * m->layer_bytes;
+        QmvArgs a{};
+        a.w = lw + m->off_q;
+        a.row_bytes = m->rb_h;
+        a.rows = (int)(QW + 2 * KW);
+        a.cols = (int)H;
+        a.nb = (int)(H / be);
+        a.x = s->state;
+        a.gain = attn_norm + (size_t)layer * H;
+        a.eps = c.eps;
+        a.y = s->qkv;
+        if ((st = emu_launch_qmv(ctx, c.encoding, a, n)) != EMU_OK) return st;
+        if ((st = emu_launch_attn(ctx, layer_attn(s, layer))) != EMU_OK) return st;
+        QmvArgs o{};
+        o.w = lw + m->off_o;
+        o.row_bytes = m->rb_q;
+        o.rows = (int)H;
+        o.cols = (int)QW;
+        o.nb = (int)(QW / be);
+        o.x = s->attn;
+        o.y = s->state;
+        o.accumulate = 1;
+        o.acc_scale = c.residual_scale;
+        if ((st = emu_launch_qmv(ctx, c.encoding, o, n)) != EMU_OK) return st;
+        if ((st = emu_rms_norm(ctx, s->state, ffn_norm + (size_t)layer * H, (uint32_t)n, H, c.eps, s->xn)) != EMU_OK)
+            return st;
+        hipLaunchKernelGGL(router_kernel, dim3(E, (unsigned)n), dim3(EMU_WAVE), 0, ctx->stream,
+                           reinterpret_cast<const float *>(lw + m->off_r), s->xn, (int)H, (int)E, s->rlog);
+        EMU_LAUNCH_CHECK(ctx);
+        if ((st = emu_route(ctx, s->rlog, (uint32_t)n, E, K, s->rids, s->rwts)) != EMU_OK) return st;
+        emu_moe_desc d{};
+        d.enc_gate_up = c.expert_encoding;
+        d.enc_down = c.expert_encoding;
+        d.d_gate = lw + m->off_ge;
+        d.d_up = lw + m->off_ue;
+        d.d_down = lw + m->off_de;
+        d.d_down_scale = nullptr;
+        d.n_experts = E;
+        d.width = H;
+        d.ff = c.expert_ff;
+        d.k = K;
+        d.act = EMU_ACT_SILU;
+        if ((st = emu_moe_ffn(ctx, &d, s->xn, (uint32_t)n, s->rids, s->rwts, s->moe_ws, s->moe_ws_bytes,
+                              s->moe_out)) != EMU_OK)
+            return st;
+        const size_t tot = (size_t)n * H;
+        hipLaunchKernelGGL(add_scaled_kernel, dim3((unsigned)((tot + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                           ctx->stream, s->state, s->moe_out, tot, c.residual_scale);
+        EMU_LAUNCH_CHECK(ctx);
+    }
+    QmvArgs out{};
+    out.w = m->base + m->off_embed; // tied (model.rs:403-407)
+    out.row_bytes = m->rb_h;
+    out.rows = (int)c.vocab;
+    out.cols = (int)H;
+    out.nb = (int)(H / be);
+    out.x = s->state;
+    out.gain = reinterpret_cast<const float *>(m->base + m->off_out_norm);
+    out.eps = c.eps;
+    out.y = s->logits;
+    out.keys = s->keys;
+    out.key_stride = (int)s->key_stride;
+    out.tie_last = 0; // top_k: ties to the lowest index (math.rs:35-40)
+    out.out_div = c.logit_div;
+    int slots = 0;
+    if ((st = emu_launch_qmv(ctx, c.encoding, out, n, &slots)) != EMU_OK) return st;
+    return launch_finalize(s, slots);
+}
+
 int run_step(emu_session *s)
 {
     emu_model *m = s->m;
@@ -500,6 +640,7 @@ int run_step(emu_session *s)
     default: return EMU_E_UNSUPPORTED;
     }
     if (st != EMU_OK) return st;
+    if (m->moe()) return run_moe(s);
     if (mfma_chain(m, s->n)) return run_chain(s);
     uint32_t be = 0, bb = 0;
     emu_block_layout(c.encoding, &be, &bb);
@@ -646,12 +787,20 @@ extern "C" int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_m
     if (!ctx || !cfg || !out) return EMU_E_ARG;
     *out = nullptr;
     const emu_model_config &c = *cfg;
-    if (c.hidden == 0 || c.heads == 0 || c.kv_heads == 0 || c.head_dim == 0 || c.ffn == 0 || c.vocab == 0 ||
-        c.layers == 0)
+    const bool moe = c.style == EMU_STYLE_GRANITE;
+    if (c.hidden == 0 || c.heads == 0 || c.kv_heads == 0 || c.head_dim == 0 || (c.ffn == 0 && !moe) ||
+        c.vocab == 0 || c.layers == 0)
+        return EMU_E_CONFIG;
+    // MoE: routes of up to 8 experts per token for up to 8 clients (the
+    // selected-expert FFN's limits), the router's rows float4-loadable, the
+    // output tied to the embedding (model.rs:403-407).
+    if (moe && (c.n_experts == 0 || c.experts_used == 0 || c.experts_used > c.n_experts || c.experts_used > 8 ||
+                c.n_experts > 64 || c.expert_ff == 0 || c.hidden % 4 != 0 || !c.tied))
         return EMU_E_CONFIG;
     if (c.heads % c.kv_heads != 0 || c.heads / c.kv_heads > 8) return EMU_E_CONFIG;
     if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256) return EMU_E_CONFIG;
-    if (c.style != EMU_STYLE_QWEN3 && c.style != EMU_STYLE_SMOL) return EMU_E_CONFIG;
+    if (c.style != EMU_STYLE_QWEN3 && c.style != EMU_STYLE_SMOL && c.style != EMU_STYLE_GRANITE)
+        return EMU_E_CONFIG;
     emu_model *m = new (std::nothrow) emu_model();
     if (!m) return EMU_E_NOMEM;
     m->ctx = ctx;
@@ -660,7 +809,9 @@ extern "C" int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_m
     int st;
     if ((st = emu_row_bytes(c.encoding, c.hidden, &m->rb_h)) != EMU_OK ||
         (st = emu_row_bytes(c.encoding, QW, &m->rb_q)) != EMU_OK ||
-        (st = emu_row_bytes(c.encoding, c.ffn, &m->rb_f)) != EMU_OK) {
+        (!moe && (st = emu_row_bytes(c.encoding, c.ffn, &m->rb_f)) != EMU_OK) ||
+        (moe && (st = emu_row_bytes(c.expert_encoding, c.hidden, &m->rb_he)) != EMU_OK) ||
+        (moe && (st = emu_row_bytes(c.expert_encoding, c.expert_ff, &m->rb_fe)) != EMU_OK)) {
         delete m;
         return st == EMU_E_SHORT ? EMU_E_CONFIG : st;
     }
@@ -668,10 +819,18 @@ extern "C" int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_m
     m->off_k = m->off_q + (size_t)QW * m->rb_h;
     m->off_v = m->off_k + (size_t)KW * m->rb_h;
     m->off_o = m->off_v + (size_t)KW * m->rb_h;
-    m->off_g = m->off_o + (size_t)c.hidden * m->rb_q;
-    m->off_u = m->off_g + (size_t)c.ffn * m->rb_h;
-    m->off_d = m->off_u + (size_t)c.ffn * m->rb_h;
-    m->layer_bytes = m->off_d + (size_t)c.hidden * m->rb_f;
+    if (moe) {
+        m->off_r = align_up(m->off_o + (size_t)c.hidden * m->rb_q, 16);
+        m->off_ge = m->off_r + sizeof(float) * c.n_experts * c.hidden;
+        m->off_ue = m->off_ge + (size_t)c.n_experts * c.expert_ff * m->rb_he;
+        m->off_de = m->off_ue + (size_t)c.n_experts * c.expert_ff * m->rb_he;
+        m->layer_bytes = align_up(m->off_de + (size_t)c.n_experts * c.hidden * m->rb_fe, 16);
+    } else {
+        m->off_g = m->off_o + (size_t)c.hidden * m->rb_q;
+        m->off_u = m->off_g + (size_t)c.ffn * m->rb_h;
+        m->off_d = m->off_u + (size_t)c.ffn * m->rb_h;
+        m->layer_bytes = m->off_d + (size_t)c.hidden * m->rb_f;
+    }
     m->embed_bytes = (size_t)c.vocab * m->rb_h;
     size_t off = 0;
     m->off_layers = off;
@@ -742,6 +901,25 @@ extern "C" int emu_model_synth(emu_model *m, uint64_t seed)
     int st;
     for (uint32_t l = 0; l < c.layers; ++l) {
         uint8_t *lw = m->base + m->off_layers + (size_t)l * m->layer_bytes;
+        if (m->moe()) {
+            const size_t sz[6] = {(size_t)QW * m->rb_h, (size_t)KW * m->rb_h, (size_t)KW * m->rb_h,
+                                  (size_t)c.hidden * m->rb_q, 0, 0};
+            const size_t of[4] = {m->off_q, m->off_k, m->off_v, m->off_o};
+            for (int t = 0; t < 4; ++t)
+                if ((st = synth_tensor(ctx, c.encoding, lw + of[t], sz[t], seed, 16ull * (l + 1) + t)) != EMU_OK)
+                    return st;
+            const size_t nr = (size_t)c.n_experts * c.hidden;
+            hipLaunchKernelGGL(synth_f32_kernel, dim3((unsigned)((nr + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                               ctx->stream, reinterpret_cast<float *>(lw + m->off_r), nr, seed, 16ull * (l + 1) + 4,
+                               0.02f);
+            EMU_LAUNCH_CHECK(ctx);
+            const size_t ge = (size_t)c.n_experts * c.expert_ff * m->rb_he, de = (size_t)c.n_experts * c.hidden * m->rb_fe;
+            if ((st = synth_tensor(ctx, c.expert_encoding, lw + m->off_ge, ge, seed, 16ull * (l + 1) + 5)) != EMU_OK ||
+                (st = synth_tensor(ctx, c.expert_encoding, lw + m->off_ue, ge, seed, 16ull * (l + 1) + 6)) != EMU_OK ||
+                (st = synth_tensor(ctx, c.expert_encoding, lw + m->off_de, de, seed, 16ull * (l + 1) + 7)) != EMU_OK)
+                return st;
+            continue;
+        }
         const size_t sizes[7] = {(size_t)QW * m->rb_h, (size_t)KW * m->rb_h, (size_t)KW * m->rb_h,
                                  (size_t)c.hidden * m->rb_q, (size_t)c.ffn * m->rb_h, (size_t)c.ffn * m->rb_h,
                                  (size_t)c.hidden * m->rb_f};
@@ -764,6 +942,13 @@ extern "C" int emu_model_synth(emu_model *m, uint64_t seed)
 extern "C" int emu_model_weight_bytes(const emu_model *m, uint64_t *bytes)
 {
     if (!m || !bytes) return EMU_E_ARG;
+    const emu_model_config &c = m->cfg;
+    if (m->moe()) {
+        // attention + router + the experts one token routes to, per layer
+        const uint64_t per_expert = (uint64_t)2 * c.expert_ff * m->rb_he + (uint64_t)c.hidden * m->rb_fe;
+        *bytes = ((uint64_t)m->off_ge + (uint64_t)c.experts_used * per_expert) * c.layers + m->embed_bytes;
+        return EMU_OK;
+    }
     *bytes = (uint64_t)m->layer_bytes * m->cfg.layers + m->embed_bytes;
     return EMU_OK;
 }
@@ -803,7 +988,16 @@ extern "C" int emu_session_create(emu_model *m, uint32_t n_clients, uint32_t con
     alloc((void **)&s->state, sizeof(float) * n_clients * c.hidden);
     alloc((void **)&s->qkv, sizeof(float) * n_clients * (QW + 2 * KW));
     alloc((void **)&s->attn, sizeof(float) * n_clients * QW);
-    alloc((void **)&s->act, sizeof(float) * n_clients * c.ffn);
+    alloc((void **)&s->act, sizeof(float) * n_clients * (c.ffn ? c.ffn : 1));
+    if (m->moe()) {
+        alloc((void **)&s->xn, sizeof(float) * n_clients * c.hidden);
+        alloc((void **)&s->rlog, sizeof(float) * n_clients * c.n_experts);
+        alloc((void **)&s->rids, sizeof(int32_t) * n_clients * c.experts_used);
+        alloc((void **)&s->rwts, sizeof(float) * n_clients * c.experts_used);
+        alloc((void **)&s->moe_out, sizeof(float) * n_clients * c.hidden);
+        s->moe_ws_bytes = emu_moe_workspace_bytes(n_clients, c.experts_used, c.hidden, c.expert_ff);
+        alloc(&s->moe_ws, s->moe_ws_bytes);
+    }
     alloc((void **)&s->logits, sizeof(float) * n_clients * c.vocab);
     s->key_stride = c.vocab + 8; // >= key slots of any output-matvec launch shape
     alloc((void **)&s->keys, sizeof(uint64_t) * n_clients * s->key_stride);
@@ -848,7 +1042,7 @@ extern "C" int emu_session_destroy(emu_session *s)
     if (s->graph) (void)hipGraphDestroy(s->graph);
     void *ptrs[] = {s->k_cache, s->v_cache, s->positions, s->tokens, s->steps, s->last, s->prompt, s->hist,
                     s->ctrl, s->counters, s->state, s->qkv, s->attn, s->act, s->logits, s->keys, s->partial,
-                    s->rope};
+                    s->rope, s->xn, s->rlog, s->rids, s->rwts, s->moe_out, s->moe_ws};
     for (void *p : ptrs) emu_free(ctx, p);
     delete s;
     return EMU_OK;

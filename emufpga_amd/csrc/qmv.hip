@@ -113,6 +113,12 @@ __global__ __launch_bounds__(kThreads) void qmv_kernel(QmvArgs a)
     for (int k = 0; k < NR; ++k)
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[k][t] = wave_sum(acc[k][t]) * scale[t];
+    if (!DUAL) {
+#pragma unroll
+        for (int k = 0; k < NR; ++k)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[k][t] = emu_out_div(acc[k][t], a.out_div);
+    }
 
     if (!DUAL && a.keys && lane == 0) {
 #pragma unroll
@@ -141,7 +147,8 @@ __global__ __launch_bounds__(kThreads) void qmv_kernel(QmvArgs a)
                     v = (gte / (1.0f + expf(-gte))) * up;
                 }
                 float *dst = a.y + (size_t)t * a.rows + row;
-                *dst = a.accumulate ? *dst + v : v;
+                if (DUAL) v = emu_out_div(v, a.out_div);
+                *dst = a.accumulate ? emu_resid_add(*dst, v, a.acc_scale) : v;
             }
         }
     }
@@ -311,8 +318,9 @@ __global__ __launch_bounds__(kThreads) void qmv_pipe_kernel(QmvArgs a, int total
                 const int row = rg * R + k;
                 float val = v[k];
                 if (DUAL) val = (val / (1.0f + expf(-val))) * v[k + R];
+                val = emu_out_div(val, a.out_div);
                 if (row < a.rows) {
-                    if (lane == k) a.y[row] = a.accumulate ? resid + val : val;
+                    if (lane == k) a.y[row] = a.accumulate ? emu_resid_add(resid, val, a.acc_scale) : val;
                     if (a.keys) {
                         const uint64_t key = emu_select_key(val, (uint32_t)row, a.tie_last);
                         best = key > best ? key : best;

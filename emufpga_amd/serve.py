@@ -15,7 +15,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from ._lib import (EMU_STYLE_QWEN3, EMU_STYLE_SMOL, EMU_T_ATTN_NORM, EMU_T_EMBED, EMU_T_FFN_NORM,
+from ._lib import (EMU_STYLE_GRANITE, EMU_STYLE_QWEN3, EMU_STYLE_SMOL, EMU_T_ATTN_NORM, EMU_T_EMBED, EMU_T_FFN_NORM,
                    EMU_T_K_NORM, EMU_T_LAYER, EMU_T_OUT_NORM, EMU_T_OUTPUT, EMU_T_Q_NORM, Q6_K, Q8_0,
                    ModelConfig)
 from .device import Context
@@ -36,11 +36,22 @@ class DenseConfig:
     encoding: int
     tied: bool
     qk_norm: bool
+    # mixture-of-experts layers (EMU_STYLE_GRANITE); zero keeps the dense forms
+    n_experts: int = 0
+    experts_used: int = 0
+    expert_ff: int = 0
+    expert_encoding: int = 0
+    embed_scale: float = 0.0
+    residual_scale: float = 0.0
+    logit_div: float = 0.0
+    score_mul: float = 0.0
 
     def native(self) -> ModelConfig:
         return ModelConfig(self.hidden, self.heads, self.kv_heads, self.head_dim, self.ffn, self.vocab,
                            self.layers, self.rope_theta, self.eps, self.style, self.encoding,
-                           int(self.tied), int(self.qk_norm))
+                           int(self.tied), int(self.qk_norm), self.n_experts, self.experts_used, self.expert_ff,
+                           self.expert_encoding, self.embed_scale, self.residual_scale, self.logit_div,
+                           self.score_mul)
 
     @property
     def q_width(self) -> int:
@@ -55,6 +66,12 @@ class DenseConfig:
 QWEN3_8B_Q6K = DenseConfig(4096, 32, 8, 128, 12288, 151936, 36, 1e6, 1e-6, EMU_STYLE_QWEN3, Q6_K, False, True)
 # SmolLM2-135M shape (spm-smol/src/config.rs:24-45), linears + tied embedding in Q8_0
 SMOLLM2_135M_Q8 = DenseConfig(576, 9, 3, 64, 1536, 49152, 30, 1e5, 1e-5, EMU_STYLE_SMOL, Q8_0, True, False)
+# Granite MoE shape (spm-granite-moe/src/model.rs:16-17, attention.rs:8-10, shape.rs:16-21): 24 layers of
+# width 1024, 16/8 heads of 64, 32 Q6_K SwiGLU experts of width 512 with 8 routed, f32 router,
+# tied 49155-row output; x12 embeddings, x0.22 residuals, logits / 6, scores x 1/64, theta 1.5e6.
+GRANITE_MOE_Q6K = DenseConfig(1024, 16, 8, 64, 0, 49155, 24, 1.5e6, 1e-6, EMU_STYLE_GRANITE, Q6_K, True, False,
+                              n_experts=32, experts_used=8, expert_ff=512, expert_encoding=Q6_K, embed_scale=12.0,
+                              residual_scale=0.22, logit_div=6.0, score_mul=0.015625)
 
 
 class Model:
@@ -188,4 +205,4 @@ class Session:
         return out.reshape(positions, -1)
 
 
-__all__ = ["DenseConfig", "Model", "Session", "QWEN3_8B_Q6K", "SMOLLM2_135M_Q8", "_lib"]
+__all__ = ["DenseConfig", "Model", "Session", "QWEN3_8B_Q6K", "SMOLLM2_135M_Q8", "GRANITE_MOE_Q6K", "_lib"]

@@ -211,7 +211,7 @@ int emu_argmax(emu_ctx *ctx, const float *d_x, uint32_t n_rows, uint32_t width, 
                int32_t *d_out);
 
 /* ---- dense decoder model and decode step (serve API) -------------------- */
-enum { EMU_STYLE_QWEN3 = 0, EMU_STYLE_SMOL = 1 };
+enum { EMU_STYLE_QWEN3 = 0, EMU_STYLE_SMOL = 1, EMU_STYLE_GRANITE = 2 };
 
 typedef struct emu_model_config {
     uint32_t hidden, heads, kv_heads, head_dim, ffn, vocab, layers;
@@ -221,6 +221,17 @@ typedef struct emu_model_config {
     int32_t encoding; /* every linear, the embedding and the output matrix */
     int32_t tied;     /* logits from the embedding matrix (SmolLM2) */
     int32_t qk_norm;  /* per-head RMSNorm of q and k before RoPE (Qwen3) */
+    /* EMU_STYLE_GRANITE (spm-granite-moe/src/model.rs:330-411): adjacent-pair
+       RoPE (attention.rs:12-26), a tied output, and mixture-of-experts layers:
+       an f32 router (n_experts x hidden, moe.rs:132-138) and experts_used of
+       n_experts SwiGLU experts of width expert_ff in expert_encoding in place
+       of the dense FFN (ffn unused).  Zero fields keep the plain forms. */
+    uint32_t n_experts, experts_used, expert_ff;
+    int32_t expert_encoding;
+    float embed_scale;    /* embeddings x this (model.rs:196-213: 12.0) */
+    float residual_scale; /* residual adds r + v * this (model.rs:356, attention.rs:103-107: 0.22) */
+    float logit_div;      /* logits / this before selection (model.rs:405-407: 6.0) */
+    float score_mul;      /* attention score = dot * this (attention.rs:40-46: 0.015625) */
 } emu_model_config;
 
 /* Tensor kinds addressable inside a model. */

@@ -86,6 +86,8 @@ def load() -> C.CDLL:
             "or_argmax": ([P, U, I], U),
             "or_gelu_tanh": ([F], F),
             "or_moe_ffn": ([C.POINTER(MoeDesc), P, U, P, P, P], I),
+            "or_moe_layer_bytes": ([C.POINTER(MoeModelCfg)], SZ),
+            "or_moe_model_step": ([C.POINTER(MoeModelCfg), C.POINTER(MoeModelWeights), P, P, P, P, U, P, U], I),
         }
         for name, (args, res) in sig.items():
             fn = getattr(lib, name)
@@ -234,6 +236,50 @@ def attend(q, keys, values, positions, heads, kv_heads, hd, variant, c=0.0) -> n
 def argmax(v: np.ndarray, tie_last: bool) -> int:
     v = np.ascontiguousarray(v, np.float32)
     return int(load().or_argmax(_p(v), v.size, int(tie_last)))
+
+
+class MoeModelCfg(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_uint32), ("heads", C.c_uint32), ("kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
+        ("vocab", C.c_uint32), ("layers", C.c_uint32), ("context", C.c_uint32), ("n_experts", C.c_uint32),
+        ("experts_used", C.c_uint32), ("expert_ff", C.c_uint32), ("rope_theta", C.c_float), ("eps", C.c_float),
+        ("embed_scale", C.c_float), ("residual_scale", C.c_float), ("logit_div", C.c_float),
+        ("score_mul", C.c_float), ("dtype", C.c_int32), ("expert_dtype", C.c_int32), ("kv_f16", C.c_int32),
+        ("qk_norm", C.c_int32),
+    ]
+
+
+class MoeModelWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("layers", "embed", "attn_norm", "ffn_norm", "q_norm", "k_norm", "out_norm")]
+
+
+def moe_layer_bytes(cfg: MoeModelCfg) -> int:
+    return int(load().or_moe_layer_bytes(C.byref(cfg)))
+
+
+class MoeModelOracle:
+    """Reference decode steps for a mixture-of-experts decoder (or_moe_model_step)."""
+
+    def __init__(self, cfg: MoeModelCfg, weights: dict, n_clients: int):
+        self.cfg = cfg
+        self.w = {k: np.ascontiguousarray(v) for k, v in weights.items()}
+        self.ws = MoeModelWeights(*[_p(self.w[k]) for k in
+                                    ("layers", "embed", "attn_norm", "ffn_norm", "q_norm", "k_norm", "out_norm")])
+        kw = cfg.kv_heads * cfg.head_dim
+        self.n = n_clients
+        self.k = np.zeros(n_clients * cfg.layers * cfg.context * kw, np.float32)
+        self.v = np.zeros_like(self.k)
+        self.pos = np.zeros(n_clients, np.uint32)
+
+    def step(self, tokens, layers_limit: int = 0) -> np.ndarray:
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        logits = np.empty(self.n * self.cfg.vocab, np.float32)
+        st = load().or_moe_model_step(C.byref(self.cfg), C.byref(self.ws), _p(self.k), _p(self.v), _p(self.pos),
+                                      _p(toks), self.n, _p(logits), layers_limit)
+        if st != 0:
+            raise ValueError(f"oracle MoE step failed ({st})")
+        self.pos += 1
+        return logits.reshape(self.n, self.cfg.vocab)
 
 
 class DenseOracle:

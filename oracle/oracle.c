@@ -836,3 +836,124 @@ int or_moe_ffn(const or_moe_desc *d, const float *x, uint32_t n_tok, const uint3
     free(tok);
     return st ? -1 : 0;
 }
+
+/* ---- mixture-of-experts decoder ------------------------------------------
+ * spm-granite-moe/src/model.rs:330-411 (block, run), attention.rs:12-112
+ * (interleaved rope, attend with score * 0.015625, add_scaled 0.22),
+ * moe.rs:124-159 (router matvec, route, experts) and math.rs:1-40. */
+size_t or_moe_layer_bytes(const or_moe_model_cfg *c)
+{
+    const uint32_t QW = c->heads * c->head_dim, KW = c->kv_heads * c->head_dim;
+    const size_t rbH = row_bytes_of(c->dtype, c->hidden), rbQ = row_bytes_of(c->dtype, QW);
+    const size_t rbHe = row_bytes_of(c->expert_dtype, c->hidden), rbFe = row_bytes_of(c->expert_dtype, c->expert_ff);
+    return (size_t)(QW + 2 * KW) * rbH + (size_t)c->hidden * rbQ + sizeof(float) * c->n_experts * c->hidden +
+           (size_t)c->n_experts * (2 * (size_t)c->expert_ff * rbHe + (size_t)c->hidden * rbFe);
+}
+
+static void add_scaled(float *a, const float *b, uint32_t n, float s)
+{
+    /* math.rs:31-33: a + b * scale, two roundings (built without contraction) */
+    for (uint32_t i = 0; i < n; ++i)
+        a[i] = s != 0.0f ? a[i] + b[i] * s : a[i] + b[i];
+}
+
+int or_moe_model_step(const or_moe_model_cfg *c, const or_moe_model_weights *w, float *kv_k, float *kv_v,
+                      const uint32_t *positions, const uint32_t *tokens, uint32_t n_clients, float *logits,
+                      uint32_t n_layers_limit)
+{
+    const uint32_t H = c->hidden, hd = c->head_dim, NH = c->heads, NKV = c->kv_heads;
+    const uint32_t QW = NH * hd, KW = NKV * hd, E = c->n_experts, K = c->experts_used, L = c->layers;
+    const uint32_t layers_run = n_layers_limit && n_layers_limit < L ? n_layers_limit : L;
+    if (NKV == 0 || NH % NKV || E == 0 || K == 0 || K > E || H % 256 || c->expert_ff % 32)
+        return -3;
+    const size_t rbH = row_bytes_of(c->dtype, H), rbQ = row_bytes_of(c->dtype, QW);
+    const size_t rbHe = row_bytes_of(c->expert_dtype, H);
+    const size_t layer_bytes = or_moe_layer_bytes(c);
+    float *buf = (float *)malloc(sizeof(float) * ((size_t)H * 4 + QW * 2 + KW * 2 + E + K + 16));
+    uint32_t ids[64];
+    if (!buf || K > 64) {
+        free(buf);
+        return -4;
+    }
+    float *state = buf, *xn = state + H, *q = xn + H, *k = q + QW, *v = k + KW, *att = v + KW, *proj = att + QW,
+          *moe = proj + H, *rl = moe + H, *rw = rl + E;
+    for (uint32_t ci = 0; ci < n_clients; ++ci) {
+        const uint32_t pos = positions[ci];
+        if (pos >= c->context) {
+            free(buf);
+            return -5;
+        }
+        float *ck = kv_k + (size_t)ci * L * c->context * KW;
+        float *cv = kv_v + (size_t)ci * L * c->context * KW;
+        /* embeddings (model.rs:196-213): one row decoded, times 12.0 */
+        if (or_decode(c->dtype, w->embed + (size_t)tokens[ci] * rbH, rbH, state) != 0) {
+            free(buf);
+            return -1;
+        }
+        if (c->embed_scale != 0.0f)
+            for (uint32_t i = 0; i < H; ++i)
+                state[i] = state[i] * c->embed_scale;
+        for (uint32_t layer = 0; layer < layers_run; ++layer) {
+            const uint8_t *base = w->layers + (size_t)layer * layer_bytes;
+            const uint8_t *wq = base, *wk = wq + (size_t)QW * rbH, *wv = wk + (size_t)KW * rbH,
+                          *wo = wv + (size_t)KW * rbH, *wr = wo + (size_t)H * rbQ;
+            const uint8_t *wg = wr + sizeof(float) * E * H, *wu = wg + (size_t)E * c->expert_ff * rbHe,
+                          *wd = wu + (size_t)E * c->expert_ff * rbHe;
+            /* block (model.rs:330-363): attention half */
+            or_rms_norm(state, w->attn_norm + (size_t)layer * H, H, c->eps, xn);
+            or_qmatvec(c->dtype, wq, QW, H, xn, 1, q, 1);
+            or_qmatvec(c->dtype, wk, KW, H, xn, 1, k, 1);
+            or_qmatvec(c->dtype, wv, KW, H, xn, 1, v, 1);
+            for (uint32_t h = 0; h < NH; ++h) {
+                if (c->qk_norm)
+                    or_rms_norm(q + h * hd, w->q_norm + (size_t)layer * hd, hd, c->eps, q + h * hd);
+                or_rope_interleaved(q + h * hd, hd, pos, c->rope_theta);
+            }
+            for (uint32_t h = 0; h < NKV; ++h) {
+                if (c->qk_norm)
+                    or_rms_norm(k + h * hd, w->k_norm + (size_t)layer * hd, hd, c->eps, k + h * hd);
+                or_rope_interleaved(k + h * hd, hd, pos, c->rope_theta);
+            }
+            float *kslot = ck + ((size_t)layer * c->context + pos) * KW;
+            float *vslot = cv + ((size_t)layer * c->context + pos) * KW;
+            for (uint32_t i = 0; i < KW; ++i) {
+                kslot[i] = c->kv_f16 ? or_f16_to_f32(or_f32_to_f16(k[i])) : k[i];
+                vslot[i] = c->kv_f16 ? or_f16_to_f32(or_f32_to_f16(v[i])) : v[i];
+            }
+            or_attend(q, ck + (size_t)layer * c->context * KW, cv + (size_t)layer * c->context * KW, pos + 1, NH,
+                      NKV, hd, 2, c->score_mul, att);
+            or_qmatvec(c->dtype, wo, H, QW, att, 1, proj, 1);
+            add_scaled(state, proj, H, c->residual_scale);
+            /* MoE half: ffn_norm, router (f32 M1), route, experts, add_scaled */
+            or_rms_norm(state, w->ffn_norm + (size_t)layer * H, H, c->eps, xn);
+            or_matvec_m1((const float *)wr, E, H, xn, rl);
+            or_route(rl, E, K, ids, rw);
+            or_moe_desc d;
+            d.enc_gate_up = c->expert_dtype;
+            d.enc_down = c->expert_dtype;
+            d.gate = wg;
+            d.up = wu;
+            d.down = wd;
+            d.down_scale = NULL;
+            d.n_experts = E;
+            d.width = H;
+            d.ff = c->expert_ff;
+            d.k = K;
+            d.act = OR_ACT_SILU;
+            if (or_moe_ffn(&d, xn, 1, ids, rw, moe) != 0) {
+                free(buf);
+                return -6;
+            }
+            add_scaled(state, moe, H, c->residual_scale);
+        }
+        /* run (model.rs:403-407): output norm, tied projection, / 6.0 */
+        or_rms_norm(state, w->out_norm, H, c->eps, xn);
+        float *lg = logits + (size_t)ci * c->vocab;
+        or_qmatvec(c->dtype, w->embed, c->vocab, H, xn, 1, lg, 1);
+        if (c->logit_div != 0.0f)
+            for (uint32_t i = 0; i < c->vocab; ++i)
+                lg[i] = lg[i] / c->logit_div;
+    }
+    free(buf);
+    return 0;
+}

@@ -163,6 +163,36 @@ size_t or_dense_layer_bytes(const or_dense_cfg *cfg);
 int or_dense_step(const or_dense_cfg *cfg, const or_dense_weights *w, float *kv_k, float *kv_v,
                   const uint32_t *positions, const uint32_t *tokens, uint32_t n_clients,
                   float *logits, uint32_t n_layers_limit);
+/* ---- mixture-of-experts decoder (Granite: spm-granite-moe) -------------- */
+typedef struct {
+    uint32_t hidden, heads, kv_heads, head_dim, vocab, layers, context;
+    uint32_t n_experts, experts_used, expert_ff;
+    float rope_theta, eps;
+    float embed_scale;    /* embeddings x this (model.rs:196-213: 12.0) */
+    float residual_scale; /* residual adds a + b*s (model.rs:356, attention.rs:103-107: 0.22) */
+    float logit_div;      /* logits / this (model.rs:405-407: 6.0) */
+    float score_mul;      /* attention score = dot * this (attention.rs:40-46: 0.015625) */
+    int32_t dtype;        /* q, k, v, o, the embedding (also the tied output) */
+    int32_t expert_dtype; /* gate/up/down experts */
+    int32_t kv_f16;
+    int32_t qk_norm;      /* per-head RMSNorm on q and k before RoPE */
+} or_moe_model_cfg;
+
+/* layers: per layer q, k, v, o, router (f32, n_experts x hidden), gate_exps,
+ * up_exps (n_experts x expert_ff x hidden), down_exps (n_experts x hidden x
+ * expert_ff), back to back; expert-major as in GGUF (weights.rs:57-73). */
+typedef struct {
+    const uint8_t *layers;
+    const uint8_t *embed; /* vocab x hidden; the output projection too (tied) */
+    const float *attn_norm, *ffn_norm, *q_norm, *k_norm, *out_norm;
+} or_moe_model_weights;
+
+size_t or_moe_layer_bytes(const or_moe_model_cfg *cfg);
+/* One decode step (model.rs:330-411, one position per client). */
+int or_moe_model_step(const or_moe_model_cfg *cfg, const or_moe_model_weights *w, float *kv_k, float *kv_v,
+                      const uint32_t *positions, const uint32_t *tokens, uint32_t n_clients, float *logits,
+                      uint32_t n_layers_limit);
+
 /* greedy selection: tie 0 -> lowest index (top_k), 1 -> last index (max_by). */
 uint32_t or_argmax(const float *v, uint32_t n, int tie_last);
 

@@ -179,3 +179,83 @@ def moe_ffn_f64(enc_in, enc_down, gate, up, down, down_scale, n_experts, width, 
                 v = v * float(down_scale[e])
             out[t] += float(weights[t][s]) * v
     return out
+
+
+def moe_model_f64(cfg, w: dict, tokens_per_step, layers_limit=0):
+    """A mixture-of-experts decoder (spm-granite-moe model.rs:330-411) in
+    float64 from this module's own decoders, for one client: returns the
+    logits of every step.  w holds the byte blobs and gains the oracle takes
+    (layers, embed, attn_norm, ffn_norm, out_norm); cfg an oracle MoeModelCfg."""
+    H, hd, NH, NKV = cfg.hidden, cfg.head_dim, cfg.heads, cfg.kv_heads
+    QW, KW, E, K, F = NH * hd, NKV * hd, cfg.n_experts, cfg.experts_used, cfg.expert_ff
+    dec, dece = DECODERS[cfg.dtype], DECODERS[cfg.expert_dtype]
+    rbH = H // 256 * {14: 210, 13: 176, 8: 34 * 8, 10: 84}[cfg.dtype]
+    rbQ = QW // 256 * {14: 210, 13: 176, 8: 34 * 8, 10: 84}[cfg.dtype]
+    rbHe = H // 256 * {14: 210, 13: 176, 8: 34 * 8, 10: 84}[cfg.expert_dtype]
+    rbFe = F // 256 * {14: 210, 13: 176, 8: 34 * 8, 10: 84}[cfg.expert_dtype]
+    layer_bytes = (QW + 2 * KW) * rbH + H * rbQ + 4 * E * H + E * (2 * F * rbHe + H * rbFe)
+    embed = dec(w["embed"]).astype(np.float64).reshape(-1, H)
+    L = cfg.layers if not layers_limit else min(layers_limit, cfg.layers)
+    mats = []
+    for layer in range(L):
+        blob = np.asarray(w["layers"]).view(np.uint8)[layer * layer_bytes:(layer + 1) * layer_bytes]
+        o = 0
+        def take(n):
+            nonlocal o
+            part = blob[o:o + n]
+            o += n
+            return part
+        wq = dec(take(QW * rbH)).astype(np.float64).reshape(QW, H)
+        wk = dec(take(KW * rbH)).astype(np.float64).reshape(KW, H)
+        wv = dec(take(KW * rbH)).astype(np.float64).reshape(KW, H)
+        wo = dec(take(H * rbQ)).astype(np.float64).reshape(H, QW)
+        wr = take(4 * E * H).view(np.float32).astype(np.float64).reshape(E, H)
+        g, u, d = take(E * F * rbHe), take(E * F * rbHe), take(E * H * rbFe)
+        mats.append((wq, wk, wv, wo, wr, g, u, d))
+
+    def norm(x, gain):
+        return x / np.sqrt(np.mean(x * x) + cfg.eps) * gain
+
+    def rope(x, pos):
+        x = x.reshape(-1, hd).copy()
+        i = np.arange(0, hd, 2)
+        ang = pos / np.power(float(np.float32(cfg.rope_theta)), i / hd)
+        c, s = np.cos(ang), np.sin(ang)
+        a, b = x[:, 0::2].copy(), x[:, 1::2].copy()
+        x[:, 0::2], x[:, 1::2] = a * c - b * s, a * s + b * c
+        return x.reshape(-1)
+
+    res = cfg.residual_scale if cfg.residual_scale else 1.0
+    keys = [[] for _ in range(L)]
+    vals = [[] for _ in range(L)]
+    out = []
+    for pos, tok in enumerate(tokens_per_step):
+        h = embed[tok] * (cfg.embed_scale if cfg.embed_scale else 1.0)
+        for layer in range(L):
+            wq, wk, wv, wo, wr, g, u, d = mats[layer]
+            xn = norm(h, np.asarray(w["attn_norm"], np.float64)[layer * H:(layer + 1) * H])
+            q, k, v = rope(wq @ xn, pos), rope(wk @ xn, pos), wv @ xn
+            keys[layer].append(k)
+            vals[layer].append(v)
+            Km, Vm = np.stack(keys[layer]), np.stack(vals[layer])
+            att = np.empty(QW)
+            for hh in range(NH):
+                kvh = hh // (NH // NKV)
+                sc = Km[:, kvh * hd:(kvh + 1) * hd] @ q[hh * hd:(hh + 1) * hd] * cfg.score_mul
+                p = np.exp(sc - sc.max())
+                p /= p.sum()
+                att[hh * hd:(hh + 1) * hd] = p @ Vm[:, kvh * hd:(kvh + 1) * hd]
+            h = h + (wo @ att) * res
+            xn = norm(h, np.asarray(w["ffn_norm"], np.float64)[layer * H:(layer + 1) * H])
+            lg = wr @ xn
+            pr = np.exp(lg - lg.max())
+            pr /= pr.sum()
+            ids = sorted(range(E), key=lambda e: (-pr[e], e))[:K]
+            wts = pr[ids] / pr[ids].sum()
+            moe = moe_ffn_f64(cfg.expert_dtype, cfg.expert_dtype, g, u, d, None, E, H, F, K, False, xn,
+                              [ids], [wts])[0]
+            h = h + moe * res
+        xn = norm(h, np.asarray(w["out_norm"], np.float64))
+        lo = embed @ xn
+        out.append(lo / (cfg.logit_div if cfg.logit_div else 1.0))
+    return out

@@ -390,3 +390,56 @@ def test_moe_ffn_sums_experts_in_ascending_id_order():  # moe.rs:166-185
                           x, np.array([[e]]), np.ones((1, 1), np.float32))[0] for e in (0, 3)]
     want = (np.float32(0.0) + one[0] * w[0, 1]).astype(np.float32) + (one[1] * w[0, 0]).astype(np.float32)
     assert np.array_equal(a[0], want.astype(np.float32))
+
+
+def small_moe_model(seed, qk_norm=0, expert_dtype=oracle.OR_Q6_K):
+    rng = np.random.default_rng(seed)
+    cfg = oracle.MoeModelCfg(hidden=256, heads=4, kv_heads=2, head_dim=64, vocab=300, layers=2, context=16,
+                             n_experts=8, experts_used=2, expert_ff=256, rope_theta=1.5e6, eps=1e-6,
+                             embed_scale=12.0, residual_scale=0.22, logit_div=6.0, score_mul=0.015625,
+                             dtype=oracle.OR_Q6_K, expert_dtype=expert_dtype, kv_f16=0, qk_norm=qk_norm)
+    H, E, F = cfg.hidden, cfg.n_experts, cfg.expert_ff
+    QW, KW = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    rb = {oracle.OR_Q6_K: 210, oracle.OR_Q2_K: 84}
+    parts = []
+    for _ in range(cfg.layers):
+        parts.append(npref.random_blocks(14, (QW + 2 * KW) * H // 256, rng, scale_exp=(-12, -10)).view(np.uint8).reshape(-1))
+        parts.append(npref.random_blocks(14, H * QW // 256, rng, scale_exp=(-12, -10)).view(np.uint8).reshape(-1))
+        parts.append((rng.normal(size=E * H) * 0.05).astype(np.float32).view(np.uint8))
+        nb = E * F * H // 256
+        for _ in range(3):
+            parts.append(npref.random_blocks(expert_dtype, nb, rng, scale_exp=(-12, -10)).view(np.uint8).reshape(-1))
+    layers = np.concatenate(parts)
+    assert layers.size == cfg.layers * oracle.moe_layer_bytes(cfg)
+    w = {"layers": layers,
+         "embed": npref.random_blocks(14, cfg.vocab * H // 256, rng, scale_exp=(-10, -8)).view(np.uint8).reshape(-1),
+         "attn_norm": rng.uniform(0.5, 1.5, cfg.layers * H).astype(np.float32),
+         "ffn_norm": rng.uniform(0.5, 1.5, cfg.layers * H).astype(np.float32),
+         "q_norm": rng.uniform(0.5, 1.5, cfg.layers * cfg.head_dim).astype(np.float32),
+         "k_norm": rng.uniform(0.5, 1.5, cfg.layers * cfg.head_dim).astype(np.float32),
+         "out_norm": rng.uniform(0.5, 1.5, H).astype(np.float32)}
+    return cfg, w
+
+
+@pytest.mark.parametrize("expert_dtype", [oracle.OR_Q6_K, oracle.OR_Q2_K])
+def test_moe_model_step_matches_float64_composition(expert_dtype):
+    """The oracle's mixture-of-experts decode step (embedding x 12, interleaved
+    RoPE, score x 1/64, residual adds x 0.22, f32 router, top-2 of 8 SwiGLU
+    experts, tied output / 6) against an independent float64 composition."""
+    cfg, w = small_moe_model(81, expert_dtype=expert_dtype)
+    orc = oracle.MoeModelOracle(cfg, w, 1)
+    toks = [5, 17, 299, 0, 42, 7]
+    ref = npref.moe_model_f64(cfg, w, toks)
+    for t, want in zip(toks, ref):
+        got = orc.step([t])[0].astype(np.float64)
+        assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want)), t
+
+
+def test_moe_model_step_residual_scale_matters():
+    """A planted change of the residual scale moves the logits: the composition
+    test above can see it (the scale is not a no-op in the restatement)."""
+    cfg, w = small_moe_model(82)
+    a = oracle.MoeModelOracle(cfg, w, 1).step([3])[0]
+    cfg.residual_scale = 0.25
+    b = oracle.MoeModelOracle(cfg, w, 1).step([3])[0]
+    assert np.max(np.abs(a - b)) > 1e-3 * np.max(np.abs(a))
