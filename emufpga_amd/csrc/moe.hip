@@ -3,16 +3,22 @@
 // gemma_smoke.rs:92-139).
 //
 // After routing (emu_route: ids and weights, n_tok x k), three launches:
-//   1. gate|up: grid (expert, 16-row tile).  A wavefront finds the tokens
-//      routed to its expert with one ballot over the n_tok*k routing table
-//      (token order, as expert_tokens does), streams each gate and up row once
-//      for all of them, and writes act(gate) * up per (token, slot);
-//   2. down: grid (expert, 16-row tile) over the hidden rows, reading the
+//   1. gate|up: grid (expert, row tile).  A wavefront finds the tokens routed
+//      to its expert with one ballot over the n_tok*k routing table (token
+//      order, as expert_tokens does), streams gate and up rows once for all of
+//      them, and writes act(gate) * up per (token, slot);
+//   2. down: grid (expert, row tile) over the hidden rows, reading the
 //      activations of the expert's tokens, times the expert's optional output
 //      scale, into a per-(token, slot) contribution;
-//   3. combine: per token, output = +0.0 plus contribution * weight added in
-//      ascending expert id (accumulate, moe.rs:58-75, with the experts visited
-//      in BTreeSet order), each product rounded before the add.
+//   3. combine: per token and column, output = +0.0 plus contribution * weight
+//      added in ascending expert id (accumulate, moe.rs:58-75, with the experts
+//      visited in BTreeSet order), each product rounded before the add.
+// Expert rows are short (a 1024-column Q6_K row is 32 units of 32 weights),
+// so a row takes L = 16, 32 or 64 lanes (the unit count rounded up to a power
+// of two) and a wavefront works 64/L rows at once: every lane loads, and a
+// wavefront's rows cost one memory round trip.  With L <= 32 the gate and up
+// rows of one hidden unit sit in neighbouring lane groups and meet by one
+// cross-group shuffle.
 // Experts nobody chose cost one ballot per wavefront.  Weights are read once
 // per step however many tokens share an expert (the reference's batch reuse).
 #include "internal.hpp"
@@ -22,8 +28,7 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kRowsPerWave = 4;
-constexpr int kRowsPerBlock = kRowsPerWave * (kThreads / EMU_WAVE);
+constexpr int kWaves = kThreads / EMU_WAVE;
 constexpr int kMaxTok = 8;
 
 struct MoeArgs {
@@ -87,13 +92,14 @@ template <int ACT> __device__ __forceinline__ float activate(float g, float u)
 }
 
 // One row of one expert matrix against the cnt routed input vectors
-// (in[slot[t] * in_stride + c]); per-lane partial sums, not yet reduced.
-template <class F>
+// (in[slot[t] * in_stride + c]), worked by the L lanes q = 0..L-1 of a lane
+// group; per-lane partial sums, not yet reduced.
+template <class F, int L>
 __device__ __forceinline__ void row_dots(const uint8_t *row, int nb, const float *in, int in_stride,
-                                         const int (&slot)[kMaxTok], int cnt, int lane, float (&acc)[kMaxTok])
+                                         const int (&slot)[kMaxTok], int cnt, int q, float (&acc)[kMaxTok])
 {
     const int U = nb * F::UPB;
-    for (int u = lane; u < U; u += EMU_WAVE) {
+    for (int u = q; u < U; u += L) {
         const int blk = u / F::UPB, sub = u % F::UPB;
         typename F::Raw raw;
         F::load(row, (uint32_t)blk * F::BB, sub, raw);
@@ -118,9 +124,21 @@ __device__ __forceinline__ void row_dots(const uint8_t *row, int nb, const float
     }
 }
 
-template <class F, int ACT>
+// Sum over the L lanes of a lane group (L a power of two, <= 64).
+template <int L> __device__ __forceinline__ float group_sum(float v)
+{
+#pragma unroll
+    for (int off = L / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, EMU_WAVE);
+    return v;
+}
+
+// Hidden units per wavefront of the gate|up kernel with L lanes per row.
+template <int L> constexpr int up_rows_per_wave() { return L >= EMU_WAVE ? 1 : EMU_WAVE / L / 2; }
+
+template <class F, int ACT, int L>
 __global__ __launch_bounds__(kThreads) void moe_up_kernel(MoeArgs a)
 {
+    constexpr int S = EMU_WAVE / L; // rows a wavefront works at once
     const int e = blockIdx.x;
     const int lane = threadIdx.x & (EMU_WAVE - 1), wv = threadIdx.x / EMU_WAVE;
     int slot[kMaxTok];
@@ -131,67 +149,98 @@ __global__ __launch_bounds__(kThreads) void moe_up_kernel(MoeArgs a)
 #pragma unroll
     for (int t = 0; t < kMaxTok; ++t) tok[t] = slot[t] / a.k;
     const size_t per = (size_t)(a.up ? 1 : 2) * a.ff;
-    for (int i = 0; i < kRowsPerWave; ++i) {
-        const int r = blockIdx.y * kRowsPerBlock + wv * kRowsPerWave + i;
-        if (r >= a.ff) break;
-        const uint8_t *grow = a.gate + ((size_t)e * per + r) * a.rb_in;
-        const uint8_t *urow = a.up ? a.up + ((size_t)e * a.ff + r) * a.rb_in
-                                   : a.gate + ((size_t)e * per + a.ff + r) * a.rb_in;
-        float ag[kMaxTok], au[kMaxTok];
+    const int j = lane / L, q = lane % L;
+    // Lane groups 2i and 2i+1 take the gate and up rows of hidden unit r; the
+    // groups of one unit (and every lane a shuffle below reads) share r, so
+    // they leave together.
+    const int r = (blockIdx.y * kWaves + wv) * up_rows_per_wave<L>() + (S >= 2 ? j >> 1 : 0);
+    if (r >= a.ff) return;
+    const uint8_t *grow = a.gate + ((size_t)e * per + r) * a.rb_in;
+    const uint8_t *urow = a.up ? a.up + ((size_t)e * a.ff + r) * a.rb_in
+                               : a.gate + ((size_t)e * per + a.ff + r) * a.rb_in;
+    float ag[kMaxTok], au[kMaxTok];
 #pragma unroll
-        for (int t = 0; t < kMaxTok; ++t) ag[t] = au[t] = 0.0f;
-        row_dots<F>(grow, a.nb_in, a.x, a.width, tok, cnt, lane, ag);
-        row_dots<F>(urow, a.nb_in, a.x, a.width, tok, cnt, lane, au);
+    for (int t = 0; t < kMaxTok; ++t) ag[t] = au[t] = 0.0f;
+    if constexpr (S >= 2) {
+        const bool is_up = j & 1;
+        row_dots<F, L>(is_up ? urow : grow, a.nb_in, a.x, a.width, tok, cnt, q, ag);
 #pragma unroll
         for (int t = 0; t < kMaxTok; ++t) {
             if (t < cnt) {
-                const float g = wave_sum(ag[t]), u = wave_sum(au[t]);
-                if (lane == 0) a.act_buf[(size_t)slot[t] * a.ff + r] = activate<ACT>(g, u);
+                ag[t] = group_sum<L>(ag[t]);
+                au[t] = __shfl_xor(ag[t], L, EMU_WAVE);
             }
         }
+        if (is_up || q != 0) return;
+    } else {
+        row_dots<F, L>(grow, a.nb_in, a.x, a.width, tok, cnt, q, ag);
+        row_dots<F, L>(urow, a.nb_in, a.x, a.width, tok, cnt, q, au);
+#pragma unroll
+        for (int t = 0; t < kMaxTok; ++t) {
+            if (t < cnt) {
+                ag[t] = group_sum<L>(ag[t]);
+                au[t] = group_sum<L>(au[t]);
+            }
+        }
+        if (q != 0) return;
     }
+#pragma unroll
+    for (int t = 0; t < kMaxTok; ++t)
+        if (t < cnt) a.act_buf[(size_t)slot[t] * a.ff + r] = activate<ACT>(ag[t], au[t]);
 }
 
-template <class F>
+template <class F, int L>
 __global__ __launch_bounds__(kThreads) void moe_down_kernel(MoeArgs a)
 {
+    constexpr int S = EMU_WAVE / L;
     const int e = blockIdx.x;
     const int lane = threadIdx.x & (EMU_WAVE - 1), wv = threadIdx.x / EMU_WAVE;
     int slot[kMaxTok];
     const int cnt = expert_slots(a, e, lane, slot);
     if (cnt == 0) return;
+    const int j = lane / L, q = lane % L;
+    const int r = (blockIdx.y * kWaves + wv) * S + j; // a lane group's row; the group leaves together
+    if (r >= a.width) return;
     const float scale = a.down_scale ? a.down_scale[e] : 1.0f;
-    for (int i = 0; i < kRowsPerWave; ++i) {
-        const int r = blockIdx.y * kRowsPerBlock + wv * kRowsPerWave + i;
-        if (r >= a.width) break;
-        const uint8_t *row = a.down + ((size_t)e * a.width + r) * a.rb_ff;
-        float acc[kMaxTok];
+    const uint8_t *row = a.down + ((size_t)e * a.width + r) * a.rb_ff;
+    float acc[kMaxTok];
 #pragma unroll
-        for (int t = 0; t < kMaxTok; ++t) acc[t] = 0.0f;
-        row_dots<F>(row, a.nb_ff, a.act_buf, a.ff, slot, cnt, lane, acc);
+    for (int t = 0; t < kMaxTok; ++t) acc[t] = 0.0f;
+    row_dots<F, L>(row, a.nb_ff, a.act_buf, a.ff, slot, cnt, q, acc);
 #pragma unroll
-        for (int t = 0; t < kMaxTok; ++t) {
-            if (t < cnt) {
-                float v = wave_sum(acc[t]);
-                if (a.down_scale) v = __fmul_rn(v, scale); // gemma_smoke.rs:129-137
-                if (lane == 0) a.contrib[(size_t)slot[t] * a.width + r] = v;
-            }
+    for (int t = 0; t < kMaxTok; ++t) {
+        if (t < cnt) {
+            float v = group_sum<L>(acc[t]);
+            if (a.down_scale) v = __fmul_rn(v, scale); // gemma_smoke.rs:129-137
+            if (q == 0) a.contrib[(size_t)slot[t] * a.width + r] = v;
         }
     }
 }
 
-// Per token: sum over its slots in ascending expert id, from +0.0.
+// Per token (blockIdx.x) and column: sum over its slots in ascending expert
+// id, from +0.0.
 __global__ __launch_bounds__(kThreads) void moe_combine_kernel(MoeArgs a)
 {
     const int t = blockIdx.x;
+    const int c = blockIdx.y * kThreads + threadIdx.x;
+    if (c >= a.width) return;
     int order[kMaxTok];
     int n = 0;
-    // Selection of the token's slots by expert id (k <= 8; ids are distinct).
+    // The token's routing entries, loaded once (k <= 8).
+    int idv[kMaxTok];
+    float wv[kMaxTok];
+#pragma unroll
+    for (int s = 0; s < kMaxTok; ++s) {
+        idv[s] = s < a.k ? a.ids[t * a.k + s] : 0x7fffffff;
+        wv[s] = s < a.k ? a.weights[t * a.k + s] : 0.0f;
+    }
+    // Selection of the token's slots by expert id (ids are distinct).
     int prev = -1;
     for (int i = 0; i < a.k; ++i) {
         int best = -1, best_id = 0x7fffffff;
-        for (int s = 0; s < a.k; ++s) {
-            const int id = a.ids[t * a.k + s];
+#pragma unroll
+        for (int s = 0; s < kMaxTok; ++s) {
+            const int id = idv[s];
             if (id > prev && id < best_id && id < a.n_experts) {
                 best = s;
                 best_id = id;
@@ -201,29 +250,64 @@ __global__ __launch_bounds__(kThreads) void moe_combine_kernel(MoeArgs a)
         order[n++] = best;
         prev = best_id;
     }
-    for (int c = threadIdx.x; c < a.width; c += kThreads) {
-        float sum = 0.0f;
-        for (int i = 0; i < n; ++i) {
-            const int s = t * a.k + order[i];
-            sum = __fadd_rn(sum, __fmul_rn(a.contrib[(size_t)s * a.width + c], a.weights[s]));
-        }
-        a.out[(size_t)t * a.width + c] = sum;
+    float v[kMaxTok], w[kMaxTok];
+#pragma unroll
+    for (int i = 0; i < kMaxTok; ++i) {
+        const int o = i < n ? order[i] : 0;
+        v[i] = i < n ? a.contrib[((size_t)t * a.k + o) * a.width + c] : 0.0f;
+        w[i] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < kMaxTok; ++s) w[i] = s == o ? wv[s] : w[i];
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxTok; ++i)
+        if (i < n) sum = __fadd_rn(sum, __fmul_rn(v[i], w[i]));
+    a.out[(size_t)t * a.width + c] = sum;
+}
+
+// Lanes per row for a row of U units: the power of two in {16, 32, 64} that
+// covers it (longer rows loop).
+int lanes_for(int units) { return units > 32 ? 64 : units > 16 ? 32 : 16; }
+
+template <class F, int ACT, int L> void launch_up_l(emu_ctx *ctx, const MoeArgs &a)
+{
+    constexpr int per_block = kWaves * up_rows_per_wave<L>();
+    const dim3 grid(a.n_experts, (a.ff + per_block - 1) / per_block);
+    hipLaunchKernelGGL((moe_up_kernel<F, ACT, L>), grid, dim3(kThreads), 0, ctx->stream, a);
+}
+
+template <class F, int ACT> void launch_up_a(emu_ctx *ctx, const MoeArgs &a)
+{
+    switch (lanes_for(a.nb_in * F::UPB)) {
+    case 16: launch_up_l<F, ACT, 16>(ctx, a); break;
+    case 32: launch_up_l<F, ACT, 32>(ctx, a); break;
+    default: launch_up_l<F, ACT, 64>(ctx, a); break;
     }
 }
 
 template <class F> void launch_up(emu_ctx *ctx, const MoeArgs &a)
 {
-    const dim3 grid(a.n_experts, (a.ff + kRowsPerBlock - 1) / kRowsPerBlock);
     if (a.act == EMU_ACT_GELU_TANH)
-        hipLaunchKernelGGL((moe_up_kernel<F, EMU_ACT_GELU_TANH>), grid, dim3(kThreads), 0, ctx->stream, a);
+        launch_up_a<F, EMU_ACT_GELU_TANH>(ctx, a);
     else
-        hipLaunchKernelGGL((moe_up_kernel<F, EMU_ACT_SILU>), grid, dim3(kThreads), 0, ctx->stream, a);
+        launch_up_a<F, EMU_ACT_SILU>(ctx, a);
+}
+
+template <class F, int L> void launch_down_l(emu_ctx *ctx, const MoeArgs &a)
+{
+    constexpr int per_block = kWaves * (EMU_WAVE / L);
+    const dim3 grid(a.n_experts, (a.width + per_block - 1) / per_block);
+    hipLaunchKernelGGL((moe_down_kernel<F, L>), grid, dim3(kThreads), 0, ctx->stream, a);
 }
 
 template <class F> void launch_down(emu_ctx *ctx, const MoeArgs &a)
 {
-    const dim3 grid(a.n_experts, (a.width + kRowsPerBlock - 1) / kRowsPerBlock);
-    hipLaunchKernelGGL(moe_down_kernel<F>, grid, dim3(kThreads), 0, ctx->stream, a);
+    switch (lanes_for(a.nb_ff * F::UPB)) {
+    case 16: launch_down_l<F, 16>(ctx, a); break;
+    case 32: launch_down_l<F, 32>(ctx, a); break;
+    default: launch_down_l<F, 64>(ctx, a); break;
+    }
 }
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -289,7 +373,8 @@ extern "C" int emu_moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x
     default: return EMU_E_UNSUPPORTED;
     }
     EMU_LAUNCH_CHECK(ctx);
-    hipLaunchKernelGGL(moe_combine_kernel, dim3(n_tok), dim3(kThreads), 0, ctx->stream, a);
+    hipLaunchKernelGGL(moe_combine_kernel, dim3(n_tok, (d->width + kThreads - 1) / kThreads), dim3(kThreads), 0,
+                       ctx->stream, a);
     EMU_LAUNCH_CHECK(ctx);
     return EMU_OK;
 }

@@ -63,6 +63,8 @@ SHAPES = [
     ("granite", _lib.Q6_K, _lib.Q6_K, 32, 1024, 512, 8, 4, False, _lib.EMU_ACT_SILU, 1.1),
     ("olmoe", _lib.Q2_K, _lib.Q2_K, 64, 2048, 1024, 8, 8, False, _lib.EMU_ACT_SILU, 1.0),
     ("gemma", _lib.Q5_K, _lib.Q8_0, 16, 2816, 704, 8, 8, True, _lib.EMU_ACT_GELU_TANH, 1.2),
+    # rows shorter than 16 units: 4 rows per wavefront in both kernels
+    ("short-rows", _lib.Q6_K, _lib.Q8_0, 8, 256, 96, 2, 3, True, _lib.EMU_ACT_SILU, 1.0),
 ]
 
 
