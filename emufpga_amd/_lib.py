@@ -22,6 +22,8 @@ EMU_E_CONFIG = 7
 EMU_E_HIP = 8
 EMU_E_ARG = 9
 EMU_E_NOMEM = 10
+EMU_E_FORMAT = 11
+EMU_E_IO = 12
 
 # GGUF dtype ids (spm-gguf/src/parse.rs:10-29)
 F32, F16, Q8_0, Q2_K, Q5_K, Q6_K = 0, 1, 8, 10, 13, 14
@@ -103,6 +105,8 @@ _ERRORS = {
     EMU_E_HIP: HipError,
     EMU_E_ARG: ArgumentError,
     EMU_E_NOMEM: EmuError,
+    EMU_E_FORMAT: EmuError,
+    EMU_E_IO: EmuError,
 }
 
 
@@ -129,8 +133,24 @@ class ModelConfig(C.Structure):
     ]
 
 
+class GgufTensorInfo(C.Structure):
+    _fields_ = [("name", C.c_void_p), ("name_len", C.c_size_t), ("n_dims", C.c_uint32), ("dims", C.c_uint64 * 8), ("dtype", C.c_uint32),
+                ("offset", C.c_uint64), ("len", C.c_uint64)]
+
+
+class SpmDescriptor(C.Structure):
+    _fields_ = [("rows", C.c_uint32), ("cols", C.c_uint32), ("group_size", C.c_uint32), ("encoding", C.c_uint32),
+                ("lane_count", C.c_uint32)]
+
+
+class SpmGroup(C.Structure):
+    _fields_ = [("stream", C.c_uint32), ("scale", C.c_float), ("count", C.c_uint32),
+                ("packed", C.POINTER(C.c_uint8)), ("packed_len", C.c_size_t)]
+
+
 P = C.c_void_p
 U32 = C.c_uint32
+U64 = C.c_uint64
 SZ = C.c_size_t
 I = C.c_int
 F = C.c_float
@@ -181,8 +201,34 @@ SIGNATURES = {
     "emu_time_decode": [P, U32, FP],
     "emu_session_positions": [P, P],
     "emu_session_read_kv": [P, U32, U32, I, P, U32],
+    "emu_gguf_open": [C.c_char_p, C.POINTER(P), C.c_char_p, SZ],
+    "emu_gguf_close": [P],
+    "emu_gguf_error": [P],
+    "emu_gguf_summary": [P, C.POINTER(U32), C.POINTER(U64), C.POINTER(U64), C.POINTER(U64)],
+    "emu_gguf_metadata_at": [P, U64, C.POINTER(P), C.POINTER(SZ), C.POINTER(P), C.POINTER(SZ)],
+    "emu_gguf_metadata_number": [P, C.c_char_p, C.POINTER(C.c_double)],
+    "emu_gguf_tensor_at": [P, U64, C.POINTER(GgufTensorInfo)],
+    "emu_gguf_find": [P, C.c_char_p, C.POINTER(U64)],
+    "emu_gguf_read_range": [P, U64, U64, U64, U64, P],
+    "emu_gguf_upload": [P, P, U64, U64, U64, P],
+    "emu_model_load_gguf": [P, P],
+    "emu_spm_bytes_for": [U32, U64, C.POINTER(U64)],
+    "emu_spm_parse": [P, SZ, C.POINTER(P), C.c_char_p, SZ],
+    "emu_spm_close": [P],
+    "emu_spm_error": [P],
+    "emu_spm_header": [P, C.POINTER(C.c_uint16), C.POINTER(C.c_uint16), C.POINTER(U32)],
+    "emu_spm_descriptor_at": [P, U32, C.POINTER(SpmDescriptor)],
+    "emu_spm_position": [P, C.POINTER(U32), C.POINTER(U64)],
+    "emu_spm_next_group": [P, C.POINTER(I), C.POINTER(SpmGroup)],
+    "emu_spm_upload_stream": [P, P, P, SZ, C.POINTER(U32)],
+    "emu_spm_writer_create": [C.POINTER(SpmDescriptor), U32, C.POINTER(P)],
+    "emu_spm_write_raw_group": [P, F, P, SZ, U64],
+    "emu_spm_writer_finish": [P, C.POINTER(C.POINTER(C.c_uint8)), C.POINTER(SZ)],
+    "emu_spm_writer_error": [P],
+    "emu_spm_writer_destroy": [P],
 }
-_RESTYPE = {"emu_strerror": C.c_char_p, "emu_last_error": C.c_char_p, "emu_moe_workspace_bytes": C.c_size_t}
+_RESTYPE = {"emu_strerror": C.c_char_p, "emu_last_error": C.c_char_p, "emu_moe_workspace_bytes": C.c_size_t,
+            "emu_gguf_error": C.c_char_p, "emu_spm_error": C.c_char_p, "emu_spm_writer_error": C.c_char_p}
 
 _lib = None
 

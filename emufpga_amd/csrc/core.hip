@@ -24,6 +24,8 @@ extern "C" const char *emu_strerror(int status)
     case EMU_E_HIP: return "HIP runtime error";
     case EMU_E_ARG: return "invalid argument";
     case EMU_E_NOMEM: return "allocation refused";
+    case EMU_E_FORMAT: return "file refused by its reader";
+    case EMU_E_IO: return "file read failed";
     default: return "unknown status";
     }
 }
@@ -79,6 +81,10 @@ extern "C" int emu_ctx_destroy(emu_ctx *ctx)
     for (auto &ev : ctx->events)
         if (ev) (void)hipEventDestroy(ev);
     if (ctx->mfma_ws) (void)hipFree(ctx->mfma_ws);
+    for (int i = 0; i < 2; ++i) {
+        if (ctx->stage_ev[i]) (void)hipEventDestroy(ctx->stage_ev[i]);
+        if (ctx->stage[i]) (void)hipHostFree(ctx->stage[i]);
+    }
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return EMU_OK;

@@ -28,6 +28,9 @@ struct emu_ctx {
     char last_error[256] = {0};
     void *mfma_ws = nullptr; // multi-token matvec workspace (mfma.hip), grown on demand
     size_t mfma_ws_bytes = 0;
+    void *stage[2] = {};         // pinned host staging for file -> HBM uploads (files.hip)
+    hipEvent_t stage_ev[2] = {}; // the copy out of each staging buffer
+    size_t stage_bytes = 0;
 };
 
 int emu_hip_fail(emu_ctx *ctx, hipError_t e, const char *what);

@@ -21,7 +21,10 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <stdio.h>
+
 #include <algorithm>
+#include <initializer_list>
 #include <vector>
 
 int emu_build_rope_table(uint32_t positions, uint32_t head_dim, float theta, int fma_form,
@@ -937,6 +940,115 @@ extern "C" int emu_model_synth(emu_model *m, uint64_t seed)
                        ctx->stream, reinterpret_cast<float *>(m->base + m->off_attn_norm), nf, 1.0f);
     EMU_LAUNCH_CHECK(ctx);
     return emu_ctx_sync(ctx);
+}
+
+namespace {
+
+// One tensor of the file and where it lands in the model's residency.
+struct Placement {
+    char name[96];
+    uint32_t dtype;
+    uint32_t n_dims;
+    uint64_t dims[3]; // GGML order: dims[0] is the row length
+    uint8_t *dst;
+    size_t bytes;
+};
+
+int place(emu_model *m, emu_gguf *g, const Placement &p)
+{
+    emu_ctx *ctx = m->ctx;
+    uint64_t idx;
+    if (emu_gguf_find(g, p.name, &idx) != EMU_OK) {
+        snprintf(ctx->last_error, sizeof ctx->last_error, "%s", emu_gguf_error(g));
+        return EMU_E_FORMAT;
+    }
+    emu_gguf_tensor_info t;
+    emu_gguf_tensor_at(g, idx, &t);
+    bool shape = t.n_dims == p.n_dims;
+    for (uint32_t d = 0; shape && d < p.n_dims; ++d) shape = t.dims[d] == p.dims[d];
+    if (t.dtype != p.dtype || !shape || t.len != p.bytes) {
+        snprintf(ctx->last_error, sizeof ctx->last_error,
+                 "tensor %s: dtype %u, %u dims [%llu, %llu, %llu], %llu bytes; the model expects dtype %u, "
+                 "[%llu, %llu, %llu], %zu bytes",
+                 p.name, t.dtype, t.n_dims, (unsigned long long)t.dims[0], (unsigned long long)t.dims[1],
+                 (unsigned long long)t.dims[2], (unsigned long long)t.len, p.dtype, (unsigned long long)p.dims[0],
+                 (unsigned long long)p.dims[1], (unsigned long long)p.dims[2], p.bytes);
+        return EMU_E_FORMAT;
+    }
+    const int st = emu_gguf_upload(ctx, g, idx, 0, p.bytes, p.dst);
+    if (st != EMU_OK && st != EMU_E_HIP)
+        snprintf(ctx->last_error, sizeof ctx->last_error, "%s: %s", p.name, emu_gguf_error(g));
+    return st;
+}
+
+Placement mk(const char *name, uint32_t dtype, std::initializer_list<uint64_t> dims, uint8_t *dst, size_t bytes)
+{
+    Placement p{};
+    snprintf(p.name, sizeof p.name, "%s", name);
+    p.dtype = dtype;
+    p.n_dims = (uint32_t)dims.size();
+    uint32_t i = 0;
+    for (uint64_t d : dims) p.dims[i++] = d;
+    p.dst = dst;
+    p.bytes = bytes;
+    return p;
+}
+
+} // namespace
+
+extern "C" int emu_model_load_gguf(emu_model *m, emu_gguf *g)
+{
+    if (!m || !g) return EMU_E_ARG;
+    const emu_model_config &c = m->cfg;
+    const uint32_t QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim;
+    const uint32_t enc = (uint32_t)c.encoding, F32 = EMU_ENC_F32;
+    std::vector<Placement> ps;
+    ps.push_back(mk("token_embd.weight", enc, {c.hidden, c.vocab}, m->base + m->off_embed, m->embed_bytes));
+    if (!c.tied)
+        ps.push_back(mk("output.weight", enc, {c.hidden, c.vocab}, m->base + m->off_output, m->embed_bytes));
+    ps.push_back(mk("output_norm.weight", F32, {c.hidden}, m->base + m->off_out_norm, sizeof(float) * c.hidden));
+    char nm[96];
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        uint8_t *lw = m->base + m->off_layers + (size_t)l * m->layer_bytes;
+        auto add = [&](const char *suffix, uint32_t dt, std::initializer_list<uint64_t> dims, uint8_t *dst,
+                       size_t bytes) {
+            snprintf(nm, sizeof nm, "blk.%u.%s.weight", l, suffix);
+            ps.push_back(mk(nm, dt, dims, dst, bytes));
+        };
+        add("attn_norm", F32, {c.hidden}, m->base + m->off_attn_norm + sizeof(float) * l * c.hidden,
+            sizeof(float) * c.hidden);
+        add("ffn_norm", F32, {c.hidden}, m->base + m->off_ffn_norm + sizeof(float) * l * c.hidden,
+            sizeof(float) * c.hidden);
+        if (c.qk_norm) {
+            add("attn_q_norm", F32, {c.head_dim}, m->base + m->off_q_norm + sizeof(float) * l * c.head_dim,
+                sizeof(float) * c.head_dim);
+            add("attn_k_norm", F32, {c.head_dim}, m->base + m->off_k_norm + sizeof(float) * l * c.head_dim,
+                sizeof(float) * c.head_dim);
+        }
+        add("attn_q", enc, {c.hidden, QW}, lw + m->off_q, (size_t)QW * m->rb_h);
+        add("attn_k", enc, {c.hidden, KW}, lw + m->off_k, (size_t)KW * m->rb_h);
+        add("attn_v", enc, {c.hidden, KW}, lw + m->off_v, (size_t)KW * m->rb_h);
+        add("attn_output", enc, {QW, c.hidden}, lw + m->off_o, (size_t)c.hidden * m->rb_q);
+        if (m->moe()) {
+            const uint32_t xe = (uint32_t)c.expert_encoding;
+            add("ffn_gate_inp", F32, {c.hidden, c.n_experts}, lw + m->off_r, sizeof(float) * c.n_experts * c.hidden);
+            add("ffn_gate_exps", xe, {c.hidden, c.expert_ff, c.n_experts}, lw + m->off_ge,
+                (size_t)c.n_experts * c.expert_ff * m->rb_he);
+            add("ffn_up_exps", xe, {c.hidden, c.expert_ff, c.n_experts}, lw + m->off_ue,
+                (size_t)c.n_experts * c.expert_ff * m->rb_he);
+            add("ffn_down_exps", xe, {c.expert_ff, c.hidden, c.n_experts}, lw + m->off_de,
+                (size_t)c.n_experts * c.hidden * m->rb_fe);
+        } else {
+            add("ffn_gate", enc, {c.hidden, c.ffn}, lw + m->off_g, (size_t)c.ffn * m->rb_h);
+            add("ffn_up", enc, {c.hidden, c.ffn}, lw + m->off_u, (size_t)c.ffn * m->rb_h);
+            add("ffn_down", enc, {c.ffn, c.hidden}, lw + m->off_d, (size_t)c.hidden * m->rb_f);
+        }
+    }
+    for (const Placement &p : ps) {
+        const int st = place(m, g, p);
+        if (st != EMU_OK) return st;
+    }
+    return EMU_OK;
 }
 
 extern "C" int emu_model_weight_bytes(const emu_model *m, uint64_t *bytes)

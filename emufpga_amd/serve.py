@@ -5,6 +5,10 @@ decode_step (src/step.rs:19-39) for every client at once, each client at its
 own position with its own KV cache (Client, src/session.rs:13-38), and
 ``Session.generate`` is the caller loop of examples/serve-demo.rs:62-91
 (prefill one prompt token per step, then greedy decode), run device-resident.
+
+``Model.from_gguf`` builds the model from a GGUF file: the configuration from
+the file's llama.cpp metadata keys and tensor shapes, every tensor uploaded to
+its place in the model's HBM residency (emu_model_load_gguf).
 """
 from __future__ import annotations
 
@@ -19,6 +23,7 @@ from ._lib import (EMU_STYLE_GRANITE, EMU_STYLE_QWEN3, EMU_STYLE_SMOL, EMU_T_ATT
                    EMU_T_K_NORM, EMU_T_LAYER, EMU_T_OUT_NORM, EMU_T_OUTPUT, EMU_T_Q_NORM, Q6_K, Q8_0,
                    ModelConfig)
 from .device import Context
+from .gguf import GgufFile
 
 
 @dataclass(frozen=True)
@@ -74,6 +79,47 @@ GRANITE_MOE_Q6K = DenseConfig(1024, 16, 8, 64, 0, 49155, 24, 1.5e6, 1e-6, EMU_ST
                               residual_scale=0.22, logit_div=6.0, score_mul=0.015625)
 
 
+_STYLES = {"qwen3": EMU_STYLE_QWEN3, "llama": EMU_STYLE_SMOL, "granitemoe": EMU_STYLE_GRANITE}
+
+
+def config_from_gguf(f: GgufFile) -> DenseConfig:
+    """The decoder shape a GGUF file declares: general.architecture picks the
+    style (qwen3, llama for the SmolLM2 path, granitemoe), {arch}.* keys give
+    the sizes and constants, token_embd gives the vocabulary and encoding,
+    and the presence of output / attn_q_norm tensors decides tied and qk_norm."""
+    meta = f.content.metadata
+    arch = meta.get("general.architecture", "")
+    if arch not in _STYLES:
+        raise ValueError(f"unsupported architecture {arch!r}")
+    names = {t.name for t in f.content.tensors}
+
+    def num(key, default=None):
+        try:
+            return f.number(f"{arch}.{key}")
+        except KeyError:
+            if default is None:
+                raise ValueError(f"GGUF metadata {arch}.{key} is missing") from None
+            return default
+
+    embd = f.tensor("token_embd.weight")
+    hidden, heads = int(num("embedding_length")), int(num("attention.head_count"))
+    style = _STYLES[arch]
+    moe = style == EMU_STYLE_GRANITE
+    kw = {}
+    if moe:
+        kw = dict(n_experts=int(num("expert_count")), experts_used=int(num("expert_used_count")),
+                  expert_ff=int(num("expert_feed_forward_length", num("feed_forward_length", 0))),
+                  expert_encoding=f.tensor("blk.0.ffn_gate_exps.weight").dtype,
+                  embed_scale=float(num("embedding_scale", 1.0)), residual_scale=float(num("residual_scale", 1.0)),
+                  logit_div=float(num("logit_scale", 1.0)), score_mul=float(num("attention.scale", 0.0)))
+    return DenseConfig(hidden=hidden, heads=heads, kv_heads=int(num("attention.head_count_kv", heads)),
+                       head_dim=int(num("attention.key_length", hidden // heads)),
+                       ffn=0 if moe else int(num("feed_forward_length")), vocab=int(embd.dims[1]),
+                       layers=int(num("block_count")), rope_theta=float(num("rope.freq_base", 10000.0)),
+                       eps=float(num("attention.layer_norm_rms_epsilon")), style=style, encoding=embd.dtype,
+                       tied="output.weight" not in names, qk_norm="blk.0.attn_q_norm.weight" in names, **kw)
+
+
 class Model:
     """Weights of a dense decoder in one HBM allocation (emu_model)."""
 
@@ -98,6 +144,18 @@ class Model:
 
     def synth(self, seed: int) -> None:
         self.ctx.check(self.ctx.lib.emu_model_synth(self.h, seed), "emu_model_synth")
+
+    def load_gguf(self, f: GgufFile) -> None:
+        """Every tensor from an open GGUF file, by name, into HBM."""
+        st = self.ctx.lib.emu_model_load_gguf(self.h, f.h)
+        self.ctx.check(st, "emu_model_load_gguf")
+
+    @classmethod
+    def from_gguf(cls, ctx: Context, path, cfg: DenseConfig | None = None) -> "Model":
+        with GgufFile(path) as f:
+            m = cls(ctx, cfg or config_from_gguf(f))
+            m.load_gguf(f)
+        return m
 
     def tensor(self, kind: int, layer: int = 0) -> tuple[int, int]:
         p, n = C.c_void_p(), C.c_size_t()

@@ -50,7 +50,14 @@ typedef enum emu_status {
     EMU_E_CONFIG = 7,
     EMU_E_HIP = 8,   /* a HIP runtime call failed */
     EMU_E_ARG = 9,   /* null pointer or out-of-range argument */
-    EMU_E_NOMEM = 10 /* device or host allocation refused (tensor.rs:108-110) */
+    EMU_E_NOMEM = 10, /* device or host allocation refused (tensor.rs:108-110) */
+    /* A file refused by its reader: the GGUF parse errors of
+     * spm-gguf/src/parse.rs:31-182 and wire.rs:12-90, the .spm HeaderError
+     * (spm-header/src/model.rs:63-89) and LayoutError (spm-layout/src/model.rs:127-145),
+     * FileError::Incomplete (spm-file/src/error.rs:34-40); the message is in
+     * the reader's error string. */
+    EMU_E_FORMAT = 11,
+    EMU_E_IO = 12 /* the operating system refused a read (tensor.rs:59-66) */
 } emu_status;
 
 /* GGUF dtype ids (spm-gguf/src/parse.rs:10-29). */
@@ -280,6 +287,120 @@ int emu_session_positions(emu_session *s, uint32_t *h_positions);
 /* Copy a client's cached K or V rows for one layer (positions x kv_width f32). */
 int emu_session_read_kv(emu_session *s, uint32_t client, uint32_t layer, int which_v,
                         float *h_out, uint32_t positions);
+
+/* ---- GGUF files (components/cli/crates/spm-gguf) ------------------------
+ * A bounded, non-executing reader: the header, metadata and tensor directory
+ * are parsed under the reference's limits (lib.rs:11-16) with its error texts;
+ * tensor bodies are reached only through bounded range reads. */
+typedef struct emu_gguf emu_gguf;
+typedef struct emu_gguf_tensor_info { /* TensorInfo (spm-gguf/src/model.rs:3-10) */
+    const char *name;                 /* valid while the reader is open */
+    size_t name_len;                  /* bytes of name (names may hold NUL) */
+    uint32_t n_dims;
+    uint64_t dims[8];                 /* GGML order: dims[0] is the row length */
+    uint32_t dtype;                   /* GGML dtype id */
+    uint64_t offset;                  /* absolute file offset of the tensor's bytes */
+    uint64_t len;                     /* bytes */
+} emu_gguf_tensor_info;
+
+/* spm_gguf::read (parse.rs:157-182).  On failure h_err (may be NULL) receives
+ * the reference's message and no reader is returned. */
+int emu_gguf_open(const char *path, emu_gguf **out, char *h_err, size_t err_len);
+int emu_gguf_close(emu_gguf *g);
+/* Message of the reader's last failed call. */
+const char *emu_gguf_error(const emu_gguf *g);
+/* Content's version, metadata_count, tensor_data_offset and tensor count. */
+int emu_gguf_summary(const emu_gguf *g, uint32_t *version, uint64_t *metadata_count,
+                     uint64_t *tensor_data_offset, uint64_t *tensor_count);
+/* Metadata entry `index` in file order, the value rendered as the reference's
+ * Content::metadata holds it ("<6>" for f32, "<9>" for arrays, "<12>" for f64).
+ * The strings live as long as the reader; the lengths count every byte. */
+int emu_gguf_metadata_at(const emu_gguf *g, uint64_t index, const char **key, size_t *key_len,
+                         const char **value, size_t *value_len);
+/* The numeric value of a scalar metadata entry, floats included (the
+ * reference keeps no float values; model configuration needs them).
+ * EMU_E_ARG when absent, EMU_E_UNSUPPORTED for strings and arrays. */
+int emu_gguf_metadata_number(const emu_gguf *g, const char *key, double *value);
+/* Tensor `index` in ascending file offset (Content::tensors order). */
+int emu_gguf_tensor_at(const emu_gguf *g, uint64_t index, emu_gguf_tensor_info *info);
+/* Index of a tensor by name; EMU_E_FORMAT "missing tensor NAME"
+ * (spm-granite-moe/src/weights.rs:9-15). */
+int emu_gguf_find(emu_gguf *g, const char *name, uint64_t *index);
+/* read_tensor_range (tensor.rs:35-67): len bytes at rel_off inside the tensor,
+ * refused past max_bytes or past the tensor's end. */
+int emu_gguf_read_range(emu_gguf *g, uint64_t index, uint64_t rel_off, uint64_t len, uint64_t max_bytes,
+                        void *h_dst);
+/* The same range placed in device memory: the file is read through two
+ * pinned 64 MiB host buffers so reading overlaps the copies.  Synchronous. */
+int emu_gguf_upload(emu_ctx *ctx, emu_gguf *g, uint64_t index, uint64_t rel_off, uint64_t len, void *d_dst);
+
+/* Every weight tensor of a model from a GGUF file of the model's architecture,
+ * by the reference's tensor names (spm-qwen3-slice/src/model.rs:42-167,
+ * spm-granite-moe/src/model.rs, weights.rs:57-94): token_embd, output (untied),
+ * output_norm, blk.N.{attn_norm, attn_q, attn_k, attn_v, attn_output,
+ * attn_q_norm, attn_k_norm (qk_norm), ffn_norm, ffn_gate, ffn_up, ffn_down}, or
+ * for mixture-of-experts layers ffn_gate_inp (f32 router) and the expert-major
+ * ffn_gate_exps / ffn_up_exps / ffn_down_exps.  Each tensor's dtype and shape
+ * must be what the model was created with (EMU_E_FORMAT otherwise, message in
+ * emu_last_error). */
+int emu_model_load_gguf(emu_model *model, emu_gguf *g);
+
+/* ---- .spm files (components/format/crates/spm-file; docs/spm-format.md) -- */
+/* Encoding profiles (spm-layout/src/model.rs:14-58, codes :48-58). */
+enum {
+    EMU_SPM_TERNARY = 1, EMU_SPM_F32 = 2, EMU_SPM_BF16 = 3,
+    EMU_SPM_Q6K = 4, EMU_SPM_Q5K = 5, EMU_SPM_Q8_0 = 6
+};
+typedef struct emu_spm emu_spm;
+typedef struct emu_spm_writer emu_spm_writer;
+typedef struct emu_spm_descriptor { /* OpDescriptor (spm-layout/src/model.rs:113-125) */
+    uint32_t rows, cols, group_size;
+    uint32_t encoding;   /* EMU_SPM_* */
+    uint32_t lane_count; /* 16 bits on the wire */
+} emu_spm_descriptor;
+typedef struct emu_spm_group { /* Group (spm-file/src/read.rs:16-25) */
+    uint32_t stream;
+    float scale;
+    uint32_t count;          /* weights in the group; short for a stream's last group */
+    const uint8_t *packed;   /* points into the parsed bytes */
+    size_t packed_len;
+} emu_spm_group;
+
+/* Encoding::bytes_for (spm-layout/src/model.rs:80-91). */
+int emu_spm_bytes_for(uint32_t encoding, uint64_t count, uint64_t *bytes);
+/* SpmReader::parse (read.rs:48-63): header and stream directory.  The reader
+ * borrows h_bytes, which must outlive it.  On failure h_err receives the
+ * reference's HeaderError / LayoutError text. */
+int emu_spm_parse(const void *h_bytes, size_t len, emu_spm **out, char *h_err, size_t err_len);
+int emu_spm_close(emu_spm *r);
+const char *emu_spm_error(const emu_spm *r);
+int emu_spm_header(const emu_spm *r, uint16_t *major, uint16_t *minor, uint32_t *stream_count);
+int emu_spm_descriptor_at(const emu_spm *r, uint32_t index, emu_spm_descriptor *d);
+/* The cursor: the stream and group next_group would return. */
+int emu_spm_position(const emu_spm *r, uint32_t *stream, uint64_t *group);
+/* SpmReader::next_group (read.rs:70-88): *has_group = 0 at the end of the
+ * payload; EMU_E_TRUNCATED "payload truncated: group needs N bytes, M remain"
+ * leaves the cursor where it was. */
+int emu_spm_next_group(emu_spm *r, int *has_group, emu_spm_group *group);
+/* The reader's current stream, from its first group, into device memory in
+ * the layout the kernels read: Q6K / Q5K / Q8_0 blocks back to back in their
+ * source row-major order (each group's inert scale dropped on the device), or
+ * an F32 stream's column-major weights as a row-major rows x cols matrix.
+ * Consumes the stream; *stream (may be NULL) receives its index.  Block
+ * streams need group_size and rows*cols in whole blocks. */
+int emu_spm_upload_stream(emu_ctx *ctx, emu_spm *r, void *d_dst, size_t dst_len, uint32_t *stream);
+/* SpmWriter (spm-file/src/write.rs:15-107): new, write_raw_group, finish.
+ * write_raw_group refuses a count or payload length the layout does not
+ * expect (EMU_E_SHAPE, "group expects N weights, got M") and a group past the
+ * last stream (EMU_E_FORMAT, "only W of D streams were written"); finish
+ * refuses a file with groups still owed.  The finished bytes stay owned by the
+ * writer until it is destroyed. */
+int emu_spm_writer_create(const emu_spm_descriptor *descs, uint32_t n, emu_spm_writer **out);
+int emu_spm_write_raw_group(emu_spm_writer *w, float scale, const void *h_payload, size_t payload_len,
+                            uint64_t count);
+int emu_spm_writer_finish(emu_spm_writer *w, const uint8_t **h_bytes, size_t *len);
+const char *emu_spm_writer_error(const emu_spm_writer *w);
+int emu_spm_writer_destroy(emu_spm_writer *w);
 
 #ifdef __cplusplus
 }
