@@ -24,7 +24,9 @@ import argparse
 import ctypes as C
 import json
 import os
+import shutil
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -34,8 +36,8 @@ sys.path.insert(0, ROOT)
 
 from emufpga_amd import _lib  # noqa: E402
 from emufpga_amd.device import Context  # noqa: E402
-from emufpga_amd.gguf import row_bytes  # noqa: E402
-from emufpga_amd.serve import GRANITE_MOE_Q6K, QWEN3_8B_Q6K, Model, Session  # noqa: E402
+from emufpga_amd.gguf import GgufFile, row_bytes  # noqa: E402
+from emufpga_amd.serve import GRANITE_MOE_Q6K, QWEN3_8B_Q6K, DenseConfig, Model, Session  # noqa: E402
 
 METRIC = "decode tok/s at batch 1 and 8; achieved HBM GB/s vs 8 TB/s peak"
 HBM_PEAK_GBS = 8000.0
@@ -150,6 +152,37 @@ def cpu_baseline(model: Model, budget_s: float = 40.0) -> dict:
     }
 
 
+def load_leg(ctx) -> dict:
+    """GGUF file -> HBM: a Qwen3-8B-width decoder cut to 4 layers (plus its
+    full 151936-row embedding and output) written to a GGUF file, then every
+    tensor placed by emu_model_load_gguf.  The file was just written, so its
+    pages come from the page cache: this is the read + PCIe placement rate,
+    not a cold-disk rate."""
+    cfg = DenseConfig(**{**QWEN3_8B_Q6K.__dict__, "layers": 4})
+    tmp = tempfile.mkdtemp(prefix="emu_gguf_")
+    try:
+        path = os.path.join(tmp, "qwen3_8b_4layers_q6k.gguf")
+        src = Model(ctx, cfg)
+        src.synth(4242)
+        nbytes = src.save_gguf(path)
+        src.close()
+        with GgufFile(path) as f:
+            dst = Model(ctx, cfg)
+            t0 = time.perf_counter()
+            dst.load_gguf(f)
+            ctx.sync()
+            dt = time.perf_counter() - t0
+            tensor_bytes = sum(t.len for t in f.content.tensors)
+        dst.close()
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    gbs = tensor_bytes / dt / 1e9
+    log(f"GGUF load: {tensor_bytes / 1e9:.2f} GB of tensors in {dt * 1e3:.1f} ms -> {gbs:.2f} GB/s")
+    return {"value": round(gbs, 2), "unit": "GB/s", "tensor_bytes": tensor_bytes, "file_bytes": nbytes,
+            "seconds": round(dt, 4),
+            "workload": "Qwen3-8B-width Q6_K decoder cut to 4 layers, GGUF file in the page cache -> HBM"}
+
+
 def moe_leg(ctx, rng) -> dict:
     """Granite-shaped MoE decode, 4 clients, 256-token prompts, 128 timed steps.
     The routing is the model's own router on seeded synthetic weights (close to
@@ -187,6 +220,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-batch8", action="store_true")
     ap.add_argument("--no-moe", action="store_true", help="skip the Granite MoE decode leg")
+    ap.add_argument("--no-load", action="store_true", help="skip the GGUF -> HBM load leg")
     ap.add_argument("--batch8-only", action="store_true",
                     help="only the 8-client decode, logged without the JSON line; for profiling")
     ap.add_argument("--roofline-rounds", type=int, default=8)
@@ -298,6 +332,8 @@ def main() -> int:
                          "matvec": "int8 MFMA (v_mfma_i32_32x32x16_i8), activation limbs as the A operand"}
     if not args.no_moe:
         out["moe_granite_b4"] = moe_leg(ctx, rng)
+    if not args.no_load:
+        out["gguf_load"] = load_leg(ctx)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(model)
     print(json.dumps(out), flush=True)

@@ -14,6 +14,7 @@ keeps a file open for many range reads and for uploads into device memory.
 from __future__ import annotations
 
 import ctypes as C
+import struct
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -203,3 +204,57 @@ def read_tensor_range(path, tensor: TensorInfo, relative_offset: int, length: in
 def read_tensor_bytes(path, tensor: TensorInfo, max_bytes: int) -> bytes:
     """spm_gguf::read_tensor_bytes (tensor.rs:21-28)."""
     return read_tensor_range(path, tensor, 0, tensor.len, max_bytes)
+
+
+# metadata value types (spm-gguf/src/wire.rs:55-90)
+(MT_U8, MT_I8, MT_U16, MT_I16, MT_U32, MT_I32, MT_F32, MT_BOOL, MT_STR, MT_ARR, MT_U64, MT_I64,
+ MT_F64) = range(13)
+_MT_FMT = {MT_U8: "B", MT_I8: "b", MT_U16: "H", MT_I16: "h", MT_U32: "I", MT_I32: "i", MT_F32: "f", MT_BOOL: "B",
+           MT_U64: "Q", MT_I64: "q", MT_F64: "d"}
+
+
+def _mt_str(s) -> bytes:
+    b = s.encode() if isinstance(s, str) else bytes(s)
+    return struct.pack("<Q", len(b)) + b
+
+
+def _mt_value(ty: int, v) -> bytes:
+    if ty == MT_STR:
+        return _mt_str(v)
+    if ty == MT_ARR:
+        inner, items = v
+        return struct.pack("<IQ", inner, len(items)) + b"".join(_mt_value(inner, x) for x in items)
+    return struct.pack("<" + _MT_FMT[ty], v)
+
+
+def write(out, metadata, tensors, align: int = 32) -> int:
+    """A GGUF v3 file: metadata [(key, type, value)] and tensors
+    [(name, dims in GGML order, dtype, data)], each tensor's data at an
+    `align`-aligned offset after the directory (the layout read() parses).
+    `out` is a path or a binary file object; returns the bytes written."""
+    head = bytearray(b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(metadata)))
+    for key, ty, v in metadata:
+        head += _mt_str(key) + struct.pack("<I", ty) + _mt_value(ty, v)
+    offs, at = [], 0
+    for _, _, _, data in tensors:
+        offs.append(at)
+        at = (at + memoryview(data).nbytes + align - 1) // align * align
+    for (name, dims, dtype, _), off in zip(tensors, offs):
+        head += _mt_str(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+        head += struct.pack("<IQ", dtype, off)
+    base = (len(head) + align - 1) // align * align
+    head += b"\0" * (base - len(head))
+    own = not hasattr(out, "write")
+    f = open(out, "wb") if own else out
+    try:
+        f.write(head)
+        pos = 0
+        for (_, _, _, data), off in zip(tensors, offs):
+            f.write(b"\0" * (off - pos))
+            mv = memoryview(data).cast("B")
+            f.write(mv)
+            pos = off + mv.nbytes
+    finally:
+        if own:
+            f.close()
+    return base + pos

@@ -23,7 +23,7 @@ from ._lib import (EMU_STYLE_GRANITE, EMU_STYLE_QWEN3, EMU_STYLE_SMOL, EMU_T_ATT
                    EMU_T_K_NORM, EMU_T_LAYER, EMU_T_OUT_NORM, EMU_T_OUTPUT, EMU_T_Q_NORM, Q6_K, Q8_0,
                    ModelConfig)
 from .device import Context
-from .gguf import GgufFile
+from .gguf import F32, MT_F32, MT_STR, MT_U32, GgufFile, row_bytes, write
 
 
 @dataclass(frozen=True)
@@ -120,6 +120,74 @@ def config_from_gguf(f: GgufFile) -> DenseConfig:
                        tied="output.weight" not in names, qk_norm="blk.0.attn_q_norm.weight" in names, **kw)
 
 
+def gguf_tensors(cfg: DenseConfig, w: dict):
+    """A model's weights (Model.host_weights()) as GGUF (metadata, tensors)
+    under llama.cpp's names, shapes in GGML order (row length first): the
+    inverse of config_from_gguf and emu_model_load_gguf."""
+    H, QW, KW = cfg.hidden, cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    enc, moe = cfg.encoding, cfg.style == _lib.EMU_STYLE_GRANITE
+    rb_h, rb_q = row_bytes(enc, H), row_bytes(enc, QW)
+    t = [("token_embd.weight", (H, cfg.vocab), enc, w["embed"].data)]
+    if not cfg.tied:
+        t.append(("output.weight", (H, cfg.vocab), enc, w["output"].data))
+    t.append(("output_norm.weight", (H,), F32, w["out_norm"].data))
+    layers = w["layers"]
+    if moe:
+        rb_he, rb_fe = row_bytes(cfg.expert_encoding, H), row_bytes(cfg.expert_encoding, cfg.expert_ff)
+        off_o = (QW + 2 * KW) * rb_h
+        off_r = (off_o + H * rb_q + 15) // 16 * 16
+        ge = cfg.n_experts * cfg.expert_ff * rb_he
+        de = cfg.n_experts * H * rb_fe
+        lb = (off_r + 4 * cfg.n_experts * H + 2 * ge + de + 15) // 16 * 16
+    else:
+        rb_f = row_bytes(enc, cfg.ffn)
+        lb = (QW + 2 * KW) * rb_h + H * rb_q + 2 * cfg.ffn * rb_h + H * rb_f
+    assert layers.size == lb * cfg.layers
+    for l in range(cfg.layers):
+        blob = layers[l * lb:(l + 1) * lb]
+        at = 0
+
+        def take(name, dims, dtype, n):
+            nonlocal at
+            t.append((f"blk.{l}.{name}.weight", dims, dtype, blob[at:at + n].data))
+            at += n
+
+        t.append((f"blk.{l}.attn_norm.weight", (H,), F32, w["attn_norm"][l * H:(l + 1) * H].data))
+        t.append((f"blk.{l}.ffn_norm.weight", (H,), F32, w["ffn_norm"][l * H:(l + 1) * H].data))
+        if cfg.qk_norm:
+            d = cfg.head_dim
+            t.append((f"blk.{l}.attn_q_norm.weight", (d,), F32, w["q_norm"][l * d:(l + 1) * d].data))
+            t.append((f"blk.{l}.attn_k_norm.weight", (d,), F32, w["k_norm"][l * d:(l + 1) * d].data))
+        take("attn_q", (H, QW), enc, QW * rb_h)
+        take("attn_k", (H, KW), enc, KW * rb_h)
+        take("attn_v", (H, KW), enc, KW * rb_h)
+        take("attn_output", (QW, H), enc, H * rb_q)
+        if moe:
+            at = off_r
+            take("ffn_gate_inp", (H, cfg.n_experts), F32, 4 * cfg.n_experts * H)
+            take("ffn_gate_exps", (H, cfg.expert_ff, cfg.n_experts), cfg.expert_encoding, ge)
+            take("ffn_up_exps", (H, cfg.expert_ff, cfg.n_experts), cfg.expert_encoding, ge)
+            take("ffn_down_exps", (cfg.expert_ff, H, cfg.n_experts), cfg.expert_encoding, de)
+        else:
+            take("ffn_gate", (H, cfg.ffn), enc, cfg.ffn * rb_h)
+            take("ffn_up", (H, cfg.ffn), enc, cfg.ffn * rb_h)
+            take("ffn_down", (cfg.ffn, H), enc, H * row_bytes(enc, cfg.ffn))
+    arch = {v: k for k, v in _STYLES.items()}[cfg.style]
+    u32 = [("embedding_length", H), ("block_count", cfg.layers), ("attention.head_count", cfg.heads),
+           ("attention.head_count_kv", cfg.kv_heads), ("attention.key_length", cfg.head_dim)]
+    f32 = [("rope.freq_base", cfg.rope_theta), ("attention.layer_norm_rms_epsilon", cfg.eps)]
+    if moe:
+        u32 += [("expert_count", cfg.n_experts), ("expert_used_count", cfg.experts_used),
+                ("expert_feed_forward_length", cfg.expert_ff)]
+        f32 += [("embedding_scale", cfg.embed_scale), ("residual_scale", cfg.residual_scale),
+                ("logit_scale", cfg.logit_div), ("attention.scale", cfg.score_mul)]
+    else:
+        u32.append(("feed_forward_length", cfg.ffn))
+    meta = [("general.architecture", MT_STR, arch), ("general.alignment", MT_U32, 64)]
+    meta += [(f"{arch}.{k}", MT_U32, v) for k, v in u32] + [(f"{arch}.{k}", MT_F32, v) for k, v in f32]
+    return meta, t
+
+
 class Model:
     """Weights of a dense decoder in one HBM allocation (emu_model)."""
 
@@ -149,6 +217,11 @@ class Model:
         """Every tensor from an open GGUF file, by name, into HBM."""
         st = self.ctx.lib.emu_model_load_gguf(self.h, f.h)
         self.ctx.check(st, "emu_model_load_gguf")
+
+    def save_gguf(self, path) -> int:
+        """Write every tensor to a GGUF file that from_gguf reads back."""
+        meta, tensors = gguf_tensors(self.cfg, self.host_weights())
+        return write(path, meta, tensors, align=64)
 
     @classmethod
     def from_gguf(cls, ctx: Context, path, cfg: DenseConfig | None = None) -> "Model":

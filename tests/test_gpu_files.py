@@ -57,7 +57,7 @@ def test_gguf_model_holds_the_same_bytes_and_decodes_identically(ctx, tmp_path, 
     _, back = ggufw.model_file_tensors(b.cfg, b.host_weights())
     assert [(n, d, t) for n, d, t, _ in back] == [(n, d, t) for n, d, t, _ in tensors]
     for (n, _, _, x), (_, _, _, y) in zip(tensors, back):
-        assert x == y, n
+        assert bytes(x) == bytes(y), n
     prompts = np.array([[3, 1, 4, 1], [2, 7, 1, 8]], np.uint32)
     sa, sb = Session(a, 2, 48), Session(b, 2, 48)
     for t in range(4):
