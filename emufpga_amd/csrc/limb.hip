@@ -329,15 +329,26 @@ __global__ __launch_bounds__(EMU_WAVE * LimbShape<S>::W) void qmv_limb_kernel(Qm
     if (a.keys && sl == 0 && lane == EMU_WAVE - 1) a.keys[grg] = best;
 }
 
-constexpr int kLimbD = 2;
+// Rows in flight per wavefront and workgroups per CU, measured per shape on
+// weights streamed from HBM: one row in flight with two workgroups per CU for
+// the gate|up pair (four waves per SIMD hide the latency better than deeper
+// prefetch in fewer waves: 18.0 us against 21.2 us with two rows and one
+// workgroup), one row and one workgroup for the other 4096-column matvecs
+// (q|k|v 7.6 against 8.7 us, o 6.2 against 6.5, the 151936-row output 92.8
+// against 95.8), and two rows for the 12288-column down projection.
+template <int S, bool DUAL> struct LimbTune {
+    static constexpr int D = S == 1 ? 1 : 2;
+    static constexpr int PER_CU = DUAL ? 2 : 1;
+};
 
 template <class LF, int S, bool DUAL, bool NORM, bool ACC>
 void launch_limb_cfg(emu_ctx *ctx, const QmvArgs &a, int blocks)
 {
     using SH = LimbShape<S>;
+    constexpr int D = LimbTune<S, DUAL>::D;
     const int total_rg = blocks * SH::RG;
-    const int rounds = (a.rows + total_rg * kLimbD - 1) / (total_rg * kLimbD);
-    hipLaunchKernelGGL((qmv_limb_kernel<LF, S, kLimbD, DUAL, NORM, ACC>), dim3(blocks), dim3(SH::T), 0, ctx->stream,
+    const int rounds = (a.rows + total_rg * D - 1) / (total_rg * D);
+    hipLaunchKernelGGL((qmv_limb_kernel<LF, S, D, DUAL, NORM, ACC>), dim3(blocks), dim3(SH::T), 0, ctx->stream,
                        a, rounds);
 }
 
@@ -347,9 +358,7 @@ int launch_limb_s(emu_ctx *ctx, const QmvArgs &a, int *key_slots)
     const bool dual = a.w_up != nullptr, norm = a.gain != nullptr, acc = a.accumulate != 0;
     if (dual && acc) return EMU_E_ARG; // the fused entry point never asks for this
     const int cus = ctx->cus > 0 ? ctx->cus : 256;
-    // One workgroup per CU: measured fastest for every decode shape (more
-    // resident waves only add contention for the same HBM stream).
-    int per_cu = 1;
+    int per_cu = dual ? LimbTune<S, true>::PER_CU : LimbTune<S, false>::PER_CU;
     if (const char *v = getenv("EMU_LIMB_BPC")) { // sweep override
         const int f = atoi(v);
         if (f >= 1 && f <= 4) per_cu = f;
