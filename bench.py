@@ -41,7 +41,7 @@ from emufpga_amd.serve import GRANITE_MOE_Q6K, QWEN3_8B_Q6K, DenseConfig, Model,
 
 METRIC = "decode tok/s at batch 1 and 8; achieved HBM GB/s vs 8 TB/s peak"
 HBM_PEAK_GBS = 8000.0
-KERNEL = "qmv_limb_kernel<LimbQ6K, S=1, D=2, dual, norm> (fused gate|up, 2 x 12288 x 4096 Q6_K)"
+KERNEL = "qmv_limb_kernel<LimbQ6K, S=1, D=1, dual, norm> (fused gate|up, 2 x 12288 x 4096 Q6_K)"
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "qmv_limb_gate_up_qwen3_8b_pmc.txt")
 COPY_BYTES = 256 << 20  # calibration copy for the PMC byte counters
 
