@@ -339,6 +339,81 @@ __device__ __forceinline__ float wave_sum(float v)
     return v;
 }
 
+// Workgroup sum: wavefront butterflies, then the wavefront totals in order.
+__device__ __forceinline__ float emu_block_sum(float v, float *red)
+{
+    v = wave_sum(v);
+    const int lane = threadIdx.x & (EMU_WAVE - 1), w = threadIdx.x / EMU_WAVE;
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float s = 0.0f;
+    const int nw = (blockDim.x + EMU_WAVE - 1) / EMU_WAVE;
+    for (int i = 0; i < nw; ++i) s += red[i];
+    return s;
+}
+
+__device__ __forceinline__ uint64_t emu_wave_max_u64(uint64_t k)
+{
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint64_t o = __shfl_xor(k, off, EMU_WAVE);
+        k = o > k ? o : k;
+    }
+    return k;
+}
+
+// Router softmax and top-k of one token (moe::route, spm-granite-moe/src/moe.rs:17-35):
+// p[0..n_experts) holds the logits in LDS and is overwritten; sel holds k
+// floats of LDS.  Softmax with the max subtracted, the sum a left fold in
+// expert order, then the k greatest probabilities in total order, lower id
+// first on ties, in that order (k rounds of argmax with the winner removed);
+// weights are the selected probabilities over their left-fold total.  Every thread of the workgroup calls it (it holds
+// the workgroup barriers); wavefront 0 does the work.
+__device__ __forceinline__ void emu_route_token(float *p, float *sel, int n_experts, int k, int32_t *ids,
+                                                float *weights)
+{
+    const int lane = threadIdx.x;
+    const bool w0 = threadIdx.x < EMU_WAVE;
+    if (w0) {
+        float m = -INFINITY;
+        for (int e = lane; e < n_experts; e += EMU_WAVE) m = fmaxf(m, p[e]);
+        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, EMU_WAVE));
+        for (int e = lane; e < n_experts; e += EMU_WAVE) p[e] = expf(p[e] - m);
+    }
+    __syncthreads();
+    if (w0) {
+        // lane 0's reads are complete before the shuffle hands the sum out,
+        // so the wavefront may overwrite p after it
+        float sum = 0.0f;
+        if (lane == 0)
+            for (int e = 0; e < n_experts; ++e) sum = __fadd_rn(sum, p[e]);
+        sum = __shfl(sum, 0, EMU_WAVE);
+        for (int e = lane; e < n_experts; e += EMU_WAVE) p[e] = p[e] / sum;
+    }
+    __syncthreads();
+    // The k rounds of (greatest, lowest id) with the winner removed are the
+    // first k places of one ranking: expert e's place is the number of
+    // experts with a greater key (keys are distinct), computed in one pass.
+    if (w0) {
+        for (int e = lane; e < n_experts; e += EMU_WAVE) {
+            const uint64_t ke = emu_select_key(p[e], (uint32_t)e, 0);
+            int rank = 0;
+            for (int j = 0; j < n_experts; ++j) rank += emu_select_key(p[j], (uint32_t)j, 0) > ke ? 1 : 0;
+            if (rank < k) {
+                ids[rank] = e;
+                sel[rank] = p[e];
+            }
+        }
+    }
+    __syncthreads();
+    if (lane == 0) {
+        float total = 0.0f;
+        for (int r = 0; r < k; ++r) total = __fadd_rn(total, sel[r]);
+        for (int r = 0; r < k; ++r) weights[r] = sel[r] / total;
+    }
+}
+
 // ------------------------------------------------------------- launchers --
 // Implemented per translation unit; declared here for the model code.
 struct QmvArgs {
@@ -429,4 +504,9 @@ struct EmuAttnLaunch {
     float *xs;
 };
 int emu_launch_attn(emu_ctx *ctx, const EmuAttnLaunch &l);
+// emu_moe_ffn whose weighted expert sum is added to the residual stream,
+// state = state + sum * scale with two roundings (moe.hip).
+int emu_moe_ffn_resid(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok, const int32_t *d_ids,
+                      const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_state,
+                      float scale);
 int emu_attn_max_chunks(int context);

@@ -69,7 +69,7 @@ struct emu_session {
           *partial = nullptr, *rope = nullptr;
     // mixture-of-experts scratch: normalised input, router logits, routes,
     // expert output, and the selected-expert FFN's workspace
-    float *xn = nullptr, *rlog = nullptr, *rwts = nullptr, *moe_out = nullptr;
+    float *xn = nullptr, *rlog = nullptr, *rwts = nullptr;
     int32_t *rids = nullptr;
     void *moe_ws = nullptr;
     size_t moe_ws_bytes = 0;
@@ -291,12 +291,78 @@ __global__ __launch_bounds__(EMU_WAVE) void router_kernel(const float *w, const 
     if (lane == 0) logits[(size_t)c * experts + e] = acc;
 }
 
-// state += v * s with two roundings (add_scaled, spm-granite-moe/src/math.rs:31-33).
-__global__ __launch_bounds__(kThreads) void add_scaled_kernel(float *state, const float *v, size_t n, float s)
+// The MoE layer's gate, one workgroup per client: the FFN RMSNorm of the
+// residual stream (the arithmetic of rms_norm_kernel, kept for the experts),
+// the f32 router logits (router_kernel's per-lane order: lane l folds columns
+// 4l + 256q, q = 0..NK-1, then a butterfly; the normalised row read from
+// LDS) and the softmax / top-k route (moe.rs:17-35, 132-138).  A wavefront
+// takes experts w, w + 4, ...; every router load of a batch of up to eight
+// experts is issued before the first fma.
+template <int NK>
+__global__ __launch_bounds__(kThreads) void moe_gate_kernel(const float *state, const float *gain, const float *router,
+                                                            int experts, int k, float eps, float *xn, int32_t *ids,
+                                                            float *weights)
 {
-    const size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x;
-    if (i < n) state[i] = emu_resid_add(state[i], v[i], s);
+    constexpr int width = NK * 4 * EMU_WAVE;
+    constexpr int EB = 32 / NK < 8 ? 32 / NK : 8; // experts per load batch
+    constexpr int NW = kThreads / EMU_WAVE;
+    __shared__ __align__(16) float xs[width];
+    __shared__ float red[NW];
+    __shared__ float p[256];
+    __shared__ float sel[64];
+    const int c = blockIdx.x, tid = threadIdx.x, lane = tid & (EMU_WAVE - 1), w = tid / EMU_WAVE;
+    float4 rw[EB][NK];
+    auto load_batch = [&](int e0) {
+#pragma unroll
+        for (int j = 0; j < EB; ++j) {
+            int e = e0 + NW * j;
+            e = e < experts ? e : experts - 1; // a valid row; its result is dropped
+            const float *row = router + (size_t)e * width + 4 * lane;
+#pragma unroll
+            for (int q = 0; q < NK; ++q) rw[j][q] = *reinterpret_cast<const float4 *>(row + 4 * EMU_WAVE * q);
+        }
+    };
+    load_batch(w); // the router rows do not wait for the norm
+    const float *xr = state + (size_t)c * width;
+    float s = 0.0f;
+    for (int i = tid; i < width; i += kThreads) s = __builtin_fmaf(xr[i], xr[i], s);
+    s = emu_block_sum(s, red);
+    const float scale = 1.0f / sqrtf(s / (float)width + eps);
+    for (int i = tid; i < width; i += kThreads) {
+        const float v = __fmul_rn(__fmul_rn(xr[i], scale), gain[i]);
+        xs[i] = v;
+        xn[(size_t)c * width + i] = v;
+    }
+    __syncthreads();
+    float4 xv[NK];
+#pragma unroll
+    for (int q = 0; q < NK; ++q) xv[q] = *reinterpret_cast<const float4 *>(xs + 4 * lane + 4 * EMU_WAVE * q);
+    for (int e0 = w; e0 < experts; e0 += NW * EB) {
+        float dots[EB];
+#pragma unroll
+        for (int j = 0; j < EB; ++j) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int q = 0; q < NK; ++q) {
+                acc = __builtin_fmaf(rw[j][q].x, xv[q].x, acc);
+                acc = __builtin_fmaf(rw[j][q].y, xv[q].y, acc);
+                acc = __builtin_fmaf(rw[j][q].z, xv[q].z, acc);
+                acc = __builtin_fmaf(rw[j][q].w, xv[q].w, acc);
+            }
+            dots[j] = acc;
+        }
+        if (e0 + NW * EB < experts) load_batch(e0 + NW * EB);
+#pragma unroll
+        for (int j = 0; j < EB; ++j) {
+            const float acc = wave_sum(dots[j]);
+            const int e = e0 + NW * j;
+            if (lane == 0 && e < experts) p[e] = acc;
+        }
+    }
+    __syncthreads();
+    emu_route_token(p, sel, experts, k, ids + (size_t)c * k, weights + (size_t)c * k);
 }
+
 // Embedding row of tokens[c]: a unit-per-thread decode of one row.
 template <class F>
 __global__ __launch_bounds__(kThreads) void embed_kernel(const uint8_t *embed, size_t row_bytes, int hidden,
@@ -582,12 +648,24 @@ int run_moe(emu_session *s)
         o.accumulate = 1;
         o.acc_scale = c.residual_scale;
         if ((st = emu_launch_qmv(ctx, c.encoding, o, n)) != EMU_OK) return st;
-        if ((st = emu_rms_norm(ctx, s->state, ffn_norm + (size_t)layer * H, (uint32_t)n, H, c.eps, s->xn)) != EMU_OK)
-            return st;
-        hipLaunchKernelGGL(router_kernel, dim3(E, (unsigned)n), dim3(EMU_WAVE), 0, ctx->stream,
-                           reinterpret_cast<const float *>(lw + m->off_r), s->xn, (int)H, (int)E, s->rlog);
-        EMU_LAUNCH_CHECK(ctx);
-        if ((st = emu_route(ctx, s->rlog, (uint32_t)n, E, K, s->rids, s->rwts)) != EMU_OK) return st;
+        if ((H == 1024 || H == 2048) && E <= 256 && K <= 64) {
+            const float *gn = ffn_norm + (size_t)layer * H, *rt = reinterpret_cast<const float *>(lw + m->off_r);
+            if (H == 1024)
+                hipLaunchKernelGGL(moe_gate_kernel<4>, dim3((unsigned)n), dim3(kThreads), 0, ctx->stream, s->state, gn,
+                                   rt, (int)E, (int)K, c.eps, s->xn, s->rids, s->rwts);
+            else
+                hipLaunchKernelGGL(moe_gate_kernel<8>, dim3((unsigned)n), dim3(kThreads), 0, ctx->stream, s->state, gn,
+                                   rt, (int)E, (int)K, c.eps, s->xn, s->rids, s->rwts);
+            EMU_LAUNCH_CHECK(ctx);
+        } else {
+            if ((st = emu_rms_norm(ctx, s->state, ffn_norm + (size_t)layer * H, (uint32_t)n, H, c.eps, s->xn)) !=
+                EMU_OK)
+                return st;
+            hipLaunchKernelGGL(router_kernel, dim3(E, (unsigned)n), dim3(EMU_WAVE), 0, ctx->stream,
+                               reinterpret_cast<const float *>(lw + m->off_r), s->xn, (int)H, (int)E, s->rlog);
+            EMU_LAUNCH_CHECK(ctx);
+            if ((st = emu_route(ctx, s->rlog, (uint32_t)n, E, K, s->rids, s->rwts)) != EMU_OK) return st;
+        }
         emu_moe_desc d{};
         d.enc_gate_up = c.expert_encoding;
         d.enc_down = c.expert_encoding;
@@ -600,13 +678,10 @@ int run_moe(emu_session *s)
         d.ff = c.expert_ff;
         d.k = K;
         d.act = EMU_ACT_SILU;
-        if ((st = emu_moe_ffn(ctx, &d, s->xn, (uint32_t)n, s->rids, s->rwts, s->moe_ws, s->moe_ws_bytes,
-                              s->moe_out)) != EMU_OK)
+        // the weighted expert sum lands on the residual stream as add_scaled does
+        if ((st = emu_moe_ffn_resid(ctx, &d, s->xn, (uint32_t)n, s->rids, s->rwts, s->moe_ws, s->moe_ws_bytes,
+                                    s->state, c.residual_scale)) != EMU_OK)
             return st;
-        const size_t tot = (size_t)n * H;
-        hipLaunchKernelGGL(add_scaled_kernel, dim3((unsigned)((tot + kThreads - 1) / kThreads)), dim3(kThreads), 0,
-                           ctx->stream, s->state, s->moe_out, tot, c.residual_scale);
-        EMU_LAUNCH_CHECK(ctx);
     }
     QmvArgs out{};
     out.w = m->base + m->off_embed; // tied (model.rs:403-407)
@@ -1106,7 +1181,6 @@ extern "C" int emu_session_create(emu_model *m, uint32_t n_clients, uint32_t con
         alloc((void **)&s->rlog, sizeof(float) * n_clients * c.n_experts);
         alloc((void **)&s->rids, sizeof(int32_t) * n_clients * c.experts_used);
         alloc((void **)&s->rwts, sizeof(float) * n_clients * c.experts_used);
-        alloc((void **)&s->moe_out, sizeof(float) * n_clients * c.hidden);
         s->moe_ws_bytes = emu_moe_workspace_bytes(n_clients, c.experts_used, c.hidden, c.expert_ff);
         alloc(&s->moe_ws, s->moe_ws_bytes);
     }
@@ -1154,7 +1228,7 @@ extern "C" int emu_session_destroy(emu_session *s)
     if (s->graph) (void)hipGraphDestroy(s->graph);
     void *ptrs[] = {s->k_cache, s->v_cache, s->positions, s->tokens, s->steps, s->last, s->prompt, s->hist,
                     s->ctrl, s->counters, s->state, s->qkv, s->attn, s->act, s->logits, s->keys, s->partial,
-                    s->rope, s->xn, s->rlog, s->rids, s->rwts, s->moe_out, s->moe_ws};
+                    s->rope, s->xn, s->rlog, s->rids, s->rwts, s->moe_ws};
     for (void *p : ptrs) emu_free(ctx, p);
     delete s;
     return EMU_OK;

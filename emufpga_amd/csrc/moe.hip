@@ -42,7 +42,9 @@ struct MoeArgs {
     const float *weights;            // n_tok x k
     float *act_buf;                  // (n_tok*k) x ff
     float *contrib;                  // (n_tok*k) x width
-    float *out;                      // n_tok x width
+    float *out;                      // n_tok x width, or
+    float *resid;                    // the residual stream it is added to (r + sum * resid_scale)
+    float resid_scale;
 };
 
 __device__ __forceinline__ void load8(const float *p, float v[8])
@@ -263,7 +265,12 @@ __global__ __launch_bounds__(kThreads) void moe_combine_kernel(MoeArgs a)
 #pragma unroll
     for (int i = 0; i < kMaxTok; ++i)
         if (i < n) sum = __fadd_rn(sum, __fmul_rn(v[i], w[i]));
-    a.out[(size_t)t * a.width + c] = sum;
+    if (a.resid) {
+        float *r = a.resid + (size_t)t * a.width + c;
+        *r = emu_resid_add(*r, sum, a.resid_scale);
+    } else {
+        a.out[(size_t)t * a.width + c] = sum;
+    }
 }
 
 // Lanes per row for a row of U units: the power of two in {16, 32, 64} that
@@ -320,11 +327,14 @@ extern "C" size_t emu_moe_workspace_bytes(uint32_t n_tok, uint32_t k, uint32_t w
     return align256(sizeof(float) * slots * ff) + align256(sizeof(float) * slots * width);
 }
 
-extern "C" int emu_moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok,
-                           const int32_t *d_ids, const float *d_weights, void *d_workspace, size_t workspace_bytes,
-                           float *d_out)
+namespace {
+
+int moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok, const int32_t *d_ids,
+            const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_out, float *d_resid,
+            float resid_scale)
 {
-    if (!ctx || !d || !d_x || !d_ids || !d_weights || !d_out || !d->d_gate || !d->d_down) return EMU_E_ARG;
+    if (!ctx || !d || !d_x || !d_ids || !d_weights || !(d_out || d_resid) || !d->d_gate || !d->d_down)
+        return EMU_E_ARG;
     if (n_tok == 0) return EMU_OK;
     if (n_tok > kMaxTok || d->k == 0 || d->k > 8 || d->n_experts == 0 || d->k > d->n_experts) return EMU_E_ARG;
     if (d->act != EMU_ACT_SILU && d->act != EMU_ACT_GELU_TANH) return EMU_E_ARG;
@@ -357,6 +367,8 @@ extern "C" int emu_moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x
     a.contrib = reinterpret_cast<float *>(static_cast<uint8_t *>(d_workspace) +
                                           align256(sizeof(float) * (size_t)n_tok * d->k * d->ff));
     a.out = d_out;
+    a.resid = d_resid;
+    a.resid_scale = resid_scale;
     switch (d->enc_gate_up) {
     case EMU_ENC_Q6_K: launch_up<FmtQ6K>(ctx, a); break;
     case EMU_ENC_Q8_0: launch_up<FmtQ8_0>(ctx, a); break;
@@ -377,4 +389,22 @@ extern "C" int emu_moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x
                        ctx->stream, a);
     EMU_LAUNCH_CHECK(ctx);
     return EMU_OK;
+}
+
+} // namespace
+
+extern "C" int emu_moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok,
+                           const int32_t *d_ids, const float *d_weights, void *d_workspace, size_t workspace_bytes,
+                           float *d_out)
+{
+    if (!d_out) return EMU_E_ARG;
+    return moe_ffn(ctx, d, d_x, n_tok, d_ids, d_weights, d_workspace, workspace_bytes, d_out, nullptr, 0.0f);
+}
+
+int emu_moe_ffn_resid(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok, const int32_t *d_ids,
+                      const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_state,
+                      float scale)
+{
+    if (!d_state) return EMU_E_ARG;
+    return moe_ffn(ctx, d, d_x, n_tok, d_ids, d_weights, d_workspace, workspace_bytes, nullptr, d_state, scale);
 }

@@ -175,43 +175,9 @@ __global__ __launch_bounds__(64) void route_kernel(const float *logits, int n_ex
     __shared__ float p[256];
     __shared__ float sel[64];
     const int t = blockIdx.x;
-    const float *lr = logits + (size_t)t * n_experts;
-    const int lane = threadIdx.x;
-    float m = -INFINITY;
-    for (int e = lane; e < n_experts; e += 64) m = fmaxf(m, lr[e]);
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    for (int e = lane; e < n_experts; e += 64) p[e] = expf(lr[e] - m);
+    for (int e = threadIdx.x; e < n_experts; e += 64) p[e] = logits[(size_t)t * n_experts + e];
     __syncthreads();
-    // Sequential sum in expert order, as the reference's left fold.
-    float sum = 0.0f;
-    if (lane == 0)
-        for (int e = 0; e < n_experts; ++e) sum = __fadd_rn(sum, p[e]);
-    sum = __shfl(sum, 0, 64);
-    __syncthreads();
-    for (int e = lane; e < n_experts; e += 64) p[e] = p[e] / sum;
-    __syncthreads();
-    // k rounds of (greatest total-order value, lowest id), removing the winner.
-    for (int r = 0; r < k; ++r) {
-        uint64_t best = 0;
-        for (int e = lane; e < n_experts; e += 64) {
-            if (p[e] == -INFINITY) continue;
-            const uint64_t key = select_key(p[e], (uint32_t)e, 0);
-            best = key > best ? key : best;
-        }
-        best = wave_max_u64(best);
-        const int e = (int)key_index(best, 0);
-        if (lane == 0) {
-            ids[(size_t)t * k + r] = e;
-            sel[r] = p[e];
-            p[e] = -INFINITY;
-        }
-        __syncthreads();
-    }
-    if (lane == 0) {
-        float total = 0.0f;
-        for (int r = 0; r < k; ++r) total = __fadd_rn(total, sel[r]);
-        for (int r = 0; r < k; ++r) weights[(size_t)t * k + r] = sel[r] / total;
-    }
+    emu_route_token(p, sel, n_experts, k, ids + (size_t)t * k, weights + (size_t)t * k);
 }
 
 } // namespace
