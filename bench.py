@@ -37,7 +37,8 @@ sys.path.insert(0, ROOT)
 from emufpga_amd import _lib  # noqa: E402
 from emufpga_amd.device import Context  # noqa: E402
 from emufpga_amd.gguf import GgufFile, row_bytes  # noqa: E402
-from emufpga_amd.serve import GRANITE_MOE_Q6K, QWEN3_8B_Q6K, DenseConfig, Model, Session  # noqa: E402
+from emufpga_amd.serve import (GRANITE_MOE_Q6K, QWEN3_8B_Q6K, SMOLLM2_135M_Q8, DenseConfig, Model,  # noqa: E402
+                               Session)
 
 METRIC = "decode tok/s at batch 1 and 8; achieved HBM GB/s vs 8 TB/s peak"
 HBM_PEAK_GBS = 8000.0
@@ -183,6 +184,48 @@ def load_leg(ctx) -> dict:
             "workload": "Qwen3-8B-width Q6_K decoder cut to 4 layers, GGUF file in the page cache -> HBM"}
 
 
+def smol_leg(ctx, rng, with_cpu: bool) -> dict:
+    """The SmolLM2-135M-shaped Q8_0 decoder (30 layers, width 576, tied 49152-row
+    output): batch 1, 32-token prompt, 256 timed greedy steps; beside it the
+    oracle's single-threaded CPU decode of the same model."""
+    cfg = SMOLLM2_135M_Q8
+    model = Model(ctx, cfg)
+    model.synth(135)
+    sess = Session(model, 1, 512, kv_f16=True)
+    prompt = rng.integers(0, cfg.vocab, size=(1, 32)).astype(np.uint32)
+    sess.generate(prompt, 1 + 8)
+    ctx.sync()
+    steps = 256
+    ms = sess.time_decode(steps)
+    pos = int(sess.positions()[0])
+    tok_s = steps / (ms / 1e3)
+    log(f"SmolLM2 batch 1: {steps} steps in {ms:.2f} ms -> {tok_s:.1f} tok/s (context {pos - steps}..{pos})")
+    out = {"value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": round(ms / steps, 4),
+           "context_at_timing": [pos - steps, pos],
+           "workload": ("SmolLM2-135M-shaped decoder, Q8_0 linears and tied embedding (seeded synthetic), batch 1, "
+                        "32-token prompt, 256 greedy decode steps, fp16 KV cache")}
+    if with_cpu:
+        import oracle
+
+        ocfg = oracle.DenseCfg(hidden=cfg.hidden, heads=cfg.heads, kv_heads=cfg.kv_heads, head_dim=cfg.head_dim,
+                               ffn=cfg.ffn, vocab=cfg.vocab, layers=cfg.layers, context=16,
+                               rope_theta=cfg.rope_theta, eps=cfg.eps, style=cfg.style, dtype=cfg.encoding,
+                               kv_f16=1, tied=1, qk_norm=0)
+        orc = oracle.DenseOracle(ocfg, model.host_weights(), 1)
+        t0 = time.perf_counter()
+        n = 8
+        for i in range(n):
+            orc.step([int(prompt[0, i])])
+        dt = (time.perf_counter() - t0) / n
+        log(f"SmolLM2 cpu oracle: {dt * 1e3:.1f} ms/token")
+        out["cpu_baseline"] = {"value": round(1.0 / dt, 3), "unit": "tok/s", "cores": 1, "kind": "port",
+                               "sample": f"{n} batch-1 decode steps at positions 0..{n - 1} on the single-threaded "
+                                         "C restatement of the reference CPU path"}
+    sess.close()
+    model.close()
+    return out
+
+
 def moe_leg(ctx, rng) -> dict:
     """Granite-shaped MoE decode, 4 clients, 256-token prompts, 128 timed steps.
     The routing is the model's own router on seeded synthetic weights (close to
@@ -221,6 +264,7 @@ def main() -> int:
     ap.add_argument("--no-batch8", action="store_true")
     ap.add_argument("--no-moe", action="store_true", help="skip the Granite MoE decode leg")
     ap.add_argument("--no-load", action="store_true", help="skip the GGUF -> HBM load leg")
+    ap.add_argument("--no-smol", action="store_true", help="skip the SmolLM2 decode leg")
     ap.add_argument("--batch8-only", action="store_true",
                     help="only the 8-client decode, logged without the JSON line; for profiling")
     ap.add_argument("--roofline-rounds", type=int, default=8)
@@ -330,6 +374,8 @@ def main() -> int:
                          "ms_per_step": round(ms8 / args.steps, 4), "context_at_timing": [pos8 - args.steps, pos8],
                          "step_hbm_gbs": round(gbs8, 1), "step_hbm_frac": round(gbs8 / HBM_PEAK_GBS, 4),
                          "matvec": "int8 MFMA (v_mfma_i32_32x32x16_i8), activation limbs as the A operand"}
+    if not args.no_smol:
+        out["smollm2_b1"] = smol_leg(ctx, rng, not args.no_cpu)
     if not args.no_moe:
         out["moe_granite_b4"] = moe_leg(ctx, rng)
     if not args.no_load:
