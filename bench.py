@@ -272,8 +272,9 @@ def main() -> int:
                     help="only time the dominant kernel (the fused gate|up matvec over all layers); for profiling")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported (the decode path is "
-              "single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: this decode path runs "
+              "on one GPU, whose share of a sharded model is the same kernels at their real shapes",
+              file=sys.stderr)
         return 2
 
     cfg = QWEN3_8B_Q6K
