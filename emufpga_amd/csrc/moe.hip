@@ -126,6 +126,83 @@ __device__ __forceinline__ void row_dots(const uint8_t *row, int nb, const float
     }
 }
 
+// The dots of one unit (lane q's unit q of a row of U <= L units) against
+// the cnt routed vectors, from the unit's raw bytes.
+template <class F>
+__device__ __forceinline__ void unit_dots(const typename F::Raw &raw, int u, const float *in, int in_stride,
+                                          const int (&slot)[kMaxTok], int cnt, float (&acc)[kMaxTok])
+{
+    const int blk = u / F::UPB, sub = u % F::UPB;
+    const int c0 = blk * F::BE;
+#pragma unroll
+    for (int g = 0; g < F::G; ++g) {
+        const Grp gp = F::group(raw, sub, g);
+        float w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = grp_weight(gp, i);
+        const int col = c0 + F::col(sub, g);
+#pragma unroll
+        for (int t = 0; t < kMaxTok; ++t) {
+            if (t < cnt) {
+                float xv[8];
+                load8(in + (size_t)slot[t] * in_stride + col, xv);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[t] = __builtin_fmaf(w[i], xv[i], acc[t]);
+            }
+        }
+    }
+}
+
+// The same unit u of R rows (so the same columns) against CNT routed
+// vectors (the expert's token count rounded up to 1, 2, 4 or 8; slots past
+// the real count read slot 0 and their sums are never used): a group's 8
+// activations per token are loaded once for all R rows, every token's loads
+// of a group issued together with no branch around them.
+template <class F, int R, int CNT>
+__device__ __forceinline__ void units_dots(const typename F::Raw (&raw)[R], int u, const float *in, int in_stride,
+                                           const int (&slot)[kMaxTok], float (&acc)[R][kMaxTok])
+{
+    const int blk = u / F::UPB, sub = u % F::UPB;
+    const int c0 = blk * F::BE;
+#pragma unroll
+    for (int g = 0; g < F::G; ++g) {
+        const int col = c0 + F::col(sub, g);
+        float xv[CNT][8];
+#pragma unroll
+        for (int t = 0; t < CNT; ++t) load8(in + (size_t)slot[t] * in_stride + col, xv[t]);
+        float w[R][8];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const Grp gp = F::group(raw[r], sub, g);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w[r][i] = grp_weight(gp, i);
+        }
+#pragma unroll
+        for (int t = 0; t < CNT; ++t)
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[r][t] = __builtin_fmaf(w[r][i], xv[t][i], acc[r][t]);
+    }
+}
+
+// units_dots with the token count bucketed at run time (uniform per wavefront).
+template <class F, int R>
+__device__ __forceinline__ void units_dots_any(const typename F::Raw (&raw)[R], int u, const float *in,
+                                               int in_stride, const int (&slot)[kMaxTok], int cnt,
+                                               float (&acc)[R][kMaxTok])
+{
+    if (cnt <= 1) units_dots<F, R, 1>(raw, u, in, in_stride, slot, acc);
+    else if (cnt <= 2) units_dots<F, R, 2>(raw, u, in, in_stride, slot, acc);
+    else if (cnt <= 4) units_dots<F, R, 4>(raw, u, in, in_stride, slot, acc);
+    else units_dots<F, R, 8>(raw, u, in, in_stride, slot, acc);
+}
+
+template <class F> __device__ __forceinline__ void unit_load(const uint8_t *row, int u, typename F::Raw &raw)
+{
+    F::load(row, (uint32_t)(u / F::UPB) * F::BB, u % F::UPB, raw);
+}
+
 // Sum over the L lanes of a lane group (L a power of two, <= 64).
 template <int L> __device__ __forceinline__ float group_sum(float v)
 {
@@ -189,6 +266,121 @@ __global__ __launch_bounds__(kThreads) void moe_up_kernel(MoeArgs a)
 #pragma unroll
     for (int t = 0; t < kMaxTok; ++t)
         if (t < cnt) a.act_buf[(size_t)slot[t] * a.ff + r] = activate<ACT>(ag[t], au[t]);
+}
+
+// Rows of at most L units (one per lane): a wavefront works P row sets, every
+// set's unit loads issued before the first dot, so one memory round trip
+// serves P times the rows.  Rows past the matrix are computed on a valid row
+// and not stored.
+constexpr int kPasses = 4;
+template <int L> constexpr int up_passes() { return L >= EMU_WAVE ? kPasses / 2 : kPasses; }
+constexpr int kUpRounds = 2;
+
+template <class F, int ACT, int L>
+__global__ __launch_bounds__(kThreads) void moe_up_p_kernel(MoeArgs a)
+{
+    constexpr int S = EMU_WAVE / L, RPW = up_rows_per_wave<L>();
+    constexpr int NR = S >= 2 ? 1 : 2;         // rows a lane loads per pass (L = 64: gate and up)
+    constexpr int P = up_passes<L>();           // four rows per lane in all
+    const int e = blockIdx.x;
+    const int lane = threadIdx.x & (EMU_WAVE - 1), wv = threadIdx.x / EMU_WAVE;
+    int slot[kMaxTok];
+    const int cnt = expert_slots(a, e, lane, slot);
+    if (cnt == 0) return;
+    int tok[kMaxTok];
+#pragma unroll
+    for (int t = 0; t < kMaxTok; ++t) tok[t] = slot[t] / a.k;
+    const size_t per = (size_t)(a.up ? 1 : 2) * a.ff;
+    const int j = lane / L, q = lane % L;
+    const int U = a.nb_in * F::UPB;
+    const bool has_unit = q < U;
+    const int u = has_unit ? q : 0;
+    // kUpRounds row sets per wavefront, one after another: half the
+    // workgroups, so the routed experts' waves fit the CUs in one round.
+    for (int round = 0; round < kUpRounds; ++round) {
+        const int r0 = ((blockIdx.y * kWaves + wv) * kUpRounds + round) * P * RPW + (S >= 2 ? j >> 1 : 0);
+        typename F::Raw raw[P * NR];
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            int r = r0 + p * RPW;
+            r = r < a.ff ? r : a.ff - 1;
+            const uint8_t *grow = a.gate + ((size_t)e * per + r) * a.rb_in;
+            const uint8_t *urow = a.up ? a.up + ((size_t)e * a.ff + r) * a.rb_in
+                                       : a.gate + ((size_t)e * per + a.ff + r) * a.rb_in;
+            if (NR == 1) unit_load<F>((j & 1) ? urow : grow, u, raw[p]);
+            else {
+                unit_load<F>(grow, u, raw[NR * p]);
+                unit_load<F>(urow, u, raw[NR * p + 1]);
+            }
+        }
+        float accs[P * NR][kMaxTok];
+#pragma unroll
+        for (int i = 0; i < P * NR; ++i)
+#pragma unroll
+            for (int t = 0; t < kMaxTok; ++t) accs[i][t] = 0.0f;
+        if (has_unit) units_dots_any<F, P * NR>(raw, u, a.x, a.width, tok, cnt, accs);
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const int r = r0 + p * RPW;
+            float ag[kMaxTok], au[kMaxTok];
+#pragma unroll
+            for (int t = 0; t < kMaxTok; ++t) {
+                ag[t] = au[t] = 0.0f;
+                if (t < cnt) {
+                    ag[t] = group_sum<L>(accs[NR * p][t]);
+                    au[t] = NR == 2 ? group_sum<L>(accs[NR * p + 1][t]) : __shfl_xor(ag[t], L, EMU_WAVE);
+                }
+            }
+            const bool writer = q == 0 && (NR == 2 || !(j & 1));
+            if (writer && r < a.ff) {
+#pragma unroll
+                for (int t = 0; t < kMaxTok; ++t)
+                    if (t < cnt) a.act_buf[(size_t)slot[t] * a.ff + r] = activate<ACT>(ag[t], au[t]);
+            }
+        }
+    }
+}
+
+template <class F, int L>
+__global__ __launch_bounds__(kThreads) void moe_down_p_kernel(MoeArgs a)
+{
+    constexpr int S = EMU_WAVE / L;
+    const int e = blockIdx.x;
+    const int lane = threadIdx.x & (EMU_WAVE - 1), wv = threadIdx.x / EMU_WAVE;
+    int slot[kMaxTok];
+    const int cnt = expert_slots(a, e, lane, slot);
+    if (cnt == 0) return;
+    const int j = lane / L, q = lane % L;
+    const int U = a.nb_ff * F::UPB;
+    const bool has_unit = q < U;
+    const int u = has_unit ? q : 0;
+    const int r0 = (blockIdx.y * kWaves + wv) * kPasses * S + j;
+    typename F::Raw raw[kPasses];
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+        int r = r0 + p * S;
+        r = r < a.width ? r : a.width - 1;
+        unit_load<F>(a.down + ((size_t)e * a.width + r) * a.rb_ff, u, raw[p]);
+    }
+    const float scale = a.down_scale ? a.down_scale[e] : 1.0f;
+    float accs[kPasses][kMaxTok];
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p)
+#pragma unroll
+        for (int t = 0; t < kMaxTok; ++t) accs[p][t] = 0.0f;
+    if (has_unit) units_dots_any<F, kPasses>(raw, u, a.act_buf, a.ff, slot, cnt, accs);
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+        const int r = r0 + p * S;
+#pragma unroll
+        for (int t = 0; t < kMaxTok; ++t) {
+            if (t < cnt) {
+                float v = group_sum<L>(accs[p][t]);
+                if (a.down_scale) v = __fmul_rn(v, scale); // gemma_smoke.rs:129-137
+                if (q == 0 && r < a.width) a.contrib[(size_t)slot[t] * a.width + r] = v;
+            }
+        }
+    }
 }
 
 template <class F, int L>
@@ -279,6 +471,12 @@ int lanes_for(int units) { return units > 32 ? 64 : units > 16 ? 32 : 16; }
 
 template <class F, int ACT, int L> void launch_up_l(emu_ctx *ctx, const MoeArgs &a)
 {
+    if (a.nb_in * F::UPB <= L) { // one unit per lane: the multi-row form
+        constexpr int per_block = kWaves * up_rows_per_wave<L>() * up_passes<L>() * kUpRounds;
+        const dim3 grid(a.n_experts, (a.ff + per_block - 1) / per_block);
+        hipLaunchKernelGGL((moe_up_p_kernel<F, ACT, L>), grid, dim3(kThreads), 0, ctx->stream, a);
+        return;
+    }
     constexpr int per_block = kWaves * up_rows_per_wave<L>();
     const dim3 grid(a.n_experts, (a.ff + per_block - 1) / per_block);
     hipLaunchKernelGGL((moe_up_kernel<F, ACT, L>), grid, dim3(kThreads), 0, ctx->stream, a);
@@ -303,6 +501,12 @@ template <class F> void launch_up(emu_ctx *ctx, const MoeArgs &a)
 
 template <class F, int L> void launch_down_l(emu_ctx *ctx, const MoeArgs &a)
 {
+    if (a.nb_ff * F::UPB <= L) {
+        constexpr int per_block = kWaves * (EMU_WAVE / L) * kPasses;
+        const dim3 grid(a.n_experts, (a.width + per_block - 1) / per_block);
+        hipLaunchKernelGGL((moe_down_p_kernel<F, L>), grid, dim3(kThreads), 0, ctx->stream, a);
+        return;
+    }
     constexpr int per_block = kWaves * (EMU_WAVE / L);
     const dim3 grid(a.n_experts, (a.width + per_block - 1) / per_block);
     hipLaunchKernelGGL((moe_down_kernel<F, L>), grid, dim3(kThreads), 0, ctx->stream, a);
