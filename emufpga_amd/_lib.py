@@ -196,6 +196,7 @@ SIGNATURES = {
     "emu_session_create": [P, U32, U32, I, C.POINTER(P)],
     "emu_session_destroy": [P],
     "emu_session_reset": [P],
+    "emu_session_reset_client": [P, U32],
     "emu_decode_step": [P, P, P, P],
     "emu_generate": [P, P, U32, U32, P],
     "emu_time_decode": [P, U32, FP],

@@ -1234,6 +1234,19 @@ extern "C" int emu_session_destroy(emu_session *s)
     return EMU_OK;
 }
 
+extern "C" int emu_session_reset_client(emu_session *s, uint32_t client)
+{
+    if (!s || client >= s->n) return EMU_E_ARG;
+    emu_ctx *ctx = s->m->ctx;
+    int st;
+    // Position and step count back to 0: attention reads only the positions
+    // below the client's own, so its old cache rows are never seen again.
+    if ((st = emu_memset(ctx, s->positions + client, 0, sizeof(uint32_t))) != EMU_OK) return st;
+    if ((st = emu_memset(ctx, s->steps + client, 0, sizeof(uint32_t))) != EMU_OK) return st;
+    s->host_pos[client] = 0;
+    return emu_ctx_sync(ctx);
+}
+
 extern "C" int emu_session_reset(emu_session *s)
 {
     if (!s) return EMU_E_ARG;

@@ -299,6 +299,10 @@ class Session:
     def reset(self) -> None:
         self.ctx.check(self.ctx.lib.emu_session_reset(self.h), "emu_session_reset")
 
+    def reset_client(self, client: int) -> None:
+        """Replace one client by a fresh one; the others keep their state."""
+        self.ctx.check(self.ctx.lib.emu_session_reset_client(self.h, client), "emu_session_reset_client")
+
     def decode_step(self, tokens, want_logits: bool = False):
         toks = np.ascontiguousarray(tokens, np.uint32)
         nxt = np.empty(self.n, np.uint32)

@@ -268,6 +268,11 @@ int emu_session_create(emu_model *model, uint32_t n_clients, uint32_t context, i
                        emu_session **out);
 int emu_session_destroy(emu_session *s);
 int emu_session_reset(emu_session *s);
+/* A fresh client in slot `client` while the others keep going (a new
+ * Client::new, spm-batch/src/session.rs:24-31, swapped into the batch): its
+ * position and step count return to 0 and the next decode step feeds it its
+ * first token. */
+int emu_session_reset_client(emu_session *s, uint32_t client);
 /* decode_step (spm-batch/src/step.rs:19-39): feed h_tokens[c] to client c at
  * its current position, advance every position by one, and greedily select
  * each client's next token.  h_next may be NULL.  d_logits, when non-NULL,

@@ -190,3 +190,36 @@ def test_generate_is_deterministic_and_replays(ctx):
     sess.reset()
     b = sess.generate(prompts, 40)
     assert np.array_equal(a, b)
+
+
+def test_a_client_replaced_mid_run_gets_what_a_fresh_client_gets(ctx):
+    """Continuous batching in lockstep: client 1 is replaced by a fresh client
+    after 10 steps; both clients then get exactly what they would alone."""
+    model = Model(ctx, SMALL_QWEN3)
+    model.synth(17)
+    rng = np.random.default_rng(18)
+    a_prompt = rng.integers(0, SMALL_QWEN3.vocab, size=30).astype(np.uint32)
+    b_prompt = rng.integers(0, SMALL_QWEN3.vocab, size=12).astype(np.uint32)
+    c_prompt = rng.integers(0, SMALL_QWEN3.vocab, size=20).astype(np.uint32)
+
+    def alone(prompt):
+        s = Session(model, 1, 64)
+        out = [int(s.decode_step([t])[0]) for t in prompt]
+        s.close()
+        return out
+
+    sess = Session(model, 2, 64)
+    got_a, got_c = [], []
+    for i in range(10):
+        nxt = sess.decode_step([a_prompt[i], b_prompt[i]])
+        got_a.append(int(nxt[0]))
+    sess.reset_client(1)
+    assert list(sess.positions()) == [10, 0]
+    for i in range(20):
+        nxt = sess.decode_step([a_prompt[10 + i], c_prompt[i]])
+        got_a.append(int(nxt[0]))
+        got_c.append(int(nxt[1]))
+    assert got_a == alone(a_prompt)
+    assert got_c == alone(c_prompt)
+    with pytest.raises(_lib.EmuError):
+        sess.reset_client(2)
