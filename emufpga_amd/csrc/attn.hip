@@ -58,22 +58,25 @@ struct AttnArgs {
     float *xs;              //           and their scales (token = client)
 };
 
-// A value of q|k|v: the sum of its partial-sum slices, in slice order.  Up
-// to four slices, every load goes out before the first add.
-__device__ __forceinline__ float qkv_at(const float *p, int ns, size_t stride)
+// A value of q|k|v: one plain load (MS false), or the sum of its ns <= 8
+// partial-sum slices in slice order.  Straight-line code either way: slots
+// past ns load slice 0 and are not added, so all of a thread's q|k|v loads
+// go out before the first wait (a branch on ns between two values' loads
+// would put a full memory round trip between them).
+constexpr int kMaxSlices = 8;
+template <bool MS> __device__ __forceinline__ float qkv_at(const float *p, int ns, size_t stride)
 {
-    if (ns <= 4) {
-        float q[4];
+    if constexpr (!MS) {
+        return p[0];
+    } else {
+        float q[kMaxSlices];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) q[s] = p[(s < ns ? s : 0) * stride];
+        for (int s = 0; s < kMaxSlices; ++s) q[s] = p[(s < ns ? s : 0) * stride];
         float v = q[0];
 #pragma unroll
-        for (int s = 1; s < 4; ++s) v = s < ns ? v + q[s] : v;
+        for (int s = 1; s < kMaxSlices; ++s) v = s < ns ? v + q[s] : v;
         return v;
     }
-    float v = p[0];
-    for (int s = 1; s < ns; ++s) v += p[s * stride];
-    return v;
 }
 
 // One column of the output written as the multi-token matvec's A operands:
@@ -84,11 +87,16 @@ __device__ __forceinline__ void emit_limbs(float v, int col, int t, uint8_t *xa,
 {
     float amax = fabsf(v);
     int bad = !(fabsf(v) <= 3.402823466e38f);
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, o, EMU_WAVE));
-        bad |= __shfl_xor(bad, o, EMU_WAVE);
-    }
+    float fb = __int_as_float(bad); // the flag rides the float exchange bit for bit
+    amax = fmaxf(amax, emu_xor_lane<1>(amax));
+    fb = __int_as_float(__float_as_int(fb) | __float_as_int(emu_xor_lane<1>(fb)));
+    amax = fmaxf(amax, emu_xor_lane<2>(amax));
+    fb = __int_as_float(__float_as_int(fb) | __float_as_int(emu_xor_lane<2>(fb)));
+    amax = fmaxf(amax, emu_xor_lane<4>(amax));
+    fb = __int_as_float(__float_as_int(fb) | __float_as_int(emu_xor_lane<4>(fb)));
+    amax = fmaxf(amax, emu_xor_lane<8>(amax));
+    fb = __int_as_float(__float_as_int(fb) | __float_as_int(emu_xor_lane<8>(fb)));
+    bad = __float_as_int(fb);
     const bool finite = !bad;
     int e = 0;
     (void)frexpf(finite ? amax : 0.0f, &e);
@@ -107,9 +115,7 @@ __device__ __forceinline__ void emit_limbs(float v, int col, int t, uint8_t *xa,
 
 __device__ __forceinline__ float wave_max(float v)
 {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, EMU_WAVE));
-    return v;
+    return emu_wave_reduce(v, [](float x, float y) { return fmaxf(x, y); });
 }
 
 // Rotation of one pair, with the reference's roundings: separate products and
@@ -131,65 +137,84 @@ __device__ __forceinline__ void rotate(float &l, float &r, float2 cs, int fma_fo
 }
 
 // One wavefront: RMSNorm (optional) + RoPE of one head of HD values from
-// global memory into dst (LDS).  Lanes own rotation pairs.
-template <int HD>
-__device__ __forceinline__ void prep_head(const float *src, int ns, size_t sstride, float *dst, const float *gain,
-                                          float eps, const float2 *rope_row, int fma_form, int interleaved, int lane)
-{
-    constexpr int NP = HD / 2;
-    constexpr int PPL = (NP + EMU_WAVE - 1) / EMU_WAVE;
+// global memory into dst (LDS).  Lanes own rotation pairs.  load() issues
+// every load of the head (values, gains, rotation table), finish() does the
+// arithmetic, so a wavefront with several heads has all of their loads in
+// flight before the first one is used.
+template <int HD, bool MS> struct HeadPrep {
+    static constexpr int NP = HD / 2;
+    static constexpr int PPL = (NP + EMU_WAVE - 1) / EMU_WAVE;
     float a[PPL], b[PPL], ga[PPL], gb[PPL];
     float2 cs[PPL];
     int ia[PPL], ib[PPL];
-    // Every load (values, gains, rotation table) first: one round trip.
+
+    __device__ __forceinline__ void load(const float *src, int ns, size_t sstride, const float *gain,
+                                         const float2 *rope_row, int interleaved, int lane)
+    {
 #pragma unroll
-    for (int j = 0; j < PPL; ++j) {
-        const int i = lane + EMU_WAVE * j;
-        const int ic = i < NP ? i : NP - 1; // in-bounds stand-in for idle lanes
-        ia[j] = interleaved ? 2 * ic : ic;
-        ib[j] = interleaved ? 2 * ic + 1 : ic + NP;
-        a[j] = qkv_at(src + ia[j], ns, sstride);
-        b[j] = qkv_at(src + ib[j], ns, sstride);
-        cs[j] = rope_row[ic];
-        if (gain) {
-            ga[j] = gain[ia[j]];
-            gb[j] = gain[ib[j]];
+        for (int j = 0; j < PPL; ++j) {
+            const int i = lane + EMU_WAVE * j;
+            const int ic = i < NP ? i : NP - 1; // in-bounds stand-in for idle lanes
+            ia[j] = interleaved ? 2 * ic : ic;
+            ib[j] = interleaved ? 2 * ic + 1 : ic + NP;
+            a[j] = qkv_at<MS>(src + ia[j], ns, sstride);
+            b[j] = qkv_at<MS>(src + ib[j], ns, sstride);
+            cs[j] = rope_row[ic];
+            const float *g = gain ? gain : src; // unconditional loads; unused without gains
+            ga[j] = g[ia[j]];
+            gb[j] = g[ib[j]];
         }
     }
-    float ss = 0.0f;
+
+    __device__ __forceinline__ void finish(float *dst, bool has_gain, float eps, int fma_form, int lane)
+    {
+        float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < PPL; ++j) {
-        if (lane + EMU_WAVE * j < NP) {
-            ss = __builtin_fmaf(a[j], a[j], ss);
-            ss = __builtin_fmaf(b[j], b[j], ss);
+        for (int j = 0; j < PPL; ++j) {
+            if (lane + EMU_WAVE * j < NP) {
+                ss = __builtin_fmaf(a[j], a[j], ss);
+                ss = __builtin_fmaf(b[j], b[j], ss);
+            }
         }
-    }
-    if (gain) {
+        // selects, not a branch: the gain loads stay where load() put them
         const float scale = 1.0f / sqrtf(wave_sum(ss) / (float)HD + eps);
 #pragma unroll
         for (int j = 0; j < PPL; ++j) {
-            a[j] = __fmul_rn(__fmul_rn(a[j], scale), ga[j]);
-            b[j] = __fmul_rn(__fmul_rn(b[j], scale), gb[j]);
+            const float na = __fmul_rn(__fmul_rn(a[j], scale), ga[j]);
+            const float nb = __fmul_rn(__fmul_rn(b[j], scale), gb[j]);
+            a[j] = has_gain ? na : a[j];
+            b[j] = has_gain ? nb : b[j];
         }
-    }
 #pragma unroll
-    for (int j = 0; j < PPL; ++j) {
-        rotate(a[j], b[j], cs[j], fma_form);
-        if (lane + EMU_WAVE * j < NP) {
-            dst[ia[j]] = a[j];
-            dst[ib[j]] = b[j];
+        for (int j = 0; j < PPL; ++j) {
+            rotate(a[j], b[j], cs[j], fma_form);
+            if (lane + EMU_WAVE * j < NP) {
+                dst[ia[j]] = a[j];
+                dst[ib[j]] = b[j];
+            }
         }
     }
-}
+};
 
 // Butterfly reduce-scatter of N (<= 64, power of two) per-lane values:
 // afterwards lane l holds the wavefront-wide sum of value (l >> log2(64/N)).
-// Each step halves the values a lane keeps, trading the other half with the
-// partner lane `OFF` away; once one value is left, plain xor-sums finish.
+// Each step halves the values a lane keeps (the lower half where the lane's
+// bit OFF is clear), adding the partner lane's copy of it; once one value is
+// left, plain xor-sums finish.  Offsets 32 and 16 use the permlane swaps, the
+// others DPP, so no step goes through the LDS crossbar.
 template <int N, int OFF>
 __device__ __forceinline__ void reduce_scatter_step(float *v, int lane)
 {
-    if constexpr (OFF > 0) {
+    if constexpr (OFF >= 16) {
+        constexpr int H = N > 1 ? N / 2 : 1;
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            float a = v[i], b = N > 1 ? v[i + H] : v[i];
+            emu_swap_halves<OFF>(a, b);
+            v[i] = a + b;
+        }
+        reduce_scatter_step<H, OFF / 2>(v, lane);
+    } else if constexpr (OFF > 0) {
         if constexpr (N > 1) {
             constexpr int H = N / 2;
             const bool up = (lane & OFF) != 0;
@@ -197,11 +222,11 @@ __device__ __forceinline__ void reduce_scatter_step(float *v, int lane)
             for (int i = 0; i < H; ++i) {
                 const float keep = up ? v[i + H] : v[i];
                 const float send = up ? v[i] : v[i + H];
-                v[i] = keep + __shfl_xor(send, OFF, EMU_WAVE);
+                v[i] = keep + emu_xor_lane<OFF>(send);
             }
             reduce_scatter_step<H, OFF / 2>(v, lane);
         } else {
-            v[0] += __shfl_xor(v[0], OFF, EMU_WAVE);
+            v[0] += emu_xor_lane<OFF>(v[0]);
             reduce_scatter_step<1, OFF / 2>(v, lane);
         }
     }
@@ -236,7 +261,7 @@ __device__ __forceinline__ void unpack_row(const V &raw, float (&out)[EPL])
     }
 }
 
-template <int HD, bool F16, int GQP>
+template <int HD, bool F16, int GQP, bool MS>
 __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
 {
     using kv_t = typename std::conditional<F16, __half, float>::type;
@@ -257,7 +282,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     const int GQ = a.heads / a.kv_heads;
 
     __shared__ float q_s[GQP][HD];
-    __shared__ float knew[HD], vnew[HD];
+    __shared__ float knew[HD], vnew[HD], junk[HD];
     __shared__ __align__(16) float sc[GQP][kChunk];
     __shared__ float mh[GQP], lh[GQP];
     __shared__ float accs[kWaves][GQP][HD];
@@ -275,7 +300,26 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     const int p0 = chunk * kChunk;
     const bool owner = pos >= p0 && pos < p0 + kChunk;
 
-    // This wavefront's 16 positions: issue every K and V row load now, with no
+    // 1-2. Rotated queries (and the new key) into LDS: item i on wavefront
+    // i % 4.  A wavefront issues the loads of all its items (and every
+    // thread its element of the new value) before any arithmetic; idle item
+    // slots load item 0 and are not finished.
+    const int items = GQ + (owner ? 1 : 0);
+    constexpr int IPW = (GQP + 1 + kWaves - 1) / kWaves; // items per wavefront at most
+    HeadPrep<HD, MS> hp[IPW];
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+        const int it = w + i * kWaves < items ? w + i * kWaves : 0;
+        const bool key = it == GQ;
+        hp[i].load(key ? row + qw + kvh * HD : row + (kvh * GQ + it) * HD, a.qkv_slices, a.qkv_slice_stride,
+                   key ? kn : qn, rope_row, a.interleaved, lane);
+    }
+    const float vv = qkv_at<MS>(row + qw + kw + kvh * HD + (tid % HD), a.qkv_slices, a.qkv_slice_stride);
+    // Keep those loads ahead of the K/V loads below: loads complete in issue
+    // order, so anything issued after the K/V rows waits for them.
+    __builtin_amdgcn_sched_barrier(0);
+    // This wavefront's 16 positions: issue every K and V row load after the
+    // queries' (which the preparation below waits for first), with no
     // branch around them (a branch per load serialises them behind waits).
     // Positions past the context read row `pos - 1` or row 0 (always inside
     // the cache) and are masked after the loads; the new position's row is
@@ -291,23 +335,21 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
         vr[pp] = *reinterpret_cast<const vec_t *>(vc + (size_t)r * HD + lane * EPL);
     }
 
-    // 1-2. Rotated queries (and the new key) into LDS: item i on wavefront i % 4.
-    const int items = GQ + (owner ? 1 : 0);
-    for (int it = w; it < items; it += kWaves) {
-        if (it < GQ)
-            prep_head<HD>(row + (kvh * GQ + it) * HD, a.qkv_slices, a.qkv_slice_stride, q_s[it], qn, a.eps,
-                          rope_row, a.rope_fma, a.interleaved,
-                          lane);
-        else
-            prep_head<HD>(row + qw + kvh * HD, a.qkv_slices, a.qkv_slice_stride, knew, kn, a.eps, rope_row,
-                          a.rope_fma, a.interleaved, lane);
+    // Every slot is finished, idle ones into a junk row: with no branch
+    // around the arithmetic the compiler cannot sink the item loads behind
+    // the K/V loads (whose in-order completion would then gate them).
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+        const int it = w + i * kWaves;
+        const bool key = it == GQ;
+        float *dst = it < items ? (key ? knew : q_s[it < GQ ? it : 0]) : junk;
+        hp[i].finish(dst, (key ? kn : qn) != nullptr, a.eps, a.rope_fma, lane);
     }
     for (int g = GQ + w; g < GQP; g += kWaves)
         for (int e = lane; e < HD; e += EMU_WAVE) q_s[g][e] = 0.0f;
     __syncthreads();
     if (owner && tid < HD) {
         const float kv = knew[tid];
-        const float vv = qkv_at(row + qw + kw + kvh * HD + tid, a.qkv_slices, a.qkv_slice_stride);
         kv_t kq, vq;
         if constexpr (F16) {
             kq = __float2half_rn(kv);
@@ -515,17 +557,24 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+template <int HD, bool F16, bool MS>
+void launch_ms(const AttnArgs &a, dim3 grid, hipStream_t stream, int gq)
+{
+    if (gq <= 1)
+        hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 1, MS>), grid, dim3(kThreads), 0, stream, a);
+    else if (gq <= 2)
+        hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 2, MS>), grid, dim3(kThreads), 0, stream, a);
+    else if (gq <= 4)
+        hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 4, MS>), grid, dim3(kThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 8, MS>), grid, dim3(kThreads), 0, stream, a);
+}
+
 template <int HD, bool F16>
 void launch_hd(const AttnArgs &a, dim3 grid, hipStream_t stream, int gq)
 {
-    if (gq <= 1)
-        hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 1>), grid, dim3(kThreads), 0, stream, a);
-    else if (gq <= 2)
-        hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 2>), grid, dim3(kThreads), 0, stream, a);
-    else if (gq <= 4)
-        hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 4>), grid, dim3(kThreads), 0, stream, a);
-    else
-        hipLaunchKernelGGL((attn_decode_kernel<HD, F16, 8>), grid, dim3(kThreads), 0, stream, a);
+    if (a.qkv_slices > 1) launch_ms<HD, F16, true>(a, grid, stream, gq);
+    else launch_ms<HD, F16, false>(a, grid, stream, gq);
 }
 
 } // namespace
@@ -562,6 +611,7 @@ int emu_launch_attn(emu_ctx *ctx, const EmuAttnLaunch &l)
     a.qkv_slice_stride = l.qkv_slice_stride;
     a.xa = l.xa;
     a.xs = l.xs;
+    if (a.qkv_slices > kMaxSlices) return EMU_E_CONFIG;
     if (a.xa && (l.clients > 8 || (l.heads * l.head_dim) % 16 != 0)) return EMU_E_CONFIG;
     const dim3 grid(l.kv_heads * l.clients, a.max_chunks);
     const int gq = l.heads / l.kv_heads;

@@ -332,11 +332,106 @@ __device__ __forceinline__ uint32_t emu_key_index(uint64_t k, int tie_last)
 
 // ------------------------------------------------------------ reductions --
 
+// The value that lane (lane ^ OFF) holds, for OFF = 1, 2, 4 or 8, by DPP row
+// operations (no trip through the LDS crossbar): quad_perm for 1 and 2,
+// row_half_mirror then quad_perm [3,2,1,0] for 4 (7 - (i ^ 3) = i ^ 4 within
+// eight lanes), row_ror:8 for 8.
+template <int OFF> __device__ __forceinline__ float emu_xor_lane(float v)
+{
+    int x = __float_as_int(v);
+    if constexpr (OFF == 1) {
+        x = __builtin_amdgcn_update_dpp(0, x, 0xb1, 0xf, 0xf, false);
+    } else if constexpr (OFF == 2) {
+        x = __builtin_amdgcn_update_dpp(0, x, 0x4e, 0xf, 0xf, false);
+    } else if constexpr (OFF == 4) {
+        x = __builtin_amdgcn_update_dpp(0, x, 0x141, 0xf, 0xf, false);
+        x = __builtin_amdgcn_update_dpp(0, x, 0x1b, 0xf, 0xf, false);
+    } else {
+        static_assert(OFF == 8, "DPP exchange within a 16-lane row");
+        x = __builtin_amdgcn_update_dpp(0, x, 0x128, 0xf, 0xf, false);
+    }
+    return __int_as_float(x);
+}
+
+// Exchange across 32 or 16 lanes with v_permlane32_swap / v_permlane16_swap:
+// for the pair (a, b) the results (a', b') hold, in every lane l, a' = the
+// operand of the lane with bit OFF clear and b' = that of the lane with it
+// set, of a where l has the bit clear and of b where it is set.  So
+// a' + b' is, in every lane, "own + partner's" of the value the lane keeps in
+// a butterfly that keeps a in the lower and b in the upper half.
+template <int OFF> __device__ __forceinline__ void emu_swap_halves(float &a, float &b)
+{
+    static_assert(OFF == 16 || OFF == 32, "permlane swap distance");
+    if constexpr (OFF == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+        a = __uint_as_float(r[0]);
+        b = __uint_as_float(r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+        a = __uint_as_float(r[0]);
+        b = __uint_as_float(r[1]);
+    }
+}
+
+// The value that lane (lane ^ OFF) holds, for any power of two OFF below 64
+// (OFF >= 64 names no other lane of the wavefront: the lane's own value, as
+// __shfl_xor gives).
+template <int OFF> __device__ __forceinline__ float emu_xor_get(float v)
+{
+    if constexpr (OFF >= 64) {
+        return v;
+    } else if constexpr (OFF >= 16) {
+        float a = v, b = v;
+        emu_swap_halves<OFF>(a, b);
+        return (__lane_id() & OFF) ? a : b;
+    } else {
+        return emu_xor_lane<OFF>(v);
+    }
+}
+
+// Sum over aligned groups of L lanes (L a power of two, <= 64), every lane
+// getting its group's sum: a xor butterfly from offset L / 2 down to 1.
+template <int L> __device__ __forceinline__ float emu_group_sum(float v)
+{
+    if constexpr (L > 32) {
+        float a = v, b = v;
+        emu_swap_halves<32>(a, b);
+        v = a + b;
+    }
+    if constexpr (L > 16) {
+        float a = v, b = v;
+        emu_swap_halves<16>(a, b);
+        v = a + b;
+    }
+    if constexpr (L > 8) v += emu_xor_lane<8>(v);
+    if constexpr (L > 4) v += emu_xor_lane<4>(v);
+    if constexpr (L > 2) v += emu_xor_lane<2>(v);
+    if constexpr (L > 1) v += emu_xor_lane<1>(v);
+    return v;
+}
+
+// Wavefront all-reduce by a xor butterfly (offsets 32, 16, ..., 1) of a
+// commutative op: every lane gets the same value, in the same association
+// order as __shfl_xor butterflies give.
+template <class Op> __device__ __forceinline__ float emu_wave_reduce(float v, Op op)
+{
+    float a = v, b = v;
+    emu_swap_halves<32>(a, b);
+    v = op(a, b);
+    a = v;
+    b = v;
+    emu_swap_halves<16>(a, b);
+    v = op(a, b);
+    v = op(v, emu_xor_lane<8>(v));
+    v = op(v, emu_xor_lane<4>(v));
+    v = op(v, emu_xor_lane<2>(v));
+    v = op(v, emu_xor_lane<1>(v));
+    return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v)
 {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, EMU_WAVE);
-    return v;
+    return emu_wave_reduce(v, [](float x, float y) { return x + y; });
 }
 
 // Workgroup sum: wavefront butterflies, then the wavefront totals in order.
@@ -378,7 +473,7 @@ __device__ __forceinline__ void emu_route_token(float *p, float *sel, int n_expe
     if (w0) {
         float m = -INFINITY;
         for (int e = lane; e < n_experts; e += EMU_WAVE) m = fmaxf(m, p[e]);
-        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, EMU_WAVE));
+        m = emu_wave_reduce(m, [](float x, float y) { return fmaxf(x, y); });
         for (int e = lane; e < n_experts; e += EMU_WAVE) p[e] = expf(p[e] - m);
     }
     __syncthreads();

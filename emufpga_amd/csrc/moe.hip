@@ -206,9 +206,7 @@ template <class F> __device__ __forceinline__ void unit_load(const uint8_t *row,
 // Sum over the L lanes of a lane group (L a power of two, <= 64).
 template <int L> __device__ __forceinline__ float group_sum(float v)
 {
-#pragma unroll
-    for (int off = L / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, EMU_WAVE);
-    return v;
+    return emu_group_sum<L>(v);
 }
 
 // Hidden units per wavefront of the gate|up kernel with L lanes per row.
@@ -247,7 +245,7 @@ __global__ __launch_bounds__(kThreads) void moe_up_kernel(MoeArgs a)
         for (int t = 0; t < kMaxTok; ++t) {
             if (t < cnt) {
                 ag[t] = group_sum<L>(ag[t]);
-                au[t] = __shfl_xor(ag[t], L, EMU_WAVE);
+                au[t] = emu_xor_get<L>(ag[t]);
             }
         }
         if (is_up || q != 0) return;
@@ -328,7 +326,7 @@ __global__ __launch_bounds__(kThreads) void moe_up_p_kernel(MoeArgs a)
                 ag[t] = au[t] = 0.0f;
                 if (t < cnt) {
                     ag[t] = group_sum<L>(accs[NR * p][t]);
-                    au[t] = NR == 2 ? group_sum<L>(accs[NR * p + 1][t]) : __shfl_xor(ag[t], L, EMU_WAVE);
+                    au[t] = NR == 2 ? group_sum<L>(accs[NR * p + 1][t]) : emu_xor_get<L>(ag[t]);
                 }
             }
             const bool writer = q == 0 && (NR == 2 || !(j & 1));

@@ -92,7 +92,7 @@ __global__ __launch_bounds__(kThreads) void attend_kernel(const float *q, const 
         m = fmaxf(m, s);
     }
     // block max
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    m = emu_wave_reduce(m, [](float x, float y) { return fmaxf(x, y); });
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();

@@ -128,6 +128,38 @@ def test_qwen3_width_batched_decode_matches_oracle(ctx):
     assert worst <= 1e-3, worst
 
 
+# One client at a 1060-token context: the attention's last-arriving workgroup
+# merges up to 17 chunks of 64 positions, past its 16-chunk load batches, and
+# the 32 query heads of 128 feed the 4096-column integer-limb o projection.
+DEEP_QWEN3 = DenseConfig(hidden=512, heads=32, kv_heads=8, head_dim=128, ffn=512, vocab=600, layers=2,
+                         rope_theta=1e6, eps=1e-6, style=_lib.EMU_STYLE_QWEN3, encoding=_lib.Q6_K, tied=False,
+                         qk_norm=True)
+
+
+def test_long_context_chunk_merge_in_the_o_projection_matches_oracle(ctx):
+    model = Model(ctx, DEEP_QWEN3)
+    model.synth(77)
+    context = 1060
+    sess = Session(model, 1, context, kv_f16=True)
+    ref = oracle_for(model, context, True, 1)
+    rng = np.random.default_rng(78)
+    worst, checked = 0.0, 0
+    for step in range(context):
+        toks = rng.integers(0, DEEP_QWEN3.vocab, size=1).astype(np.uint32)
+        check = step < 2 or step in (63, 64, 65, 127, 128, 1023, 1024) or step % 101 == 0 or step >= context - 2
+        r = ref.step(toks)
+        if not check:
+            sess.decode_step(toks)
+        else:
+            nxt, logits = sess.decode_step(toks, want_logits=True)
+            worst = max(worst, rel_inf(logits[0], r[0]))
+            assert int(nxt[0]) == oracle.argmax(r[0], False), step
+            checked += 1
+    assert checked > 15 and worst <= 1e-3, worst
+    sess.close()
+    model.close()
+
+
 ATTN_SHAPES = [
     # (heads, kv_heads, head_dim, style): group sizes 8, 1, 3 and 2; head dims 64, 256, 128
     (8, 1, 64, _lib.EMU_STYLE_QWEN3),
