@@ -478,10 +478,11 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     // the device-coherent level) and a relaxed arrival counter, with every
     // store completed (s_waitcnt) before the counter moves: no L2 write-back
     // fence, which costs several microseconds per workgroup on this part.
-    for (int idx = tid; idx < GQ * (HD + 2); idx += kThreads) {
-        const int g = idx / (HD + 2), j = idx % (HD + 2);
+    constexpr int PS = HD + 2; // floats per (head, chunk) partial: output, max, exp sum
+    for (int idx = tid; idx < GQ * PS; idx += kThreads) {
+        const int g = idx / PS, j = idx % PS;
         const int head = kvh * GQ + g;
-        float *pp = a.partial + (((size_t)client * a.heads + head) * a.max_chunks + chunk) * (HD + 2);
+        float *pp = a.partial + (((size_t)client * a.heads + head) * a.max_chunks + chunk) * PS;
         float val;
         if (j < HD)
             val = (accs[0][g][j] + accs[1][g][j]) + (accs[2][g][j] + accs[3][g][j]);
@@ -495,13 +496,23 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     if (tid == 0) arrived = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (arrived != (uint32_t)(n_chunks - 1)) return;
-    // Merge (last workgroup to arrive): each thread owns NI (head, dim)
-    // outputs, and every batch of MB chunks' (max, sum, output) values for
-    // all of them is loaded at once and folded into running (M, L, O): one
-    // memory round trip per batch for the whole thread.
+    // Merge (last workgroup to arrive), MB chunks per batch.  The chunk
+    // weights depend only on the head, so they are formed once: thread
+    // t < GQ * MB owns (head t / MB, chunk t % MB) and the MB lanes of a head
+    // take the batch's max and exp sum by DPP butterflies, one expf per lane.
+    // Each item thread (NI (head, dim) outputs) loads its output values of
+    // the whole batch at once and folds them with the weights from LDS:
+    //   O = O * exp(M_old - M) + sum_j o_j * exp(m_j - M), in chunk order.
     constexpr int NI = (GQP * HD + kThreads - 1) / kThreads;
     constexpr int MB = NI <= 2 ? kMergeBatch : 32 / NI;
-    float M[NI], L[NI], O[NI];
+    static_assert(GQP * MB <= kThreads && MB <= 16, "one 16-lane row per head and batch");
+    __shared__ float wt[GQP][MB];
+    __shared__ float rs[GQP];
+    const int pg = tid / MB, pj = tid % MB;
+    const bool pair = pg < GQ;
+    const float *pm = a.partial + ((size_t)client * a.heads + kvh * GQ + (pair ? pg : 0)) * a.max_chunks * PS;
+    float Mrun = -INFINITY, Lrun = 0.0f; // per head, the same in its MB lanes
+    float O[NI];
     const float *pb[NI];
     int head_of[NI], dim_of[NI];
     bool live[NI];
@@ -510,49 +521,59 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
         const int idx = tid + i * kThreads;
         live[i] = idx < GQ * HD;
         const int ic = live[i] ? idx : 0; // in-bounds stand-in
-        head_of[i] = kvh * GQ + ic / HD;
+        head_of[i] = ic / HD;             // within the kv head's group
         dim_of[i] = ic % HD;
-        pb[i] = a.partial + ((size_t)client * a.heads + head_of[i]) * a.max_chunks * (HD + 2);
-        M[i] = -INFINITY;
-        L[i] = 0.0f;
+        pb[i] = a.partial + ((size_t)client * a.heads + kvh * GQ + head_of[i]) * a.max_chunks * PS;
         O[i] = 0.0f;
     }
     for (int c0 = 0; c0 < n_chunks; c0 += MB) {
-        float m[NI][MB], l[NI][MB], o[NI][MB];
+        const int cp = c0 + pj < n_chunks ? c0 + pj : n_chunks - 1;
+        const float mj = __hip_atomic_load(pm + (size_t)cp * PS + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float lj = __hip_atomic_load(pm + (size_t)cp * PS + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        float o[NI][MB];
 #pragma unroll
         for (int i = 0; i < NI; ++i)
 #pragma unroll
             for (int j = 0; j < MB; ++j) {
                 const int c = c0 + j < n_chunks ? c0 + j : n_chunks - 1;
-                const float *pc = pb[i] + (size_t)c * (HD + 2);
-                m[i][j] = __hip_atomic_load(pc + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                l[i][j] = __hip_atomic_load(pc + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                o[i][j] = __hip_atomic_load(pc + dim_of[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                o[i][j] = __hip_atomic_load(pb[i] + (size_t)c * PS + dim_of[i], __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
             }
+        const bool valid = c0 + pj < n_chunks;
+        float bm = valid ? mj : -INFINITY;
+        if constexpr (MB > 8) bm = fmaxf(bm, emu_xor_lane<8>(bm));
+        if constexpr (MB > 4) bm = fmaxf(bm, emu_xor_lane<4>(bm));
+        if constexpr (MB > 2) bm = fmaxf(bm, emu_xor_lane<2>(bm));
+        if constexpr (MB > 1) bm = fmaxf(bm, emu_xor_lane<1>(bm));
+        bm = fmaxf(bm, Mrun);
+        const float f = valid ? expf(mj - bm) : 0.0f;
+        const float r = expf(Mrun - bm); // 0 on the first batch (M = -inf)
+        const float lsum = emu_group_sum<MB>(lj * f);
+        Lrun = __builtin_fmaf(Lrun, r, lsum);
+        Mrun = bm;
+        if (pair) {
+            wt[pg][pj] = f;
+            if (pj == 0) rs[pg] = r;
+        }
+        __syncthreads();
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            float bm = M[i];
+            const int g = head_of[i];
+            O[i] *= rs[g];
 #pragma unroll
-            for (int j = 0; j < MB; ++j)
-                if (c0 + j < n_chunks) bm = fmaxf(bm, m[i][j]);
-            const float r = expf(M[i] - bm); // 0 on the first batch (M = -inf)
-            L[i] *= r;
-            O[i] *= r;
-#pragma unroll
-            for (int j = 0; j < MB; ++j) {
-                const float f = c0 + j < n_chunks ? expf(m[i][j] - bm) : 0.0f;
-                L[i] = __builtin_fmaf(l[i][j], f, L[i]);
-                O[i] = __builtin_fmaf(o[i][j], f, O[i]);
-            }
-            M[i] = bm;
+            for (int j = 0; j < MB; ++j) O[i] = __builtin_fmaf(o[i][j], wt[g][j], O[i]);
         }
+        __syncthreads(); // the next batch rewrites wt and rs
     }
+    if (pair && pj == 0) lh[pg] = Lrun;
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < NI; ++i)
         if (live[i]) {
-            const float r = O[i] / L[i];
-            outp[head_of[i] * HD + dim_of[i]] = r;
-            if (a.xa) emit_limbs(r, head_of[i] * HD + dim_of[i], client, a.xa, a.xs); // whole 16-lane groups
+            const int head = kvh * GQ + head_of[i];
+            const float r = O[i] / lh[head_of[i]];
+            outp[head * HD + dim_of[i]] = r;
+            if (a.xa) emit_limbs(r, head * HD + dim_of[i], client, a.xa, a.xs); // whole 16-lane groups
         }
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
