@@ -25,7 +25,8 @@
 // of 4096*S columns use S wavefronts per row-group, whose partial sums meet in
 // LDS in a fixed order (deterministic results).
 //
-// Prologue (per workgroup, overlapped with the first rows' loads): x is read,
+// Prologue (per workgroup, overlapped with the first rows' loads, which are
+// issued right after x's): x is read,
 // optionally RMS-normalised as (x * scale) * gain with
 // scale = 1 / sqrt(mean(x^2) + eps), and split into limbs in LDS.  A
 // sub-block holding an inf or NaN gets a NaN scale, so every row it meets
@@ -231,11 +232,11 @@ __global__ __launch_bounds__(EMU_WAVE * LimbShape<S>::W) void qmv_limb_kernel(Qm
         if (ACC) s.resid = a.y[row];
     };
 
-    // First rows' loads go out before the prologue, which hides under them.
+    // The activation (and gain) loads go out first, then the first rows'
+    // weight loads, and the prologue's arithmetic hides under the latter:
+    // loads complete in issue order, so a prologue value loaded after the
+    // weights would wait for their HBM round trip.
     Slot buf[D];
-#pragma unroll
-    for (int d = 0; d < D; ++d) load_slot(0, d, buf[d]);
-
     {
         const int sb = tid / SH::G, pi = tid % SH::G;
         const int c0 = 16 * sb + SH::CPT * pi;
@@ -249,6 +250,10 @@ __global__ __launch_bounds__(EMU_WAVE * LimbShape<S>::W) void qmv_limb_kernel(Qm
                 gv[k] = g.x; gv[k + 1] = g.y; gv[k + 2] = g.z; gv[k + 3] = g.w;
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int d = 0; d < D; ++d) load_slot(0, d, buf[d]);
+        __builtin_amdgcn_sched_barrier(0);
         if (NORM) {
             float ss = 0.0f;
 #pragma unroll
