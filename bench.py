@@ -267,6 +267,8 @@ def main() -> int:
     ap.add_argument("--no-smol", action="store_true", help="skip the SmolLM2 decode leg")
     ap.add_argument("--batch8-only", action="store_true",
                     help="only the 8-client decode, logged without the JSON line; for profiling")
+    ap.add_argument("--moe-only", action="store_true",
+                    help="only the Granite MoE decode leg, logged without the JSON line; for profiling")
     ap.add_argument("--roofline-rounds", type=int, default=8)
     ap.add_argument("--kernel-only", action="store_true",
                     help="only time the dominant kernel (the fused gate|up matvec over all layers); for profiling")
@@ -281,6 +283,10 @@ def main() -> int:
     ctx = Context(0)
     cus, arch = ctx.device_info()
     log(f"device: {arch}, {cus} CUs")
+    if args.moe_only:
+        log(json.dumps(moe_leg(ctx, np.random.default_rng(43))))
+        ctx.close()
+        return 0
     t0 = time.perf_counter()
     model = Model(ctx, cfg)
     model.synth(20260101)
