@@ -322,14 +322,29 @@ __global__ __launch_bounds__(kThreads) void moe_gate_kernel(const float *state, 
             for (int q = 0; q < NK; ++q) rw[j][q] = *reinterpret_cast<const float4 *>(row + 4 * EMU_WAVE * q);
         }
     };
-    load_batch(w); // the router rows do not wait for the norm
+    // The residual row and gains load first, then the router rows: loads
+    // complete in issue order, so the norm finishes under the router's loads
+    // instead of after them.
+    constexpr int PT = width / kThreads; // values per thread
     const float *xr = state + (size_t)c * width;
+    float xv0[PT], gv0[PT];
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+        xv0[j] = xr[tid + j * kThreads];
+        gv0[j] = gain[tid + j * kThreads];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_batch(w); // the router rows do not wait for the norm
+    __builtin_amdgcn_sched_barrier(0);
     float s = 0.0f;
-    for (int i = tid; i < width; i += kThreads) s = __builtin_fmaf(xr[i], xr[i], s);
+#pragma unroll
+    for (int j = 0; j < PT; ++j) s = __builtin_fmaf(xv0[j], xv0[j], s);
     s = emu_block_sum(s, red);
     const float scale = 1.0f / sqrtf(s / (float)width + eps);
-    for (int i = tid; i < width; i += kThreads) {
-        const float v = __fmul_rn(__fmul_rn(xr[i], scale), gain[i]);
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+        const int i = tid + j * kThreads;
+        const float v = __fmul_rn(__fmul_rn(xv0[j], scale), gv0[j]);
         xs[i] = v;
         xn[(size_t)c * width + i] = v;
     }
