@@ -13,7 +13,8 @@
 //      head dimension, so every K and V row is one coalesced load per lane and
 //      all 32 of a lane's loads are in flight at once; the per-lane partial
 //      dots of (position, head) pairs are combined by a butterfly
-//      reduce-scatter across the wavefront (one shuffle per pair);
+//      reduce-scatter across the wavefront (DPP and permlane swaps, one
+//      exchange per pair);
 //   4. softmax per head over the chunk (max, exp, sum), weighted values,
 //      wavefronts merged through LDS;
 //   5. writes (max, sum, unnormalised output) per query head; the last
@@ -21,6 +22,9 @@
 //      (flash-decoding) and resets the arrival counter for the next step.
 //      The hand-off uses agent-scope atomic stores/loads and a relaxed
 //      counter rather than an L2 write-back fence.
+// Load order matters: vector loads complete in issue order, so the query
+// values, gains and rotation rows are issued before the K/V rows (which come
+// from HBM), and nothing that the preparation needs sits behind them.
 // Cache layout: [client][layer][kv_head][context][head_dim], f16 or f32.
 #include "internal.hpp"
 
@@ -58,12 +62,12 @@ struct AttnArgs {
     float *xs;              //           and their scales (token = client)
 };
 
-// A value of q|k|v: one plain load (MS false), or the sum of its ns <= 8
-// partial-sum slices in slice order.  Straight-line code either way: slots
+// A value of q|k|v: one plain load (MS false), or the sum of its ns <= 12
+// partial-sum slices (as many as the multi-token matvec makes) in slice order.  Straight-line code either way: slots
 // past ns load slice 0 and are not added, so all of a thread's q|k|v loads
 // go out before the first wait (a branch on ns between two values' loads
 // would put a full memory round trip between them).
-constexpr int kMaxSlices = 8;
+constexpr int kMaxSlices = 12;
 template <bool MS> __device__ __forceinline__ float qkv_at(const float *p, int ns, size_t stride)
 {
     if constexpr (!MS) {
