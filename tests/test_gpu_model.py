@@ -160,6 +160,34 @@ def test_long_context_chunk_merge_in_the_o_projection_matches_oracle(ctx):
     model.close()
 
 
+# Hidden width 12288 at two clients: the chained multi-token matvec leaves
+# q|k|v as twelve 1024-column partial-sum slices, the most the attention's
+# branch-free slice sum takes.
+TWELVE_SLICES = DenseConfig(hidden=12288, heads=64, kv_heads=8, head_dim=128, ffn=12288, vocab=512, layers=1,
+                            rope_theta=1e6, eps=1e-6, style=_lib.EMU_STYLE_QWEN3, encoding=_lib.Q6_K, tied=False,
+                            qk_norm=True)
+
+
+def test_twelve_slice_width_batched_decode_matches_oracle(ctx):
+    model = Model(ctx, TWELVE_SLICES)
+    model.synth(1212)
+    steps, context, n = 5, 16, 2
+    sess = Session(model, n, context, kv_f16=True)
+    ref = oracle_for(model, context, True, n)
+    rng = np.random.default_rng(12)
+    worst = 0.0
+    for step in range(steps):
+        toks = rng.integers(0, TWELVE_SLICES.vocab, size=n).astype(np.uint32)
+        nxt, logits = sess.decode_step(toks, want_logits=True)
+        r = ref.step(toks)
+        for c in range(n):
+            worst = max(worst, rel_inf(logits[c], r[c]))
+            assert int(nxt[c]) == oracle.argmax(r[c], False), (step, c)
+    assert worst <= 1e-3, worst
+    sess.close()
+    model.close()
+
+
 ATTN_SHAPES = [
     # (heads, kv_heads, head_dim, style): group sizes 8, 1, 3 and 2; head dims 64, 256, 128
     (8, 1, 64, _lib.EMU_STYLE_QWEN3),
