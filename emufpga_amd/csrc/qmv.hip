@@ -199,39 +199,6 @@ __global__ __launch_bounds__(kThreads) void qmv_pipe_kernel(QmvArgs a, int total
     __shared__ float red[kThreads / EMU_WAVE];
     const int tid = threadIdx.x, lane = tid & (EMU_WAVE - 1), wv = tid / EMU_WAVE;
 
-    // Padded LDS layout: column c lives at px(c), 8-column group q's sum at
-    // xg[pg(q)].  Lane units sit 32 columns apart except for their 8-column
-    // slot, so without padding 16 lanes would share each bank group.
-    float *xg = xs + lds_x_floats(a.cols);
-    float ss = 0.0f;
-    for (int c = tid * 4; c < a.cols; c += kThreads * 4) {
-        const float4 v = *reinterpret_cast<const float4 *>(a.x + c);
-        if (NORM) ss = __builtin_fmaf(v.w, v.w, __builtin_fmaf(v.z, v.z, __builtin_fmaf(v.y, v.y, __builtin_fmaf(v.x, v.x, ss))));
-        *reinterpret_cast<float4 *>(xs + px(c)) = v;
-    }
-    if (NORM) {
-        ss = wave_sum(ss);
-        if (lane == 0) red[wv] = ss;
-        __syncthreads();
-        const float tot = (red[0] + red[1]) + (red[2] + red[3]);
-        const float scale = 1.0f / sqrtf(tot / (float)a.cols + a.eps);
-        for (int c = tid * 4; c < a.cols; c += kThreads * 4) {
-            float4 v = *reinterpret_cast<float4 *>(xs + px(c));
-            const float4 g = *reinterpret_cast<const float4 *>(a.gain + c);
-            v.x = __fmul_rn(__fmul_rn(v.x, scale), g.x);
-            v.y = __fmul_rn(__fmul_rn(v.y, scale), g.y);
-            v.z = __fmul_rn(__fmul_rn(v.z, scale), g.z);
-            v.w = __fmul_rn(__fmul_rn(v.w, scale), g.w);
-            *reinterpret_cast<float4 *>(xs + px(c)) = v;
-        }
-    }
-    __syncthreads();
-    for (int q = tid; q < a.cols / 8; q += kThreads) {
-        const float *p = xs + px(8 * q);
-        xg[pg(q)] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-    }
-    __syncthreads();
-
     const int gw = blockIdx.x * (kThreads / EMU_WAVE) + wv;
     const int n_rg = (a.rows + R - 1) / R;
     const int U = a.nb * F::UPB;
@@ -269,6 +236,62 @@ __global__ __launch_bounds__(kThreads) void qmv_pipe_kernel(QmvArgs a, int total
             dst.resid = a.y[row];
         }
     };
+
+    // Padded LDS layout: column c lives at px(c), 8-column group q's sum at
+    // xg[pg(q)].  Lane units sit 32 columns apart except for their 8-column
+    // slot, so without padding 16 lanes would share each bank group.
+    float *xg = xs + lds_x_floats(a.cols);
+    // The first 2 * kThreads * 4 columns of x load into registers, then the
+    // first item's weight loads go out, then x is staged and normalised:
+    // loads complete in issue order, so the prologue waits only for x while
+    // the weights' round trip runs.
+    float4 xr[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = tid * 4 + i * kThreads * 4;
+        xr[i] = *reinterpret_cast<const float4 *>(a.x + (c < a.cols ? c : 0)); // in-bounds stand-in
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    Buf b0, b1;
+    load_item(0, b0); // clamped to valid rows even when this wave has no item
+    __builtin_amdgcn_sched_barrier(0);
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = tid * 4 + i * kThreads * 4;
+        if (c < a.cols) {
+            const float4 v = xr[i];
+            if (NORM) ss = __builtin_fmaf(v.w, v.w, __builtin_fmaf(v.z, v.z, __builtin_fmaf(v.y, v.y, __builtin_fmaf(v.x, v.x, ss))));
+            *reinterpret_cast<float4 *>(xs + px(c)) = v;
+        }
+    }
+    for (int c = tid * 4 + 2 * kThreads * 4; c < a.cols; c += kThreads * 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(a.x + c);
+        if (NORM) ss = __builtin_fmaf(v.w, v.w, __builtin_fmaf(v.z, v.z, __builtin_fmaf(v.y, v.y, __builtin_fmaf(v.x, v.x, ss))));
+        *reinterpret_cast<float4 *>(xs + px(c)) = v;
+    }
+    if (NORM) {
+        ss = wave_sum(ss);
+        if (lane == 0) red[wv] = ss;
+        __syncthreads();
+        const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+        const float scale = 1.0f / sqrtf(tot / (float)a.cols + a.eps);
+        for (int c = tid * 4; c < a.cols; c += kThreads * 4) {
+            float4 v = *reinterpret_cast<float4 *>(xs + px(c));
+            const float4 g = *reinterpret_cast<const float4 *>(a.gain + c);
+            v.x = __fmul_rn(__fmul_rn(v.x, scale), g.x);
+            v.y = __fmul_rn(__fmul_rn(v.y, scale), g.y);
+            v.z = __fmul_rn(__fmul_rn(v.z, scale), g.z);
+            v.w = __fmul_rn(__fmul_rn(v.w, scale), g.w);
+            *reinterpret_cast<float4 *>(xs + px(c)) = v;
+        }
+    }
+    __syncthreads();
+    for (int q = tid; q < a.cols / 8; q += kThreads) {
+        const float *p = xs + px(8 * q);
+        xg[pg(q)] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    }
+    __syncthreads();
 
     float acc[NR];
 #pragma unroll
@@ -335,8 +358,6 @@ __global__ __launch_bounds__(kThreads) void qmv_pipe_kernel(QmvArgs a, int total
     // compiler's wait counts never have to cover a maybe-issued load.
     if (items > 0) {
         const int last = items - 1;
-        Buf b0, b1;
-        load_item(0, b0);
         for (int it = 0; it < items; it += 2) {
             load_item(it + 1 < last ? it + 1 : last, b1);
             process(it, b0);
