@@ -261,6 +261,7 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
     __shared__ float red[kWaves][kMaxTok][kTileRows];
 
     Unit b;
+    float4 xsv;
     __shared__ __align__(16) uint8_t wl[kWaves][kTileRows * kRowStride];
     {
         const int u = blockIdx.x;
@@ -269,6 +270,17 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
         b.rt = v % nrt;
         b.mat = v / nrt;
         const int cb = b.ks * kWaves + w; // this wavefront's 256-column block
+        // The A operands (activation limbs, from L2) load before the weights
+        // (from HBM): loads complete in issue order, so the other way round
+        // their round trip would follow the weights' instead of overlapping it.
+        const uint8_t *ap = a.xa + (size_t)cb * 16 * kSbBytes + (size_t)(kh * 24 + (live ? j : 0)) * 8;
+#pragma unroll
+        for (int sb = 0; sb < 16; ++sb) b.av[sb] = *reinterpret_cast<const long *>(ap + sb * kSbBytes);
+        // and so do the slice's activation scales (one float4 per thread)
+        static_assert(kSlice / 16 * kMaxTok / 4 <= EMU_WAVE * kWaves, "one scale load per thread");
+        const float4 *xsrc = reinterpret_cast<const float4 *>(a.xs + (size_t)b.ks * (kSlice / 16) * kMaxTok);
+        xsv = xsrc[tid < kSlice / 16 * kMaxTok / 4 ? tid : 0];
+        __builtin_amdgcn_sched_barrier(0);
         // Coalesced: instruction k covers rows 4k..4k+3 of the tile, 16 lanes
         // per row (13 x 16 bytes + the 2-byte d), into this wavefront's LDS rows.
         const int r4 = lane >> 4, c16 = lane & 15;
@@ -306,15 +318,10 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
         const uint2 s0 = *reinterpret_cast<const uint2 *>(bp + 192), s1 = *reinterpret_cast<const uint2 *>(bp + 200);
         b.sc = make_uint4(s0.x, s0.y, s1.x, s1.y);
         b.d = *reinterpret_cast<const uint16_t *>(bp + 208);
-        const uint8_t *ap = a.xa + (size_t)cb * 16 * kSbBytes + (size_t)(kh * 24 + (live ? j : 0)) * 8;
 #pragma unroll
-        for (int sb = 0; sb < 16; ++sb) b.av[sb] = live ? *reinterpret_cast<const long *>(ap + sb * kSbBytes) : 0;
+        for (int sb = 0; sb < 16; ++sb) b.av[sb] = live ? b.av[sb] : 0; // rows past the tokens are zero
     }
-    {
-        const float4 *src = reinterpret_cast<const float4 *>(a.xs + (size_t)b.ks * (kSlice / 16) * kMaxTok);
-        for (int i = tid; i < kSlice / 16 * kMaxTok / 4; i += EMU_WAVE * kWaves)
-            reinterpret_cast<float4 *>(xs)[i] = src[i];
-    }
+    if (tid < kSlice / 16 * kMaxTok / 4) reinterpret_cast<float4 *>(xs)[tid] = xsv;
     __syncthreads();
 
     // Sub-block sb = 8h + 2q + p: D = A x codes + A x (-32), then the float
