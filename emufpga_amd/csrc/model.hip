@@ -291,6 +291,10 @@ __global__ __launch_bounds__(EMU_WAVE) void router_kernel(const float *w, const 
     if (lane == 0) logits[(size_t)c * experts + e] = acc;
 }
 
+// Tokens per partial-sum block of the multi-token matvec ([slice][matrix]
+// [8 tokens][rows]).
+constexpr int kMaxTokChain = 8;
+
 // The MoE layer's gate, one workgroup per client: the FFN RMSNorm of the
 // residual stream (the arithmetic of rms_norm_kernel, kept for the experts),
 // the f32 router logits (router_kernel's per-lane order: lane l folds columns
@@ -301,7 +305,8 @@ __global__ __launch_bounds__(EMU_WAVE) void router_kernel(const float *w, const 
 template <int NK>
 __global__ __launch_bounds__(kThreads) void moe_gate_kernel(const float *state, const float *gain, const float *router,
                                                             int experts, int k, float eps, float *xn, int32_t *ids,
-                                                            float *weights)
+                                                            float *weights, float *state_out, const float *opart,
+                                                            int o_nks, float o_scale)
 {
     constexpr int width = NK * 4 * EMU_WAVE;
     constexpr int EB = 32 / NK < 8 ? 32 / NK : 8; // experts per load batch
@@ -325,17 +330,33 @@ __global__ __launch_bounds__(kThreads) void moe_gate_kernel(const float *state, 
     // The residual row and gains load first, then the router rows: loads
     // complete in issue order, so the norm finishes under the router's loads
     // instead of after them.
+    // With opart (the chained step) the o projection's partial sums, its
+    // slices added in order, first join the residual as r + v * o_scale
+    // (what the matvec's finishing pass would do), and the row is written
+    // back for the expert sum to add to.
     constexpr int PT = width / kThreads; // values per thread
     const float *xr = state + (size_t)c * width;
-    float xv0[PT], gv0[PT];
+    float xv0[PT], gv0[PT], ov0[PT];
+    const float *op = opart ? opart + (size_t)c * width : xr; // a valid source either way
 #pragma unroll
     for (int j = 0; j < PT; ++j) {
         xv0[j] = xr[tid + j * kThreads];
         gv0[j] = gain[tid + j * kThreads];
+        ov0[j] = op[tid + j * kThreads];
     }
     __builtin_amdgcn_sched_barrier(0);
     load_batch(w); // the router rows do not wait for the norm
     __builtin_amdgcn_sched_barrier(0);
+    if (opart) {
+        const size_t stride = (size_t)kMaxTokChain * width; // floats between slices
+#pragma unroll
+        for (int j = 0; j < PT; ++j) {
+            float v = ov0[j];
+            for (int q = 1; q < o_nks; ++q) v += op[q * stride + tid + j * kThreads];
+            xv0[j] = emu_resid_add(xv0[j], v, o_scale);
+            state_out[(size_t)c * width + tid + j * kThreads] = xv0[j];
+        }
+    }
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < PT; ++j) s = __builtin_fmaf(xv0[j], xv0[j], s);
@@ -625,6 +646,30 @@ int run_chain(emu_session *s)
 // with adjacent-pair RoPE and score * score_mul, residual adds r + v * 0.22,
 // then per layer RMSNorm, the f32 router, top-k routing and the selected
 // experts, and logits from the tied embedding divided by logit_div.
+// The fused gate kernel covers widths 1024 and 2048, up to 256 experts and
+// 64 routed.
+bool moe_gate_fits(const emu_model *m)
+{
+    const emu_model_config &c = m->cfg;
+    return (c.hidden == 1024 || c.hidden == 2048) && c.n_experts <= 256 && c.experts_used <= 64;
+}
+
+bool moe_chain(const emu_model *m, uint32_t n)
+{
+    const emu_model_config &c = m->cfg;
+    const int QW = (int)(c.heads * c.head_dim);
+    return m->moe() && n >= 2 && moe_gate_fits(m) && emu_mfma_supports(c.encoding, (int)c.hidden, (int)n) &&
+           emu_mfma_supports(c.encoding, QW, (int)n) && QW % 16 == 0;
+}
+
+size_t moe_chain_bytes(const emu_model *m)
+{
+    const emu_model_config &c = m->cfg;
+    const int H = (int)c.hidden, QW = (int)(c.heads * c.head_dim), KW = (int)(c.kv_heads * c.head_dim);
+    const size_t part = std::max(emu_mfma_part_bytes(QW + 2 * KW, H, 1), emu_mfma_part_bytes(H, QW, 1));
+    return emu_mfma_chain_bytes(std::max(H, QW), part);
+}
+
 int run_moe(emu_session *s)
 {
     emu_model *m = s->m;
@@ -638,8 +683,55 @@ int run_moe(emu_session *s)
     const float *attn_norm = reinterpret_cast<const float *>(m->base + m->off_attn_norm);
     const float *ffn_norm = reinterpret_cast<const float *>(m->base + m->off_ffn_norm);
     int st = EMU_OK;
+    // Chained at 2-8 clients: the q|k|v and o projections on the matrix
+    // cores with the attention adding q|k|v's partial sums and writing o's
+    // operands, and the gate kernel adding o's partial sums to the residual
+    // (no finishing or link launch around the attention).
+    const bool chain = moe_chain(m, s->n);
+    const int cap = (int)std::max(H, QW);
+    uint8_t *xa = nullptr;
+    float *xs = nullptr, *part = nullptr;
+    if (chain) emu_mfma_buffers(ctx, cap, &xa, &xs, &part);
     for (uint32_t layer = 0; layer < c.layers; ++layer) {
         const uint8_t *lw = m->base + m->off_layers + (size_t)layer * m->layer_bytes;
+        const float *opart = nullptr;
+        int o_nks = 0;
+        if (chain) {
+            EmuMfmaLink l{};
+            l.mode = 0; // input: the residual, normalised, as operands
+            l.x = s->state;
+            l.cols = (int)H;
+            l.cols_cap = cap;
+            l.n_tok = n;
+            l.gain = attn_norm + (size_t)layer * H;
+            l.eps = c.eps;
+            l.limbs = true;
+            if ((st = emu_mfma_link(ctx, l)) != EMU_OK) return st;
+            QmvArgs q{};
+            q.w = lw + m->off_q;
+            q.row_bytes = m->rb_h;
+            q.rows = (int)(QW + 2 * KW);
+            q.cols = (int)H;
+            q.nb = (int)(H / be);
+            int nks = 0;
+            if ((st = emu_mfma_matvec(ctx, q, n, cap, &nks)) != EMU_OK) return st;
+            EmuAttnLaunch al = layer_attn(s, layer);
+            al.qkv = part;
+            al.qkv_slices = nks;
+            al.qkv_client_stride = (int)(QW + 2 * KW);
+            al.qkv_slice_stride = (size_t)kMaxTokChain * (QW + 2 * KW);
+            al.xa = xa;
+            al.xs = xs;
+            if ((st = emu_launch_attn(ctx, al)) != EMU_OK) return st;
+            QmvArgs o{};
+            o.w = lw + m->off_o;
+            o.row_bytes = m->rb_q;
+            o.rows = (int)H;
+            o.cols = (int)QW;
+            o.nb = (int)(QW / be);
+            if ((st = emu_mfma_matvec(ctx, o, n, cap, &o_nks)) != EMU_OK) return st;
+            opart = part;
+        } else {
         QmvArgs a{};
         a.w = lw + m->off_q;
         a.row_bytes = m->rb_h;
@@ -663,14 +755,17 @@ int run_moe(emu_session *s)
         o.accumulate = 1;
         o.acc_scale = c.residual_scale;
         if ((st = emu_launch_qmv(ctx, c.encoding, o, n)) != EMU_OK) return st;
-        if ((H == 1024 || H == 2048) && E <= 256 && K <= 64) {
+        }
+        if (moe_gate_fits(m)) {
             const float *gn = ffn_norm + (size_t)layer * H, *rt = reinterpret_cast<const float *>(lw + m->off_r);
             if (H == 1024)
                 hipLaunchKernelGGL(moe_gate_kernel<4>, dim3((unsigned)n), dim3(kThreads), 0, ctx->stream, s->state, gn,
-                                   rt, (int)E, (int)K, c.eps, s->xn, s->rids, s->rwts);
+                                   rt, (int)E, (int)K, c.eps, s->xn, s->rids, s->rwts, s->state, opart, o_nks,
+                                   c.residual_scale);
             else
                 hipLaunchKernelGGL(moe_gate_kernel<8>, dim3((unsigned)n), dim3(kThreads), 0, ctx->stream, s->state, gn,
-                                   rt, (int)E, (int)K, c.eps, s->xn, s->rids, s->rwts);
+                                   rt, (int)E, (int)K, c.eps, s->xn, s->rids, s->rwts, s->state, opart, o_nks,
+                                   c.residual_scale);
             EMU_LAUNCH_CHECK(ctx);
         } else {
             if ((st = emu_rms_norm(ctx, s->state, ffn_norm + (size_t)layer * H, (uint32_t)n, H, c.eps, s->xn)) !=
@@ -1218,7 +1313,7 @@ extern "C" int emu_session_create(emu_model *m, uint32_t n_clients, uint32_t con
                                   {(int)c.ffn, (int)c.hidden, 2},
                                   {(int)c.hidden, (int)c.ffn, 1},
                                   {(int)c.vocab, (int)c.hidden, 1}};
-        size_t ws = mfma_chain(m, n_clients) ? mfma_chain_bytes(m) : 0;
+        size_t ws = mfma_chain(m, n_clients) ? mfma_chain_bytes(m) : moe_chain(m, n_clients) ? moe_chain_bytes(m) : 0;
         for (const auto &sh : shapes)
             if (emu_mfma_supports(c.encoding, sh[1], (int)n_clients)) {
                 const size_t b = emu_mfma_workspace_bytes(sh[0], sh[1], sh[2]);

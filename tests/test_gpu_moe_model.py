@@ -73,22 +73,25 @@ def test_moe_batched_client_gets_what_it_would_alone(ctx):  # spm-batch/tests/ba
         assert np.array_equal(alone[0], together[c])
 
 
-def test_granite_shape_decodes_and_matches_oracle(ctx):
+@pytest.mark.parametrize("n_clients", [2, 4])
+def test_granite_shape_decodes_and_matches_oracle(ctx, n_clients):
     """The Granite shape itself (24 layers cut to 2 for the oracle's speed):
-    width 1024, 32 experts of 512 with 8 routed, 49155-row tied output."""
+    width 1024, 32 experts of 512 with 8 routed, 49155-row tied output.
+    Several clients take the chained step: q|k|v and o on the matrix cores,
+    the attention adding q|k|v's partial sums, the gate kernel o's."""
     cfg = GRANITE_MOE_Q6K
     small = DenseConfig(**{**cfg.__dict__, "layers": 2})
     model = Model(ctx, small)
     model.synth(5150)
     context = 40
-    sess = Session(model, 2, context, kv_f16=True)
-    ref = oracle_for(model, context, True, 2)
+    sess = Session(model, n_clients, context, kv_f16=True)
+    ref = oracle_for(model, context, True, n_clients)
     rng = np.random.default_rng(9)
     for step in range(6):
-        toks = rng.integers(0, cfg.vocab, size=2).astype(np.uint32)
+        toks = rng.integers(0, cfg.vocab, size=n_clients).astype(np.uint32)
         nxt, logits = sess.decode_step(toks, want_logits=True)
         r = ref.step(toks)
-        for c in range(2):
+        for c in range(n_clients):
             assert rel_inf(logits[c], r[c]) <= 1e-3, (step, c)
             assert int(nxt[c]) == oracle.argmax(r[c], False), (step, c)
 
