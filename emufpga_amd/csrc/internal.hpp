@@ -509,6 +509,47 @@ __device__ __forceinline__ void emu_route_token(float *p, float *sel, int n_expe
     }
 }
 
+// One token's k (<= 8) routes in ascending expert id (ids are distinct;
+// entries past k or outside the expert range are skipped): order[i] is the
+// slot and w[i] its weight; returns how many (moe.rs:37-159 combines in that
+// order, from +0.0).
+__device__ __forceinline__ int emu_route_order(const int32_t *ids, const float *wts, int k, int n_experts,
+                                               int (&order)[8], float (&w)[8])
+{
+    int idv[8];
+    float wv[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        idv[s] = s < k ? ids[s] : 0x7fffffff;
+        wv[s] = s < k ? wts[s] : 0.0f;
+    }
+    int n = 0, prev = -1;
+    for (int i = 0; i < k; ++i) {
+        int best = -1, best_id = 0x7fffffff;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const int id = idv[s];
+            if (id > prev && id < best_id && id < n_experts) {
+                best = s;
+                best_id = id;
+            }
+        }
+        if (best < 0) break;
+        order[n++] = best;
+        prev = best_id;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int o = i < n ? order[i] : 0;
+        order[i] = o;
+        float wi = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) wi = s == o ? wv[s] : wi;
+        w[i] = wi;
+    }
+    return n;
+}
+
 // ------------------------------------------------------------- launchers --
 // Implemented per translation unit; declared here for the model code.
 struct QmvArgs {
@@ -568,6 +609,14 @@ struct EmuMfmaLink {
     const float *gain;
     float eps;
     bool limbs; // write the next matvec's A operands
+    // Mode 0 only, optional: before the norm, add a MoE layer's expert sum
+    // to x (its k routes' contributions, weighted, in expert-id order), as
+    // x + sum * m_scale, and write the result back to h.
+    const float *m_contrib;
+    const int32_t *m_ids;
+    const float *m_wts;
+    int m_k, m_experts;
+    float m_scale;
 };
 size_t emu_mfma_chain_bytes(int cols_cap, size_t max_part_bytes);
 size_t emu_mfma_part_bytes(int rows, int cols, int nmat);
@@ -601,7 +650,10 @@ struct EmuAttnLaunch {
 int emu_launch_attn(emu_ctx *ctx, const EmuAttnLaunch &l);
 // emu_moe_ffn whose weighted expert sum is added to the residual stream,
 // state = state + sum * scale with two roundings (moe.hip).
+// With combine false the weighted sum is left for the caller: the expert
+// outputs stay at emu_moe_contrib(workspace, ...) ([token][slot][width]).
 int emu_moe_ffn_resid(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok, const int32_t *d_ids,
                       const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_state,
-                      float scale);
+                      float scale, bool combine = true);
+const float *emu_moe_contrib(const void *d_workspace, uint32_t n_tok, uint32_t k, uint32_t ff);
 int emu_attn_max_chunks(int context);

@@ -72,6 +72,14 @@ struct LinkArgs {
     float eps;
     uint8_t *xa; // A operands (null: none wanted)
     float *xs;
+    // kLinkInput, optional: a MoE layer's expert sum joins x first (h gets
+    // the result): x + sum * m_scale, the sum over the token's routes in
+    // expert-id order from +0.0 (the combining pass's arithmetic).
+    const float *m_contrib;
+    const int32_t *m_ids;
+    const float *m_wts;
+    int m_k, m_experts;
+    float m_scale;
 };
 
 // A-operand layout: sub-block sb, half kh (columns 8kh..8kh+7 of the
@@ -124,6 +132,26 @@ __global__ __launch_bounds__(kLinkThreads) void mfma_link_kernel(LinkArgs a)
         const int c0 = 8 * p;
         if (a.mode == kLinkInput) {
             ld8f(a.x + (size_t)t * a.cols + c0, v[k]);
+            if (a.m_contrib) {
+                int order[8];
+                float w[8];
+                const int n = emu_route_order(a.m_ids + t * a.m_k, a.m_wts + t * a.m_k, a.m_k, a.m_experts, order, w);
+                float cv[8][8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    ld8f(a.m_contrib + ((size_t)t * a.m_k + order[i]) * a.cols + c0, cv[i]); // slot 0 past n
+                float *hp = a.h + (size_t)t * a.cols + c0;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        if (i < n) sum = __fadd_rn(sum, __fmul_rn(cv[i][e], w[i]));
+                    v[k][e] = emu_resid_add(v[k][e], sum, a.m_scale);
+                }
+                *reinterpret_cast<float4 *>(hp) = make_float4(v[k][0], v[k][1], v[k][2], v[k][3]);
+                *reinterpret_cast<float4 *>(hp + 4) = make_float4(v[k][4], v[k][5], v[k][6], v[k][7]);
+            }
         } else {
             // Slices added in slice order (the finishing pass's order).
             const size_t stride = (size_t)a.nmat * kMaxTok * a.cols;
@@ -523,6 +551,13 @@ int emu_mfma_link(emu_ctx *ctx, const EmuMfmaLink &l)
     a.eps = l.eps;
     a.xa = l.limbs ? w.xa : nullptr;
     a.xs = l.limbs ? w.xs : nullptr;
+    a.m_contrib = l.mode == kLinkInput ? l.m_contrib : nullptr;
+    a.m_ids = l.m_ids;
+    a.m_wts = l.m_wts;
+    a.m_k = l.m_k;
+    a.m_experts = l.m_experts;
+    a.m_scale = l.m_scale;
+    if (a.m_contrib && (!a.h || !a.m_ids || !a.m_wts || a.m_k < 1 || a.m_k > 8)) return EMU_E_CONFIG;
     if (l.from_part && (size_t)a.nks * a.nmat * kMaxTok * (size_t)l.cols * sizeof(float) > w.part_bytes)
         return EMU_E_CONFIG;
     // Without a norm there is no row-wide sum: one workgroup per 4096 columns.

@@ -706,6 +706,15 @@ int run_moe(emu_session *s)
             l.gain = attn_norm + (size_t)layer * H;
             l.eps = c.eps;
             l.limbs = true;
+            if (layer > 0) { // the previous layer's expert sum joins the residual here
+                l.h = s->state;
+                l.m_contrib = emu_moe_contrib(s->moe_ws, (uint32_t)n, K, c.expert_ff);
+                l.m_ids = s->rids;
+                l.m_wts = s->rwts;
+                l.m_k = (int)K;
+                l.m_experts = (int)E;
+                l.m_scale = c.residual_scale;
+            }
             if ((st = emu_mfma_link(ctx, l)) != EMU_OK) return st;
             QmvArgs q{};
             q.w = lw + m->off_q;
@@ -789,8 +798,11 @@ int run_moe(emu_session *s)
         d.k = K;
         d.act = EMU_ACT_SILU;
         // the weighted expert sum lands on the residual stream as add_scaled does
+        // chained: the next layer's link adds the expert sum (the last layer's
+        // is combined here, for the output matvec)
+        const bool combine = !chain || layer + 1 == c.layers;
         if ((st = emu_moe_ffn_resid(ctx, &d, s->xn, (uint32_t)n, s->rids, s->rwts, s->moe_ws, s->moe_ws_bytes,
-                                    s->state, c.residual_scale)) != EMU_OK)
+                                    s->state, c.residual_scale, combine)) != EMU_OK)
             return st;
     }
     QmvArgs out{};

@@ -416,41 +416,12 @@ __global__ __launch_bounds__(kThreads) void moe_combine_kernel(MoeArgs a)
     const int t = blockIdx.x;
     const int c = blockIdx.y * kThreads + threadIdx.x;
     if (c >= a.width) return;
-    int order[kMaxTok];
-    int n = 0;
-    // The token's routing entries, loaded once (k <= 8).
-    int idv[kMaxTok];
-    float wv[kMaxTok];
+    int order[8];
+    float w[8];
+    const int n = emu_route_order(a.ids + t * a.k, a.weights + t * a.k, a.k, a.n_experts, order, w);
+    float v[kMaxTok];
 #pragma unroll
-    for (int s = 0; s < kMaxTok; ++s) {
-        idv[s] = s < a.k ? a.ids[t * a.k + s] : 0x7fffffff;
-        wv[s] = s < a.k ? a.weights[t * a.k + s] : 0.0f;
-    }
-    // Selection of the token's slots by expert id (ids are distinct).
-    int prev = -1;
-    for (int i = 0; i < a.k; ++i) {
-        int best = -1, best_id = 0x7fffffff;
-#pragma unroll
-        for (int s = 0; s < kMaxTok; ++s) {
-            const int id = idv[s];
-            if (id > prev && id < best_id && id < a.n_experts) {
-                best = s;
-                best_id = id;
-            }
-        }
-        if (best < 0) break;
-        order[n++] = best;
-        prev = best_id;
-    }
-    float v[kMaxTok], w[kMaxTok];
-#pragma unroll
-    for (int i = 0; i < kMaxTok; ++i) {
-        const int o = i < n ? order[i] : 0;
-        v[i] = i < n ? a.contrib[((size_t)t * a.k + o) * a.width + c] : 0.0f;
-        w[i] = 0.0f;
-#pragma unroll
-        for (int s = 0; s < kMaxTok; ++s) w[i] = s == o ? wv[s] : w[i];
-    }
+    for (int i = 0; i < kMaxTok; ++i) v[i] = i < n ? a.contrib[((size_t)t * a.k + order[i]) * a.width + c] : 0.0f;
     float sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < kMaxTok; ++i)
@@ -533,7 +504,7 @@ namespace {
 
 int moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok, const int32_t *d_ids,
             const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_out, float *d_resid,
-            float resid_scale)
+            float resid_scale, bool combine = true)
 {
     if (!ctx || !d || !d_x || !d_ids || !d_weights || !(d_out || d_resid) || !d->d_gate || !d->d_down)
         return EMU_E_ARG;
@@ -566,8 +537,7 @@ int moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_to
     a.ids = d_ids;
     a.weights = d_weights;
     a.act_buf = static_cast<float *>(d_workspace);
-    a.contrib = reinterpret_cast<float *>(static_cast<uint8_t *>(d_workspace) +
-                                          align256(sizeof(float) * (size_t)n_tok * d->k * d->ff));
+    a.contrib = const_cast<float *>(emu_moe_contrib(d_workspace, n_tok, d->k, d->ff));
     a.out = d_out;
     a.resid = d_resid;
     a.resid_scale = resid_scale;
@@ -587,6 +557,7 @@ int moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_to
     default: return EMU_E_UNSUPPORTED;
     }
     EMU_LAUNCH_CHECK(ctx);
+    if (!combine) return EMU_OK;
     hipLaunchKernelGGL(moe_combine_kernel, dim3(n_tok, (d->width + kThreads - 1) / kThreads), dim3(kThreads), 0,
                        ctx->stream, a);
     EMU_LAUNCH_CHECK(ctx);
@@ -605,8 +576,15 @@ extern "C" int emu_moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x
 
 int emu_moe_ffn_resid(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok, const int32_t *d_ids,
                       const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_state,
-                      float scale)
+                      float scale, bool combine)
 {
     if (!d_state) return EMU_E_ARG;
-    return moe_ffn(ctx, d, d_x, n_tok, d_ids, d_weights, d_workspace, workspace_bytes, nullptr, d_state, scale);
+    return moe_ffn(ctx, d, d_x, n_tok, d_ids, d_weights, d_workspace, workspace_bytes, nullptr, d_state, scale,
+                   combine);
+}
+
+const float *emu_moe_contrib(const void *d_workspace, uint32_t n_tok, uint32_t k, uint32_t ff)
+{
+    return reinterpret_cast<const float *>(static_cast<const uint8_t *>(d_workspace) +
+                                           align256(sizeof(float) * (size_t)n_tok * k * ff));
 }
