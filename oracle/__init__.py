@@ -7,6 +7,7 @@ point and the benchmark's CPU-baseline leg use it; the product never does.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 
@@ -52,11 +53,14 @@ _lib = None
 
 
 def load() -> C.CDLL:
+    """The oracle library; ORACLE_LIB names another build of oracle.c (the
+    planted-mistake tests load mutated copies that way, in a child process)."""
     global _lib
     if _lib is None:
-        if not LIB.exists():
+        alt = os.environ.get("ORACLE_LIB")
+        if alt is None and not LIB.exists():
             build()
-        lib = C.CDLL(str(LIB))
+        lib = C.CDLL(alt or str(LIB))
         P, U, I, F, SZ = C.c_void_p, C.c_uint32, C.c_int, C.c_float, C.c_size_t
         sig = {
             "or_f16_to_f32": ([C.c_uint16], F),
@@ -84,6 +88,7 @@ def load() -> C.CDLL:
             "or_dense_layer_bytes": ([C.POINTER(DenseCfg)], SZ),
             "or_dense_step": ([C.POINTER(DenseCfg), C.POINTER(DenseWeights), P, P, P, P, U, P, U], I),
             "or_argmax": ([P, U, I], U),
+            "or_set_threads": ([I], None),
             "or_gelu_tanh": ([F], F),
             "or_moe_ffn": ([C.POINTER(MoeDesc), P, U, P, P, P], I),
             "or_moe_layer_bytes": ([C.POINTER(MoeModelCfg)], SZ),
@@ -102,6 +107,11 @@ def _p(a: np.ndarray):
 
 
 BLOCK = {OR_Q8_0: (32, 34), OR_Q2_K: (256, 84), OR_Q5_K: (256, 176), OR_Q6_K: (256, 210), OR_F32: (1, 4)}
+
+
+def set_threads(n: int) -> None:
+    """Threads for the oracle's row loops (1 = the reference's scalar path)."""
+    load().or_set_threads(int(n))
 
 
 def decode(dtype: int, data) -> np.ndarray:

@@ -260,6 +260,19 @@ void or_matvec_m2(const float *w, uint32_t rows, uint32_t cols, const float *x,
     }
 }
 
+/* Threads for the row loops: 1 (the reference's single-threaded scalar
+ * path, the default) up to the host's cores.  Results are identical for any
+ * count. */
+static int g_threads = 1;
+
+void or_set_threads(int n) { g_threads = n > 0 ? n : 1; }
+
+static int or_threads_in_use(uint32_t rows)
+{
+    /* small matrices are not worth a thread team */
+    return rows >= 64 ? g_threads : 1;
+}
+
 /* Quantized projection: spm-qwen3-slice/src/weights.rs:27-63 (decode, M1 per
  * token) or spm-granite-moe/src/layout.rs:208-242 (decode, M2 chain). */
 int or_qmatvec(int dtype, const uint8_t *w, uint32_t rows, uint32_t cols, const float *x,
@@ -271,33 +284,45 @@ int or_qmatvec(int dtype, const uint8_t *w, uint32_t rows, uint32_t cols, const 
     if (cols % be != 0)
         return -3;
     size_t row_bytes = (size_t)(cols / be) * bb;
-    float *row = (float *)malloc(sizeof(float) * cols);
-    if (!row)
-        return -4;
-    for (uint32_t r = 0; r < rows; ++r) {
-        if (or_decode(dtype, w + (size_t)r * row_bytes, row_bytes, row) != 0) {
-            free(row);
-            return -1;
+    int failed = 0;
+    /* Rows are independent and each keeps its own sequential fold, so the
+     * result does not depend on how many threads share the rows. */
+#pragma omp parallel num_threads(or_threads_in_use(rows))
+    {
+        float *row = (float *)malloc(sizeof(float) * cols);
+        if (!row) {
+#pragma omp atomic write
+            failed = -4;
         }
-        for (uint32_t t = 0; t < n_tok; ++t) {
-            const float *xt = x + (size_t)t * cols;
-            float acc;
-            if (mode == 2) {
-                acc = 0.0f;
-                for (uint32_t c = 0; c < cols; ++c)
-                    acc = fmaf(row[c], xt[c], acc);
-            } else {
-                acc = -0.0f;
-                for (uint32_t c = 0; c < cols; ++c) {
-                    float p = row[c] * xt[c];
-                    acc = acc + p;
-                }
+#pragma omp for schedule(static)
+        for (uint32_t r = 0; r < rows; ++r) {
+            if (!row)
+                continue;
+            if (or_decode(dtype, w + (size_t)r * row_bytes, row_bytes, row) != 0) {
+#pragma omp atomic write
+                failed = -1;
+                continue;
             }
-            y[(size_t)t * rows + r] = acc;
+            for (uint32_t t = 0; t < n_tok; ++t) {
+                const float *xt = x + (size_t)t * cols;
+                float acc;
+                if (mode == 2) {
+                    acc = 0.0f;
+                    for (uint32_t c = 0; c < cols; ++c)
+                        acc = fmaf(row[c], xt[c], acc);
+                } else {
+                    acc = -0.0f;
+                    for (uint32_t c = 0; c < cols; ++c) {
+                        float p = row[c] * xt[c];
+                        acc = acc + p;
+                    }
+                }
+                y[(size_t)t * rows + r] = acc;
+            }
         }
+        free(row);
     }
-    free(row);
-    return 0;
+    return failed;
 }
 
 /* int8 activation blocks of 32 (no reference counterpart: the reference has

@@ -29,16 +29,25 @@
  *                        sequential-fold brute force in numpy float32.
  *   or_rms_norm          reference KAT math.rs:54-60.
  *   or_rope_*            reference KATs attention.rs:85-99 (identity at 0,
- *                        cos(1)/sin(1) pair at position 1) and rotation
- *                        invariance of the pair norm.
+ *                        cos(1)/sin(1) pair at position 1), rotation
+ *                        invariance of the pair norm, and the float64
+ *                        rotation by pos*theta^(-2i/d) at every index for
+ *                        positions 1, 517 and 2047.
  *   or_softmax_*         reference KAT softmax([1000,1000]) == [0.5,0.5].
  *   or_top_k             reference KAT math.rs:67-70 tie order, moe.rs:183-191.
  *   or_attend_*          reference KATs attention.rs:101-131 (GQA head map,
- *                        causal exclusion) and single-position identity.
+ *                        causal exclusion), single-position identity, and a
+ *                        float64 softmax(q.K*scale)V with non-zero queries
+ *                        for each variant's score scale.
  *   or_block_dots_*      brute-force integer sums (order independent).
- *   or_dense_step        composition only; pinned through its parts and the
+ *   or_dense_step        an independent float64 composition (tests/npref.py
+ *                        dense_model_f64) in both styles, Q6_K/Q8_0, tied and
+ *                        untied, f32 and fp16 KV, over 8 positions; the
  *                        batched == alone property (spm-batch/tests/
- *                        batching.rs:128-145).
+ *                        batching.rs:128-145); planted mistakes (RoPE
+ *                        exponents, score scales, SwiGLU order, k QK-norm,
+ *                        either residual, final gain, tied output) each fail
+ *                        (tests/test_oracle_mutations.py).
  *   or_gelu_tanh         closed form in float64 (error bound), gelu(0) = 0,
  *                        odd-part identity gelu(v) - gelu(-v) = v.
  *   or_moe_ffn           composition of or_qmatvec / or_silu / or_gelu_tanh;
@@ -76,6 +85,9 @@ int or_decode(int dtype, const uint8_t *src, size_t len, float *out);
 void or_matvec_m1(const float *w, uint32_t rows, uint32_t cols, const float *x, float *y);
 void or_matvec_m2(const float *w, uint32_t rows, uint32_t cols, const float *x,
                   uint32_t positions, float *out);
+/* Threads used by or_qmatvec's row loop (default 1, the reference's
+ * single-threaded path); any count gives bit-identical results. */
+void or_set_threads(int n);
 /* Quantized matvec: decode each row exactly, then M1 (mode 1) or M2 (mode 2)
  * for every token.  x is n_tok x cols, y is n_tok x rows. */
 int or_qmatvec(int dtype, const uint8_t *w, uint32_t rows, uint32_t cols, const float *x,

@@ -259,3 +259,102 @@ def moe_model_f64(cfg, w: dict, tokens_per_step, layers_limit=0):
         lo = embed @ xn
         out.append(lo / (cfg.logit_div if cfg.logit_div else 1.0))
     return out
+
+
+def _rb(dtype: int, cols: int) -> int:
+    return cols // BLOCK_ELEMS[dtype] * BLOCK_BYTES[dtype]
+
+
+def rope_neox_f64(x, pos: int, theta: float, hd: int):
+    """Half-split rotation of each head of x by angle pos * theta^(-2i/hd),
+    i = 0..hd/2-1 (the rotation both the Qwen3 slice, spm-qwen3-slice/src/
+    attention.rs:11-25, and spm_ops::rope, spm-ops/src/attention.rs:20-32,
+    apply): x_i' = x_i cos - x_{i+hd/2} sin, x_{i+hd/2}' = x_i sin + x_{i+hd/2} cos."""
+    x = np.asarray(x, np.float64).reshape(-1, hd).copy()
+    i = np.arange(hd // 2)
+    ang = pos * np.power(float(np.float32(theta)), -2.0 * i / hd)
+    c, s = np.cos(ang), np.sin(ang)
+    a, b = x[:, :hd // 2].copy(), x[:, hd // 2:].copy()
+    x[:, :hd // 2], x[:, hd // 2:] = a * c - b * s, a * s + b * c
+    return x.reshape(-1)
+
+
+def attend_f64(q, keys, values, heads: int, kv_heads: int, hd: int, scale: float):
+    """softmax(q_h . K_g * scale) V_g for each query head h, g = h / (heads/kv_heads)."""
+    q = np.asarray(q, np.float64)
+    K, V = np.asarray(keys, np.float64), np.asarray(values, np.float64)
+    out = np.empty(heads * hd)
+    for h in range(heads):
+        g = h // (heads // kv_heads)
+        sc = K[:, g * hd:(g + 1) * hd] @ q[h * hd:(h + 1) * hd] * scale
+        p = np.exp(sc - sc.max())
+        p /= p.sum()
+        out[h * hd:(h + 1) * hd] = p @ V[:, g * hd:(g + 1) * hd]
+    return out
+
+
+def dense_model_f64(cfg, w: dict, tokens_per_step):
+    """A dense decoder in float64 from this module's own decoders, one client:
+    the logits of every step.  The composition of spm-qwen3-slice/src/
+    model.rs:35-171 and of spm-batch/src/inner.rs:16-105 (they differ only in
+    rounding order and tie rule, which float64 does not see):
+      h = embed[tok]
+      per layer: xn = rms(h)*g_attn; q,k,v = W xn; per head q,k: rms*g_qk
+        (if qk_norm) then the half-split RoPE at the position; K/V appended
+        (rounded to fp16 if the cache is fp16); att = softmax(q.k/sqrt(hd)) V;
+        h += Wo att; xn = rms(h)*g_ffn; h += Wd (silu(Wg xn) * (Wu xn))
+      logits = (tied ? embed : output) (rms(h)*g_out).
+    cfg is an oracle DenseCfg; w holds the byte blobs and gains it takes."""
+    H, hd, NH, NKV, F = cfg.hidden, cfg.head_dim, cfg.heads, cfg.kv_heads, cfg.ffn
+    QW, KW, L = NH * hd, NKV * hd, cfg.layers
+    dt = cfg.dtype
+    dec = DECODERS[dt]
+    rbH, rbQ, rbF = _rb(dt, H), _rb(dt, QW), _rb(dt, F)
+    layer_bytes = (QW + 2 * KW) * rbH + H * rbQ + 2 * F * rbH + H * rbF
+    blob = np.asarray(w["layers"]).view(np.uint8).reshape(-1)
+    mats = []
+    for layer in range(L):
+        o = layer * layer_bytes
+        shapes = [(QW, H, rbH), (KW, H, rbH), (KW, H, rbH), (H, QW, rbQ), (F, H, rbH), (F, H, rbH), (H, F, rbF)]
+        ms = []
+        for rows, cols, rb in shapes:
+            ms.append(dec(blob[o:o + rows * rb]).astype(np.float64).reshape(rows, cols))
+            o += rows * rb
+        mats.append(ms)
+    embed = dec(np.asarray(w["embed"]).view(np.uint8).reshape(-1)).astype(np.float64).reshape(-1, H)
+    out_w = embed if cfg.tied else dec(np.asarray(w["output"]).view(np.uint8).reshape(-1)).astype(
+        np.float64).reshape(-1, H)
+
+    def gains(name, layer, n):
+        return np.asarray(w[name], np.float64)[layer * n:(layer + 1) * n]
+
+    def rms(x, g):
+        return x / np.sqrt(np.mean(x * x) + float(np.float32(cfg.eps))) * g
+
+    def heads_rms(x, g):
+        x = x.reshape(-1, hd)
+        return (x / np.sqrt(np.mean(x * x, axis=1, keepdims=True) + float(np.float32(cfg.eps))) * g).reshape(-1)
+
+    def cache_round(x):
+        return x.astype(np.float16).astype(np.float64) if cfg.kv_f16 else x.astype(np.float32).astype(np.float64)
+
+    keys = [[] for _ in range(L)]
+    vals = [[] for _ in range(L)]
+    out = []
+    for pos, tok in enumerate(tokens_per_step):
+        h = embed[int(tok)].copy()
+        for layer in range(L):
+            wq, wk, wv, wo, wg, wu, wd = mats[layer]
+            xn = rms(h, gains("attn_norm", layer, H))
+            q, k, v = wq @ xn, wk @ xn, wv @ xn
+            if cfg.qk_norm:
+                q, k = heads_rms(q, gains("q_norm", layer, hd)), heads_rms(k, gains("k_norm", layer, hd))
+            q, k = rope_neox_f64(q, pos, cfg.rope_theta, hd), rope_neox_f64(k, pos, cfg.rope_theta, hd)
+            keys[layer].append(cache_round(k))
+            vals[layer].append(cache_round(v))
+            att = attend_f64(q, np.stack(keys[layer]), np.stack(vals[layer]), NH, NKV, hd, 1.0 / np.sqrt(hd))
+            h = h + wo @ att
+            xn = rms(h, gains("ffn_norm", layer, H))
+            h = h + wd @ (silu_f64(wg @ xn) * (wu @ xn))
+        out.append(out_w @ rms(h, np.asarray(w["out_norm"], np.float64)))
+    return out

@@ -443,3 +443,120 @@ def test_moe_model_step_residual_scale_matters():
     cfg.residual_scale = 0.25
     b = oracle.MoeModelOracle(cfg, w, 1).step([3])[0]
     assert np.max(np.abs(a - b)) > 1e-3 * np.max(np.abs(a))
+
+
+# ---- closed forms at positions past the KATs ------------------------------
+
+@pytest.mark.parametrize("kind,theta,hd", [("qwen3", 1e6, 128), ("fma", 1e5, 64), ("interleaved", 1.5e6, 64),
+                                           ("qwen3", 1e6, 256)])
+@pytest.mark.parametrize("pos", [1, 517, 2047])
+def test_rope_matches_float64_rotation_at_every_index(kind, theta, hd, pos):
+    """Every pair i turns by pos * theta^(-2i/hd) (spm-qwen3-slice/src/
+    attention.rs:11-25, spm-ops/src/attention.rs:20-32, spm-granite-moe/src/
+    attention.rs:12-26); half-split pairs (i, i+hd/2) or adjacent pairs
+    (2i, 2i+1).  The f32 angle carries at most ~2 ulp of pos, hence the bound."""
+    rng = np.random.default_rng(pos + hd)
+    h = rng.normal(size=hd).astype(np.float32)
+    got = oracle.rope(kind, h, pos, theta).astype(np.float64)
+    i = np.arange(hd // 2)
+    ang = pos * np.power(float(np.float32(theta)), -2.0 * i / hd)
+    c, s = np.cos(ang), np.sin(ang)
+    if kind == "interleaved":
+        a, b = h[0::2].astype(np.float64), h[1::2].astype(np.float64)
+        ga, gb = got[0::2], got[1::2]
+    else:
+        a, b = h[:hd // 2].astype(np.float64), h[hd // 2:].astype(np.float64)
+        ga, gb = got[:hd // 2], got[hd // 2:]
+    norm = np.sqrt(a * a + b * b)
+    tol = norm * (3e-7 * pos + 1e-6)
+    assert np.all(np.abs(ga - (a * c - b * s)) <= tol)
+    assert np.all(np.abs(gb - (a * s + b * c)) <= tol)
+
+
+@pytest.mark.parametrize("variant", [0, 1, 2])
+def test_attend_with_nonzero_queries_matches_float64(variant):
+    """Scores scaled as each reference form states -- dot / c (spm-qwen3-slice/
+    src/attention.rs:63), dot * (1/sqrt(hd)) (spm-kv/src/attend.rs:37-60),
+    dot * c (spm-granite-moe/src/attention.rs:44) -- then softmax and the
+    probability-weighted sum of values, in float64 at a real spread of scores."""
+    rng = np.random.default_rng(40 + variant)
+    heads, kvh, hd, positions = 8, 2, 64, 37
+    q = rng.normal(size=heads * hd).astype(np.float32)
+    keys = rng.normal(size=(positions, kvh * hd)).astype(np.float32)
+    values = rng.normal(size=(positions, kvh * hd)).astype(np.float32)
+    c = {0: 8.0, 1: 0.0, 2: 0.125}[variant]
+    got = oracle.attend(q, keys, values, positions, heads, kvh, hd, variant, c)
+    scale = {0: 1.0 / 8.0, 1: 1.0 / math.sqrt(hd), 2: 0.125}[variant]
+    ref = npref.attend_f64(q, keys, values, heads, kvh, hd, scale)
+    assert np.max(np.abs(got - ref)) <= 2e-6 * np.max(np.abs(ref))
+    # the scores are far from uniform, so a wrong scale cannot hide
+    flat = npref.attend_f64(q, keys, values, heads, kvh, hd, scale * 0.5)
+    assert np.max(np.abs(flat - ref)) > 1e-2 * np.max(np.abs(ref))
+
+
+def small_dense_model(seed, style, dtype, tied, qk_norm, kv_f16, hidden=256, heads=4, kv_heads=2, head_dim=64,
+                      ffn=512, vocab=300, layers=2, context=16):
+    rng = np.random.default_rng(seed)
+    theta, eps = (1e6, 1e-6) if style == oracle.STYLE_QWEN3 else (1e5, 1e-5)
+    cfg = oracle.DenseCfg(hidden=hidden, heads=heads, kv_heads=kv_heads, head_dim=head_dim, ffn=ffn, vocab=vocab,
+                          layers=layers, context=context, rope_theta=theta, eps=eps, style=style, dtype=dtype,
+                          kv_f16=kv_f16, tied=tied, qk_norm=qk_norm)
+    lb = oracle.load().or_dense_layer_bytes(cfg)
+    bb, be = npref.BLOCK_BYTES[dtype], npref.BLOCK_ELEMS[dtype]
+    sexp = (-12, -10) if dtype == Q6 else (-8, -6)
+    w = {
+        "layers": npref.random_blocks(dtype, layers * lb // bb, rng, scale_exp=sexp),
+        "embed": npref.random_blocks(dtype, vocab * hidden // be, rng, scale_exp=sexp),
+        "output": npref.random_blocks(dtype, vocab * hidden // be, rng, scale_exp=sexp),
+        "attn_norm": rng.uniform(0.5, 1.5, layers * hidden).astype(np.float32),
+        "ffn_norm": rng.uniform(0.5, 1.5, layers * hidden).astype(np.float32),
+        "q_norm": rng.uniform(0.5, 1.5, layers * head_dim).astype(np.float32),
+        "k_norm": rng.uniform(0.5, 1.5, layers * head_dim).astype(np.float32),
+        "out_norm": rng.uniform(0.5, 1.5, hidden).astype(np.float32),
+    }
+    return cfg, w
+
+
+DENSE_FORMS = {
+    "qwen3": dict(style=oracle.STYLE_QWEN3, dtype=Q6, tied=0, qk_norm=1, kv_f16=0),
+    "qwen3_f16kv": dict(style=oracle.STYLE_QWEN3, dtype=Q6, tied=0, qk_norm=1, kv_f16=1),
+    "smol": dict(style=oracle.STYLE_SMOL, dtype=Q8, tied=1, qk_norm=0, kv_f16=0),
+    "smol_f16kv_untied": dict(style=oracle.STYLE_SMOL, dtype=Q8, tied=0, qk_norm=0, kv_f16=1),
+}
+
+
+@pytest.mark.parametrize("form", list(DENSE_FORMS))
+def test_dense_step_matches_float64_composition(form):
+    """or_dense_step (the Qwen3 slice's layer, spm-qwen3-slice/src/model.rs:35-171,
+    and spm-batch's, inner.rs:16-105) against an independent float64
+    composition: QK-norm, the RoPE schedule at positions 0..7, the score scale,
+    SwiGLU, both residual adds, the final norm, tied or untied logits.  A
+    planted mistake in any of these moves the logits well past the bound."""
+    cfg, w = small_dense_model(70 + len(form), **DENSE_FORMS[form])
+    orc = oracle.DenseOracle(cfg, w, 1)
+    toks = [5, 17, 299, 0, 42, 7, 123, 5]
+    ref = npref.dense_model_f64(cfg, w, toks)
+    for t, want in zip(toks, ref):
+        got = orc.step([t])[0].astype(np.float64)
+        assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want)), (form, t)
+
+
+
+def test_qmatvec_threads_give_identical_bits():
+    """Rows are independent and keep their own sequential fold, so the
+    multi-threaded oracle equals the single-threaded one bit for bit."""
+    rng = np.random.default_rng(90)
+    rows, cols = 1024, 4096
+    raw = npref.random_blocks(Q6, rows * cols // 256, rng)
+    x = rng.normal(size=(2, cols)).astype(np.float32)
+    try:
+        oracle.set_threads(1)
+        one = oracle.qmatvec(Q6, raw, rows, cols, x, 2, mode=1)
+        one_m2 = oracle.qmatvec(Q6, raw, rows, cols, x, 2, mode=2)
+        oracle.set_threads(8)
+        many = oracle.qmatvec(Q6, raw, rows, cols, x, 2, mode=1)
+        many_m2 = oracle.qmatvec(Q6, raw, rows, cols, x, 2, mode=2)
+    finally:
+        oracle.set_threads(1)
+    assert np.array_equal(bits(one), bits(many))
+    assert np.array_equal(bits(one_m2), bits(many_m2))
