@@ -42,7 +42,7 @@ from emufpga_amd.serve import (GRANITE_MOE_Q6K, QWEN3_8B_Q6K, SMOLLM2_135M_Q8, D
 
 METRIC = "decode tok/s at batch 1 and 8; achieved HBM GB/s vs 8 TB/s peak"
 HBM_PEAK_GBS = 8000.0
-KERNEL = "qmv_limb_kernel<LimbQ6K, S=1, D=1, dual, norm> (fused gate|up, 2 x 12288 x 4096 Q6_K)"
+KERNEL = "qmv_limb_kernel<LimbQ6KLM, S=1, D=1, dual, norm> (fused gate|up, 2 x 12288 x 4096 Q6_K, lane-major)"
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "qmv_limb_gate_up_qwen3_8b_pmc.txt")
 COPY_BYTES = 256 << 20  # calibration copy for the PMC byte counters
 
@@ -79,12 +79,13 @@ def time_gate_up(ctx: Context, model: Model, rounds: int) -> tuple[float, int, i
     x = ctx.upload(rng.normal(size=cfg.hidden).astype(np.float32))
     gain = ctx.upload(np.ones(cfg.hidden, np.float32))
     y = ctx.alloc(cfg.ffn * 4)
-    bases = [model.tensor(_lib.EMU_T_LAYER, l)[0] for l in range(cfg.layers)]
+    # the copy the batch-1 decode step reads (the lane-major Q6_K layout)
+    bases = [model.tensor_lane_major(_lib.EMU_T_LAYER, l)[0] for l in range(cfg.layers)]
 
     def launch(base):
         ctx.check(ctx.lib.emu_qmatvec_fused(ctx.h, cfg.encoding, C.c_void_p(base + off_g),
                                             C.c_void_p(base + off_u), cfg.ffn, cfg.hidden, x.ptr, 1,
-                                            gain.ptr, cfg.eps, y.ptr, 0), "gate_up")
+                                            gain.ptr, cfg.eps, y.ptr, _lib.EMU_MV_LANE_MAJOR), "gate_up")
 
     for base in bases:  # warm
         launch(base)

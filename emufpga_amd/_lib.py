@@ -30,8 +30,10 @@ F32, F16, Q8_0, Q2_K, Q5_K, Q6_K = 0, 1, 8, 10, 13, 14
 ENCODINGS = {"F32": F32, "F16": F16, "Q8_0": Q8_0, "Q2_K": Q2_K, "Q5_K": Q5_K, "Q6_K": Q6_K}
 
 EMU_MV_ACCUMULATE = 1
+EMU_MV_LANE_MAJOR = 2
 EMU_ROPE_NEOX = 0
 EMU_ROPE_INTERLEAVED = 1
+EMU_ROPE_NEOX_FMA = 2
 EMU_STYLE_QWEN3 = 0
 EMU_STYLE_SMOL = 1
 EMU_STYLE_GRANITE = 2
@@ -182,6 +184,10 @@ SIGNATURES = {
     "emu_qmatvec_i8": [P, I, P, SZ, U32, U32, P, P, U32, P],
     "emu_rms_norm": [P, P, P, U32, U32, F, P],
     "emu_rope_table": [P, U32, U32, F, P],
+    "emu_weights_lane_major": [P, I, P, SZ, P],
+    "emu_model_sync": [P],
+    "emu_model_tensor_lane_major": [P, I, U32, C.POINTER(P), C.POINTER(SZ)],
+    "emu_rope_table_style": [P, I, U32, U32, F, P],
     "emu_rope": [P, P, U32, U32, U32, P, P, U32, I],
     "emu_attend_cached": [P, P, P, P, I, U32, U32, U32, U32, F, P],
     "emu_route": [P, P, U32, U32, U32, P, P],

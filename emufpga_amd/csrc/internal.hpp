@@ -567,6 +567,7 @@ struct QmvArgs {
     int tie_last;
     float acc_scale;       // accumulate as y + v * acc_scale (0: y + v)
     float out_div;         // results divided by this before store and keys (0: none)
+    int lane_major;        // w / w_up in the Q6_K lane-major layout (emu_lane_major_q6k)
 };
 
 // A matvec result's epilogue: divided by out_div (when set), then added to
@@ -586,6 +587,13 @@ int emu_row_bytes(int encoding, uint32_t cols, size_t *row_bytes);
 // its launcher (EMU_E_UNSUPPORTED for anything else).
 bool emu_limb_supports(int encoding, int cols);
 int emu_launch_limb(emu_ctx *ctx, int encoding, const QmvArgs &a, int *key_slots);
+// Q6_K lane-major layout (limb.hip): the block stream cut into chunks of 16
+// blocks (the last may hold fewer, n), each chunk permuted so that unit L =
+// 4*(block) + 2*h + m finds its ql-low 16 bytes at 16L, ql-high at 64n + 16L,
+// qh at 128n + 16L, the 8 scale bytes of (block, h) at 192n + 8*(L/2) and the
+// block's d at 208n + 2*(L/4).  A pure byte permutation of each chunk: sizes
+// and chunk offsets are unchanged.  src and dst must not overlap.
+int emu_lane_major_q6k(emu_ctx *ctx, const uint8_t *src, size_t nblocks, uint8_t *dst);
 // Multi-token (2..8) matvec on the int8 matrix cores (mfma.hip).  Its
 // workspace lives in the context and grows on demand (hipMalloc); callers
 // that capture graphs reserve it beforehand with emu_mfma_reserve.

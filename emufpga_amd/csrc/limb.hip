@@ -137,6 +137,24 @@ struct LimbQ6K {
     }
 };
 
+// The same units read from the lane-major layout: a 4096-column stretch of a
+// row (16 blocks) is one chunk, so each load instruction of a wavefront
+// covers one contiguous kilobyte (three of them), then 256 bytes of scales
+// and 32 of d.  The registers hold exactly what LimbQ6K::load gives, so the
+// arithmetic and its results are identical.
+struct LimbQ6KLM : LimbQ6K {
+    __device__ static __forceinline__ void load(const uint8_t *row, int unit, Raw &r)
+    {
+        const uint32_t L = (uint32_t)unit & 63u;
+        const uint8_t *c = row + 3360u * ((uint32_t)unit >> 6);
+        r.a = ld16(c + 16u * L);
+        r.b = ld16(c + 1024u + 16u * L);
+        r.q = ld16(c + 2048u + 16u * L);
+        r.sc = ld8(c + 3072u + 8u * (L >> 1));
+        r.d = ld2(c + 3328u + 2u * (L >> 2));
+    }
+};
+
 template <int S> struct LimbShape {
     static constexpr int W = S == 1 ? 8 : 4 * S; // wavefronts per workgroup
     static constexpr int RG = W / S;             // row-groups per workgroup
@@ -411,8 +429,75 @@ int emu_launch_limb(emu_ctx *ctx, int encoding, const QmvArgs &a, int *key_slots
     if (!emu_limb_supports(encoding, a.cols)) return EMU_E_UNSUPPORTED;
     if (a.rows <= 0) return EMU_E_ARG;
     switch (a.cols) {
-    case 4096: return launch_limb_s<LimbQ6K, 1>(ctx, a, key_slots);
-    case 12288: return launch_limb_s<LimbQ6K, 3>(ctx, a, key_slots);
+    case 4096:
+        return a.lane_major ? launch_limb_s<LimbQ6KLM, 1>(ctx, a, key_slots)
+                            : launch_limb_s<LimbQ6K, 1>(ctx, a, key_slots);
+    case 12288:
+        return a.lane_major ? launch_limb_s<LimbQ6KLM, 3>(ctx, a, key_slots)
+                            : launch_limb_s<LimbQ6K, 3>(ctx, a, key_slots);
     default: return EMU_E_UNSUPPORTED;
     }
+}
+
+namespace {
+
+// Byte offset, inside a chunk of n blocks in GGUF order, of the byte that the
+// lane-major layout puts at offset o.
+__device__ __forceinline__ uint32_t lane_major_source(uint32_t o, uint32_t n)
+{
+    if (o < 192u * n) {
+        const uint32_t region = o / (64u * n), r = o % (64u * n);
+        const uint32_t L = r >> 4, i = r & 15u;
+        const uint32_t j = L >> 2, h = (L >> 1) & 1u, m = L & 1u;
+        if (region == 0) return 210u * j + 64u * h + 16u * m + i;
+        if (region == 1) return 210u * j + 64u * h + 32u + 16u * m + i;
+        return 210u * j + 128u + 32u * h + 16u * m + i;
+    }
+    if (o < 208u * n) {
+        const uint32_t r = o - 192u * n, k = r >> 3, t = r & 7u;
+        return 210u * (k >> 1) + 192u + 8u * (k & 1u) + t;
+    }
+    const uint32_t r = o - 208u * n;
+    return 210u * (r >> 1) + 208u + (r & 1u);
+}
+
+// One workgroup per chunk (grid-stride): the chunk's bytes come into LDS,
+// and each destination byte is gathered from there.
+__global__ __launch_bounds__(256) void lane_major_kernel(const uint8_t *src, size_t nblocks, uint8_t *dst)
+{
+    __shared__ uint8_t in[16 * 210];
+    const size_t chunks = (nblocks + 15) / 16;
+    for (size_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+        const size_t b0 = 16 * c;
+        const uint32_t n = (uint32_t)(nblocks - b0 < 16 ? nblocks - b0 : 16);
+        const uint8_t *s = src + 210 * b0;
+        uint8_t *d = dst + 210 * b0;
+        for (uint32_t o = threadIdx.x; o < 210u * n; o += 256u) in[o] = s[o];
+        __syncthreads();
+        for (uint32_t o = threadIdx.x; o < 210u * n; o += 256u) d[o] = in[lane_major_source(o, n)];
+        __syncthreads();
+    }
+}
+
+} // namespace
+
+int emu_lane_major_q6k(emu_ctx *ctx, const uint8_t *src, size_t nblocks, uint8_t *dst)
+{
+    if (nblocks == 0) return EMU_OK;
+    const size_t chunks = (nblocks + 15) / 16;
+    const unsigned grid = (unsigned)(chunks < 65536 ? chunks : 65536);
+    hipLaunchKernelGGL(lane_major_kernel, dim3(grid), dim3(256), 0, ctx->stream, src, nblocks, dst);
+    EMU_LAUNCH_CHECK(ctx);
+    return EMU_OK;
+}
+
+extern "C" int emu_weights_lane_major(emu_ctx *ctx, int encoding, const void *d_src, size_t len, void *d_dst)
+{
+    if (!ctx || (!d_src && len) || (!d_dst && len)) return EMU_E_ARG;
+    if (encoding != EMU_ENC_Q6_K) return EMU_E_UNSUPPORTED;
+    if (len % 210 != 0) return EMU_E_SHORT;
+    const uint8_t *s = static_cast<const uint8_t *>(d_src);
+    uint8_t *d = static_cast<uint8_t *>(d_dst);
+    if (len && s < d + len && d < s + len) return EMU_E_ARG; // the permutation is not in place
+    return emu_lane_major_q6k(ctx, s, len / 210, d);
 }

@@ -52,7 +52,21 @@ struct emu_model {
     // Mixture-of-experts layers: router (f32) and gate/up/down experts,
     // expert-major (spm-granite-moe/src/weights.rs:57-73), after q, k, v, o.
     size_t off_r = 0, off_ge = 0, off_ue = 0, off_de = 0, rb_he = 0, rb_fe = 0;
+    // Lane-major copy (emu_lane_major_q6k) of the Q6_K matrices the batch-1
+    // limb matvec reads, at the same offsets as in `base` for the layers and
+    // at off_embed for the output matrix (tied or not).  Rebuilt before the
+    // next decode launch whenever the weights may have changed.
+    uint8_t *lm = nullptr;
+    bool lm_dirty = true;
     bool moe() const { return cfg.style == EMU_STYLE_GRANITE; }
+    bool lm_takes(uint32_t cols) const { return lm && emu_limb_supports(cfg.encoding, (int)cols); }
+    // The matrix a batch-1 matvec over `cols` columns reads, and whether it
+    // is the lane-major copy.
+    const uint8_t *lm_or(const uint8_t *w, uint32_t cols, uint32_t n, int *lane_major) const
+    {
+        *lane_major = n == 1 && lm_takes(cols);
+        return *lane_major ? lm + (w - base) : w;
+    }
 };
 
 struct emu_session {
@@ -849,7 +863,7 @@ int run_step(emu_session *s)
         const uint8_t *lw = m->base + m->off_layers + (size_t)layer * m->layer_bytes;
         QmvArgs a{};
         // q|k|v with the attention RMSNorm fused.
-        a.w = lw + m->off_q;
+        a.w = m->lm_or(lw + m->off_q, H, s->n, &a.lane_major);
         a.row_bytes = m->rb_h;
         a.rows = (int)(QW + 2 * KW);
         a.cols = (int)H;
@@ -862,7 +876,7 @@ int run_step(emu_session *s)
         if ((st = emu_launch_attn(ctx, layer_attn(s, layer))) != EMU_OK) return st;
         // o projection + residual.
         QmvArgs o{};
-        o.w = lw + m->off_o;
+        o.w = m->lm_or(lw + m->off_o, QW, s->n, &o.lane_major);
         o.row_bytes = m->rb_q;
         o.rows = (int)H;
         o.cols = (int)QW;
@@ -873,8 +887,8 @@ int run_step(emu_session *s)
         if ((st = emu_launch_qmv(ctx, c.encoding, o, n)) != EMU_OK) return st;
         // gate|up with the FFN RMSNorm and SwiGLU fused.
         QmvArgs g{};
-        g.w = lw + m->off_g;
-        g.w_up = lw + m->off_u;
+        g.w = m->lm_or(lw + m->off_g, H, s->n, &g.lane_major);
+        g.w_up = m->lm_or(lw + m->off_u, H, s->n, &g.lane_major);
         g.row_bytes = m->rb_h;
         g.rows = (int)F;
         g.cols = (int)H;
@@ -886,7 +900,7 @@ int run_step(emu_session *s)
         if ((st = emu_launch_qmv(ctx, c.encoding, g, n)) != EMU_OK) return st;
         // down projection + residual.
         QmvArgs d{};
-        d.w = lw + m->off_d;
+        d.w = m->lm_or(lw + m->off_d, F, s->n, &d.lane_major);
         d.row_bytes = m->rb_f;
         d.rows = (int)H;
         d.cols = (int)F;
@@ -898,6 +912,10 @@ int run_step(emu_session *s)
     }
     QmvArgs out{};
     out.w = m->base + (c.tied ? m->off_embed : m->off_output);
+    if (n == 1 && m->lm_takes(H)) {
+        out.w = m->lm + m->off_embed;
+        out.lane_major = 1;
+    }
     out.row_bytes = m->rb_h;
     out.rows = (int)c.vocab;
     out.cols = (int)H;
@@ -914,9 +932,42 @@ int run_step(emu_session *s)
     return launch_finalize(s, slots);
 }
 
+// Rebuild the lane-major copy (outside any graph capture).
+int model_sync(emu_model *m)
+{
+    if (!m->lm || !m->lm_dirty) return EMU_OK;
+    emu_ctx *ctx = m->ctx;
+    const emu_model_config &c = m->cfg;
+    const uint32_t QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim;
+    int st;
+    auto put = [&](size_t off, uint32_t rows, uint32_t cols, size_t rb) -> int {
+        if (!m->lm_takes(cols)) return EMU_OK;
+        return emu_lane_major_q6k(ctx, m->base + off, (size_t)rows * rb / 210, m->lm + off);
+    };
+    for (uint32_t l = 0; l < c.layers; ++l) {
+        const size_t lo = m->off_layers + (size_t)l * m->layer_bytes;
+        if ((st = put(lo + m->off_q, QW + 2 * KW, c.hidden, m->rb_h)) != EMU_OK ||
+            (st = put(lo + m->off_o, c.hidden, QW, m->rb_q)) != EMU_OK ||
+            (st = put(lo + m->off_g, c.ffn, c.hidden, m->rb_h)) != EMU_OK ||
+            (st = put(lo + m->off_u, c.ffn, c.hidden, m->rb_h)) != EMU_OK ||
+            (st = put(lo + m->off_d, c.hidden, c.ffn, m->rb_f)) != EMU_OK)
+            return st;
+    }
+    if (m->lm_takes(c.hidden)) {
+        const size_t src = c.tied ? m->off_embed : m->off_output;
+        if ((st = emu_lane_major_q6k(ctx, m->base + src, m->embed_bytes / 210, m->lm + m->off_embed)) != EMU_OK)
+            return st;
+    }
+    if ((st = emu_ctx_sync(ctx)) != EMU_OK) return st;
+    m->lm_dirty = false;
+    return EMU_OK;
+}
+
 int ensure_graph(emu_session *s)
 {
     if (s->exec) return EMU_OK;
+    int st0 = model_sync(s->m);
+    if (st0 != EMU_OK) return st0;
     emu_ctx *ctx = s->m->ctx;
     EMU_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
     int st = run_step(s);
@@ -951,6 +1002,7 @@ bool graphs_enabled()
 int launch_steps(emu_session *s, uint32_t count)
 {
     emu_ctx *ctx = s->m->ctx;
+    if (int st = model_sync(s->m); st != EMU_OK) return st;
     if (!graphs_enabled()) {
         for (uint32_t i = 0; i < count; ++i) {
             const int st = run_step(s);
@@ -1056,6 +1108,19 @@ extern "C" int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_m
         return st;
     }
     m->base = static_cast<uint8_t *>(p);
+    // The lane-major copy: dense Q6_K models with a width the batch-1 limb
+    // matvec takes (the layers' region plus one output matrix).
+    const bool lm_any = !moe && (emu_limb_supports(c.encoding, (int)c.hidden) ||
+                                 emu_limb_supports(c.encoding, (int)QW) || emu_limb_supports(c.encoding, (int)c.ffn));
+    if (lm_any) {
+        void *q = nullptr;
+        if ((st = emu_malloc(ctx, m->off_embed + m->embed_bytes, &q)) != EMU_OK) {
+            emu_free(ctx, m->base);
+            delete m;
+            return st;
+        }
+        m->lm = static_cast<uint8_t *>(q);
+    }
     *out = m;
     return EMU_OK;
 }
@@ -1064,6 +1129,7 @@ extern "C" int emu_model_destroy(emu_model *m)
 {
     if (!m) return EMU_E_ARG;
     emu_free(m->ctx, m->base);
+    if (m->lm) emu_free(m->ctx, m->lm);
     delete m;
     return EMU_OK;
 }
@@ -1089,12 +1155,47 @@ extern "C" int emu_model_tensor(emu_model *m, int kind, uint32_t layer, void **d
     }
     *d_ptr = m->base + off;
     *bytes = len;
+    m->lm_dirty = true; // the caller may write through the pointer
+    return EMU_OK;
+}
+
+extern "C" int emu_model_sync(emu_model *m)
+{
+    if (!m) return EMU_E_ARG;
+    m->lm_dirty = true;
+    return model_sync(m);
+}
+
+extern "C" int emu_model_tensor_lane_major(emu_model *m, int kind, uint32_t layer, void **d_ptr, size_t *bytes)
+{
+    if (!m || !d_ptr || !bytes) return EMU_E_ARG;
+    if (!m->lm) return EMU_E_UNSUPPORTED;
+    const emu_model_config &c = m->cfg;
+    size_t off = 0, len = 0;
+    switch (kind) {
+    case EMU_T_LAYER:
+        if (layer >= c.layers) return EMU_E_ARG;
+        off = m->off_layers + (size_t)layer * m->layer_bytes;
+        len = m->layer_bytes;
+        break;
+    case EMU_T_OUTPUT:
+        if (!m->lm_takes(c.hidden)) return EMU_E_UNSUPPORTED;
+        off = m->off_embed;
+        len = m->embed_bytes;
+        break;
+    default: return EMU_E_ARG;
+    }
+    const int st = model_sync(m);
+    if (st != EMU_OK) return st;
+    *d_ptr = m->lm + off;
+    *bytes = len;
     return EMU_OK;
 }
 
 extern "C" int emu_model_synth(emu_model *m, uint64_t seed)
 {
     if (!m) return EMU_E_ARG;
+    m->lm_dirty = true;
     emu_ctx *ctx = m->ctx;
     const emu_model_config &c = m->cfg;
     const uint32_t QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim;
@@ -1196,6 +1297,7 @@ Placement mk(const char *name, uint32_t dtype, std::initializer_list<uint64_t> d
 extern "C" int emu_model_load_gguf(emu_model *m, emu_gguf *g)
 {
     if (!m || !g) return EMU_E_ARG;
+    m->lm_dirty = true;
     const emu_model_config &c = m->cfg;
     const uint32_t QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim;
     const uint32_t enc = (uint32_t)c.encoding, F32 = EMU_ENC_F32;

@@ -57,11 +57,18 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(float *x, int n_tok, int
     if (pos >= (uint32_t)table_positions) pos = table_positions - 1; // host validated
     const float2 cs = table[(size_t)pos * half + i];
     float *head = x + ((size_t)t * heads + h) * hd;
-    const int a = style == EMU_ROPE_NEOX ? i : 2 * i;
-    const int b = style == EMU_ROPE_NEOX ? i + half : 2 * i + 1;
+    const bool halves = style != EMU_ROPE_INTERLEAVED; // NEOX and its fma form pair i with i + hd/2
+    const int a = halves ? i : 2 * i;
+    const int b = halves ? i + half : 2 * i + 1;
     const float l = head[a], r = head[b];
-    head[a] = l * cs.x - r * cs.y;
-    head[b] = r * cs.x + l * cs.y;
+    if (style == EMU_ROPE_NEOX_FMA) {
+        // spm-ops/src/attention.rs:28-30: fma(x, cos, -(y*sin)), fma(x, sin, y*cos)
+        head[a] = __builtin_fmaf(l, cs.x, -(r * cs.y));
+        head[b] = __builtin_fmaf(l, cs.y, r * cs.x);
+    } else {
+        head[a] = l * cs.x - r * cs.y;
+        head[b] = r * cs.x + l * cs.y;
+    }
 }
 
 // attend_cached (spm-kv/src/attend.rs:37-94): one workgroup per query head.
@@ -232,12 +239,23 @@ extern "C" int emu_rope_table(emu_ctx *ctx, uint32_t positions, uint32_t head_di
     return emu_memcpy_htod(ctx, d_table, t.data(), t.size() * sizeof(float));
 }
 
+extern "C" int emu_rope_table_style(emu_ctx *ctx, int style, uint32_t positions, uint32_t head_dim, float theta,
+                                    float *d_table)
+{
+    if (!ctx || !d_table || head_dim == 0 || head_dim % 2) return EMU_E_ARG;
+    if (style != EMU_ROPE_NEOX && style != EMU_ROPE_INTERLEAVED && style != EMU_ROPE_NEOX_FMA) return EMU_E_ARG;
+    if (positions > 65536) return EMU_E_CONFIG;
+    std::vector<float> t;
+    emu_build_rope_table(positions, head_dim, theta, style == EMU_ROPE_NEOX_FMA, t);
+    return emu_memcpy_htod(ctx, d_table, t.data(), t.size() * sizeof(float));
+}
+
 extern "C" int emu_rope(emu_ctx *ctx, float *d_x, uint32_t n_tok, uint32_t heads, uint32_t head_dim,
                         const uint32_t *d_positions, const float *d_table, uint32_t table_positions,
                         int style)
 {
     if (!ctx || !d_x || !d_positions || !d_table || head_dim % 2 || table_positions == 0) return EMU_E_ARG;
-    if (style != EMU_ROPE_NEOX && style != EMU_ROPE_INTERLEAVED) return EMU_E_ARG;
+    if (style != EMU_ROPE_NEOX && style != EMU_ROPE_INTERLEAVED && style != EMU_ROPE_NEOX_FMA) return EMU_E_ARG;
     const size_t n = (size_t)n_tok * heads * (head_dim / 2);
     if (n == 0) return EMU_OK;
     hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((n + kThreads - 1) / kThreads)), dim3(kThreads), 0,

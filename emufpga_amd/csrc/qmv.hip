@@ -646,6 +646,7 @@ int emu_launch_qmv(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int 
     if (a.rows == 0 || n_tok == 0) return EMU_OK;
     if (n_tok == 1 && emu_limb_supports(encoding, a.cols) && !(a.w_up && a.accumulate))
         return emu_launch_limb(ctx, encoding, a, key_slots);
+    if (a.lane_major) return EMU_E_UNSUPPORTED; // only the batch-1 limb kernel reads that layout
     if (emu_mfma_supports(encoding, a.cols, n_tok) && !(a.w_up && a.accumulate))
         return emu_launch_mfma(ctx, encoding, a, n_tok, key_slots);
     switch (encoding) {
@@ -696,6 +697,7 @@ extern "C" int emu_qmatvec(emu_ctx *ctx, int encoding, const void *d_w, size_t w
     a.x = d_x;
     a.y = d_y;
     a.accumulate = (flags & EMU_MV_ACCUMULATE) ? 1 : 0;
+    a.lane_major = (flags & EMU_MV_LANE_MAJOR) ? 1 : 0;
     return emu_launch_qmv(ctx, encoding, a, (int)n_tok);
 }
 
@@ -722,6 +724,7 @@ extern "C" int emu_qmatvec_fused(emu_ctx *ctx, int encoding, const void *d_w, co
     a.eps = eps;
     a.y = d_y;
     a.accumulate = (flags & EMU_MV_ACCUMULATE) ? 1 : 0;
+    a.lane_major = (flags & EMU_MV_LANE_MAJOR) ? 1 : 0;
     return emu_launch_qmv(ctx, encoding, a, (int)n_tok);
 }
 

@@ -236,6 +236,13 @@ class Model:
                        "emu_model_tensor")
         return p.value, n.value
 
+    def tensor_lane_major(self, kind: int, layer: int = 0) -> tuple[int, int]:
+        """Address and size of the lane-major copy the batch-1 matvec reads."""
+        p, n = C.c_void_p(), C.c_size_t()
+        self.ctx.check(self.ctx.lib.emu_model_tensor_lane_major(self.h, kind, layer, C.byref(p), C.byref(n)),
+                       "emu_model_tensor_lane_major")
+        return p.value, n.value
+
     def read_tensor(self, kind: int, layer: int = 0, dtype=np.uint8) -> np.ndarray:
         addr, n = self.tensor(kind, layer)
         out = np.empty(n, np.uint8)

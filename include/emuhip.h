@@ -118,11 +118,27 @@ int emu_dequant(emu_ctx *ctx, int encoding, const void *d_src, size_t src_len, f
  * EMU_E_SHAPE otherwise, EMU_E_SHORT if cols is not whole blocks).
  * x: n_tok x cols f32 (x_len elements; EMU_E_ACTIVATION_LEN if short).
  * y: n_tok x rows f32, overwritten (zero-fill semantics of stream.rs:41),
- * or accumulated into with EMU_MV_ACCUMULATE.  n_tok 1..8. */
-enum { EMU_MV_ACCUMULATE = 1u };
+ * or accumulated into with EMU_MV_ACCUMULATE.  n_tok 1..8.
+ * EMU_MV_LANE_MAJOR: W is in the Q6_K lane-major layout that
+ * emu_weights_lane_major makes; taken by Q6_K at one token with 4096 or
+ * 12288 columns, EMU_E_UNSUPPORTED otherwise.  Same results, bit for bit. */
+enum { EMU_MV_ACCUMULATE = 1u, EMU_MV_LANE_MAJOR = 2u };
 int emu_qmatvec(emu_ctx *ctx, int encoding, const void *d_w, size_t w_len, uint32_t rows,
                 uint32_t cols, const float *d_x, size_t x_len, uint32_t n_tok, float *d_y,
                 uint32_t flags);
+
+/* Device layout of Q6_K weights for the batch-1 matvec.  No reference
+ * counterpart: the reference streams GGUF block order (spm-gguf/src/
+ * tensor.rs:103-139), which is kept as the resident order everywhere else.
+ * The block stream is cut into chunks of 16 blocks (the last may hold n < 16)
+ * and each chunk's bytes are permuted so that a wavefront's loads read
+ * contiguous kilobytes: unit L = 4*block + 2*half + slot finds its 16 bytes
+ * of ql low nibbles at 16L, of ql high nibbles at 64n + 16L, of qh at
+ * 128n + 16L, its half-block's 8 scale bytes at 192n + 8*(L/2) and its
+ * block's d at 208n + 2*(L/4).  Sizes and chunk offsets are unchanged.
+ * len must be whole 210-byte blocks (EMU_E_SHORT); src and dst must not
+ * overlap (EMU_E_ARG); Q6_K only (EMU_E_UNSUPPORTED). */
+int emu_weights_lane_major(emu_ctx *ctx, int encoding, const void *d_src, size_t len, void *d_dst);
 
 /* Fused forms used by the decode step (no separate reference entry point;
  * each equals a composition of reference calls):
@@ -159,13 +175,21 @@ int emu_rms_norm(emu_ctx *ctx, const float *d_x, const float *d_gain, uint32_t n
 enum {
     EMU_ROPE_NEOX = 0,       /* halves: spm-qwen3-slice/src/attention.rs:11-25 and
                                 spm-ops/src/attention.rs:20-32 */
-    EMU_ROPE_INTERLEAVED = 1 /* adjacent pairs: spm-granite-moe/src/attention.rs:12-26 */
+    EMU_ROPE_INTERLEAVED = 1, /* adjacent pairs: spm-granite-moe/src/attention.rs:12-26 */
+    EMU_ROPE_NEOX_FMA = 2     /* halves, spm_ops::rope (spm-ops/src/attention.rs:20-32, used by
+                                 spm-kv/src/attend.rs:13-19): angle base^(-2i/d) * pos,
+                                 x' = fma(x, cos, -(y*sin)), y' = fma(x, sin, y*cos) */
 };
 /* Host-built cos/sin table (glibc powf/sinf/cosf, the reference's libm):
  * d_table[pos][i] = (cos, sin) of pos / theta^(2i/head_dim), pos < positions.
  * Built on the host and uploaded; bytes = positions * head_dim/2 * 8. */
 int emu_rope_table(emu_ctx *ctx, uint32_t positions, uint32_t head_dim, float theta,
                    float *d_table);
+/* The table of one RoPE style: EMU_ROPE_NEOX and EMU_ROPE_INTERLEAVED take
+ * pos / theta^(2i/head_dim) (as emu_rope_table); EMU_ROPE_NEOX_FMA takes
+ * theta^(-2i/head_dim) * pos (spm-ops/src/attention.rs:24-27). */
+int emu_rope_table_style(emu_ctx *ctx, int style, uint32_t positions, uint32_t head_dim, float theta,
+                         float *d_table);
 /* rotate_at (spm-kv/src/attend.rs:13-19): rotate n_tok tokens of `heads` heads
  * in place, token t at position d_positions[t]. */
 int emu_rope(emu_ctx *ctx, float *d_x, uint32_t n_tok, uint32_t heads, uint32_t head_dim,
@@ -259,6 +283,18 @@ int emu_model_tensor(emu_model *model, int kind, uint32_t layer, void **d_ptr, s
 /* Seeded synthetic weights: every quantized tensor from N(0, 0.02) draws,
  * quantized on the device; gains 1.0. */
 int emu_model_synth(emu_model *model, uint64_t seed);
+/* Rebuild the model's lane-major copy of the Q6_K matrices that the batch-1
+ * step reads (emu_weights_lane_major).  The decode entry points do this by
+ * themselves after emu_model_synth, the GGUF loaders and any
+ * emu_model_tensor call; call it after writing weights through a pointer
+ * that emu_model_tensor returned earlier. */
+int emu_model_sync(emu_model *model);
+/* Device address of the lane-major copy: a layer (same offsets as its
+ * EMU_T_LAYER tensor; only the matrices whose columns the batch-1 limb
+ * matvec takes are filled) or EMU_T_OUTPUT (the output rows, or the tied
+ * embedding's).  Brings the copy up to date first.  EMU_E_UNSUPPORTED when
+ * the model keeps no such copy (not Q6_K, or no 4096/12288-column matrix). */
+int emu_model_tensor_lane_major(emu_model *model, int kind, uint32_t layer, void **d_ptr, size_t *bytes);
 /* Algorithmic weight bytes one decode step reads (all linears + output rows). */
 int emu_model_weight_bytes(const emu_model *model, uint64_t *bytes);
 

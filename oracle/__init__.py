@@ -255,12 +255,17 @@ class MoeModelCfg(C.Structure):
         ("experts_used", C.c_uint32), ("expert_ff", C.c_uint32), ("rope_theta", C.c_float), ("eps", C.c_float),
         ("embed_scale", C.c_float), ("residual_scale", C.c_float), ("logit_div", C.c_float),
         ("score_mul", C.c_float), ("dtype", C.c_int32), ("expert_dtype", C.c_int32), ("kv_f16", C.c_int32),
-        ("qk_norm", C.c_int32),
+        ("qk_norm", C.c_int32), ("rope_neox", C.c_int32), ("untied", C.c_int32), ("gemma", C.c_int32),
+        ("expert_down_dtype", C.c_int32), ("shared_ff", C.c_uint32), ("window", C.c_uint32),
+        ("global_every", C.c_uint32), ("rope_theta_global", C.c_float), ("softcap", C.c_float),
     ]
 
 
+MOE_WEIGHT_KEYS = ("layers", "embed", "attn_norm", "ffn_norm", "q_norm", "k_norm", "out_norm", "output", "ffn_norm2")
+
+
 class MoeModelWeights(C.Structure):
-    _fields_ = [(n, C.c_void_p) for n in ("layers", "embed", "attn_norm", "ffn_norm", "q_norm", "k_norm", "out_norm")]
+    _fields_ = [(n, C.c_void_p) for n in MOE_WEIGHT_KEYS]
 
 
 def moe_layer_bytes(cfg: MoeModelCfg) -> int:
@@ -273,8 +278,7 @@ class MoeModelOracle:
     def __init__(self, cfg: MoeModelCfg, weights: dict, n_clients: int):
         self.cfg = cfg
         self.w = {k: np.ascontiguousarray(v) for k, v in weights.items()}
-        self.ws = MoeModelWeights(*[_p(self.w[k]) for k in
-                                    ("layers", "embed", "attn_norm", "ffn_norm", "q_norm", "k_norm", "out_norm")])
+        self.ws = MoeModelWeights(*[_p(self.w[k]) if k in self.w else None for k in MOE_WEIGHT_KEYS])
         kw = cfg.kv_heads * cfg.head_dim
         self.n = n_clients
         self.k = np.zeros(n_clients * cfg.layers * cfg.context * kw, np.float32)

@@ -683,11 +683,14 @@ size_t or_dense_layer_bytes(const or_dense_cfg *cfg)
            (size_t)H * rbF;
 }
 
+/* Projection of every client's row at once: each weight row is decoded once
+ * and applied to each client's vector with that client's own fold, so the
+ * result equals one call per client. */
 static int project(const or_dense_cfg *cfg, const uint8_t *w, uint32_t rows, uint32_t cols,
-                   const float *x, float *y)
+                   const float *x, uint32_t n, float *y)
 {
     int mode = cfg->style == OR_STYLE_SMOL ? 2 : 1;
-    return or_qmatvec(cfg->dtype, w, rows, cols, x, 1, y, mode);
+    return or_qmatvec(cfg->dtype, w, rows, cols, x, n, y, mode);
 }
 
 int or_dense_step(const or_dense_cfg *cfg, const or_dense_weights *w, float *kv_k, float *kv_v,
@@ -700,41 +703,45 @@ int or_dense_step(const or_dense_cfg *cfg, const or_dense_weights *w, float *kv_
     const size_t rbH = row_bytes_of(cfg->dtype, H), rbQ = row_bytes_of(cfg->dtype, QW);
     const size_t layer_bytes = or_dense_layer_bytes(cfg);
     const int smol = cfg->style == OR_STYLE_SMOL;
+    const uint32_t n = n_clients;
     if (H % 32 || QW % 32 || F % 32 || NKV == 0 || NH % NKV)
         return -3;
+    for (uint32_t ci = 0; ci < n; ++ci)
+        if (positions[ci] >= cfg->context)
+            return -5; /* context exhausted (spm-kv/src/cache.rs:50-54) */
+    if (n == 0)
+        return 0;
 
-    size_t nfl = (size_t)H * 3 + QW * 2 + KW * 2 + F * 3 + 16;
-    float *buf = (float *)malloc(sizeof(float) * nfl);
+    /* per client: state, xn, q, k, v, att, proj, gate, up (client-major) */
+    size_t per = (size_t)H * 3 + QW * 2 + KW * 2 + F * 2;
+    float *buf = (float *)malloc(sizeof(float) * per * n);
     if (!buf)
         return -4;
-    float *state = buf, *xn = state + H, *q = xn + H, *k = q + QW, *v = k + KW, *att = v + KW,
-          *proj = att + QW, *gate = proj + H, *up = gate + F, *act = up + F;
-    (void)act;
+    float *state = buf, *xn = state + (size_t)H * n, *q = xn + (size_t)H * n, *k = q + (size_t)QW * n,
+          *v = k + (size_t)KW * n, *att = v + (size_t)KW * n, *proj = att + (size_t)QW * n,
+          *gate = proj + (size_t)H * n, *up = gate + (size_t)F * n;
 
-    for (uint32_t ci = 0; ci < n_clients; ++ci) {
-        uint32_t pos = positions[ci];
-        if (pos >= cfg->context) {
-            free(buf);
-            return -5; /* context exhausted (spm-kv/src/cache.rs:50-54) */
-        }
-        float *ck = kv_k + (size_t)ci * L * cfg->context * KW;
-        float *cv = kv_v + (size_t)ci * L * cfg->context * KW;
-        /* embedding row: spm-qwen3-slice/src/model.rs:14-23, spm-batch/src/step.rs:27-30 */
-        if (or_decode(cfg->dtype, w->embed + (size_t)tokens[ci] * rbH, rbH, state) != 0) {
+    /* embedding row: spm-qwen3-slice/src/model.rs:14-23, spm-batch/src/step.rs:27-30 */
+    for (uint32_t ci = 0; ci < n; ++ci)
+        if (or_decode(cfg->dtype, w->embed + (size_t)tokens[ci] * rbH, rbH, state + (size_t)ci * H) != 0) {
             free(buf);
             return -1;
         }
-        for (uint32_t layer = 0; layer < layers_run; ++layer) {
-            const uint8_t *base = w->layers + (size_t)layer * layer_bytes;
-            const uint8_t *wq = base, *wk = wq + (size_t)QW * rbH, *wv = wk + (size_t)KW * rbH,
-                          *wo = wv + (size_t)KW * rbH, *wg = wo + (size_t)H * rbQ,
-                          *wu = wg + (size_t)F * rbH, *wd = wu + (size_t)F * rbH;
-            or_rms_norm(state, w->attn_norm + (size_t)layer * H, H, cfg->eps, xn);
-            project(cfg, wq, QW, H, xn, q);
-            project(cfg, wk, KW, H, xn, k);
-            project(cfg, wv, KW, H, xn, v);
+    for (uint32_t layer = 0; layer < layers_run; ++layer) {
+        const uint8_t *base = w->layers + (size_t)layer * layer_bytes;
+        const uint8_t *wq = base, *wk = wq + (size_t)QW * rbH, *wv = wk + (size_t)KW * rbH,
+                      *wo = wv + (size_t)KW * rbH, *wg = wo + (size_t)H * rbQ,
+                      *wu = wg + (size_t)F * rbH, *wd = wu + (size_t)F * rbH;
+        for (uint32_t ci = 0; ci < n; ++ci)
+            or_rms_norm(state + (size_t)ci * H, w->attn_norm + (size_t)layer * H, H, cfg->eps, xn + (size_t)ci * H);
+        project(cfg, wq, QW, H, xn, n, q);
+        project(cfg, wk, KW, H, xn, n, k);
+        project(cfg, wv, KW, H, xn, n, v);
+        for (uint32_t ci = 0; ci < n; ++ci) {
+            const uint32_t pos = positions[ci];
+            float *cq = q + (size_t)ci * QW, *ck_ = k + (size_t)ci * KW, *cv_ = v + (size_t)ci * KW;
             for (uint32_t h = 0; h < NH; ++h) {
-                float *qh = q + h * hd;
+                float *qh = cq + h * hd;
                 if (cfg->qk_norm)
                     or_rms_norm(qh, w->q_norm + (size_t)layer * hd, hd, cfg->eps, qh);
                 if (smol)
@@ -743,7 +750,7 @@ int or_dense_step(const or_dense_cfg *cfg, const or_dense_weights *w, float *kv_
                     or_rope_qwen3(qh, hd, pos, cfg->rope_theta);
             }
             for (uint32_t h = 0; h < NKV; ++h) {
-                float *kh = k + h * hd;
+                float *kh = ck_ + h * hd;
                 if (cfg->qk_norm)
                     or_rms_norm(kh, w->k_norm + (size_t)layer * hd, hd, cfg->eps, kh);
                 if (smol)
@@ -752,36 +759,42 @@ int or_dense_step(const or_dense_cfg *cfg, const or_dense_weights *w, float *kv_
                     or_rope_qwen3(kh, hd, pos, cfg->rope_theta);
             }
             /* KvCache::append (spm-kv/src/cache.rs:49-58) */
+            float *ck = kv_k + (size_t)ci * L * cfg->context * KW;
+            float *cv = kv_v + (size_t)ci * L * cfg->context * KW;
             float *kslot = ck + ((size_t)layer * cfg->context + pos) * KW;
             float *vslot = cv + ((size_t)layer * cfg->context + pos) * KW;
             for (uint32_t i = 0; i < KW; ++i) {
-                kslot[i] = cfg->kv_f16 ? or_f16_to_f32(or_f32_to_f16(k[i])) : k[i];
-                vslot[i] = cfg->kv_f16 ? or_f16_to_f32(or_f32_to_f16(v[i])) : v[i];
+                kslot[i] = cfg->kv_f16 ? or_f16_to_f32(or_f32_to_f16(ck_[i])) : ck_[i];
+                vslot[i] = cfg->kv_f16 ? or_f16_to_f32(or_f32_to_f16(cv_[i])) : cv_[i];
             }
             const float *pk = ck + (size_t)layer * cfg->context * KW;
             const float *pv = cv + (size_t)layer * cfg->context * KW;
             if (smol)
-                or_attend(q, pk, pv, pos + 1, NH, NKV, hd, 1, 0.0f, att);
+                or_attend(cq, pk, pv, pos + 1, NH, NKV, hd, 1, 0.0f, att + (size_t)ci * QW);
             else
-                or_attend(q, pk, pv, pos + 1, NH, NKV, hd, 0, sqrtf((float)hd), att);
-            project(cfg, wo, H, QW, att, proj);
-            for (uint32_t i = 0; i < H; ++i)
-                state[i] = state[i] + proj[i];
-            or_rms_norm(state, w->ffn_norm + (size_t)layer * H, H, cfg->eps, xn);
-            project(cfg, wg, F, H, xn, gate);
-            project(cfg, wu, F, H, xn, up);
-            for (uint32_t i = 0; i < F; ++i)
-                gate[i] = or_silu(gate[i]) * up[i];
-            project(cfg, wd, H, F, gate, proj);
-            for (uint32_t i = 0; i < H; ++i)
-                state[i] = state[i] + proj[i];
+                or_attend(cq, pk, pv, pos + 1, NH, NKV, hd, 0, sqrtf((float)hd), att + (size_t)ci * QW);
         }
-        or_rms_norm(state, w->out_norm, H, cfg->eps, xn);
-        const uint8_t *out_w = cfg->tied ? w->embed : w->output;
-        /* logits: M1 over vocabulary rows (spm-qwen3-slice/src/weights.rs:41-63,
-         * spm-batch/src/inner.rs:97-104) */
-        or_qmatvec(cfg->dtype, out_w, cfg->vocab, H, xn, 1, logits + (size_t)ci * cfg->vocab, 1);
+        project(cfg, wo, H, QW, att, n, proj);
+        for (size_t i = 0; i < (size_t)H * n; ++i)
+            state[i] = state[i] + proj[i];
+        for (uint32_t ci = 0; ci < n; ++ci)
+            or_rms_norm(state + (size_t)ci * H, w->ffn_norm + (size_t)layer * H, H, cfg->eps, xn + (size_t)ci * H);
+        project(cfg, wg, F, H, xn, n, gate);
+        project(cfg, wu, F, H, xn, n, up);
+        for (size_t i = 0; i < (size_t)F * n; ++i)
+            gate[i] = or_silu(gate[i]) * up[i];
+        project(cfg, wd, H, F, gate, n, proj);
+        for (size_t i = 0; i < (size_t)H * n; ++i)
+            state[i] = state[i] + proj[i];
     }
+    for (uint32_t ci = 0; ci < n; ++ci) {
+        float *cs = state + (size_t)ci * H, *cx = xn + (size_t)ci * H;
+        or_rms_norm(cs, w->out_norm, H, cfg->eps, cx);
+    }
+    const uint8_t *out_w = cfg->tied ? w->embed : w->output;
+    /* logits: M1 over vocabulary rows (spm-qwen3-slice/src/weights.rs:41-63,
+     * spm-batch/src/inner.rs:97-104) */
+    or_qmatvec(cfg->dtype, out_w, cfg->vocab, H, xn, n, logits, 1);
     free(buf);
     return 0;
 }
@@ -865,14 +878,26 @@ int or_moe_ffn(const or_moe_desc *d, const float *x, uint32_t n_tok, const uint3
 /* ---- mixture-of-experts decoder ------------------------------------------
  * spm-granite-moe/src/model.rs:330-411 (block, run), attention.rs:12-112
  * (interleaved rope, attend with score * 0.015625, add_scaled 0.22),
- * moe.rs:124-159 (router matvec, route, experts) and math.rs:1-40. */
+ * moe.rs:124-159 (router matvec, route, experts) and math.rs:1-40.  The
+ * OLMoE form changes only constants and the RoPE / output choices; the
+ * Gemma-4 form (oracle.h) follows gemma_smoke.rs for the experts. */
 size_t or_moe_layer_bytes(const or_moe_model_cfg *c)
 {
-    const uint32_t QW = c->heads * c->head_dim, KW = c->kv_heads * c->head_dim;
-    const size_t rbH = row_bytes_of(c->dtype, c->hidden), rbQ = row_bytes_of(c->dtype, QW);
-    const size_t rbHe = row_bytes_of(c->expert_dtype, c->hidden), rbFe = row_bytes_of(c->expert_dtype, c->expert_ff);
-    return (size_t)(QW + 2 * KW) * rbH + (size_t)c->hidden * rbQ + sizeof(float) * c->n_experts * c->hidden +
-           (size_t)c->n_experts * (2 * (size_t)c->expert_ff * rbHe + (size_t)c->hidden * rbFe);
+    const uint32_t QW = c->heads * c->head_dim, KW = c->kv_heads * c->head_dim, H = c->hidden;
+    const size_t rbH = row_bytes_of(c->dtype, H), rbQ = row_bytes_of(c->dtype, QW);
+    const size_t rbHe = row_bytes_of(c->expert_dtype, H);
+    const size_t attn = (size_t)(QW + 2 * KW) * rbH + (size_t)H * rbQ;
+    if (c->gemma) {
+        const size_t rbFd = row_bytes_of(c->expert_down_dtype, c->expert_ff);
+        const size_t shared = c->shared_ff ? 2 * (size_t)c->shared_ff * rbH +
+                                                 (size_t)H * row_bytes_of(c->dtype, c->shared_ff)
+                                           : 0;
+        return attn + sizeof(float) * ((size_t)c->n_experts * H + H + c->n_experts) + shared +
+               (size_t)c->n_experts * (2 * (size_t)c->expert_ff * rbHe + (size_t)H * rbFd);
+    }
+    const size_t rbFe = row_bytes_of(c->expert_dtype, c->expert_ff);
+    return attn + sizeof(float) * c->n_experts * H +
+           (size_t)c->n_experts * (2 * (size_t)c->expert_ff * rbHe + (size_t)H * rbFe);
 }
 
 static void add_scaled(float *a, const float *b, uint32_t n, float s)
@@ -882,26 +907,48 @@ static void add_scaled(float *a, const float *b, uint32_t n, float s)
         a[i] = s != 0.0f ? a[i] + b[i] * s : a[i] + b[i];
 }
 
+/* Gemma router input (gemma_smoke.rs:57-86): rms = (sum x^2 / W + 1e-6)
+ * .sqrt().recip() / W.sqrt(); value * scale * rms. */
+static void gemma_router_input(const float *x, const float *scale, uint32_t n, float *out)
+{
+    float acc = -0.0f;
+    for (uint32_t i = 0; i < n; ++i) {
+        float sq = x[i] * x[i];
+        acc = acc + sq;
+    }
+    const float w = (float)n;
+    float mean = acc / w;
+    float r = 1.0f / sqrtf(mean + 1e-6f);
+    r = r / sqrtf(w);
+    for (uint32_t i = 0; i < n; ++i) {
+        float t = x[i] * scale[i];
+        out[i] = t * r;
+    }
+}
+
 int or_moe_model_step(const or_moe_model_cfg *c, const or_moe_model_weights *w, float *kv_k, float *kv_v,
                       const uint32_t *positions, const uint32_t *tokens, uint32_t n_clients, float *logits,
                       uint32_t n_layers_limit)
 {
     const uint32_t H = c->hidden, hd = c->head_dim, NH = c->heads, NKV = c->kv_heads;
     const uint32_t QW = NH * hd, KW = NKV * hd, E = c->n_experts, K = c->experts_used, L = c->layers;
+    const uint32_t FF = c->expert_ff, SF = c->gemma ? c->shared_ff : 0;
     const uint32_t layers_run = n_layers_limit && n_layers_limit < L ? n_layers_limit : L;
-    if (NKV == 0 || NH % NKV || E == 0 || K == 0 || K > E || H % 256 || c->expert_ff % 32)
+    if (NKV == 0 || NH % NKV || E == 0 || K == 0 || K > E || K > 64 || H % 256 || FF % 32)
+        return -3;
+    if (c->gemma && c->global_every == 0)
         return -3;
     const size_t rbH = row_bytes_of(c->dtype, H), rbQ = row_bytes_of(c->dtype, QW);
     const size_t rbHe = row_bytes_of(c->expert_dtype, H);
     const size_t layer_bytes = or_moe_layer_bytes(c);
-    float *buf = (float *)malloc(sizeof(float) * ((size_t)H * 4 + QW * 2 + KW * 2 + E + K + 16));
+    float *buf = (float *)malloc(sizeof(float) * ((size_t)H * 6 + QW * 2 + KW * 2 + E + K + 2 * SF + 16));
     uint32_t ids[64];
-    if (!buf || K > 64) {
+    if (!buf) {
         free(buf);
         return -4;
     }
     float *state = buf, *xn = state + H, *q = xn + H, *k = q + QW, *v = k + KW, *att = v + KW, *proj = att + QW,
-          *moe = proj + H, *rl = moe + H, *rw = rl + E;
+          *moe = proj + H, *rin = moe + H, *xe = rin + H, *rl = xe + H, *rw = rl + E, *sg = rw + K, *su = sg + SF;
     for (uint32_t ci = 0; ci < n_clients; ++ci) {
         const uint32_t pos = positions[ci];
         if (pos >= c->context) {
@@ -922,8 +969,8 @@ int or_moe_model_step(const or_moe_model_cfg *c, const or_moe_model_weights *w, 
             const uint8_t *base = w->layers + (size_t)layer * layer_bytes;
             const uint8_t *wq = base, *wk = wq + (size_t)QW * rbH, *wv = wk + (size_t)KW * rbH,
                           *wo = wv + (size_t)KW * rbH, *wr = wo + (size_t)H * rbQ;
-            const uint8_t *wg = wr + sizeof(float) * E * H, *wu = wg + (size_t)E * c->expert_ff * rbHe,
-                          *wd = wu + (size_t)E * c->expert_ff * rbHe;
+            const int global = !c->gemma || c->window == 0 || (layer + 1) % c->global_every == 0;
+            const float theta = c->gemma && global ? c->rope_theta_global : c->rope_theta;
             /* block (model.rs:330-363): attention half */
             or_rms_norm(state, w->attn_norm + (size_t)layer * H, H, c->eps, xn);
             or_qmatvec(c->dtype, wq, QW, H, xn, 1, q, 1);
@@ -932,12 +979,18 @@ int or_moe_model_step(const or_moe_model_cfg *c, const or_moe_model_weights *w, 
             for (uint32_t h = 0; h < NH; ++h) {
                 if (c->qk_norm)
                     or_rms_norm(q + h * hd, w->q_norm + (size_t)layer * hd, hd, c->eps, q + h * hd);
-                or_rope_interleaved(q + h * hd, hd, pos, c->rope_theta);
+                if (c->rope_neox)
+                    or_rope_qwen3(q + h * hd, hd, pos, theta);
+                else
+                    or_rope_interleaved(q + h * hd, hd, pos, theta);
             }
             for (uint32_t h = 0; h < NKV; ++h) {
                 if (c->qk_norm)
                     or_rms_norm(k + h * hd, w->k_norm + (size_t)layer * hd, hd, c->eps, k + h * hd);
-                or_rope_interleaved(k + h * hd, hd, pos, c->rope_theta);
+                if (c->rope_neox)
+                    or_rope_qwen3(k + h * hd, hd, pos, theta);
+                else
+                    or_rope_interleaved(k + h * hd, hd, pos, theta);
             }
             float *kslot = ck + ((size_t)layer * c->context + pos) * KW;
             float *vslot = cv + ((size_t)layer * c->context + pos) * KW;
@@ -945,39 +998,85 @@ int or_moe_model_step(const or_moe_model_cfg *c, const or_moe_model_weights *w, 
                 kslot[i] = c->kv_f16 ? or_f16_to_f32(or_f32_to_f16(k[i])) : k[i];
                 vslot[i] = c->kv_f16 ? or_f16_to_f32(or_f32_to_f16(v[i])) : v[i];
             }
-            or_attend(q, ck + (size_t)layer * c->context * KW, cv + (size_t)layer * c->context * KW, pos + 1, NH,
-                      NKV, hd, 2, c->score_mul, att);
+            /* local layers see the last `window` positions, the new one included */
+            const uint32_t lo = global || pos + 1 <= c->window ? 0 : pos + 1 - c->window;
+            or_attend(q, ck + ((size_t)layer * c->context + lo) * KW, cv + ((size_t)layer * c->context + lo) * KW,
+                      pos + 1 - lo, NH, NKV, hd, 2, c->score_mul, att);
             or_qmatvec(c->dtype, wo, H, QW, att, 1, proj, 1);
             add_scaled(state, proj, H, c->residual_scale);
-            /* MoE half: ffn_norm, router (f32 M1), route, experts, add_scaled */
-            or_rms_norm(state, w->ffn_norm + (size_t)layer * H, H, c->eps, xn);
-            or_matvec_m1((const float *)wr, E, H, xn, rl);
-            or_route(rl, E, K, ids, rw);
             or_moe_desc d;
-            d.enc_gate_up = c->expert_dtype;
-            d.enc_down = c->expert_dtype;
-            d.gate = wg;
-            d.up = wu;
-            d.down = wd;
-            d.down_scale = NULL;
-            d.n_experts = E;
-            d.width = H;
-            d.ff = c->expert_ff;
-            d.k = K;
-            d.act = OR_ACT_SILU;
-            if (or_moe_ffn(&d, xn, 1, ids, rw, moe) != 0) {
-                free(buf);
-                return -6;
+            if (c->gemma) {
+                const float *router = (const float *)wr, *rscale = router + (size_t)E * H, *dscale = rscale + H;
+                const uint8_t *sgw = (const uint8_t *)(dscale + E);
+                const uint8_t *suw = sgw + (size_t)SF * rbH, *sdw = suw + (size_t)SF * rbH;
+                const uint8_t *gue = sdw + (SF ? (size_t)H * row_bytes_of(c->dtype, SF) : 0);
+                const uint8_t *dne = gue + (size_t)E * 2 * FF * rbHe;
+                /* router and experts read the residual before the shared FFN */
+                gemma_router_input(state, rscale, H, rin);
+                or_rms_norm(state, w->ffn_norm2 + (size_t)layer * H, H, 1e-6f, xe);
+                if (SF) {
+                    or_rms_norm(state, w->ffn_norm + (size_t)layer * H, H, c->eps, xn);
+                    or_qmatvec(c->dtype, sgw, SF, H, xn, 1, sg, 1);
+                    or_qmatvec(c->dtype, suw, SF, H, xn, 1, su, 1);
+                    for (uint32_t i = 0; i < SF; ++i)
+                        sg[i] = or_gelu_tanh(sg[i]) * su[i];
+                    or_qmatvec(c->dtype, sdw, H, SF, sg, 1, proj, 1);
+                    add_scaled(state, proj, H, c->residual_scale);
+                }
+                or_matvec_m1(router, E, H, rin, rl);
+                or_route(rl, E, K, ids, rw);
+                d.enc_gate_up = c->expert_dtype;
+                d.enc_down = c->expert_down_dtype;
+                d.gate = gue;
+                d.up = NULL;
+                d.down = dne;
+                d.down_scale = dscale;
+                d.act = OR_ACT_GELU_TANH;
+                d.n_experts = E;
+                d.width = H;
+                d.ff = FF;
+                d.k = K;
+                if (or_moe_ffn(&d, xe, 1, ids, rw, moe) != 0) {
+                    free(buf);
+                    return -6;
+                }
+            } else {
+                const uint8_t *wg = wr + sizeof(float) * E * H, *wu = wg + (size_t)E * FF * rbHe,
+                              *wd = wu + (size_t)E * FF * rbHe;
+                /* MoE half: ffn_norm, router (f32 M1), route, experts, add_scaled */
+                or_rms_norm(state, w->ffn_norm + (size_t)layer * H, H, c->eps, xn);
+                or_matvec_m1((const float *)wr, E, H, xn, rl);
+                or_route(rl, E, K, ids, rw);
+                d.enc_gate_up = c->expert_dtype;
+                d.enc_down = c->expert_dtype;
+                d.gate = wg;
+                d.up = wu;
+                d.down = wd;
+                d.down_scale = NULL;
+                d.n_experts = E;
+                d.width = H;
+                d.ff = FF;
+                d.k = K;
+                d.act = OR_ACT_SILU;
+                if (or_moe_ffn(&d, xn, 1, ids, rw, moe) != 0) {
+                    free(buf);
+                    return -6;
+                }
             }
             add_scaled(state, moe, H, c->residual_scale);
         }
         /* run (model.rs:403-407): output norm, tied projection, / 6.0 */
         or_rms_norm(state, w->out_norm, H, c->eps, xn);
         float *lg = logits + (size_t)ci * c->vocab;
-        or_qmatvec(c->dtype, w->embed, c->vocab, H, xn, 1, lg, 1);
+        or_qmatvec(c->dtype, c->untied ? w->output : w->embed, c->vocab, H, xn, 1, lg, 1);
         if (c->logit_div != 0.0f)
             for (uint32_t i = 0; i < c->vocab; ++i)
                 lg[i] = lg[i] / c->logit_div;
+        if (c->softcap != 0.0f)
+            for (uint32_t i = 0; i < c->vocab; ++i) {
+                float t = lg[i] / c->softcap;
+                lg[i] = c->softcap * tanhf(t);
+            }
     }
     free(buf);
     return 0;

@@ -188,15 +188,45 @@ typedef struct {
     int32_t expert_dtype; /* gate/up/down experts */
     int32_t kv_f16;
     int32_t qk_norm;      /* per-head RMSNorm on q and k before RoPE */
+    /* Forms beyond Granite's (all zero: the Granite decoder). */
+    int32_t rope_neox;    /* half-split RoPE of spm-qwen3-slice/src/attention.rs:11-25
+                             instead of Granite's adjacent pairs */
+    int32_t untied;       /* logits from the separate output matrix */
+    int32_t gemma;        /* Gemma-4 FFN half, below */
+    int32_t expert_down_dtype; /* encoding of the down experts (gemma) */
+    uint32_t shared_ff;   /* gemma: width of the shared dense GeGLU FFN (0: none) */
+    uint32_t window;      /* gemma: sliding-window length of the local layers (0: all global) */
+    uint32_t global_every;/* gemma: layer l is global when (l + 1) % global_every == 0 */
+    float rope_theta_global; /* gemma: RoPE base of the global layers */
+    float softcap;        /* gemma: logits -> softcap * tanh(logits / softcap) (0: none) */
 } or_moe_model_cfg;
 
 /* layers: per layer q, k, v, o, router (f32, n_experts x hidden), gate_exps,
  * up_exps (n_experts x expert_ff x hidden), down_exps (n_experts x hidden x
- * expert_ff), back to back; expert-major as in GGUF (weights.rs:57-73). */
+ * expert_ff), back to back; expert-major as in GGUF (weights.rs:57-73).
+ * The gemma form instead holds q, k, v, o, router (f32 n_experts x hidden),
+ * router scale (f32 hidden), down scale (f32 n_experts), the shared FFN's
+ * gate, up (shared_ff x hidden) and down (hidden x shared_ff) in `dtype`,
+ * then gate_up_exps (n_experts x 2*expert_ff x hidden: gate rows then up
+ * rows) and down_exps (n_experts x hidden x expert_ff in expert_down_dtype).
+ *
+ * Gemma-4 FFN half (no reference decoder: the reference runs layer 0's
+ * experts only, gemma_smoke.rs): with r the residual after attention,
+ *   r += down_s(gelu(gate_s xn) * up_s xn),  xn = rms(r) * ffn_norm
+ *   router input  r * rscale * (1/sqrt(mean(r^2) + 1e-6) / sqrt(hidden))
+ *                 (gemma_smoke.rs:57-86); softmax, top_k, weights p/sum p
+ *                 (gemma_smoke.rs:333-351)
+ *   r += sum over routed e, ascending: w_e * dscale_e * down_e(gelu(g) * u),
+ *        [g; u] = gate_up_e (rms(r0) * ffn_norm2) (gemma_smoke.rs:92-139,
+ *        pre_ffw_norm_2 at :278), r0 the residual before the shared FFN
+ * and attention with the half-split RoPE at theta (local layers, keys in the
+ * last `window` positions) or rope_theta_global (global layers). */
 typedef struct {
     const uint8_t *layers;
     const uint8_t *embed; /* vocab x hidden; the output projection too (tied) */
     const float *attn_norm, *ffn_norm, *q_norm, *k_norm, *out_norm;
+    const uint8_t *output; /* untied: vocab x hidden */
+    const float *ffn_norm2; /* gemma: the experts' input gains [layer][hidden] */
 } or_moe_model_weights;
 
 size_t or_moe_layer_bytes(const or_moe_model_cfg *cfg);

@@ -182,82 +182,132 @@ def moe_ffn_f64(enc_in, enc_down, gate, up, down, down_scale, n_experts, width, 
 
 
 def moe_model_f64(cfg, w: dict, tokens_per_step, layers_limit=0):
-    """A mixture-of-experts decoder (spm-granite-moe model.rs:330-411) in
-    float64 from this module's own decoders, for one client: returns the
-    logits of every step.  w holds the byte blobs and gains the oracle takes
-    (layers, embed, attn_norm, ffn_norm, out_norm); cfg an oracle MoeModelCfg."""
+    """A mixture-of-experts decoder in float64 from this module's own
+    decoders, for one client: the logits of every step.  Granite
+    (spm-granite-moe model.rs:330-411: interleaved RoPE, scores x score_mul,
+    residual x residual_scale, embeddings x embed_scale, logits / logit_div),
+    OLMoE (half-split RoPE, QK-norm, untied output) and the Gemma-4 form
+    (windowed local layers, a shared GeGLU FFN, the router input of
+    gemma_smoke.rs:57-86, fused Q5_K gate|up experts with a Q8_0 down and a
+    per-expert scale, logit soft-cap).  w holds the byte blobs and gains the
+    oracle takes; cfg an oracle MoeModelCfg."""
     H, hd, NH, NKV = cfg.hidden, cfg.head_dim, cfg.heads, cfg.kv_heads
     QW, KW, E, K, F = NH * hd, NKV * hd, cfg.n_experts, cfg.experts_used, cfg.expert_ff
-    dec, dece = DECODERS[cfg.dtype], DECODERS[cfg.expert_dtype]
-    rbH = H // 256 * {14: 210, 13: 176, 8: 34 * 8, 10: 84}[cfg.dtype]
-    rbQ = QW // 256 * {14: 210, 13: 176, 8: 34 * 8, 10: 84}[cfg.dtype]
-    rbHe = H // 256 * {14: 210, 13: 176, 8: 34 * 8, 10: 84}[cfg.expert_dtype]
-    rbFe = F // 256 * {14: 210, 13: 176, 8: 34 * 8, 10: 84}[cfg.expert_dtype]
-    layer_bytes = (QW + 2 * KW) * rbH + H * rbQ + 4 * E * H + E * (2 * F * rbHe + H * rbFe)
-    embed = dec(w["embed"]).astype(np.float64).reshape(-1, H)
+    gemma = bool(cfg.gemma)
+    dt, et = cfg.dtype, cfg.expert_dtype
+    dn_t = cfg.expert_down_dtype if gemma else et
+    SF = cfg.shared_ff if gemma else 0
+    dec = DECODERS[dt]
+    rbH, rbQ, rbHe, rbFd = _rb(dt, H), _rb(dt, QW), _rb(et, H), _rb(dn_t, F)
+    if gemma:
+        layer_bytes = ((QW + 2 * KW) * rbH + H * rbQ + 4 * (E * H + H + E) + (2 * SF * rbH + H * _rb(dt, SF)
+                       if SF else 0) + E * (2 * F * rbHe + H * rbFd))
+    else:
+        layer_bytes = (QW + 2 * KW) * rbH + H * rbQ + 4 * E * H + E * (2 * F * rbHe + H * rbFd)
+    embed = dec(np.asarray(w["embed"]).view(np.uint8).reshape(-1)).astype(np.float64).reshape(-1, H)
+    out_w = dec(np.asarray(w["output"]).view(np.uint8).reshape(-1)).astype(np.float64).reshape(-1, H) \
+        if cfg.untied else embed
     L = cfg.layers if not layers_limit else min(layers_limit, cfg.layers)
+    blob_all = np.asarray(w["layers"]).view(np.uint8).reshape(-1)
     mats = []
     for layer in range(L):
-        blob = np.asarray(w["layers"]).view(np.uint8)[layer * layer_bytes:(layer + 1) * layer_bytes]
+        blob = blob_all[layer * layer_bytes:(layer + 1) * layer_bytes]
         o = 0
+
         def take(n):
             nonlocal o
             part = blob[o:o + n]
             o += n
             return part
-        wq = dec(take(QW * rbH)).astype(np.float64).reshape(QW, H)
-        wk = dec(take(KW * rbH)).astype(np.float64).reshape(KW, H)
-        wv = dec(take(KW * rbH)).astype(np.float64).reshape(KW, H)
-        wo = dec(take(H * rbQ)).astype(np.float64).reshape(H, QW)
-        wr = take(4 * E * H).view(np.float32).astype(np.float64).reshape(E, H)
-        g, u, d = take(E * F * rbHe), take(E * F * rbHe), take(E * H * rbFe)
-        mats.append((wq, wk, wv, wo, wr, g, u, d))
+        m = {"q": dec(take(QW * rbH)).astype(np.float64).reshape(QW, H),
+             "k": dec(take(KW * rbH)).astype(np.float64).reshape(KW, H),
+             "v": dec(take(KW * rbH)).astype(np.float64).reshape(KW, H),
+             "o": dec(take(H * rbQ)).astype(np.float64).reshape(H, QW),
+             "r": take(4 * E * H).view(np.float32).astype(np.float64).reshape(E, H)}
+        if gemma:
+            m["rscale"] = take(4 * H).view(np.float32).astype(np.float64)
+            m["dscale"] = take(4 * E).view(np.float32).astype(np.float64)
+            if SF:
+                m["sg"] = dec(take(SF * rbH)).astype(np.float64).reshape(SF, H)
+                m["su"] = dec(take(SF * rbH)).astype(np.float64).reshape(SF, H)
+                m["sd"] = dec(take(H * _rb(dt, SF))).astype(np.float64).reshape(H, SF)
+            m["gu"], m["d"] = take(E * 2 * F * rbHe), take(E * H * rbFd)
+        else:
+            m["g"], m["u"], m["d"] = take(E * F * rbHe), take(E * F * rbHe), take(E * H * rbFd)
+        mats.append(m)
 
-    def norm(x, gain):
-        return x / np.sqrt(np.mean(x * x) + cfg.eps) * gain
+    eps = float(np.float32(cfg.eps))
 
-    def rope(x, pos):
+    def gains(name, layer, n):
+        return np.asarray(w[name], np.float64)[layer * n:(layer + 1) * n]
+
+    def norm(x, gain, e=eps):
+        return x / np.sqrt(np.mean(x * x) + e) * gain
+
+    def heads_norm(x, gain):
+        x = x.reshape(-1, hd)
+        return (x / np.sqrt(np.mean(x * x, axis=1, keepdims=True) + eps) * gain).reshape(-1)
+
+    def rope(x, pos, theta):
+        if cfg.rope_neox:
+            return rope_neox_f64(x, pos, theta, hd)
         x = x.reshape(-1, hd).copy()
-        i = np.arange(0, hd, 2)
-        ang = pos / np.power(float(np.float32(cfg.rope_theta)), i / hd)
+        i = np.arange(hd // 2)
+        ang = pos * np.power(float(np.float32(theta)), -2.0 * i / hd)
         c, s = np.cos(ang), np.sin(ang)
         a, b = x[:, 0::2].copy(), x[:, 1::2].copy()
         x[:, 0::2], x[:, 1::2] = a * c - b * s, a * s + b * c
         return x.reshape(-1)
+
+    def cache_round(x):
+        return x.astype(np.float16).astype(np.float64) if cfg.kv_f16 else x.astype(np.float32).astype(np.float64)
 
     res = cfg.residual_scale if cfg.residual_scale else 1.0
     keys = [[] for _ in range(L)]
     vals = [[] for _ in range(L)]
     out = []
     for pos, tok in enumerate(tokens_per_step):
-        h = embed[tok] * (cfg.embed_scale if cfg.embed_scale else 1.0)
+        h = embed[int(tok)] * (float(np.float32(cfg.embed_scale)) if cfg.embed_scale else 1.0)
         for layer in range(L):
-            wq, wk, wv, wo, wr, g, u, d = mats[layer]
-            xn = norm(h, np.asarray(w["attn_norm"], np.float64)[layer * H:(layer + 1) * H])
-            q, k, v = rope(wq @ xn, pos), rope(wk @ xn, pos), wv @ xn
-            keys[layer].append(k)
-            vals[layer].append(v)
-            Km, Vm = np.stack(keys[layer]), np.stack(vals[layer])
-            att = np.empty(QW)
-            for hh in range(NH):
-                kvh = hh // (NH // NKV)
-                sc = Km[:, kvh * hd:(kvh + 1) * hd] @ q[hh * hd:(hh + 1) * hd] * cfg.score_mul
-                p = np.exp(sc - sc.max())
-                p /= p.sum()
-                att[hh * hd:(hh + 1) * hd] = p @ Vm[:, kvh * hd:(kvh + 1) * hd]
-            h = h + (wo @ att) * res
-            xn = norm(h, np.asarray(w["ffn_norm"], np.float64)[layer * H:(layer + 1) * H])
-            lg = wr @ xn
+            m = mats[layer]
+            glob = (not gemma) or cfg.window == 0 or (layer + 1) % cfg.global_every == 0
+            theta = cfg.rope_theta_global if gemma and glob else cfg.rope_theta
+            xn = norm(h, gains("attn_norm", layer, H))
+            q, k, v = m["q"] @ xn, m["k"] @ xn, m["v"] @ xn
+            if cfg.qk_norm:
+                q, k = heads_norm(q, gains("q_norm", layer, hd)), heads_norm(k, gains("k_norm", layer, hd))
+            q, k = rope(q, pos, theta), rope(k, pos, theta)
+            keys[layer].append(cache_round(k))
+            vals[layer].append(cache_round(v))
+            lo = 0 if glob else max(0, pos + 1 - cfg.window)
+            att = attend_f64(q, np.stack(keys[layer][lo:]), np.stack(vals[layer][lo:]), NH, NKV, hd,
+                             float(np.float32(cfg.score_mul)))
+            h = h + (m["o"] @ att) * res
+            if gemma:
+                rin = h * m["rscale"] / np.sqrt(np.mean(h * h) + 1e-6) / np.sqrt(H)
+                xe = norm(h, gains("ffn_norm2", layer, H), 1e-6)
+                if SF:
+                    xs = norm(h, gains("ffn_norm", layer, H))
+                    h = h + (m["sd"] @ (gelu_tanh_f64(m["sg"] @ xs) * (m["su"] @ xs))) * res
+                lg = m["r"] @ rin
+            else:
+                xe = norm(h, gains("ffn_norm", layer, H))
+                lg = m["r"] @ xe
             pr = np.exp(lg - lg.max())
             pr /= pr.sum()
             ids = sorted(range(E), key=lambda e: (-pr[e], e))[:K]
             wts = pr[ids] / pr[ids].sum()
-            moe = moe_ffn_f64(cfg.expert_dtype, cfg.expert_dtype, g, u, d, None, E, H, F, K, False, xn,
-                              [ids], [wts])[0]
+            if gemma:
+                moe = moe_ffn_f64(et, dn_t, m["gu"], None, m["d"], m["dscale"], E, H, F, K, True, xe,
+                                  [ids], [wts])[0]
+            else:
+                moe = moe_ffn_f64(et, et, m["g"], m["u"], m["d"], None, E, H, F, K, False, xe, [ids], [wts])[0]
             h = h + moe * res
-        xn = norm(h, np.asarray(w["out_norm"], np.float64))
-        lo = embed @ xn
-        out.append(lo / (cfg.logit_div if cfg.logit_div else 1.0))
+        lo = out_w @ norm(h, np.asarray(w["out_norm"], np.float64))
+        lo = lo / (cfg.logit_div if cfg.logit_div else 1.0)
+        if gemma and cfg.softcap:
+            lo = cfg.softcap * np.tanh(lo / cfg.softcap)
+        out.append(lo)
     return out
 
 
@@ -358,3 +408,24 @@ def dense_model_f64(cfg, w: dict, tokens_per_step):
             h = h + wd @ (silu_f64(wg @ xn) * (wu @ xn))
         out.append(out_w @ rms(h, np.asarray(w["out_norm"], np.float64)))
     return out
+
+
+def lane_major_q6k(raw: np.ndarray) -> np.ndarray:
+    """The Q6_K lane-major layout: the block stream in chunks of 16 blocks
+    (the last may hold n < 16); within a chunk unit L = 4*block + 2*half +
+    slot gets its ql-low 16 bytes at 16L, ql-high at 64n + 16L, qh at
+    128n + 16L; then the n blocks' 16 scale bytes (256 B for n = 16), then
+    their d values."""
+    blocks = np.asarray(raw, np.uint8).reshape(-1, 210)
+    out = []
+    for c0 in range(0, blocks.shape[0], 16):
+        ch = blocks[c0:c0 + 16]
+        n = ch.shape[0]
+        units = np.arange(4 * n)
+        j, h, m = units // 4, (units // 2) % 2, units % 2
+        col = np.arange(16)
+        a = ch[j[:, None], (64 * h + 16 * m)[:, None] + col]
+        b = ch[j[:, None], (64 * h + 32 + 16 * m)[:, None] + col]
+        q = ch[j[:, None], (128 + 32 * h + 16 * m)[:, None] + col]
+        out += [a.reshape(-1), b.reshape(-1), q.reshape(-1), ch[:, 192:208].reshape(-1), ch[:, 208:210].reshape(-1)]
+    return np.concatenate(out) if out else np.zeros(0, np.uint8)

@@ -245,14 +245,20 @@ def test_rms_norm(ctx):
     assert np.allclose(got, ref, rtol=4e-6, atol=0)
 
 
-@pytest.mark.parametrize("style,kind,theta", [(0, "qwen3", 1e6), (1, "interleaved", 1.5e6)])
-def test_rope_bit_exact(ctx, style, kind, theta):
+@pytest.mark.parametrize("style,kind,theta,hd", [(0, "qwen3", 1e6, 128), (1, "interleaved", 1.5e6, 128),
+                                                 (2, "fma", 1e5, 64), (2, "fma", 1e5, 128)])
+def test_rope_bit_exact(ctx, style, kind, theta, hd):
+    """All three RoPE forms, table and rotation, bit for bit against the
+    oracle; style 2 is spm_ops::rope's fma form (SmolLM2)."""
     rng = np.random.default_rng(80 + style)
-    heads, hd, n_tok, table_pos = 8, 128, 4, 2048
+    heads, n_tok, table_pos = 8, 4, 2048
     x = rng.normal(size=(n_tok, heads, hd)).astype(np.float32)
     pos = np.array([0, 1, 777, 2047], np.uint32)
     tb = ctx.alloc(table_pos * hd * 4)
-    ctx.check(ctx.lib.emu_rope_table(ctx.h, table_pos, hd, theta, tb.ptr), "rope_table")
+    if style == 2:
+        ctx.check(ctx.lib.emu_rope_table_style(ctx.h, style, table_pos, hd, theta, tb.ptr), "rope_table_style")
+    else:
+        ctx.check(ctx.lib.emu_rope_table(ctx.h, table_pos, hd, theta, tb.ptr), "rope_table")
     bx, bp = ctx.upload(x), ctx.upload(pos)
     ctx.check(ctx.lib.emu_rope(ctx.h, bx.ptr, n_tok, heads, hd, bp.ptr, tb.ptr, table_pos, style), "rope")
     got = bx.read(np.float32).reshape(n_tok, heads, hd)

@@ -153,3 +153,62 @@ def test_repeatable(ctx):
     a = streamed(ctx, m, (x, 1))
     b = streamed(ctx, m, (x, 1))
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ---- the lane-major device layout ------------------------------------------
+
+@pytest.mark.parametrize("nblocks", [16, 48, 16 * 5 + 7, 3])
+def test_lane_major_permutation_matches_numpy(ctx, nblocks):
+    raw = np.random.default_rng(nblocks).integers(0, 256, size=nblocks * 210, dtype=np.uint8)
+    src, dst = ctx.upload(raw), ctx.alloc(raw.size)
+    ctx.check(ctx.lib.emu_weights_lane_major(ctx.h, Q6, src.ptr, raw.size, dst.ptr), "lane_major")
+    assert np.array_equal(dst.read(np.uint8), npref.lane_major_q6k(raw))
+
+
+def test_lane_major_refusals(ctx):
+    raw = np.zeros(210 * 16, np.uint8)
+    src, dst = ctx.upload(raw), ctx.alloc(raw.size)
+    L = ctx.lib
+    assert L.emu_weights_lane_major(ctx.h, _lib.Q8_0, src.ptr, raw.size, dst.ptr) == _lib.EMU_E_UNSUPPORTED
+    assert L.emu_weights_lane_major(ctx.h, Q6, src.ptr, raw.size - 1, dst.ptr) == _lib.EMU_E_SHORT
+    assert L.emu_weights_lane_major(ctx.h, Q6, src.ptr, raw.size, src.ptr) == _lib.EMU_E_ARG
+    # the flag is for one token at 4096 / 12288 columns only
+    x, y = ctx.upload(np.zeros(2 * 4096, np.float32)), ctx.alloc(16 * 2 * 4)
+    w = ctx.upload(np.zeros(16 * 210, np.uint8))
+    assert L.emu_qmatvec(ctx.h, Q6, w.ptr, 16 * 210, 1, 4096, x.ptr, 8192, 2, y.ptr,
+                         _lib.EMU_MV_LANE_MAJOR) == _lib.EMU_E_UNSUPPORTED
+    assert L.emu_qmatvec(ctx.h, Q6, w.ptr, 16 * 210, 4, 1024, x.ptr, 8192, 1, y.ptr,
+                         _lib.EMU_MV_LANE_MAJOR) == _lib.EMU_E_UNSUPPORTED
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 4096), (4099, 4096), (37, 12288), (4096, 12288)])
+def test_lane_major_matvec_equals_gguf_order_bit_for_bit(ctx, rows, cols):
+    """Same register contents, same arithmetic: the lane-major copy gives the
+    GGUF-order kernel's bits, plain, accumulated, normalised and SwiGLU."""
+    raw = weights(rows, cols, 3 * rows + cols)
+    rng = np.random.default_rng(rows + 1)
+    x = rng.normal(size=cols).astype(np.float32)
+    base = rng.normal(size=rows).astype(np.float32)
+    gain = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    w = ctx.upload(raw)
+    lm = ctx.alloc(raw.size)
+    ctx.check(ctx.lib.emu_weights_lane_major(ctx.h, Q6, w.ptr, raw.size, lm.ptr), "lane_major")
+    bx, bg = ctx.upload(x), ctx.upload(gain)
+
+    def run(wp, flags, acc):
+        y = ctx.upload(base.copy()) if acc else ctx.alloc(rows * 4)
+        ctx.check(ctx.lib.emu_qmatvec(ctx.h, Q6, wp, raw.size, rows, cols, bx.ptr, cols, 1, y.ptr,
+                                      flags | (_lib.EMU_MV_ACCUMULATE if acc else 0)), "qmatvec")
+        return y.read(np.uint32)
+
+    for acc in (False, True):
+        assert np.array_equal(run(w.ptr, 0, acc), run(lm.ptr, _lib.EMU_MV_LANE_MAJOR, acc))
+
+    def run_fused(wp, up, flags):
+        y = ctx.alloc(rows * 4)
+        ctx.check(ctx.lib.emu_qmatvec_fused(ctx.h, Q6, wp, up, rows, cols, bx.ptr, 1, bg.ptr, 1e-6, y.ptr, flags),
+                  "fused")
+        return y.read(np.uint32)
+
+    assert np.array_equal(run_fused(w.ptr, None, 0), run_fused(lm.ptr, None, _lib.EMU_MV_LANE_MAJOR))
+    assert np.array_equal(run_fused(w.ptr, w.ptr, 0), run_fused(lm.ptr, lm.ptr, _lib.EMU_MV_LANE_MAJOR))

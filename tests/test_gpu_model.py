@@ -283,3 +283,92 @@ def test_a_client_replaced_mid_run_gets_what_a_fresh_client_gets(ctx):
     assert got_c == alone(c_prompt)
     with pytest.raises(_lib.EmuError):
         sess.reset_client(2)
+
+
+def _oracle_greedy(ref: oracle.DenseOracle, prompt: np.ndarray, steps: int, tie_last: bool) -> np.ndarray:
+    """Feed each client's prompt one token per step, then its own greedy
+    token for `steps` steps (serve-demo.rs:62-91), all clients in lockstep."""
+    n = prompt.shape[0]
+    for t in range(prompt.shape[1]):
+        logits = ref.step(prompt[:, t])
+    toks = np.empty((n, steps), np.uint32)
+    nxt = np.array([oracle.argmax(logits[c], tie_last) for c in range(n)], np.uint32)
+    for s in range(steps):
+        toks[:, s] = nxt
+        if s + 1 < steps:
+            logits = ref.step(nxt)
+            nxt = np.array([oracle.argmax(logits[c], tie_last) for c in range(n)], np.uint32)
+    return toks
+
+
+def _oracle_threads():
+    import os
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def test_greedy_256_steps_on_the_batch1_limb_kernels(ctx):
+    """One client at Qwen3-8B widths: every projection (q|k|v, o, gate|up,
+    the 12288-column down, the output rows) runs the timed integer-limb
+    matvec; 256 greedy tokens after a 16-token prompt equal the oracle's."""
+    model = Model(ctx, WIDE_QWEN3)
+    model.synth(2024)
+    prompt_len, steps = 16, 256
+    context = prompt_len + steps
+    sess = Session(model, 1, context, kv_f16=True)
+    rng = np.random.default_rng(11)
+    prompt = rng.integers(0, WIDE_QWEN3.vocab, size=(1, prompt_len)).astype(np.uint32)
+    got = sess.generate(prompt, steps)
+    oracle.set_threads(_oracle_threads())
+    try:
+        want = _oracle_greedy(oracle_for(model, context, True, 1), prompt, steps, False)
+    finally:
+        oracle.set_threads(1)
+    assert np.array_equal(got, want), int(np.argmax(got[0] != want[0]))
+    sess.close()
+    model.close()
+
+
+# Eight clients at Qwen3-8B widths through the chained int8 matrix-core
+# matvecs; a 4096-wide FFN keeps the oracle's 256 steps short.
+WIDE_QWEN3_FF4K = DenseConfig(hidden=4096, heads=32, kv_heads=8, head_dim=128, ffn=4096, vocab=2000, layers=2,
+                              rope_theta=1e6, eps=1e-6, style=_lib.EMU_STYLE_QWEN3, encoding=_lib.Q6_K,
+                              tied=False, qk_norm=True)
+
+
+def test_greedy_256_steps_on_the_eight_client_mfma_chain(ctx):
+    """Eight clients, 16-token prompts, 256 greedy steps through the chained
+    int8 matrix-core matvecs, step by step beside the oracle: every step's
+    logits within 1e-3 of the oracle's, and every client's greedy token equal
+    to the oracle's argmax unless the oracle's top-2 gap is inside that
+    step's measured logit error (a numerical tie, reported with its size)."""
+    model = Model(ctx, WIDE_QWEN3_FF4K)
+    model.synth(2025)
+    n, prompt_len, steps = 8, 16, 256
+    context = prompt_len + steps
+    sess = Session(model, n, context, kv_f16=True)
+    rng = np.random.default_rng(12)
+    prompt = rng.integers(0, WIDE_QWEN3_FF4K.vocab, size=(n, prompt_len)).astype(np.uint32)
+    ref = oracle_for(model, context, True, n)
+    oracle.set_threads(_oracle_threads())
+    worst, ties, diverged = 0.0, [], []
+    try:
+        toks = prompt[:, 0]
+        for step in range(prompt_len - 1 + steps):
+            nxt, logits = sess.decode_step(toks, want_logits=True)
+            r = ref.step(toks)
+            for c in range(n):
+                err = float(np.max(np.abs(logits[c].astype(np.float64) - r[c])))
+                worst = max(worst, err / float(np.max(np.abs(r[c]))))
+                want = oracle.argmax(r[c], False)
+                if step >= prompt_len - 1 and int(nxt[c]) != want:
+                    top2 = np.sort(r[c].astype(np.float64))[-2:]
+                    gap = float(top2[1] - top2[0])
+                    (ties if gap <= 2.0 * err else diverged).append((step, c, gap, err))
+            toks = prompt[:, step + 1] if step + 1 < prompt_len else nxt
+    finally:
+        oracle.set_threads(1)
+    print(f"8-client chain: worst logit error {worst:.2e} (relative to max |logit|); numerical ties {ties}")
+    assert worst <= 1e-3, worst
+    assert not diverged, diverged
+    sess.close()
+    model.close()

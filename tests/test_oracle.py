@@ -560,3 +560,110 @@ def test_qmatvec_threads_give_identical_bits():
         oracle.set_threads(1)
     assert np.array_equal(bits(one), bits(many))
     assert np.array_equal(bits(one_m2), bits(many_m2))
+
+
+def test_lane_major_layout_gives_each_unit_its_gguf_bytes():
+    """The lane-major Q6_K layout (the batch-1 device copy) read at the offsets
+    the kernel's loader uses -- 16L, 1024 + 16L, 2048 + 16L, 3072 + 8(L/2),
+    3328 + 2(L/4) in each 16-block chunk -- yields, for every unit, exactly
+    the bytes the GGUF-order loader reads: ql at 64h + 16m and 64h + 32 + 16m,
+    qh at 128 + 32h + 16m, scales at 192 + 8h, d at 208 of block L/4."""
+    rng = np.random.default_rng(95)
+    raw = rng.integers(0, 256, size=48 * 210, dtype=np.uint8)  # three chunks: one 12288-column row
+    lm = npref.lane_major_q6k(raw)
+    assert lm.size == raw.size and sorted(lm.tolist()) == sorted(raw.tolist())
+    for chunk in range(3):
+        c, g = lm[3360 * chunk:3360 * (chunk + 1)], raw[3360 * chunk:3360 * (chunk + 1)]
+        for L in range(64):
+            blk, h, m = L // 4, (L // 2) % 2, L % 2
+            o = 210 * blk
+            assert np.array_equal(c[16 * L:16 * L + 16], g[o + 64 * h + 16 * m:o + 64 * h + 16 * m + 16])
+            assert np.array_equal(c[1024 + 16 * L:1040 + 16 * L], g[o + 64 * h + 32 + 16 * m:o + 64 * h + 48 + 16 * m])
+            assert np.array_equal(c[2048 + 16 * L:2064 + 16 * L], g[o + 128 + 32 * h + 16 * m:o + 144 + 32 * h + 16 * m])
+            assert np.array_equal(c[3072 + 8 * (L // 2):3080 + 8 * (L // 2)], g[o + 192 + 8 * h:o + 200 + 8 * h])
+            assert np.array_equal(c[3328 + 2 * (L // 4):3330 + 2 * (L // 4)], g[o + 208:o + 210])
+
+
+def _moe_weights(cfg, rng, w_extra=None):
+    """Seeded blobs in the layer layout of or_moe_layer_bytes for cfg."""
+    H, E, F = cfg.hidden, cfg.n_experts, cfg.expert_ff
+    QW, KW = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    dt, et = cfg.dtype, cfg.expert_dtype
+
+    def blocks(dtype, n_elems, sexp=(-12, -10)):
+        return npref.random_blocks(dtype, n_elems // npref.BLOCK_ELEMS[dtype], rng,
+                                   scale_exp=sexp).view(np.uint8).reshape(-1)
+
+    parts = []
+    for _ in range(cfg.layers):
+        parts.append(blocks(dt, (QW + 2 * KW) * H))
+        parts.append(blocks(dt, H * QW))
+        parts.append((rng.normal(size=E * H) * 0.05).astype(np.float32).view(np.uint8))
+        if cfg.gemma:
+            parts.append(rng.uniform(0.5, 1.5, H).astype(np.float32).view(np.uint8))  # router scale
+            parts.append(rng.uniform(0.5, 2.0, E).astype(np.float32).view(np.uint8))  # down scale
+            if cfg.shared_ff:
+                parts += [blocks(dt, cfg.shared_ff * H), blocks(dt, cfg.shared_ff * H), blocks(dt, H * cfg.shared_ff)]
+            parts.append(blocks(et, E * 2 * F * H, (-8, -6) if et == Q5 else (-12, -10)))
+            parts.append(blocks(cfg.expert_down_dtype, E * H * F, (-8, -6)))
+        else:
+            for _ in range(3):
+                parts.append(blocks(et, E * F * H))
+    layers = np.concatenate(parts)
+    assert layers.size == cfg.layers * oracle.moe_layer_bytes(cfg)
+    w = {"layers": layers, "embed": blocks(dt, cfg.vocab * H, (-10, -8)),
+         "output": blocks(dt, cfg.vocab * H, (-10, -8)),
+         "attn_norm": rng.uniform(0.5, 1.5, cfg.layers * H).astype(np.float32),
+         "ffn_norm": rng.uniform(0.5, 1.5, cfg.layers * H).astype(np.float32),
+         "ffn_norm2": rng.uniform(0.5, 1.5, cfg.layers * H).astype(np.float32),
+         "q_norm": rng.uniform(0.5, 1.5, cfg.layers * cfg.head_dim).astype(np.float32),
+         "k_norm": rng.uniform(0.5, 1.5, cfg.layers * cfg.head_dim).astype(np.float32),
+         "out_norm": rng.uniform(0.5, 1.5, H).astype(np.float32)}
+    return w
+
+
+def small_olmoe_model(seed):
+    """OLMoE form: Q6_K attention with per-head QK-norm and half-split RoPE,
+    16/16-style equal head counts, Q2_K SwiGLU experts, untied output, no
+    Granite constants."""
+    rng = np.random.default_rng(seed)
+    cfg = oracle.MoeModelCfg(hidden=256, heads=4, kv_heads=4, head_dim=64, vocab=300, layers=2, context=16,
+                             n_experts=8, experts_used=3, expert_ff=256, rope_theta=1e4, eps=1e-5, embed_scale=0.0,
+                             residual_scale=0.0, logit_div=0.0, score_mul=0.125, dtype=Q6, expert_dtype=Q2,
+                             kv_f16=0, qk_norm=1, rope_neox=1, untied=1)
+    return cfg, _moe_weights(cfg, rng)
+
+
+def small_gemma_model(seed, kv_f16=0):
+    """Gemma-4 form: head_dim 256, local layers with a 4-position window and
+    global ones at a second RoPE base, a shared GeGLU FFN, fused Q5_K
+    gate|up experts and Q8_0 downs with per-expert scales, the scaled router
+    input, x sqrt(hidden) embeddings, logits soft-capped at 30."""
+    rng = np.random.default_rng(seed)
+    cfg = oracle.MoeModelCfg(hidden=512, heads=2, kv_heads=1, head_dim=256, vocab=300, layers=2, context=16,
+                             n_experts=8, experts_used=3, expert_ff=64, rope_theta=1e4, eps=1e-6,
+                             embed_scale=float(np.float32(np.sqrt(512.0))), residual_scale=0.0, logit_div=0.0,
+                             score_mul=1.0 / 16, dtype=Q6, expert_dtype=Q5, kv_f16=kv_f16, qk_norm=1, rope_neox=1,
+                             untied=0, gemma=1, expert_down_dtype=Q8, shared_ff=256, window=4, global_every=2,
+                             rope_theta_global=1e6, softcap=30.0)
+    return cfg, _moe_weights(cfg, rng)
+
+
+@pytest.mark.parametrize("form", ["olmoe", "gemma", "gemma_f16kv"])
+def test_moe_model_forms_match_float64_composition(form):
+    cfg, w = small_olmoe_model(83) if form == "olmoe" else small_gemma_model(84, kv_f16=int(form.endswith("kv")))
+    orc = oracle.MoeModelOracle(cfg, w, 1)
+    toks = [5, 17, 299, 0, 42, 7, 123, 5, 9]  # positions 0..8 pass the 4-position window
+    ref = npref.moe_model_f64(cfg, w, toks)
+    for t, want in zip(toks, ref):
+        got = orc.step([t])[0].astype(np.float64)
+        assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want)), (form, t)
+    if form.startswith("gemma"):
+        assert np.max(np.abs(ref[-1])) < 30.0  # the soft-cap bounds the logits
+
+
+def test_moe_model_batched_equals_alone():  # spm-batch/tests/batching.rs:128-145
+    for cfg, w in (small_olmoe_model(85), small_gemma_model(86)):
+        both, alone = oracle.MoeModelOracle(cfg, w, 2), oracle.MoeModelOracle(cfg, w, 1)
+        for a, b in [(3, 7), (11, 2), (5, 5), (1, 0), (2, 2), (9, 8)]:
+            assert np.array_equal(bits(both.step([a, b])[0]), bits(alone.step([a])[0]))
