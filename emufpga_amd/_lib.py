@@ -38,7 +38,7 @@ EMU_STYLE_QWEN3 = 0
 EMU_STYLE_SMOL = 1
 EMU_STYLE_GRANITE = 2
 (EMU_T_LAYER, EMU_T_EMBED, EMU_T_OUTPUT, EMU_T_ATTN_NORM, EMU_T_FFN_NORM, EMU_T_Q_NORM,
- EMU_T_K_NORM, EMU_T_OUT_NORM) = range(8)
+ EMU_T_K_NORM, EMU_T_OUT_NORM, EMU_T_FFN_NORM2) = range(9)
 
 
 class EmuError(RuntimeError):
@@ -132,6 +132,9 @@ class ModelConfig(C.Structure):
         ("qk_norm", C.c_int32), ("n_experts", C.c_uint32), ("experts_used", C.c_uint32),
         ("expert_ff", C.c_uint32), ("expert_encoding", C.c_int32), ("embed_scale", C.c_float),
         ("residual_scale", C.c_float), ("logit_div", C.c_float), ("score_mul", C.c_float),
+        ("rope_neox", C.c_int32), ("gemma", C.c_int32), ("expert_down_encoding", C.c_int32),
+        ("shared_ff", C.c_uint32), ("window", C.c_uint32), ("global_every", C.c_uint32),
+        ("rope_theta_global", C.c_float), ("logit_softcap", C.c_float),
     ]
 
 
@@ -186,6 +189,9 @@ SIGNATURES = {
     "emu_rope_table": [P, U32, U32, F, P],
     "emu_weights_lane_major": [P, I, P, SZ, P],
     "emu_model_sync": [P],
+    "emu_session_route_zipf": [P, F, C.c_uint64],
+    "emu_session_route_trace": [P, U32],
+    "emu_session_read_routes": [P, U32, P, P],
     "emu_model_tensor_lane_major": [P, I, U32, C.POINTER(P), C.POINTER(SZ)],
     "emu_rope_table_style": [P, I, U32, U32, F, P],
     "emu_rope": [P, P, U32, U32, U32, P, P, U32, I],

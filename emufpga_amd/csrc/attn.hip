@@ -60,6 +60,7 @@ struct AttnArgs {
     float *out;             // [client][heads * hd]
     uint8_t *xa;            // optional: the output as the multi-token matvec's A operands
     float *xs;              //           and their scales (token = client)
+    int window;             // attend to the last `window` positions only (0: all)
 };
 
 // A value of q|k|v: one plain load (MS false), or the sum of its ns <= 12
@@ -282,7 +283,11 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     const int pos = (int)a.positions[client];
     const int n = pos + 1;
     const int n_chunks = (n + kChunk - 1) / kChunk;
-    if (chunk >= n_chunks) return; // uniform per workgroup
+    // Positions lo..pos are attended: all of them, or the last `window`.
+    const int lo = a.window > 0 && n > a.window ? n - a.window : 0;
+    const int c_lo = lo / kChunk;
+    if (chunk >= n_chunks || chunk < c_lo) return; // uniform per workgroup
+    const int live_chunks = n_chunks - c_lo;
     const int GQ = a.heads / a.kv_heads;
 
     __shared__ float q_s[GQP][HD];
@@ -334,7 +339,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
 #pragma unroll
     for (int pp = 0; pp < kPP; ++pp) {
         const int p = pw + pp;
-        const int r = (p < n && p != pos) ? p : safe_row;
+        const int r = (p >= lo && p < n && p != pos) ? p : safe_row;
         kr[pp] = *reinterpret_cast<const vec_t *>(kc + (size_t)r * HD + lane * EPL);
         vr[pp] = *reinterpret_cast<const vec_t *>(vc + (size_t)r * HD + lane * EPL);
     }
@@ -407,7 +412,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
             const int pp = idx / GH, g = pass * GH + idx % GH;
             const int p = pw + pp;
             const float s = a.score_div > 0.0f ? dot / a.score_div : dot * a.score_mul;
-            sc[g][w * kPP + pp] = p < n ? s : -INFINITY;
+            sc[g][w * kPP + pp] = p < n && p >= lo ? s : -INFINITY;
         }
     }
     __syncthreads();
@@ -454,7 +459,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
         // the new position takes the appended value; stand-in rows past the
         // context are zeroed so that their zero weight cannot meet a NaN
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) vf[e] = p == pos ? vn[e] : (p >= n ? 0.0f : vf[e]);
+        for (int e = 0; e < EPL; ++e) vf[e] = p == pos ? vn[e] : (p >= n || p < lo ? 0.0f : vf[e]);
 #pragma unroll
         for (int g = 0; g < GQP; ++g)
 #pragma unroll
@@ -467,7 +472,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     __syncthreads();
 
     float *outp = a.out + (size_t)client * qw;
-    if (n_chunks == 1) {
+    if (live_chunks == 1) {
         for (int idx = tid; idx < GQ * HD; idx += kThreads) {
             const int g = idx / HD, d = idx % HD;
             const float o = (accs[0][g][d] + accs[1][g][d]) + (accs[2][g][d] + accs[3][g][d]);
@@ -499,7 +504,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     uint32_t *counter = a.counters + (size_t)client * a.kv_heads + kvh;
     if (tid == 0) arrived = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (arrived != (uint32_t)(n_chunks - 1)) return;
+    if (arrived != (uint32_t)(live_chunks - 1)) return;
     // Merge (last workgroup to arrive), MB chunks per batch.  The chunk
     // weights depend only on the head, so they are formed once: thread
     // t < GQ * MB owns (head t / MB, chunk t % MB) and the MB lanes of a head
@@ -530,7 +535,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
         pb[i] = a.partial + ((size_t)client * a.heads + kvh * GQ + head_of[i]) * a.max_chunks * PS;
         O[i] = 0.0f;
     }
-    for (int c0 = 0; c0 < n_chunks; c0 += MB) {
+    for (int c0 = c_lo; c0 < n_chunks; c0 += MB) {
         const int cp = c0 + pj < n_chunks ? c0 + pj : n_chunks - 1;
         const float mj = __hip_atomic_load(pm + (size_t)cp * PS + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const float lj = __hip_atomic_load(pm + (size_t)cp * PS + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -636,6 +641,7 @@ int emu_launch_attn(emu_ctx *ctx, const EmuAttnLaunch &l)
     a.qkv_slice_stride = l.qkv_slice_stride;
     a.xa = l.xa;
     a.xs = l.xs;
+    a.window = l.window > 0 ? l.window : 0;
     if (a.qkv_slices > kMaxSlices) return EMU_E_CONFIG;
     if (a.xa && (l.clients > 8 || (l.heads * l.head_dim) % 16 != 0)) return EMU_E_CONFIG;
     const dim3 grid(l.kv_heads * l.clients, a.max_chunks);

@@ -568,12 +568,42 @@ struct QmvArgs {
     float acc_scale;       // accumulate as y + v * acc_scale (0: y + v)
     float out_div;         // results divided by this before store and keys (0: none)
     int lane_major;        // w / w_up in the Q6_K lane-major layout (emu_lane_major_q6k)
+    int act;               // gate|up pair: EMU_ACT_SILU (SwiGLU) or EMU_ACT_GELU_TANH (GeGLU)
+    float softcap;         // results -> softcap * tanh(v / softcap) after out_div (0: none)
 };
 
 // A matvec result's epilogue: divided by out_div (when set), then added to
 // the residual as r + v * s with two roundings (the reference's add_scaled,
 // spm-granite-moe/src/math.rs:31-33), or r + v when s is 0.
 __device__ __forceinline__ float emu_out_div(float v, float d) { return d != 0.0f ? v / d : v; }
+// The output epilogue: divided by d (when set), then soft-capped as
+// cap * tanh(v / cap) (when cap is set).
+__device__ __forceinline__ float emu_out_epi(float v, float d, float cap)
+{
+    v = emu_out_div(v, d);
+    return cap != 0.0f ? cap * tanhf(v / cap) : v;
+}
+// gelu, tanh form (spm-granite-moe/src/gemma_smoke.rs:88-90), left to right,
+// no contraction.
+__device__ __forceinline__ float emu_gelu_tanh(float v)
+{
+#pragma clang fp contract(off)
+    float inner = 0.044715f * v;
+    inner = inner * v;
+    inner = 1.0f + inner;
+    float arg = 0.7978846f * v;
+    arg = arg * inner;
+    const float t = tanhf(arg);
+    const float half = 0.5f * v;
+    return half * (1.0f + t);
+}
+// A gate|up pair's activation: silu(g) * u (spm-ops/src/nonlinear.rs:5-7) or
+// gelu(g) * u (gemma_smoke.rs:111-120).
+__device__ __forceinline__ float emu_glu(float g, float u, int act)
+{
+#pragma clang fp contract(off)
+    return act == 1 ? emu_gelu_tanh(g) * u : (g / (1.0f + expf(-g))) * u;
+}
 __device__ __forceinline__ float emu_resid_add(float r, float v, float s)
 {
     return s != 0.0f ? r + __fmul_rn(v, s) : r + v;
@@ -654,6 +684,8 @@ struct EmuAttnLaunch {
     size_t qkv_slice_stride;
     uint8_t *xa;
     float *xs;
+    // Sliding window: attend to the last `window` positions only (0: all).
+    int window;
 };
 int emu_launch_attn(emu_ctx *ctx, const EmuAttnLaunch &l);
 // emu_moe_ffn whose weighted expert sum is added to the residual stream,

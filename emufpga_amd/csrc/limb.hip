@@ -155,8 +155,8 @@ struct LimbQ6KLM : LimbQ6K {
     }
 };
 
-template <int S> struct LimbShape {
-    static constexpr int W = S == 1 ? 8 : 4 * S; // wavefronts per workgroup
+template <int S, int WV = 0> struct LimbShape {
+    static constexpr int W = WV ? WV : S == 1 ? 8 : 4 * S; // wavefronts per workgroup
     static constexpr int RG = W / S;             // row-groups per workgroup
     static constexpr int T = EMU_WAVE * W;
     static constexpr int NSB = 256 * S;          // 16-column sub-blocks per row
@@ -223,10 +223,10 @@ __device__ __forceinline__ void make_limbs(const float (&xv)[CPT], LimbRec *rec,
     }
 }
 
-template <class LF, int S, int D, bool DUAL, bool NORM, bool ACC>
-__global__ __launch_bounds__(EMU_WAVE * LimbShape<S>::W) void qmv_limb_kernel(QmvArgs a, int rounds)
+template <class LF, int S, int D, bool DUAL, bool NORM, bool ACC, int WV>
+__global__ __launch_bounds__((EMU_WAVE * LimbShape<S, WV>::W)) void qmv_limb_kernel(QmvArgs a, int rounds)
 {
-    using SH = LimbShape<S>;
+    using SH = LimbShape<S, WV>;
     constexpr int NR = DUAL ? 2 : 1;
     __shared__ LimbRec rec[SH::NSB];
     __shared__ float red[SH::W];
@@ -303,8 +303,8 @@ __global__ __launch_bounds__(EMU_WAVE * LimbShape<S>::W) void qmv_limb_kernel(Qm
     uint64_t best = 0;
     auto finish = [&](int row, const float (&p)[NR], float resid) {
         float val = p[0];
-        if (DUAL) val = (val / (1.0f + expf(-val))) * p[1];
-        val = emu_out_div(val, a.out_div);
+        if (DUAL) val = emu_glu(val, p[1], a.act);
+        val = emu_out_epi(val, a.out_div, a.softcap);
         if (row < a.rows) {
             a.y[row] = ACC ? emu_resid_add(resid, val, a.acc_scale) : val;
             if (a.keys) {
@@ -364,15 +364,57 @@ template <int S, bool DUAL> struct LimbTune {
     static constexpr int PER_CU = DUAL ? 2 : 1;
 };
 
+// Sixteen wavefronts per workgroup (one workgroup per CU doing one
+// prologue) instead of eight, for S = 1: EMU_LIMB_W=16, a sweep override.
+bool limb_wide()
+{
+    static const bool w = [] {
+        const char *v = getenv("EMU_LIMB_W");
+        return v && atoi(v) == 16;
+    }();
+    return w;
+}
+
+template <class LF, int S, int D, bool DUAL, bool NORM, bool ACC>
+void launch_limb_d(emu_ctx *ctx, const QmvArgs &a, int blocks)
+{
+    if constexpr (S == 1) {
+        if (limb_wide()) {
+            using SH = LimbShape<S, 16>;
+            const int wb = (blocks + 1) / 2;
+            const int total_rg = wb * SH::RG;
+            const int rounds = (a.rows + total_rg * D - 1) / (total_rg * D);
+            hipLaunchKernelGGL((qmv_limb_kernel<LF, S, D, DUAL, NORM, ACC, 16>), dim3(wb), dim3(SH::T), 0,
+                               ctx->stream, a, rounds);
+            return;
+        }
+    }
+    using SH = LimbShape<S>;
+    const int total_rg = blocks * SH::RG;
+    const int rounds = (a.rows + total_rg * D - 1) / (total_rg * D);
+    hipLaunchKernelGGL((qmv_limb_kernel<LF, S, D, DUAL, NORM, ACC, 0>), dim3(blocks), dim3(SH::T), 0, ctx->stream,
+                       a, rounds);
+}
+
+// Rows in flight per wavefront: the tuned depth, or EMU_LIMB_D (1..3) for sweeps.
+int limb_depth_override()
+{
+    static const int d = [] {
+        const char *v = getenv("EMU_LIMB_D");
+        const int f = v ? atoi(v) : 0;
+        return f >= 1 && f <= 3 ? f : 0;
+    }();
+    return d;
+}
+
 template <class LF, int S, bool DUAL, bool NORM, bool ACC>
 void launch_limb_cfg(emu_ctx *ctx, const QmvArgs &a, int blocks)
 {
-    using SH = LimbShape<S>;
-    constexpr int D = LimbTune<S, DUAL>::D;
-    const int total_rg = blocks * SH::RG;
-    const int rounds = (a.rows + total_rg * D - 1) / (total_rg * D);
-    hipLaunchKernelGGL((qmv_limb_kernel<LF, S, D, DUAL, NORM, ACC>), dim3(blocks), dim3(SH::T), 0, ctx->stream,
-                       a, rounds);
+    switch (limb_depth_override() ? limb_depth_override() : LimbTune<S, DUAL>::D) {
+    case 1: launch_limb_d<LF, S, 1, DUAL, NORM, ACC>(ctx, a, blocks); break;
+    case 2: launch_limb_d<LF, S, 2, DUAL, NORM, ACC>(ctx, a, blocks); break;
+    default: launch_limb_d<LF, S, 3, DUAL, NORM, ACC>(ctx, a, blocks); break;
+    }
 }
 
 template <class LF, int S>
@@ -390,7 +432,9 @@ int launch_limb_s(emu_ctx *ctx, const QmvArgs &a, int *key_slots)
     // caller's key stride, which holds rows + 8).
     const int need = (a.rows + LimbShape<S>::RG - 1) / LimbShape<S>::RG;
     const int blocks = cus * per_cu < need ? cus * per_cu : need;
-    if (a.keys && blocks * LimbShape<S>::RG > a.key_stride) return EMU_E_CONFIG;
+    // key slots the launch writes: one per row-group of the grid it takes
+    const int slots = S == 1 && limb_wide() ? (blocks + 1) / 2 * LimbShape<1, 16>::RG : blocks * LimbShape<S>::RG;
+    if (a.keys && slots > a.key_stride) return EMU_E_CONFIG;
     if (dual) {
         if (norm) launch_limb_cfg<LF, S, true, true, false>(ctx, a, blocks);
         else launch_limb_cfg<LF, S, true, false, false>(ctx, a, blocks);
@@ -402,7 +446,7 @@ int launch_limb_s(emu_ctx *ctx, const QmvArgs &a, int *key_slots)
         else launch_limb_cfg<LF, S, false, false, false>(ctx, a, blocks);
     }
     EMU_LAUNCH_CHECK(ctx);
-    if (key_slots) *key_slots = blocks * LimbShape<S>::RG;
+    if (key_slots) *key_slots = slots;
     return EMU_OK;
 }
 

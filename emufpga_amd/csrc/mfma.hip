@@ -412,7 +412,8 @@ struct FinishArgs {
     int nks, nmat, rows;
     float *y; // n_tok x rows
     int accumulate;
-    float acc_scale, out_div;
+    float acc_scale, out_div, softcap;
+    int act;
     uint64_t *keys;
     int key_stride, tie_last;
 };
@@ -431,9 +432,9 @@ __global__ __launch_bounds__(kFinishThreads) void mfma_finish_kernel(FinishArgs 
             const float *pu = p + (size_t)kMaxTok * a.rows;
             float up = pu[0];
             for (int k = 1; k < a.nks; ++k) up += pu[k * stride];
-            v = (v / (1.0f + expf(-v))) * up;
+            v = emu_glu(v, up, a.act);
         }
-        v = emu_out_div(v, a.out_div);
+        v = emu_out_epi(v, a.out_div, a.softcap);
         float *dst = a.y + (size_t)t * a.rows + row;
         *dst = a.accumulate ? emu_resid_add(*dst, v, a.acc_scale) : v;
     }
@@ -610,6 +611,8 @@ int emu_mfma_finish(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int
     fa.accumulate = q.accumulate;
     fa.acc_scale = q.acc_scale;
     fa.out_div = q.out_div;
+    fa.softcap = q.softcap;
+    fa.act = q.act;
     fa.keys = q.keys;
     fa.key_stride = q.key_stride;
     fa.tie_last = q.tie_last;

@@ -52,6 +52,10 @@ struct emu_model {
     // Mixture-of-experts layers: router (f32) and gate/up/down experts,
     // expert-major (spm-granite-moe/src/weights.rs:57-73), after q, k, v, o.
     size_t off_r = 0, off_ge = 0, off_ue = 0, off_de = 0, rb_he = 0, rb_fe = 0;
+    // Gemma-4 form: router and down scales, the shared FFN (off_ge holds the
+    // fused gate|up experts), and the experts' input gains.
+    size_t off_rs = 0, off_ds = 0, off_sg = 0, off_su = 0, off_sd = 0, rb_sf = 0, off_ffn_norm2 = 0;
+    bool gemma() const { return moe() && cfg.gemma; }
     // Lane-major copy (emu_lane_major_q6k) of the Q6_K matrices the batch-1
     // limb matvec reads, at the same offsets as in `base` for the layers and
     // at off_embed for the output matrix (tied or not).  Rebuilt before the
@@ -84,6 +88,15 @@ struct emu_session {
     // mixture-of-experts scratch: normalised input, router logits, routes,
     // expert output, and the selected-expert FFN's workspace
     float *xn = nullptr, *rlog = nullptr, *rwts = nullptr;
+    // Gemma form: the router's input and the global layers' RoPE table
+    float *rin = nullptr, *rope2 = nullptr;
+    // Zipf routing for throughput runs and the device route trace
+    // ([capacity][layer][client][k] ids and weights, slot = step % capacity)
+    float zipf_s = 0.0f;
+    uint64_t zipf_seed = 0;
+    int32_t *trace_ids = nullptr;
+    float *trace_w = nullptr;
+    uint32_t trace_cap = 0;
     int32_t *rids = nullptr;
     void *moe_ws = nullptr;
     size_t moe_ws_bytes = 0;
@@ -110,6 +123,26 @@ __device__ __forceinline__ float gauss(uint64_t seed, uint64_t stream, uint64_t 
     const float u1 = (float)((h >> 40) + 1) * (1.0f / 16777216.0f); // (0, 1]
     const float u2 = (float)(h & 0xffffffu) * (1.0f / 16777216.0f); // [0, 1)
     return sd * sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+}
+
+// Zipf(s) routing for throughput runs: expert e (Zipf rank e + 1) gets the
+// logit -s * ln(e + 1) + G with G a Gumbel draw keyed by (seed, client,
+// position, layer, expert).  The top k of these are a sample without
+// replacement with probabilities proportional to (e + 1)^-s (Gumbel-top-k).
+struct ZipfRoute {
+    float s;           // 0: the model's own router
+    uint64_t seed;
+    const uint32_t *positions;
+    int layer;
+};
+
+__device__ __forceinline__ float zipf_logit(const ZipfRoute &z, int client, int e)
+{
+    const uint64_t key = ((uint64_t)(uint32_t)client << 48) ^ ((uint64_t)z.positions[client] << 24) ^
+                         ((uint64_t)(uint32_t)z.layer << 12) ^ (uint64_t)(uint32_t)e;
+    const uint64_t h = splitmix64(z.seed ^ splitmix64(key));
+    const float u = (float)((h >> 40) + 1) * (1.0f / 16777217.0f); // (0, 1)
+    return -z.s * logf((float)(e + 1)) - logf(-logf(u));
 }
 
 __device__ __forceinline__ uint16_t f2h(float x) { return __half_as_ushort(__float2half_rn(x)); }
@@ -287,7 +320,7 @@ __global__ __launch_bounds__(kThreads) void synth_f32_kernel(float *dst, size_t 
 // Router logits of every client (spm-granite-moe/src/moe.rs:132-138, an M1
 // matvec of the f32 router): one wavefront per (expert, client).
 __global__ __launch_bounds__(EMU_WAVE) void router_kernel(const float *w, const float *x, int width, int experts,
-                                                           float *logits)
+                                                           float *logits, ZipfRoute z)
 {
     const int e = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
     const float *row = w + (size_t)e * width;
@@ -302,7 +335,7 @@ __global__ __launch_bounds__(EMU_WAVE) void router_kernel(const float *w, const 
         acc = __builtin_fmaf(a.w, b.w, acc);
     }
     acc = wave_sum(acc);
-    if (lane == 0) logits[(size_t)c * experts + e] = acc;
+    if (lane == 0) logits[(size_t)c * experts + e] = z.s > 0.0f ? zipf_logit(z, c, e) : acc;
 }
 
 // Tokens per partial-sum block of the multi-token matvec ([slice][matrix]
@@ -320,7 +353,7 @@ template <int NK>
 __global__ __launch_bounds__(kThreads) void moe_gate_kernel(const float *state, const float *gain, const float *router,
                                                             int experts, int k, float eps, float *xn, int32_t *ids,
                                                             float *weights, float *state_out, const float *opart,
-                                                            int o_nks, float o_scale)
+                                                            int o_nks, float o_scale, ZipfRoute z)
 {
     constexpr int width = NK * 4 * EMU_WAVE;
     constexpr int EB = 32 / NK < 8 ? 32 / NK : 8; // experts per load batch
@@ -410,7 +443,25 @@ __global__ __launch_bounds__(kThreads) void moe_gate_kernel(const float *state, 
         }
     }
     __syncthreads();
+    if (z.s > 0.0f) { // throughput runs: Zipf routing in place of the router's logits
+        for (int e = tid; e < experts; e += kThreads) p[e] = zipf_logit(z, c, e);
+        __syncthreads();
+    }
     emu_route_token(p, sel, experts, k, ids + (size_t)c * k, weights + (size_t)c * k);
+}
+
+// Copy of one layer's routes into the session's route trace, slot
+// steps[c] % capacity (one thread per (client, slot)).
+__global__ void trace_routes_kernel(const int32_t *ids, const float *weights, int n, int k, int layer, int layers,
+                                    const uint32_t *steps, int capacity, int32_t *t_ids, float *t_w)
+{
+    const int i = threadIdx.x;
+    if (i >= n * k) return;
+    const int c = i / k, r = i % k;
+    const size_t slot = steps[c] % (uint32_t)capacity;
+    const size_t at = ((slot * layers + layer) * n + c) * k + r;
+    t_ids[at] = ids[i];
+    t_w[at] = weights[i];
 }
 
 // Embedding row of tokens[c]: a unit-per-thread decode of one row.
@@ -514,7 +565,12 @@ EmuAttnLaunch layer_attn(emu_session *s, uint32_t layer)
     if (m->moe()) { // spm-granite-moe/src/attention.rs:12-26, 40-46
         al.score_mul = c.score_mul != 0.0f ? c.score_mul : 1.0f / sqrtf((float)hd);
         al.score_div = 0.0f;
-        al.interleaved = 1;
+        al.interleaved = c.rope_neox ? 0 : 1;
+        if (m->gemma() && c.window) { // local layers: the last `window` positions, the local RoPE base
+            const bool global = (layer + 1) % c.global_every == 0;
+            al.window = global ? 0 : (int)c.window;
+            al.rope = global ? s->rope2 : s->rope;
+        }
     }
     al.heads = (int)c.heads;
     al.kv_heads = (int)c.kv_heads;
@@ -655,6 +711,29 @@ int run_chain(emu_session *s)
     return launch_finalize(s, slots);
 }
 
+// The Gemma form's inputs of the router and of the experts, one workgroup per
+// client, from the residual r: with q = 1/sqrt(sum r^2 / W + 1e-6),
+//   rin = (r * rscale) * (q / sqrt(W))   (gemma_smoke.rs:57-86)
+//   xe  = (r * q) * gain2                (math::rms_norm with pre_ffw_norm_2)
+__global__ __launch_bounds__(kThreads) void gemma_route_in_kernel(const float *state, const float *rscale,
+                                                                  const float *gain2, int width, float *rin,
+                                                                  float *xe)
+{
+    __shared__ float red[kThreads / EMU_WAVE];
+    const int c = blockIdx.x;
+    const float *x = state + (size_t)c * width;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < width; i += kThreads) ss = __builtin_fmaf(x[i], x[i], ss);
+    ss = emu_block_sum(ss, red);
+    const float q = 1.0f / sqrtf(ss / (float)width + 1e-6f);
+    const float qr = q / sqrtf((float)width);
+    for (int i = threadIdx.x; i < width; i += kThreads) {
+        const float v = x[i];
+        rin[(size_t)c * width + i] = __fmul_rn(__fmul_rn(v, rscale[i]), qr);
+        xe[(size_t)c * width + i] = __fmul_rn(__fmul_rn(v, q), gain2[i]);
+    }
+}
+
 // The layers, output matvec and selection of a mixture-of-experts step
 // (spm-granite-moe/src/model.rs:330-411): attention as in the dense step but
 // with adjacent-pair RoPE and score * score_mul, residual adds r + v * 0.22,
@@ -710,6 +789,7 @@ int run_moe(emu_session *s)
         const uint8_t *lw = m->base + m->off_layers + (size_t)layer * m->layer_bytes;
         const float *opart = nullptr;
         int o_nks = 0;
+        const ZipfRoute zr{s->zipf_s, s->zipf_seed, s->positions, (int)layer};
         if (chain) {
             EmuMfmaLink l{};
             l.mode = 0; // input: the residual, normalised, as operands
@@ -779,38 +859,79 @@ int run_moe(emu_session *s)
         o.acc_scale = c.residual_scale;
         if ((st = emu_launch_qmv(ctx, c.encoding, o, n)) != EMU_OK) return st;
         }
-        if (moe_gate_fits(m)) {
+        if (m->gemma()) {
+            // router and expert inputs from the residual before the shared FFN
+            const float *g2 = reinterpret_cast<const float *>(m->base + m->off_ffn_norm2) + (size_t)layer * H;
+            hipLaunchKernelGGL(gemma_route_in_kernel, dim3((unsigned)n), dim3(kThreads), 0, ctx->stream, s->state,
+                               reinterpret_cast<const float *>(lw + m->off_rs), g2, (int)H, s->rin, s->xn);
+            EMU_LAUNCH_CHECK(ctx);
+            hipLaunchKernelGGL(router_kernel, dim3(E, (unsigned)n), dim3(EMU_WAVE), 0, ctx->stream,
+                               reinterpret_cast<const float *>(lw + m->off_r), s->rin, (int)H, (int)E, s->rlog, zr);
+            EMU_LAUNCH_CHECK(ctx);
+            if ((st = emu_route(ctx, s->rlog, (uint32_t)n, E, K, s->rids, s->rwts)) != EMU_OK) return st;
+            if (c.shared_ff) {
+                QmvArgs g{};
+                g.w = lw + m->off_sg;
+                g.w_up = lw + m->off_su;
+                g.row_bytes = m->rb_h;
+                g.rows = (int)c.shared_ff;
+                g.cols = (int)H;
+                g.nb = (int)(H / be);
+                g.x = s->state;
+                g.gain = ffn_norm + (size_t)layer * H;
+                g.eps = c.eps;
+                g.y = s->act;
+                g.act = EMU_ACT_GELU_TANH;
+                if ((st = emu_launch_qmv(ctx, c.encoding, g, n)) != EMU_OK) return st;
+                QmvArgs d{};
+                d.w = lw + m->off_sd;
+                d.row_bytes = m->rb_sf;
+                d.rows = (int)H;
+                d.cols = (int)c.shared_ff;
+                d.nb = (int)(c.shared_ff / be);
+                d.x = s->act;
+                d.y = s->state;
+                d.accumulate = 1;
+                d.acc_scale = c.residual_scale;
+                if ((st = emu_launch_qmv(ctx, c.encoding, d, n)) != EMU_OK) return st;
+            }
+        } else if (moe_gate_fits(m)) {
             const float *gn = ffn_norm + (size_t)layer * H, *rt = reinterpret_cast<const float *>(lw + m->off_r);
             if (H == 1024)
                 hipLaunchKernelGGL(moe_gate_kernel<4>, dim3((unsigned)n), dim3(kThreads), 0, ctx->stream, s->state, gn,
                                    rt, (int)E, (int)K, c.eps, s->xn, s->rids, s->rwts, s->state, opart, o_nks,
-                                   c.residual_scale);
+                                   c.residual_scale, zr);
             else
                 hipLaunchKernelGGL(moe_gate_kernel<8>, dim3((unsigned)n), dim3(kThreads), 0, ctx->stream, s->state, gn,
                                    rt, (int)E, (int)K, c.eps, s->xn, s->rids, s->rwts, s->state, opart, o_nks,
-                                   c.residual_scale);
+                                   c.residual_scale, zr);
             EMU_LAUNCH_CHECK(ctx);
         } else {
             if ((st = emu_rms_norm(ctx, s->state, ffn_norm + (size_t)layer * H, (uint32_t)n, H, c.eps, s->xn)) !=
                 EMU_OK)
                 return st;
             hipLaunchKernelGGL(router_kernel, dim3(E, (unsigned)n), dim3(EMU_WAVE), 0, ctx->stream,
-                               reinterpret_cast<const float *>(lw + m->off_r), s->xn, (int)H, (int)E, s->rlog);
+                               reinterpret_cast<const float *>(lw + m->off_r), s->xn, (int)H, (int)E, s->rlog, zr);
             EMU_LAUNCH_CHECK(ctx);
             if ((st = emu_route(ctx, s->rlog, (uint32_t)n, E, K, s->rids, s->rwts)) != EMU_OK) return st;
         }
+        if (s->trace_cap) {
+            hipLaunchKernelGGL(trace_routes_kernel, dim3(1), dim3(64), 0, ctx->stream, s->rids, s->rwts, n, (int)K,
+                               (int)layer, (int)c.layers, s->steps, (int)s->trace_cap, s->trace_ids, s->trace_w);
+            EMU_LAUNCH_CHECK(ctx);
+        }
         emu_moe_desc d{};
         d.enc_gate_up = c.expert_encoding;
-        d.enc_down = c.expert_encoding;
+        d.enc_down = m->gemma() ? c.expert_down_encoding : c.expert_encoding;
         d.d_gate = lw + m->off_ge;
-        d.d_up = lw + m->off_ue;
+        d.d_up = m->gemma() ? nullptr : lw + m->off_ue; // gemma: fused gate|up rows per expert
         d.d_down = lw + m->off_de;
-        d.d_down_scale = nullptr;
+        d.d_down_scale = m->gemma() ? reinterpret_cast<const float *>(lw + m->off_ds) : nullptr;
         d.n_experts = E;
         d.width = H;
         d.ff = c.expert_ff;
         d.k = K;
-        d.act = EMU_ACT_SILU;
+        d.act = m->gemma() ? EMU_ACT_GELU_TANH : EMU_ACT_SILU;
         // the weighted expert sum lands on the residual stream as add_scaled does
         // chained: the next layer's link adds the expert sum (the last layer's
         // is combined here, for the output matvec)
@@ -820,7 +941,7 @@ int run_moe(emu_session *s)
             return st;
     }
     QmvArgs out{};
-    out.w = m->base + m->off_embed; // tied (model.rs:403-407)
+    out.w = m->base + (c.tied ? m->off_embed : m->off_output); // Granite: tied (model.rs:403-407)
     out.row_bytes = m->rb_h;
     out.rows = (int)c.vocab;
     out.cols = (int)H;
@@ -833,6 +954,7 @@ int run_moe(emu_session *s)
     out.key_stride = (int)s->key_stride;
     out.tie_last = 0; // top_k: ties to the lowest index (math.rs:35-40)
     out.out_div = c.logit_div;
+    out.softcap = c.logit_softcap;
     int slots = 0;
     if ((st = emu_launch_qmv(ctx, c.encoding, out, n, &slots)) != EMU_OK) return st;
     return launch_finalize(s, slots);
@@ -1047,8 +1169,10 @@ extern "C" int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_m
     // selected-expert FFN's limits), the router's rows float4-loadable, the
     // output tied to the embedding (model.rs:403-407).
     if (moe && (c.n_experts == 0 || c.experts_used == 0 || c.experts_used > c.n_experts || c.experts_used > 8 ||
-                c.n_experts > 64 || c.expert_ff == 0 || c.hidden % 4 != 0 || !c.tied))
+                c.n_experts > 256 || c.expert_ff == 0 || c.hidden % 8 != 0))
         return EMU_E_CONFIG;
+    if (!moe && (c.gemma || c.rope_neox)) return EMU_E_CONFIG;
+    if (c.gemma && c.window && c.global_every == 0) return EMU_E_CONFIG;
     if (c.heads % c.kv_heads != 0 || c.heads / c.kv_heads > 8) return EMU_E_CONFIG;
     if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256) return EMU_E_CONFIG;
     if (c.style != EMU_STYLE_QWEN3 && c.style != EMU_STYLE_SMOL && c.style != EMU_STYLE_GRANITE)
@@ -1063,7 +1187,9 @@ extern "C" int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_m
         (st = emu_row_bytes(c.encoding, QW, &m->rb_q)) != EMU_OK ||
         (!moe && (st = emu_row_bytes(c.encoding, c.ffn, &m->rb_f)) != EMU_OK) ||
         (moe && (st = emu_row_bytes(c.expert_encoding, c.hidden, &m->rb_he)) != EMU_OK) ||
-        (moe && (st = emu_row_bytes(c.expert_encoding, c.expert_ff, &m->rb_fe)) != EMU_OK)) {
+        (moe && (st = emu_row_bytes(c.gemma ? c.expert_down_encoding : c.expert_encoding, c.expert_ff, &m->rb_fe)) !=
+                    EMU_OK) ||
+        (c.gemma && c.shared_ff && (st = emu_row_bytes(c.encoding, c.shared_ff, &m->rb_sf)) != EMU_OK)) {
         delete m;
         return st == EMU_E_SHORT ? EMU_E_CONFIG : st;
     }
@@ -1071,7 +1197,20 @@ extern "C" int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_m
     m->off_k = m->off_q + (size_t)QW * m->rb_h;
     m->off_v = m->off_k + (size_t)KW * m->rb_h;
     m->off_o = m->off_v + (size_t)KW * m->rb_h;
-    if (moe) {
+    if (moe && c.gemma) {
+        // q k v o | router | router scale | down scales | shared gate, up,
+        // down | fused gate|up experts | down experts
+        m->off_r = align_up(m->off_o + (size_t)c.hidden * m->rb_q, 16);
+        m->off_rs = m->off_r + sizeof(float) * c.n_experts * c.hidden;
+        m->off_ds = align_up(m->off_rs + sizeof(float) * c.hidden, 16);
+        m->off_sg = align_up(m->off_ds + sizeof(float) * c.n_experts, 16);
+        m->off_su = m->off_sg + (size_t)c.shared_ff * m->rb_h;
+        m->off_sd = m->off_su + (size_t)c.shared_ff * m->rb_h;
+        m->off_ge = m->off_sd + (size_t)c.hidden * m->rb_sf;
+        m->off_ue = m->off_ge;
+        m->off_de = m->off_ge + (size_t)c.n_experts * 2 * c.expert_ff * m->rb_he;
+        m->layer_bytes = align_up(m->off_de + (size_t)c.n_experts * c.hidden * m->rb_fe, 16);
+    } else if (moe) {
         m->off_r = align_up(m->off_o + (size_t)c.hidden * m->rb_q, 16);
         m->off_ge = m->off_r + sizeof(float) * c.n_experts * c.hidden;
         m->off_ue = m->off_ge + (size_t)c.n_experts * c.expert_ff * m->rb_he;
@@ -1101,6 +1240,8 @@ extern "C" int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_m
     off = align_up(off + sizeof(float) * c.layers * c.head_dim, 256);
     m->off_out_norm = off;
     off = align_up(off + sizeof(float) * c.hidden, 256);
+    m->off_ffn_norm2 = off;
+    if (c.gemma) off = align_up(off + sizeof(float) * c.layers * c.hidden, 256);
     m->total = off;
     void *p = nullptr;
     if ((st = emu_malloc(ctx, m->total, &p)) != EMU_OK) {
@@ -1151,6 +1292,9 @@ extern "C" int emu_model_tensor(emu_model *m, int kind, uint32_t layer, void **d
     case EMU_T_Q_NORM: off = m->off_q_norm; len = sizeof(float) * c.layers * c.head_dim; break;
     case EMU_T_K_NORM: off = m->off_k_norm; len = sizeof(float) * c.layers * c.head_dim; break;
     case EMU_T_OUT_NORM: off = m->off_out_norm; len = sizeof(float) * c.hidden; break;
+    case EMU_T_FFN_NORM2:
+        if (!m->gemma()) return EMU_E_ARG;
+        off = m->off_ffn_norm2; len = sizeof(float) * c.layers * c.hidden; break;
     default: return EMU_E_ARG;
     }
     *d_ptr = m->base + off;
@@ -1202,6 +1346,36 @@ extern "C" int emu_model_synth(emu_model *m, uint64_t seed)
     int st;
     for (uint32_t l = 0; l < c.layers; ++l) {
         uint8_t *lw = m->base + m->off_layers + (size_t)l * m->layer_bytes;
+        if (m->gemma()) {
+            const size_t sz[4] = {(size_t)QW * m->rb_h, (size_t)KW * m->rb_h, (size_t)KW * m->rb_h,
+                                  (size_t)c.hidden * m->rb_q};
+            const size_t of[4] = {m->off_q, m->off_k, m->off_v, m->off_o};
+            for (int t = 0; t < 4; ++t)
+                if ((st = synth_tensor(ctx, c.encoding, lw + of[t], sz[t], seed, 16ull * (l + 1) + t)) != EMU_OK)
+                    return st;
+            const size_t nr = (size_t)c.n_experts * c.hidden;
+            hipLaunchKernelGGL(synth_f32_kernel, dim3((unsigned)((nr + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                               ctx->stream, reinterpret_cast<float *>(lw + m->off_r), nr, seed, 16ull * (l + 1) + 4,
+                               0.02f);
+            EMU_LAUNCH_CHECK(ctx);
+            // router and down scales: 1.0
+            hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((c.hidden + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                               ctx->stream, reinterpret_cast<float *>(lw + m->off_rs), (size_t)c.hidden, 1.0f);
+            hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((c.n_experts + kThreads - 1) / kThreads)), dim3(kThreads),
+                               0, ctx->stream, reinterpret_cast<float *>(lw + m->off_ds), (size_t)c.n_experts, 1.0f);
+            EMU_LAUNCH_CHECK(ctx);
+            const size_t ssz = (size_t)c.shared_ff * m->rb_h;
+            const size_t ge = (size_t)c.n_experts * 2 * c.expert_ff * m->rb_he, de = (size_t)c.n_experts * c.hidden * m->rb_fe;
+            if ((c.shared_ff &&
+                 ((st = synth_tensor(ctx, c.encoding, lw + m->off_sg, ssz, seed, 16ull * (l + 1) + 8)) != EMU_OK ||
+                  (st = synth_tensor(ctx, c.encoding, lw + m->off_su, ssz, seed, 16ull * (l + 1) + 9)) != EMU_OK ||
+                  (st = synth_tensor(ctx, c.encoding, lw + m->off_sd, (size_t)c.hidden * m->rb_sf, seed,
+                                     16ull * (l + 1) + 10)) != EMU_OK)) ||
+                (st = synth_tensor(ctx, c.expert_encoding, lw + m->off_ge, ge, seed, 16ull * (l + 1) + 5)) != EMU_OK ||
+                (st = synth_tensor(ctx, c.expert_down_encoding, lw + m->off_de, de, seed, 16ull * (l + 1) + 7)) != EMU_OK)
+                return st;
+            continue;
+        }
         if (m->moe()) {
             const size_t sz[6] = {(size_t)QW * m->rb_h, (size_t)KW * m->rb_h, (size_t)KW * m->rb_h,
                                   (size_t)c.hidden * m->rb_q, 0, 0};
@@ -1297,6 +1471,7 @@ Placement mk(const char *name, uint32_t dtype, std::initializer_list<uint64_t> d
 extern "C" int emu_model_load_gguf(emu_model *m, emu_gguf *g)
 {
     if (!m || !g) return EMU_E_ARG;
+    if (m->gemma()) return EMU_E_UNSUPPORTED; // the Gemma form's tensors are placed through emu_model_tensor
     m->lm_dirty = true;
     const emu_model_config &c = m->cfg;
     const uint32_t QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim;
@@ -1399,9 +1574,10 @@ extern "C" int emu_session_create(emu_model *m, uint32_t n_clients, uint32_t con
     alloc((void **)&s->state, sizeof(float) * n_clients * c.hidden);
     alloc((void **)&s->qkv, sizeof(float) * n_clients * (QW + 2 * KW));
     alloc((void **)&s->attn, sizeof(float) * n_clients * QW);
-    alloc((void **)&s->act, sizeof(float) * n_clients * (c.ffn ? c.ffn : 1));
+    alloc((void **)&s->act, sizeof(float) * n_clients * std::max(std::max(c.ffn, c.gemma ? c.shared_ff : 0u), 1u));
     if (m->moe()) {
         alloc((void **)&s->xn, sizeof(float) * n_clients * c.hidden);
+        if (m->gemma()) alloc((void **)&s->rin, sizeof(float) * n_clients * c.hidden);
         alloc((void **)&s->rlog, sizeof(float) * n_clients * c.n_experts);
         alloc((void **)&s->rids, sizeof(int32_t) * n_clients * c.experts_used);
         alloc((void **)&s->rwts, sizeof(float) * n_clients * c.experts_used);
@@ -1417,6 +1593,14 @@ extern "C" int emu_session_create(emu_model *m, uint32_t n_clients, uint32_t con
         std::vector<float> table;
         emu_build_rope_table(context, c.head_dim, c.rope_theta, c.style == EMU_STYLE_SMOL, table);
         st = emu_memcpy_htod(ctx, s->rope, table.data(), table.size() * sizeof(float));
+    }
+    if (m->gemma() && c.window) {
+        alloc((void **)&s->rope2, sizeof(float) * (size_t)context * c.head_dim);
+        if (st == EMU_OK) {
+            std::vector<float> table;
+            emu_build_rope_table(context, c.head_dim, c.rope_theta_global, 0, table);
+            st = emu_memcpy_htod(ctx, s->rope2, table.data(), table.size() * sizeof(float));
+        }
     }
     if (st == EMU_OK) st = emu_memset(ctx, s->counters, 0, sizeof(uint32_t) * n_clients * c.kv_heads);
     if (st == EMU_OK) {
@@ -1452,7 +1636,8 @@ extern "C" int emu_session_destroy(emu_session *s)
     if (s->graph) (void)hipGraphDestroy(s->graph);
     void *ptrs[] = {s->k_cache, s->v_cache, s->positions, s->tokens, s->steps, s->last, s->prompt, s->hist,
                     s->ctrl, s->counters, s->state, s->qkv, s->attn, s->act, s->logits, s->keys, s->partial,
-                    s->rope, s->xn, s->rlog, s->rids, s->rwts, s->moe_ws};
+                    s->rope, s->xn, s->rlog, s->rids, s->rwts, s->moe_ws, s->rin, s->rope2, s->trace_ids,
+                    s->trace_w};
     for (void *p : ptrs) emu_free(ctx, p);
     delete s;
     return EMU_OK;
@@ -1543,6 +1728,69 @@ extern "C" int emu_time_decode(emu_session *s, uint32_t steps, float *ms)
     if ((st = launch_steps(s, steps)) != EMU_OK) return st;
     if ((st = emu_event_record(ctx, 15)) != EMU_OK) return st;
     return emu_event_elapsed(ctx, 14, 15, ms);
+}
+
+namespace {
+// The captured step bakes in launch arguments: drop it so the next step
+// captures the new routing settings.
+void drop_graph(emu_session *s)
+{
+    if (s->exec) (void)hipGraphExecDestroy(s->exec);
+    if (s->graph) (void)hipGraphDestroy(s->graph);
+    s->exec = nullptr;
+    s->graph = nullptr;
+}
+} // namespace
+
+extern "C" int emu_session_route_zipf(emu_session *s, float zipf_s, uint64_t seed)
+{
+    if (!s || !(zipf_s >= 0.0f)) return EMU_E_ARG;
+    if (!s->m->moe()) return EMU_E_UNSUPPORTED;
+    s->zipf_s = zipf_s;
+    s->zipf_seed = seed;
+    drop_graph(s);
+    return EMU_OK;
+}
+
+extern "C" int emu_session_route_trace(emu_session *s, uint32_t capacity)
+{
+    if (!s) return EMU_E_ARG;
+    if (!s->m->moe()) return EMU_E_UNSUPPORTED;
+    emu_ctx *ctx = s->m->ctx;
+    const emu_model_config &c = s->m->cfg;
+    emu_free(ctx, s->trace_ids);
+    emu_free(ctx, s->trace_w);
+    s->trace_ids = nullptr;
+    s->trace_w = nullptr;
+    s->trace_cap = 0;
+    drop_graph(s);
+    if (capacity == 0) return EMU_OK;
+    const size_t n = (size_t)capacity * c.layers * s->n * c.experts_used;
+    int st = emu_malloc(ctx, sizeof(int32_t) * n, (void **)&s->trace_ids);
+    if (st == EMU_OK) st = emu_malloc(ctx, sizeof(float) * n, (void **)&s->trace_w);
+    if (st == EMU_OK) st = emu_memset(ctx, s->trace_ids, 0xff, sizeof(int32_t) * n); // -1: no step yet
+    if (st != EMU_OK) {
+        emu_free(ctx, s->trace_ids);
+        emu_free(ctx, s->trace_w);
+        s->trace_ids = nullptr;
+        s->trace_w = nullptr;
+        return st;
+    }
+    s->trace_cap = capacity;
+    return EMU_OK;
+}
+
+extern "C" int emu_session_read_routes(emu_session *s, uint32_t slot, int32_t *h_ids, float *h_weights)
+{
+    if (!s || !h_ids) return EMU_E_ARG;
+    if (!s->trace_cap) return EMU_E_UNSUPPORTED;
+    if (slot >= s->trace_cap) return EMU_E_ARG;
+    const emu_model_config &c = s->m->cfg;
+    const size_t per = (size_t)c.layers * s->n * c.experts_used;
+    int st = emu_memcpy_dtoh(s->m->ctx, h_ids, s->trace_ids + per * slot, sizeof(int32_t) * per);
+    if (st == EMU_OK && h_weights)
+        st = emu_memcpy_dtoh(s->m->ctx, h_weights, s->trace_w + per * slot, sizeof(float) * per);
+    return st;
 }
 
 extern "C" int emu_session_positions(emu_session *s, uint32_t *h_positions)

@@ -72,24 +72,10 @@ __device__ __forceinline__ int expert_slots(const MoeArgs &a, int e, int lane, i
     return cnt;
 }
 
-// gelu, tanh form (gemma_smoke.rs:88-90), left to right, no contraction.
-__device__ __forceinline__ float gelu_tanh(float v)
-{
-#pragma clang fp contract(off)
-    float inner = 0.044715f * v;
-    inner = inner * v;
-    inner = 1.0f + inner;
-    float arg = 0.7978846f * v;
-    arg = arg * inner;
-    const float t = tanhf(arg);
-    const float half = 0.5f * v;
-    return half * (1.0f + t);
-}
-
 template <int ACT> __device__ __forceinline__ float activate(float g, float u)
 {
 #pragma clang fp contract(off)
-    if (ACT == EMU_ACT_GELU_TANH) return gelu_tanh(g) * u;
+    if (ACT == EMU_ACT_GELU_TANH) return emu_gelu_tanh(g) * u;
     return (g / (1.0f + expf(-g))) * u; // moe.rs:46-56
 }
 

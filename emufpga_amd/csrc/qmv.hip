@@ -117,7 +117,7 @@ __global__ __launch_bounds__(kThreads) void qmv_kernel(QmvArgs a)
 #pragma unroll
         for (int k = 0; k < NR; ++k)
 #pragma unroll
-            for (int t = 0; t < NT; ++t) acc[k][t] = emu_out_div(acc[k][t], a.out_div);
+            for (int t = 0; t < NT; ++t) acc[k][t] = emu_out_epi(acc[k][t], a.out_div, a.softcap);
     }
 
     if (!DUAL && a.keys && lane == 0) {
@@ -142,12 +142,9 @@ __global__ __launch_bounds__(kThreads) void qmv_kernel(QmvArgs a)
         for (int t = 0; t < NT; ++t) {
             if (lane == k * NT + t && row < a.rows) {
                 float v = acc[k][t];
-                if (DUAL) {
-                    const float gte = v, up = acc[k + R][t];
-                    v = (gte / (1.0f + expf(-gte))) * up;
-                }
+                if (DUAL) v = emu_glu(v, acc[k + R][t], a.act);
                 float *dst = a.y + (size_t)t * a.rows + row;
-                if (DUAL) v = emu_out_div(v, a.out_div);
+                if (DUAL) v = emu_out_epi(v, a.out_div, a.softcap);
                 *dst = a.accumulate ? emu_resid_add(*dst, v, a.acc_scale) : v;
             }
         }
@@ -340,8 +337,8 @@ __global__ __launch_bounds__(kThreads) void qmv_pipe_kernel(QmvArgs a, int total
             for (int k = 0; k < R; ++k) {
                 const int row = rg * R + k;
                 float val = v[k];
-                if (DUAL) val = (val / (1.0f + expf(-val))) * v[k + R];
-                val = emu_out_div(val, a.out_div);
+                if (DUAL) val = emu_glu(val, v[k + R], a.act);
+                val = emu_out_epi(val, a.out_div, a.softcap);
                 if (row < a.rows) {
                     if (lane == k) a.y[row] = a.accumulate ? emu_resid_add(resid, val, a.acc_scale) : val;
                     if (a.keys) {

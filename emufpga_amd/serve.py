@@ -20,8 +20,8 @@ import numpy as np
 
 from . import _lib
 from ._lib import (EMU_STYLE_GRANITE, EMU_STYLE_QWEN3, EMU_STYLE_SMOL, EMU_T_ATTN_NORM, EMU_T_EMBED, EMU_T_FFN_NORM,
-                   EMU_T_K_NORM, EMU_T_LAYER, EMU_T_OUT_NORM, EMU_T_OUTPUT, EMU_T_Q_NORM, Q6_K, Q8_0,
-                   ModelConfig)
+                   EMU_T_FFN_NORM2, EMU_T_K_NORM, EMU_T_LAYER, EMU_T_OUT_NORM, EMU_T_OUTPUT, EMU_T_Q_NORM, Q6_K,
+                   Q8_0, ModelConfig)
 from .device import Context
 from .gguf import F32, MT_F32, MT_STR, MT_U32, GgufFile, row_bytes, write
 
@@ -50,13 +50,24 @@ class DenseConfig:
     residual_scale: float = 0.0
     logit_div: float = 0.0
     score_mul: float = 0.0
+    # OLMoE / Gemma-4 forms of the mixture-of-experts decoder (emu_model_config)
+    rope_neox: bool = False
+    gemma: bool = False
+    expert_down_encoding: int = 0
+    shared_ff: int = 0
+    window: int = 0
+    global_every: int = 0
+    rope_theta_global: float = 0.0
+    logit_softcap: float = 0.0
 
     def native(self) -> ModelConfig:
         return ModelConfig(self.hidden, self.heads, self.kv_heads, self.head_dim, self.ffn, self.vocab,
                            self.layers, self.rope_theta, self.eps, self.style, self.encoding,
                            int(self.tied), int(self.qk_norm), self.n_experts, self.experts_used, self.expert_ff,
                            self.expert_encoding, self.embed_scale, self.residual_scale, self.logit_div,
-                           self.score_mul)
+                           self.score_mul, int(self.rope_neox), int(self.gemma), self.expert_down_encoding,
+                           self.shared_ff, self.window, self.global_every, self.rope_theta_global,
+                           self.logit_softcap)
 
     @property
     def q_width(self) -> int:
@@ -78,6 +89,23 @@ GRANITE_MOE_Q6K = DenseConfig(1024, 16, 8, 64, 0, 49155, 24, 1.5e6, 1e-6, EMU_ST
                               n_experts=32, experts_used=8, expert_ff=512, expert_encoding=Q6_K, embed_scale=12.0,
                               residual_scale=0.22, logit_div=6.0, score_mul=0.015625)
 
+
+# OLMoE-1B-7B shape (spm-granite-moe/src/shape.rs:16-21: width 2048, FF 1024, 64 experts, top 8): 16 layers,
+# 16 heads of 128 (no GQA), per-head QK-norm, half-split RoPE at 1e4, Q6_K attention and untied 50304-row
+# output, Q2_K SwiGLU experts, f32 router, scores x 1/sqrt(128).
+OLMOE_1B_7B = DenseConfig(2048, 16, 16, 128, 0, 50304, 16, 1e4, 1e-5, EMU_STYLE_GRANITE, Q6_K, False, True,
+                          n_experts=64, experts_used=8, expert_ff=1024, expert_encoding=_lib.Q2_K,
+                          score_mul=float(np.float32(1.0 / np.sqrt(128.0))), rope_neox=True)
+# Gemma-4-style MoE shape (gemma_smoke.rs:13-20: width 2816, FF 704, 8 routed, Q5_K gate|up, Q8_0 down): 30
+# layers, 16 heads / 8 KV heads of 256, per-head QK-norm, five sliding-window (1024) layers to one global,
+# RoPE 1e4 local / 1e6 global, 128 experts plus a shared dense GeGLU FFN of 2048 (a size chosen here: the
+# workload leaves it open), Q6_K attention, shared FFN and tied 262144-row output, embeddings x sqrt(2816),
+# scores x 1/16, logits soft-capped at 30.
+GEMMA4_MOE = DenseConfig(2816, 16, 8, 256, 0, 262144, 30, 1e4, 1e-6, EMU_STYLE_GRANITE, Q6_K, True, True,
+                         n_experts=128, experts_used=8, expert_ff=704, expert_encoding=_lib.Q5_K,
+                         embed_scale=float(np.float32(np.sqrt(2816.0))), score_mul=1.0 / 16, rope_neox=True,
+                         gemma=True, expert_down_encoding=Q8_0, shared_ff=2048, window=1024, global_every=6,
+                         rope_theta_global=1e6, logit_softcap=30.0)
 
 _STYLES = {"qwen3": EMU_STYLE_QWEN3, "llama": EMU_STYLE_SMOL, "granitemoe": EMU_STYLE_GRANITE}
 
@@ -277,6 +305,8 @@ class Model:
             "out_norm": self.read_tensor(EMU_T_OUT_NORM, dtype=np.float32),
         }
         out["output"] = out["embed"] if c.tied else self.read_tensor(EMU_T_OUTPUT)
+        if c.gemma:
+            out["ffn_norm2"] = self.read_tensor(EMU_T_FFN_NORM2, dtype=np.float32)
         return out
 
 
@@ -333,6 +363,24 @@ class Session:
         self.ctx.check(self.ctx.lib.emu_time_decode(self.h, steps, C.byref(ms)), "emu_time_decode")
         return ms.value
 
+    def route_zipf(self, s: float, seed: int = 0) -> None:
+        """Zipf(s) routing for throughput runs (0: the model's own router)."""
+        self.ctx.check(self.ctx.lib.emu_session_route_zipf(self.h, float(s), int(seed)), "emu_session_route_zipf")
+
+    def route_trace(self, capacity: int) -> None:
+        """Record the routes of every step on the device (capacity steps)."""
+        self.ctx.check(self.ctx.lib.emu_session_route_trace(self.h, int(capacity)), "emu_session_route_trace")
+        self._trace_cap = int(capacity)
+
+    def read_routes(self, slot: int) -> tuple[np.ndarray, np.ndarray]:
+        """(ids, weights) of one trace slot: layers x clients x k."""
+        c = self.model.cfg
+        ids = np.empty((c.layers, self.n, c.experts_used), np.int32)
+        w = np.empty((c.layers, self.n, c.experts_used), np.float32)
+        self.ctx.check(self.ctx.lib.emu_session_read_routes(self.h, int(slot), ids.ctypes.data_as(C.c_void_p),
+                                                            w.ctypes.data_as(C.c_void_p)), "emu_session_read_routes")
+        return ids, w
+
     def positions(self) -> np.ndarray:
         out = np.empty(self.n, np.uint32)
         self.ctx.check(self.ctx.lib.emu_session_positions(self.h, out.ctypes.data_as(C.c_void_p)),
@@ -347,4 +395,5 @@ class Session:
         return out.reshape(positions, -1)
 
 
-__all__ = ["DenseConfig", "Model", "Session", "QWEN3_8B_Q6K", "SMOLLM2_135M_Q8", "GRANITE_MOE_Q6K", "_lib"]
+__all__ = ["DenseConfig", "Model", "Session", "QWEN3_8B_Q6K", "SMOLLM2_135M_Q8", "GRANITE_MOE_Q6K", "OLMOE_1B_7B",
+           "GEMMA4_MOE", "_lib"]

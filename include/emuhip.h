@@ -263,6 +263,28 @@ typedef struct emu_model_config {
     float residual_scale; /* residual adds r + v * this (model.rs:356, attention.rs:103-107: 0.22) */
     float logit_div;      /* logits / this before selection (model.rs:405-407: 6.0) */
     float score_mul;      /* attention score = dot * this (attention.rs:40-46: 0.015625) */
+    /* More mixture-of-experts forms (EMU_STYLE_GRANITE; zeros keep Granite's).
+       rope_neox: the half-split RoPE of spm-qwen3-slice/src/attention.rs:11-25
+       (the OLMoE-shaped decoder, which also takes tied = 0 for its separate
+       output matrix and qk_norm for per-head QK-norm).
+       gemma: the Gemma-4 FFN half.  No reference decoder exists for it (the
+       reference runs layer 0's experts, gemma_smoke.rs), so it is defined
+       here from those pieces: with r the residual after attention,
+         r0 = r; r += down_s(gelu(gate_s x) * up_s x), x = rms(r0) * ffn_norm
+             (a shared dense GeGLU FFN of shared_ff, in `encoding`; none if 0)
+         router input r0 * rscale * (1/sqrt(mean(r0^2) + 1e-6) / sqrt(hidden))
+             (gemma_smoke.rs:57-86), softmax, top_k, w = p / sum p (:333-351)
+         r += sum over routed experts, ascending id, of
+             w * dscale[e] * down_e(gelu(g) * u), [g; u] = gate_up_e(rms(r0) *
+             ffn_norm2) (fused gate|up rows in expert_encoding, downs in
+             expert_down_encoding; gemma_smoke.rs:92-139, pre_ffw_norm_2 :278);
+       layers attend to the last `window` positions (window 0: all) except
+       every global_every-th (l % global_every == global_every - 1), which
+       attend to all and take rope_theta_global; logits are soft-capped as
+       logit_softcap * tanh(l / logit_softcap) when logit_softcap != 0. */
+    int32_t rope_neox, gemma, expert_down_encoding;
+    uint32_t shared_ff, window, global_every;
+    float rope_theta_global, logit_softcap;
 } emu_model_config;
 
 /* Tensor kinds addressable inside a model. */
@@ -271,7 +293,8 @@ enum {
     EMU_T_EMBED = 1,    /* vocab x hidden */
     EMU_T_OUTPUT = 2,   /* vocab x hidden (absent when tied) */
     EMU_T_ATTN_NORM = 3, EMU_T_FFN_NORM = 4, EMU_T_Q_NORM = 5, EMU_T_K_NORM = 6,
-    EMU_T_OUT_NORM = 7  /* f32 gains */
+    EMU_T_OUT_NORM = 7, /* f32 gains */
+    EMU_T_FFN_NORM2 = 8 /* gemma: the experts' input gains [layer][hidden] (pre_ffw_norm_2) */
 };
 
 int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_model **out);
@@ -323,6 +346,21 @@ int emu_generate(emu_session *s, const uint32_t *h_prompt, uint32_t prompt_len, 
 /* Time `steps` greedy steps (after the caller's warmup) with events around the
  * region; ms receives the elapsed time. */
 int emu_time_decode(emu_session *s, uint32_t steps, float *ms);
+/* Routing for throughput runs of a mixture-of-experts model: with zipf_s > 0
+ * every (client, position, layer) routes by the logits -s*ln(e+1) + G_e
+ * (G_e Gumbel draws seeded by `seed`) in place of the router's, so its top k
+ * is a sample without replacement with P(e) proportional to (e+1)^-s; the
+ * router is still read.  zipf_s = 0 restores the model's own router.  No
+ * reference counterpart (the reference routes by its router only). */
+int emu_session_route_zipf(emu_session *s, float zipf_s, uint64_t seed);
+/* Record every step's routes on the device: [capacity][layer][client][k]
+ * expert ids and weights, a step going to slot (client's step count) %
+ * capacity; the RouteEvent data of spm-viz-trace/src/lib.rs:27-39.
+ * capacity 0 stops recording.  Mixture-of-experts models only. */
+int emu_session_route_trace(emu_session *s, uint32_t capacity);
+/* One slot of the route trace: layers x clients x k ids (-1 before any step
+ * wrote the slot) and, when h_weights is not NULL, their weights. */
+int emu_session_read_routes(emu_session *s, uint32_t slot, int32_t *h_ids, float *h_weights);
 /* Current position (tokens consumed) of every client. */
 int emu_session_positions(emu_session *s, uint32_t *h_positions);
 /* Copy a client's cached K or V rows for one layer (positions x kv_width f32). */

@@ -1,5 +1,6 @@
 """Mixture-of-experts decode step (spm-granite-moe/src/model.rs:330-411) on the
-GPU against the oracle's or_moe_model_step.
+GPU against the oracle's or_moe_model_step, in its Granite, OLMoE and
+Gemma-4 forms.
 
 Same bars as the dense decoder: logits within ||gpu - ref||_inf <= 1e-3 *
 ||ref||_inf per step and greedy tokens identical (ties to the lowest index,
@@ -13,7 +14,8 @@ import pytest
 
 import oracle
 from emufpga_amd import _lib
-from emufpga_amd.serve import GRANITE_MOE_Q6K, DenseConfig, Model, Session
+from emufpga_amd.gguf import row_bytes
+from emufpga_amd.serve import GEMMA4_MOE, GRANITE_MOE_Q6K, OLMOE_1B_7B, DenseConfig, Model, Session
 
 pytestmark = pytest.mark.gpu
 
@@ -33,7 +35,10 @@ def oracle_for(model: Model, context: int, kv_f16: bool, n_clients: int) -> orac
                              experts_used=c.experts_used, expert_ff=c.expert_ff, rope_theta=c.rope_theta, eps=c.eps,
                              embed_scale=c.embed_scale, residual_scale=c.residual_scale, logit_div=c.logit_div,
                              score_mul=c.score_mul, dtype=c.encoding, expert_dtype=c.expert_encoding,
-                             kv_f16=int(kv_f16), qk_norm=int(c.qk_norm))
+                             kv_f16=int(kv_f16), qk_norm=int(c.qk_norm), rope_neox=int(c.rope_neox),
+                             untied=int(not c.tied), gemma=int(c.gemma), expert_down_dtype=c.expert_down_encoding,
+                             shared_ff=c.shared_ff, window=c.window, global_every=c.global_every,
+                             rope_theta_global=c.rope_theta_global, softcap=c.logit_softcap)
     w = model.host_weights()
     assert w["layers"].size == c.layers * oracle.moe_layer_bytes(cfg)
     return oracle.MoeModelOracle(cfg, w, n_clients)
@@ -96,8 +101,169 @@ def test_granite_shape_decodes_and_matches_oracle(ctx, n_clients):
             assert int(nxt[c]) == oracle.argmax(r[c], False), (step, c)
 
 
-def test_moe_config_rejects_untied_and_oversized_routes(ctx):
-    with pytest.raises(_lib.EmuError):
-        Model(ctx, DenseConfig(**{**small_granite().__dict__, "tied": False}))
+def test_moe_config_rejects_unsupported_forms(ctx):
     with pytest.raises(_lib.EmuError):
         Model(ctx, DenseConfig(**{**small_granite().__dict__, "experts_used": 9, "n_experts": 16}))
+    with pytest.raises(_lib.EmuError):  # a sliding window needs the global-layer period
+        Model(ctx, DenseConfig(**{**small_gemma().__dict__, "global_every": 0}))
+    with pytest.raises(_lib.EmuError):  # the MoE forms are not dense-model options
+        Model(ctx, DenseConfig(**{**small_granite().__dict__, "style": _lib.EMU_STYLE_QWEN3, "ffn": 512,
+                                  "n_experts": 0, "experts_used": 0, "expert_ff": 0, "rope_neox": True}))
+
+
+# ---- the OLMoE form -------------------------------------------------------
+
+def small_olmoe():
+    return DenseConfig(hidden=256, heads=4, kv_heads=4, head_dim=64, ffn=0, vocab=300, layers=2, rope_theta=1e4,
+                       eps=1e-5, style=_lib.EMU_STYLE_GRANITE, encoding=_lib.Q6_K, tied=False, qk_norm=True,
+                       n_experts=8, experts_used=3, expert_ff=256, expert_encoding=_lib.Q2_K,
+                       score_mul=0.125, rope_neox=True)
+
+
+def run_against_oracle(ctx, cfg, n_clients, steps, context, seed, gains=None):
+    model = Model(ctx, cfg)
+    model.synth(seed)
+    if gains:
+        gains(model)
+    sess = Session(model, n_clients, context, kv_f16=True)
+    ref = oracle_for(model, context, True, n_clients)
+    rng = np.random.default_rng(seed)
+    worst = 0.0
+    oracle.set_threads(16)
+    try:
+        for step in range(steps):
+            toks = rng.integers(0, cfg.vocab, size=n_clients).astype(np.uint32)
+            nxt, logits = sess.decode_step(toks, want_logits=True)
+            r = ref.step(toks)
+            for c in range(n_clients):
+                worst = max(worst, rel_inf(logits[c], r[c]))
+                assert int(nxt[c]) == oracle.argmax(r[c], False), (step, c)
+    finally:
+        oracle.set_threads(1)
+    assert worst <= 1e-3, worst
+    sess.close()
+    model.close()
+    return worst
+
+
+def random_norm_gains(model):
+    """Gains away from 1.0, so a gain that is dropped or misplaced shows."""
+    c, rng = model.cfg, np.random.default_rng(3)
+    kinds = [(_lib.EMU_T_ATTN_NORM, c.layers * c.hidden), (_lib.EMU_T_FFN_NORM, c.layers * c.hidden),
+             (_lib.EMU_T_Q_NORM, c.layers * c.head_dim), (_lib.EMU_T_K_NORM, c.layers * c.head_dim),
+             (_lib.EMU_T_OUT_NORM, c.hidden)]
+    if c.gemma:
+        kinds.append((_lib.EMU_T_FFN_NORM2, c.layers * c.hidden))
+    for kind, n in kinds:
+        model.write_tensor(kind, rng.uniform(0.5, 1.5, n).astype(np.float32))
+
+
+@pytest.mark.parametrize("n_clients", [1, 3])
+def test_olmoe_form_matches_oracle(ctx, n_clients):
+    """Half-split RoPE, per-head QK-norm, equal query and KV heads, Q2_K
+    experts, an untied output, no Granite constants."""
+    run_against_oracle(ctx, small_olmoe(), n_clients, 70, 80, 31 + n_clients, random_norm_gains)
+
+
+@pytest.mark.parametrize("n_clients", [1, 8])
+def test_olmoe_shape_matches_oracle(ctx, n_clients):
+    """The OLMoE-1B-7B shape (16 layers cut to 2): width 2048, 16 heads of
+    128, 64 Q2_K experts of 1024 with 8 routed, 50304-row untied output;
+    eight clients take the chained matrix-core step."""
+    cfg = DenseConfig(**{**OLMOE_1B_7B.__dict__, "layers": 2})
+    run_against_oracle(ctx, cfg, n_clients, 5, 24, 41 + n_clients, random_norm_gains)
+
+
+# ---- the Gemma-4 form -----------------------------------------------------
+
+def small_gemma(window=70):
+    return DenseConfig(hidden=512, heads=2, kv_heads=1, head_dim=256, ffn=0, vocab=300, layers=2, rope_theta=1e4,
+                       eps=1e-6, style=_lib.EMU_STYLE_GRANITE, encoding=_lib.Q6_K, tied=True, qk_norm=True,
+                       n_experts=8, experts_used=3, expert_ff=64, expert_encoding=_lib.Q5_K,
+                       embed_scale=float(np.float32(np.sqrt(512.0))), score_mul=1.0 / 16, rope_neox=True, gemma=True,
+                       expert_down_encoding=_lib.Q8_0, shared_ff=256, window=window, global_every=2,
+                       rope_theta_global=1e6, logit_softcap=30.0)
+
+
+def gemma_layer_scales(model):
+    """Random router and down scales written into each layer (the layer
+    layout of emu_model_config's gemma form), and random gains."""
+    random_norm_gains(model)
+    c, rng = model.cfg, np.random.default_rng(4)
+    rb = lambda enc, cols: row_bytes(enc, cols)  # noqa: E731
+    QW, KW = c.heads * c.head_dim, c.kv_heads * c.head_dim
+    off_r = -(-((QW + 2 * KW) * rb(c.encoding, c.hidden) + c.hidden * rb(c.encoding, QW)) // 16) * 16
+    off_rs = off_r + 4 * c.n_experts * c.hidden
+    off_ds = -(-(off_rs + 4 * c.hidden) // 16) * 16
+    for layer in range(c.layers):
+        blob = model.read_tensor(_lib.EMU_T_LAYER, layer)
+        blob[off_rs:off_rs + 4 * c.hidden] = rng.uniform(0.5, 1.5, c.hidden).astype(np.float32).view(np.uint8)
+        blob[off_ds:off_ds + 4 * c.n_experts] = rng.uniform(0.5, 2.0, c.n_experts).astype(np.float32).view(np.uint8)
+        model.write_tensor(_lib.EMU_T_LAYER, blob, layer)
+
+
+@pytest.mark.parametrize("n_clients", [1, 3])
+def test_gemma_form_matches_oracle(ctx, n_clients):
+    """head_dim 256; the local layer attends to the last 70 positions (its
+    first live chunk moves past chunk 0 after position 127), the global one
+    to all at its own RoPE base; the shared GeGLU FFN; fused Q5_K gate|up
+    experts with Q8_0 downs and per-expert scales; the scaled router input;
+    x sqrt(512) embeddings; logits soft-capped at 30."""
+    run_against_oracle(ctx, small_gemma(), n_clients, 140, 150, 51 + n_clients, gemma_layer_scales)
+
+
+def test_gemma_shape_matches_oracle(ctx):
+    """The Gemma-4-style shape (30 layers cut to 2): width 2816, 16 heads /
+    8 KV heads of 256, 128 experts of 704 with 8 routed, a shared FFN of
+    2048, the tied 262144-row output soft-capped at 30; two clients."""
+    cfg = DenseConfig(**{**GEMMA4_MOE.__dict__, "layers": 2})
+    run_against_oracle(ctx, cfg, 2, 4, 16, 61, gemma_layer_scales)
+
+
+# ---- Zipf routing for throughput runs, and the device route trace -----------
+
+def zipf_inclusion(E, k, s, draws, rng):
+    """Monte Carlo inclusion probability of each expert in a Gumbel-top-k
+    sample with P(e) proportional to (e + 1)^-s."""
+    logits = -s * np.log(np.arange(1, E + 1))
+    g = rng.gumbel(size=(draws, E))
+    top = np.argsort(-(logits + g), axis=1)[:, :k]
+    return np.bincount(top.reshape(-1), minlength=E) / draws
+
+
+def test_zipf_routing_and_route_trace(ctx):
+    cfg = small_granite(experts=32, used=8)
+    model = Model(ctx, cfg)
+    model.synth(91)
+    n, steps, cap = 4, 48, 64
+    prompts = np.arange(n * 4, dtype=np.uint32).reshape(n, 4)
+
+    def run(s, seed):
+        sess = Session(model, n, 128)
+        sess.route_trace(cap)
+        sess.route_zipf(s, seed)
+        sess.generate(prompts, steps)
+        slots = [sess.read_routes(i) for i in range(4 + steps - 1)]
+        sess.close()
+        return slots
+
+    traced = run(1.1, 7)
+    ids = np.stack([t[0] for t in traced])       # steps x layers x clients x k
+    w = np.stack([t[1] for t in traced])
+    assert ids.min() >= 0 and ids.max() < 32
+    assert all(len(set(row)) == 8 for row in ids.reshape(-1, 8).tolist())  # distinct experts per token
+    assert np.allclose(w.sum(-1), 1.0, atol=1e-5) and np.all(np.diff(w, axis=-1) <= 0)  # rank order
+    freq = np.bincount(ids.reshape(-1), minlength=32) / ids.reshape(-1, 8).shape[0]
+    want = zipf_inclusion(32, 8, 1.1, 20000, np.random.default_rng(0))
+    assert np.max(np.abs(freq - want)) < 0.15, (freq, want)
+    assert freq[0] > 0.8 and freq[31] < 0.35
+    # the same seed routes the same way; another seed does not
+    again = np.stack([t[0] for t in run(1.1, 7)])
+    assert np.array_equal(again, ids)
+    other = np.stack([t[0] for t in run(1.1, 8)])
+    assert not np.array_equal(other, ids)
+    # back on the model's own router: routes are the router's (distinct, weights summing to one)
+    own = run(0.0, 0)
+    oi = np.stack([t[0] for t in own])
+    assert all(len(set(row)) == 8 for row in oi.reshape(-1, 8).tolist())
+    model.close()
