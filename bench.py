@@ -37,8 +37,8 @@ sys.path.insert(0, ROOT)
 from emufpga_amd import _lib  # noqa: E402
 from emufpga_amd.device import Context  # noqa: E402
 from emufpga_amd.gguf import GgufFile, row_bytes  # noqa: E402
-from emufpga_amd.serve import (GRANITE_MOE_Q6K, QWEN3_8B_Q6K, SMOLLM2_135M_Q8, DenseConfig, Model,  # noqa: E402
-                               Session)
+from emufpga_amd.serve import (GEMMA4_MOE, GRANITE_MOE_Q6K, OLMOE_1B_7B, QWEN3_8B_Q6K, SMOLLM2_135M_Q8,  # noqa: E402
+                               DenseConfig, Model, Session)
 
 METRIC = "decode tok/s at batch 1 and 8; achieved HBM GB/s vs 8 TB/s peak"
 HBM_PEAK_GBS = 8000.0
@@ -227,31 +227,136 @@ def smol_leg(ctx, rng, with_cpu: bool) -> dict:
     return out
 
 
-def moe_leg(ctx, rng) -> dict:
-    """Granite-shaped MoE decode, 4 clients, 256-token prompts, 128 timed steps.
-    The routing is the model's own router on seeded synthetic weights (close to
-    uniform: about 21 distinct experts per layer for 4 x 8 routes, against
-    about 18 under the Zipf(1.1) injection the MoE workload describes)."""
-    cfg = GRANITE_MOE_Q6K
+def moe_layer_bytes(cfg, experts: float) -> float:
+    """Algorithmic weight bytes one MoE layer reads in a step that routes to
+    `experts` distinct experts: q|k|v and o, the f32 router, the Gemma form's
+    scales and shared FFN, and the routed experts' gate, up and down rows."""
+    H, QW, KW = cfg.hidden, cfg.q_width, cfg.kv_width
+    attn = (QW + 2 * KW) * row_bytes(cfg.encoding, H) + H * row_bytes(cfg.encoding, QW)
+    router = 4 * cfg.n_experts * H
+    down_enc = cfg.expert_down_encoding if cfg.gemma else cfg.expert_encoding
+    per_expert = 2 * cfg.expert_ff * row_bytes(cfg.expert_encoding, H) + H * row_bytes(down_enc, cfg.expert_ff)
+    extra = 0
+    if cfg.gemma:
+        extra = 4 * (H + cfg.n_experts)
+        if cfg.shared_ff:
+            extra += 2 * cfg.shared_ff * row_bytes(cfg.encoding, H) + H * row_bytes(cfg.encoding, cfg.shared_ff)
+    return attn + router + extra + experts * per_expert
+
+
+def moe_cpu_baseline(model: Model, budget_layers: int = 2) -> dict:
+    """One batch-1 token through the oracle's MoE decoder (single-threaded C
+    restatement of the reference CPU path): 1 and 2 layers + the output
+    timed, the per-layer cost extrapolated to the whole model."""
+    import oracle
+
+    c = model.cfg
+    w = {"layers": np.concatenate([model.read_tensor(_lib.EMU_T_LAYER, l) for l in range(budget_layers)]),
+         "embed": model.read_tensor(_lib.EMU_T_EMBED),
+         "attn_norm": model.read_tensor(_lib.EMU_T_ATTN_NORM, dtype=np.float32),
+         "ffn_norm": model.read_tensor(_lib.EMU_T_FFN_NORM, dtype=np.float32),
+         "q_norm": model.read_tensor(_lib.EMU_T_Q_NORM, dtype=np.float32),
+         "k_norm": model.read_tensor(_lib.EMU_T_K_NORM, dtype=np.float32),
+         "out_norm": model.read_tensor(_lib.EMU_T_OUT_NORM, dtype=np.float32)}
+    if not c.tied:
+        w["output"] = model.read_tensor(_lib.EMU_T_OUTPUT)
+    if c.gemma:
+        w["ffn_norm2"] = model.read_tensor(_lib.EMU_T_FFN_NORM2, dtype=np.float32)
+    ocfg = oracle.MoeModelCfg(hidden=c.hidden, heads=c.heads, kv_heads=c.kv_heads, head_dim=c.head_dim,
+                              vocab=c.vocab, layers=c.layers, context=4, n_experts=c.n_experts,
+                              experts_used=c.experts_used, expert_ff=c.expert_ff, rope_theta=c.rope_theta,
+                              eps=c.eps, embed_scale=c.embed_scale, residual_scale=c.residual_scale,
+                              logit_div=c.logit_div, score_mul=c.score_mul, dtype=c.encoding,
+                              expert_dtype=c.expert_encoding, kv_f16=1, qk_norm=int(c.qk_norm),
+                              rope_neox=int(c.rope_neox), untied=int(not c.tied), gemma=int(c.gemma),
+                              expert_down_dtype=c.expert_down_encoding, shared_ff=c.shared_ff, window=c.window,
+                              global_every=c.global_every, rope_theta_global=c.rope_theta_global,
+                              softcap=c.logit_softcap)
+    oracle.set_threads(1)
+
+    def timed(limit):
+        orc = oracle.MoeModelOracle(ocfg, w, 1)
+        t0 = time.perf_counter()
+        orc.step([17], layers_limit=limit)
+        return time.perf_counter() - t0
+
+    t1, t2 = timed(1), timed(2)
+    per_layer = max(t2 - t1, 0.0)
+    full = t1 + (c.layers - 1) * per_layer
+    log(f"cpu oracle ({c.layers}-layer MoE): 1 layer + output {t1:.2f} s, 2 layers {t2:.2f} s -> {full:.2f} s/token")
+    return {"value": round(1.0 / full, 5), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": (f"one batch-1 token at position 0 on the single-threaded C restatement of the reference "
+                       f"CPU path with the model's own router: 1 and 2 layers + the output timed "
+                       f"({t1:.2f} s, {t2:.2f} s), per-layer cost extrapolated to {c.layers} layers")}
+
+
+def moe_leg(ctx, rng, name: str, cfg, n_clients: int, prompt_len: int, steps: int, zipf_s: float,
+            with_cpu: bool, seed: int) -> dict:
+    """A mixture-of-experts decoder: n_clients concurrent sequences after
+    prompt_len-token prompts, `steps` timed greedy steps with Zipf(zipf_s)
+    routing (the workload's skew; the router is still read), the number of
+    distinct experts per layer measured from the device route trace of a
+    further untimed stretch, and the step's algorithmic HBM rate from it."""
     model = Model(ctx, cfg)
-    model.synth(20260202)
-    sess = Session(model, 4, 1024, kv_f16=True)
-    prompt = rng.integers(0, cfg.vocab, size=(4, 256)).astype(np.uint32)
+    t0 = time.perf_counter()
+    model.synth(seed)
+    ctx.sync()
+    log(f"{name}: synthesised in {time.perf_counter() - t0:.1f} s")
+    sess = Session(model, n_clients, prompt_len + steps + 64 + 16, kv_f16=True)
+    sess.route_zipf(zipf_s, seed)
+    prompt = rng.integers(0, cfg.vocab, size=(n_clients, prompt_len)).astype(np.uint32)
+    t0 = time.perf_counter()
     sess.generate(prompt, 1 + 8)
     ctx.sync()
-    steps = 128
+    log(f"{name}: {prompt_len}-token prompts + 8 warmup steps in {time.perf_counter() - t0:.1f} s")
     ms = sess.time_decode(steps)
     ctx.sync()
     pos = int(sess.positions()[0])
-    tok_s = 4 * steps / (ms / 1e3)
-    log(f"granite MoE batch 4: {steps} steps in {ms:.2f} ms -> {tok_s:.1f} tok/s (context {pos - steps}..{pos})")
+    # distinct experts per (step, layer), from the routes of 32 further steps
+    trace_steps = 32
+    sess.route_trace(trace_steps)
+    sess.time_decode(trace_steps)
+    ctx.sync()
+    us = []
+    for slot in range(trace_steps):
+        ids, _ = sess.read_routes(slot)
+        us += [len(set(ids[layer].reshape(-1).tolist())) for layer in range(cfg.layers)]
+    mean_u = float(np.mean(us))
     sess.close()
+    tok_s = n_clients * steps / (ms / 1e3)
+    ctx_mid = pos - steps // 2
+    kv_ctx = [min(ctx_mid, cfg.window) if cfg.gemma and cfg.window and (l + 1) % cfg.global_every else ctx_mid
+              for l in range(cfg.layers)]
+    kv_bytes = n_clients * sum(2 * cfg.kv_width * 2 * k for k in kv_ctx)
+    step_bytes = cfg.layers * moe_layer_bytes(cfg, mean_u) + cfg.vocab * row_bytes(cfg.encoding, cfg.hidden) + kv_bytes
+    gbs = step_bytes / (ms / steps / 1e3) / 1e9
+    log(f"{name}: {steps} steps in {ms:.2f} ms -> {tok_s:.1f} tok/s, {mean_u:.1f} distinct experts per layer, "
+        f"{step_bytes / 1e9:.3f} GB/step -> {gbs:.0f} GB/s (context {pos - steps}..{pos})")
+    out = {"value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": round(ms / steps, 4), "clients": n_clients,
+           "context_at_timing": [pos - steps, pos], "routing": f"Zipf(s={zipf_s}) Gumbel-top-k, seed {seed}",
+           "distinct_experts_per_layer": round(mean_u, 2), "algorithmic_bytes_per_step": int(step_bytes),
+           "step_hbm_gbs": round(gbs, 1), "step_hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    if with_cpu:
+        out["cpu_baseline"] = moe_cpu_baseline(model)
     model.close()
-    return {"value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": round(ms / steps, 4),
-            "context_at_timing": [pos - steps, pos], "clients": 4,
-            "workload": ("Granite-shaped MoE decoder (24 layers, width 1024, 32 Q6_K SwiGLU experts of 512, "
-                         "8 routed, tied 49155-row output), seeded synthetic weights, 256-token prompts, "
-                         "routing by the model's own router")}
+    return out
+
+
+def decode_256(ctx, model: Model, rng, batch: int, prompt: int, context: int) -> dict:
+    """The workload's full decode: a `prompt`-token prompt, then 256 timed
+    greedy steps (context prompt -> prompt + 256)."""
+    sess = Session(model, batch, context, kv_f16=True)
+    toks = rng.integers(0, model.cfg.vocab, size=(batch, prompt)).astype(np.uint32)
+    sess.generate(toks, 1)
+    ctx.sync()
+    ms = sess.time_decode(256)
+    ctx.sync()
+    pos = int(sess.positions()[0])
+    sess.close()
+    tok_s = batch * 256 / (ms / 1e3)
+    log(f"batch {batch}: 256 steps from context {pos - 256} to {pos} in {ms:.1f} ms -> {tok_s:.1f} tok/s")
+    return {"value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": round(ms / 256, 4),
+            "context_at_timing": [pos - 256, pos]}
 
 
 def main() -> int:
@@ -266,6 +371,9 @@ def main() -> int:
     ap.add_argument("--no-moe", action="store_true", help="skip the Granite MoE decode leg")
     ap.add_argument("--no-load", action="store_true", help="skip the GGUF -> HBM load leg")
     ap.add_argument("--no-smol", action="store_true", help="skip the SmolLM2 decode leg")
+    ap.add_argument("--no-gemma", action="store_true", help="skip the Gemma-4-style MoE leg")
+    ap.add_argument("--moe-prompt", type=int, default=0,
+                    help="prompt length of the OLMoE / Gemma legs (default: the workloads' 1024 / 2048)")
     ap.add_argument("--batch8-only", action="store_true",
                     help="only the 8-client decode, logged without the JSON line; for profiling")
     ap.add_argument("--moe-only", action="store_true",
@@ -285,7 +393,8 @@ def main() -> int:
     cus, arch = ctx.device_info()
     log(f"device: {arch}, {cus} CUs")
     if args.moe_only:
-        log(json.dumps(moe_leg(ctx, np.random.default_rng(43))))
+        log(json.dumps(moe_leg(ctx, np.random.default_rng(43), "granite", GRANITE_MOE_Q6K, 4, 256, 128, 1.1,
+                               False, 20260202)))
         ctx.close()
         return 0
     t0 = time.perf_counter()
@@ -384,8 +493,29 @@ def main() -> int:
                          "matvec": "int8 MFMA (v_mfma_i32_32x32x16_i8), activation limbs as the A operand"}
     if not args.no_smol:
         out["smollm2_b1"] = smol_leg(ctx, rng, not args.no_cpu)
+    out["decode_256_steps_b1"] = decode_256(ctx, model, rng, 1, args.prompt, args.context)
+    if not args.no_batch8:
+        out["decode_256_steps_b8"] = decode_256(ctx, model, rng, 8, args.prompt, args.context)
     if not args.no_moe:
-        out["moe_granite_b4"] = moe_leg(ctx, rng)
+        wl = "seeded synthetic weights; routing Zipf(s) injected (Gumbel-top-k), the router still read"
+        leg = moe_leg(ctx, rng, "granite", GRANITE_MOE_Q6K, 4, 256, 128, 1.1, not args.no_cpu, 20260202)
+        leg["workload"] = ("Granite-shaped MoE decoder (24 layers, width 1024, 16/8 heads of 64, 32 Q6_K SwiGLU "
+                           "experts of 512, 8 routed, tied 49155-row output), 4 clients, 256-token prompts; " + wl)
+        out["moe_granite_b4"] = leg
+        leg = moe_leg(ctx, rng, "olmoe", OLMOE_1B_7B, 8, args.moe_prompt or 1024, args.steps, 1.0,
+                      not args.no_cpu, 20260303)
+        leg["workload"] = ("OLMoE-1B-7B-shaped decoder (16 layers, width 2048, 16 heads of 128 with QK-norm, "
+                           "Q6_K attention and untied 50304-row output, 64 Q2_K SwiGLU experts of 1024, 8 "
+                           "routed), 8 clients; " + wl)
+        out["moe_olmoe_b8"] = leg
+        if not args.no_gemma:
+            leg = moe_leg(ctx, rng, "gemma", GEMMA4_MOE, 8, args.moe_prompt or 2048, args.steps, 1.2,
+                          not args.no_cpu, 20260404)
+            leg["workload"] = ("Gemma-4-style MoE decoder (30 layers, width 2816, 16/8 heads of 256 with QK-norm, "
+                               "5 sliding-window (1024) : 1 global layers, 128 Q5_K GeGLU experts of 704 with Q8_0 "
+                               "downs and per-expert scales, 8 routed, shared GeGLU FFN of 2048, Q6_K attention "
+                               "and tied 262144-row output soft-capped at 30), 8 clients; " + wl)
+            out["moe_gemma_b8"] = leg
     if not args.no_load:
         out["gguf_load"] = load_leg(ctx)
     if not args.no_cpu:

@@ -196,6 +196,7 @@ SIGNATURES = {
     "emu_rope_table_style": [P, I, U32, U32, F, P],
     "emu_rope": [P, P, U32, U32, U32, P, P, U32, I],
     "emu_attend_cached": [P, P, P, P, I, U32, U32, U32, U32, F, P],
+    "emu_attend_cached_noalloc": [P, P, P, P, I, U32, U32, U32, U32, F, P],
     "emu_route": [P, P, U32, U32, U32, P, P],
     "emu_argmax": [P, P, U32, U32, I, P],
     "emu_moe_workspace_bytes": [U32, U32, U32, U32],

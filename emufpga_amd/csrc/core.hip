@@ -69,6 +69,10 @@ extern "C" int emu_ctx_create(int device, emu_ctx **out)
         ctx->cus = prop.multiProcessorCount;
         snprintf(ctx->arch, sizeof ctx->arch, "%s", prop.gcnArchName);
     }
+    if (emu_ops_device_init(ctx) != EMU_OK) {
+        emu_ctx_destroy(ctx);
+        return EMU_E_HIP;
+    }
     *out = ctx;
     return EMU_OK;
 }

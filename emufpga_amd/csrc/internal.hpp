@@ -33,6 +33,10 @@ struct emu_ctx {
     size_t stage_bytes = 0;
 };
 
+// Per-device set-up of ops.hip's no-allocation scratch (the device address of
+// its file-scope array on the context's device); called by emu_ctx_create.
+int emu_ops_device_init(emu_ctx *ctx);
+
 int emu_hip_fail(emu_ctx *ctx, hipError_t e, const char *what);
 
 #define EMU_HIP(ctx, call)                                                   \

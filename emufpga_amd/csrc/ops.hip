@@ -4,6 +4,8 @@
 // hooks and the building blocks of the MoE path.
 #include "internal.hpp"
 
+#include <mutex>
+
 #include <math.h>
 #include <vector>
 
@@ -281,6 +283,58 @@ extern "C" int emu_attend_cached(emu_ctx *ctx, const float *d_q, const void *d_k
     hipError_t e = hipGetLastError();
     emu_free(ctx, ws);
     if (e != hipSuccess) return emu_hip_fail(ctx, e, "attend_kernel");
+    return EMU_OK;
+}
+
+// ---- attend_cached without allocation -------------------------------------
+// The scores of emu_attend_cached_noalloc live in this file-scope device
+// array: heads * positions floats at most.  Each device holds its own copy,
+// at its own address, for the life of the process; host code reaches it only
+// through that address (the array's name is not a device address on the
+// host).  Every call on a device shares the device's copy, so calls that
+// overlap on one device race; the kernel writes every score it reads, so
+// nothing needs clearing between calls.
+constexpr size_t kAttendScratchFloats = (size_t)1 << 20; // 4 MiB
+static __device__ __align__(256) float scratch[kAttendScratchFloats];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch[kMaxDevices] = {};
+} // namespace
+
+int emu_ops_device_init(emu_ctx *ctx)
+{
+    if (ctx->device < 0 || ctx->device >= kMaxDevices) return EMU_E_ARG;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[ctx->device]) return EMU_OK;
+    // the context's device is current (emu_ctx_create set it)
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return emu_hip_fail(ctx, e != hipSuccess ? e : hipErrorInvalidSymbol,
+                                                     "hipGetSymbolAddress(scratch)");
+    g_scratch[ctx->device] = static_cast<float *>(ptr);
+    return EMU_OK;
+}
+
+extern "C" int emu_attend_cached_noalloc(emu_ctx *ctx, const float *d_q, const void *d_keys, const void *d_values,
+                                         int kv_f16, uint32_t positions, uint32_t heads, uint32_t kv_heads,
+                                         uint32_t head_dim, float scale, float *d_out)
+{
+    if (!ctx || !d_q || !d_keys || !d_values || !d_out || head_dim == 0) return EMU_E_ARG;
+    if (kv_heads == 0 || heads % kv_heads != 0) return EMU_E_CONFIG; // attend.rs:82-85
+    if (positions == 0 || heads == 0) return EMU_OK;
+    if ((uint64_t)heads * positions > kAttendScratchFloats) {
+        snprintf(ctx->last_error, sizeof ctx->last_error,
+                 "emu_attend_cached_noalloc: heads * positions = %llu exceeds its scratch of %zu scores",
+                 (unsigned long long)heads * positions, kAttendScratchFloats);
+        return EMU_E_CONFIG;
+    }
+    float *ws = ctx->device >= 0 && ctx->device < kMaxDevices ? g_scratch[ctx->device] : nullptr;
+    if (!ws) return EMU_E_ARG; // no context set this device up
+    hipLaunchKernelGGL(attend_kernel, dim3(heads), dim3(kThreads), 0, ctx->stream, d_q, d_keys, d_values, kv_f16,
+                       (int)positions, (int)heads, (int)kv_heads, (int)head_dim, scale, ws, d_out);
+    EMU_LAUNCH_CHECK(ctx);
     return EMU_OK;
 }
 

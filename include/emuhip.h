@@ -202,6 +202,15 @@ int emu_rope(emu_ctx *ctx, float *d_x, uint32_t n_tok, uint32_t heads, uint32_t 
 int emu_attend_cached(emu_ctx *ctx, const float *d_q, const void *d_keys, const void *d_values,
                       int kv_f16, uint32_t positions, uint32_t heads, uint32_t kv_heads,
                       uint32_t head_dim, float scale, float *d_out);
+/* emu_attend_cached that allocates nothing.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The scores
+ * go to a fixed device scratch of 1,048,576 floats (4 MiB) per device, held
+ * until the process ends: heads * positions beyond that is EMU_E_CONFIG.
+ * Calls that overlap on one device share that scratch and race. */
+int emu_attend_cached_noalloc(emu_ctx *ctx, const float *d_q, const void *d_keys, const void *d_values,
+                              int kv_f16, uint32_t positions, uint32_t heads, uint32_t kv_heads,
+                              uint32_t head_dim, float scale, float *d_out);
 
 /* moe::route (spm-granite-moe/src/moe.rs:17-35): softmax over n_experts
  * logits per token, top-k by (prob desc, id asc), weights renormalised by the
