@@ -34,7 +34,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from emufpga_amd import _lib  # noqa: E402
+from emufpga_amd import _lib, metrics  # noqa: E402
 from emufpga_amd.device import Context  # noqa: E402
 from emufpga_amd.gguf import GgufFile, row_bytes  # noqa: E402
 from emufpga_amd.serve import (GEMMA4_MOE, GRANITE_MOE_Q6K, OLMOE_1B_7B, QWEN3_8B_Q6K, SMOLLM2_135M_Q8,  # noqa: E402
@@ -45,6 +45,7 @@ HBM_PEAK_GBS = 8000.0
 KERNEL = "qmv_limb_kernel<LimbQ6KLM, S=1, D=1, dual, norm> (fused gate|up, 2 x 12288 x 4096 Q6_K, lane-major)"
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "qmv_limb_gate_up_qwen3_8b_pmc.txt")
 COPY_BYTES = 256 << 20  # calibration copy for the PMC byte counters
+TRACE_DIR = ""  # --trace-dir
 
 
 def measured_traffic():
@@ -317,12 +318,19 @@ def moe_leg(ctx, rng, name: str, cfg, n_clients: int, prompt_len: int, steps: in
     sess.route_trace(trace_steps)
     sess.time_decode(trace_steps)
     ctx.sync()
-    us = []
+    us, traced = [], []
     for slot in range(trace_steps):
         ids, _ = sess.read_routes(slot)
+        traced.append(ids)
         us += [len(set(ids[layer].reshape(-1).tolist())) for layer in range(cfg.layers)]
     mean_u = float(np.mean(us))
     sess.close()
+    if TRACE_DIR:
+        os.makedirs(TRACE_DIR, exist_ok=True)
+        with open(os.path.join(TRACE_DIR, f"{name}_routes.json"), "w") as f:
+            f.write(metrics.routing_trace(name, traced, n_clients, cfg.n_experts).to_json())
+        with open(os.path.join(TRACE_DIR, f"{name}_experts.json"), "w") as f:
+            f.write(metrics.expert_trace(name, cfg, traced[0], ms / steps / 1e3).to_json())
     tok_s = n_clients * steps / (ms / 1e3)
     ctx_mid = pos - steps // 2
     kv_ctx = [min(ctx_mid, cfg.window) if cfg.gemma and cfg.window and (l + 1) % cfg.global_every else ctx_mid
@@ -335,7 +343,9 @@ def moe_leg(ctx, rng, name: str, cfg, n_clients: int, prompt_len: int, steps: in
     out = {"value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": round(ms / steps, 4), "clients": n_clients,
            "context_at_timing": [pos - steps, pos], "routing": f"Zipf(s={zipf_s}) Gumbel-top-k, seed {seed}",
            "distinct_experts_per_layer": round(mean_u, 2), "algorithmic_bytes_per_step": int(step_bytes),
-           "step_hbm_gbs": round(gbs, 1), "step_hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+           "step_hbm_gbs": round(gbs, 1), "step_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+           # Ps / Rp / eta of one traced step (its own routes) at the timed step time
+           "scan_metrics": metrics.step_metrics(cfg, n_clients, ms / steps / 1e3, traced[0]).report()}
     if with_cpu:
         out["cpu_baseline"] = moe_cpu_baseline(model)
     model.close()
@@ -372,16 +382,21 @@ def main() -> int:
     ap.add_argument("--no-load", action="store_true", help="skip the GGUF -> HBM load leg")
     ap.add_argument("--no-smol", action="store_true", help="skip the SmolLM2 decode leg")
     ap.add_argument("--no-gemma", action="store_true", help="skip the Gemma-4-style MoE leg")
+    ap.add_argument("--trace-dir", default="",
+                    help="write each MoE leg's routing trace (emufpga.moe-routing.v1) and one step's expert "
+                         "trace (emufpga.serial-moe.v1) as JSON files here")
     ap.add_argument("--moe-prompt", type=int, default=0,
                     help="prompt length of the OLMoE / Gemma legs (default: the workloads' 1024 / 2048)")
     ap.add_argument("--batch8-only", action="store_true",
                     help="only the 8-client decode, logged without the JSON line; for profiling")
-    ap.add_argument("--moe-only", action="store_true",
-                    help="only the Granite MoE decode leg, logged without the JSON line; for profiling")
+    ap.add_argument("--moe-only", nargs="?", const="granite", choices=["granite", "olmoe", "gemma"],
+                    help="only one MoE decode leg (default granite), logged without the JSON line; for profiling")
     ap.add_argument("--roofline-rounds", type=int, default=8)
     ap.add_argument("--kernel-only", action="store_true",
                     help="only time the dominant kernel (the fused gate|up matvec over all layers); for profiling")
     args = ap.parse_args()
+    global TRACE_DIR
+    TRACE_DIR = args.trace_dir
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: this decode path runs "
               "on one GPU, whose share of a sharded model is the same kernels at their real shapes",
@@ -393,8 +408,12 @@ def main() -> int:
     cus, arch = ctx.device_info()
     log(f"device: {arch}, {cus} CUs")
     if args.moe_only:
-        log(json.dumps(moe_leg(ctx, np.random.default_rng(43), "granite", GRANITE_MOE_Q6K, 4, 256, 128, 1.1,
-                               False, 20260202)))
+        leg = {"granite": (GRANITE_MOE_Q6K, 4, 256, 128, 1.1, 20260202),
+               "olmoe": (OLMOE_1B_7B, 8, args.moe_prompt or 1024, args.steps, 1.0, 20260303),
+               "gemma": (GEMMA4_MOE, 8, args.moe_prompt or 2048, args.steps, 1.2, 20260404)}[args.moe_only]
+        m_cfg, n, prompt, steps, zs, seed = leg
+        log(json.dumps(moe_leg(ctx, np.random.default_rng(43), args.moe_only, m_cfg, n, prompt, steps, zs, False,
+                               seed)))
         ctx.close()
         return 0
     t0 = time.perf_counter()
@@ -470,6 +489,7 @@ def main() -> int:
         },
         "step_hbm_gbs": round(step_gbs, 1),
         "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
+        "scan_metrics": metrics.step_metrics(cfg, 1, step_ms / 1e3).report(),
         "weight_bytes_per_step": weight_bytes,
         "roofline": {
             "kernel": KERNEL,
@@ -490,6 +510,7 @@ def main() -> int:
         out["batch8"] = {"value": round(8 * args.steps / (ms8 / 1e3), 2), "unit": "tok/s",
                          "ms_per_step": round(ms8 / args.steps, 4), "context_at_timing": [pos8 - args.steps, pos8],
                          "step_hbm_gbs": round(gbs8, 1), "step_hbm_frac": round(gbs8 / HBM_PEAK_GBS, 4),
+                         "scan_metrics": metrics.step_metrics(cfg, 8, ms8 / args.steps / 1e3).report(),
                          "matvec": "int8 MFMA (v_mfma_i32_32x32x16_i8), activation limbs as the A operand"}
     if not args.no_smol:
         out["smollm2_b1"] = smol_leg(ctx, rng, not args.no_cpu)
