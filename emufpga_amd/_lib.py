@@ -115,6 +115,11 @@ _ERRORS = {
 EMU_ACT_SILU, EMU_ACT_GELU_TANH = 0, 1
 
 
+class ExpertCacheStats(C.Structure):
+    _fields_ = [("hits", C.c_uint64), ("misses", C.c_uint64), ("loads", C.c_uint64), ("evictions", C.c_uint64),
+                ("streamed", C.c_uint64), ("bytes_uploaded", C.c_uint64), ("resident", C.c_uint32)]
+
+
 class MoeDesc(C.Structure):
     _fields_ = [
         ("enc_gate_up", C.c_int32), ("enc_down", C.c_int32), ("d_gate", C.c_void_p), ("d_up", C.c_void_p),
@@ -189,6 +194,15 @@ SIGNATURES = {
     "emu_rope_table": [P, U32, U32, F, P],
     "emu_weights_lane_major": [P, I, P, SZ, P],
     "emu_model_sync": [P],
+    "emu_host_alloc": [P, SZ, C.POINTER(P)],
+    "emu_host_free": [P, P],
+    "emu_expert_cache_create": [P, U32, U32, SZ, U32, U32, I, C.POINTER(P)],
+    "emu_expert_cache_destroy": [P],
+    "emu_expert_cache_set_source": [P, U32, U32, P],
+    "emu_expert_cache_stats": [P, P],
+    "emu_expert_cache_slot": [P, U32, U32, P],
+    "emu_moe_ffn_cached": [P, P, P, U32, P, U32, P, P, P, P, SZ, P],
+    "emu_expert_cache_policy_trace": [U32, I, P, P, P, U32, P, P],
     "emu_session_route_zipf": [P, F, C.c_uint64],
     "emu_session_route_trace": [P, U32],
     "emu_session_read_routes": [P, U32, P, P],

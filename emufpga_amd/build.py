@@ -15,7 +15,8 @@ CSRC = PKG / "csrc"
 LIB = PKG / "libemuhip.so"
 ARCH = os.environ.get("EMU_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["core.hip", "qmv.hip", "limb.hip", "mfma.hip", "ops.hip", "attn.hip", "moe.hip", "model.hip", "files.hip"]
+SOURCES = ["core.hip", "qmv.hip", "limb.hip", "mfma.hip", "ops.hip", "attn.hip", "moe.hip", "model.hip", "files.hip",
+           "cache.hip"]
 
 FLAGS = [
     "-O3",

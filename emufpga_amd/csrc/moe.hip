@@ -24,6 +24,7 @@
 #include "internal.hpp"
 
 #include <math.h>
+#include <stdlib.h>
 
 namespace {
 
@@ -45,7 +46,30 @@ struct MoeArgs {
     float *out;                      // n_tok x width, or
     float *resid;                    // the residual stream it is added to (r + sum * resid_scale)
     float resid_scale;
+    // Experts in cache slots instead of expert-major tensors: table[e] holds
+    // expert e's gate rows, up rows and down rows back to back (null for an
+    // expert no token routes to).
+    const uint8_t *const *table;
 };
+
+// Rows of expert e: gate row r, up row r (hidden unit r), down row r.
+__device__ __forceinline__ const uint8_t *gate_row(const MoeArgs &a, int e, int r)
+{
+    if (a.table) return a.table[e] + (size_t)r * a.rb_in;
+    const size_t per = (size_t)(a.up ? 1 : 2) * a.ff;
+    return a.gate + ((size_t)e * per + r) * a.rb_in;
+}
+__device__ __forceinline__ const uint8_t *up_row(const MoeArgs &a, int e, int r)
+{
+    if (a.table) return a.table[e] + ((size_t)a.ff + r) * a.rb_in;
+    if (a.up) return a.up + ((size_t)e * a.ff + r) * a.rb_in;
+    return a.gate + ((size_t)e * 2 * a.ff + a.ff + r) * a.rb_in;
+}
+__device__ __forceinline__ const uint8_t *down_row(const MoeArgs &a, int e, int r)
+{
+    if (a.table) return a.table[e] + 2 * (size_t)a.ff * a.rb_in + (size_t)r * a.rb_ff;
+    return a.down + ((size_t)e * a.width + r) * a.rb_ff;
+}
 
 __device__ __forceinline__ void load8(const float *p, float v[8])
 {
@@ -211,16 +235,14 @@ __global__ __launch_bounds__(kThreads) void moe_up_kernel(MoeArgs a)
     int tok[kMaxTok];
 #pragma unroll
     for (int t = 0; t < kMaxTok; ++t) tok[t] = slot[t] / a.k;
-    const size_t per = (size_t)(a.up ? 1 : 2) * a.ff;
     const int j = lane / L, q = lane % L;
     // Lane groups 2i and 2i+1 take the gate and up rows of hidden unit r; the
     // groups of one unit (and every lane a shuffle below reads) share r, so
     // they leave together.
     const int r = (blockIdx.y * kWaves + wv) * up_rows_per_wave<L>() + (S >= 2 ? j >> 1 : 0);
     if (r >= a.ff) return;
-    const uint8_t *grow = a.gate + ((size_t)e * per + r) * a.rb_in;
-    const uint8_t *urow = a.up ? a.up + ((size_t)e * a.ff + r) * a.rb_in
-                               : a.gate + ((size_t)e * per + a.ff + r) * a.rb_in;
+    const uint8_t *grow = gate_row(a, e, r);
+    const uint8_t *urow = up_row(a, e, r);
     float ag[kMaxTok], au[kMaxTok];
 #pragma unroll
     for (int t = 0; t < kMaxTok; ++t) ag[t] = au[t] = 0.0f;
@@ -274,7 +296,6 @@ __global__ __launch_bounds__(kThreads) void moe_up_p_kernel(MoeArgs a)
     int tok[kMaxTok];
 #pragma unroll
     for (int t = 0; t < kMaxTok; ++t) tok[t] = slot[t] / a.k;
-    const size_t per = (size_t)(a.up ? 1 : 2) * a.ff;
     const int j = lane / L, q = lane % L;
     const int U = a.nb_in * F::UPB;
     const bool has_unit = q < U;
@@ -288,9 +309,8 @@ __global__ __launch_bounds__(kThreads) void moe_up_p_kernel(MoeArgs a)
         for (int p = 0; p < P; ++p) {
             int r = r0 + p * RPW;
             r = r < a.ff ? r : a.ff - 1;
-            const uint8_t *grow = a.gate + ((size_t)e * per + r) * a.rb_in;
-            const uint8_t *urow = a.up ? a.up + ((size_t)e * a.ff + r) * a.rb_in
-                                       : a.gate + ((size_t)e * per + a.ff + r) * a.rb_in;
+            const uint8_t *grow = gate_row(a, e, r);
+            const uint8_t *urow = up_row(a, e, r);
             if (NR == 1) unit_load<F>((j & 1) ? urow : grow, u, raw[p]);
             else {
                 unit_load<F>(grow, u, raw[NR * p]);
@@ -344,7 +364,7 @@ __global__ __launch_bounds__(kThreads) void moe_down_p_kernel(MoeArgs a)
     for (int p = 0; p < kPasses; ++p) {
         int r = r0 + p * S;
         r = r < a.width ? r : a.width - 1;
-        unit_load<F>(a.down + ((size_t)e * a.width + r) * a.rb_ff, u, raw[p]);
+        unit_load<F>(down_row(a, e, r), u, raw[p]);
     }
     const float scale = a.down_scale ? a.down_scale[e] : 1.0f;
     float accs[kPasses][kMaxTok];
@@ -380,7 +400,7 @@ __global__ __launch_bounds__(kThreads) void moe_down_kernel(MoeArgs a)
     const int r = (blockIdx.y * kWaves + wv) * S + j; // a lane group's row; the group leaves together
     if (r >= a.width) return;
     const float scale = a.down_scale ? a.down_scale[e] : 1.0f;
-    const uint8_t *row = a.down + ((size_t)e * a.width + r) * a.rb_ff;
+    const uint8_t *row = down_row(a, e, r);
     float acc[kMaxTok];
 #pragma unroll
     for (int t = 0; t < kMaxTok; ++t) acc[t] = 0.0f;
@@ -490,9 +510,9 @@ namespace {
 
 int moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok, const int32_t *d_ids,
             const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_out, float *d_resid,
-            float resid_scale, bool combine = true)
+            float resid_scale, bool combine = true, const uint8_t *const *d_table = nullptr)
 {
-    if (!ctx || !d || !d_x || !d_ids || !d_weights || !(d_out || d_resid) || !d->d_gate || !d->d_down)
+    if (!ctx || !d || !d_x || !d_ids || !d_weights || !(d_out || d_resid) || (!d_table && (!d->d_gate || !d->d_down)))
         return EMU_E_ARG;
     if (n_tok == 0) return EMU_OK;
     if (n_tok > kMaxTok || d->k == 0 || d->k > 8 || d->n_experts == 0 || d->k > d->n_experts) return EMU_E_ARG;
@@ -527,6 +547,7 @@ int moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_to
     a.out = d_out;
     a.resid = d_resid;
     a.resid_scale = resid_scale;
+    a.table = d_table;
     switch (d->enc_gate_up) {
     case EMU_ENC_Q6_K: launch_up<FmtQ6K>(ctx, a); break;
     case EMU_ENC_Q8_0: launch_up<FmtQ8_0>(ctx, a); break;
@@ -558,6 +579,17 @@ extern "C" int emu_moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x
 {
     if (!d_out) return EMU_E_ARG;
     return moe_ffn(ctx, d, d_x, n_tok, d_ids, d_weights, d_workspace, workspace_bytes, d_out, nullptr, 0.0f);
+}
+
+// The selected-expert FFN with expert e's gate, up and down rows at
+// d_table[e] (cache.hip).
+int emu_moe_ffn_table(emu_ctx *ctx, const emu_moe_desc *d, const uint8_t *const *d_table, const float *d_x,
+                      uint32_t n_tok, const int32_t *d_ids, const float *d_weights, void *d_workspace,
+                      size_t workspace_bytes, float *d_out)
+{
+    if (!d_out || !d_table) return EMU_E_ARG;
+    return moe_ffn(ctx, d, d_x, n_tok, d_ids, d_weights, d_workspace, workspace_bytes, d_out, nullptr, 0.0f, true,
+                   d_table);
 }
 
 int emu_moe_ffn_resid(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok, const int32_t *d_ids,

@@ -244,6 +244,49 @@ int emu_moe_ffn(emu_ctx *ctx, const emu_moe_desc *desc, const float *d_x, uint32
                 const int32_t *d_ids, const float *d_weights, void *d_workspace, size_t workspace_bytes,
                 float *d_out);
 
+/* ---- expert cache: experts in host memory behind HBM slots -------------
+ * The reference's ExpertCache (spm-granite-moe/src/expert_cache.rs:20-90) in
+ * front of the GPU: n_slots HBM slots of expert_bytes hold resident experts;
+ * an expert is admitted on its second miss (admit on second use), evicting
+ * the least recently used resident expert, or with layer_aware the least
+ * recently used one of the incoming expert's layer first
+ * (tools/llama-logits/mmid-cache.hpp:134-173).  An expert not admitted is
+ * streamed through one of n_transient slots for that call.  Experts of the
+ * call in progress are never evicted by it.  An expert's host bytes are its
+ * gate rows, up rows (ff x width each, in desc's enc_gate_up)
+ * and down rows (width x ff) back to back, registered per (layer, expert);
+ * they are uploaded with hipMemcpyAsync, so pinned memory (emu_host_alloc)
+ * lets the copies run asynchronously. */
+typedef struct emu_expert_cache emu_expert_cache;
+typedef struct emu_cache_stats {
+    uint64_t hits, misses, loads, evictions, streamed, bytes_uploaded;
+    uint32_t resident; /* slots holding an expert */
+} emu_cache_stats;
+int emu_host_alloc(emu_ctx *ctx, size_t bytes, void **h_out);
+int emu_host_free(emu_ctx *ctx, void *h);
+int emu_expert_cache_create(emu_ctx *ctx, uint32_t layers, uint32_t n_experts, size_t expert_bytes,
+                            uint32_t n_slots, uint32_t n_transient, int layer_aware, emu_expert_cache **out);
+int emu_expert_cache_destroy(emu_expert_cache *c);
+int emu_expert_cache_set_source(emu_expert_cache *c, uint32_t layer, uint32_t expert, const void *h_bytes);
+int emu_expert_cache_stats(const emu_expert_cache *c, emu_cache_stats *out);
+/* The resident slot of (layer, expert), or -1. */
+int emu_expert_cache_slot(const emu_expert_cache *c, uint32_t layer, uint32_t expert, int32_t *slot);
+/* emu_moe_ffn with the layer's experts taken through the cache: h_ids is the
+ * host copy of d_ids (n_tok x k), which decides what to upload; each
+ * distinct expert is looked up once, in ascending id (the reference's
+ * BTreeSet order).  d_gate/d_up/d_down of desc are not used.  EMU_E_CONFIG
+ * when more experts must stream through than there are transient slots;
+ * EMU_E_SHAPE when expert_bytes does not match desc. */
+int emu_moe_ffn_cached(emu_ctx *ctx, const emu_moe_desc *desc, emu_expert_cache *c, uint32_t layer,
+                       const float *d_x, uint32_t n_tok, const int32_t *h_ids, const int32_t *d_ids,
+                       const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_out);
+/* The cache policy alone, on the CPU (no device): n lookups (calls[i] groups
+ * them into calls; layers[i], experts[i]), each outcome 0 hit, 1 admitted,
+ * 2 streamed through, and the slot (-1 when streamed). */
+int emu_expert_cache_policy_trace(uint32_t n_slots, int layer_aware, const uint32_t *calls,
+                                  const uint32_t *layers, const uint32_t *experts, uint32_t n,
+                                  int32_t *outcome, int32_t *slot);
+
 /* Greedy selection over n_rows rows of width: tie_last 0 = lowest index of the
  * maximum (top_k, spm-qwen3-slice/src/math.rs:38-48); 1 = last index
  * (max_by(partial_cmp), spm-batch/tests/batching.rs:111-123). */
