@@ -2,7 +2,16 @@
 // spm-granite-moe/src/moe.rs:37-159; the Gemma expert form of
 // gemma_smoke.rs:92-139).
 //
-// After routing (emu_route: ids and weights, n_tok x k), three launches:
+// After routing (emu_route: ids and weights, n_tok x k), inputs of up to 4096
+// columns take the matrix-core form (the section "matrix-core form" below):
+//   1. limbs: the tokens' x as int8 limb planes, and the call's list of
+//      routed experts;
+//   2. gate|up on v_mfma_i32_32x32x16_i8, one grid row per listed expert,
+//      writing act(gate) * up per (token, slot);
+//   3. limbs: the activations as limb planes;
+//   4. down on the matrix cores into a per-(token, slot) contribution;
+//   5. combine, as below.
+// Wider inputs (and EMU_MOE_MMA=0) take the direct form, three launches:
 //   1. gate|up: grid (expert, row tile).  A wavefront finds the tokens routed
 //      to its expert with one ballot over the n_tok*k routing table (token
 //      order, as expert_tokens does), streams gate and up rows once for all of
@@ -496,6 +505,742 @@ template <class F> void launch_down(emu_ctx *ctx, const MoeArgs &a)
     }
 }
 
+// ---- matrix-core form ---------------------------------------------------------
+// The batch-1 limb idea on v_mfma_i32_32x32x16_i8, for every expert format.
+// Each routed input vector (a token's x for gate|up, a route's activation for
+// down) is carried as three signed 7-bit limbs per column with one
+// power-of-two scale per 256-column span, x ~= s * (16384*L0 + 128*L1 + L2),
+// exact to 2^-20 of the span's largest |x|.  One MFMA takes one 16-column
+// chunk: A (32 x 16) holds M row 8*limb + position (an expert's routed vectors
+// are its positions 0..7; rows 24..31 and positions past its count are zero),
+// B (16 x 32) the codes of 32 weight rows.  Lane l, register r of the result
+// holds limb r/4 of position 4*(l/32) + r%4 for weight row l%32.
+//
+// Within a span the sums stay integers and the span's d (and dmin) and the
+// activation scale apply once per span:
+//   Q2_K  a code times its 4-bit sub-block scale fits a byte, so B carries
+//         the scaled codes and the chunks chain on the matrix pipe;
+//   Q6_K  each chunk's limb sums times the chunk's int8 scale, added into a
+//         32-bit integer per limb;
+//   Q5_K  a sub-block's two chunks chain, times its 6-bit scale, likewise;
+//   Q8_0  a block's two chunks chain, times its d, in float.
+// The per-chunk terms that do not depend on the codes -- Q6_K's code bias
+// (-32 * sc * sum x) and the K-quant mins (dmin * m * sum x) -- are one more
+// product per span: each vector's per-chunk limb sums S (|S| <= 1024) are kept
+// as two int8 digits, S = 64 h + l, and two MFMAs take them against the
+// chunks' coefficients (K = the span's 16 chunks).
+//
+// A workgroup's wavefronts each own a 32-row tile (gate|up: 16 gate rows and
+// the 16 matching up rows, so the activation meets its pair in a lane
+// shuffle) and a share of its spans; the shares meet in LDS in a fixed order.
+// A wavefront stages each span's 32 rows through its own LDS rows with
+// coalesced 16-byte loads while the next span's loads are in flight; a
+// chunk's A operand register is refilled with the next span's chunk as soon
+// as its MFMA has issued.
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kChunkBytes = 48; // three int8 limbs of 16 columns
+constexpr int kSpanChunks = 16; // 16-column chunks per 256-column span
+constexpr int kSpanMeta = 112; // per vector and span: digits [h, l][limb][16 chunks] int8, then the scale
+constexpr int kMmaMaxCols = 4096;
+
+// Limb planes of n vectors of C chunks: limbs [vec][C][3][16] int8, then per
+// vector and span a kSpanMeta block: the limb sum digits [h, l][limb][16
+// chunks] int8 and, at byte 96, the span's scale (NaN: the span holds an inf
+// or NaN).
+struct LimbPlanes {
+    uint8_t *q;
+    uint8_t *dg;
+    int C, ns;
+};
+int spans_of(int C) { return (C + kSpanChunks - 1) / kSpanChunks; }
+size_t limb_plane_bytes(size_t n_vec, int C)
+{
+    return n_vec * ((size_t)C * kChunkBytes + (size_t)spans_of(C) * kSpanMeta);
+}
+LimbPlanes limb_planes(void *base, size_t n_vec, int C)
+{
+    LimbPlanes p;
+    p.C = C;
+    p.ns = spans_of(C);
+    p.q = static_cast<uint8_t *>(base);
+    p.dg = p.q + n_vec * C * kChunkBytes;
+    return p;
+}
+
+// v * 2^(20 - e2) as three signed 7-bit limbs (|v| < 2^e2): L[l].
+__device__ __forceinline__ void limb3(float v, int e2, int (&L)[3])
+{
+    const float s = ldexpf(v, 6 - e2); // exact, |s| < 64
+    const float f0 = rintf(s);
+    const float r1 = (s - f0) * 128.0f; // exact
+    const float f1 = rintf(r1);
+    const float f2 = rintf((r1 - f1) * 128.0f);
+    L[0] = (int)f0;
+    L[1] = (int)f1;
+    L[2] = (int)f2;
+}
+
+// The routed experts of a call, ascending, each with its routing-table
+// entries (t*k + slot, ascending): [0] the count, then kListEntry ints per
+// expert {e, n, -, -, slots[8]}.  The matrix-core launches take one grid row
+// per listed expert, so no workgroup slot is spent on experts nobody chose.
+constexpr int kListEntry = 12;
+size_t expert_list_bytes(int max_experts) { return sizeof(int32_t) * (4 + (size_t)kListEntry * max_experts); }
+
+// One wavefront, lane t holding routing-table entry t: one ballot per expert.
+__device__ void build_expert_list(const int32_t *ids, int nk, int n_experts, int32_t *list)
+{
+    const int lane = threadIdx.x;
+    const int my = lane < nk ? ids[lane] : -1;
+    int n = 0;
+    for (int e = 0; e < n_experts; ++e) { // uniform
+        const uint64_t m = __ballot(my == e);
+        if (m == 0) continue; // uniform
+        int32_t *en = list + 4 + (size_t)n * kListEntry;
+        const int rank = __popcll(m & ((1ull << lane) - 1));
+        if (my == e && rank < kMaxTok) en[4 + rank] = lane;
+        const int c = __popcll(m);
+        if (lane == 0) {
+            en[0] = e;
+            en[1] = c < kMaxTok ? c : kMaxTok;
+        }
+        if (lane >= c && lane < kMaxTok) en[4 + lane] = 0;
+        ++n;
+    }
+    if (lane == 0) list[0] = n;
+}
+
+// n_vec vectors of cols floats (row stride cols) into limb planes: sixteen
+// threads per span, one 16-column chunk each.  With a list, the last
+// workgroup's first wavefront also builds the call's expert list.
+__global__ __launch_bounds__(kThreads) void moe_limbs_kernel(const float *x, int n_vec, int cols, LimbPlanes P,
+                                                             const int32_t *ids, int nk, int n_experts, int32_t *list)
+{
+    if (list && blockIdx.x == gridDim.x - 1 && threadIdx.x < EMU_WAVE) build_expert_list(ids, nk, n_experts, list);
+    const int idx = blockIdx.x * kThreads + threadIdx.x;
+    const int total = n_vec * P.ns * kSpanChunks; // whole groups of 16 lanes
+    const int i = idx < total ? idx : total - 1;
+    const int m = i % kSpanChunks, vs = i / kSpanChunks;
+    const int vec = vs / P.ns, c = (vs % P.ns) * kSpanChunks + m;
+    const bool col = c < P.C;
+    float w[16];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) load8(x + (size_t)vec * cols + 16 * (col ? c : 0) + 8 * k, w + 8 * k);
+    float amax = 0.0f;
+    int bad = 0;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const float a = col ? fabsf(w[e]) : 0.0f;
+        amax = fmaxf(amax, a);
+        bad |= !(a <= 3.402823466e38f);
+    }
+#pragma unroll
+    for (int o = 1; o < kSpanChunks; o <<= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, o, EMU_WAVE));
+        bad |= __shfl_xor(bad, o, EMU_WAVE);
+    }
+    const bool finite = !bad;
+    int e2 = 0;
+    (void)frexpf(finite ? amax : 0.0f, &e2);
+    if (idx >= total) return;
+    uint32_t q[3][4] = {};
+    int S[3] = {0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        int L[3];
+        limb3(finite && col ? w[e] : 0.0f, e2, L);
+#pragma unroll
+        for (int l = 0; l < 3; ++l) {
+            q[l][e >> 2] |= ((uint32_t)L[l] & 0xffu) << (8 * (e & 3));
+            S[l] += L[l];
+        }
+    }
+    // the digits, also for chunks past the columns (zero), so the span's
+    // digit block is whole
+    uint8_t *dg = P.dg + (size_t)vs * kSpanMeta + m;
+#pragma unroll
+    for (int l = 0; l < 3; ++l) {
+        const int h = (S[l] + 32) >> 6; // |S| <= 1024: h in [-16, 16], S - 64h in [-32, 31]
+        dg[16 * l] = (uint8_t)h;
+        dg[48 + 16 * l] = (uint8_t)(S[l] - 64 * h);
+    }
+    if (col) {
+        uint8_t *dst = P.q + ((size_t)vec * P.C + c) * kChunkBytes;
+#pragma unroll
+        for (int l = 0; l < 3; ++l)
+            *reinterpret_cast<uint4 *>(dst + 16 * l) = make_uint4(q[l][0], q[l][1], q[l][2], q[l][3]);
+    }
+    if (m == 0)
+        *reinterpret_cast<float *>(P.dg + (size_t)vs * kSpanMeta + 96) = finite ? ldexpf(1.0f, e2 - 20) : __int_as_float(0x7fc00000);
+}
+
+__device__ __forceinline__ double limb_combine(int d0, int d1, int d2)
+{
+    return (double)d0 * 16384.0 + (double)d1 * 128.0 + (double)d2; // exact
+}
+
+// Byte b of the eight packed bytes (b < 8).
+__device__ __forceinline__ uint32_t byte8(uint2 v, int b) { return ((b < 4 ? v.x : v.y) >> (8 * (b & 3))) & 0xffu; }
+
+__device__ __forceinline__ long pack8(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
+
+// Pins twelve running sums at this point of the program: without it the
+// compiler reassociates a span's sixteen chunk products into a tree at the
+// end, which keeps every chunk's 16-register MFMA result alive at once.
+__device__ __forceinline__ void pin12(int (&I)[12])
+{
+    asm volatile(""
+                 : "+v"(I[0]), "+v"(I[1]), "+v"(I[2]), "+v"(I[3]), "+v"(I[4]), "+v"(I[5]), "+v"(I[6]), "+v"(I[7]),
+                   "+v"(I[8]), "+v"(I[9]), "+v"(I[10]), "+v"(I[11]));
+}
+
+// The A operands of one span: the 16 chunks' limbs and the two limb sum
+// digits, refilled chunk by chunk with the next span's; and the lane's
+// position's span scale.
+struct SpanA {
+    long av[kSpanChunks];
+    long ad[2];
+    float sc;
+};
+
+// Where a lane's A operands come from: M row j = limb j/8 of position j%8,
+// column half kh; zero for rows 24..31, positions past the count and chunks
+// past the columns.
+struct ASource {
+    const uint8_t *q, *dg, *meta;
+    int C, ns;
+    bool live, pos;
+    __device__ long chunk(int span, int m) const
+    {
+        const int c = kSpanChunks * span + m;
+        return live && c < C ? *reinterpret_cast<const long *>(q + (size_t)c * kChunkBytes) : 0;
+    }
+    __device__ long digit(int span, int d) const
+    {
+        return live ? *reinterpret_cast<const long *>(dg + (size_t)span * kSpanMeta + 48 * d) : 0;
+    }
+    __device__ float scale(int span) const
+    {
+        return pos ? *reinterpret_cast<const float *>(meta + (size_t)span * kSpanMeta + 96) : 0.0f;
+    }
+};
+
+// The span's sum-times-coefficient term: per position 4*kh + r (r < 4) and
+// the lane's row, sum over chunks m of coef_m * (16384 S0 + 128 S1 + S2)_m,
+// coef in the B bytes (chunks 8*kh .. 8*kh + 7).
+__device__ __forceinline__ void digit_sums(const long (&ad)[2], long coef, double (&t)[4])
+{
+    v16i Dh = {}, Dl = {};
+    Dh = __builtin_amdgcn_mfma_i32_32x32x16_i8(ad[0], coef, Dh, 0, 0, 0);
+    Dl = __builtin_amdgcn_mfma_i32_32x32x16_i8(ad[1], coef, Dl, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        t[r] = limb_combine(64 * Dh[r] + Dl[r], 64 * Dh[r + 4] + Dl[r + 4], 64 * Dh[r + 8] + Dl[r + 8]);
+}
+
+// Per format: a 256-column span of a row (SPAN bytes) is staged into an LDS
+// row of STRIDE bytes as NP 16-byte pieces and NT tails of TB bytes, and
+// span_dots() gives, for the lane's weight row and positions 4*kh + r, the
+// span's dot of the weights with the positions' combined limb integers (the
+// span's share of the matvec before the activation scale), refilling each A
+// register through next() once its MFMA has issued.
+template <class F> struct Mma;
+
+// Q6_K, 210 bytes: ql[128], qh[64], sc[16] (int8), d.  Chunk m = 8h + 2q + p
+// holds elements 128h + 32q + 16p + l (l < 16) with scale sc[m]:
+// |sc * (A x codes)| < 2^23 per chunk, sixteen chunks < 2^27.
+template <> struct Mma<FmtQ6K> {
+    static constexpr int SPAN = 210, STRIDE = 232, NP = 13, NT = 1, TB = 2;
+    static constexpr bool DIGITS = true;
+    __device__ static int gp(int k) { return 16 * k; }
+    __device__ static int lp(int k) { return 16 * k; }
+    __device__ static int gt(int) { return 208; }
+    __device__ static int lt(int) { return 208; }
+    __device__ static bool live_p(int, int) { return true; }
+    __device__ static bool live_t(int, int) { return true; }
+    __device__ static long codes(const uint8_t *rp, int m, int kh)
+    {
+        const int h = m >> 3, q = (m >> 1) & 3, p = m & 1;
+        const uint2 ql = *reinterpret_cast<const uint2 *>(rp + 64 * h + 32 * (q & 1) + 16 * p + 8 * kh);
+        const uint2 qh = *reinterpret_cast<const uint2 *>(rp + 128 + 32 * h + 16 * p + 8 * kh);
+        const int ns = 4 * (q >> 1), hs = 2 * q;
+        return pack8(((ql.x >> ns) & 0x0f0f0f0fu) | (((qh.x >> hs) & 0x03030303u) << 4),
+                     ((ql.y >> ns) & 0x0f0f0f0fu) | (((qh.y >> hs) & 0x03030303u) << 4));
+    }
+    template <class Next>
+    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int, int kh, float (&v)[4], const Next &next)
+    {
+        const uint2 s0 = *reinterpret_cast<const uint2 *>(rp + 192), s1 = *reinterpret_cast<const uint2 *>(rp + 200);
+        const float d = h2f(*reinterpret_cast<const uint16_t *>(rp + 208));
+        int I[12];
+#pragma unroll
+        for (int i = 0; i < 12; ++i) I[i] = 0;
+#pragma unroll
+        for (int m = 0; m < kSpanChunks; ++m) {
+            v16i D = {};
+            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.av[m], codes(rp, m, kh), D, 0, 0, 0);
+            A.av[m] = next(m);
+            const int sc = (int)(int8_t)byte8(m < 8 ? s0 : s1, m & 7);
+#pragma unroll
+            for (int i = 0; i < 12; ++i) I[i] += sc * D[i];
+            pin12(I);
+        }
+        double ts[4];
+        const uint2 sk = kh ? s1 : s0; // the int8 scales of chunks 8kh .. 8kh + 7
+        digit_sums(A.ad, pack8(sk.x, sk.y), ts);
+        A.ad[0] = next(kSpanChunks);
+        A.ad[1] = next(kSpanChunks + 1);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = (float)((double)d * (limb_combine(I[r], I[r + 4], I[r + 8]) - 32.0 * ts[r]));
+    }
+};
+
+// Q5_K, 176 bytes: d, dmin, 12 scale bytes, qh[32], qs[128].  Chunk m: group
+// g = m/4, nibble half = (m/2)&1, l in 16(m&1) + [0, 16); sub-block m/2 (32
+// columns, two chunks) has scale sc and min mn: |sc * D| < 2^22 per
+// sub-block, eight < 2^25.
+template <> struct Mma<FmtQ5K> {
+    static constexpr int SPAN = 176, STRIDE = 184, NP = 11, NT = 0, TB = 2;
+    static constexpr bool DIGITS = true;
+    __device__ static int gp(int k) { return 16 * k; }
+    __device__ static int lp(int k) { return 16 * k; }
+    __device__ static int gt(int) { return 0; }
+    __device__ static int lt(int) { return 0; }
+    __device__ static bool live_p(int, int) { return true; }
+    __device__ static bool live_t(int, int) { return true; }
+    __device__ static long codes(const uint8_t *rp, int m, int kh)
+    {
+        const int g = m >> 2, half = (m >> 1) & 1, l0 = 16 * (m & 1) + 8 * kh;
+        const uint2 w = *reinterpret_cast<const uint2 *>(rp + 48 + 32 * g + l0);
+        const uint2 h = *reinterpret_cast<const uint2 *>(rp + 16 + l0);
+        const int ns = 4 * half, hs = 2 * g + half;
+        return pack8(((w.x >> ns) & 0x0f0f0f0fu) | (((h.x >> hs) & 0x01010101u) << 4),
+                     ((w.y >> ns) & 0x0f0f0f0fu) | (((h.y >> hs) & 0x01010101u) << 4));
+    }
+    template <class Next>
+    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int, int kh, float (&v)[4], const Next &next)
+    {
+        FmtQ5K::Raw r;
+        const uint2 a = *reinterpret_cast<const uint2 *>(rp), b = *reinterpret_cast<const uint2 *>(rp + 8);
+        r.dd = a.x;
+        r.s0 = a.y;
+        r.s1 = b.x;
+        r.s2 = b.y;
+        int I[12];
+#pragma unroll
+        for (int i = 0; i < 12; ++i) I[i] = 0;
+#pragma unroll
+        for (int sb = 0; sb < kSpanChunks / 2; ++sb) {
+            v16i D = {};
+            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.av[2 * sb], codes(rp, 2 * sb, kh), D, 0, 0, 0);
+            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.av[2 * sb + 1], codes(rp, 2 * sb + 1, kh), D, 0, 0, 0);
+            A.av[2 * sb] = next(2 * sb);
+            A.av[2 * sb + 1] = next(2 * sb + 1);
+            uint32_t sc, mn;
+            FmtQ5K::scale_min(r, sb, sc, mn);
+#pragma unroll
+            for (int i = 0; i < 12; ++i) I[i] += (int)sc * D[i];
+            pin12(I);
+        }
+        // the mins of chunks 8kh .. 8kh + 7: sub-blocks 4kh .. 4kh + 3, two chunks each
+        uint32_t mb[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t sc, mn;
+            FmtQ5K::scale_min(r, 4 * kh + k, sc, mn);
+            mb[k] = mn * 0x0101u;
+        }
+        double ts[4];
+        digit_sums(A.ad, pack8(mb[0] | (mb[1] << 16), mb[2] | (mb[3] << 16)), ts);
+        A.ad[0] = next(kSpanChunks);
+        A.ad[1] = next(kSpanChunks + 1);
+        const double d = h2f((uint16_t)(r.dd & 0xffffu)), dmin = h2f((uint16_t)(r.dd >> 16));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = (float)(d * limb_combine(I[q], I[q + 4], I[q + 8]) - dmin * ts[q]);
+    }
+};
+
+// Q2_K, 84 bytes: sc[16] (scale low nibble, min high nibble), qs[64], d,
+// dmin.  Chunk m = 8N + 2j + s: codes (qs[32N + 16s + l] >> 2j) & 3, scale
+// byte sc[m].  The scaled codes (<= 45) chain over the span on the matrix
+// pipe (< 2^20 per limb).
+template <> struct Mma<FmtQ2K> {
+    static constexpr int SPAN = 84, STRIDE = 88, NP = 5, NT = 1, TB = 4;
+    static constexpr bool DIGITS = true;
+    __device__ static int gp(int k) { return 16 * k; }
+    __device__ static int lp(int k) { return 16 * k; }
+    __device__ static int gt(int) { return 80; }
+    __device__ static int lt(int) { return 80; }
+    __device__ static bool live_p(int, int) { return true; }
+    __device__ static bool live_t(int, int) { return true; }
+    template <class Next>
+    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int, int kh, float (&v)[4], const Next &next)
+    {
+        const uint2 s0 = *reinterpret_cast<const uint2 *>(rp), s1 = *reinterpret_cast<const uint2 *>(rp + 8);
+        const uint32_t dd = *reinterpret_cast<const uint32_t *>(rp + 80);
+        v16i Dq = {};
+#pragma unroll
+        for (int m = 0; m < kSpanChunks; ++m) {
+            const int N = m >> 3, j = (m >> 1) & 3, s = m & 1;
+            const uint2 w = *reinterpret_cast<const uint2 *>(rp + 16 + 32 * N + 16 * s + 8 * kh);
+            const uint32_t sc = byte8(m < 8 ? s0 : s1, m & 7) & 15u;
+            Dq = __builtin_amdgcn_mfma_i32_32x32x16_i8(
+                A.av[m], pack8(((w.x >> (2 * j)) & 0x03030303u) * sc, ((w.y >> (2 * j)) & 0x03030303u) * sc), Dq, 0,
+                0, 0);
+            A.av[m] = next(m);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        const uint2 sk = kh ? s1 : s0; // min nibbles of chunks 8kh .. 8kh + 7
+        double ts[4];
+        digit_sums(A.ad, pack8((sk.x >> 4) & 0x0f0f0f0fu, (sk.y >> 4) & 0x0f0f0f0fu), ts);
+        A.ad[0] = next(kSpanChunks);
+        A.ad[1] = next(kSpanChunks + 1);
+        const double d = h2f((uint16_t)(dd & 0xffffu)), dmin = h2f((uint16_t)(dd >> 16));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = (float)(d * limb_combine(Dq[q], Dq[q + 4], Dq[q + 8]) - dmin * ts[q]);
+    }
+};
+
+// Q8_0: a span is eight 34-byte blocks (d, 32 int8 codes).  The LDS row holds
+// the 256 codes first (block b at 32b) and the eight d values at 256 + 2b, so
+// every operand read is 8-byte aligned.  A row's last span may be partial.
+// A block's two chunks chain in one accumulator; its d scales the limb sums
+// in float.
+template <> struct Mma<FmtQ8_0> {
+    static constexpr int SPAN = 272, STRIDE = 280, NP = 16, NT = 8, TB = 2;
+    static constexpr bool DIGITS = false;
+    __device__ static int gp(int k) { return 34 * (k >> 1) + 2 + 16 * (k & 1); }
+    __device__ static int lp(int k) { return 16 * k; }
+    __device__ static int gt(int k) { return 34 * k; }
+    __device__ static int lt(int k) { return 256 + 2 * k; }
+    // nch chunks of the span are present: blocks below nch / 2
+    __device__ static bool live_p(int k, int nch) { return (k >> 1) < (nch >> 1); }
+    __device__ static bool live_t(int k, int nch) { return k < (nch >> 1); }
+    template <class Next>
+    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int nch, int kh, float (&v)[4], const Next &next)
+    {
+        const uint2 d0 = *reinterpret_cast<const uint2 *>(rp + 256), d1 = *reinterpret_cast<const uint2 *>(rp + 264);
+        float acc[12];
+#pragma unroll
+        for (int i = 0; i < 12; ++i) acc[i] = 0.0f;
+#pragma unroll
+        for (int b = 0; b < kSpanChunks / 2; ++b) {
+            v16i D = {};
+            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.av[2 * b], *reinterpret_cast<const long *>(rp + 32 * b + 8 * kh),
+                                                     D, 0, 0, 0);
+            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(
+                A.av[2 * b + 1], *reinterpret_cast<const long *>(rp + 32 * b + 16 + 8 * kh), D, 0, 0, 0);
+            A.av[2 * b] = next(2 * b);
+            A.av[2 * b + 1] = next(2 * b + 1);
+            if (2 * b < nch) { // uniform
+                const uint2 dv = b < 4 ? d0 : d1;
+                const float db = h2f((uint16_t)(((b & 3) < 2 ? dv.x : dv.y) >> (16 * (b & 1))));
+#pragma unroll
+                for (int i = 0; i < 12; ++i) acc[i] = __builtin_fmaf((float)D[i], db, acc[i]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = __builtin_fmaf(acc[q], 16384.0f, __builtin_fmaf(acc[q + 4], 128.0f, acc[q + 8]));
+    }
+};
+
+template <class M> constexpr int mma_piece_iters() { return (32 * M::NP + EMU_WAVE - 1) / EMU_WAVE; }
+template <class M> constexpr int mma_tail_iters() { return (32 * M::NT + EMU_WAVE - 1) / EMU_WAVE; }
+
+// One span's weight pieces, in flight.
+template <class M> struct SpanW {
+    uint4 p[mma_piece_iters<M>()];
+    uint32_t t[mma_tail_iters<M>() > 0 ? mma_tail_iters<M>() : 1];
+};
+
+enum { kMmaUp = 0, kMmaDown = 1 };
+
+struct MmaArgs {
+    MoeArgs a;
+    const int32_t *list; // the call's expert list
+    LimbPlanes in;       // the input vectors: tokens (gate|up) or routes (down)
+    int ks;        // wavefronts sharing a tile's spans (1, 2 or 4)
+    int tiles;     // tiles per expert
+};
+
+// Global-memory views of the weight rows.  The rows are reached through
+// the expert table or the layer's tensors; loading through a global pointer
+// keeps the loads off the flat path (whose completions also count against
+// the LDS counter, so every LDS wait would wait for the next span's rows).
+typedef __attribute__((address_space(1))) const uint8_t gbyte;
+struct __attribute__((packed)) Pk16 {
+    uint32_t x, y, z, w;
+};
+struct __attribute__((packed)) Pk4 {
+    uint32_t v;
+};
+struct __attribute__((packed)) Pk2 {
+    uint16_t v;
+};
+__device__ __forceinline__ uint4 gld16(gbyte *p)
+{
+    const __attribute__((address_space(1))) Pk16 *q = (const __attribute__((address_space(1))) Pk16 *)p;
+    return make_uint4(q->x, q->y, q->z, q->w);
+}
+__device__ __forceinline__ uint32_t gld4(gbyte *p) { return ((const __attribute__((address_space(1))) Pk4 *)p)->v; }
+__device__ __forceinline__ uint32_t gld2(gbyte *p) { return ((const __attribute__((address_space(1))) Pk2 *)p)->v; }
+
+// Expert e's row bases (wave-uniform): gate|up: its gate rows and up rows;
+// down: its down rows (in lo).
+template <int KIND> struct RowBases {
+    gbyte *lo, *hi;
+    size_t rb;
+};
+template <int KIND> __device__ __forceinline__ RowBases<KIND> row_bases(const MoeArgs &a, int e)
+{
+    RowBases<KIND> b;
+    if (KIND == kMmaUp) {
+        b.lo = (gbyte *)gate_row(a, e, 0);
+        b.hi = (gbyte *)up_row(a, e, 0);
+        b.rb = a.rb_in;
+    } else {
+        b.lo = b.hi = (gbyte *)down_row(a, e, 0);
+        b.rb = a.rb_ff;
+    }
+    return b;
+}
+
+// Row rr (0..31) of tile `tile`: gate|up rows 16*tile + rr (gate) and
+// 16*tile + rr - 16 (up); down rows 32*tile + rr (clamped to a valid row;
+// rows past the matrix are never stored).
+template <int KIND>
+__device__ __forceinline__ gbyte *tile_row(const MoeArgs &a, const RowBases<KIND> &b, int tile, int rr)
+{
+    if (KIND == kMmaUp) return (rr < 16 ? b.lo : b.hi) + (size_t)(uint32_t)(16 * tile + (rr & 15)) * b.rb;
+    const int r = 32 * tile + rr;
+    return b.lo + (size_t)(uint32_t)(r < a.width ? r : a.width - 1) * b.rb;
+}
+
+template <class F, int KIND>
+__device__ __forceinline__ void span_wload(const MoeArgs &a, const RowBases<KIND> &rbs, int C, int tile, int span,
+                                           int lane, SpanW<Mma<F>> &sw)
+{
+    using M = Mma<F>;
+    const int nch = C - kSpanChunks * span < kSpanChunks ? C - kSpanChunks * span : kSpanChunks;
+    const size_t so = (size_t)span * M::SPAN;
+#pragma unroll
+    for (int i = 0; i < mma_piece_iters<M>(); ++i) {
+        const int item = i * EMU_WAVE + lane;
+        const int rr = item / M::NP, k = item % M::NP;
+        if (item < 32 * M::NP && M::live_p(k, nch)) sw.p[i] = gld16(tile_row<KIND>(a, rbs, tile, rr) + so + M::gp(k));
+    }
+#pragma unroll
+    for (int i = 0; i < mma_tail_iters<M>(); ++i) {
+        const int item = i * EMU_WAVE + lane;
+        const int rr = item / (M::NT > 0 ? M::NT : 1), k = item % (M::NT > 0 ? M::NT : 1);
+        if (item < 32 * M::NT && M::live_t(k, nch)) {
+            gbyte *src = tile_row<KIND>(a, rbs, tile, rr) + so + M::gt(k);
+            sw.t[i] = M::TB == 4 ? gld4(src) : gld2(src);
+        }
+    }
+}
+
+template <class F>
+__device__ __forceinline__ void span_stage(const SpanW<Mma<F>> &sw, uint8_t *stage, int lane, int nch)
+{
+    using M = Mma<F>;
+#pragma unroll
+    for (int i = 0; i < mma_piece_iters<M>(); ++i) {
+        const int item = i * EMU_WAVE + lane;
+        const int rr = item / M::NP, k = item % M::NP;
+        if (item < 32 * M::NP && M::live_p(k, nch)) {
+            uint8_t *d = stage + rr * M::STRIDE + M::lp(k);
+            *reinterpret_cast<uint2 *>(d) = make_uint2(sw.p[i].x, sw.p[i].y);
+            *reinterpret_cast<uint2 *>(d + 8) = make_uint2(sw.p[i].z, sw.p[i].w);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < mma_tail_iters<M>(); ++i) {
+        const int item = i * EMU_WAVE + lane;
+        const int rr = item / (M::NT > 0 ? M::NT : 1), k = item % (M::NT > 0 ? M::NT : 1);
+        if (item < 32 * M::NT && M::live_t(k, nch)) {
+            uint8_t *d = stage + rr * M::STRIDE + M::lt(k);
+            if (M::TB == 4) *reinterpret_cast<uint32_t *>(d) = sw.t[i];
+            else *reinterpret_cast<uint16_t *>(d) = (uint16_t)sw.t[i];
+        }
+    }
+}
+
+// The routed position p's vector: the token (gate|up) or the route (down).
+template <int KIND> __device__ __forceinline__ int position_vec(const MoeArgs &a, const int (&slot)[kMaxTok], int p)
+{
+    int v = 0;
+#pragma unroll
+    for (int t = 0; t < kMaxTok; ++t) v = t == p ? slot[t] : v;
+    return KIND == kMmaUp ? v / a.k : v;
+}
+
+template <class F, int KIND, int ACT>
+__global__ __launch_bounds__(kThreads, 2) void moe_mma_kernel(MmaArgs g)
+{
+    using M = Mma<F>;
+    const MoeArgs &a = g.a;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int C = g.in.C, ns = g.in.ns, ks = g.ks;
+    float *red = reinterpret_cast<float *>(smem); // [kWaves][8][32]
+    const int tid = threadIdx.x, lane = tid & (EMU_WAVE - 1), w = tid / EMU_WAVE;
+    float *wsc = red + kWaves * kMaxTok * 32 + w * kMaxTok; // this wavefront's positions' span scales
+    uint8_t *stage = reinterpret_cast<uint8_t *>(red + kWaves * kMaxTok * 32 + kWaves * kMaxTok) + w * 32 * M::STRIDE;
+    // Grid: x = tile group, fastest, so that consecutive workgroups -- which
+    // the dispatcher deals round-robin to the XCDs -- are one expert's tiles
+    // and every routed expert's work spreads over all XCDs; y = the expert's
+    // place in the list.
+    // (the entry's address is valid whatever the count: the grid has at
+    // most as many rows as the list has room for)
+    const int32_t *en = g.list + 4 + (size_t)blockIdx.y * kListEntry;
+    const int4 eh = *reinterpret_cast<const int4 *>(en);
+    const int4 sa = *reinterpret_cast<const int4 *>(en + 4), sb = *reinterpret_cast<const int4 *>(en + 8);
+    if ((int)blockIdx.y >= g.list[0]) return; // uniform over the workgroup
+    const int e = eh.x, cnt = eh.y;
+    const int slot[kMaxTok] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
+    const int tl = w / ks, kp = w % ks;
+    const int tile_raw = blockIdx.x * (kWaves / ks) + tl;
+    const int tile = tile_raw < g.tiles ? tile_raw : g.tiles - 1;
+    const int s0 = kp * ns / ks, s1 = (kp + 1) * ns / ks;
+    // The first span's rows go out first: they do not depend on the routes.
+    const RowBases<KIND> rbs = row_bases<KIND>(a, e);
+    SpanW<M> sw;
+    if (s0 < s1) span_wload<F, KIND>(a, rbs, C, tile, s0, lane, sw);
+    const int j = lane & 31, kh = lane >> 5;
+    ASource src;
+    src.live = j < 24 && (j & 7) < cnt;
+    src.pos = lane < kMaxTok && lane < cnt; // lane p reads position p's scales
+    src.C = C;
+    src.ns = ns;
+    const int myvec = position_vec<KIND>(a, slot, j & 7);
+    src.q = g.in.q + (size_t)myvec * C * kChunkBytes + 16 * (j >> 3) + 8 * kh;
+    src.meta = g.in.dg + (size_t)myvec * ns * kSpanMeta;
+    src.dg = src.meta + 16 * (j >> 3) + 8 * kh;
+    SpanA A;
+    if (s0 < s1) {
+#pragma unroll
+        for (int m = 0; m < kSpanChunks; ++m) A.av[m] = src.chunk(s0, m);
+        A.ad[0] = M::DIGITS ? src.digit(s0, 0) : 0;
+        A.ad[1] = M::DIGITS ? src.digit(s0, 1) : 0;
+        A.sc = src.scale(s0);
+    }
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = s0; s < s1; ++s) {
+        const int nch = C - kSpanChunks * s < kSpanChunks ? C - kSpanChunks * s : kSpanChunks;
+        span_stage<F>(sw, stage, lane, nch);
+        if (s + 1 < s1) span_wload<F, KIND>(a, rbs, C, tile, s + 1, lane, sw); // in flight
+        __builtin_amdgcn_wave_barrier(); // LDS accesses of one wavefront complete in order
+        const bool more = s + 1 < s1;
+        auto next = [&](int m) -> long {
+            if (!more) return 0;
+            if (m < kSpanChunks) return src.chunk(s + 1, m);
+            return M::DIGITS ? src.digit(s + 1, m - kSpanChunks) : 0;
+        };
+        if (lane < kMaxTok) wsc[lane] = A.sc; // positions past the count: 0
+        if (more) A.sc = src.scale(s + 1);
+        float v[4];
+        M::span_dots(stage + j * M::STRIDE, A, nch, kh, v, next);
+        const float4 s4 = *reinterpret_cast<const float4 *>(wsc + 4 * kh);
+        acc[0] = __builtin_fmaf(v[0], s4.x, acc[0]);
+        acc[1] = __builtin_fmaf(v[1], s4.y, acc[1]);
+        acc[2] = __builtin_fmaf(v[2], s4.z, acc[2]);
+        acc[3] = __builtin_fmaf(v[3], s4.w, acc[3]);
+        __builtin_amdgcn_wave_barrier();
+    }
+    // The tile's span shares meet in LDS, added in share order.
+    float v[4] = {acc[0], acc[1], acc[2], acc[3]};
+    if (ks > 1) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[(w * kMaxTok + 4 * kh + r) * 32 + j] = acc[r];
+        __syncthreads();
+        if (kp == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float sum = red[(w * kMaxTok + 4 * kh + r) * 32 + j];
+                for (int k = 1; k < ks; ++k) sum += red[((w + k) * kMaxTok + 4 * kh + r) * 32 + j];
+                v[r] = sum;
+            }
+        }
+    }
+    if (kp != 0 || tile_raw >= g.tiles) return; // uniform per wavefront
+    if (KIND == kMmaDown) {
+        const int row = 32 * tile + j;
+        const float scale = a.down_scale ? a.down_scale[e] : 1.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int p = 4 * kh + r;
+            float o = v[r];
+            if (a.down_scale) o = __fmul_rn(o, scale); // gemma_smoke.rs:129-137
+            if (p < cnt && row < a.width) a.contrib[(size_t)position_vec<KIND>(a, slot, p) * a.width + row] = o;
+        }
+        return;
+    }
+    // gate|up: lanes j < 16 hold gate row 16*tile + j, lanes j + 16 its up row.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float u = __shfl_xor(v[r], 16, EMU_WAVE);
+        const int p = 4 * kh + r;
+        if (j < 16 && p < cnt)
+            a.act_buf[(size_t)position_vec<kMmaDown>(a, slot, p) * a.ff + 16 * tile + j] = activate<ACT>(v[r], u);
+    }
+}
+
+bool mma_enabled()
+{
+    static const bool on = [] {
+        const char *v = getenv("EMU_MOE_MMA");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
+
+// Wavefronts per tile: enough shares of the spans for about 2048 wavefronts
+// over the experts the step can route to.
+int mma_shares(const MoeArgs &a, int tiles, int spans)
+{
+    const int active = a.n_tok * a.k < a.n_experts ? a.n_tok * a.k : a.n_experts;
+    int ks = 1;
+    while (ks < kWaves && 2 * ks <= spans && active * tiles * ks < 2048) ks *= 2;
+    return ks;
+}
+
+template <class F, int KIND, int ACT>
+int launch_mma(emu_ctx *ctx, const MoeArgs &a, const LimbPlanes &in, const int32_t *list)
+{
+    using M = Mma<F>;
+    MmaArgs g;
+    g.a = a;
+    g.list = list;
+    g.in = in;
+    g.tiles = KIND == kMmaUp ? a.ff / 16 : (a.width + 31) / 32;
+    g.ks = mma_shares(a, g.tiles, in.ns);
+    const int tpw = kWaves / g.ks;
+    const size_t lds = kWaves * kMaxTok * 32 * 4 + kWaves * kMaxTok * 4 + kWaves * 32 * M::STRIDE;
+    const int listed = a.n_tok * a.k < a.n_experts ? a.n_tok * a.k : a.n_experts;
+    const dim3 grid((g.tiles + tpw - 1) / tpw, listed);
+    hipLaunchKernelGGL((moe_mma_kernel<F, KIND, ACT>), grid, dim3(kThreads), lds, ctx->stream, g);
+    EMU_LAUNCH_CHECK(ctx);
+    return EMU_OK;
+}
+
+template <class F> int launch_mma_up(emu_ctx *ctx, const MoeArgs &a, const LimbPlanes &in, const int32_t *list)
+{
+    if (a.act == EMU_ACT_GELU_TANH) return launch_mma<F, kMmaUp, EMU_ACT_GELU_TANH>(ctx, a, in, list);
+    return launch_mma<F, kMmaUp, EMU_ACT_SILU>(ctx, a, in, list);
+}
+
+int launch_limbs(emu_ctx *ctx, const float *x, int n_vec, int cols, const LimbPlanes &L, const int32_t *ids = nullptr,
+                 int nk = 0, int n_experts = 0, int32_t *list = nullptr)
+{
+    const int total = n_vec * L.ns * kSpanChunks;
+    hipLaunchKernelGGL(moe_limbs_kernel, dim3((total + kThreads - 1) / kThreads), dim3(kThreads), 0, ctx->stream, x,
+                       n_vec, cols, L, ids, nk, n_experts, list);
+    EMU_LAUNCH_CHECK(ctx);
+    return EMU_OK;
+}
+
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 } // namespace
@@ -503,7 +1248,9 @@ size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 extern "C" size_t emu_moe_workspace_bytes(uint32_t n_tok, uint32_t k, uint32_t width, uint32_t ff)
 {
     const size_t slots = (size_t)n_tok * k;
-    return align256(sizeof(float) * slots * ff) + align256(sizeof(float) * slots * width);
+    return align256(sizeof(float) * slots * ff) + align256(sizeof(float) * slots * width) +
+           align256(limb_plane_bytes(n_tok, (int)((width + 15) / 16))) +
+           align256(limb_plane_bytes(slots, (int)((ff + 15) / 16))) + align256(expert_list_bytes((int)slots));
 }
 
 namespace {
@@ -548,6 +1295,37 @@ int moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_to
     a.resid = d_resid;
     a.resid_scale = resid_scale;
     a.table = d_table;
+    if (mma_enabled() && d->width <= kMmaMaxCols && d->ff <= kMmaMaxCols && d->width % 16 == 0 && d->ff % 16 == 0) {
+        // matrix-core form: the tokens' limb planes, gate|up into the
+        // activations, the routes' limb planes, down into the contributions
+        const int c_in = (int)(d->width / 16), c_ff = (int)(d->ff / 16);
+        const size_t slots = (size_t)n_tok * d->k;
+        uint8_t *xp = static_cast<uint8_t *>(d_workspace) + align256(sizeof(float) * slots * d->ff) +
+                      align256(sizeof(float) * slots * d->width);
+        uint8_t *fp = xp + align256(limb_plane_bytes(n_tok, c_in));
+        int32_t *list = reinterpret_cast<int32_t *>(fp + align256(limb_plane_bytes(slots, c_ff)));
+        const LimbPlanes lx = limb_planes(xp, n_tok, c_in), lf = limb_planes(fp, slots, c_ff);
+        if ((st = launch_limbs(ctx, d_x, (int)n_tok, (int)d->width, lx, d_ids, (int)slots, (int)d->n_experts,
+                               list)) != EMU_OK)
+            return st;
+        switch (d->enc_gate_up) {
+        case EMU_ENC_Q6_K: st = launch_mma_up<FmtQ6K>(ctx, a, lx, list); break;
+        case EMU_ENC_Q8_0: st = launch_mma_up<FmtQ8_0>(ctx, a, lx, list); break;
+        case EMU_ENC_Q5_K: st = launch_mma_up<FmtQ5K>(ctx, a, lx, list); break;
+        case EMU_ENC_Q2_K: st = launch_mma_up<FmtQ2K>(ctx, a, lx, list); break;
+        default: return EMU_E_UNSUPPORTED;
+        }
+        if (st != EMU_OK) return st;
+        if ((st = launch_limbs(ctx, a.act_buf, (int)slots, (int)d->ff, lf)) != EMU_OK) return st;
+        switch (d->enc_down) {
+        case EMU_ENC_Q6_K: st = launch_mma<FmtQ6K, kMmaDown, 0>(ctx, a, lf, list); break;
+        case EMU_ENC_Q8_0: st = launch_mma<FmtQ8_0, kMmaDown, 0>(ctx, a, lf, list); break;
+        case EMU_ENC_Q5_K: st = launch_mma<FmtQ5K, kMmaDown, 0>(ctx, a, lf, list); break;
+        case EMU_ENC_Q2_K: st = launch_mma<FmtQ2K, kMmaDown, 0>(ctx, a, lf, list); break;
+        default: return EMU_E_UNSUPPORTED;
+        }
+        if (st != EMU_OK) return st;
+    } else {
     switch (d->enc_gate_up) {
     case EMU_ENC_Q6_K: launch_up<FmtQ6K>(ctx, a); break;
     case EMU_ENC_Q8_0: launch_up<FmtQ8_0>(ctx, a); break;
@@ -564,6 +1342,7 @@ int moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_to
     default: return EMU_E_UNSUPPORTED;
     }
     EMU_LAUNCH_CHECK(ctx);
+    }
     if (!combine) return EMU_OK;
     hipLaunchKernelGGL(moe_combine_kernel, dim3(n_tok, (d->width + kThreads - 1) / kThreads), dim3(kThreads), 0,
                        ctx->stream, a);

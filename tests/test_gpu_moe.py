@@ -4,7 +4,10 @@ through the C ABI, against the oracle.
 Bar: max |gpu - ref| <= 1e-4 * max |ref| over the layer output (two
 quantized matvecs of the reference's rounding bar, an activation and the
 weighted expert sum, propagated).  Expert order of the weighted sum is the
-reference's (ascending id); routing ids are identical.
+reference's (ascending id); routing ids are identical.  Inputs of up to 4096
+columns run on the int8 matrix cores with the activations carried as limbs
+exact to 2^-20 of each 256-column span's largest |x| (well inside the bar);
+wider ones run the vector kernels.
 """
 import ctypes as C
 
@@ -65,6 +68,12 @@ SHAPES = [
     ("gemma", _lib.Q5_K, _lib.Q8_0, 16, 2816, 704, 8, 8, True, _lib.EMU_ACT_GELU_TANH, 1.2),
     # rows shorter than 16 units: 4 rows per wavefront in both kernels
     ("short-rows", _lib.Q6_K, _lib.Q8_0, 8, 256, 96, 2, 3, True, _lib.EMU_ACT_SILU, 1.0),
+    # inputs wider than 4096 columns take the direct (vector) kernels
+    ("wide-rows", _lib.Q6_K, _lib.Q6_K, 4, 4352, 256, 2, 2, False, _lib.EMU_ACT_SILU, 1.0),
+    # one token: every expert holds a single position of the matrix-core operands
+    ("one-token-olmoe", _lib.Q2_K, _lib.Q2_K, 64, 2048, 1024, 8, 1, False, _lib.EMU_ACT_SILU, 1.0),
+    # a partial last span of Q8_0 down input (ff = 704: 2.75 spans) and 128 experts
+    ("gemma-b1", _lib.Q5_K, _lib.Q8_0, 128, 2816, 704, 8, 1, True, _lib.EMU_ACT_GELU_TANH, 1.2),
 ]
 
 
