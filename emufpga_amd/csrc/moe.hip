@@ -744,7 +744,7 @@ __device__ __forceinline__ void digit_sums(const long (&ad)[2], long coef, doubl
 // span_dots() gives, for the lane's weight row and positions 4*kh + r, the
 // span's dot of the weights with the positions' combined limb integers (the
 // span's share of the matvec before the activation scale), refilling each A
-// register through next() once its MFMA has issued.
+// register through refill() once its MFMA has issued.
 template <class F> struct Mma;
 
 // Q6_K, 210 bytes: ql[128], qh[64], sc[16] (int8), d.  Chunk m = 8h + 2q + p
@@ -759,18 +759,16 @@ template <> struct Mma<FmtQ6K> {
     __device__ static int lt(int) { return 208; }
     __device__ static bool live_p(int, int) { return true; }
     __device__ static bool live_t(int, int) { return true; }
-    __device__ static long codes(const uint8_t *rp, int m, int kh)
+    template <class Refill>
+    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int, int kh, float (&v)[4], const Refill &refill)
     {
-        const int h = m >> 3, q = (m >> 1) & 3, p = m & 1;
-        const uint2 ql = *reinterpret_cast<const uint2 *>(rp + 64 * h + 32 * (q & 1) + 16 * p + 8 * kh);
-        const uint2 qh = *reinterpret_cast<const uint2 *>(rp + 128 + 32 * h + 16 * p + 8 * kh);
-        const int ns = 4 * (q >> 1), hs = 2 * q;
-        return pack8(((ql.x >> ns) & 0x0f0f0f0fu) | (((qh.x >> hs) & 0x03030303u) << 4),
-                     ((ql.y >> ns) & 0x0f0f0f0fu) | (((qh.y >> hs) & 0x03030303u) << 4));
-    }
-    template <class Next>
-    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int, int kh, float (&v)[4], const Next &next)
-    {
+        // The span's operand words, read once: ql of (h, q&1, p) and qh of (h, p).
+        uint2 ql[8], qh[4];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            ql[i] = *reinterpret_cast<const uint2 *>(rp + 64 * (i >> 2) + 32 * ((i >> 1) & 1) + 16 * (i & 1) + 8 * kh);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qh[i] = *reinterpret_cast<const uint2 *>(rp + 128 + 32 * (i >> 1) + 16 * (i & 1) + 8 * kh);
         const uint2 s0 = *reinterpret_cast<const uint2 *>(rp + 192), s1 = *reinterpret_cast<const uint2 *>(rp + 200);
         const float d = h2f(*reinterpret_cast<const uint16_t *>(rp + 208));
         int I[12];
@@ -778,9 +776,15 @@ template <> struct Mma<FmtQ6K> {
         for (int i = 0; i < 12; ++i) I[i] = 0;
 #pragma unroll
         for (int m = 0; m < kSpanChunks; ++m) {
+            // chunk m = 8h + 2q + p: elements 128h + 32q + 16p + l
+            const int h = m >> 3, q = (m >> 1) & 3, p = m & 1;
+            const uint2 lo = ql[4 * h + 2 * (q & 1) + p], hi = qh[2 * h + p];
+            const int ns = 4 * (q >> 1), hs = 2 * q;
+            const long b = pack8(((lo.x >> ns) & 0x0f0f0f0fu) | (((hi.x >> hs) & 0x03030303u) << 4),
+                                 ((lo.y >> ns) & 0x0f0f0f0fu) | (((hi.y >> hs) & 0x03030303u) << 4));
             v16i D = {};
-            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.av[m], codes(rp, m, kh), D, 0, 0, 0);
-            A.av[m] = next(m);
+            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.av[m], b, D, 0, 0, 0);
+            refill(m);
             const int sc = (int)(int8_t)byte8(m < 8 ? s0 : s1, m & 7);
 #pragma unroll
             for (int i = 0; i < 12; ++i) I[i] += sc * D[i];
@@ -789,8 +793,7 @@ template <> struct Mma<FmtQ6K> {
         double ts[4];
         const uint2 sk = kh ? s1 : s0; // the int8 scales of chunks 8kh .. 8kh + 7
         digit_sums(A.ad, pack8(sk.x, sk.y), ts);
-        A.ad[0] = next(kSpanChunks);
-        A.ad[1] = next(kSpanChunks + 1);
+        refill(kSpanChunks);
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[r] = (float)((double)d * (limb_combine(I[r], I[r + 4], I[r + 8]) - 32.0 * ts[r]));
     }
@@ -809,17 +812,8 @@ template <> struct Mma<FmtQ5K> {
     __device__ static int lt(int) { return 0; }
     __device__ static bool live_p(int, int) { return true; }
     __device__ static bool live_t(int, int) { return true; }
-    __device__ static long codes(const uint8_t *rp, int m, int kh)
-    {
-        const int g = m >> 2, half = (m >> 1) & 1, l0 = 16 * (m & 1) + 8 * kh;
-        const uint2 w = *reinterpret_cast<const uint2 *>(rp + 48 + 32 * g + l0);
-        const uint2 h = *reinterpret_cast<const uint2 *>(rp + 16 + l0);
-        const int ns = 4 * half, hs = 2 * g + half;
-        return pack8(((w.x >> ns) & 0x0f0f0f0fu) | (((h.x >> hs) & 0x01010101u) << 4),
-                     ((w.y >> ns) & 0x0f0f0f0fu) | (((h.y >> hs) & 0x01010101u) << 4));
-    }
-    template <class Next>
-    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int, int kh, float (&v)[4], const Next &next)
+    template <class Refill>
+    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int, int kh, float (&v)[4], const Refill &refill)
     {
         FmtQ5K::Raw r;
         const uint2 a = *reinterpret_cast<const uint2 *>(rp), b = *reinterpret_cast<const uint2 *>(rp + 8);
@@ -827,16 +821,30 @@ template <> struct Mma<FmtQ5K> {
         r.s0 = a.y;
         r.s1 = b.x;
         r.s2 = b.y;
+        // The span's operand words, read once: qs of (g, m&1) and qh of m&1.
+        uint2 qs[8], qh[2];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qs[i] = *reinterpret_cast<const uint2 *>(rp + 48 + 32 * (i >> 1) + 16 * (i & 1) + 8 * kh);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) qh[i] = *reinterpret_cast<const uint2 *>(rp + 16 + 16 * i + 8 * kh);
+        auto codes = [&](int m) {
+            // chunk m: group g = m/4, nibble half = (m/2)&1, l in 16(m&1) + [0, 16)
+            const int g = m >> 2, half = (m >> 1) & 1;
+            const uint2 w = qs[2 * g + (m & 1)], h = qh[m & 1];
+            const int ns = 4 * half, hs = 2 * g + half;
+            return pack8(((w.x >> ns) & 0x0f0f0f0fu) | (((h.x >> hs) & 0x01010101u) << 4),
+                         ((w.y >> ns) & 0x0f0f0f0fu) | (((h.y >> hs) & 0x01010101u) << 4));
+        };
         int I[12];
 #pragma unroll
         for (int i = 0; i < 12; ++i) I[i] = 0;
 #pragma unroll
         for (int sb = 0; sb < kSpanChunks / 2; ++sb) {
             v16i D = {};
-            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.av[2 * sb], codes(rp, 2 * sb, kh), D, 0, 0, 0);
-            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.av[2 * sb + 1], codes(rp, 2 * sb + 1, kh), D, 0, 0, 0);
-            A.av[2 * sb] = next(2 * sb);
-            A.av[2 * sb + 1] = next(2 * sb + 1);
+            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.av[2 * sb], codes(2 * sb), D, 0, 0, 0);
+            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.av[2 * sb + 1], codes(2 * sb + 1), D, 0, 0, 0);
+            refill(2 * sb);
+            refill(2 * sb + 1);
             uint32_t sc, mn;
             FmtQ5K::scale_min(r, sb, sc, mn);
 #pragma unroll
@@ -853,8 +861,7 @@ template <> struct Mma<FmtQ5K> {
         }
         double ts[4];
         digit_sums(A.ad, pack8(mb[0] | (mb[1] << 16), mb[2] | (mb[3] << 16)), ts);
-        A.ad[0] = next(kSpanChunks);
-        A.ad[1] = next(kSpanChunks + 1);
+        refill(kSpanChunks);
         const double d = h2f((uint16_t)(r.dd & 0xffffu)), dmin = h2f((uint16_t)(r.dd >> 16));
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = (float)(d * limb_combine(I[q], I[q + 4], I[q + 8]) - dmin * ts[q]);
@@ -874,28 +881,30 @@ template <> struct Mma<FmtQ2K> {
     __device__ static int lt(int) { return 80; }
     __device__ static bool live_p(int, int) { return true; }
     __device__ static bool live_t(int, int) { return true; }
-    template <class Next>
-    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int, int kh, float (&v)[4], const Next &next)
+    template <class Refill>
+    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int, int kh, float (&v)[4], const Refill &refill)
     {
         const uint2 s0 = *reinterpret_cast<const uint2 *>(rp), s1 = *reinterpret_cast<const uint2 *>(rp + 8);
         const uint32_t dd = *reinterpret_cast<const uint32_t *>(rp + 80);
+        // The span's code words, read once: qs of (N, s); chunk 8N + 2j + s shifts them by 2j.
+        uint2 qs[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qs[i] = *reinterpret_cast<const uint2 *>(rp + 16 + 32 * (i >> 1) + 16 * (i & 1) + 8 * kh);
         v16i Dq = {};
 #pragma unroll
         for (int m = 0; m < kSpanChunks; ++m) {
-            const int N = m >> 3, j = (m >> 1) & 3, s = m & 1;
-            const uint2 w = *reinterpret_cast<const uint2 *>(rp + 16 + 32 * N + 16 * s + 8 * kh);
+            const int N = m >> 3, j = (m >> 1) & 3, sh = m & 1;
+            const uint2 w = qs[2 * N + sh];
             const uint32_t sc = byte8(m < 8 ? s0 : s1, m & 7) & 15u;
             Dq = __builtin_amdgcn_mfma_i32_32x32x16_i8(
                 A.av[m], pack8(((w.x >> (2 * j)) & 0x03030303u) * sc, ((w.y >> (2 * j)) & 0x03030303u) * sc), Dq, 0,
                 0, 0);
-            A.av[m] = next(m);
-            __builtin_amdgcn_sched_barrier(0);
+            refill(m);
         }
         const uint2 sk = kh ? s1 : s0; // min nibbles of chunks 8kh .. 8kh + 7
         double ts[4];
         digit_sums(A.ad, pack8((sk.x >> 4) & 0x0f0f0f0fu, (sk.y >> 4) & 0x0f0f0f0fu), ts);
-        A.ad[0] = next(kSpanChunks);
-        A.ad[1] = next(kSpanChunks + 1);
+        refill(kSpanChunks);
         const double d = h2f((uint16_t)(dd & 0xffffu)), dmin = h2f((uint16_t)(dd >> 16));
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = (float)(d * limb_combine(Dq[q], Dq[q + 4], Dq[q + 8]) - dmin * ts[q]);
@@ -917,30 +926,32 @@ template <> struct Mma<FmtQ8_0> {
     // nch chunks of the span are present: blocks below nch / 2
     __device__ static bool live_p(int k, int nch) { return (k >> 1) < (nch >> 1); }
     __device__ static bool live_t(int k, int nch) { return k < (nch >> 1); }
-    template <class Next>
-    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int nch, int kh, float (&v)[4], const Next &next)
+    template <class Refill>
+    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int nch, int kh, float (&v)[4],
+                                     const Refill &refill)
     {
         const uint2 d0 = *reinterpret_cast<const uint2 *>(rp + 256), d1 = *reinterpret_cast<const uint2 *>(rp + 264);
         float acc[12];
 #pragma unroll
         for (int i = 0; i < 12; ++i) acc[i] = 0.0f;
+        long cw[kSpanChunks]; // the span's codes, read once
+#pragma unroll
+        for (int m = 0; m < kSpanChunks; ++m) cw[m] = *reinterpret_cast<const long *>(rp + 16 * m + 8 * kh);
 #pragma unroll
         for (int b = 0; b < kSpanChunks / 2; ++b) {
             v16i D = {};
-            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.av[2 * b], *reinterpret_cast<const long *>(rp + 32 * b + 8 * kh),
-                                                     D, 0, 0, 0);
-            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(
-                A.av[2 * b + 1], *reinterpret_cast<const long *>(rp + 32 * b + 16 + 8 * kh), D, 0, 0, 0);
-            A.av[2 * b] = next(2 * b);
-            A.av[2 * b + 1] = next(2 * b + 1);
+            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.av[2 * b], cw[2 * b], D, 0, 0, 0);
+            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.av[2 * b + 1], cw[2 * b + 1], D, 0, 0, 0);
+            refill(2 * b);
+            refill(2 * b + 1);
             if (2 * b < nch) { // uniform
                 const uint2 dv = b < 4 ? d0 : d1;
                 const float db = h2f((uint16_t)(((b & 3) < 2 ? dv.x : dv.y) >> (16 * (b & 1))));
 #pragma unroll
                 for (int i = 0; i < 12; ++i) acc[i] = __builtin_fmaf((float)D[i], db, acc[i]);
             }
-            __builtin_amdgcn_sched_barrier(0);
         }
+        refill(kSpanChunks);
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = __builtin_fmaf(acc[q], 16384.0f, __builtin_fmaf(acc[q + 4], 128.0f, acc[q + 8]));
     }
@@ -1133,15 +1144,24 @@ __global__ __launch_bounds__(kThreads, 2) void moe_mma_kernel(MmaArgs g)
         if (s + 1 < s1) span_wload<F, KIND>(a, rbs, C, tile, s + 1, lane, sw); // in flight
         __builtin_amdgcn_wave_barrier(); // LDS accesses of one wavefront complete in order
         const bool more = s + 1 < s1;
-        auto next = [&](int m) -> long {
-            if (!more) return 0;
-            if (m < kSpanChunks) return src.chunk(s + 1, m);
-            return M::DIGITS ? src.digit(s + 1, m - kSpanChunks) : 0;
+        // The next span's A operands go into each register as soon as its
+        // MFMA has issued (lanes outside the positions keep their zeros).
+        const int nchn = more ? (C - kSpanChunks * (s + 1) < kSpanChunks ? C - kSpanChunks * (s + 1) : kSpanChunks) : 0;
+        const uint8_t *an = src.q + (size_t)kSpanChunks * (s + 1) * kChunkBytes;
+        const uint8_t *dn = src.dg + (size_t)(s + 1) * kSpanMeta;
+        auto refill = [&](int m) {
+            if (m < kSpanChunks) {
+                if (m >= nchn) A.av[m] = 0; // uniform: no next span, or past its columns
+                else if (src.live) A.av[m] = *reinterpret_cast<const long *>(an + m * kChunkBytes);
+            } else if (M::DIGITS && more && src.live) {
+                A.ad[0] = *reinterpret_cast<const long *>(dn);
+                A.ad[1] = *reinterpret_cast<const long *>(dn + 48);
+            }
         };
         if (lane < kMaxTok) wsc[lane] = A.sc; // positions past the count: 0
         if (more) A.sc = src.scale(s + 1);
         float v[4];
-        M::span_dots(stage + j * M::STRIDE, A, nch, kh, v, next);
+        M::span_dots(stage + j * M::STRIDE, A, nch, kh, v, refill);
         const float4 s4 = *reinterpret_cast<const float4 *>(wsc + 4 * kh);
         acc[0] = __builtin_fmaf(v[0], s4.x, acc[0]);
         acc[1] = __builtin_fmaf(v[1], s4.y, acc[1]);
