@@ -245,7 +245,7 @@ struct MfmaArgs {
     int rows, cols, n_tok;
     const uint8_t *xa;
     const float *xs;
-    float *part; // [cols/kSlice][nmat][kMaxTok][rows]
+    float *part; // [slices][nmat][kMaxTok][rows], slices = ceil(cols / kSlice)
 };
 
 // Q6_K codes (0..63) of 8 columns, two dwords: sub-block (h, q, p) takes
@@ -281,7 +281,7 @@ struct Unit {
 // while the weights load.
 __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs a, int units)
 {
-    const int nks = a.cols / kSlice, nrt = (a.rows + kTileRows - 1) / kTileRows;
+    const int nks = (a.cols + kSlice - 1) / kSlice, nrt = (a.rows + kTileRows - 1) / kTileRows;
     const int tid = threadIdx.x, lane = tid & (EMU_WAVE - 1), w = tid / EMU_WAVE;
     const int j = lane & 31, kh = lane >> 5;
     const bool live = j < 24 && (j & 7) < a.n_tok; // A row j: limb j / 8 of token j % 8
@@ -298,54 +298,70 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
         b.rt = v % nrt;
         b.mat = v / nrt;
         const int cb = b.ks * kWaves + w; // this wavefront's 256-column block
+        // The last slice of a row whose width is not a multiple of the slice
+        // has wavefronts past the row: they load nothing and add zeros.
+        const bool has = cb < a.cols / 256;
         // The A operands (activation limbs, from L2) load before the weights
         // (from HBM): loads complete in issue order, so the other way round
         // their round trip would follow the weights' instead of overlapping it.
         const uint8_t *ap = a.xa + (size_t)cb * 16 * kSbBytes + (size_t)(kh * 24 + (live ? j : 0)) * 8;
 #pragma unroll
-        for (int sb = 0; sb < 16; ++sb) b.av[sb] = *reinterpret_cast<const long *>(ap + sb * kSbBytes);
-        // and so do the slice's activation scales (one float4 per thread)
+        for (int sb = 0; sb < 16; ++sb) b.av[sb] = has ? *reinterpret_cast<const long *>(ap + sb * kSbBytes) : 0;
+        // and so do the slice's activation scales (one float4 per thread:
+        // half a sub-block's eight tokens; zero past the row)
         static_assert(kSlice / 16 * kMaxTok / 4 <= EMU_WAVE * kWaves, "one scale load per thread");
         const float4 *xsrc = reinterpret_cast<const float4 *>(a.xs + (size_t)b.ks * (kSlice / 16) * kMaxTok);
-        xsv = xsrc[tid < kSlice / 16 * kMaxTok / 4 ? tid : 0];
+        const int t4 = tid < kSlice / 16 * kMaxTok / 4 ? tid : 0;
+        xsv = b.ks * (kSlice / 16) + t4 / 2 < a.cols / 16 ? xsrc[t4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         __builtin_amdgcn_sched_barrier(0);
         // Coalesced: instruction k covers rows 4k..4k+3 of the tile, 16 lanes
         // per row (13 x 16 bytes + the 2-byte d), into this wavefront's LDS rows.
         const int r4 = lane >> 4, c16 = lane & 15;
-        uint4 raw[8];
-        uint16_t dd[8];
+        if (has) { // uniform
+            uint4 raw[8];
+            uint16_t dd[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            int row = b.rt * kTileRows + 4 * k + r4;
-            row = row < a.rows ? row : a.rows - 1; // a valid row; never stored
-            const uint8_t *bp = a.w[b.mat] + (size_t)row * a.row_bytes + (size_t)cb * 210;
-            if (c16 < 13) raw[k] = ld16(bp + 16 * c16);
-            else if (c16 == 13) dd[k] = ld2(bp + 208);
-        }
-        uint8_t *mine = wl[w];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            uint8_t *rp = mine + (4 * k + r4) * kRowStride;
-            if (c16 < 13) {
-                *reinterpret_cast<uint2 *>(rp + 16 * c16) = make_uint2(raw[k].x, raw[k].y);
-                *reinterpret_cast<uint2 *>(rp + 16 * c16 + 8) = make_uint2(raw[k].z, raw[k].w);
-            } else if (c16 == 13) {
-                *reinterpret_cast<uint16_t *>(rp + 208) = dd[k];
+            for (int k = 0; k < 8; ++k) {
+                int row = b.rt * kTileRows + 4 * k + r4;
+                row = row < a.rows ? row : a.rows - 1; // a valid row; never stored
+                const uint8_t *bp = a.w[b.mat] + (size_t)row * a.row_bytes + (size_t)cb * 210;
+                if (c16 < 13) raw[k] = ld16(bp + 16 * c16);
+                else if (c16 == 13) dd[k] = ld2(bp + 208);
             }
-        }
-        __builtin_amdgcn_wave_barrier(); // LDS accesses of one wavefront complete in order
-        const uint8_t *bp = mine + j * kRowStride;
+            uint8_t *mine = wl[w];
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                b.ql[h][0][p] = *reinterpret_cast<const uint2 *>(bp + 64 * h + 16 * p + 8 * kh);
-                b.ql[h][1][p] = *reinterpret_cast<const uint2 *>(bp + 64 * h + 32 + 16 * p + 8 * kh);
-                b.qh[h][p] = *reinterpret_cast<const uint2 *>(bp + 128 + 32 * h + 16 * p + 8 * kh);
+            for (int k = 0; k < 8; ++k) {
+                uint8_t *rp = mine + (4 * k + r4) * kRowStride;
+                if (c16 < 13) {
+                    *reinterpret_cast<uint2 *>(rp + 16 * c16) = make_uint2(raw[k].x, raw[k].y);
+                    *reinterpret_cast<uint2 *>(rp + 16 * c16 + 8) = make_uint2(raw[k].z, raw[k].w);
+                } else if (c16 == 13) {
+                    *reinterpret_cast<uint16_t *>(rp + 208) = dd[k];
+                }
             }
-        const uint2 s0 = *reinterpret_cast<const uint2 *>(bp + 192), s1 = *reinterpret_cast<const uint2 *>(bp + 200);
-        b.sc = make_uint4(s0.x, s0.y, s1.x, s1.y);
-        b.d = *reinterpret_cast<const uint16_t *>(bp + 208);
+            __builtin_amdgcn_wave_barrier(); // LDS accesses of one wavefront complete in order
+            const uint8_t *bp = mine + j * kRowStride;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    b.ql[h][0][p] = *reinterpret_cast<const uint2 *>(bp + 64 * h + 16 * p + 8 * kh);
+                    b.ql[h][1][p] = *reinterpret_cast<const uint2 *>(bp + 64 * h + 32 + 16 * p + 8 * kh);
+                    b.qh[h][p] = *reinterpret_cast<const uint2 *>(bp + 128 + 32 * h + 16 * p + 8 * kh);
+                }
+            const uint2 s0 = *reinterpret_cast<const uint2 *>(bp + 192), s1 = *reinterpret_cast<const uint2 *>(bp + 200);
+            b.sc = make_uint4(s0.x, s0.y, s1.x, s1.y);
+            b.d = *reinterpret_cast<const uint16_t *>(bp + 208);
+        } else { // zero codes, scales and d: this wavefront adds exact zeros
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    b.ql[h][0][p] = b.ql[h][1][p] = b.qh[h][p] = make_uint2(0u, 0u);
+                }
+            b.sc = make_uint4(0u, 0u, 0u, 0u);
+            b.d = 0;
+        }
 #pragma unroll
         for (int sb = 0; sb < 16; ++sb) b.av[sb] = live ? b.av[sb] : 0; // rows past the tokens are zero
     }
@@ -493,7 +509,7 @@ Ws workspace(emu_ctx *ctx, int cols_cap)
 }
 size_t part_bytes(int rows, int cols, int nmat)
 {
-    return (size_t)(cols / kSlice) * nmat * kMaxTok * (size_t)rows * sizeof(float);
+    return (size_t)((cols + kSlice - 1) / kSlice) * nmat * kMaxTok * (size_t)rows * sizeof(float);
 }
 
 } // namespace
@@ -527,8 +543,11 @@ int emu_mfma_reserve(emu_ctx *ctx, size_t bytes)
 bool emu_mfma_supports(int encoding, int cols, int n_tok)
 {
     if (mfma_disabled()) return false;
-    return encoding == EMU_ENC_Q6_K && n_tok >= 2 && n_tok <= kMaxTok && cols > 0 && cols % kSlice == 0 &&
-           cols / kSlice <= kMaxSlices &&
+    // Widths that are not whole slices (a multiple of 256 columns, the last
+    // slice partly empty) only from 2048 columns: below that the single-launch
+    // vector kernel costs less than link, matvec and finish.
+    return encoding == EMU_ENC_Q6_K && n_tok >= 2 && n_tok <= kMaxTok && cols > 0 &&
+           (cols % kSlice == 0 || (cols % 256 == 0 && cols >= 2048)) && (cols + kSlice - 1) / kSlice <= kMaxSlices &&
            cols <= 8 * kLinkThreads * kLinkPairs;
 }
 
@@ -588,7 +607,7 @@ int emu_mfma_matvec(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int
     ma.xa = w.xa;
     ma.xs = w.xs;
     ma.part = w.part;
-    const int nks = q.cols / kSlice, nrt = (q.rows + kTileRows - 1) / kTileRows;
+    const int nks = (q.cols + kSlice - 1) / kSlice, nrt = (q.rows + kTileRows - 1) / kTileRows;
     const int units = nks * nrt * nmat;
     hipLaunchKernelGGL(qmv_mfma_kernel, dim3((unsigned)units), dim3(EMU_WAVE * kWaves), 0, ctx->stream, ma, units);
     EMU_LAUNCH_CHECK(ctx);
@@ -604,7 +623,7 @@ int emu_mfma_finish(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int
     const Ws w = workspace(ctx, cols_cap);
     FinishArgs fa{};
     fa.part = w.part;
-    fa.nks = q.cols / kSlice;
+    fa.nks = (q.cols + kSlice - 1) / kSlice;
     fa.nmat = nmat;
     fa.rows = q.rows;
     fa.y = q.y;

@@ -45,7 +45,9 @@ def check(got, ref, bound):
 
 
 @pytest.mark.parametrize("rows,cols,n_tok", [(1, 4096, 2), (31, 4096, 8), (33, 4096, 3), (4099, 4096, 8),
-                                             (6144, 4096, 5), (37, 12288, 2), (4096, 12288, 8), (100, 2048, 7)])
+                                             (6144, 4096, 5), (37, 12288, 2), (4096, 12288, 8), (100, 2048, 7),
+                                             # widths that end in a partly empty slice
+                                             (77, 2816, 8), (40, 2304, 2), (300, 3328, 5)])
 def test_plain_matches_oracle(ctx, rows, cols, n_tok):
     raw = weights(rows, cols, rows * 7 + cols + n_tok)
     x = np.random.default_rng(rows + n_tok).normal(size=(n_tok, cols)).astype(np.float32)
