@@ -291,6 +291,69 @@ def moe_cpu_baseline(model: Model, budget_layers: int = 2) -> dict:
                        f"({t1:.2f} s, {t2:.2f} s), per-layer cost extrapolated to {c.layers} layers")}
 
 
+# The expert layers of the three MoE workloads: (gate|up encoding, down encoding,
+# experts, width, expert ff, routes per token, tokens, gate and up fused per
+# expert, activation, Zipf exponent).
+MOE_LAYERS = {
+    "granite": (_lib.Q6_K, _lib.Q6_K, 32, 1024, 512, 8, 4, False, _lib.EMU_ACT_SILU, 1.1),
+    "olmoe": (_lib.Q2_K, _lib.Q2_K, 64, 2048, 1024, 8, 8, False, _lib.EMU_ACT_SILU, 1.0),
+    "gemma": (_lib.Q5_K, _lib.Q8_0, 128, 2816, 704, 8, 8, True, _lib.EMU_ACT_GELU_TANH, 1.2),
+}
+BLOCK = {_lib.Q6_K: (256, 210, (208,)), _lib.Q5_K: (256, 176, (0, 2)), _lib.Q2_K: (256, 84, (80, 82)),
+         _lib.Q8_0: (32, 34, (0,))}
+
+
+def random_blocks(enc: int, nblocks: int, rng) -> np.ndarray:
+    """Random block bytes with moderate f16 scales at the format's scale offsets."""
+    _, bb, scales = BLOCK[enc]
+    raw = rng.integers(0, 256, size=(nblocks, bb), dtype=np.uint8)
+    for off in scales:
+        raw[:, off:off + 2] = (rng.uniform(0.5, 1.0, nblocks) * 2.0 ** -10).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    return raw
+
+
+def moe_layer_leg(ctx, name: str, reps: int) -> dict:
+    """One selected-expert FFN layer (emu_moe_ffn) of a MoE workload at its shape,
+    with Zipf routes, called back to back: the expert kernels alone, for counters."""
+    enc_in, enc_down, E, W, FF, K, T, fused, act, s = MOE_LAYERS[name]
+    rng = np.random.default_rng(7)
+    be_in, bb_in, _ = BLOCK[enc_in]
+    be_ff, bb_ff, _ = BLOCK[enc_down]
+    n_in = E * (2 if fused else 1) * FF * W // be_in
+    bufs = [ctx.upload(random_blocks(enc_in, n_in, rng)),
+            None if fused else ctx.upload(random_blocks(enc_in, n_in, rng)),
+            ctx.upload(random_blocks(enc_down, E * W * FF // be_ff, rng))]
+    bs = ctx.upload(rng.uniform(0.5, 2.0, E).astype(np.float32)) if fused else None
+    desc = _lib.MoeDesc(enc_in, enc_down, bufs[0].addr, bufs[1].addr if bufs[1] else None, bufs[2].addr,
+                        bs.addr if bs else None, E, W, FF, K, act)
+    rank = rng.permutation(E) + 1
+    logits = -s * np.log(rank)[None, :] - np.log(-np.log(rng.uniform(1e-9, 1.0, size=(T, E))))
+    ids = np.argsort(-logits, axis=1, kind="stable")[:, :K].astype(np.int32)
+    wts = np.full((T, K), 1.0 / K, np.float32)
+    distinct = len(set(ids.reshape(-1).tolist()))
+    bx, bi, bw = ctx.upload(rng.normal(size=(T, W)).astype(np.float32)), ctx.upload(ids), ctx.upload(wts)
+    ws_bytes = ctx.lib.emu_moe_workspace_bytes(T, K, W, FF)
+    ws, out = ctx.alloc(ws_bytes), ctx.alloc(T * W * 4)
+
+    def call():
+        ctx.check(ctx.lib.emu_moe_ffn(ctx.h, C.byref(desc), bx.ptr, T, bi.ptr, bw.ptr, ws.ptr, ws_bytes, out.ptr),
+                  "emu_moe_ffn")
+
+    for _ in range(5):
+        call()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        call()
+    ctx.sync()
+    us = (time.perf_counter() - t0) / reps * 1e6
+    expert_bytes = 2 * FF * (W // be_in) * bb_in + W * (FF // be_ff) * bb_ff
+    log(f"{name} expert layer: {T} tokens x {K} routes, {distinct} distinct experts of {expert_bytes} B: "
+        f"{us:.1f} us per call ({reps} calls)")
+    return {"layer": name, "us_per_call": round(us, 2), "distinct_experts": distinct,
+            "expert_bytes": expert_bytes, "algorithmic_bytes": distinct * expert_bytes}
+
+
 def moe_leg(ctx, rng, name: str, cfg, n_clients: int, prompt_len: int, steps: int, zipf_s: float,
             with_cpu: bool, seed: int) -> dict:
     """A mixture-of-experts decoder: n_clients concurrent sequences after
@@ -391,6 +454,10 @@ def main() -> int:
                     help="only the 8-client decode, logged without the JSON line; for profiling")
     ap.add_argument("--moe-only", nargs="?", const="granite", choices=["granite", "olmoe", "gemma"],
                     help="only one MoE decode leg (default granite), logged without the JSON line; for profiling")
+    ap.add_argument("--moe-layer", choices=sorted(MOE_LAYERS),
+                    help="only one MoE workload's selected-expert FFN layer, called back to back; for counters")
+    ap.add_argument("--smol-only", action="store_true",
+                    help="only the SmolLM2 decode leg, logged without the JSON line; for profiling")
     ap.add_argument("--roofline-rounds", type=int, default=8)
     ap.add_argument("--kernel-only", action="store_true",
                     help="only time the dominant kernel (the fused gate|up matvec over all layers); for profiling")
@@ -407,6 +474,14 @@ def main() -> int:
     ctx = Context(0)
     cus, arch = ctx.device_info()
     log(f"device: {arch}, {cus} CUs")
+    if args.moe_layer:
+        log(json.dumps(moe_layer_leg(ctx, args.moe_layer, args.steps)))
+        ctx.close()
+        return 0
+    if args.smol_only:
+        log(json.dumps(smol_leg(ctx, np.random.default_rng(42), False)))
+        ctx.close()
+        return 0
     if args.moe_only:
         leg = {"granite": (GRANITE_MOE_Q6K, 4, 256, 128, 1.1, 20260202),
                "olmoe": (OLMOE_1B_7B, 8, args.moe_prompt or 1024, args.steps, 1.0, 20260303),
