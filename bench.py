@@ -574,6 +574,9 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(),
+            # not measured in this run: the committed counter summary's figure
+            "traffic_source": f"{os.path.relpath(PMC_SUMMARY, os.path.dirname(os.path.abspath(__file__)))} "
+                              "(rocprofv3 FETCH_SIZE + WRITE_SIZE passes, each scaled by a 256 MiB copy's reading)",
             "avg_launch_us": round(ku_ms * 1e3, 3),
             "algorithmic_bytes_per_launch": ku_bytes,
         },
@@ -616,6 +619,8 @@ def main() -> int:
         out["gguf_load"] = load_leg(ctx)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(model)
+        # vs_baseline stays null: it is reserved for a published number of this metric
+        out["vs_cpu_baseline"] = round(out["value"] / out["cpu_baseline"]["value"], 1)
     print(json.dumps(out), flush=True)
     model.close()
     ctx.close()

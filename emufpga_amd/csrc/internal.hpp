@@ -632,6 +632,10 @@ int emu_lane_major_q6k(emu_ctx *ctx, const uint8_t *src, size_t nblocks, uint8_t
 // workspace lives in the context and grows on demand (hipMalloc); callers
 // that capture graphs reserve it beforehand with emu_mfma_reserve.
 bool emu_mfma_supports(int encoding, int cols, int n_tok);
+// The same shapes at any token count 1..8 (the chained MoE step runs a single
+// client on the matrix cores too, so that a client's bits do not depend on
+// how many share the step).
+bool emu_mfma_shape_ok(int encoding, int cols);
 size_t emu_mfma_workspace_bytes(int rows, int cols, int nmat);
 int emu_mfma_reserve(emu_ctx *ctx, size_t bytes);
 int emu_launch_mfma(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int *key_slots);

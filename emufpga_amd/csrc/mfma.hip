@@ -540,6 +540,13 @@ int emu_mfma_reserve(emu_ctx *ctx, size_t bytes)
     return EMU_OK;
 }
 
+bool emu_mfma_shape_ok(int encoding, int cols)
+{
+    if (mfma_disabled()) return false;
+    return encoding == EMU_ENC_Q6_K && cols > 0 && (cols % kSlice == 0 || (cols % 256 == 0 && cols >= 2048)) &&
+           (cols + kSlice - 1) / kSlice <= kMaxSlices && cols <= 8 * kLinkThreads * kLinkPairs;
+}
+
 bool emu_mfma_supports(int encoding, int cols, int n_tok)
 {
     if (mfma_disabled()) return false;
@@ -592,7 +599,8 @@ int emu_mfma_link(emu_ctx *ctx, const EmuMfmaLink &l)
 
 int emu_mfma_matvec(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int *part_nks)
 {
-    if (!emu_mfma_supports(EMU_ENC_Q6_K, q.cols, n_tok) || q.cols > cols_cap || q.rows <= 0) return EMU_E_CONFIG;
+    if (n_tok < 1 || n_tok > kMaxTok || !emu_mfma_shape_ok(EMU_ENC_Q6_K, q.cols) || q.cols > cols_cap || q.rows <= 0)
+        return EMU_E_CONFIG;
     const int nmat = q.w_up ? 2 : 1;
     const Ws w = workspace(ctx, cols_cap);
     if (!ctx->mfma_ws || part_bytes(q.rows, q.cols, nmat) > w.part_bytes) return EMU_E_CONFIG;
@@ -652,7 +660,7 @@ void emu_mfma_buffers(emu_ctx *ctx, int cols_cap, uint8_t **xa, float **xs, floa
 
 int emu_launch_mfma(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int *key_slots)
 {
-    if (!emu_mfma_supports(encoding, a.cols, n_tok)) return EMU_E_UNSUPPORTED;
+    if (n_tok < 1 || n_tok > kMaxTok || !emu_mfma_shape_ok(encoding, a.cols)) return EMU_E_UNSUPPORTED;
     if (a.rows <= 0) return EMU_E_ARG;
     const int nmat = a.w_up ? 2 : 1;
     if (nmat == 2 && a.accumulate) return EMU_E_ARG; // the fused entry point never asks for this

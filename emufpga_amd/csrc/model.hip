@@ -751,8 +751,8 @@ bool moe_chain(const emu_model *m, uint32_t n)
 {
     const emu_model_config &c = m->cfg;
     const int QW = (int)(c.heads * c.head_dim);
-    return m->moe() && n >= 2 && moe_gate_fits(m) && emu_mfma_supports(c.encoding, (int)c.hidden, (int)n) &&
-           emu_mfma_supports(c.encoding, QW, (int)n) && QW % 16 == 0;
+    return m->moe() && n >= 1 && n <= 8 && moe_gate_fits(m) && emu_mfma_shape_ok(c.encoding, (int)c.hidden) &&
+           emu_mfma_shape_ok(c.encoding, QW) && QW % 16 == 0;
 }
 
 size_t moe_chain_bytes(const emu_model *m)
@@ -956,7 +956,11 @@ int run_moe(emu_session *s)
     out.out_div = c.logit_div;
     out.softcap = c.logit_softcap;
     int slots = 0;
-    if ((st = emu_launch_qmv(ctx, c.encoding, out, n, &slots)) != EMU_OK) return st;
+    // chained: the output on the matrix cores at any client count, as the
+    // projections before it (a client's logits do not depend on the batch)
+    if ((st = chain ? emu_launch_mfma(ctx, c.encoding, out, n, &slots) : emu_launch_qmv(ctx, c.encoding, out, n, &slots)) !=
+        EMU_OK)
+        return st;
     return launch_finalize(s, slots);
 }
 
@@ -1617,6 +1621,10 @@ extern "C" int emu_session_create(emu_model *m, uint32_t n_clients, uint32_t con
                 const size_t b = emu_mfma_workspace_bytes(sh[0], sh[1], sh[2]);
                 ws = b > ws ? b : ws;
             }
+        if (moe_chain(m, n_clients)) { // the output matvec runs on the matrix cores at any client count
+            const size_t b = emu_mfma_workspace_bytes((int)c.vocab, (int)c.hidden, 1);
+            ws = b > ws ? b : ws;
+        }
         if (ws) st = emu_mfma_reserve(ctx, ws);
     }
     if (st == EMU_OK) st = emu_session_reset(s);

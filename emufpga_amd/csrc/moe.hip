@@ -1217,10 +1217,12 @@ bool mma_enabled()
 }
 
 // Wavefronts per tile: enough shares of the spans for about 2048 wavefronts
-// over the experts the step can route to.
+// over the experts eight tokens can route to.  It depends on the layer's
+// shape only, not on the token count, so that a token's sums are added in the
+// same order whichever tokens share the call.
 int mma_shares(const MoeArgs &a, int tiles, int spans)
 {
-    const int active = a.n_tok * a.k < a.n_experts ? a.n_tok * a.k : a.n_experts;
+    const int active = kMaxTok * a.k < a.n_experts ? kMaxTok * a.k : a.n_experts;
     int ks = 1;
     while (ks < kWaves && 2 * ks <= spans && active * tiles * ks < 2048) ks *= 2;
     return ks;

@@ -78,6 +78,27 @@ def test_moe_batched_client_gets_what_it_would_alone(ctx):  # spm-batch/tests/ba
         assert np.array_equal(alone[0], together[c])
 
 
+def test_granite_shape_batched_client_gets_what_it_would_alone(ctx):  # spm-batch/tests/batching.rs:128-145
+    """At the Granite width (1024) one client takes the same chained
+    matrix-core step as two or four together -- q|k|v, o, the experts and the
+    output on the int8 matrix cores, the expert sums joining the residual in
+    the next layer's link -- so its logits and tokens are the same bits."""
+    model = Model(ctx, DenseConfig(**{**GRANITE_MOE_Q6K.__dict__, "layers": 3}))
+    model.synth(31)
+    rng = np.random.default_rng(4)
+    prompts = rng.integers(0, GRANITE_MOE_Q6K.vocab, size=(4, 6)).astype(np.uint32)
+    alone = [Session(model, 1, 64).generate(prompts[c:c + 1], 12)[0] for c in range(4)]
+    for n in (2, 4):
+        together = Session(model, n, 64).generate(prompts[:n], 12)
+        for c in range(n):
+            assert np.array_equal(together[c], alone[c]), (n, c)
+    toks = prompts[:, 0].copy()
+    _, l4 = Session(model, 4, 16).decode_step(toks, want_logits=True)
+    for c in range(4):
+        _, l1 = Session(model, 1, 16).decode_step(toks[c:c + 1], want_logits=True)
+        assert np.array_equal(l1[0].view(np.uint32), l4[c].view(np.uint32)), c
+
+
 @pytest.mark.parametrize("n_clients", [2, 4])
 def test_granite_shape_decodes_and_matches_oracle(ctx, n_clients):
     """The Granite shape itself (24 layers cut to 2 for the oracle's speed):
