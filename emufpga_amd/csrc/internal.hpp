@@ -14,6 +14,7 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 #include <stddef.h>
+#include <type_traits>
 
 #include "../../include/emuhip.h"
 
@@ -454,62 +455,94 @@ __device__ __forceinline__ float emu_block_sum(float v, float *red)
 
 __device__ __forceinline__ uint64_t emu_wave_max_u64(uint64_t k)
 {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const uint64_t o = __shfl_xor(k, off, EMU_WAVE);
-        k = o > k ? o : k;
-    }
+    auto step = [](uint64_t v, auto off) {
+        constexpr int OFF = decltype(off)::value;
+        const uint32_t lo = __float_as_uint(emu_xor_get<OFF>(__uint_as_float((uint32_t)v)));
+        const uint32_t hi = __float_as_uint(emu_xor_get<OFF>(__uint_as_float((uint32_t)(v >> 32))));
+        const uint64_t o = ((uint64_t)hi << 32) | lo;
+        return o > v ? o : v;
+    };
+    k = step(k, std::integral_constant<int, 32>{});
+    k = step(k, std::integral_constant<int, 16>{});
+    k = step(k, std::integral_constant<int, 8>{});
+    k = step(k, std::integral_constant<int, 4>{});
+    k = step(k, std::integral_constant<int, 2>{});
+    k = step(k, std::integral_constant<int, 1>{});
     return k;
 }
 
-// Router softmax and top-k of one token (moe::route, spm-granite-moe/src/moe.rs:17-35):
-// p[0..n_experts) holds the logits in LDS and is overwritten; sel holds k
-// floats of LDS.  Softmax with the max subtracted, the sum a left fold in
-// expert order, then the k greatest probabilities in total order, lower id
-// first on ties, in that order (k rounds of argmax with the winner removed);
-// weights are the selected probabilities over their left-fold total.  Every thread of the workgroup calls it (it holds
-// the workgroup barriers); wavefront 0 does the work.
-__device__ __forceinline__ void emu_route_token(float *p, float *sel, int n_experts, int k, int32_t *ids,
-                                                float *weights)
+// v[j] of a four-entry register array at a wavefront-uniform j (selects, so
+// the array stays in registers).
+__device__ __forceinline__ float emu_pick4(const float (&v)[4], int j)
 {
+    return j == 0 ? v[0] : j == 1 ? v[1] : j == 2 ? v[2] : v[3];
+}
+
+// Router softmax and top-k of one token (moe::route, spm-granite-moe/src/moe.rs:17-35),
+// by one wavefront (threads past the first wavefront return at once; no
+// barrier inside): p[0..n_experts) holds the logits (n_experts <= 256,
+// k <= 64), lane l keeping experts l, l + 64, ... in registers.  Softmax with
+// the max subtracted, the sum a left fold in expert order (lane by lane,
+// v_readlane); then k rounds of argmax in total order, lower id first on
+// ties, with the winner removed; weights are the selected probabilities
+// over their left-fold total, in selection order.
+__device__ __forceinline__ void emu_route_token(const float *p, int n_experts, int k, int32_t *ids, float *weights)
+{
+    if (threadIdx.x >= EMU_WAVE) return;
     const int lane = threadIdx.x;
-    const bool w0 = threadIdx.x < EMU_WAVE;
-    if (w0) {
-        float m = -INFINITY;
-        for (int e = lane; e < n_experts; e += EMU_WAVE) m = fmaxf(m, p[e]);
-        m = emu_wave_reduce(m, [](float x, float y) { return fmaxf(x, y); });
-        for (int e = lane; e < n_experts; e += EMU_WAVE) p[e] = expf(p[e] - m);
+    float v[4];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + EMU_WAVE * j;
+        v[j] = e < n_experts ? p[e] : -INFINITY;
+        m = fmaxf(m, v[j]);
     }
-    __syncthreads();
-    if (w0) {
-        // lane 0's reads are complete before the shuffle hands the sum out,
-        // so the wavefront may overwrite p after it
-        float sum = 0.0f;
-        if (lane == 0)
-            for (int e = 0; e < n_experts; ++e) sum = __fadd_rn(sum, p[e]);
-        sum = __shfl(sum, 0, EMU_WAVE);
-        for (int e = lane; e < n_experts; e += EMU_WAVE) p[e] = p[e] / sum;
+    m = emu_wave_reduce(m, [](float x, float y) { return fmaxf(x, y); });
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = lane + EMU_WAVE * j < n_experts ? expf(v[j] - m) : 0.0f;
+    // the fold over experts 0, 1, ...: entries past n_experts are +0.0 and
+    // leave the (non-negative) sum unchanged
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (EMU_WAVE * j >= n_experts) break; // uniform
+        const int bits = __float_as_int(v[j]);
+#pragma unroll
+        for (int l = 0; l < EMU_WAVE; ++l) sum = __fadd_rn(sum, __int_as_float(__builtin_amdgcn_readlane(bits, l)));
     }
-    __syncthreads();
-    // The k rounds of (greatest, lowest id) with the winner removed are the
-    // first k places of one ranking: expert e's place is the number of
-    // experts with a greater key (keys are distinct), computed in one pass.
-    if (w0) {
-        for (int e = lane; e < n_experts; e += EMU_WAVE) {
-            const uint64_t ke = emu_select_key(p[e], (uint32_t)e, 0);
-            int rank = 0;
-            for (int j = 0; j < n_experts; ++j) rank += emu_select_key(p[j], (uint32_t)j, 0) > ke ? 1 : 0;
-            if (rank < k) {
-                ids[rank] = e;
-                sel[rank] = p[e];
-            }
+    uint64_t key[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int e = lane + EMU_WAVE * j;
+        v[j] = v[j] / sum;
+        key[j] = e < n_experts ? emu_select_key(v[j], (uint32_t)e, 0) : 0; // every live key is > 0
+    }
+    float my_sel = 0.0f;
+    int my_id = 0;
+    for (int r = 0; r < k; ++r) {
+        uint64_t best = key[0];
+#pragma unroll
+        for (int j = 1; j < 4; ++j) best = key[j] > best ? key[j] : best;
+        best = emu_wave_max_u64(best);
+        const int e = __builtin_amdgcn_readfirstlane((int)emu_key_index(best, 0));
+        const int wl = e & (EMU_WAVE - 1), wj = e / EMU_WAVE;
+        const float pe = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(emu_pick4(v, wj)), wl));
+        if (lane == wl) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (j == wj) key[j] = 0;
+        }
+        if (lane == r) {
+            my_sel = pe;
+            my_id = e;
         }
     }
-    __syncthreads();
-    if (lane == 0) {
-        float total = 0.0f;
-        for (int r = 0; r < k; ++r) total = __fadd_rn(total, sel[r]);
-        for (int r = 0; r < k; ++r) weights[r] = sel[r] / total;
+    float total = 0.0f;
+    for (int r = 0; r < k; ++r) total = __fadd_rn(total, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_sel), r)));
+    if (lane < k) {
+        ids[lane] = my_id;
+        weights[lane] = my_sel / total;
     }
 }
 

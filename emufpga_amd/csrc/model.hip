@@ -89,7 +89,8 @@ struct emu_session {
     // expert output, and the selected-expert FFN's workspace
     float *xn = nullptr, *rlog = nullptr, *rwts = nullptr;
     // Gemma form: the router's input and the global layers' RoPE table
-    float *rin = nullptr, *rope2 = nullptr;
+    float *rope2 = nullptr;
+    uint32_t *gate_counters = nullptr; // [client] arrivals at the MoE gate
     // Zipf routing for throughput runs and the device route trace
     // ([capacity][layer][client][k] ids and weights, slot = step % capacity)
     float zipf_s = 0.0f;
@@ -317,137 +318,178 @@ __global__ __launch_bounds__(kThreads) void synth_f32_kernel(float *dst, size_t 
 }
 
 // --------------------------------------------------------- step kernels --
-// Router logits of every client (spm-granite-moe/src/moe.rs:132-138, an M1
-// matvec of the f32 router): one wavefront per (expert, client).
-__global__ __launch_bounds__(EMU_WAVE) void router_kernel(const float *w, const float *x, int width, int experts,
-                                                           float *logits, ZipfRoute z)
-{
-    const int e = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
-    const float *row = w + (size_t)e * width;
-    const float *xc = x + (size_t)c * width;
-    float acc = 0.0f;
-    for (int i = 4 * lane; i < width; i += 4 * EMU_WAVE) {
-        const float4 a = *reinterpret_cast<const float4 *>(row + i);
-        const float4 b = *reinterpret_cast<const float4 *>(xc + i);
-        acc = __builtin_fmaf(a.x, b.x, acc);
-        acc = __builtin_fmaf(a.y, b.y, acc);
-        acc = __builtin_fmaf(a.z, b.z, acc);
-        acc = __builtin_fmaf(a.w, b.w, acc);
-    }
-    acc = wave_sum(acc);
-    if (lane == 0) logits[(size_t)c * experts + e] = z.s > 0.0f ? zipf_logit(z, c, e) : acc;
-}
-
 // Tokens per partial-sum block of the multi-token matvec ([slice][matrix]
 // [8 tokens][rows]).
 constexpr int kMaxTokChain = 8;
 
-// The MoE layer's gate, one workgroup per client: the FFN RMSNorm of the
-// residual stream (the arithmetic of rms_norm_kernel, kept for the experts),
-// the f32 router logits (router_kernel's per-lane order: lane l folds columns
-// 4l + 256q, q = 0..NK-1, then a butterfly; the normalised row read from
-// LDS) and the softmax / top-k route (moe.rs:17-35, 132-138).  A wavefront
-// takes experts w, w + 4, ...; every router load of a batch of up to eight
-// experts is issued before the first fma.
-template <int NK>
-__global__ __launch_bounds__(kThreads) void moe_gate_kernel(const float *state, const float *gain, const float *router,
-                                                            int experts, int k, float eps, float *xn, int32_t *ids,
-                                                            float *weights, float *state_out, const float *opart,
-                                                            int o_nks, float o_scale, ZipfRoute z)
+// The MoE layer's gate (moe.rs:17-35, 132-138), in both forms:
+//   Granite / OLMoE  router input = expert input = RMSNorm(r) * ffn_norm
+//   Gemma            router input = (r * rscale) * (q / sqrt(W)),
+//                    expert input = (r * q) * pre_ffw_norm_2,
+//                    q = 1 / sqrt(sum r^2 / W + 1e-6)   (gemma_smoke.rs:57-86)
+struct GateArgs {
+    const float *state;  // [client][width] residual
+    const float *gain;   // ffn_norm (Gemma: pre_ffw_norm_2)
+    const float *rscale; // Gemma: the router input scale; else null
+    const float *router; // [experts][width] f32
+    const float *opart;  // chained: the o projection's partial sums; else null
+    int o_nks;
+    float o_scale;
+    int width, experts, k;
+    float eps;
+    float *xn;           // [client][width] expert input
+    float *state_out;    // chained: r + o * o_scale
+    float *logits;       // [client][experts] hand-off between workgroups
+    uint32_t *counters;  // [client] arrivals, zero between launches
+    int32_t *ids;
+    float *weights;
+    ZipfRoute z;
+};
+
+// Grid (expert groups of four, clients), one wavefront per (expert, client):
+// lane l holds columns 4l + 256q (q < NQ) of the client's residual row and
+// of the expert's router row, all loaded before the first use.  Every
+// wavefront of a client forms the same row (the same instructions on the
+// same data: the sum of squares folded per lane in column order, then a
+// butterfly) and dots it with its router row (fma per lane in column order,
+// then a butterfly); the logit goes to the device-coherent level by an
+// agent-scope store, every store completes before the arrival counter
+// moves, and the client's last workgroup to arrive routes (wavefront 0:
+// softmax and top-k over the logits read back by agent-scope loads) while
+// wavefront 1 writes the expert input, and chained the updated residual,
+// and resets the counter.  No other workgroup of the client writes the
+// residual, so all of them read it whole.
+template <int NQ, bool GEMMA>
+__global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)
 {
-    constexpr int width = NK * 4 * EMU_WAVE;
-    constexpr int EB = 32 / NK < 8 ? 32 / NK : 8; // experts per load batch
     constexpr int NW = kThreads / EMU_WAVE;
-    __shared__ __align__(16) float xs[width];
-    __shared__ float red[NW];
     __shared__ float p[256];
-    __shared__ float sel[64];
-    const int c = blockIdx.x, tid = threadIdx.x, lane = tid & (EMU_WAVE - 1), w = tid / EMU_WAVE;
-    float4 rw[EB][NK];
-    auto load_batch = [&](int e0) {
-#pragma unroll
-        for (int j = 0; j < EB; ++j) {
-            int e = e0 + NW * j;
-            e = e < experts ? e : experts - 1; // a valid row; its result is dropped
-            const float *row = router + (size_t)e * width + 4 * lane;
-#pragma unroll
-            for (int q = 0; q < NK; ++q) rw[j][q] = *reinterpret_cast<const float4 *>(row + 4 * EMU_WAVE * q);
-        }
+    __shared__ uint32_t arrived;
+    const int c = blockIdx.y, tid = threadIdx.x, lane = tid & (EMU_WAVE - 1), w = tid / EMU_WAVE;
+    const int W = a.width, E = a.experts;
+    const int e = NW * blockIdx.x + w;
+    const float *xr = a.state + (size_t)c * W;
+    const float *rr = a.router + (size_t)(e < E ? e : E - 1) * W; // a valid row; its result is dropped
+    auto ld = [&](const float *base, int q) {
+        const int i = 4 * lane + 4 * EMU_WAVE * q;
+        return i < W ? *reinterpret_cast<const float4 *>(base + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     };
-    // The residual row and gains load first, then the router rows: loads
-    // complete in issue order, so the norm finishes under the router's loads
-    // instead of after them.
-    // With opart (the chained step) the o projection's partial sums, its
-    // slices added in order, first join the residual as r + v * o_scale
-    // (what the matvec's finishing pass would do), and the row is written
-    // back for the expert sum to add to.
-    constexpr int PT = width / kThreads; // values per thread
-    const float *xr = state + (size_t)c * width;
-    float xv0[PT], gv0[PT], ov0[PT];
-    const float *op = opart ? opart + (size_t)c * width : xr; // a valid source either way
+    float4 x[NQ], rw[NQ], sc[NQ], ov[NQ];
+    const bool chained = !GEMMA && a.opart;
 #pragma unroll
-    for (int j = 0; j < PT; ++j) {
-        xv0[j] = xr[tid + j * kThreads];
-        gv0[j] = gain[tid + j * kThreads];
-        ov0[j] = op[tid + j * kThreads];
+    for (int q = 0; q < NQ; ++q) x[q] = ld(xr, q);
+    if (chained) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) ov[q] = ld(a.opart + (size_t)c * W, q);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    load_batch(w); // the router rows do not wait for the norm
-    __builtin_amdgcn_sched_barrier(0);
-    if (opart) {
-        const size_t stride = (size_t)kMaxTokChain * width; // floats between slices
 #pragma unroll
-        for (int j = 0; j < PT; ++j) {
-            float v = ov0[j];
-            for (int q = 1; q < o_nks; ++q) v += op[q * stride + tid + j * kThreads];
-            xv0[j] = emu_resid_add(xv0[j], v, o_scale);
-            state_out[(size_t)c * width + tid + j * kThreads] = xv0[j];
-        }
-    }
-    float s = 0.0f;
+    for (int q = 0; q < NQ; ++q) rw[q] = ld(rr, q);
 #pragma unroll
-    for (int j = 0; j < PT; ++j) s = __builtin_fmaf(xv0[j], xv0[j], s);
-    s = emu_block_sum(s, red);
-    const float scale = 1.0f / sqrtf(s / (float)width + eps);
+    for (int q = 0; q < NQ; ++q) sc[q] = ld(GEMMA ? a.rscale : a.gain, q);
+    if (chained) {
+        // the o projection's slices added in order, then r + v * o_scale
+        // (what the matvec's finishing pass would do)
+        const size_t stride = (size_t)kMaxTokChain * W; // floats between slices
+        for (int s = 1; s < a.o_nks; ++s) {
 #pragma unroll
-    for (int j = 0; j < PT; ++j) {
-        const int i = tid + j * kThreads;
-        const float v = __fmul_rn(__fmul_rn(xv0[j], scale), gv0[j]);
-        xs[i] = v;
-        xn[(size_t)c * width + i] = v;
-    }
-    __syncthreads();
-    float4 xv[NK];
-#pragma unroll
-    for (int q = 0; q < NK; ++q) xv[q] = *reinterpret_cast<const float4 *>(xs + 4 * lane + 4 * EMU_WAVE * q);
-    for (int e0 = w; e0 < experts; e0 += NW * EB) {
-        float dots[EB];
-#pragma unroll
-        for (int j = 0; j < EB; ++j) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int q = 0; q < NK; ++q) {
-                acc = __builtin_fmaf(rw[j][q].x, xv[q].x, acc);
-                acc = __builtin_fmaf(rw[j][q].y, xv[q].y, acc);
-                acc = __builtin_fmaf(rw[j][q].z, xv[q].z, acc);
-                acc = __builtin_fmaf(rw[j][q].w, xv[q].w, acc);
+            for (int q = 0; q < NQ; ++q) {
+                const float4 t = ld(a.opart + s * stride + (size_t)c * W, q);
+                ov[q].x += t.x;
+                ov[q].y += t.y;
+                ov[q].z += t.z;
+                ov[q].w += t.w;
             }
-            dots[j] = acc;
         }
-        if (e0 + NW * EB < experts) load_batch(e0 + NW * EB);
 #pragma unroll
-        for (int j = 0; j < EB; ++j) {
-            const float acc = wave_sum(dots[j]);
-            const int e = e0 + NW * j;
-            if (lane == 0 && e < experts) p[e] = acc;
+        for (int q = 0; q < NQ; ++q) {
+            x[q].x = emu_resid_add(x[q].x, ov[q].x, a.o_scale);
+            x[q].y = emu_resid_add(x[q].y, ov[q].y, a.o_scale);
+            x[q].z = emu_resid_add(x[q].z, ov[q].z, a.o_scale);
+            x[q].w = emu_resid_add(x[q].w, ov[q].w, a.o_scale);
         }
     }
-    __syncthreads();
-    if (z.s > 0.0f) { // throughput runs: Zipf routing in place of the router's logits
-        for (int e = tid; e < experts; e += kThreads) p[e] = zipf_logit(z, c, e);
-        __syncthreads();
+    float ss = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        ss = __builtin_fmaf(x[q].x, x[q].x, ss);
+        ss = __builtin_fmaf(x[q].y, x[q].y, ss);
+        ss = __builtin_fmaf(x[q].z, x[q].z, ss);
+        ss = __builtin_fmaf(x[q].w, x[q].w, ss);
     }
-    emu_route_token(p, sel, experts, k, ids + (size_t)c * k, weights + (size_t)c * k);
+    ss = wave_sum(ss);
+    const float scale = 1.0f / sqrtf(ss / (float)W + (GEMMA ? 1e-6f : a.eps));
+    const float qr = GEMMA ? scale / sqrtf((float)W) : scale;
+    // router input: Gemma (r * rscale) * qr, else (r * scale) * gain
+    auto rin = [&](float v, float s) { return GEMMA ? __fmul_rn(__fmul_rn(v, s), qr) : __fmul_rn(__fmul_rn(v, scale), s); };
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        acc = __builtin_fmaf(rw[q].x, rin(x[q].x, sc[q].x), acc);
+        acc = __builtin_fmaf(rw[q].y, rin(x[q].y, sc[q].y), acc);
+        acc = __builtin_fmaf(rw[q].z, rin(x[q].z, sc[q].z), acc);
+        acc = __builtin_fmaf(rw[q].w, rin(x[q].w, sc[q].w), acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0 && e < E) {
+        // throughput runs: Zipf routing in place of the router's logit
+        const float lg = a.z.s > 0.0f ? zipf_logit(a.z, c, e) : acc;
+        __hip_atomic_store(a.logits + (size_t)c * E + e, lg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    uint32_t *counter = a.counters + c;
+    if (tid == 0) arrived = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrived != gridDim.x - 1) return;
+    for (int j = tid; j < E; j += kThreads)
+        p[j] = __hip_atomic_load(a.logits + (size_t)c * E + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (w == 0) {
+        emu_route_token(p, E, a.k, a.ids + (size_t)c * a.k, a.weights + (size_t)c * a.k);
+    } else if (w == 1) {
+        float4 g[NQ];
+        if constexpr (GEMMA) {
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) g[q] = ld(a.gain, q);
+        }
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int i = 4 * lane + 4 * EMU_WAVE * q;
+            if (i >= W) continue;
+            float4 v;
+            if constexpr (GEMMA) { // (r * q) * gain2
+                v.x = __fmul_rn(__fmul_rn(x[q].x, scale), g[q].x);
+                v.y = __fmul_rn(__fmul_rn(x[q].y, scale), g[q].y);
+                v.z = __fmul_rn(__fmul_rn(x[q].z, scale), g[q].z);
+                v.w = __fmul_rn(__fmul_rn(x[q].w, scale), g[q].w);
+            } else { // the router input is the expert input
+                v.x = rin(x[q].x, sc[q].x);
+                v.y = rin(x[q].y, sc[q].y);
+                v.z = rin(x[q].z, sc[q].z);
+                v.w = rin(x[q].w, sc[q].w);
+            }
+            *reinterpret_cast<float4 *>(a.xn + (size_t)c * W + i) = v;
+            if (chained) *reinterpret_cast<float4 *>(a.state_out + (size_t)c * W + i) = x[q];
+        }
+    } else if (tid == 2 * EMU_WAVE) {
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Launch of the gate: NQ = 256-column groups per row, up to 16 (width 4096).
+template <bool GEMMA> int launch_gate(emu_ctx *ctx, const GateArgs &a, int n)
+{
+    const dim3 grid((unsigned)((a.experts + 3) / 4), (unsigned)n);
+    const int nq = (a.width + 255) / 256;
+    if (nq <= 1) hipLaunchKernelGGL((moe_gate_kernel<1, GEMMA>), grid, dim3(kThreads), 0, ctx->stream, a);
+    else if (nq <= 2) hipLaunchKernelGGL((moe_gate_kernel<2, GEMMA>), grid, dim3(kThreads), 0, ctx->stream, a);
+    else if (nq <= 4) hipLaunchKernelGGL((moe_gate_kernel<4, GEMMA>), grid, dim3(kThreads), 0, ctx->stream, a);
+    else if (nq <= 8) hipLaunchKernelGGL((moe_gate_kernel<8, GEMMA>), grid, dim3(kThreads), 0, ctx->stream, a);
+    else if (nq <= 12) hipLaunchKernelGGL((moe_gate_kernel<12, GEMMA>), grid, dim3(kThreads), 0, ctx->stream, a);
+    else if (nq <= 16) hipLaunchKernelGGL((moe_gate_kernel<16, GEMMA>), grid, dim3(kThreads), 0, ctx->stream, a);
+    else return EMU_E_CONFIG;
+    EMU_LAUNCH_CHECK(ctx);
+    return EMU_OK;
 }
 
 // Copy of one layer's routes into the session's route trace, slot
@@ -711,48 +753,19 @@ int run_chain(emu_session *s)
     return launch_finalize(s, slots);
 }
 
-// The Gemma form's inputs of the router and of the experts, one workgroup per
-// client, from the residual r: with q = 1/sqrt(sum r^2 / W + 1e-6),
-//   rin = (r * rscale) * (q / sqrt(W))   (gemma_smoke.rs:57-86)
-//   xe  = (r * q) * gain2                (math::rms_norm with pre_ffw_norm_2)
-__global__ __launch_bounds__(kThreads) void gemma_route_in_kernel(const float *state, const float *rscale,
-                                                                  const float *gain2, int width, float *rin,
-                                                                  float *xe)
-{
-    __shared__ float red[kThreads / EMU_WAVE];
-    const int c = blockIdx.x;
-    const float *x = state + (size_t)c * width;
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < width; i += kThreads) ss = __builtin_fmaf(x[i], x[i], ss);
-    ss = emu_block_sum(ss, red);
-    const float q = 1.0f / sqrtf(ss / (float)width + 1e-6f);
-    const float qr = q / sqrtf((float)width);
-    for (int i = threadIdx.x; i < width; i += kThreads) {
-        const float v = x[i];
-        rin[(size_t)c * width + i] = __fmul_rn(__fmul_rn(v, rscale[i]), qr);
-        xe[(size_t)c * width + i] = __fmul_rn(__fmul_rn(v, q), gain2[i]);
-    }
-}
-
 // The layers, output matvec and selection of a mixture-of-experts step
 // (spm-granite-moe/src/model.rs:330-411): attention as in the dense step but
 // with adjacent-pair RoPE and score * score_mul, residual adds r + v * 0.22,
 // then per layer RMSNorm, the f32 router, top-k routing and the selected
 // experts, and logits from the tied embedding divided by logit_div.
-// The fused gate kernel covers widths 1024 and 2048, up to 256 experts and
-// 64 routed.
-bool moe_gate_fits(const emu_model *m)
-{
-    const emu_model_config &c = m->cfg;
-    return (c.hidden == 1024 || c.hidden == 2048) && c.n_experts <= 256 && c.experts_used <= 64;
-}
-
+// The chained step takes the Granite and OLMoE forms at widths 1024 and
+// 2048 (the gate adds the o projection's partial sums to the residual).
 bool moe_chain(const emu_model *m, uint32_t n)
 {
     const emu_model_config &c = m->cfg;
     const int QW = (int)(c.heads * c.head_dim);
-    return m->moe() && n >= 1 && n <= 8 && moe_gate_fits(m) && emu_mfma_shape_ok(c.encoding, (int)c.hidden) &&
-           emu_mfma_shape_ok(c.encoding, QW) && QW % 16 == 0;
+    return m->moe() && !m->gemma() && n >= 1 && n <= 8 && (c.hidden == 1024 || c.hidden == 2048) &&
+           emu_mfma_shape_ok(c.encoding, (int)c.hidden) && emu_mfma_shape_ok(c.encoding, QW) && QW % 16 == 0;
 }
 
 size_t moe_chain_bytes(const emu_model *m)
@@ -859,16 +872,24 @@ int run_moe(emu_session *s)
         o.acc_scale = c.residual_scale;
         if ((st = emu_launch_qmv(ctx, c.encoding, o, n)) != EMU_OK) return st;
         }
+        GateArgs ga{};
+        ga.state = s->state;
+        ga.router = reinterpret_cast<const float *>(lw + m->off_r);
+        ga.width = (int)H;
+        ga.experts = (int)E;
+        ga.k = (int)K;
+        ga.eps = c.eps;
+        ga.xn = s->xn;
+        ga.logits = s->rlog;
+        ga.counters = s->gate_counters;
+        ga.ids = s->rids;
+        ga.weights = s->rwts;
+        ga.z = zr;
         if (m->gemma()) {
             // router and expert inputs from the residual before the shared FFN
-            const float *g2 = reinterpret_cast<const float *>(m->base + m->off_ffn_norm2) + (size_t)layer * H;
-            hipLaunchKernelGGL(gemma_route_in_kernel, dim3((unsigned)n), dim3(kThreads), 0, ctx->stream, s->state,
-                               reinterpret_cast<const float *>(lw + m->off_rs), g2, (int)H, s->rin, s->xn);
-            EMU_LAUNCH_CHECK(ctx);
-            hipLaunchKernelGGL(router_kernel, dim3(E, (unsigned)n), dim3(EMU_WAVE), 0, ctx->stream,
-                               reinterpret_cast<const float *>(lw + m->off_r), s->rin, (int)H, (int)E, s->rlog, zr);
-            EMU_LAUNCH_CHECK(ctx);
-            if ((st = emu_route(ctx, s->rlog, (uint32_t)n, E, K, s->rids, s->rwts)) != EMU_OK) return st;
+            ga.gain = reinterpret_cast<const float *>(m->base + m->off_ffn_norm2) + (size_t)layer * H;
+            ga.rscale = reinterpret_cast<const float *>(lw + m->off_rs);
+            if ((st = launch_gate<true>(ctx, ga, n)) != EMU_OK) return st;
             if (c.shared_ff) {
                 QmvArgs g{};
                 g.w = lw + m->off_sg;
@@ -879,7 +900,7 @@ int run_moe(emu_session *s)
                 g.nb = (int)(H / be);
                 g.x = s->state;
                 g.gain = ffn_norm + (size_t)layer * H;
-                g.eps = c.eps;
+                ga.eps = c.eps;
                 g.y = s->act;
                 g.act = EMU_ACT_GELU_TANH;
                 if ((st = emu_launch_qmv(ctx, c.encoding, g, n)) != EMU_OK) return st;
@@ -895,25 +916,13 @@ int run_moe(emu_session *s)
                 d.acc_scale = c.residual_scale;
                 if ((st = emu_launch_qmv(ctx, c.encoding, d, n)) != EMU_OK) return st;
             }
-        } else if (moe_gate_fits(m)) {
-            const float *gn = ffn_norm + (size_t)layer * H, *rt = reinterpret_cast<const float *>(lw + m->off_r);
-            if (H == 1024)
-                hipLaunchKernelGGL(moe_gate_kernel<4>, dim3((unsigned)n), dim3(kThreads), 0, ctx->stream, s->state, gn,
-                                   rt, (int)E, (int)K, c.eps, s->xn, s->rids, s->rwts, s->state, opart, o_nks,
-                                   c.residual_scale, zr);
-            else
-                hipLaunchKernelGGL(moe_gate_kernel<8>, dim3((unsigned)n), dim3(kThreads), 0, ctx->stream, s->state, gn,
-                                   rt, (int)E, (int)K, c.eps, s->xn, s->rids, s->rwts, s->state, opart, o_nks,
-                                   c.residual_scale, zr);
-            EMU_LAUNCH_CHECK(ctx);
         } else {
-            if ((st = emu_rms_norm(ctx, s->state, ffn_norm + (size_t)layer * H, (uint32_t)n, H, c.eps, s->xn)) !=
-                EMU_OK)
-                return st;
-            hipLaunchKernelGGL(router_kernel, dim3(E, (unsigned)n), dim3(EMU_WAVE), 0, ctx->stream,
-                               reinterpret_cast<const float *>(lw + m->off_r), s->xn, (int)H, (int)E, s->rlog, zr);
-            EMU_LAUNCH_CHECK(ctx);
-            if ((st = emu_route(ctx, s->rlog, (uint32_t)n, E, K, s->rids, s->rwts)) != EMU_OK) return st;
+            ga.gain = ffn_norm + (size_t)layer * H;
+            ga.opart = opart;
+            ga.o_nks = o_nks;
+            ga.o_scale = c.residual_scale;
+            ga.state_out = s->state;
+            if ((st = launch_gate<false>(ctx, ga, n)) != EMU_OK) return st;
         }
         if (s->trace_cap) {
             hipLaunchKernelGGL(trace_routes_kernel, dim3(1), dim3(64), 0, ctx->stream, s->rids, s->rwts, n, (int)K,
@@ -1173,7 +1182,7 @@ extern "C" int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_m
     // selected-expert FFN's limits), the router's rows float4-loadable, the
     // output tied to the embedding (model.rs:403-407).
     if (moe && (c.n_experts == 0 || c.experts_used == 0 || c.experts_used > c.n_experts || c.experts_used > 8 ||
-                c.n_experts > 256 || c.expert_ff == 0 || c.hidden % 8 != 0))
+                c.n_experts > 256 || c.expert_ff == 0 || c.hidden % 8 != 0 || c.hidden > 4096))
         return EMU_E_CONFIG;
     if (!moe && (c.gemma || c.rope_neox)) return EMU_E_CONFIG;
     if (c.gemma && c.window && c.global_every == 0) return EMU_E_CONFIG;
@@ -1581,7 +1590,7 @@ extern "C" int emu_session_create(emu_model *m, uint32_t n_clients, uint32_t con
     alloc((void **)&s->act, sizeof(float) * n_clients * std::max(std::max(c.ffn, c.gemma ? c.shared_ff : 0u), 1u));
     if (m->moe()) {
         alloc((void **)&s->xn, sizeof(float) * n_clients * c.hidden);
-        if (m->gemma()) alloc((void **)&s->rin, sizeof(float) * n_clients * c.hidden);
+        alloc((void **)&s->gate_counters, sizeof(uint32_t) * n_clients);
         alloc((void **)&s->rlog, sizeof(float) * n_clients * c.n_experts);
         alloc((void **)&s->rids, sizeof(int32_t) * n_clients * c.experts_used);
         alloc((void **)&s->rwts, sizeof(float) * n_clients * c.experts_used);
@@ -1607,6 +1616,7 @@ extern "C" int emu_session_create(emu_model *m, uint32_t n_clients, uint32_t con
         }
     }
     if (st == EMU_OK) st = emu_memset(ctx, s->counters, 0, sizeof(uint32_t) * n_clients * c.kv_heads);
+    if (st == EMU_OK && s->gate_counters) st = emu_memset(ctx, s->gate_counters, 0, sizeof(uint32_t) * n_clients);
     if (st == EMU_OK) {
         // The multi-token matvec's workspace must exist before the step is
         // captured into a graph: size it for every matvec of the step.
@@ -1644,7 +1654,7 @@ extern "C" int emu_session_destroy(emu_session *s)
     if (s->graph) (void)hipGraphDestroy(s->graph);
     void *ptrs[] = {s->k_cache, s->v_cache, s->positions, s->tokens, s->steps, s->last, s->prompt, s->hist,
                     s->ctrl, s->counters, s->state, s->qkv, s->attn, s->act, s->logits, s->keys, s->partial,
-                    s->rope, s->xn, s->rlog, s->rids, s->rwts, s->moe_ws, s->rin, s->rope2, s->trace_ids,
+                    s->rope, s->xn, s->rlog, s->rids, s->rwts, s->moe_ws, s->gate_counters, s->rope2, s->trace_ids,
                     s->trace_w};
     for (void *p : ptrs) emu_free(ctx, p);
     delete s;

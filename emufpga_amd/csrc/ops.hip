@@ -181,12 +181,8 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *x, int width,
 __global__ __launch_bounds__(64) void route_kernel(const float *logits, int n_experts, int k,
                                                    int32_t *ids, float *weights)
 {
-    __shared__ float p[256];
-    __shared__ float sel[64];
     const int t = blockIdx.x;
-    for (int e = threadIdx.x; e < n_experts; e += 64) p[e] = logits[(size_t)t * n_experts + e];
-    __syncthreads();
-    emu_route_token(p, sel, n_experts, k, ids + (size_t)t * k, weights + (size_t)t * k);
+    emu_route_token(logits + (size_t)t * n_experts, n_experts, k, ids + (size_t)t * k, weights + (size_t)t * k);
 }
 
 } // namespace
