@@ -696,6 +696,14 @@ struct EmuMfmaLink {
     const float *m_wts;
     int m_k, m_experts;
     float m_scale;
+    // Mode 0 only, optional, before the expert sum: a dense FFN's down
+    // projection, as the last matvec's d_nks partial-sum slices (one
+    // matrix), joins x as x + v * d_scale.
+    bool d_part;
+    int d_nks;
+    float d_scale;
+    // Mode 2: the gate/up pair's activation (EMU_ACT_SILU or EMU_ACT_GELU_TANH).
+    int act;
 };
 size_t emu_mfma_chain_bytes(int cols_cap, size_t max_part_bytes);
 size_t emu_mfma_part_bytes(int rows, int cols, int nmat);

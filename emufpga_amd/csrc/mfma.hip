@@ -80,6 +80,12 @@ struct LinkArgs {
     const float *m_wts;
     int m_k, m_experts;
     float m_scale;
+    // kLinkInput, optional, before the expert sum: a dense FFN's down
+    // projection (part, d_nks slices of one matrix) joins x as x + v * d_scale.
+    const float *d_part;
+    int d_nks;
+    float d_scale;
+    int act; // kLinkSwiglu: EMU_ACT_SILU or EMU_ACT_GELU_TANH
 };
 
 // A-operand layout: sub-block sb, half kh (columns 8kh..8kh+7 of the
@@ -132,6 +138,17 @@ __global__ __launch_bounds__(kLinkThreads) void mfma_link_kernel(LinkArgs a)
         const int c0 = 8 * p;
         if (a.mode == kLinkInput) {
             ld8f(a.x + (size_t)t * a.cols + c0, v[k]);
+            if (a.d_part) {
+                float dv[8];
+                slice_sum<MAXS>(a.d_part + (size_t)t * a.cols + c0, (size_t)kMaxTok * a.cols, a.d_nks, dv);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[k][e] = emu_resid_add(v[k][e], dv[e], a.d_scale);
+            }
+            if (a.d_part && !a.m_contrib) {
+                float *hp = a.h + (size_t)t * a.cols + c0;
+                *reinterpret_cast<float4 *>(hp) = make_float4(v[k][0], v[k][1], v[k][2], v[k][3]);
+                *reinterpret_cast<float4 *>(hp + 4) = make_float4(v[k][4], v[k][5], v[k][6], v[k][7]);
+            }
             if (a.m_contrib) {
                 int order[8];
                 float w[8];
@@ -162,7 +179,7 @@ __global__ __launch_bounds__(kLinkThreads) void mfma_link_kernel(LinkArgs a)
                 float u[8];
                 slice_sum<MAXS>(pu, stride, a.nks, u);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[k][e] = (v[k][e] / (1.0f + expf(-v[k][e]))) * u[e];
+                for (int e = 0; e < 8; ++e) v[k][e] = emu_glu(v[k][e], u[e], a.act);
             }
             if (a.mode == kLinkResid || a.mode == kLinkPlain) {
                 float *hp = a.h + (size_t)t * a.cols + c0;
@@ -584,12 +601,19 @@ int emu_mfma_link(emu_ctx *ctx, const EmuMfmaLink &l)
     a.m_k = l.m_k;
     a.m_experts = l.m_experts;
     a.m_scale = l.m_scale;
+    a.d_part = l.mode == kLinkInput && l.d_part ? w.part : nullptr;
+    a.d_nks = l.d_nks;
+    a.d_scale = l.d_scale;
+    a.act = l.act;
     if (a.m_contrib && (!a.h || !a.m_ids || !a.m_wts || a.m_k < 1 || a.m_k > 8)) return EMU_E_CONFIG;
+    if (a.d_part && (!a.h || a.d_nks < 1 || a.d_nks > kMaxSlices ||
+                     (size_t)a.d_nks * kMaxTok * (size_t)l.cols * sizeof(float) > w.part_bytes))
+        return EMU_E_CONFIG;
     if (l.from_part && (size_t)a.nks * a.nmat * kMaxTok * (size_t)l.cols * sizeof(float) > w.part_bytes)
         return EMU_E_CONFIG;
     // Without a norm there is no row-wide sum: one workgroup per 4096 columns.
     const int gy = a.gain ? 1 : (l.cols / 8 + kLinkThreads - 1) / kLinkThreads;
-    if (a.nks <= 4)
+    if (a.nks <= 4 && a.d_nks <= 4)
         hipLaunchKernelGGL(mfma_link_kernel<4>, dim3(l.n_tok, gy), dim3(kLinkThreads), 0, ctx->stream, a);
     else
         hipLaunchKernelGGL(mfma_link_kernel<kMaxSlices>, dim3(l.n_tok, gy), dim3(kLinkThreads), 0, ctx->stream, a);

@@ -375,7 +375,7 @@ __global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)
         return i < W ? *reinterpret_cast<const float4 *>(base + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     };
     float4 x[NQ], rw[NQ], sc[NQ], ov[NQ];
-    const bool chained = !GEMMA && a.opart;
+    const bool chained = a.opart != nullptr;
 #pragma unroll
     for (int q = 0; q < NQ; ++q) x[q] = ld(xr, q);
     if (chained) {
@@ -758,21 +758,29 @@ int run_chain(emu_session *s)
 // with adjacent-pair RoPE and score * score_mul, residual adds r + v * 0.22,
 // then per layer RMSNorm, the f32 router, top-k routing and the selected
 // experts, and logits from the tied embedding divided by logit_div.
-// The chained step takes the Granite and OLMoE forms at widths 1024 and
-// 2048 (the gate adds the o projection's partial sums to the residual).
+// The chained step: every projection on the matrix cores (the gate adds
+// the o projection's partial sums to the residual; the Gemma form's shared
+// FFN chains link -> gate|up -> link -> down, its down projection's partial
+// sums joining the residual in the next layer's link).
 bool moe_chain(const emu_model *m, uint32_t n)
 {
     const emu_model_config &c = m->cfg;
     const int QW = (int)(c.heads * c.head_dim);
-    return m->moe() && !m->gemma() && n >= 1 && n <= 8 && (c.hidden == 1024 || c.hidden == 2048) &&
-           emu_mfma_shape_ok(c.encoding, (int)c.hidden) && emu_mfma_shape_ok(c.encoding, QW) && QW % 16 == 0;
+    const bool shared = !m->gemma() || c.shared_ff == 0 ||
+                        (emu_mfma_shape_ok(c.encoding, (int)c.shared_ff) && c.shared_ff <= std::max(c.hidden, (uint32_t)QW));
+    return m->moe() && n >= 1 && n <= 8 && shared && emu_mfma_shape_ok(c.encoding, (int)c.hidden) &&
+           emu_mfma_shape_ok(c.encoding, QW) && QW % 16 == 0;
 }
 
 size_t moe_chain_bytes(const emu_model *m)
 {
     const emu_model_config &c = m->cfg;
     const int H = (int)c.hidden, QW = (int)(c.heads * c.head_dim), KW = (int)(c.kv_heads * c.head_dim);
-    const size_t part = std::max(emu_mfma_part_bytes(QW + 2 * KW, H, 1), emu_mfma_part_bytes(H, QW, 1));
+    size_t part = std::max(emu_mfma_part_bytes(QW + 2 * KW, H, 1), emu_mfma_part_bytes(H, QW, 1));
+    if (m->gemma() && c.shared_ff) {
+        part = std::max(part, emu_mfma_part_bytes((int)c.shared_ff, H, 2));
+        part = std::max(part, emu_mfma_part_bytes(H, (int)c.shared_ff, 1));
+    }
     return emu_mfma_chain_bytes(std::max(H, QW), part);
 }
 
@@ -798,6 +806,7 @@ int run_moe(emu_session *s)
     uint8_t *xa = nullptr;
     float *xs = nullptr, *part = nullptr;
     if (chain) emu_mfma_buffers(ctx, cap, &xa, &xs, &part);
+    int sd_nks = 0; // chained Gemma form: the previous layer's shared down projection, as partial sums
     for (uint32_t layer = 0; layer < c.layers; ++layer) {
         const uint8_t *lw = m->base + m->off_layers + (size_t)layer * m->layer_bytes;
         const float *opart = nullptr;
@@ -813,8 +822,11 @@ int run_moe(emu_session *s)
             l.gain = attn_norm + (size_t)layer * H;
             l.eps = c.eps;
             l.limbs = true;
-            if (layer > 0) { // the previous layer's expert sum joins the residual here
+            if (layer > 0) { // the previous layer's (shared down and) expert sum join the residual here
                 l.h = s->state;
+                l.d_part = sd_nks > 0;
+                l.d_nks = sd_nks;
+                l.d_scale = c.residual_scale;
                 l.m_contrib = emu_moe_contrib(s->moe_ws, (uint32_t)n, K, c.expert_ff);
                 l.m_ids = s->rids;
                 l.m_wts = s->rwts;
@@ -889,8 +901,57 @@ int run_moe(emu_session *s)
             // router and expert inputs from the residual before the shared FFN
             ga.gain = reinterpret_cast<const float *>(m->base + m->off_ffn_norm2) + (size_t)layer * H;
             ga.rscale = reinterpret_cast<const float *>(lw + m->off_rs);
+            ga.opart = opart;
+            ga.o_nks = o_nks;
+            ga.o_scale = c.residual_scale;
+            ga.state_out = s->state;
             if ((st = launch_gate<true>(ctx, ga, n)) != EMU_OK) return st;
-            if (c.shared_ff) {
+            if (c.shared_ff && chain) {
+                // link -> gate|up -> link (GeGLU) -> down; the down's partial
+                // sums join the residual in the next layer's link (the last
+                // layer's here, before the expert sum)
+                EmuMfmaLink li{};
+                li.mode = 0;
+                li.x = s->state;
+                li.cols = (int)H;
+                li.cols_cap = cap;
+                li.n_tok = n;
+                li.gain = ffn_norm + (size_t)layer * H;
+                li.eps = c.eps;
+                li.limbs = true;
+                if ((st = emu_mfma_link(ctx, li)) != EMU_OK) return st;
+                QmvArgs g{};
+                g.w = lw + m->off_sg;
+                g.w_up = lw + m->off_su;
+                g.row_bytes = m->rb_h;
+                g.rows = (int)c.shared_ff;
+                g.cols = (int)H;
+                g.nb = (int)(H / be);
+                int gu_nks = 0;
+                if ((st = emu_mfma_matvec(ctx, g, n, cap, &gu_nks)) != EMU_OK) return st;
+                EmuMfmaLink la{};
+                la.mode = 2; // the gate/up pair's activation
+                la.from_part = true;
+                la.part_nks = gu_nks;
+                la.part_nmat = 2;
+                la.cols = (int)c.shared_ff;
+                la.cols_cap = cap;
+                la.n_tok = n;
+                la.limbs = true;
+                la.act = EMU_ACT_GELU_TANH;
+                if ((st = emu_mfma_link(ctx, la)) != EMU_OK) return st;
+                QmvArgs dq{};
+                dq.w = lw + m->off_sd;
+                dq.row_bytes = m->rb_sf;
+                dq.rows = (int)H;
+                dq.cols = (int)c.shared_ff;
+                dq.nb = (int)(c.shared_ff / be);
+                dq.y = s->state;
+                dq.accumulate = 1;
+                dq.acc_scale = c.residual_scale;
+                if ((st = emu_mfma_matvec(ctx, dq, n, cap, &sd_nks)) != EMU_OK) return st;
+                if (layer + 1 == c.layers && (st = emu_mfma_finish(ctx, dq, n, cap, nullptr)) != EMU_OK) return st;
+            } else if (c.shared_ff) {
                 QmvArgs g{};
                 g.w = lw + m->off_sg;
                 g.w_up = lw + m->off_su;

@@ -233,10 +233,35 @@ def test_gemma_form_matches_oracle(ctx, n_clients):
     run_against_oracle(ctx, small_gemma(), n_clients, 140, 150, 51 + n_clients, gemma_layer_scales)
 
 
+def test_gemma_shape_batched_client_gets_what_it_would_alone(ctx):  # spm-batch/tests/batching.rs:128-145
+    """The Gemma-4-style shape (3 layers): one client takes the same chained
+    matrix-core step as two or four together -- the gate adding o's partial
+    sums, the shared GeGLU FFN chained link -> gate|up -> link -> down, its
+    partial sums and the expert sum joining the residual in the next layer's
+    link (the last layer's finished before the output) -- so its logits and
+    tokens are the same bits."""
+    model = Model(ctx, DenseConfig(**{**GEMMA4_MOE.__dict__, "layers": 3}))
+    model.synth(73)
+    gemma_layer_scales(model)
+    rng = np.random.default_rng(6)
+    prompts = rng.integers(0, GEMMA4_MOE.vocab, size=(4, 5)).astype(np.uint32)
+    alone = [Session(model, 1, 32).generate(prompts[c:c + 1], 8)[0] for c in range(4)]
+    for n in (2, 4):
+        together = Session(model, n, 32).generate(prompts[:n], 8)
+        for c in range(n):
+            assert np.array_equal(together[c], alone[c]), (n, c)
+    toks = prompts[:, 0].copy()
+    _, l4 = Session(model, 4, 16).decode_step(toks, want_logits=True)
+    for c in range(4):
+        _, l1 = Session(model, 1, 16).decode_step(toks[c:c + 1], want_logits=True)
+        assert np.array_equal(l1[0].view(np.uint32), l4[c].view(np.uint32)), c
+
+
 def test_gemma_shape_matches_oracle(ctx):
     """The Gemma-4-style shape (30 layers cut to 2): width 2816, 16 heads /
     8 KV heads of 256, 128 experts of 704 with 8 routed, a shared FFN of
-    2048, the tied 262144-row output soft-capped at 30; two clients."""
+    2048, the tied 262144-row output soft-capped at 30; two clients, on the
+    chained matrix-core step."""
     cfg = DenseConfig(**{**GEMMA4_MOE.__dict__, "layers": 2})
     run_against_oracle(ctx, cfg, 2, 4, 16, 61, gemma_layer_scales)
 
