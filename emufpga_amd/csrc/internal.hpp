@@ -546,6 +546,90 @@ __device__ __forceinline__ void emu_route_token(const float *p, int n_experts, i
     }
 }
 
+// The MoE matrix-core form's limb planes (moe.hip) of n vectors of C
+// 16-column chunks: limbs [vec][C][3][16] int8, then per vector and
+// 256-column span kEmuSpanMeta bytes: the limb sum digits [h, l][limb][16
+// chunks] int8 and, at byte 96, the span's scale (NaN: the span holds an inf
+// or NaN).  A vector v ~= scale * (16384 L0 + 128 L1 + L2) per span.
+constexpr int kEmuChunkBytes = 48;  // three int8 limbs of 16 columns
+constexpr int kEmuSpanChunks = 16;  // 16-column chunks per 256-column span
+constexpr int kEmuSpanMeta = 112;
+struct EmuLimbPlanes {
+    uint8_t *q;
+    uint8_t *dg;
+    int C, ns;
+};
+
+// v * 2^(20 - e2) as three signed 7-bit limbs (|v| < 2^e2).
+__device__ __forceinline__ void emu_limb3(float v, int e2, int (&L)[3])
+{
+    const float s = ldexpf(v, 6 - e2); // exact, |s| < 64
+    const float f0 = rintf(s);
+    const float r1 = (s - f0) * 128.0f; // exact
+    const float f1 = rintf(r1);
+    const float f2 = rintf((r1 - f1) * 128.0f);
+    L[0] = (int)f0;
+    L[1] = (int)f1;
+    L[2] = (int)f2;
+}
+
+// Span `span` of vector `vec` into limb planes by one wavefront whose lane l
+// holds the span's columns 4l..4l+3 (live: inside the row; zero otherwise):
+// the span's largest |v| sets the power-of-two scale, each value splits into
+// three limbs, and each 16-column chunk's limb sums go in as two digits
+// S = 64 h + l (|S| <= 1024).
+__device__ __forceinline__ void emu_span_limbs_wave(float4 v4, bool live, int vec, int span, const EmuLimbPlanes &P)
+{
+    const int lane = threadIdx.x & (EMU_WAVE - 1);
+    const float x[4] = {v4.x, v4.y, v4.z, v4.w};
+    float amax = 0.0f;
+    int bad = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = live ? fabsf(x[i]) : 0.0f;
+        amax = fmaxf(amax, a);
+        bad |= !(a <= 3.402823466e38f);
+    }
+    amax = emu_wave_reduce(amax, [](float p, float q) { return fmaxf(p, q); });
+    const bool finite = __ballot(bad) == 0;
+    int e2 = 0;
+    (void)frexpf(finite ? amax : 0.0f, &e2);
+    uint32_t q[3] = {0u, 0u, 0u};
+    int S[3] = {0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int L[3];
+        emu_limb3(finite && live ? x[i] : 0.0f, e2, L);
+#pragma unroll
+        for (int l = 0; l < 3; ++l) {
+            q[l] |= ((uint32_t)L[l] & 0xffu) << (8 * i);
+            S[l] += L[l];
+        }
+    }
+#pragma unroll
+    for (int l = 0; l < 3; ++l) { // the chunk's 16 columns: lanes 4m..4m+3
+        S[l] += __shfl_xor(S[l], 1, EMU_WAVE);
+        S[l] += __shfl_xor(S[l], 2, EMU_WAVE);
+    }
+    const int m = lane >> 2, c = kEmuSpanChunks * span + m;
+    uint8_t *meta = P.dg + ((size_t)vec * P.ns + span) * kEmuSpanMeta;
+    if ((lane & 3) == 0) {
+#pragma unroll
+        for (int l = 0; l < 3; ++l) {
+            const int h = (S[l] + 32) >> 6; // h in [-16, 16], S - 64h in [-32, 31]
+            meta[16 * l + m] = (uint8_t)h;
+            meta[48 + 16 * l + m] = (uint8_t)(S[l] - 64 * h);
+        }
+    }
+    if (c < P.C) {
+        uint8_t *dst = P.q + ((size_t)vec * P.C + c) * kEmuChunkBytes + 4 * (lane & 3);
+#pragma unroll
+        for (int l = 0; l < 3; ++l) *reinterpret_cast<uint32_t *>(dst + 16 * l) = q[l];
+    }
+    if (lane == 0)
+        *reinterpret_cast<float *>(meta + 96) = finite ? ldexpf(1.0f, e2 - 20) : __int_as_float(0x7fc00000);
+}
+
 // One token's k (<= 8) routes in ascending expert id (ids are distinct;
 // entries past k or outside the expert range are skipped): order[i] is the
 // slot and w[i] its weight; returns how many (moe.rs:37-159 combines in that
@@ -741,8 +825,14 @@ int emu_launch_attn(emu_ctx *ctx, const EmuAttnLaunch &l);
 // state = state + sum * scale with two roundings (moe.hip).
 // With combine false the weighted sum is left for the caller: the expert
 // outputs stay at emu_moe_contrib(workspace, ...) ([token][slot][width]).
+// With x_planes_ready the tokens' limb planes (emu_moe_x_planes) already
+// hold x (the matrix-core form only: see emu_moe_mma_form).
 int emu_moe_ffn_resid(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok, const int32_t *d_ids,
                       const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_state,
-                      float scale, bool combine = true);
+                      float scale, bool combine = true, bool x_planes_ready = false);
 const float *emu_moe_contrib(const void *d_workspace, uint32_t n_tok, uint32_t k, uint32_t ff);
+// Whether the layer takes the matrix-core form, and where its workspace
+// keeps the tokens' limb planes.
+bool emu_moe_mma_form(const emu_moe_desc *d);
+EmuLimbPlanes emu_moe_x_planes(void *d_workspace, uint32_t n_tok, uint32_t k, uint32_t width, uint32_t ff);
 int emu_attn_max_chunks(int context);

@@ -338,6 +338,7 @@ struct GateArgs {
     int width, experts, k;
     float eps;
     float *xn;           // [client][width] expert input
+    EmuLimbPlanes xp;    // and, when xp.q is set, as the experts' limb planes
     float *state_out;    // chained: r + o * o_scale
     float *logits;       // [client][experts] hand-off between workgroups
     uint32_t *counters;  // [client] arrivals, zero between launches
@@ -356,9 +357,10 @@ struct GateArgs {
 // agent-scope store, every store completes before the arrival counter
 // moves, and the client's last workgroup to arrive routes (wavefront 0:
 // softmax and top-k over the logits read back by agent-scope loads) while
-// wavefront 1 writes the expert input, and chained the updated residual,
-// and resets the counter.  No other workgroup of the client writes the
-// residual, so all of them read it whole.
+// wavefront 1 writes the expert input (also as the experts' limb planes)
+// and, chained, the updated residual, and wavefront 2 resets the counter.
+// No other workgroup of the client writes the residual, so all of them read
+// it whole.
 template <int NQ, bool GEMMA>
 __global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)
 {
@@ -447,7 +449,9 @@ __global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)
     if (w == 0) {
         emu_route_token(p, E, a.k, a.ids + (size_t)c * a.k, a.weights + (size_t)c * a.k);
     } else if (w == 1) {
-        float4 g[NQ];
+        float4 g[NQ], xe[NQ];
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) xe[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if constexpr (GEMMA) {
 #pragma unroll
             for (int q = 0; q < NQ; ++q) g[q] = ld(a.gain, q);
@@ -470,6 +474,12 @@ __global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)
             }
             *reinterpret_cast<float4 *>(a.xn + (size_t)c * W + i) = v;
             if (chained) *reinterpret_cast<float4 *>(a.state_out + (size_t)c * W + i) = x[q];
+            xe[q] = v;
+        }
+        if (a.xp.q) { // the experts' limb planes of the expert input, span by span
+#pragma unroll
+            for (int q = 0; q < NQ; ++q)
+                if (4 * EMU_WAVE * q < W) emu_span_limbs_wave(xe[q], 4 * lane + 4 * EMU_WAVE * q < W, c, q, a.xp);
         }
     } else if (tid == 2 * EMU_WAVE) {
         __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -884,7 +894,22 @@ int run_moe(emu_session *s)
         o.acc_scale = c.residual_scale;
         if ((st = emu_launch_qmv(ctx, c.encoding, o, n)) != EMU_OK) return st;
         }
+        emu_moe_desc d{};
+        d.enc_gate_up = c.expert_encoding;
+        d.enc_down = m->gemma() ? c.expert_down_encoding : c.expert_encoding;
+        d.d_gate = lw + m->off_ge;
+        d.d_up = m->gemma() ? nullptr : lw + m->off_ue; // gemma: fused gate|up rows per expert
+        d.d_down = lw + m->off_de;
+        d.d_down_scale = m->gemma() ? reinterpret_cast<const float *>(lw + m->off_ds) : nullptr;
+        d.n_experts = E;
+        d.width = H;
+        d.ff = c.expert_ff;
+        d.k = K;
+        d.act = m->gemma() ? EMU_ACT_GELU_TANH : EMU_ACT_SILU;
+        // the gate writes the experts' limb planes of the expert input
+        const bool planes = emu_moe_mma_form(&d);
         GateArgs ga{};
+        if (planes) ga.xp = emu_moe_x_planes(s->moe_ws, (uint32_t)n, K, H, c.expert_ff);
         ga.state = s->state;
         ga.router = reinterpret_cast<const float *>(lw + m->off_r);
         ga.width = (int)H;
@@ -990,24 +1015,12 @@ int run_moe(emu_session *s)
                                (int)layer, (int)c.layers, s->steps, (int)s->trace_cap, s->trace_ids, s->trace_w);
             EMU_LAUNCH_CHECK(ctx);
         }
-        emu_moe_desc d{};
-        d.enc_gate_up = c.expert_encoding;
-        d.enc_down = m->gemma() ? c.expert_down_encoding : c.expert_encoding;
-        d.d_gate = lw + m->off_ge;
-        d.d_up = m->gemma() ? nullptr : lw + m->off_ue; // gemma: fused gate|up rows per expert
-        d.d_down = lw + m->off_de;
-        d.d_down_scale = m->gemma() ? reinterpret_cast<const float *>(lw + m->off_ds) : nullptr;
-        d.n_experts = E;
-        d.width = H;
-        d.ff = c.expert_ff;
-        d.k = K;
-        d.act = m->gemma() ? EMU_ACT_GELU_TANH : EMU_ACT_SILU;
         // the weighted expert sum lands on the residual stream as add_scaled does
         // chained: the next layer's link adds the expert sum (the last layer's
         // is combined here, for the output matvec)
         const bool combine = !chain || layer + 1 == c.layers;
         if ((st = emu_moe_ffn_resid(ctx, &d, s->xn, (uint32_t)n, s->rids, s->rwts, s->moe_ws, s->moe_ws_bytes,
-                                    s->state, c.residual_scale, combine)) != EMU_OK)
+                                    s->state, c.residual_scale, combine, planes)) != EMU_OK)
             return st;
     }
     QmvArgs out{};

@@ -4,10 +4,11 @@
 //
 // After routing (emu_route: ids and weights, n_tok x k), inputs of up to 4096
 // columns take the matrix-core form (the section "matrix-core form" below):
-//   1. limbs: the tokens' x as int8 limb planes, and the call's list of
-//      routed experts;
-//   2. gate|up on v_mfma_i32_32x32x16_i8, one grid row per listed expert,
-//      writing act(gate) * up per (token, slot);
+//   1. limbs: the tokens' x as int8 limb planes (or the decode step's gate
+//      kernel writes them);
+//   2. gate|up on v_mfma_i32_32x32x16_i8, one grid row per routed expert
+//      (each workgroup reads its expert off the routing table), writing
+//      act(gate) * up per (token, slot);
 //   3. limbs: the activations as limb planes;
 //   4. down on the matrix cores into a per-(token, slot) contribution;
 //   5. combine, as below.
@@ -539,20 +540,13 @@ template <class F> void launch_down(emu_ctx *ctx, const MoeArgs &a)
 // as its MFMA has issued.
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int kChunkBytes = 48; // three int8 limbs of 16 columns
-constexpr int kSpanChunks = 16; // 16-column chunks per 256-column span
-constexpr int kSpanMeta = 112; // per vector and span: digits [h, l][limb][16 chunks] int8, then the scale
+constexpr int kChunkBytes = kEmuChunkBytes; // three int8 limbs of 16 columns
+constexpr int kSpanChunks = kEmuSpanChunks; // 16-column chunks per 256-column span
+constexpr int kSpanMeta = kEmuSpanMeta;     // per vector and span: digits [h, l][limb][16 chunks] int8, then the scale
 constexpr int kMmaMaxCols = 4096;
 
-// Limb planes of n vectors of C chunks: limbs [vec][C][3][16] int8, then per
-// vector and span a kSpanMeta block: the limb sum digits [h, l][limb][16
-// chunks] int8 and, at byte 96, the span's scale (NaN: the span holds an inf
-// or NaN).
-struct LimbPlanes {
-    uint8_t *q;
-    uint8_t *dg;
-    int C, ns;
-};
+// Limb planes of n vectors of C chunks (EmuLimbPlanes).
+using LimbPlanes = EmuLimbPlanes;
 int spans_of(int C) { return (C + kSpanChunks - 1) / kSpanChunks; }
 size_t limb_plane_bytes(size_t n_vec, int C)
 {
@@ -568,56 +562,67 @@ LimbPlanes limb_planes(void *base, size_t n_vec, int C)
     return p;
 }
 
-// v * 2^(20 - e2) as three signed 7-bit limbs (|v| < 2^e2): L[l].
-__device__ __forceinline__ void limb3(float v, int e2, int (&L)[3])
+// OR of a 64-bit value over the wavefront, every lane getting it.
+__device__ __forceinline__ uint64_t wave_or_u64(uint64_t v)
 {
-    const float s = ldexpf(v, 6 - e2); // exact, |s| < 64
-    const float f0 = rintf(s);
-    const float r1 = (s - f0) * 128.0f; // exact
-    const float f1 = rintf(r1);
-    const float f2 = rintf((r1 - f1) * 128.0f);
-    L[0] = (int)f0;
-    L[1] = (int)f1;
-    L[2] = (int)f2;
+    auto step = [](uint64_t x, auto off) {
+        constexpr int OFF = decltype(off)::value;
+        const uint32_t lo = __float_as_uint(emu_xor_get<OFF>(__uint_as_float((uint32_t)x)));
+        const uint32_t hi = __float_as_uint(emu_xor_get<OFF>(__uint_as_float((uint32_t)(x >> 32))));
+        return x | ((uint64_t)hi << 32) | lo;
+    };
+    v = step(v, std::integral_constant<int, 32>{});
+    v = step(v, std::integral_constant<int, 16>{});
+    v = step(v, std::integral_constant<int, 8>{});
+    v = step(v, std::integral_constant<int, 4>{});
+    v = step(v, std::integral_constant<int, 2>{});
+    v = step(v, std::integral_constant<int, 1>{});
+    return v;
 }
 
-// The routed experts of a call, ascending, each with its routing-table
-// entries (t*k + slot, ascending): [0] the count, then kListEntry ints per
-// expert {e, n, -, -, slots[8]}.  The matrix-core launches take one grid row
-// per listed expert, so no workgroup slot is spent on experts nobody chose.
-constexpr int kListEntry = 12;
-size_t expert_list_bytes(int max_experts) { return sizeof(int32_t) * (4 + (size_t)kListEntry * max_experts); }
-
-// One wavefront, lane t holding routing-table entry t: one ballot per expert.
-__device__ void build_expert_list(const int32_t *ids, int nk, int n_experts, int32_t *list)
+// Entry y of the call's routed experts in ascending id, read off the
+// routing table itself (ids[t], t < nk <= 64; a token's ids are distinct, so
+// an expert has at most kMaxTok entries): the expert, its entry count and its
+// entries t in ascending order (0 past the count); false past the last
+// expert.  The matrix-core launches take one grid row per routed expert, so
+// no workgroup slot is spent on experts nobody chose.  Every wavefront forms
+// the same (uniform) result: the present experts as a 256-bit mask (an OR
+// butterfly per 64-bit word), its y-th set bit, one ballot for the entries.
+__device__ __forceinline__ bool list_entry(const int32_t *ids, int nk, int n_experts, int y, int &e, int &cnt,
+                                           int (&slot)[kMaxTok])
 {
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & (EMU_WAVE - 1);
     const int my = lane < nk ? ids[lane] : -1;
-    int n = 0;
-    for (int e = 0; e < n_experts; ++e) { // uniform
-        const uint64_t m = __ballot(my == e);
-        if (m == 0) continue; // uniform
-        int32_t *en = list + 4 + (size_t)n * kListEntry;
-        const int rank = __popcll(m & ((1ull << lane) - 1));
-        if (my == e && rank < kMaxTok) en[4 + rank] = lane;
-        const int c = __popcll(m);
-        if (lane == 0) {
-            en[0] = e;
-            en[1] = c < kMaxTok ? c : kMaxTok;
+    const bool ok = my >= 0 && my < n_experts;
+    int base = 0;
+    e = -1;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint64_t b = wave_or_u64(ok && (my >> 6) == w ? 1ull << (my & 63) : 0ull);
+        const int pc = __popcll(b);
+        if (e < 0 && y < base + pc) { // uniform
+            const int want = y - base; // lane l tests bit l
+            const bool hit = ((b >> lane) & 1ull) && __popcll(b & ((1ull << lane) - 1ull)) == want;
+            e = 64 * w + __ffsll((unsigned long long)__ballot(hit)) - 1;
         }
-        if (lane >= c && lane < kMaxTok) en[4 + lane] = 0;
-        ++n;
+        base += pc;
     }
-    if (lane == 0) list[0] = n;
+    if (e < 0) return false;
+    uint64_t m = __ballot(my == e);
+    const int c = __popcll(m);
+    cnt = c < kMaxTok ? c : kMaxTok;
+#pragma unroll
+    for (int i = 0; i < kMaxTok; ++i) {
+        slot[i] = m ? __ffsll((unsigned long long)m) - 1 : 0;
+        m &= m - 1ull;
+    }
+    return true;
 }
 
 // n_vec vectors of cols floats (row stride cols) into limb planes: sixteen
-// threads per span, one 16-column chunk each.  With a list, the last
-// workgroup's first wavefront also builds the call's expert list.
-__global__ __launch_bounds__(kThreads) void moe_limbs_kernel(const float *x, int n_vec, int cols, LimbPlanes P,
-                                                             const int32_t *ids, int nk, int n_experts, int32_t *list)
+// threads per span, one 16-column chunk each.
+__global__ __launch_bounds__(kThreads) void moe_limbs_kernel(const float *x, int n_vec, int cols, LimbPlanes P)
 {
-    if (list && blockIdx.x == gridDim.x - 1 && threadIdx.x < EMU_WAVE) build_expert_list(ids, nk, n_experts, list);
     const int idx = blockIdx.x * kThreads + threadIdx.x;
     const int total = n_vec * P.ns * kSpanChunks; // whole groups of 16 lanes
     const int i = idx < total ? idx : total - 1;
@@ -649,7 +654,7 @@ __global__ __launch_bounds__(kThreads) void moe_limbs_kernel(const float *x, int
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
         int L[3];
-        limb3(finite && col ? w[e] : 0.0f, e2, L);
+        emu_limb3(finite && col ? w[e] : 0.0f, e2, L);
 #pragma unroll
         for (int l = 0; l < 3; ++l) {
             q[l][e >> 2] |= ((uint32_t)L[l] & 0xffu) << (8 * (e & 3));
@@ -970,7 +975,6 @@ enum { kMmaUp = 0, kMmaDown = 1 };
 
 struct MmaArgs {
     MoeArgs a;
-    const int32_t *list; // the call's expert list
     LimbPlanes in;       // the input vectors: tokens (gate|up) or routes (down)
     int ks;        // wavefronts sharing a tile's spans (1, 2 or 4)
     int tiles;     // tiles per expert
@@ -1102,15 +1106,9 @@ __global__ __launch_bounds__(kThreads, 2) void moe_mma_kernel(MmaArgs g)
     // Grid: x = tile group, fastest, so that consecutive workgroups -- which
     // the dispatcher deals round-robin to the XCDs -- are one expert's tiles
     // and every routed expert's work spreads over all XCDs; y = the expert's
-    // place in the list.
-    // (the entry's address is valid whatever the count: the grid has at
-    // most as many rows as the list has room for)
-    const int32_t *en = g.list + 4 + (size_t)blockIdx.y * kListEntry;
-    const int4 eh = *reinterpret_cast<const int4 *>(en);
-    const int4 sa = *reinterpret_cast<const int4 *>(en + 4), sb = *reinterpret_cast<const int4 *>(en + 8);
-    if ((int)blockIdx.y >= g.list[0]) return; // uniform over the workgroup
-    const int e = eh.x, cnt = eh.y;
-    const int slot[kMaxTok] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
+    // place among the routed experts.
+    int e = 0, cnt = 0, slot[kMaxTok];
+    if (!list_entry(a.ids, a.n_tok * a.k, a.n_experts, (int)blockIdx.y, e, cnt, slot)) return; // uniform
     const int tl = w / ks, kp = w % ks;
     const int tile_raw = blockIdx.x * (kWaves / ks) + tl;
     const int tile = tile_raw < g.tiles ? tile_raw : g.tiles - 1;
@@ -1229,12 +1227,11 @@ int mma_shares(const MoeArgs &a, int tiles, int spans)
 }
 
 template <class F, int KIND, int ACT>
-int launch_mma(emu_ctx *ctx, const MoeArgs &a, const LimbPlanes &in, const int32_t *list)
+int launch_mma(emu_ctx *ctx, const MoeArgs &a, const LimbPlanes &in)
 {
     using M = Mma<F>;
     MmaArgs g;
     g.a = a;
-    g.list = list;
     g.in = in;
     g.tiles = KIND == kMmaUp ? a.ff / 16 : (a.width + 31) / 32;
     g.ks = mma_shares(a, g.tiles, in.ns);
@@ -1247,18 +1244,17 @@ int launch_mma(emu_ctx *ctx, const MoeArgs &a, const LimbPlanes &in, const int32
     return EMU_OK;
 }
 
-template <class F> int launch_mma_up(emu_ctx *ctx, const MoeArgs &a, const LimbPlanes &in, const int32_t *list)
+template <class F> int launch_mma_up(emu_ctx *ctx, const MoeArgs &a, const LimbPlanes &in)
 {
-    if (a.act == EMU_ACT_GELU_TANH) return launch_mma<F, kMmaUp, EMU_ACT_GELU_TANH>(ctx, a, in, list);
-    return launch_mma<F, kMmaUp, EMU_ACT_SILU>(ctx, a, in, list);
+    if (a.act == EMU_ACT_GELU_TANH) return launch_mma<F, kMmaUp, EMU_ACT_GELU_TANH>(ctx, a, in);
+    return launch_mma<F, kMmaUp, EMU_ACT_SILU>(ctx, a, in);
 }
 
-int launch_limbs(emu_ctx *ctx, const float *x, int n_vec, int cols, const LimbPlanes &L, const int32_t *ids = nullptr,
-                 int nk = 0, int n_experts = 0, int32_t *list = nullptr)
+int launch_limbs(emu_ctx *ctx, const float *x, int n_vec, int cols, const LimbPlanes &L)
 {
     const int total = n_vec * L.ns * kSpanChunks;
     hipLaunchKernelGGL(moe_limbs_kernel, dim3((total + kThreads - 1) / kThreads), dim3(kThreads), 0, ctx->stream, x,
-                       n_vec, cols, L, ids, nk, n_experts, list);
+                       n_vec, cols, L);
     EMU_LAUNCH_CHECK(ctx);
     return EMU_OK;
 }
@@ -1272,14 +1268,27 @@ extern "C" size_t emu_moe_workspace_bytes(uint32_t n_tok, uint32_t k, uint32_t w
     const size_t slots = (size_t)n_tok * k;
     return align256(sizeof(float) * slots * ff) + align256(sizeof(float) * slots * width) +
            align256(limb_plane_bytes(n_tok, (int)((width + 15) / 16))) +
-           align256(limb_plane_bytes(slots, (int)((ff + 15) / 16))) + align256(expert_list_bytes((int)slots));
+           align256(limb_plane_bytes(slots, (int)((ff + 15) / 16)));
 }
 
 namespace {
 
+bool mma_form(const emu_moe_desc *d)
+{
+    return mma_enabled() && d->width <= kMmaMaxCols && d->ff <= kMmaMaxCols && d->width % 16 == 0 && d->ff % 16 == 0;
+}
+
+// The workspace: activations, contributions, the tokens' limb planes, the
+// routes' limb planes.
+uint8_t *x_plane_base(void *ws, size_t slots, uint32_t width, uint32_t ff)
+{
+    return static_cast<uint8_t *>(ws) + align256(sizeof(float) * slots * ff) + align256(sizeof(float) * slots * width);
+}
+
 int moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok, const int32_t *d_ids,
             const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_out, float *d_resid,
-            float resid_scale, bool combine = true, const uint8_t *const *d_table = nullptr)
+            float resid_scale, bool combine = true, const uint8_t *const *d_table = nullptr,
+            bool x_planes_ready = false)
 {
     if (!ctx || !d || !d_x || !d_ids || !d_weights || !(d_out || d_resid) || (!d_table && (!d->d_gate || !d->d_down)))
         return EMU_E_ARG;
@@ -1317,33 +1326,30 @@ int moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_to
     a.resid = d_resid;
     a.resid_scale = resid_scale;
     a.table = d_table;
-    if (mma_enabled() && d->width <= kMmaMaxCols && d->ff <= kMmaMaxCols && d->width % 16 == 0 && d->ff % 16 == 0) {
-        // matrix-core form: the tokens' limb planes, gate|up into the
-        // activations, the routes' limb planes, down into the contributions
+    if (mma_form(d)) {
+        // matrix-core form: the tokens' limb planes (unless the caller wrote
+        // them), gate|up into the activations, the routes' limb planes, down
+        // into the contributions
         const int c_in = (int)(d->width / 16), c_ff = (int)(d->ff / 16);
         const size_t slots = (size_t)n_tok * d->k;
-        uint8_t *xp = static_cast<uint8_t *>(d_workspace) + align256(sizeof(float) * slots * d->ff) +
-                      align256(sizeof(float) * slots * d->width);
+        uint8_t *xp = x_plane_base(d_workspace, slots, d->width, d->ff);
         uint8_t *fp = xp + align256(limb_plane_bytes(n_tok, c_in));
-        int32_t *list = reinterpret_cast<int32_t *>(fp + align256(limb_plane_bytes(slots, c_ff)));
         const LimbPlanes lx = limb_planes(xp, n_tok, c_in), lf = limb_planes(fp, slots, c_ff);
-        if ((st = launch_limbs(ctx, d_x, (int)n_tok, (int)d->width, lx, d_ids, (int)slots, (int)d->n_experts,
-                               list)) != EMU_OK)
-            return st;
+        if (!x_planes_ready && (st = launch_limbs(ctx, d_x, (int)n_tok, (int)d->width, lx)) != EMU_OK) return st;
         switch (d->enc_gate_up) {
-        case EMU_ENC_Q6_K: st = launch_mma_up<FmtQ6K>(ctx, a, lx, list); break;
-        case EMU_ENC_Q8_0: st = launch_mma_up<FmtQ8_0>(ctx, a, lx, list); break;
-        case EMU_ENC_Q5_K: st = launch_mma_up<FmtQ5K>(ctx, a, lx, list); break;
-        case EMU_ENC_Q2_K: st = launch_mma_up<FmtQ2K>(ctx, a, lx, list); break;
+        case EMU_ENC_Q6_K: st = launch_mma_up<FmtQ6K>(ctx, a, lx); break;
+        case EMU_ENC_Q8_0: st = launch_mma_up<FmtQ8_0>(ctx, a, lx); break;
+        case EMU_ENC_Q5_K: st = launch_mma_up<FmtQ5K>(ctx, a, lx); break;
+        case EMU_ENC_Q2_K: st = launch_mma_up<FmtQ2K>(ctx, a, lx); break;
         default: return EMU_E_UNSUPPORTED;
         }
         if (st != EMU_OK) return st;
         if ((st = launch_limbs(ctx, a.act_buf, (int)slots, (int)d->ff, lf)) != EMU_OK) return st;
         switch (d->enc_down) {
-        case EMU_ENC_Q6_K: st = launch_mma<FmtQ6K, kMmaDown, 0>(ctx, a, lf, list); break;
-        case EMU_ENC_Q8_0: st = launch_mma<FmtQ8_0, kMmaDown, 0>(ctx, a, lf, list); break;
-        case EMU_ENC_Q5_K: st = launch_mma<FmtQ5K, kMmaDown, 0>(ctx, a, lf, list); break;
-        case EMU_ENC_Q2_K: st = launch_mma<FmtQ2K, kMmaDown, 0>(ctx, a, lf, list); break;
+        case EMU_ENC_Q6_K: st = launch_mma<FmtQ6K, kMmaDown, 0>(ctx, a, lf); break;
+        case EMU_ENC_Q8_0: st = launch_mma<FmtQ8_0, kMmaDown, 0>(ctx, a, lf); break;
+        case EMU_ENC_Q5_K: st = launch_mma<FmtQ5K, kMmaDown, 0>(ctx, a, lf); break;
+        case EMU_ENC_Q2_K: st = launch_mma<FmtQ2K, kMmaDown, 0>(ctx, a, lf); break;
         default: return EMU_E_UNSUPPORTED;
         }
         if (st != EMU_OK) return st;
@@ -1395,11 +1401,18 @@ int emu_moe_ffn_table(emu_ctx *ctx, const emu_moe_desc *d, const uint8_t *const 
 
 int emu_moe_ffn_resid(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok, const int32_t *d_ids,
                       const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_state,
-                      float scale, bool combine)
+                      float scale, bool combine, bool x_planes_ready)
 {
     if (!d_state) return EMU_E_ARG;
     return moe_ffn(ctx, d, d_x, n_tok, d_ids, d_weights, d_workspace, workspace_bytes, nullptr, d_state, scale,
-                   combine);
+                   combine, nullptr, x_planes_ready && mma_form(d));
+}
+
+bool emu_moe_mma_form(const emu_moe_desc *d) { return d && mma_form(d); }
+
+EmuLimbPlanes emu_moe_x_planes(void *d_workspace, uint32_t n_tok, uint32_t k, uint32_t width, uint32_t ff)
+{
+    return limb_planes(x_plane_base(d_workspace, (size_t)n_tok * k, width, ff), n_tok, (int)((width + 15) / 16));
 }
 
 const float *emu_moe_contrib(const void *d_workspace, uint32_t n_tok, uint32_t k, uint32_t ff)
