@@ -347,26 +347,33 @@ struct GateArgs {
     ZipfRoute z;
 };
 
-// Grid (expert groups of four, clients), one wavefront per (expert, client):
-// lane l holds columns 4l + 256q (q < NQ) of the client's residual row and
-// of the expert's router row, all loaded before the first use.  Every
-// wavefront of a client forms the same row (the same instructions on the
-// same data: the sum of squares folded per lane in column order, then a
-// butterfly) and dots it with its router row (fma per lane in column order,
-// then a butterfly); the logit goes to the device-coherent level by an
-// agent-scope store, every store completes before the arrival counter
-// moves, and the client's last workgroup to arrive routes (wavefront 0:
-// softmax and top-k over the logits read back by agent-scope loads) while
-// wavefront 1 writes the expert input (also as the experts' limb planes)
-// and, chained, the updated residual, and wavefront 2 resets the counter.
-// No other workgroup of the client writes the residual, so all of them read
-// it whole.
+// Grid (expert groups of four, clients), one wavefront per (expert, client).
+// Lane l works on columns 4l + 256q of a row.  First the workgroup forms the
+// client's row once, wavefront w taking the column groups q = w, w + 4, ...:
+// the residual (chained: with the o projection's partial sums added), its
+// sum of squares (folded per lane in column order, a butterfly per
+// wavefront, the four wavefront sums added in order) and the router input,
+// both into LDS -- every workgroup of a client forms the same row, the same
+// instructions on the same data.  Then each wavefront dots its expert's
+// router row (loaded at the start, with the row's operands) with the router
+// input (fma per lane in column order, then a butterfly).  The logit goes to
+// the device-coherent level by an agent-scope store, every store completes
+// before the arrival counter moves, and the client's last workgroup to
+// arrive routes (wavefront 0: softmax and top-k over the logits read back by
+// agent-scope loads) while wavefronts 1-3 write the expert input (also as
+// the experts' limb planes, one 256-column span per wavefront at a time)
+// and, chained, the updated residual, and reset the counter.  No other
+// workgroup of the client writes the residual, so all of them read it whole.
 template <int NQ, bool GEMMA>
 __global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)
 {
     constexpr int NW = kThreads / EMU_WAVE;
+    constexpr int QW = (NQ + NW - 1) / NW; // column groups per wavefront in the row phase
     __shared__ float p[256];
+    __shared__ float red[NW];
     __shared__ uint32_t arrived;
+    __shared__ __align__(16) float xrow[NQ * 4 * EMU_WAVE]; // the residual (chained: with o added)
+    __shared__ __align__(16) float rrow[NQ * 4 * EMU_WAVE]; // the router input
     const int c = blockIdx.y, tid = threadIdx.x, lane = tid & (EMU_WAVE - 1), w = tid / EMU_WAVE;
     const int W = a.width, E = a.experts;
     const int e = NW * blockIdx.x + w;
@@ -376,60 +383,77 @@ __global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)
         const int i = 4 * lane + 4 * EMU_WAVE * q;
         return i < W ? *reinterpret_cast<const float4 *>(base + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     };
-    float4 x[NQ], rw[NQ], sc[NQ], ov[NQ];
     const bool chained = a.opart != nullptr;
+    float4 xv[QW], ov[QW], sv[QW], rw[NQ];
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) x[q] = ld(xr, q);
-    if (chained) {
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) ov[q] = ld(a.opart + (size_t)c * W, q);
+    for (int j = 0; j < QW; ++j) {
+        const int q = w + NW * j;
+        xv[j] = q < NQ ? ld(xr, q) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        ov[j] = q < NQ && chained ? ld(a.opart + (size_t)c * W, q) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        sv[j] = q < NQ ? ld(GEMMA ? a.rscale : a.gain, q) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 #pragma unroll
     for (int q = 0; q < NQ; ++q) rw[q] = ld(rr, q);
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) sc[q] = ld(GEMMA ? a.rscale : a.gain, q);
     if (chained) {
         // the o projection's slices added in order, then r + v * o_scale
         // (what the matvec's finishing pass would do)
         const size_t stride = (size_t)kMaxTokChain * W; // floats between slices
         for (int s = 1; s < a.o_nks; ++s) {
 #pragma unroll
-            for (int q = 0; q < NQ; ++q) {
+            for (int j = 0; j < QW; ++j) {
+                const int q = w + NW * j;
+                if (q >= NQ) continue;
                 const float4 t = ld(a.opart + s * stride + (size_t)c * W, q);
-                ov[q].x += t.x;
-                ov[q].y += t.y;
-                ov[q].z += t.z;
-                ov[q].w += t.w;
+                ov[j].x += t.x;
+                ov[j].y += t.y;
+                ov[j].z += t.z;
+                ov[j].w += t.w;
             }
         }
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) {
-            x[q].x = emu_resid_add(x[q].x, ov[q].x, a.o_scale);
-            x[q].y = emu_resid_add(x[q].y, ov[q].y, a.o_scale);
-            x[q].z = emu_resid_add(x[q].z, ov[q].z, a.o_scale);
-            x[q].w = emu_resid_add(x[q].w, ov[q].w, a.o_scale);
+        for (int j = 0; j < QW; ++j) {
+            xv[j].x = emu_resid_add(xv[j].x, ov[j].x, a.o_scale);
+            xv[j].y = emu_resid_add(xv[j].y, ov[j].y, a.o_scale);
+            xv[j].z = emu_resid_add(xv[j].z, ov[j].z, a.o_scale);
+            xv[j].w = emu_resid_add(xv[j].w, ov[j].w, a.o_scale);
         }
     }
     float ss = 0.0f;
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-        ss = __builtin_fmaf(x[q].x, x[q].x, ss);
-        ss = __builtin_fmaf(x[q].y, x[q].y, ss);
-        ss = __builtin_fmaf(x[q].z, x[q].z, ss);
-        ss = __builtin_fmaf(x[q].w, x[q].w, ss);
+    for (int j = 0; j < QW; ++j) {
+        ss = __builtin_fmaf(xv[j].x, xv[j].x, ss);
+        ss = __builtin_fmaf(xv[j].y, xv[j].y, ss);
+        ss = __builtin_fmaf(xv[j].z, xv[j].z, ss);
+        ss = __builtin_fmaf(xv[j].w, xv[j].w, ss);
     }
     ss = wave_sum(ss);
-    const float scale = 1.0f / sqrtf(ss / (float)W + (GEMMA ? 1e-6f : a.eps));
+    if (lane == 0) red[w] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NW; ++k) tot += red[k];
+    const float scale = 1.0f / sqrtf(tot / (float)W + (GEMMA ? 1e-6f : a.eps));
     const float qr = GEMMA ? scale / sqrtf((float)W) : scale;
     // router input: Gemma (r * rscale) * qr, else (r * scale) * gain
     auto rin = [&](float v, float s) { return GEMMA ? __fmul_rn(__fmul_rn(v, s), qr) : __fmul_rn(__fmul_rn(v, scale), s); };
+#pragma unroll
+    for (int j = 0; j < QW; ++j) {
+        const int q = w + NW * j;
+        if (q >= NQ) continue;
+        const int i = 4 * lane + 4 * EMU_WAVE * q; // zeros past the row
+        *reinterpret_cast<float4 *>(xrow + i) = xv[j];
+        *reinterpret_cast<float4 *>(rrow + i) = make_float4(rin(xv[j].x, sv[j].x), rin(xv[j].y, sv[j].y),
+                                                            rin(xv[j].z, sv[j].z), rin(xv[j].w, sv[j].w));
+    }
+    __syncthreads();
     float acc = 0.0f;
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
-        acc = __builtin_fmaf(rw[q].x, rin(x[q].x, sc[q].x), acc);
-        acc = __builtin_fmaf(rw[q].y, rin(x[q].y, sc[q].y), acc);
-        acc = __builtin_fmaf(rw[q].z, rin(x[q].z, sc[q].z), acc);
-        acc = __builtin_fmaf(rw[q].w, rin(x[q].w, sc[q].w), acc);
+        const float4 in = *reinterpret_cast<const float4 *>(rrow + 4 * lane + 4 * EMU_WAVE * q);
+        acc = __builtin_fmaf(rw[q].x, in.x, acc);
+        acc = __builtin_fmaf(rw[q].y, in.y, acc);
+        acc = __builtin_fmaf(rw[q].z, in.z, acc);
+        acc = __builtin_fmaf(rw[q].w, in.w, acc);
     }
     acc = wave_sum(acc);
     if (lane == 0 && e < E) {
@@ -448,41 +472,29 @@ __global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)
     __syncthreads();
     if (w == 0) {
         emu_route_token(p, E, a.k, a.ids + (size_t)c * a.k, a.weights + (size_t)c * a.k);
-    } else if (w == 1) {
-        float4 g[NQ], xe[NQ];
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) xe[q] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if constexpr (GEMMA) {
-#pragma unroll
-            for (int q = 0; q < NQ; ++q) g[q] = ld(a.gain, q);
+        return;
+    }
+    if (tid == EMU_WAVE) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // wavefronts 1..NW-1: the expert input (and chained the residual), one
+    // column group at a time
+    for (int q = w - 1; q < NQ; q += NW - 1) {
+        const int i = 4 * lane + 4 * EMU_WAVE * q;
+        if (4 * EMU_WAVE * q >= W) break; // uniform: past the row
+        const bool live = i < W;
+        const float4 x4 = *reinterpret_cast<const float4 *>(xrow + i);
+        float4 v;
+        if constexpr (GEMMA) { // (r * q) * gain2
+            const float4 g = live ? *reinterpret_cast<const float4 *>(a.gain + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            v = make_float4(__fmul_rn(__fmul_rn(x4.x, scale), g.x), __fmul_rn(__fmul_rn(x4.y, scale), g.y),
+                            __fmul_rn(__fmul_rn(x4.z, scale), g.z), __fmul_rn(__fmul_rn(x4.w, scale), g.w));
+        } else { // the router input is the expert input
+            v = *reinterpret_cast<const float4 *>(rrow + i);
         }
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) {
-            const int i = 4 * lane + 4 * EMU_WAVE * q;
-            if (i >= W) continue;
-            float4 v;
-            if constexpr (GEMMA) { // (r * q) * gain2
-                v.x = __fmul_rn(__fmul_rn(x[q].x, scale), g[q].x);
-                v.y = __fmul_rn(__fmul_rn(x[q].y, scale), g[q].y);
-                v.z = __fmul_rn(__fmul_rn(x[q].z, scale), g[q].z);
-                v.w = __fmul_rn(__fmul_rn(x[q].w, scale), g[q].w);
-            } else { // the router input is the expert input
-                v.x = rin(x[q].x, sc[q].x);
-                v.y = rin(x[q].y, sc[q].y);
-                v.z = rin(x[q].z, sc[q].z);
-                v.w = rin(x[q].w, sc[q].w);
-            }
+        if (live) {
             *reinterpret_cast<float4 *>(a.xn + (size_t)c * W + i) = v;
-            if (chained) *reinterpret_cast<float4 *>(a.state_out + (size_t)c * W + i) = x[q];
-            xe[q] = v;
+            if (chained) *reinterpret_cast<float4 *>(a.state_out + (size_t)c * W + i) = x4;
         }
-        if (a.xp.q) { // the experts' limb planes of the expert input, span by span
-#pragma unroll
-            for (int q = 0; q < NQ; ++q)
-                if (4 * EMU_WAVE * q < W) emu_span_limbs_wave(xe[q], 4 * lane + 4 * EMU_WAVE * q < W, c, q, a.xp);
-        }
-    } else if (tid == 2 * EMU_WAVE) {
-        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a.xp.q) emu_span_limbs_wave(v, live, c, q, a.xp); // span q of the experts' limb planes
     }
 }
 
