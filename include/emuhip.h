@@ -349,6 +349,9 @@ enum {
     EMU_T_FFN_NORM2 = 8 /* gemma: the experts' input gains [layer][hidden] (pre_ffw_norm_2) */
 };
 
+/* EMU_E_CONFIG for shapes the kernels do not take; the mixture-of-experts
+ * forms need n_experts <= 256, experts_used <= 8 and hidden a multiple of 8
+ * up to 4096. */
 int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_model **out);
 int emu_model_destroy(emu_model *model);
 /* Device address and size of a tensor inside the model's HBM residency (for
