@@ -630,6 +630,50 @@ __device__ __forceinline__ void emu_span_limbs_wave(float4 v4, bool live, int ve
         *reinterpret_cast<float *>(meta + 96) = finite ? ldexpf(1.0f, e2 - 20) : __int_as_float(0x7fc00000);
 }
 
+// Columns col..col+3 (col a multiple of 4) of token t as the multi-token
+// matvec's A operands (mfma.hip layout: 16-column sub-block sb, 8-column half
+// kh, limb l, token t -> 8 bytes at xa + 384 sb + (24 kh + 8 l + t) 8, the
+// scale at xs[8 sb + t]), by the four neighbouring lanes that hold the
+// sub-block (live: inside the row, the same for all four): three 7-bit limbs
+// under the sub-block's power-of-two scale, the link kernel's split.
+__device__ __forceinline__ void emu_emit_limbs4(float4 v4, bool live, int col, int t, uint8_t *xa, float *xs)
+{
+    const float x[4] = {v4.x, v4.y, v4.z, v4.w};
+    float amax = 0.0f;
+    int bad = 0; // an inf or NaN (fmaxf alone would drop a NaN)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = live ? fabsf(x[i]) : 0.0f;
+        amax = fmaxf(amax, a);
+        bad |= !(a <= 3.402823466e38f);
+    }
+    amax = fmaxf(amax, emu_xor_lane<1>(amax));
+    amax = fmaxf(amax, emu_xor_lane<2>(amax));
+    bad |= __shfl_xor(bad, 1, EMU_WAVE);
+    bad |= __shfl_xor(bad, 2, EMU_WAVE);
+    const bool finite = !bad;
+    int e2 = 0;
+    (void)frexpf(finite ? amax : 0.0f, &e2); // amax < 2^e2, so |x| * 2^(6-e2) < 64
+    uint32_t b[3] = {0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float s = finite && live ? ldexpf(x[i], 6 - e2) : 0.0f; // exact
+        const float f0 = rintf(s);
+        const float r1 = (s - f0) * 128.0f; // exact
+        const float f1 = rintf(r1);
+        const float f2 = rintf((r1 - f1) * 128.0f);
+        b[0] |= ((uint32_t)(int)f0 & 0xffu) << (8 * i);
+        b[1] |= ((uint32_t)(int)f1 & 0xffu) << (8 * i);
+        b[2] |= ((uint32_t)(int)f2 & 0xffu) << (8 * i);
+    }
+    if (!live) return;
+    const int sb = col >> 4, kh = (col >> 3) & 1;
+    uint8_t *dst = xa + (size_t)sb * 384 + (size_t)(kh * 24 + t) * 8 + (col & 7);
+#pragma unroll
+    for (int l = 0; l < 3; ++l) *reinterpret_cast<uint32_t *>(dst + 64 * l) = b[l];
+    if ((col & 15) == 0) xs[(size_t)sb * 8 + t] = finite ? ldexpf(1.0f, e2 - 20) : __int_as_float(0x7fc00000);
+}
+
 // One token's k (<= 8) routes in ascending expert id (ids are distinct;
 // entries past k or outside the expert range are skipped): order[i] is the
 // slot and w[i] its weight; returns how many (moe.rs:37-159 combines in that

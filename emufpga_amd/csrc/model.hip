@@ -339,6 +339,12 @@ struct GateArgs {
     float eps;
     float *xn;           // [client][width] expert input
     EmuLimbPlanes xp;    // and, when xp.q is set, as the experts' limb planes
+    // Gemma form, chained: the shared FFN's input rms(r) * ffn_gain as the
+    // gate|up matvec's A operands (null: none)
+    uint8_t *ffn_xa;
+    float *ffn_xs;
+    const float *ffn_gain;
+    float ffn_eps;
     float *state_out;    // chained: r + o * o_scale
     float *logits;       // [client][experts] hand-off between workgroups
     uint32_t *counters;  // [client] arrivals, zero between launches
@@ -495,6 +501,13 @@ __global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)
             if (chained) *reinterpret_cast<float4 *>(a.state_out + (size_t)c * W + i) = x4;
         }
         if (a.xp.q) emu_span_limbs_wave(v, live, c, q, a.xp); // span q of the experts' limb planes
+        if (GEMMA && a.ffn_xa) { // the shared FFN's input, as the link kernel would form it
+            const float s2 = 1.0f / sqrtf(tot / (float)W + a.ffn_eps);
+            const float4 g = live ? *reinterpret_cast<const float4 *>(a.ffn_gain + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float4 u = make_float4(__fmul_rn(__fmul_rn(x4.x, s2), g.x), __fmul_rn(__fmul_rn(x4.y, s2), g.y),
+                                         __fmul_rn(__fmul_rn(x4.z, s2), g.z), __fmul_rn(__fmul_rn(x4.w, s2), g.w));
+            emu_emit_limbs4(u, live, i, c, a.ffn_xa, a.ffn_xs);
+        }
     }
 }
 
@@ -942,21 +955,17 @@ int run_moe(emu_session *s)
             ga.o_nks = o_nks;
             ga.o_scale = c.residual_scale;
             ga.state_out = s->state;
+            if (c.shared_ff && chain) { // the gate writes the shared FFN's operands
+                ga.ffn_xa = xa;
+                ga.ffn_xs = xs;
+                ga.ffn_gain = ffn_norm + (size_t)layer * H;
+                ga.ffn_eps = c.eps;
+            }
             if ((st = launch_gate<true>(ctx, ga, n)) != EMU_OK) return st;
             if (c.shared_ff && chain) {
-                // link -> gate|up -> link (GeGLU) -> down; the down's partial
-                // sums join the residual in the next layer's link (the last
-                // layer's here, before the expert sum)
-                EmuMfmaLink li{};
-                li.mode = 0;
-                li.x = s->state;
-                li.cols = (int)H;
-                li.cols_cap = cap;
-                li.n_tok = n;
-                li.gain = ffn_norm + (size_t)layer * H;
-                li.eps = c.eps;
-                li.limbs = true;
-                if ((st = emu_mfma_link(ctx, li)) != EMU_OK) return st;
+                // (gate's operands) -> gate|up -> link (GeGLU) -> down; the
+                // down's partial sums join the residual in the next layer's
+                // link (the last layer's here, before the expert sum)
                 QmvArgs g{};
                 g.w = lw + m->off_sg;
                 g.w_up = lw + m->off_su;
