@@ -291,6 +291,28 @@ def test_attend_cached(ctx, kv_f16):
         == _lib.EMU_E_CONFIG  # heads must group evenly (spm-kv/src/attend.rs:82-85)
 
 
+@pytest.mark.parametrize("experts,k", [(256, 64), (256, 8), (128, 8), (65, 1), (40, 8), (3, 3)])
+def test_route_shapes_match_oracle(ctx, experts, k):
+    """The register-resident route at every expert count it takes (up to 256
+    experts, 64 routed): entries past a 64-expert boundary, ties across the
+    boundary (lowest id first), and all experts routed."""
+    rng = np.random.default_rng(experts * 100 + k)
+    n_tok = 5
+    logits = rng.normal(size=(n_tok, experts)).astype(np.float32)
+    logits[1, :] = 0.5  # all tied
+    logits[2, ::3] = 2.0  # ties spread over every 64-expert word
+    logits[3] = -logits[3] * 40.0  # probabilities far apart (underflow to zero)
+    bl, bi, bw = ctx.upload(logits), ctx.alloc(n_tok * k * 4), ctx.alloc(n_tok * k * 4)
+    ctx.check(ctx.lib.emu_route(ctx.h, bl.ptr, n_tok, experts, k, bi.ptr, bw.ptr), "route")
+    ids = bi.read(np.int32).reshape(n_tok, k)
+    w = bw.read(np.float32).reshape(n_tok, k)
+    for t in range(n_tok):
+        rid, rw = oracle.route(logits[t], k)
+        assert list(ids[t]) == list(rid), t
+        assert np.allclose(w[t], rw, rtol=2e-6, atol=1e-30), t
+    assert list(ids[1]) == list(range(k))
+
+
 def test_route_matches_oracle(ctx):
     rng = np.random.default_rng(95)
     n_tok, experts, k = 8, 64, 8
