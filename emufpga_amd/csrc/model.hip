@@ -482,17 +482,28 @@ __global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)
     }
     if (tid == EMU_WAVE) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // wavefronts 1..NW-1: the expert input (and chained the residual), one
-    // column group at a time
-    for (int q = w - 1; q < NQ; q += NW - 1) {
+    // column group at a time, every gain load issued before the first use
+    constexpr int QT = (NQ + NW - 2) / (NW - 1); // column groups per wavefront
+    float4 g2[QT], fg[QT];
+#pragma unroll
+    for (int j = 0; j < QT; ++j) {
+        const int q = w - 1 + (NW - 1) * j, i = 4 * lane + 4 * EMU_WAVE * q;
+        const bool ok = q < NQ && i < W;
+        const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        g2[j] = GEMMA && ok ? *reinterpret_cast<const float4 *>(a.gain + i) : z;
+        fg[j] = GEMMA && ok && a.ffn_xa ? *reinterpret_cast<const float4 *>(a.ffn_gain + i) : z;
+    }
+#pragma unroll
+    for (int j = 0; j < QT; ++j) {
+        const int q = w - 1 + (NW - 1) * j;
+        if (q >= NQ || 4 * EMU_WAVE * q >= W) break; // uniform: past the row
         const int i = 4 * lane + 4 * EMU_WAVE * q;
-        if (4 * EMU_WAVE * q >= W) break; // uniform: past the row
         const bool live = i < W;
         const float4 x4 = *reinterpret_cast<const float4 *>(xrow + i);
         float4 v;
         if constexpr (GEMMA) { // (r * q) * gain2
-            const float4 g = live ? *reinterpret_cast<const float4 *>(a.gain + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            v = make_float4(__fmul_rn(__fmul_rn(x4.x, scale), g.x), __fmul_rn(__fmul_rn(x4.y, scale), g.y),
-                            __fmul_rn(__fmul_rn(x4.z, scale), g.z), __fmul_rn(__fmul_rn(x4.w, scale), g.w));
+            v = make_float4(__fmul_rn(__fmul_rn(x4.x, scale), g2[j].x), __fmul_rn(__fmul_rn(x4.y, scale), g2[j].y),
+                            __fmul_rn(__fmul_rn(x4.z, scale), g2[j].z), __fmul_rn(__fmul_rn(x4.w, scale), g2[j].w));
         } else { // the router input is the expert input
             v = *reinterpret_cast<const float4 *>(rrow + i);
         }
@@ -503,9 +514,8 @@ __global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)
         if (a.xp.q) emu_span_limbs_wave(v, live, c, q, a.xp); // span q of the experts' limb planes
         if (GEMMA && a.ffn_xa) { // the shared FFN's input, as the link kernel would form it
             const float s2 = 1.0f / sqrtf(tot / (float)W + a.ffn_eps);
-            const float4 g = live ? *reinterpret_cast<const float4 *>(a.ffn_gain + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            const float4 u = make_float4(__fmul_rn(__fmul_rn(x4.x, s2), g.x), __fmul_rn(__fmul_rn(x4.y, s2), g.y),
-                                         __fmul_rn(__fmul_rn(x4.z, s2), g.z), __fmul_rn(__fmul_rn(x4.w, s2), g.w));
+            const float4 u = make_float4(__fmul_rn(__fmul_rn(x4.x, s2), fg[j].x), __fmul_rn(__fmul_rn(x4.y, s2), fg[j].y),
+                                         __fmul_rn(__fmul_rn(x4.z, s2), fg[j].z), __fmul_rn(__fmul_rn(x4.w, s2), fg[j].w));
             emu_emit_limbs4(u, live, i, c, a.ffn_xa, a.ffn_xs);
         }
     }
