@@ -367,8 +367,9 @@ struct GateArgs {
 // before the arrival counter moves, and the client's last workgroup to
 // arrive routes (wavefront 0: softmax and top-k over the logits read back by
 // agent-scope loads) while wavefronts 1-3 write the expert input (also as
-// the experts' limb planes, one 256-column span per wavefront at a time)
-// and, chained, the updated residual, and reset the counter.  No other
+// the experts' limb planes, one 256-column span per wavefront at a time),
+// chained the updated residual (and, in the Gemma form, the shared FFN's
+// input as its matvec's operands), and reset the counter.  No other
 // workgroup of the client writes the residual, so all of them read it whole.
 template <int NQ, bool GEMMA>
 __global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)

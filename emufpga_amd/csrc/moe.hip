@@ -690,6 +690,12 @@ __device__ __forceinline__ uint32_t byte8(uint2 v, int b) { return ((b < 4 ? v.x
 
 __device__ __forceinline__ long pack8(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
 
+// a * b + c for |a|, |b| < 2^23 (both sign-extended from 24 bits, which the
+// compiler folds into v_mad_i32_i24, a full-rate instruction; a 32-bit
+// integer multiply is quarter rate).  A chunk's limb sums are below 2^17
+// and the scales below 2^7.
+__device__ __forceinline__ int mad24(int a, int b, int c) { return ((a << 8) >> 8) * ((b << 8) >> 8) + c; }
+
 // Pins twelve running sums at this point of the program: without it the
 // compiler reassociates a span's sixteen chunk products into a tree at the
 // end, which keeps every chunk's 16-register MFMA result alive at once.
@@ -792,7 +798,7 @@ template <> struct Mma<FmtQ6K> {
             refill(m);
             const int sc = (int)(int8_t)byte8(m < 8 ? s0 : s1, m & 7);
 #pragma unroll
-            for (int i = 0; i < 12; ++i) I[i] += sc * D[i];
+            for (int i = 0; i < 12; ++i) I[i] = mad24(sc, D[i], I[i]);
             pin12(I);
         }
         double ts[4];
@@ -853,7 +859,7 @@ template <> struct Mma<FmtQ5K> {
             uint32_t sc, mn;
             FmtQ5K::scale_min(r, sb, sc, mn);
 #pragma unroll
-            for (int i = 0; i < 12; ++i) I[i] += (int)sc * D[i];
+            for (int i = 0; i < 12; ++i) I[i] = mad24((int)sc, D[i], I[i]);
             pin12(I);
         }
         // the mins of chunks 8kh .. 8kh + 7: sub-blocks 4kh .. 4kh + 3, two chunks each
