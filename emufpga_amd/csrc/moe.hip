@@ -1246,8 +1246,8 @@ int launch_mma(emu_ctx *ctx, const MoeArgs &a, const LimbPlanes &in)
     g.ks = mma_shares(a, g.tiles, in.ns, KIND == kMmaUp ? 8192 : 2048);
     const int tpw = kWaves / g.ks;
     const size_t lds = kWaves * kMaxTok * 32 * 4 + kWaves * kMaxTok * 4 + kWaves * 32 * M::STRIDE;
-    const int listed = a.n_tok * a.k < a.n_experts ? a.n_tok * a.k : a.n_experts;
-    const dim3 grid((g.tiles + tpw - 1) / tpw, listed);
+    const int routed = a.n_tok * a.k < a.n_experts ? a.n_tok * a.k : a.n_experts; // grid rows: at most this many experts
+    const dim3 grid((g.tiles + tpw - 1) / tpw, routed);
     hipLaunchKernelGGL((moe_mma_kernel<F, KIND, ACT>), grid, dim3(kThreads), lds, ctx->stream, g);
     EMU_LAUNCH_CHECK(ctx);
     return EMU_OK;
