@@ -90,7 +90,13 @@ def time_gate_up(ctx: Context, model: Model, rounds: int) -> tuple[float, int, i
 
     for base in bases:  # warm
         launch(base)
+    # A run of large fills ahead of the first event keeps the GPU busy while
+    # the host queues the timed launches, so the events time the kernels back
+    # to back and not the host's launch rate (a ctypes call per launch).
+    spacer = ctx.alloc(1 << 30)
     ctx.sync()
+    for _ in range(8 + rounds * len(bases) // 16):
+        spacer.zero()
     ctx.event_record(0)
     for _ in range(rounds):
         for base in bases:

@@ -111,15 +111,32 @@ struct LimbQ6K {
     }
     __device__ static __forceinline__ float dot(const Raw &r, const Limbs &L, int unit)
     {
+        return q6k_dot<LimbQ6K>(r, L, unit);
+    }
+    // The limb dots of one unit: per sub-block three v_dot4_i32_i8 chains
+    // over its four code words, combined exactly, then one float step.
+    template <class CODES>
+    __device__ static __forceinline__ float q6k_dot(const Raw &r, const Limbs &L, int unit)
+    {
         const int m = unit & 1;
         const float d = h2f((uint16_t)r.d);
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            int a0 = 0, a1 = 0, a2 = L.c[j];
+            // Each chain starts with the three-operand form, its accumulator
+            // (0, or the bias term, which later rows reuse) read in place:
+            // the accumulate-in-place form the compiler picks would need a
+            // register copy of it first.
+            int a0, a1, a2;
+            {
+                const int q = (int)CODES::code(r, j, 0);
+                asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(a0) : "v"(q), "v"(comp(L.l[j][0], 0)));
+                asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(a1) : "v"(q), "v"(comp(L.l[j][1], 0)));
+                asm("v_dot4_i32_i8 %0, %1, %2, %3" : "=v"(a2) : "v"(q), "v"(comp(L.l[j][2], 0)), "v"(L.c[j]));
+            }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int q = (int)code(r, j, i);
+            for (int i = 1; i < 4; ++i) {
+                const int q = (int)CODES::code(r, j, i);
                 a0 = __builtin_amdgcn_sdot4(q, comp(L.l[j][0], i), a0, false);
                 a1 = __builtin_amdgcn_sdot4(q, comp(L.l[j][1], i), a1, false);
                 a2 = __builtin_amdgcn_sdot4(q, comp(L.l[j][2], i), a2, false);
@@ -140,9 +157,28 @@ struct LimbQ6K {
 // The same units read from the lane-major layout: a 4096-column stretch of a
 // row (16 blocks) is one chunk, so each load instruction of a wavefront
 // covers one contiguous kilobyte (three of them), then 256 bytes of scales
-// and 32 of d.  The registers hold exactly what LimbQ6K::load gives, so the
-// arithmetic and its results are identical.
+// and 32 of d.  The three code words of a column quad are re-packed so that
+// three of its four sub-blocks' codes are one mask each: byte b of
+//   W0 = c0 | (c3 & 3) << 6,  W1 = c1 | (c3 >> 2 & 3) << 6,
+//   W2 = c2 | (c3 >> 4) << 6
+// for the 6-bit codes c0..c3 of sub-blocks j = 0..3 (the GGUF form takes
+// three or four operations per code word).  Same codes, so the arithmetic
+// and its results are identical to the GGUF-order kernel's.
 struct LimbQ6KLM : LimbQ6K {
+    __device__ static __forceinline__ uint32_t code(const Raw &r, int j, int i)
+    {
+        const uint32_t W0 = (uint32_t)comp(r.a, i), W1 = (uint32_t)comp(r.b, i), W2 = (uint32_t)comp(r.q, i);
+        switch (j) {
+        case 0: return W0 & 0x3f3f3f3fu;
+        case 1: return W1 & 0x3f3f3f3fu;
+        case 2: return W2 & 0x3f3f3f3fu;
+        default: return ((W0 >> 6) & 0x03030303u) | ((W1 >> 4) & 0x0c0c0c0cu) | ((W2 >> 2) & 0x30303030u);
+        }
+    }
+    __device__ static __forceinline__ float dot(const Raw &r, const Limbs &L, int unit)
+    {
+        return q6k_dot<LimbQ6KLM>(r, L, unit);
+    }
     __device__ static __forceinline__ void load(const uint8_t *row, int unit, Raw &r)
     {
         const uint32_t L = (uint32_t)unit & 63u;
@@ -518,7 +554,21 @@ __global__ __launch_bounds__(256) void lane_major_kernel(const uint8_t *src, siz
         uint8_t *d = dst + 210 * b0;
         for (uint32_t o = threadIdx.x; o < 210u * n; o += 256u) in[o] = s[o];
         __syncthreads();
-        for (uint32_t o = threadIdx.x; o < 210u * n; o += 256u) d[o] = in[lane_major_source(o, n)];
+        for (uint32_t o = threadIdx.x; o < 210u * n; o += 256u) {
+            uint8_t v;
+            if (o < 192u * n) { // a code byte: re-packed from its column's ql-low, ql-high and qh bytes
+                const uint32_t r = o % (64u * n);
+                const uint32_t A = in[lane_major_source(r, n)], B = in[lane_major_source(64u * n + r, n)],
+                               Q = in[lane_major_source(128u * n + r, n)];
+                const uint32_t region = o / (64u * n);
+                v = (uint8_t)(region == 0   ? (A & 15u) | (Q & 3u) << 4 | (B >> 4 & 3u) << 6
+                              : region == 1 ? (B & 15u) | (Q >> 2 & 3u) << 4 | (B >> 6) << 6
+                                            : (A >> 4) | (Q & 0xf0u));
+            } else {
+                v = in[lane_major_source(o, n)];
+            }
+            d[o] = v;
+        }
         __syncthreads();
     }
 }

@@ -131,11 +131,17 @@ int emu_qmatvec(emu_ctx *ctx, int encoding, const void *d_w, size_t w_len, uint3
  * counterpart: the reference streams GGUF block order (spm-gguf/src/
  * tensor.rs:103-139), which is kept as the resident order everywhere else.
  * The block stream is cut into chunks of 16 blocks (the last may hold n < 16)
- * and each chunk's bytes are permuted so that a wavefront's loads read
- * contiguous kilobytes: unit L = 4*block + 2*half + slot finds its 16 bytes
- * of ql low nibbles at 16L, of ql high nibbles at 64n + 16L, of qh at
- * 128n + 16L, its half-block's 8 scale bytes at 192n + 8*(L/2) and its
- * block's d at 208n + 2*(L/4).  Sizes and chunk offsets are unchanged.
+ * and each chunk's bytes are rearranged so that a wavefront's loads read
+ * contiguous kilobytes: unit L = 4*block + 2*half + slot finds three
+ * 16-byte code words at 16L, 64n + 16L and 128n + 16L, made from its ql low
+ * nibble bytes a, ql high nibble bytes b and qh bytes q (byte by byte) as
+ *   W0 = (a & 15) | (q & 3) << 4 | (b >> 4 & 3) << 6
+ *   W1 = (b & 15) | (q >> 2 & 3) << 4 | (b >> 6) << 6
+ *   W2 = (a >> 4) | (q & 0xf0)
+ * (the 6-bit codes of three of its four sub-blocks are the low six bits of
+ * W0..W2, the fourth's the top two bits of each), its half-block's 8 scale
+ * bytes at 192n + 8*(L/2) and its block's d at 208n + 2*(L/4).  Sizes and
+ * chunk offsets are unchanged.
  * len must be whole 210-byte blocks (EMU_E_SHORT); src and dst must not
  * overlap (EMU_E_ARG); Q6_K only (EMU_E_UNSUPPORTED). */
 int emu_weights_lane_major(emu_ctx *ctx, int encoding, const void *d_src, size_t len, void *d_dst);

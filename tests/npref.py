@@ -413,9 +413,13 @@ def dense_model_f64(cfg, w: dict, tokens_per_step):
 def lane_major_q6k(raw: np.ndarray) -> np.ndarray:
     """The Q6_K lane-major layout: the block stream in chunks of 16 blocks
     (the last may hold n < 16); within a chunk unit L = 4*block + 2*half +
-    slot gets its ql-low 16 bytes at 16L, ql-high at 64n + 16L, qh at
-    128n + 16L; then the n blocks' 16 scale bytes (256 B for n = 16), then
-    their d values."""
+    slot gets three 16-byte code words at 16L, 64n + 16L and 128n + 16L, made
+    from its ql-low bytes a, ql-high bytes b and qh bytes q as
+      W0 = (a & 15) | (q & 3) << 4 | (b >> 4 & 3) << 6
+      W1 = (b & 15) | (q >> 2 & 3) << 4 | (b >> 6) << 6
+      W2 = (a >> 4) | (q & 0xf0)
+    then the n blocks' 16 scale bytes (256 B for n = 16), then their d
+    values."""
     blocks = np.asarray(raw, np.uint8).reshape(-1, 210)
     out = []
     for c0 in range(0, blocks.shape[0], 16):
@@ -427,5 +431,8 @@ def lane_major_q6k(raw: np.ndarray) -> np.ndarray:
         a = ch[j[:, None], (64 * h + 16 * m)[:, None] + col]
         b = ch[j[:, None], (64 * h + 32 + 16 * m)[:, None] + col]
         q = ch[j[:, None], (128 + 32 * h + 16 * m)[:, None] + col]
-        out += [a.reshape(-1), b.reshape(-1), q.reshape(-1), ch[:, 192:208].reshape(-1), ch[:, 208:210].reshape(-1)]
+        w0 = (a & 15) | (q & 3) << 4 | (b >> 4 & 3) << 6
+        w1 = (b & 15) | (q >> 2 & 3) << 4 | (b >> 6) << 6
+        w2 = (a >> 4) | (q & 0xF0)
+        out += [w0.reshape(-1), w1.reshape(-1), w2.reshape(-1), ch[:, 192:208].reshape(-1), ch[:, 208:210].reshape(-1)]
     return np.concatenate(out) if out else np.zeros(0, np.uint8)

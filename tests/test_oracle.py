@@ -562,26 +562,36 @@ def test_qmatvec_threads_give_identical_bits():
     assert np.array_equal(bits(one_m2), bits(many_m2))
 
 
-def test_lane_major_layout_gives_each_unit_its_gguf_bytes():
+def test_lane_major_layout_gives_each_unit_its_codes():
     """The lane-major Q6_K layout (the batch-1 device copy) read at the offsets
-    the kernel's loader uses -- 16L, 1024 + 16L, 2048 + 16L, 3072 + 8(L/2),
-    3328 + 2(L/4) in each 16-block chunk -- yields, for every unit, exactly
-    the bytes the GGUF-order loader reads: ql at 64h + 16m and 64h + 32 + 16m,
-    qh at 128 + 32h + 16m, scales at 192 + 8h, d at 208 of block L/4."""
+    the kernel's loader uses -- code words at 16L, 1024 + 16L, 2048 + 16L,
+    scales at 3072 + 8(L/2), d at 3328 + 2(L/4) in each 16-block chunk -- and
+    decoded as the kernel decodes (sub-blocks 0-2: the low six bits of W0, W1,
+    W2; sub-block 3: their top two bits, in that order) dequantizes, weight for
+    weight, to the oracle's GGUF decoder (spm-gguf/src/tensor.rs:103-139):
+    d * scales[8h + 2j + m] * (code - 32) at column 128h + 32j + 16m + i."""
     rng = np.random.default_rng(95)
     raw = rng.integers(0, 256, size=48 * 210, dtype=np.uint8)  # three chunks: one 12288-column row
+    raw.reshape(-1, 210)[:, 208:210] = np.frombuffer(rng.uniform(0.5, 2.0, 48).astype(np.float16).tobytes(),
+                                                     np.uint8).reshape(-1, 2)  # finite d
     lm = npref.lane_major_q6k(raw)
-    assert lm.size == raw.size and sorted(lm.tolist()) == sorted(raw.tolist())
+    assert lm.size == raw.size
+    ref = oracle.decode(Q6, raw).reshape(-1, 256)
+    checked = 0
     for chunk in range(3):
-        c, g = lm[3360 * chunk:3360 * (chunk + 1)], raw[3360 * chunk:3360 * (chunk + 1)]
+        c = lm[3360 * chunk:3360 * (chunk + 1)]
         for L in range(64):
             blk, h, m = L // 4, (L // 2) % 2, L % 2
-            o = 210 * blk
-            assert np.array_equal(c[16 * L:16 * L + 16], g[o + 64 * h + 16 * m:o + 64 * h + 16 * m + 16])
-            assert np.array_equal(c[1024 + 16 * L:1040 + 16 * L], g[o + 64 * h + 32 + 16 * m:o + 64 * h + 48 + 16 * m])
-            assert np.array_equal(c[2048 + 16 * L:2064 + 16 * L], g[o + 128 + 32 * h + 16 * m:o + 144 + 32 * h + 16 * m])
-            assert np.array_equal(c[3072 + 8 * (L // 2):3080 + 8 * (L // 2)], g[o + 192 + 8 * h:o + 200 + 8 * h])
-            assert np.array_equal(c[3328 + 2 * (L // 4):3330 + 2 * (L // 4)], g[o + 208:o + 210])
+            w0, w1, w2 = (c[o + 16 * L:o + 16 * L + 16].astype(np.int32) for o in (0, 1024, 2048))
+            codes = [w0 & 63, w1 & 63, w2 & 63, (w0 >> 6) | (w1 >> 6) << 2 | (w2 >> 6) << 4]
+            sc = c[3072 + 8 * (L // 2):3080 + 8 * (L // 2)].view(np.int8)
+            d = c[3328 + 2 * (L // 4):3330 + 2 * (L // 4)].view(np.float16)[0].astype(np.float32)
+            for j in range(4):
+                w = (d * np.float32(sc[2 * j + m])) * (codes[j].astype(np.float32) - np.float32(32))
+                cols = 128 * h + 32 * j + 16 * m + np.arange(16)
+                assert np.array_equal(w, ref[16 * chunk + blk, cols]), (chunk, L, j)
+                checked += 16
+    assert checked == 48 * 256
 
 
 def _moe_weights(cfg, rng, w_extra=None):
