@@ -21,9 +21,12 @@
 // keeps its 64 columns' limbs in registers for the whole launch, so a row
 // costs only its weight bytes.  Waves are persistent: row-group g handles rows
 // g, g + G, g + 2G, ... (G row-groups in the grid) with the next D rows'
-// loads in flight while the current ones are reduced (DPP wave sums).  Rows
-// of 4096*S columns use S wavefronts per row-group, whose partial sums meet in
-// LDS in a fixed order (deterministic results).
+// loads in flight while the current ones are reduced (DPP wave sums, two
+// values per reduction).  A wavefront's rows are finished (activation,
+// residual, store) a window of up to 64 at a time, one row per lane, not
+// once per row by a single lane.  Rows of 4096*S columns use S wavefronts
+// per row-group, whose partial sums meet in LDS in a fixed order
+// (deterministic results).
 //
 // Prologue (per workgroup, overlapped with the first rows' loads, which are
 // issued right after x's): x is read,
@@ -70,6 +73,57 @@ __device__ __forceinline__ float wave_sum63(float v)
     v += EMU_DPP(v, 0x142, 0xa); // row_bcast:15 into rows 1 and 3
     v += EMU_DPP(v, 0x143, 0xc); // row_bcast:31 into rows 2 and 3
     return v;
+}
+
+// Wave-wide sums of two values at once, bit for bit those of wave_sum63:
+// lanes 0..15 and 32..47 get a's total, lanes 16..31 and 48..63 b's.  Both
+// get their 16-lane row sums by DPP, a permlane16 swap adds row pairs of a
+// into rows 0 and 2 and of b into rows 1 and 3, and a permlane32 swap adds
+// the two halves: (r0 + r1) + (r2 + r3) per value, the same sum in the same
+// order as wave_sum63's (r3 + r2) + (r1 + r0).  12 instructions for both
+// totals, against 20 for two wave_sum63.
+__device__ __forceinline__ float row_sum(float v)
+{
+    v += EMU_DPP(v, 0xb1, 0xf);  // quad_perm [1,0,3,2]
+    v += EMU_DPP(v, 0x4e, 0xf);  // quad_perm [2,3,0,1]
+    v += EMU_DPP(v, 0x141, 0xf); // row_half_mirror
+    v += EMU_DPP(v, 0x140, 0xf); // row_mirror: every lane holds its row's sum
+    return v;
+}
+
+__device__ __forceinline__ float pair_sum(float a, float b)
+{
+    a = row_sum(a);
+    b = row_sum(b);
+    emu_swap_halves<16>(a, b); // rows: a = [a0 b0 a2 b2], b = [a1 b1 a3 b3]
+    const float v = a + b;
+    float x = v, y = v;
+    emu_swap_halves<32>(x, y);
+    return x + y;
+}
+
+// The same for one value: its total in every lane.
+__device__ __forceinline__ float wave_total(float v)
+{
+    v = row_sum(v);
+    float x = v, y = v;
+    emu_swap_halves<16>(x, y);
+    v = x + y;
+    x = v;
+    y = v;
+    emu_swap_halves<32>(x, y);
+    return x + y;
+}
+
+__device__ __forceinline__ float lane_value(float v, int l)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// v with lane l's value replaced by the wave-uniform s.
+__device__ __forceinline__ float set_lane(float v, float s, int l)
+{
+    return (int)__lane_id() == l ? s : v;
 }
 
 // Q6_K (210-byte blocks of 256: ql[128], qh[64], int8 scales[16], f16 d).
@@ -350,42 +404,80 @@ __global__ __launch_bounds__((EMU_WAVE * LimbShape<S, WV>::W)) void qmv_limb_ker
         }
     };
 
+    // A round's NV = D * NR dot sums, in (d, n) order, are reduced two at a
+    // time (pair i: value 2i in lane 0, value 2i + 1 in lane 16).
+    // With one wavefront per row (S == 1) the rows' epilogues are deferred:
+    // lane j of dv / dr holds the sums and residual of the j-th row of a
+    // window of 64, and the window's rows are finished together, one per
+    // lane, so the activation and store run once per window, not per row.
+    constexpr int NV = D * NR, NP = (NV + 1) / 2;
+    float dv[NR], dr = 0.0f;
+#pragma unroll
+    for (int n = 0; n < NR; ++n) dv[n] = 0.0f;
     for (int k = 0; k < rounds; ++k) {
         float resid[D]; // this round's residuals (the slots are refilled below)
+        float v[NV];
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            float p[NR];
 #pragma unroll
-            for (int n = 0; n < NR; ++n) p[n] = wave_sum63(LF::dot(buf[d].raw[n], L, unit));
+            for (int n = 0; n < NR; ++n) {
+                v[d * NR + n] = LF::dot(buf[d].raw[n], L, unit);
+                // The dot is finished here, above the refill: sunk below it
+                // (its sums are not used before the reduction), it would
+                // keep the slot's old words alive beside the new ones, a
+                // register copy per word and a wavefront per SIMD lost.
+                asm volatile("" ::"v"(v[d * NR + n]));
+            }
             resid[d] = ACC ? buf[d].resid : 0.0f;
             if (k + 1 < rounds) load_slot(k + 1, d, buf[d]);
-            if (S == 1) {
-                if (lane == EMU_WAVE - 1) finish(grg + (k * D + d) * total_rg, p, resid[d]);
-            } else if (lane == EMU_WAVE - 1) {
-#pragma unroll
-                for (int n = 0; n < NR; ++n) part[k & 1][rg][sl][d][n] = p[n];
-            }
         }
-        if (S > 1) {
-            // Double-buffered by round parity: one barrier per round suffices.
-            __syncthreads();
-            if (sl == 0 && lane == EMU_WAVE - 1) {
+        float tot[NP];
 #pragma unroll
-                for (int d = 0; d < D; ++d) {
-                    float p[NR];
+        for (int i = 0; i < NP; ++i) tot[i] = 2 * i + 1 < NV ? pair_sum(v[2 * i], v[2 * i + 1]) : wave_total(v[2 * i]);
+        if constexpr (S == 1) {
 #pragma unroll
-                    for (int n = 0; n < NR; ++n) {
-                        float t = part[k & 1][rg][0][d][n];
+            for (int d = 0; d < D; ++d) {
+                const int slot = k * D + d, pos = slot & (EMU_WAVE - 1);
 #pragma unroll
-                        for (int s = 1; s < S; ++s) t += part[k & 1][rg][s][d][n];
-                        p[n] = t;
-                    }
-                    finish(grg + (k * D + d) * total_rg, p, resid[d]);
+                for (int n = 0; n < NR; ++n) {
+                    const int i = d * NR + n;
+                    dv[n] = set_lane(dv[n], lane_value(tot[i / 2], (i & 1) * 16), pos);
                 }
+                if (ACC) dr = set_lane(dr, lane_value(resid[d], 0), pos);
+                if (pos == EMU_WAVE - 1 || slot == rounds * D - 1) {
+                    if (lane <= pos) finish(grg + (slot - pos + lane) * total_rg, dv, dr);
+                }
+            }
+        } else {
+            // Double-buffered by round parity: one barrier per round suffices.
+            float *pk = &part[k & 1][rg][sl][0][0];
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                const int idx = 2 * i + ((lane >> 4) & 1);
+                if ((lane & 47) == 0 && idx < NV) pk[idx] = tot[i]; // lanes 0 and 16
+            }
+            __syncthreads();
+            if (sl == 0 && lane < D) { // lane d finishes the round's row d
+                const int d = lane;
+                float p[NR];
+#pragma unroll
+                for (int n = 0; n < NR; ++n) {
+                    float t = part[k & 1][rg][0][d][n];
+#pragma unroll
+                    for (int s2 = 1; s2 < S; ++s2) t += part[k & 1][rg][s2][d][n];
+                    p[n] = t;
+                }
+                float r = resid[0];
+#pragma unroll
+                for (int e = 1; e < D; ++e) r = d == e ? resid[e] : r;
+                finish(grg + (k * D + d) * total_rg, p, r);
             }
         }
     }
-    if (a.keys && sl == 0 && lane == EMU_WAVE - 1) a.keys[grg] = best;
+    if (a.keys) {
+        best = emu_wave_max_u64(best);
+        if (sl == 0 && lane == 0) a.keys[grg] = best;
+    }
 }
 
 // Rows in flight per wavefront and workgroups per CU, measured per shape on
