@@ -255,6 +255,16 @@ template <int S, int WV = 0> struct LimbShape {
     static_assert(G * NSB == T && (G == 1 || G == 2 || G == 4), "prologue mapping");
 };
 
+// The low bytes of four words, in order, as one word: three v_perm_b32
+// (selector bytes 0..3 pick the second operand's bytes, 4..7 the first's,
+// 0x0c gives zero).
+__device__ __forceinline__ uint32_t pack_low_bytes(const uint32_t (&w)[4])
+{
+    const uint32_t lo = __builtin_amdgcn_perm(w[1], w[0], 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(w[3], w[2], 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
 // Split this thread's CPT columns (already normalised) into limbs; the G
 // threads of a sub-block are neighbouring lanes.
 template <int G, int CPT>
@@ -278,24 +288,39 @@ __device__ __forceinline__ void make_limbs(const float (&xv)[CPT], LimbRec *rec,
     const bool finite = !bad;
     int e = 0;
     (void)frexpf(finite ? amax : 0.0f, &e);      // amax < 2^e, so |x| * 2^(6-e) < 64
+    // Digits by the float recurrence f0 = rint(v), r1 = (v - f0) * 128,
+    // f1 = rint(r1), f2 = rint((r1 - f1) * 128), each rint as an add of
+    // 1.5 * 2^23 (whose ulp is 1, so the add rounds to the nearest integer,
+    // ties to even, for |value| < 2^22) that leaves the integer in the sum's
+    // low mantissa bits: its low byte is the limb's int8, no convert needed.
+    // The limbs' sum, sum_c (16384 L0 + 128 L1 + L2), comes from the packed
+    // bytes by dot products with ones.
+    constexpr float kRound = 12582912.0f;
     uint32_t p0[CPT / 4], p1[CPT / 4], p2[CPT / 4];
-    int sum = 0;
+    int s0 = 0, s1 = 0, s2 = 0;
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-        const float v = finite ? ldexpf(xv[k], 6 - e) : 0.0f; // exact
-        const float f0 = rintf(v);
-        const float r1 = (v - f0) * 128.0f; // exact
-        const float f1 = rintf(r1);
-        const float f2 = rintf((r1 - f1) * 128.0f);
-        const int i0 = (int)f0, i1 = (int)f1, i2 = (int)f2;
-        sum += i0 * 16384 + i1 * 128 + i2;
-        const uint32_t b = ((uint32_t)i0 & 0xffu) | ((uint32_t)i1 & 0xffu) << 8 | ((uint32_t)i2 & 0xffu) << 16;
-        const int sh = 8 * (k & 3);
-        if ((k & 3) == 0) p0[k >> 2] = p1[k >> 2] = p2[k >> 2] = 0u;
-        p0[k >> 2] |= (b & 0xffu) << sh;
-        p1[k >> 2] |= ((b >> 8) & 0xffu) << sh;
-        p2[k >> 2] |= ((b >> 16) & 0xffu) << sh;
+    for (int q = 0; q < CPT / 4; ++q) {
+        uint32_t t[3][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float v = finite ? ldexpf(xv[4 * q + u], 6 - e) : 0.0f; // exact
+            const float t0 = v + kRound;
+            const float r1 = (v - (t0 - kRound)) * 128.0f; // exact
+            const float t1 = r1 + kRound;
+            const float t2 = (r1 - (t1 - kRound)) * 128.0f + kRound;
+            t[0][u] = __float_as_uint(t0);
+            t[1][u] = __float_as_uint(t1);
+            t[2][u] = __float_as_uint(t2);
+        }
+        const uint32_t b0 = pack_low_bytes(t[0]), b1 = pack_low_bytes(t[1]), b2 = pack_low_bytes(t[2]);
+        p0[q] = b0;
+        p1[q] = b1;
+        p2[q] = b2;
+        s0 = __builtin_amdgcn_sdot4((int)b0, 0x01010101, s0, false);
+        s1 = __builtin_amdgcn_sdot4((int)b1, 0x01010101, s1, false);
+        s2 = __builtin_amdgcn_sdot4((int)b2, 0x01010101, s2, false);
     }
+    int sum = s0 * 16384 + s1 * 128 + s2;
     if (G >= 2) sum += __shfl_xor(sum, 1, EMU_WAVE);
     if (G >= 4) sum += __shfl_xor(sum, 2, EMU_WAVE);
     uint32_t *d0 = reinterpret_cast<uint32_t *>(&rec[sb].l0);
