@@ -303,7 +303,9 @@ __device__ __forceinline__ void make_limbs(const float (&xv)[CPT], LimbRec *rec,
         uint32_t t[3][4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const float v = finite ? ldexpf(xv[4 * q + u], 6 - e) : 0.0f; // exact
+            // exact; in a sub-block holding an inf or NaN the digits are
+            // garbage, and the NaN scale makes every dot with it NaN anyway
+            const float v = ldexpf(xv[4 * q + u], 6 - e);
             const float t0 = v + kRound;
             const float r1 = (v - (t0 - kRound)) * 128.0f; // exact
             const float t1 = r1 + kRound;
