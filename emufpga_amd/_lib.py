@@ -31,6 +31,7 @@ ENCODINGS = {"F32": F32, "F16": F16, "Q8_0": Q8_0, "Q2_K": Q2_K, "Q5_K": Q5_K, "
 
 EMU_MV_ACCUMULATE = 1
 EMU_MV_LANE_MAJOR = 2
+EMU_MV_MFMA_MAJOR = 4
 EMU_ROPE_NEOX = 0
 EMU_ROPE_INTERLEAVED = 1
 EMU_ROPE_NEOX_FMA = 2
@@ -193,6 +194,8 @@ SIGNATURES = {
     "emu_rms_norm": [P, P, P, U32, U32, F, P],
     "emu_rope_table": [P, U32, U32, F, P],
     "emu_weights_lane_major": [P, I, P, SZ, P],
+    "emu_weights_mfma_major": [P, I, P, SZ, U32, U32, P],
+    "emu_weights_mfma_major_bytes": [U32, U32],
     "emu_model_sync": [P],
     "emu_host_alloc": [P, SZ, C.POINTER(P)],
     "emu_host_free": [P, P],
@@ -256,6 +259,7 @@ SIGNATURES = {
     "emu_spm_writer_destroy": [P],
 }
 _RESTYPE = {"emu_strerror": C.c_char_p, "emu_last_error": C.c_char_p, "emu_moe_workspace_bytes": C.c_size_t,
+            "emu_weights_mfma_major_bytes": C.c_size_t,
             "emu_gguf_error": C.c_char_p, "emu_spm_error": C.c_char_p, "emu_spm_writer_error": C.c_char_p}
 
 _lib = None

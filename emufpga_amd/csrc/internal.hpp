@@ -733,6 +733,7 @@ struct QmvArgs {
     float acc_scale;       // accumulate as y + v * acc_scale (0: y + v)
     float out_div;         // results divided by this before store and keys (0: none)
     int lane_major;        // w / w_up in the Q6_K lane-major layout (emu_lane_major_q6k)
+    int mfma_major;        // w / w_up in the Q6_K matrix-core operand layout (emu_mfma_major_q6k)
     int act;               // gate|up pair: EMU_ACT_SILU (SwiGLU) or EMU_ACT_GELU_TANH (GeGLU)
     float softcap;         // results -> softcap * tanh(v / softcap) after out_div (0: none)
 };
@@ -789,6 +790,11 @@ int emu_launch_limb(emu_ctx *ctx, int encoding, const QmvArgs &a, int *key_slots
 // block's d at 208n + 2*(L/4).  A pure byte permutation of each chunk: sizes
 // and chunk offsets are unchanged.  src and dst must not overlap.
 int emu_lane_major_q6k(emu_ctx *ctx, const uint8_t *src, size_t nblocks, uint8_t *dst);
+// The Q6_K matrix-core operand copy of a rows x cols matrix (mfma.hip):
+// emu_mfma_major_bytes(rows, cols) bytes, rows rounded up to whole 32-row
+// tiles (the padding rows repeat the last row).
+size_t emu_mfma_major_bytes(uint32_t rows, uint32_t cols);
+int emu_mfma_major_q6k(emu_ctx *ctx, const uint8_t *src, uint32_t rows, uint32_t cols, uint8_t *dst);
 // Multi-token (2..8) matvec on the int8 matrix cores (mfma.hip).  Its
 // workspace lives in the context and grows on demand (hipMalloc); callers
 // that capture graphs reserve it beforehand with emu_mfma_reserve.

@@ -277,12 +277,34 @@ __device__ __forceinline__ uint32_t code8(uint32_t ql, uint32_t qh, int q)
     }
 }
 
+// The operand-order copy: per 32-row tile and 256-column block one chunk of
+// kMmChunk bytes -- six 1 KB code segments (lane l's 16 bytes at 16 l of
+// each), the 32 rows' 16 scale bytes, their 32 d.  Lane l = 32 kh + j holds
+// row j's codes for columns 8 kh .. 8 kh + 7 of each 16-column sub-block sb
+// in 24 words: for the sub-block group g = sb / 4 and half p (columns
+// 8 kh + 4 p .. + 3), word 6 g + 3 p + w, w = 0..2, has in byte b the code of
+// sub-block 4 g + w in its low six bits and two bits of sub-block 4 g + 3's
+// code in its top two (bits 0-1 in w = 0, 2-3 in w = 1, 4-5 in w = 2).
+constexpr int kMmChunk = 6720;
+
+// Four codes (one word of the MFMA B operand) of sub-block 4 g + jj.
+__device__ __forceinline__ uint32_t mm_code4(const uint32_t *w, int jj)
+{
+    switch (jj) {
+    case 0: return w[0] & 0x3f3f3f3fu;
+    case 1: return w[1] & 0x3f3f3f3fu;
+    case 2: return w[2] & 0x3f3f3f3fu;
+    default: return ((w[0] >> 6) & 0x03030303u) | ((w[1] >> 4) & 0x0c0c0c0cu) | ((w[2] >> 2) & 0x30303030u);
+    }
+}
+
 // One unit of work: 32 weight rows of one matrix x one 1024-column slice.
 // A lane holds, for its row (lane % 32) and column half kh = lane / 32 of
 // each 16-column sub-block of its wavefront's 256-column block, the weight
 // bytes and the A operands (limbs of M row lane % 32).
 struct Unit {
     uint2 ql[2][2][2], qh[2][2];
+    uint32_t cw[24]; // the operand-order copy's code words (MM)
     uint4 sc;
     uint32_t d;
     long av[16];
@@ -296,6 +318,13 @@ struct Unit {
 // directly, 8 bytes from each of 32 rows per instruction, streams at about
 // two thirds of the rate).  The unit's per-token scales are staged in LDS
 // while the weights load.
+// MM: the weights come from the operand-order copy (emu_mfma_major_q6k):
+// each 32-row x 256-column tile block is one 6720-byte chunk whose code words
+// are already in each lane's operand order, so six 1 KB loads per wavefront
+// bring them straight into registers (no LDS round trip), and its scales and
+// d follow.  The codes are the same, so the results are bit for bit those of
+// the GGUF-order path.
+template <bool MM>
 __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs a, int units)
 {
     const int nks = (a.cols + kSlice - 1) / kSlice, nrt = (a.rows + kTileRows - 1) / kTileRows;
@@ -334,7 +363,19 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
         // Coalesced: instruction k covers rows 4k..4k+3 of the tile, 16 lanes
         // per row (13 x 16 bytes + the 2-byte d), into this wavefront's LDS rows.
         const int r4 = lane >> 4, c16 = lane & 15;
-        if (has) { // uniform
+        if (MM && has) { // uniform
+            const uint8_t *cp = a.w[b.mat] + ((size_t)b.rt * (a.cols / 256) + cb) * kMmChunk;
+#pragma unroll
+            for (int i = 0; i < 6; ++i) {
+                const uint4 q4 = ld16(cp + 1024 * i + 16 * lane);
+                b.cw[4 * i] = q4.x;
+                b.cw[4 * i + 1] = q4.y;
+                b.cw[4 * i + 2] = q4.z;
+                b.cw[4 * i + 3] = q4.w;
+            }
+            b.sc = ld16(cp + 6144 + 16 * j);
+            b.d = ld2(cp + 6656 + 2 * j);
+        } else if (has) { // uniform
             uint4 raw[8];
             uint16_t dd[8];
 #pragma unroll
@@ -371,6 +412,8 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
             b.d = *reinterpret_cast<const uint16_t *>(bp + 208);
         } else { // zero codes, scales and d: this wavefront adds exact zeros
 #pragma unroll
+            for (int i = 0; i < 24; ++i) b.cw[i] = 0u;
+#pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int p = 0; p < 2; ++p) {
@@ -393,9 +436,16 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
     const float d = h2f((uint16_t)b.d);
     const float *sp = xs + (size_t)w * 16 * kMaxTok + 4 * kh;
     auto mma = [&](int sb) {
-        const int h = sb >> 3, q = (sb >> 1) & 3, p = sb & 1;
-        const uint2 lq = b.ql[h][q & 1][p], hq = b.qh[h][p];
-        const long bv = (long)(((uint64_t)code8(lq.y, hq.y, q) << 32) | code8(lq.x, hq.x, q));
+        long bv;
+        if constexpr (MM) {
+            const int g = sb >> 2, jj = sb & 3;
+            const uint32_t lo = mm_code4(b.cw + 6 * g, jj), hi = mm_code4(b.cw + 6 * g + 3, jj);
+            bv = (long)(((uint64_t)hi << 32) | lo);
+        } else {
+            const int h = sb >> 3, q = (sb >> 1) & 3, p = sb & 1;
+            const uint2 lq = b.ql[h][q & 1][p], hq = b.qh[h][p];
+            bv = (long)(((uint64_t)code8(lq.y, hq.y, q) << 32) | code8(lq.x, hq.x, q));
+        }
         v16i D = {};
         D = __builtin_amdgcn_mfma_i32_32x32x16_i8(b.av[sb], bv, D, 0, 0, 0);
         return __builtin_amdgcn_mfma_i32_32x32x16_i8(b.av[sb], neg32, D, 0, 0, 0);
@@ -641,7 +691,12 @@ int emu_mfma_matvec(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int
     ma.part = w.part;
     const int nks = (q.cols + kSlice - 1) / kSlice, nrt = (q.rows + kTileRows - 1) / kTileRows;
     const int units = nks * nrt * nmat;
-    hipLaunchKernelGGL(qmv_mfma_kernel, dim3((unsigned)units), dim3(EMU_WAVE * kWaves), 0, ctx->stream, ma, units);
+    if (q.mfma_major)
+        hipLaunchKernelGGL(qmv_mfma_kernel<true>, dim3((unsigned)units), dim3(EMU_WAVE * kWaves), 0, ctx->stream, ma,
+                           units);
+    else
+        hipLaunchKernelGGL(qmv_mfma_kernel<false>, dim3((unsigned)units), dim3(EMU_WAVE * kWaves), 0, ctx->stream, ma,
+                           units);
     EMU_LAUNCH_CHECK(ctx);
     if (part_nks) *part_nks = nks;
     return EMU_OK;
@@ -704,4 +759,96 @@ int emu_launch_mfma(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int
     if ((st = emu_mfma_link(ctx, l)) != EMU_OK) return st;
     if ((st = emu_mfma_matvec(ctx, a, n_tok, a.cols, nullptr)) != EMU_OK) return st;
     return emu_mfma_finish(ctx, a, n_tok, a.cols, key_slots);
+}
+
+namespace {
+
+// Code (0..63) of column c of a Q6_K block held at in[0..209]: column
+// 128h + 32q + 16m + i takes the nibble q >> 1 of ql[64h + 32(q & 1) + 16m + i]
+// and bits 2q..2q+1 of qh[32h + 16m + i].
+__device__ __forceinline__ uint32_t q6k_code(const uint8_t *in, uint32_t c)
+{
+    const uint32_t h = c >> 7, q = (c >> 5) & 3u, m = (c >> 4) & 1u, i = c & 15u;
+    const uint32_t lo = (uint32_t)in[64u * h + 32u * (q & 1u) + 16u * m + i] >> (4u * (q >> 1)) & 15u;
+    const uint32_t hi = (uint32_t)in[128u + 32u * h + 16u * m + i] >> (2u * q) & 3u;
+    return lo | hi << 4;
+}
+
+// One workgroup per (32-row tile, 256-column block) chunk, grid-stride: the
+// chunk's 32 blocks come into LDS (rows past the matrix repeat its last row)
+// and each destination byte is formed from there.
+__global__ __launch_bounds__(256) void mfma_major_kernel(const uint8_t *src, uint32_t rows, uint32_t nblk,
+                                                         size_t row_bytes, uint8_t *dst, size_t chunks)
+{
+    __shared__ uint8_t in[kTileRows][210];
+    for (size_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+        const uint32_t rt = (uint32_t)(c / nblk), cb = (uint32_t)(c % nblk);
+        for (uint32_t o = threadIdx.x; o < kTileRows * 210u; o += 256u) {
+            const uint32_t r = o / 210u, k = o % 210u;
+            const uint32_t row = rt * kTileRows + r < rows ? rt * kTileRows + r : rows - 1;
+            in[r][k] = src[(size_t)row * row_bytes + (size_t)cb * 210u + k];
+        }
+        __syncthreads();
+        uint8_t *d = dst + c * kMmChunk;
+        for (uint32_t o = threadIdx.x; o < (uint32_t)kMmChunk; o += 256u) {
+            uint8_t v;
+            if (o < 6144u) { // code word 6g + 3p + w of lane 32 kh + j, byte b
+                const uint32_t within = o & 1023u, lane = within >> 4, q = within & 15u;
+                const uint32_t k = 4u * (o >> 10) + (q >> 2), b = q & 3u;
+                const uint32_t g = k / 6u, p = (k % 6u) / 3u, w = k % 3u;
+                const uint32_t col = 8u * (lane >> 5) + 4u * p + b;
+                const uint8_t *r = in[lane & 31u];
+                const uint32_t cw = q6k_code(r, 16u * (4u * g + w) + col);
+                const uint32_t c3 = q6k_code(r, 16u * (4u * g + 3u) + col);
+                v = (uint8_t)(cw | ((c3 >> (2u * w)) & 3u) << 6);
+            } else if (o < 6656u) { // the 32 rows' scale bytes
+                const uint32_t r = o - 6144u;
+                v = in[r >> 4][192u + (r & 15u)];
+            } else { // and their d
+                const uint32_t r = o - 6656u;
+                v = in[r >> 1][208u + (r & 1u)];
+            }
+            d[o] = v;
+        }
+        __syncthreads();
+    }
+}
+
+} // namespace
+
+size_t emu_mfma_major_bytes(uint32_t rows, uint32_t cols)
+{
+    return (size_t)((rows + kTileRows - 1) / kTileRows) * (cols / 256) * kMmChunk;
+}
+
+int emu_mfma_major_q6k(emu_ctx *ctx, const uint8_t *src, uint32_t rows, uint32_t cols, uint8_t *dst)
+{
+    if (rows == 0 || cols == 0) return EMU_OK;
+    if (cols % 256 != 0) return EMU_E_SHORT;
+    const uint32_t nblk = cols / 256;
+    const size_t chunks = (size_t)((rows + kTileRows - 1) / kTileRows) * nblk;
+    const unsigned grid = (unsigned)(chunks < 65536 ? chunks : 65536);
+    hipLaunchKernelGGL(mfma_major_kernel, dim3(grid), dim3(256), 0, ctx->stream, src, rows, nblk, (size_t)nblk * 210,
+                       dst, chunks);
+    EMU_LAUNCH_CHECK(ctx);
+    return EMU_OK;
+}
+
+extern "C" size_t emu_weights_mfma_major_bytes(uint32_t rows, uint32_t cols)
+{
+    return cols % 256 == 0 ? emu_mfma_major_bytes(rows, cols) : 0;
+}
+
+extern "C" int emu_weights_mfma_major(emu_ctx *ctx, int encoding, const void *d_src, size_t len, uint32_t rows,
+                                      uint32_t cols, void *d_dst)
+{
+    if (!ctx || !d_src || !d_dst) return EMU_E_ARG;
+    if (encoding != EMU_ENC_Q6_K) return EMU_E_UNSUPPORTED;
+    if (rows == 0 || cols == 0 || cols % 256 != 0) return EMU_E_SHORT;
+    if (len != (size_t)rows * (cols / 256) * 210) return EMU_E_SHAPE;
+    const uint8_t *s = static_cast<const uint8_t *>(d_src);
+    uint8_t *d = static_cast<uint8_t *>(d_dst);
+    const size_t out = emu_mfma_major_bytes(rows, cols);
+    if (s < d + out && d < s + len) return EMU_E_ARG; // not in place
+    return emu_mfma_major_q6k(ctx, s, rows, cols, d);
 }

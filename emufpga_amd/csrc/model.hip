@@ -71,6 +71,20 @@ struct emu_model {
         *lane_major = n == 1 && lm_takes(cols);
         return *lane_major ? lm + (w - base) : w;
     }
+    // Matrix-core operand copy (emu_mfma_major_q6k) of the Q6_K matrices the
+    // 2..8-token chain reads: the layers' matrices with whole 32-row tiles at
+    // the same offsets as in `base`, the output matrix (padded to whole
+    // tiles) at off_embed.  Rebuilt with the lane-major copy.
+    uint8_t *mm = nullptr;
+    bool mm_takes(uint32_t rows, uint32_t cols) const
+    {
+        return mm && rows % 32 == 0 && emu_mfma_shape_ok(cfg.encoding, (int)cols);
+    }
+    const uint8_t *mm_or(const uint8_t *w, uint32_t rows, uint32_t cols, int *mfma_major) const
+    {
+        *mfma_major = mm_takes(rows, cols);
+        return *mfma_major ? mm + (w - base) : w;
+    }
 };
 
 struct emu_session {
@@ -748,8 +762,8 @@ int run_chain(emu_session *s)
     };
     auto matvec = [&](const uint8_t *w, const uint8_t *w_up, size_t rb, int rows, int cols, int *nks) {
         QmvArgs q{};
-        q.w = w;
-        q.w_up = w_up;
+        q.w = m->mm_or(w, (uint32_t)rows, (uint32_t)cols, &q.mfma_major);
+        q.w_up = w_up ? m->mm_or(w_up, (uint32_t)rows, (uint32_t)cols, &q.mfma_major) : nullptr;
         q.row_bytes = rb;
         q.rows = rows;
         q.cols = cols;
@@ -785,6 +799,10 @@ int run_chain(emu_session *s)
     }
     QmvArgs out{};
     out.w = m->base + (c.tied ? m->off_embed : m->off_output);
+    if (m->mm && emu_mfma_shape_ok(c.encoding, H)) { // the padded output copy (any row count)
+        out.w = m->mm + m->off_embed;
+        out.mfma_major = 1;
+    }
     out.row_bytes = m->rb_h;
     out.rows = (int)c.vocab;
     out.cols = H;
@@ -1176,12 +1194,16 @@ int run_step(emu_session *s)
 // Rebuild the lane-major copy (outside any graph capture).
 int model_sync(emu_model *m)
 {
-    if (!m->lm || !m->lm_dirty) return EMU_OK;
+    if ((!m->lm && !m->mm) || !m->lm_dirty) return EMU_OK;
     emu_ctx *ctx = m->ctx;
     const emu_model_config &c = m->cfg;
     const uint32_t QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim;
     int st;
     auto put = [&](size_t off, uint32_t rows, uint32_t cols, size_t rb) -> int {
+        if (m->mm_takes(rows, cols)) {
+            const int st2 = emu_mfma_major_q6k(ctx, m->base + off, rows, cols, m->mm + off);
+            if (st2 != EMU_OK) return st2;
+        }
         if (!m->lm_takes(cols)) return EMU_OK;
         return emu_lane_major_q6k(ctx, m->base + off, (size_t)rows * rb / 210, m->lm + off);
     };
@@ -1194,9 +1216,13 @@ int model_sync(emu_model *m)
             (st = put(lo + m->off_d, c.hidden, c.ffn, m->rb_f)) != EMU_OK)
             return st;
     }
+    const size_t out_src = c.tied ? m->off_embed : m->off_output;
     if (m->lm_takes(c.hidden)) {
-        const size_t src = c.tied ? m->off_embed : m->off_output;
-        if ((st = emu_lane_major_q6k(ctx, m->base + src, m->embed_bytes / 210, m->lm + m->off_embed)) != EMU_OK)
+        if ((st = emu_lane_major_q6k(ctx, m->base + out_src, m->embed_bytes / 210, m->lm + m->off_embed)) != EMU_OK)
+            return st;
+    }
+    if (m->mm && emu_mfma_shape_ok(c.encoding, (int)c.hidden)) { // the output matrix, padded to whole tiles
+        if ((st = emu_mfma_major_q6k(ctx, m->base + out_src, c.vocab, c.hidden, m->mm + m->off_embed)) != EMU_OK)
             return st;
     }
     if ((st = emu_ctx_sync(ctx)) != EMU_OK) return st;
@@ -1381,6 +1407,22 @@ extern "C" int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_m
         }
         m->lm = static_cast<uint8_t *>(q);
     }
+    // The matrix-core operand copy: dense Q6_K models whose widths the
+    // multi-token chain takes (the layers' region plus the padded output).
+    const bool mm_any = !moe && c.encoding == EMU_ENC_Q6_K &&
+                        (emu_mfma_shape_ok(c.encoding, (int)c.hidden) || emu_mfma_shape_ok(c.encoding, (int)QW) ||
+                         emu_mfma_shape_ok(c.encoding, (int)c.ffn));
+    if (mm_any) {
+        void *q = nullptr;
+        const size_t out_mm = emu_mfma_shape_ok(c.encoding, (int)c.hidden) ? emu_mfma_major_bytes(c.vocab, c.hidden) : 0;
+        if ((st = emu_malloc(ctx, m->off_embed + out_mm, &q)) != EMU_OK) {
+            if (m->lm) emu_free(ctx, m->lm);
+            emu_free(ctx, m->base);
+            delete m;
+            return st;
+        }
+        m->mm = static_cast<uint8_t *>(q);
+    }
     *out = m;
     return EMU_OK;
 }
@@ -1390,6 +1432,7 @@ extern "C" int emu_model_destroy(emu_model *m)
     if (!m) return EMU_E_ARG;
     emu_free(m->ctx, m->base);
     if (m->lm) emu_free(m->ctx, m->lm);
+    if (m->mm) emu_free(m->ctx, m->mm);
     delete m;
     return EMU_OK;
 }

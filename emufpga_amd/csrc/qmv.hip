@@ -641,6 +641,10 @@ int emu_row_bytes(int encoding, uint32_t cols, size_t *row_bytes)
 int emu_launch_qmv(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int *key_slots)
 {
     if (a.rows == 0 || n_tok == 0) return EMU_OK;
+    if (a.mfma_major) { // only the multi-token matrix-core kernel reads that layout
+        if (!emu_mfma_supports(encoding, a.cols, n_tok) || (a.w_up && a.accumulate)) return EMU_E_UNSUPPORTED;
+        return emu_launch_mfma(ctx, encoding, a, n_tok, key_slots);
+    }
     if (n_tok == 1 && emu_limb_supports(encoding, a.cols) && !(a.w_up && a.accumulate))
         return emu_launch_limb(ctx, encoding, a, key_slots);
     if (a.lane_major) return EMU_E_UNSUPPORTED; // only the batch-1 limb kernel reads that layout
@@ -679,9 +683,12 @@ extern "C" int emu_qmatvec(emu_ctx *ctx, int encoding, const void *d_w, size_t w
 {
     if (!ctx || !d_w || !d_x || !d_y) return EMU_E_ARG;
     if (n_tok < 1 || n_tok > 8) return EMU_E_ARG;
+    const bool mm = (flags & EMU_MV_MFMA_MAJOR) != 0;
+    if (mm && (flags & EMU_MV_LANE_MAJOR)) return EMU_E_ARG;
     size_t rb = 0;
-    int st = check_matrix(encoding, w_len, rows, cols, &rb);
+    int st = mm ? emu_row_bytes(encoding, cols, &rb) : check_matrix(encoding, w_len, rows, cols, &rb);
     if (st != EMU_OK) return st;
+    if (mm && w_len != emu_mfma_major_bytes(rows, cols)) return EMU_E_SHAPE;
     if (x_len < (size_t)n_tok * cols) return EMU_E_ACTIVATION_LEN;
     QmvArgs a{};
     a.w = static_cast<const uint8_t *>(d_w);
@@ -695,6 +702,7 @@ extern "C" int emu_qmatvec(emu_ctx *ctx, int encoding, const void *d_w, size_t w
     a.y = d_y;
     a.accumulate = (flags & EMU_MV_ACCUMULATE) ? 1 : 0;
     a.lane_major = (flags & EMU_MV_LANE_MAJOR) ? 1 : 0;
+    a.mfma_major = mm ? 1 : 0;
     return emu_launch_qmv(ctx, encoding, a, (int)n_tok);
 }
 
@@ -722,6 +730,8 @@ extern "C" int emu_qmatvec_fused(emu_ctx *ctx, int encoding, const void *d_w, co
     a.y = d_y;
     a.accumulate = (flags & EMU_MV_ACCUMULATE) ? 1 : 0;
     a.lane_major = (flags & EMU_MV_LANE_MAJOR) ? 1 : 0;
+    a.mfma_major = (flags & EMU_MV_MFMA_MAJOR) ? 1 : 0;
+    if (a.lane_major && a.mfma_major) return EMU_E_ARG;
     return emu_launch_qmv(ctx, encoding, a, (int)n_tok);
 }
 

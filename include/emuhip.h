@@ -121,8 +121,13 @@ int emu_dequant(emu_ctx *ctx, int encoding, const void *d_src, size_t src_len, f
  * or accumulated into with EMU_MV_ACCUMULATE.  n_tok 1..8.
  * EMU_MV_LANE_MAJOR: W is in the Q6_K lane-major layout that
  * emu_weights_lane_major makes; taken by Q6_K at one token with 4096 or
- * 12288 columns, EMU_E_UNSUPPORTED otherwise.  Same results, bit for bit. */
-enum { EMU_MV_ACCUMULATE = 1u, EMU_MV_LANE_MAJOR = 2u };
+ * 12288 columns, EMU_E_UNSUPPORTED otherwise.  Same results, bit for bit.
+ * EMU_MV_MFMA_MAJOR: W is in the Q6_K matrix-core operand layout that
+ * emu_weights_mfma_major makes (w_len = emu_weights_mfma_major_bytes(rows,
+ * cols), EMU_E_SHAPE otherwise); taken by Q6_K at 2..8 tokens on the widths
+ * the matrix-core matvec takes, EMU_E_UNSUPPORTED otherwise.  Same results
+ * as GGUF order on that kernel, bit for bit. */
+enum { EMU_MV_ACCUMULATE = 1u, EMU_MV_LANE_MAJOR = 2u, EMU_MV_MFMA_MAJOR = 4u };
 int emu_qmatvec(emu_ctx *ctx, int encoding, const void *d_w, size_t w_len, uint32_t rows,
                 uint32_t cols, const float *d_x, size_t x_len, uint32_t n_tok, float *d_y,
                 uint32_t flags);
@@ -145,6 +150,26 @@ int emu_qmatvec(emu_ctx *ctx, int encoding, const void *d_w, size_t w_len, uint3
  * len must be whole 210-byte blocks (EMU_E_SHORT); src and dst must not
  * overlap (EMU_E_ARG); Q6_K only (EMU_E_UNSUPPORTED). */
 int emu_weights_lane_major(emu_ctx *ctx, int encoding, const void *d_src, size_t len, void *d_dst);
+
+/* Device layout of Q6_K weights for the 2..8-token matrix-core matvec.  No
+ * reference counterpart (the reference streams GGUF block order,
+ * spm-gguf/src/tensor.rs:103-139).  The rows x cols matrix (cols a multiple
+ * of 256) is cut into 32-row tiles (the last one padded by repeating the last
+ * row) and 256-column blocks; chunk (tile t, block k) is the 6720 bytes at
+ * 6720 * (t * cols/256 + k): six 1024-byte code segments, then the tile's 32
+ * rows' 16 scale bytes (512 B), then their f16 d (64 B).  Lane l = 32 kh + j
+ * of a wavefront reads the 16 bytes at 16 l of each code segment: 24 words
+ * holding row j's codes for columns 8 kh .. 8 kh + 7 of each 16-column
+ * sub-block s, word 6 (s / 4) + 3 p + w (p: columns 8 kh + 4 p .. + 3;
+ * w = 0..2) carrying in byte b the 6-bit code of sub-block 4 (s / 4) + w in
+ * its low six bits and bits 2w, 2w + 1 of sub-block 4 (s / 4) + 3's code in
+ * its top two.  emu_weights_mfma_major_bytes gives the size (0 if cols is
+ * not a multiple of 256).  len must be rows * cols / 256 * 210 (EMU_E_SHAPE);
+ * cols a multiple of 256 (EMU_E_SHORT); src and dst must not overlap
+ * (EMU_E_ARG); Q6_K only (EMU_E_UNSUPPORTED). */
+size_t emu_weights_mfma_major_bytes(uint32_t rows, uint32_t cols);
+int emu_weights_mfma_major(emu_ctx *ctx, int encoding, const void *d_src, size_t len, uint32_t rows, uint32_t cols,
+                           void *d_dst);
 
 /* Fused forms used by the decode step (no separate reference entry point;
  * each equals a composition of reference calls):

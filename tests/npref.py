@@ -436,3 +436,37 @@ def lane_major_q6k(raw: np.ndarray) -> np.ndarray:
         w2 = (a >> 4) | (q & 0xF0)
         out += [w0.reshape(-1), w1.reshape(-1), w2.reshape(-1), ch[:, 192:208].reshape(-1), ch[:, 208:210].reshape(-1)]
     return np.concatenate(out) if out else np.zeros(0, np.uint8)
+
+
+def mfma_major_q6k(raw: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """The Q6_K matrix-core operand layout of a rows x cols matrix: 32-row
+    tiles (the last padded by repeating the last row) by 256-column blocks,
+    one 6720-byte chunk each, chunk (t, k) at 6720 (t cols/256 + k).  Lane
+    l = 32 kh + j owns row j's codes for columns 8 kh + 4 p + b (p, b in
+    0..1, 0..3) of each 16-column sub-block s; word 6 (s/4) + 3 p + w of the
+    lane (w in 0..2), at 1024 (word // 4) + 16 l + 4 (word % 4), holds in
+    byte b the code of sub-block 4 (s/4) + w in its low six bits and bits
+    2w, 2w + 1 of sub-block 4 (s/4) + 3's code in its top two.  Then the 32
+    rows' scale bytes (16 per row) and their d (2 bytes per row)."""
+    nblk = cols // 256
+    blocks = np.asarray(raw, np.uint8).reshape(rows, nblk, 210)
+    ntile = (rows + 31) // 32
+    blocks = blocks[np.minimum(np.arange(32 * ntile), rows - 1)].reshape(ntile, 32, nblk, 210)
+    code = (q6_k_codes(blocks.reshape(-1, 210))[0] + 32).reshape(ntile, 32, nblk, 256)  # 0..63
+    out = np.zeros((ntile, nblk, 6720), np.uint8)
+    lane = np.arange(64)
+    j, kh = lane % 32, lane // 32
+    for g in range(4):
+        for p in range(2):
+            for b in range(4):
+                col = 8 * kh + 4 * p + b  # per lane
+                c3 = code[:, j, :, 16 * (4 * g + 3) + col]  # (64, ntile, nblk): lanes first
+                for w in range(3):
+                    cw = code[:, j, :, 16 * (4 * g + w) + col]
+                    byte = cw | ((c3 >> (2 * w)) & 3) << 6
+                    word = 6 * g + 3 * p + w
+                    off = 1024 * (word // 4) + 16 * lane + 4 * (word % 4) + b  # (64,)
+                    out[:, :, off] = byte.transpose(1, 2, 0)
+    out[:, :, 6144:6656] = blocks[:, :, :, 192:208].transpose(0, 2, 1, 3).reshape(ntile, nblk, 512)
+    out[:, :, 6656:6720] = blocks[:, :, :, 208:210].transpose(0, 2, 1, 3).reshape(ntile, nblk, 64)
+    return out.reshape(-1)

@@ -149,3 +149,74 @@ def test_repeatable(ctx):
     a = streamed(ctx, m, (x, n_tok))
     b = streamed(ctx, m, (x, n_tok))
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ---- the matrix-core operand device layout ---------------------------------
+
+@pytest.mark.parametrize("rows,cols", [(32, 256), (37, 1024), (96, 4096), (5, 2816)])
+def test_mfma_major_layout_matches_numpy(ctx, rows, cols):
+    raw = np.random.default_rng(rows * cols).integers(0, 256, size=rows * cols // 256 * 210, dtype=np.uint8)
+    n = ctx.lib.emu_weights_mfma_major_bytes(rows, cols)
+    assert n == (rows + 31) // 32 * cols // 256 * 6720
+    src, dst = ctx.upload(raw), ctx.alloc(n)
+    ctx.check(ctx.lib.emu_weights_mfma_major(ctx.h, Q6, src.ptr, raw.size, rows, cols, dst.ptr), "mfma_major")
+    assert np.array_equal(dst.read(np.uint8), npref.mfma_major_q6k(raw, rows, cols))
+
+
+def test_mfma_major_refusals(ctx):
+    L = ctx.lib
+    rows, cols = 32, 4096
+    raw = np.zeros(rows * cols // 256 * 210, np.uint8)
+    n = L.emu_weights_mfma_major_bytes(rows, cols)
+    src, dst = ctx.upload(raw), ctx.alloc(n)
+    assert L.emu_weights_mfma_major_bytes(rows, 1000) == 0
+    assert L.emu_weights_mfma_major(ctx.h, _lib.Q8_0, src.ptr, raw.size, rows, cols, dst.ptr) == _lib.EMU_E_UNSUPPORTED
+    assert L.emu_weights_mfma_major(ctx.h, Q6, src.ptr, raw.size - 210, rows, cols, dst.ptr) == _lib.EMU_E_SHAPE
+    assert L.emu_weights_mfma_major(ctx.h, Q6, src.ptr, raw.size, rows, 1000, dst.ptr) == _lib.EMU_E_SHORT
+    assert L.emu_weights_mfma_major(ctx.h, Q6, src.ptr, raw.size, rows, cols, src.ptr) == _lib.EMU_E_ARG
+    x, y = ctx.upload(np.zeros(8 * cols, np.float32)), ctx.alloc(8 * rows * 4)
+    ctx.check(L.emu_weights_mfma_major(ctx.h, Q6, src.ptr, raw.size, rows, cols, dst.ptr), "mfma_major")
+    # the flag is for 2..8 tokens on the matrix-core widths, with the padded length
+    assert L.emu_qmatvec(ctx.h, Q6, dst.ptr, n, rows, cols, x.ptr, cols, 1, y.ptr,
+                         _lib.EMU_MV_MFMA_MAJOR) == _lib.EMU_E_UNSUPPORTED
+    assert L.emu_qmatvec(ctx.h, Q6, dst.ptr, n - 1, rows, cols, x.ptr, 2 * cols, 2, y.ptr,
+                         _lib.EMU_MV_MFMA_MAJOR) == _lib.EMU_E_SHAPE
+    assert L.emu_qmatvec(ctx.h, Q6, dst.ptr, n, rows, cols, x.ptr, 2 * cols, 2, y.ptr,
+                         _lib.EMU_MV_MFMA_MAJOR | _lib.EMU_MV_LANE_MAJOR) == _lib.EMU_E_ARG
+
+
+@pytest.mark.parametrize("rows,cols,n_tok", [(33, 4096, 2), (4096, 4096, 8), (37, 12288, 5), (6144, 4096, 3),
+                                             (77, 2816, 8), (100, 2048, 7)])
+def test_mfma_major_matvec_equals_gguf_order_bit_for_bit(ctx, rows, cols, n_tok):
+    """Same codes in the same operand registers: the operand-order copy gives
+    the GGUF-order matrix-core kernel's bits, plain, accumulated, normalised
+    and SwiGLU."""
+    raw = weights(rows, cols, 5 * rows + cols + n_tok)
+    rng = np.random.default_rng(rows + 2 * n_tok)
+    x = rng.normal(size=(n_tok, cols)).astype(np.float32)
+    base = rng.normal(size=(n_tok, rows)).astype(np.float32)
+    gain = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    L = ctx.lib
+    n = L.emu_weights_mfma_major_bytes(rows, cols)
+    w = ctx.upload(raw)
+    mm = ctx.alloc(n)
+    ctx.check(L.emu_weights_mfma_major(ctx.h, Q6, w.ptr, raw.size, rows, cols, mm.ptr), "mfma_major")
+    bx, bg = ctx.upload(x), ctx.upload(gain)
+
+    def run(wp, wlen, flags, acc):
+        y = ctx.upload(base.copy()) if acc else ctx.alloc(n_tok * rows * 4)
+        ctx.check(L.emu_qmatvec(ctx.h, Q6, wp, wlen, rows, cols, bx.ptr, n_tok * cols, n_tok, y.ptr,
+                                flags | (_lib.EMU_MV_ACCUMULATE if acc else 0)), "qmatvec")
+        return y.read(np.uint32)
+
+    for acc in (False, True):
+        assert np.array_equal(run(w.ptr, raw.size, 0, acc), run(mm.ptr, n, _lib.EMU_MV_MFMA_MAJOR, acc))
+
+    def run_fused(wp, up, flags):
+        y = ctx.alloc(n_tok * rows * 4)
+        ctx.check(L.emu_qmatvec_fused(ctx.h, Q6, wp, up, rows, cols, bx.ptr, n_tok, bg.ptr, 1e-6, y.ptr, flags),
+                  "fused")
+        return y.read(np.uint32)
+
+    assert np.array_equal(run_fused(w.ptr, None, 0), run_fused(mm.ptr, None, _lib.EMU_MV_MFMA_MAJOR))
+    assert np.array_equal(run_fused(w.ptr, w.ptr, 0), run_fused(mm.ptr, mm.ptr, _lib.EMU_MV_MFMA_MAJOR))

@@ -594,6 +594,47 @@ def test_lane_major_layout_gives_each_unit_its_codes():
     assert checked == 48 * 256
 
 
+def test_mfma_major_layout_gives_each_lane_its_operand_codes():
+    """The matrix-core operand layout of Q6_K (the multi-token device copy),
+    read where the kernel's loader reads -- lane l = 32 kh + j's 24 code words
+    at 1024 (w // 4) + 16 l + 4 (w % 4), the row's scales at 6144 + 16 j and
+    d at 6656 + 2 j of each 6720-byte (tile, block) chunk -- and decoded as
+    the kernel decodes (sub-blocks 4g..4g+2: the low six bits of words 6g+3p,
+    6g+3p+1, 6g+3p+2; sub-block 4g+3: their top two bits, in that order),
+    dequantizes, weight for weight, to the oracle's GGUF decoder
+    (spm-gguf/src/tensor.rs:103-139), the padding rows of the last tile
+    repeating the last row."""
+    rng = np.random.default_rng(96)
+    rows, cols = 37, 512  # two tiles, the second padded
+    raw = rng.integers(0, 256, size=rows * cols // 256 * 210, dtype=np.uint8)
+    raw.reshape(-1, 210)[:, 208:210] = np.frombuffer(
+        rng.uniform(0.5, 2.0, raw.size // 210).astype(np.float16).tobytes(), np.uint8).reshape(-1, 2)
+    mm = npref.mfma_major_q6k(raw, rows, cols)
+    nblk, ntile = cols // 256, (rows + 31) // 32
+    assert mm.size == ntile * nblk * 6720
+    ref = oracle.decode(Q6, raw).reshape(rows, cols)
+    checked = 0
+    for t in range(ntile):
+        for k in range(nblk):
+            c = mm[6720 * (t * nblk + k):6720 * (t * nblk + k + 1)]
+            for lane in range(64):
+                j, kh = lane % 32, lane // 32
+                row = min(32 * t + j, rows - 1)
+                words = [c[1024 * (w // 4) + 16 * lane + 4 * (w % 4):][:4].astype(np.int32) for w in range(24)]
+                sc = c[6144 + 16 * j:6160 + 16 * j].view(np.int8)
+                d = c[6656 + 2 * j:6658 + 2 * j].view(np.float16)[0].astype(np.float32)
+                for sb in range(16):
+                    g, jj = sb // 4, sb % 4
+                    for p in range(2):
+                        w0, w1, w2 = words[6 * g + 3 * p:6 * g + 3 * p + 3]
+                        code = [w0 & 63, w1 & 63, w2 & 63, (w0 >> 6) | (w1 >> 6) << 2 | (w2 >> 6) << 4][jj]
+                        wt = (d * np.float32(sc[sb])) * (code.astype(np.float32) - np.float32(32))
+                        cols_here = 256 * k + 16 * sb + 8 * kh + 4 * p + np.arange(4)
+                        assert np.array_equal(wt, ref[row, cols_here]), (t, k, lane, sb, p)
+                        checked += 4
+    assert checked == ntile * 32 * cols
+
+
 def _moe_weights(cfg, rng, w_extra=None):
     """Seeded blobs in the layer layout of or_moe_layer_bytes for cfg."""
     H, E, F = cfg.hidden, cfg.n_experts, cfg.expert_ff
