@@ -72,18 +72,26 @@ struct emu_model {
         return *lane_major ? lm + (w - base) : w;
     }
     // Matrix-core operand copy (emu_mfma_major_q6k) of the Q6_K matrices the
-    // 2..8-token chain reads: the layers' matrices with whole 32-row tiles at
-    // the same offsets as in `base`, the output matrix (padded to whole
-    // tiles) at off_embed.  Rebuilt with the lane-major copy.
+    // chained matrix-core matvecs read: each listed matrix (its offset in
+    // `base`, rows, cols) has its copy at `dst` in `mm`, rows padded to whole
+    // 32-row tiles.  Rebuilt with the lane-major copy.
+    struct MmEntry {
+        size_t src, dst;
+        uint32_t rows, cols;
+    };
     uint8_t *mm = nullptr;
-    bool mm_takes(uint32_t rows, uint32_t cols) const
+    std::vector<MmEntry> mm_map;
+    // The matrix a chained matvec reads, and whether it is the operand copy.
+    const uint8_t *mm_or(const uint8_t *w, int *mfma_major) const
     {
-        return mm && rows % 32 == 0 && emu_mfma_shape_ok(cfg.encoding, (int)cols);
-    }
-    const uint8_t *mm_or(const uint8_t *w, uint32_t rows, uint32_t cols, int *mfma_major) const
-    {
-        *mfma_major = mm_takes(rows, cols);
-        return *mfma_major ? mm + (w - base) : w;
+        const size_t off = (size_t)(w - base);
+        for (const MmEntry &e : mm_map)
+            if (e.src == off) {
+                *mfma_major = 1;
+                return mm + e.dst;
+            }
+        *mfma_major = 0;
+        return w;
     }
 };
 
@@ -762,8 +770,8 @@ int run_chain(emu_session *s)
     };
     auto matvec = [&](const uint8_t *w, const uint8_t *w_up, size_t rb, int rows, int cols, int *nks) {
         QmvArgs q{};
-        q.w = m->mm_or(w, (uint32_t)rows, (uint32_t)cols, &q.mfma_major);
-        q.w_up = w_up ? m->mm_or(w_up, (uint32_t)rows, (uint32_t)cols, &q.mfma_major) : nullptr;
+        q.w = m->mm_or(w, &q.mfma_major);
+        q.w_up = w_up ? m->mm_or(w_up, &q.mfma_major) : nullptr;
         q.row_bytes = rb;
         q.rows = rows;
         q.cols = cols;
@@ -798,11 +806,7 @@ int run_chain(emu_session *s)
         if ((st = link(1, nks, 1, s->state, nullptr, H, next, true)) != EMU_OK) return st;
     }
     QmvArgs out{};
-    out.w = m->base + (c.tied ? m->off_embed : m->off_output);
-    if (m->mm && emu_mfma_shape_ok(c.encoding, H)) { // the padded output copy (any row count)
-        out.w = m->mm + m->off_embed;
-        out.mfma_major = 1;
-    }
+    out.w = m->mm_or(m->base + (c.tied ? m->off_embed : m->off_output), &out.mfma_major);
     out.row_bytes = m->rb_h;
     out.rows = (int)c.vocab;
     out.cols = H;
@@ -900,7 +904,7 @@ int run_moe(emu_session *s)
             }
             if ((st = emu_mfma_link(ctx, l)) != EMU_OK) return st;
             QmvArgs q{};
-            q.w = lw + m->off_q;
+            q.w = m->mm_or(lw + m->off_q, &q.mfma_major);
             q.row_bytes = m->rb_h;
             q.rows = (int)(QW + 2 * KW);
             q.cols = (int)H;
@@ -916,7 +920,7 @@ int run_moe(emu_session *s)
             al.xs = xs;
             if ((st = emu_launch_attn(ctx, al)) != EMU_OK) return st;
             QmvArgs o{};
-            o.w = lw + m->off_o;
+            o.w = m->mm_or(lw + m->off_o, &o.mfma_major);
             o.row_bytes = m->rb_q;
             o.rows = (int)H;
             o.cols = (int)QW;
@@ -996,8 +1000,8 @@ int run_moe(emu_session *s)
                 // down's partial sums join the residual in the next layer's
                 // link (the last layer's here, before the expert sum)
                 QmvArgs g{};
-                g.w = lw + m->off_sg;
-                g.w_up = lw + m->off_su;
+                g.w = m->mm_or(lw + m->off_sg, &g.mfma_major);
+                g.w_up = m->mm_or(lw + m->off_su, &g.mfma_major);
                 g.row_bytes = m->rb_h;
                 g.rows = (int)c.shared_ff;
                 g.cols = (int)H;
@@ -1016,7 +1020,7 @@ int run_moe(emu_session *s)
                 la.act = EMU_ACT_GELU_TANH;
                 if ((st = emu_mfma_link(ctx, la)) != EMU_OK) return st;
                 QmvArgs dq{};
-                dq.w = lw + m->off_sd;
+                dq.w = m->mm_or(lw + m->off_sd, &dq.mfma_major);
                 dq.row_bytes = m->rb_sf;
                 dq.rows = (int)H;
                 dq.cols = (int)c.shared_ff;
@@ -1075,6 +1079,7 @@ int run_moe(emu_session *s)
     }
     QmvArgs out{};
     out.w = m->base + (c.tied ? m->off_embed : m->off_output); // Granite: tied (model.rs:403-407)
+    if (chain) out.w = m->mm_or(out.w, &out.mfma_major); // the matrix-core launch below reads either order
     out.row_bytes = m->rb_h;
     out.rows = (int)c.vocab;
     out.cols = (int)H;
@@ -1199,11 +1204,9 @@ int model_sync(emu_model *m)
     const emu_model_config &c = m->cfg;
     const uint32_t QW = c.heads * c.head_dim, KW = c.kv_heads * c.head_dim;
     int st;
+    for (const emu_model::MmEntry &e : m->mm_map)
+        if ((st = emu_mfma_major_q6k(ctx, m->base + e.src, e.rows, e.cols, m->mm + e.dst)) != EMU_OK) return st;
     auto put = [&](size_t off, uint32_t rows, uint32_t cols, size_t rb) -> int {
-        if (m->mm_takes(rows, cols)) {
-            const int st2 = emu_mfma_major_q6k(ctx, m->base + off, rows, cols, m->mm + off);
-            if (st2 != EMU_OK) return st2;
-        }
         if (!m->lm_takes(cols)) return EMU_OK;
         return emu_lane_major_q6k(ctx, m->base + off, (size_t)rows * rb / 210, m->lm + off);
     };
@@ -1219,10 +1222,6 @@ int model_sync(emu_model *m)
     const size_t out_src = c.tied ? m->off_embed : m->off_output;
     if (m->lm_takes(c.hidden)) {
         if ((st = emu_lane_major_q6k(ctx, m->base + out_src, m->embed_bytes / 210, m->lm + m->off_embed)) != EMU_OK)
-            return st;
-    }
-    if (m->mm && emu_mfma_shape_ok(c.encoding, (int)c.hidden)) { // the output matrix, padded to whole tiles
-        if ((st = emu_mfma_major_q6k(ctx, m->base + out_src, c.vocab, c.hidden, m->mm + m->off_embed)) != EMU_OK)
             return st;
     }
     if ((st = emu_ctx_sync(ctx)) != EMU_OK) return st;
@@ -1407,21 +1406,44 @@ extern "C" int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_m
         }
         m->lm = static_cast<uint8_t *>(q);
     }
-    // The matrix-core operand copy: dense Q6_K models whose widths the
-    // multi-token chain takes (the layers' region plus the padded output).
-    const bool mm_any = !moe && c.encoding == EMU_ENC_Q6_K &&
-                        (emu_mfma_shape_ok(c.encoding, (int)c.hidden) || emu_mfma_shape_ok(c.encoding, (int)QW) ||
-                         emu_mfma_shape_ok(c.encoding, (int)c.ffn));
-    if (mm_any) {
-        void *q = nullptr;
-        const size_t out_mm = emu_mfma_shape_ok(c.encoding, (int)c.hidden) ? emu_mfma_major_bytes(c.vocab, c.hidden) : 0;
-        if ((st = emu_malloc(ctx, m->off_embed + out_mm, &q)) != EMU_OK) {
-            if (m->lm) emu_free(ctx, m->lm);
-            emu_free(ctx, m->base);
-            delete m;
-            return st;
+    // The matrix-core operand copy: every Q6_K matrix that a chained
+    // matrix-core matvec reads (a width it takes, whole 32-row tiles but for
+    // the output): q|k|v and o, the dense FFN or the Gemma shared FFN, and
+    // the output.
+    if (c.encoding == EMU_ENC_Q6_K) {
+        size_t mm_off = 0;
+        auto add = [&](size_t src, uint32_t rows, uint32_t cols, bool any_rows) {
+            if (!emu_mfma_shape_ok(c.encoding, (int)cols) || (!any_rows && rows % 32 != 0)) return;
+            m->mm_map.push_back({src, mm_off, rows, cols});
+            mm_off = align_up(mm_off + emu_mfma_major_bytes(rows, cols), 256);
+        };
+        for (uint32_t l = 0; l < c.layers; ++l) {
+            const size_t lo = m->off_layers + (size_t)l * m->layer_bytes;
+            add(lo + m->off_q, QW + 2 * KW, c.hidden, false);
+            add(lo + m->off_o, c.hidden, QW, false);
+            if (!moe) {
+                add(lo + m->off_g, c.ffn, c.hidden, false);
+                add(lo + m->off_u, c.ffn, c.hidden, false);
+                add(lo + m->off_d, c.hidden, c.ffn, false);
+            } else if (c.gemma && c.shared_ff) {
+                add(lo + m->off_sg, c.shared_ff, c.hidden, false);
+                add(lo + m->off_su, c.shared_ff, c.hidden, false);
+                add(lo + m->off_sd, c.hidden, c.shared_ff, false);
+            }
         }
-        m->mm = static_cast<uint8_t *>(q);
+        add(c.tied ? m->off_embed : m->off_output, c.vocab, c.hidden, true);
+        if (mm_off) {
+            void *q = nullptr;
+            if ((st = emu_malloc(ctx, mm_off, &q)) != EMU_OK) {
+                if (m->lm) emu_free(ctx, m->lm);
+                emu_free(ctx, m->base);
+                delete m;
+                return st;
+            }
+            m->mm = static_cast<uint8_t *>(q);
+        } else {
+            m->mm_map.clear();
+        }
     }
     *out = m;
     return EMU_OK;
