@@ -63,23 +63,25 @@ struct AttnArgs {
     int window;             // attend to the last `window` positions only (0: all)
 };
 
-// A value of q|k|v: one plain load (MS false), or the sum of its ns <= 12
-// partial-sum slices (as many as the multi-token matvec makes) in slice order.  Straight-line code either way: slots
-// past ns load slice 0 and are not added, so all of a thread's q|k|v loads
-// go out before the first wait (a branch on ns between two values' loads
-// would put a full memory round trip between them).
+// A value of q|k|v: one plain load (MS 1), or the sum of its ns <= MS
+// partial-sum slices (as many as the multi-token matvec makes) in slice
+// order, MS being 4 or 12 (the launch takes the smaller that holds ns).
+// Straight-line code either way: slots past ns load slice 0 and are not
+// added, so all of a thread's q|k|v loads go out before the first wait (a
+// branch on ns between two values' loads would put a full memory round trip
+// between them).
 constexpr int kMaxSlices = 12;
-template <bool MS> __device__ __forceinline__ float qkv_at(const float *p, int ns, size_t stride)
+template <int MS> __device__ __forceinline__ float qkv_at(const float *p, int ns, size_t stride)
 {
-    if constexpr (!MS) {
+    if constexpr (MS == 1) {
         return p[0];
     } else {
-        float q[kMaxSlices];
+        float q[MS];
 #pragma unroll
-        for (int s = 0; s < kMaxSlices; ++s) q[s] = p[(s < ns ? s : 0) * stride];
+        for (int s = 0; s < MS; ++s) q[s] = p[(s < ns ? s : 0) * stride];
         float v = q[0];
 #pragma unroll
-        for (int s = 1; s < kMaxSlices; ++s) v = s < ns ? v + q[s] : v;
+        for (int s = 1; s < MS; ++s) v = s < ns ? v + q[s] : v;
         return v;
     }
 }
@@ -146,7 +148,7 @@ __device__ __forceinline__ void rotate(float &l, float &r, float2 cs, int fma_fo
 // every load of the head (values, gains, rotation table), finish() does the
 // arithmetic, so a wavefront with several heads has all of their loads in
 // flight before the first one is used.
-template <int HD, bool MS> struct HeadPrep {
+template <int HD, int MS> struct HeadPrep {
     static constexpr int NP = HD / 2;
     static constexpr int PPL = (NP + EMU_WAVE - 1) / EMU_WAVE;
     float a[PPL], b[PPL], ga[PPL], gb[PPL];
@@ -266,7 +268,7 @@ __device__ __forceinline__ void unpack_row(const V &raw, float (&out)[EPL])
     }
 }
 
-template <int HD, bool F16, int GQP, bool MS>
+template <int HD, bool F16, int GQP, int MS>
 __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
 {
     using kv_t = typename std::conditional<F16, __half, float>::type;
@@ -587,7 +589,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
     if (tid == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int HD, bool F16, bool MS>
+template <int HD, bool F16, int MS>
 void launch_ms(const AttnArgs &a, dim3 grid, hipStream_t stream, int gq)
 {
     if (gq <= 1)
@@ -603,8 +605,9 @@ void launch_ms(const AttnArgs &a, dim3 grid, hipStream_t stream, int gq)
 template <int HD, bool F16>
 void launch_hd(const AttnArgs &a, dim3 grid, hipStream_t stream, int gq)
 {
-    if (a.qkv_slices > 1) launch_ms<HD, F16, true>(a, grid, stream, gq);
-    else launch_ms<HD, F16, false>(a, grid, stream, gq);
+    if (a.qkv_slices > 4) launch_ms<HD, F16, kMaxSlices>(a, grid, stream, gq);
+    else if (a.qkv_slices > 1) launch_ms<HD, F16, 4>(a, grid, stream, gq);
+    else launch_ms<HD, F16, 1>(a, grid, stream, gq);
 }
 
 } // namespace
