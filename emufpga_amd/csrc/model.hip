@@ -413,21 +413,40 @@ __global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)
         return i < W ? *reinterpret_cast<const float4 *>(base + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     };
     const bool chained = a.opart != nullptr;
-    float4 xv[QW], ov[QW], sv[QW], rw[NQ];
+    // The o projection's slices 1..kGateSlices-1 load with the first loads
+    // (a slot past o_nks reads slice 0 and is not added): a loop over the
+    // slices would wait a round trip per slice.
+    constexpr int kGateSlices = 4;
+    const size_t stride = (size_t)kMaxTokChain * W; // floats between slices
+    float4 xv[QW], ov[QW], sv[QW], rw[NQ], os[kGateSlices - 1][QW];
 #pragma unroll
     for (int j = 0; j < QW; ++j) {
         const int q = w + NW * j;
-        xv[j] = q < NQ ? ld(xr, q) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        ov[j] = q < NQ && chained ? ld(a.opart + (size_t)c * W, q) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        sv[j] = q < NQ ? ld(GEMMA ? a.rscale : a.gain, q) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        xv[j] = q < NQ ? ld(xr, q) : z;
+        ov[j] = q < NQ && chained ? ld(a.opart + (size_t)c * W, q) : z;
+#pragma unroll
+        for (int s = 1; s < kGateSlices; ++s)
+            os[s - 1][j] = q < NQ && chained ? ld(a.opart + (s < a.o_nks ? s : 0) * stride + (size_t)c * W, q) : z;
+        sv[j] = q < NQ ? ld(GEMMA ? a.rscale : a.gain, q) : z;
     }
 #pragma unroll
     for (int q = 0; q < NQ; ++q) rw[q] = ld(rr, q);
     if (chained) {
         // the o projection's slices added in order, then r + v * o_scale
         // (what the matvec's finishing pass would do)
-        const size_t stride = (size_t)kMaxTokChain * W; // floats between slices
-        for (int s = 1; s < a.o_nks; ++s) {
+#pragma unroll
+        for (int s = 1; s < kGateSlices; ++s) {
+            if (s >= a.o_nks) break; // uniform
+#pragma unroll
+            for (int j = 0; j < QW; ++j) {
+                ov[j].x += os[s - 1][j].x;
+                ov[j].y += os[s - 1][j].y;
+                ov[j].z += os[s - 1][j].z;
+                ov[j].w += os[s - 1][j].w;
+            }
+        }
+        for (int s = kGateSlices; s < a.o_nks; ++s) { // wider o projections
 #pragma unroll
             for (int j = 0; j < QW; ++j) {
                 const int q = w + NW * j;
