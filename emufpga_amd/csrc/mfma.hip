@@ -501,6 +501,20 @@ struct FinishArgs {
     int key_stride, tie_last;
 };
 
+// A row's slices added in slice order, every load issued before the first
+// add (slots past n read slice 0 and are dropped): one memory round trip.
+template <int MAXS> __device__ __forceinline__ float slice_sum1(const float *p, size_t stride, int n)
+{
+    float q[MAXS];
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) q[s] = p[(s < n ? s : 0) * stride];
+    float v = q[0];
+#pragma unroll
+    for (int s = 1; s < MAXS; ++s) v = s < n ? v + q[s] : v;
+    return v;
+}
+
+template <int MAXS>
 __global__ __launch_bounds__(kFinishThreads) void mfma_finish_kernel(FinishArgs a)
 {
     const int t = blockIdx.y, row = blockIdx.x * kFinishThreads + threadIdx.x;
@@ -509,12 +523,9 @@ __global__ __launch_bounds__(kFinishThreads) void mfma_finish_kernel(FinishArgs 
     if (ok) {
         const size_t stride = (size_t)a.nmat * kMaxTok * a.rows;
         const float *p = a.part + (size_t)t * a.rows + row;
-        v = p[0];
-        for (int k = 1; k < a.nks; ++k) v += p[k * stride];
+        v = slice_sum1<MAXS>(p, stride, a.nks);
         if (a.nmat == 2) {
-            const float *pu = p + (size_t)kMaxTok * a.rows;
-            float up = pu[0];
-            for (int k = 1; k < a.nks; ++k) up += pu[k * stride];
+            const float up = slice_sum1<MAXS>(p + (size_t)kMaxTok * a.rows, stride, a.nks);
             v = emu_glu(v, up, a.act);
         }
         v = emu_out_epi(v, a.out_div, a.softcap);
@@ -722,8 +733,12 @@ int emu_mfma_finish(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int
     fa.keys = q.keys;
     fa.key_stride = q.key_stride;
     fa.tie_last = q.tie_last;
-    hipLaunchKernelGGL(mfma_finish_kernel, dim3((unsigned)gx, (unsigned)n_tok), dim3(kFinishThreads), 0,
-                       ctx->stream, fa);
+    if (fa.nks <= 4)
+        hipLaunchKernelGGL(mfma_finish_kernel<4>, dim3((unsigned)gx, (unsigned)n_tok), dim3(kFinishThreads), 0,
+                           ctx->stream, fa);
+    else
+        hipLaunchKernelGGL(mfma_finish_kernel<kMaxSlices>, dim3((unsigned)gx, (unsigned)n_tok), dim3(kFinishThreads),
+                           0, ctx->stream, fa);
     EMU_LAUNCH_CHECK(ctx);
     if (key_slots) *key_slots = gx;
     return EMU_OK;
