@@ -486,7 +486,10 @@ __device__ __forceinline__ float emu_pick4(const float (&v)[4], int j)
 // v_readlane); then k rounds of argmax in total order, lower id first on
 // ties, with the winner removed; weights are the selected probabilities
 // over their left-fold total, in selection order.
-__device__ __forceinline__ void emu_route_token(const float *p, int n_experts, int k, int32_t *ids, float *weights)
+// ids_sorted / weights_sorted (optional): the same k routes again, in
+// ascending expert id.
+__device__ __forceinline__ void emu_route_token(const float *p, int n_experts, int k, int32_t *ids, float *weights,
+                                                int32_t *ids_sorted = nullptr, float *weights_sorted = nullptr)
 {
     if (threadIdx.x >= EMU_WAVE) return;
     const int lane = threadIdx.x;
@@ -543,6 +546,14 @@ __device__ __forceinline__ void emu_route_token(const float *p, int n_experts, i
     if (lane < k) {
         ids[lane] = my_id;
         weights[lane] = my_sel / total;
+    }
+    if (ids_sorted) { // the ids are distinct: a route's place is the count of smaller ids
+        int rank = 0;
+        for (int r = 0; r < k; ++r) rank += __builtin_amdgcn_readlane(my_id, r) < my_id ? 1 : 0;
+        if (lane < k) {
+            ids_sorted[rank] = my_id;
+            weights_sorted[rank] = my_sel / total;
+        }
     }
 }
 
@@ -830,6 +841,7 @@ struct EmuMfmaLink {
     const float *m_wts;
     int m_k, m_experts;
     float m_scale;
+    int m_sorted; // the routes come in ascending expert id (no reordering)
     // Mode 0 only, optional, before the expert sum: a dense FFN's down
     // projection, as the last matvec's d_nks partial-sum slices (one
     // matrix), joins x as x + v * d_scale.

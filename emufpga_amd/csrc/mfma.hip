@@ -80,6 +80,7 @@ struct LinkArgs {
     const float *m_wts;
     int m_k, m_experts;
     float m_scale;
+    int m_sorted; // the routes come in ascending expert id (no reordering)
     // kLinkInput, optional, before the expert sum: a dense FFN's down
     // projection (part, d_nks slices of one matrix) joins x as x + v * d_scale.
     const float *d_part;
@@ -152,7 +153,21 @@ __global__ __launch_bounds__(kLinkThreads) void mfma_link_kernel(LinkArgs a)
             if (a.m_contrib) {
                 int order[8];
                 float w[8];
-                const int n = emu_route_order(a.m_ids + t * a.m_k, a.m_wts + t * a.m_k, a.m_k, a.m_experts, order, w);
+                int n = 0;
+                if (a.m_sorted) { // no reordering: the loads below wait for nothing
+                    const int32_t *ip = a.m_ids + t * a.m_k;
+                    const float *wp = a.m_wts + t * a.m_k;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const bool in = i < a.m_k;
+                        const int id = in ? ip[i] : -1;
+                        order[i] = in ? i : 0;
+                        w[i] = in ? wp[i] : 0.0f;
+                        n += in && id >= 0 && id < a.m_experts ? 1 : 0; // ascending: the valid ones lead
+                    }
+                } else {
+                    n = emu_route_order(a.m_ids + t * a.m_k, a.m_wts + t * a.m_k, a.m_k, a.m_experts, order, w);
+                }
                 float cv[8][8];
 #pragma unroll
                 for (int i = 0; i < 8; ++i)
@@ -657,6 +672,7 @@ int emu_mfma_link(emu_ctx *ctx, const EmuMfmaLink &l)
     a.xa = l.limbs ? w.xa : nullptr;
     a.xs = l.limbs ? w.xs : nullptr;
     a.m_contrib = l.mode == kLinkInput ? l.m_contrib : nullptr;
+    a.m_sorted = l.m_sorted;
     a.m_ids = l.m_ids;
     a.m_wts = l.m_wts;
     a.m_k = l.m_k;

@@ -109,7 +109,7 @@ struct emu_session {
           *partial = nullptr, *rope = nullptr;
     // mixture-of-experts scratch: normalised input, router logits, routes,
     // expert output, and the selected-expert FFN's workspace
-    float *xn = nullptr, *rlog = nullptr, *rwts = nullptr;
+    float *xn = nullptr, *rlog = nullptr, *rwts = nullptr, *rwts_s = nullptr;
     // Gemma form: the router's input and the global layers' RoPE table
     float *rope2 = nullptr;
     uint32_t *gate_counters = nullptr; // [client] arrivals at the MoE gate
@@ -120,7 +120,7 @@ struct emu_session {
     int32_t *trace_ids = nullptr;
     float *trace_w = nullptr;
     uint32_t trace_cap = 0;
-    int32_t *rids = nullptr;
+    int32_t *rids = nullptr, *rids_s = nullptr; // routes in top-k order (traced) and in ascending id (used)
     void *moe_ws = nullptr;
     size_t moe_ws_bytes = 0;
     std::vector<uint32_t> host_pos;
@@ -372,6 +372,8 @@ struct GateArgs {
     uint32_t *counters;  // [client] arrivals, zero between launches
     int32_t *ids;
     float *weights;
+    int32_t *ids_sorted; // and again in ascending expert id (null: not wanted)
+    float *weights_sorted;
     ZipfRoute z;
 };
 
@@ -519,7 +521,9 @@ __global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)
         p[j] = __hip_atomic_load(a.logits + (size_t)c * E + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (w == 0) {
-        emu_route_token(p, E, a.k, a.ids + (size_t)c * a.k, a.weights + (size_t)c * a.k);
+        emu_route_token(p, E, a.k, a.ids + (size_t)c * a.k, a.weights + (size_t)c * a.k,
+                        a.ids_sorted ? a.ids_sorted + (size_t)c * a.k : nullptr,
+                        a.weights_sorted ? a.weights_sorted + (size_t)c * a.k : nullptr);
         return;
     }
     if (tid == EMU_WAVE) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -915,8 +919,9 @@ int run_moe(emu_session *s)
                 l.d_nks = sd_nks;
                 l.d_scale = c.residual_scale;
                 l.m_contrib = emu_moe_contrib(s->moe_ws, (uint32_t)n, K, c.expert_ff);
-                l.m_ids = s->rids;
-                l.m_wts = s->rwts;
+                l.m_ids = s->rids_s;
+                l.m_wts = s->rwts_s;
+                l.m_sorted = 1;
                 l.m_k = (int)K;
                 l.m_experts = (int)E;
                 l.m_scale = c.residual_scale;
@@ -998,6 +1003,8 @@ int run_moe(emu_session *s)
         ga.counters = s->gate_counters;
         ga.ids = s->rids;
         ga.weights = s->rwts;
+        ga.ids_sorted = s->rids_s;
+        ga.weights_sorted = s->rwts_s;
         ga.z = zr;
         if (m->gemma()) {
             // router and expert inputs from the residual before the shared FFN
@@ -1092,7 +1099,7 @@ int run_moe(emu_session *s)
         // chained: the next layer's link adds the expert sum (the last layer's
         // is combined here, for the output matvec)
         const bool combine = !chain || layer + 1 == c.layers;
-        if ((st = emu_moe_ffn_resid(ctx, &d, s->xn, (uint32_t)n, s->rids, s->rwts, s->moe_ws, s->moe_ws_bytes,
+        if ((st = emu_moe_ffn_resid(ctx, &d, s->xn, (uint32_t)n, s->rids_s, s->rwts_s, s->moe_ws, s->moe_ws_bytes,
                                     s->state, c.residual_scale, combine, planes)) != EMU_OK)
             return st;
     }
@@ -1784,6 +1791,8 @@ extern "C" int emu_session_create(emu_model *m, uint32_t n_clients, uint32_t con
         alloc((void **)&s->rlog, sizeof(float) * n_clients * c.n_experts);
         alloc((void **)&s->rids, sizeof(int32_t) * n_clients * c.experts_used);
         alloc((void **)&s->rwts, sizeof(float) * n_clients * c.experts_used);
+        alloc((void **)&s->rids_s, sizeof(int32_t) * n_clients * c.experts_used);
+        alloc((void **)&s->rwts_s, sizeof(float) * n_clients * c.experts_used);
         s->moe_ws_bytes = emu_moe_workspace_bytes(n_clients, c.experts_used, c.hidden, c.expert_ff);
         alloc(&s->moe_ws, s->moe_ws_bytes);
     }
@@ -1844,8 +1853,8 @@ extern "C" int emu_session_destroy(emu_session *s)
     if (s->graph) (void)hipGraphDestroy(s->graph);
     void *ptrs[] = {s->k_cache, s->v_cache, s->positions, s->tokens, s->steps, s->last, s->prompt, s->hist,
                     s->ctrl, s->counters, s->state, s->qkv, s->attn, s->act, s->logits, s->keys, s->partial,
-                    s->rope, s->xn, s->rlog, s->rids, s->rwts, s->moe_ws, s->gate_counters, s->rope2, s->trace_ids,
-                    s->trace_w};
+                    s->rope, s->xn, s->rlog, s->rids, s->rwts, s->rids_s, s->rwts_s, s->moe_ws, s->gate_counters,
+                    s->rope2, s->trace_ids, s->trace_w};
     for (void *p : ptrs) emu_free(ctx, p);
     delete s;
     return EMU_OK;
