@@ -390,11 +390,13 @@ struct GateArgs {
 // the device-coherent level by an agent-scope store, every store completes
 // before the arrival counter moves, and the client's last workgroup to
 // arrive routes (wavefront 0: softmax and top-k over the logits read back by
-// agent-scope loads) while wavefronts 1-3 write the expert input (also as
-// the experts' limb planes, one 256-column span per wavefront at a time),
-// chained the updated residual (and, in the Gemma form, the shared FFN's
-// input as its matvec's operands), and reset the counter.  No other
-// workgroup of the client writes the residual, so all of them read it whole.
+// agent-scope loads) while its wavefronts 1-3 write, chained, the updated
+// residual and reset the counter.  No other workgroup of the client writes
+// the residual, so all of them read it whole.  After arriving, wavefronts 1-3
+// of every workgroup write the expert input (also as the experts' limb
+// planes, one 256-column span per wavefront, and in the Gemma form the
+// shared FFN's input as its matvec's operands), the spans dealt one per
+// wavefront across the workgroups.
 template <int NQ, bool GEMMA>
 __global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)
 {
@@ -434,6 +436,15 @@ __global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)
     }
 #pragma unroll
     for (int q = 0; q < NQ; ++q) rw[q] = ld(rr, q);
+    // this wavefront's first expert-input column group (wavefronts 1..NW-1)
+    // and, in the Gemma form, its gains
+    const int nq = (W + 4 * EMU_WAVE - 1) / (4 * EMU_WAVE);
+    const int q0 = w > 0 ? (w - 1) * (int)gridDim.x + (int)blockIdx.x : nq;
+    float4 g2 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), fg = g2;
+    if (GEMMA && q0 < nq && 4 * lane + 4 * EMU_WAVE * q0 < W) {
+        g2 = *reinterpret_cast<const float4 *>(a.gain + 4 * lane + 4 * EMU_WAVE * q0);
+        if (a.ffn_xa) fg = *reinterpret_cast<const float4 *>(a.ffn_gain + 4 * lane + 4 * EMU_WAVE * q0);
+    }
     if (chained) {
         // the o projection's slices added in order, then r + v * o_scale
         // (what the matvec's finishing pass would do)
@@ -516,52 +527,52 @@ __global__ __launch_bounds__(kThreads) void moe_gate_kernel(GateArgs a)
     uint32_t *counter = a.counters + c;
     if (tid == 0) arrived = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (arrived != gridDim.x - 1) return;
-    for (int j = tid; j < E; j += kThreads)
-        p[j] = __hip_atomic_load(a.logits + (size_t)c * E + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (w == 0) {
-        emu_route_token(p, E, a.k, a.ids + (size_t)c * a.k, a.weights + (size_t)c * a.k,
-                        a.ids_sorted ? a.ids_sorted + (size_t)c * a.k : nullptr,
-                        a.weights_sorted ? a.weights_sorted + (size_t)c * a.k : nullptr);
+    const bool last = arrived == gridDim.x - 1; // uniform: from LDS
+    if (last) {
+        for (int j = tid; j < E; j += kThreads)
+            p[j] = __hip_atomic_load(a.logits + (size_t)c * E + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (w == 0) {
+            emu_route_token(p, E, a.k, a.ids + (size_t)c * a.k, a.weights + (size_t)c * a.k,
+                            a.ids_sorted ? a.ids_sorted + (size_t)c * a.k : nullptr,
+                            a.weights_sorted ? a.weights_sorted + (size_t)c * a.k : nullptr);
+            return;
+        }
+        if (tid == EMU_WAVE) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (chained) { // the updated residual, once every workgroup has read it
+            for (int q = w - 1; q < nq; q += NW - 1) {
+                const int i = 4 * lane + 4 * EMU_WAVE * q;
+                if (i < W) *reinterpret_cast<float4 *>(a.state_out + (size_t)c * W + i) = *reinterpret_cast<const float4 *>(xrow + i);
+            }
+        }
+    } else if (w == 0) {
         return;
     }
-    if (tid == EMU_WAVE) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // wavefronts 1..NW-1: the expert input (and chained the residual), one
-    // column group at a time, every gain load issued before the first use
-    constexpr int QT = (NQ + NW - 2) / (NW - 1); // column groups per wavefront
-    float4 g2[QT], fg[QT];
-#pragma unroll
-    for (int j = 0; j < QT; ++j) {
-        const int q = w - 1 + (NW - 1) * j, i = 4 * lane + 4 * EMU_WAVE * q;
-        const bool ok = q < NQ && i < W;
-        const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        g2[j] = GEMMA && ok ? *reinterpret_cast<const float4 *>(a.gain + i) : z;
-        fg[j] = GEMMA && ok && a.ffn_xa ? *reinterpret_cast<const float4 *>(a.ffn_gain + i) : z;
-    }
-#pragma unroll
-    for (int j = 0; j < QT; ++j) {
-        const int q = w - 1 + (NW - 1) * j;
-        if (q >= NQ || 4 * EMU_WAVE * q >= W) break; // uniform: past the row
+    // Wavefronts 1..NW-1 of every workgroup of the client: the expert input
+    // (and in the Gemma form the shared FFN's operands), one column group
+    // each, groups dealt across the workgroups first.  It does not depend on
+    // the routes, so only the routing waits for the last arrival.
+    for (int q = q0, j = 0; q < nq; q += (NW - 1) * gridDim.x, ++j) {
         const int i = 4 * lane + 4 * EMU_WAVE * q;
         const bool live = i < W;
+        if (GEMMA && j > 0 && live) { // further groups (narrow grids): gains loaded here
+            g2 = *reinterpret_cast<const float4 *>(a.gain + i);
+            if (a.ffn_xa) fg = *reinterpret_cast<const float4 *>(a.ffn_gain + i);
+        }
         const float4 x4 = *reinterpret_cast<const float4 *>(xrow + i);
         float4 v;
         if constexpr (GEMMA) { // (r * q) * gain2
-            v = make_float4(__fmul_rn(__fmul_rn(x4.x, scale), g2[j].x), __fmul_rn(__fmul_rn(x4.y, scale), g2[j].y),
-                            __fmul_rn(__fmul_rn(x4.z, scale), g2[j].z), __fmul_rn(__fmul_rn(x4.w, scale), g2[j].w));
+            v = make_float4(__fmul_rn(__fmul_rn(x4.x, scale), g2.x), __fmul_rn(__fmul_rn(x4.y, scale), g2.y),
+                            __fmul_rn(__fmul_rn(x4.z, scale), g2.z), __fmul_rn(__fmul_rn(x4.w, scale), g2.w));
         } else { // the router input is the expert input
             v = *reinterpret_cast<const float4 *>(rrow + i);
         }
-        if (live) {
-            *reinterpret_cast<float4 *>(a.xn + (size_t)c * W + i) = v;
-            if (chained) *reinterpret_cast<float4 *>(a.state_out + (size_t)c * W + i) = x4;
-        }
+        if (live) *reinterpret_cast<float4 *>(a.xn + (size_t)c * W + i) = v;
         if (a.xp.q) emu_span_limbs_wave(v, live, c, q, a.xp); // span q of the experts' limb planes
         if (GEMMA && a.ffn_xa) { // the shared FFN's input, as the link kernel would form it
             const float s2 = 1.0f / sqrtf(tot / (float)W + a.ffn_eps);
-            const float4 u = make_float4(__fmul_rn(__fmul_rn(x4.x, s2), fg[j].x), __fmul_rn(__fmul_rn(x4.y, s2), fg[j].y),
-                                         __fmul_rn(__fmul_rn(x4.z, s2), fg[j].z), __fmul_rn(__fmul_rn(x4.w, s2), fg[j].w));
+            const float4 u = make_float4(__fmul_rn(__fmul_rn(x4.x, s2), fg.x), __fmul_rn(__fmul_rn(x4.y, s2), fg.y),
+                                         __fmul_rn(__fmul_rn(x4.z, s2), fg.z), __fmul_rn(__fmul_rn(x4.w, s2), fg.w));
             emu_emit_limbs4(u, live, i, c, a.ffn_xa, a.ffn_xs);
         }
     }
