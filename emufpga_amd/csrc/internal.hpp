@@ -888,10 +888,15 @@ int emu_launch_attn(emu_ctx *ctx, const EmuAttnLaunch &l);
 // With combine false the weighted sum is left for the caller: the expert
 // outputs stay at emu_moe_contrib(workspace, ...) ([token][slot][width]).
 // With x_planes_ready the tokens' limb planes (emu_moe_x_planes) already
-// hold x (the matrix-core form only: see emu_moe_mma_form).
+// hold x (the matrix-core form only: see emu_moe_mma_form).  With
+// span_counters (emu_moe_span_counters() entries, zero before the first
+// call; every call leaves them zero) the gate|up launch also writes the
+// routes' limb planes, one launch fewer; calls sharing them must not overlap.
 int emu_moe_ffn_resid(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok, const int32_t *d_ids,
                       const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_state,
-                      float scale, bool combine = true, bool x_planes_ready = false);
+                      float scale, bool combine = true, bool x_planes_ready = false,
+                      uint32_t *span_counters = nullptr);
+size_t emu_moe_span_counters();
 const float *emu_moe_contrib(const void *d_workspace, uint32_t n_tok, uint32_t k, uint32_t ff);
 // Whether the layer takes the matrix-core form, and where its workspace
 // keeps the tokens' limb planes.

@@ -113,6 +113,7 @@ struct emu_session {
     // Gemma form: the router's input and the global layers' RoPE table
     float *rope2 = nullptr;
     uint32_t *gate_counters = nullptr; // [client] arrivals at the MoE gate
+    uint32_t *span_counters = nullptr; // arrivals per (expert, span) at the experts' gate|up
     // Zipf routing for throughput runs and the device route trace
     // ([capacity][layer][client][k] ids and weights, slot = step % capacity)
     float zipf_s = 0.0f;
@@ -1111,7 +1112,7 @@ int run_moe(emu_session *s)
         // is combined here, for the output matvec)
         const bool combine = !chain || layer + 1 == c.layers;
         if ((st = emu_moe_ffn_resid(ctx, &d, s->xn, (uint32_t)n, s->rids_s, s->rwts_s, s->moe_ws, s->moe_ws_bytes,
-                                    s->state, c.residual_scale, combine, planes)) != EMU_OK)
+                                    s->state, c.residual_scale, combine, planes, s->span_counters)) != EMU_OK)
             return st;
     }
     QmvArgs out{};
@@ -1799,6 +1800,7 @@ extern "C" int emu_session_create(emu_model *m, uint32_t n_clients, uint32_t con
     if (m->moe()) {
         alloc((void **)&s->xn, sizeof(float) * n_clients * c.hidden);
         alloc((void **)&s->gate_counters, sizeof(uint32_t) * n_clients);
+        alloc((void **)&s->span_counters, sizeof(uint32_t) * emu_moe_span_counters());
         alloc((void **)&s->rlog, sizeof(float) * n_clients * c.n_experts);
         alloc((void **)&s->rids, sizeof(int32_t) * n_clients * c.experts_used);
         alloc((void **)&s->rwts, sizeof(float) * n_clients * c.experts_used);
@@ -1827,6 +1829,8 @@ extern "C" int emu_session_create(emu_model *m, uint32_t n_clients, uint32_t con
     }
     if (st == EMU_OK) st = emu_memset(ctx, s->counters, 0, sizeof(uint32_t) * n_clients * c.kv_heads);
     if (st == EMU_OK && s->gate_counters) st = emu_memset(ctx, s->gate_counters, 0, sizeof(uint32_t) * n_clients);
+    if (st == EMU_OK && s->span_counters)
+        st = emu_memset(ctx, s->span_counters, 0, sizeof(uint32_t) * emu_moe_span_counters());
     if (st == EMU_OK) {
         // The multi-token matvec's workspace must exist before the step is
         // captured into a graph: size it for every matvec of the step.
@@ -1865,7 +1869,7 @@ extern "C" int emu_session_destroy(emu_session *s)
     void *ptrs[] = {s->k_cache, s->v_cache, s->positions, s->tokens, s->steps, s->last, s->prompt, s->hist,
                     s->ctrl, s->counters, s->state, s->qkv, s->attn, s->act, s->logits, s->keys, s->partial,
                     s->rope, s->xn, s->rlog, s->rids, s->rwts, s->rids_s, s->rwts_s, s->moe_ws, s->gate_counters,
-                    s->rope2, s->trace_ids, s->trace_w};
+                    s->span_counters, s->rope2, s->trace_ids, s->trace_w};
     for (void *p : ptrs) emu_free(ctx, p);
     delete s;
     return EMU_OK;

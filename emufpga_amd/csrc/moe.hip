@@ -544,6 +544,7 @@ constexpr int kChunkBytes = kEmuChunkBytes; // three int8 limbs of 16 columns
 constexpr int kSpanChunks = kEmuSpanChunks; // 16-column chunks per 256-column span
 constexpr int kSpanMeta = kEmuSpanMeta;     // per vector and span: digits [h, l][limb][16 chunks] int8, then the scale
 constexpr int kMmaMaxCols = 4096;
+constexpr int kMmaMaxSpans = kMmaMaxCols / 256;
 
 // Limb planes of n vectors of C chunks (EmuLimbPlanes).
 using LimbPlanes = EmuLimbPlanes;
@@ -984,6 +985,11 @@ struct MmaArgs {
     LimbPlanes in;       // the input vectors: tokens (gate|up) or routes (down)
     int ks;        // wavefronts sharing a tile's spans (1, 2 or 4)
     int tiles;     // tiles per expert
+    // gate|up with counters set: the routes' limb planes, written by the
+    // last tile of each 256-column span to arrive (counters [expert slot]
+    // [span], zero between launches)
+    LimbPlanes out;
+    uint32_t *counters;
 };
 
 // Global-memory views of the weight rows.  The rows are reached through
@@ -1202,13 +1208,50 @@ __global__ __launch_bounds__(kThreads, 2) void moe_mma_kernel(MmaArgs g)
         return;
     }
     // gate|up: lanes j < 16 hold gate row 16*tile + j, lanes j + 16 its up row.
+    const bool handoff = g.counters != nullptr;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const float u = __shfl_xor(v[r], 16, EMU_WAVE);
         const int p = 4 * kh + r;
-        if (j < 16 && p < cnt)
-            a.act_buf[(size_t)position_vec<kMmaDown>(a, slot, p) * a.ff + 16 * tile + j] = activate<ACT>(v[r], u);
+        if (j < 16 && p < cnt) {
+            float *dst = a.act_buf + (size_t)position_vec<kMmaDown>(a, slot, p) * a.ff + 16 * tile + j;
+            const float o = activate<ACT>(v[r], u);
+            if (handoff) __hip_atomic_store(dst, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else *dst = o;
+        }
     }
+    if (!handoff) return;
+    // The routes' limb planes, in place of a launch of the limb kernel: the
+    // activations went to the device-coherent level, every store completes
+    // before the span's arrival counter moves, and the last of the span's
+    // tiles to arrive reads the span back (agent-scope loads) and splits it
+    // for each position, as the limb kernel would, then resets the counter.
+    __builtin_amdgcn_s_waitcnt(0);
+    const int span = tile / kSpanChunks;
+    const int need = g.tiles - kSpanChunks * span < kSpanChunks ? g.tiles - kSpanChunks * span : kSpanChunks;
+    uint32_t *counter = g.counters + (size_t)blockIdx.y * kMmaMaxSpans + span;
+    uint32_t old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = (uint32_t)__shfl((int)old, 0, EMU_WAVE);
+    if ((int)old != need - 1) return; // uniform
+    if (lane == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int col = kSpanChunks * 16 * span + 4 * lane;
+    const bool live = col < a.ff;
+    float4 xv[kMaxTok];
+#pragma unroll
+    for (int p = 0; p < kMaxTok; ++p) {
+        xv[p] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (p < cnt && live) {
+            const float *src = a.act_buf + (size_t)position_vec<kMmaDown>(a, slot, p) * a.ff + col;
+            xv[p].x = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            xv[p].y = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            xv[p].z = __hip_atomic_load(src + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            xv[p].w = __hip_atomic_load(src + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < kMaxTok; ++p)
+        if (p < cnt) emu_span_limbs_wave(xv[p], live, position_vec<kMmaDown>(a, slot, p), span, g.out); // uniform
 }
 
 bool mma_enabled()
@@ -1236,12 +1279,15 @@ int mma_shares(const MoeArgs &a, int tiles, int spans, int budget)
 }
 
 template <class F, int KIND, int ACT>
-int launch_mma(emu_ctx *ctx, const MoeArgs &a, const LimbPlanes &in)
+int launch_mma(emu_ctx *ctx, const MoeArgs &a, const LimbPlanes &in, const LimbPlanes &out = LimbPlanes{},
+               uint32_t *counters = nullptr)
 {
     using M = Mma<F>;
     MmaArgs g;
     g.a = a;
     g.in = in;
+    g.out = out;
+    g.counters = KIND == kMmaUp ? counters : nullptr;
     g.tiles = KIND == kMmaUp ? a.ff / 16 : (a.width + 31) / 32;
     g.ks = mma_shares(a, g.tiles, in.ns, KIND == kMmaUp ? 8192 : 2048);
     const int tpw = kWaves / g.ks;
@@ -1253,10 +1299,11 @@ int launch_mma(emu_ctx *ctx, const MoeArgs &a, const LimbPlanes &in)
     return EMU_OK;
 }
 
-template <class F> int launch_mma_up(emu_ctx *ctx, const MoeArgs &a, const LimbPlanes &in)
+template <class F>
+int launch_mma_up(emu_ctx *ctx, const MoeArgs &a, const LimbPlanes &in, const LimbPlanes &out, uint32_t *counters)
 {
-    if (a.act == EMU_ACT_GELU_TANH) return launch_mma<F, kMmaUp, EMU_ACT_GELU_TANH>(ctx, a, in);
-    return launch_mma<F, kMmaUp, EMU_ACT_SILU>(ctx, a, in);
+    if (a.act == EMU_ACT_GELU_TANH) return launch_mma<F, kMmaUp, EMU_ACT_GELU_TANH>(ctx, a, in, out, counters);
+    return launch_mma<F, kMmaUp, EMU_ACT_SILU>(ctx, a, in, out, counters);
 }
 
 int launch_limbs(emu_ctx *ctx, const float *x, int n_vec, int cols, const LimbPlanes &L)
@@ -1297,7 +1344,7 @@ uint8_t *x_plane_base(void *ws, size_t slots, uint32_t width, uint32_t ff)
 int moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok, const int32_t *d_ids,
             const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_out, float *d_resid,
             float resid_scale, bool combine = true, const uint8_t *const *d_table = nullptr,
-            bool x_planes_ready = false)
+            bool x_planes_ready = false, uint32_t *span_counters = nullptr)
 {
     if (!ctx || !d || !d_x || !d_ids || !d_weights || !(d_out || d_resid) || (!d_table && (!d->d_gate || !d->d_down)))
         return EMU_E_ARG;
@@ -1337,8 +1384,9 @@ int moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_to
     a.table = d_table;
     if (mma_form(d)) {
         // matrix-core form: the tokens' limb planes (unless the caller wrote
-        // them), gate|up into the activations, the routes' limb planes, down
-        // into the contributions
+        // them), gate|up into the activations, the routes' limb planes (by
+        // the gate|up launch when the caller keeps span counters), down into
+        // the contributions
         const int c_in = (int)(d->width / 16), c_ff = (int)(d->ff / 16);
         const size_t slots = (size_t)n_tok * d->k;
         uint8_t *xp = x_plane_base(d_workspace, slots, d->width, d->ff);
@@ -1346,14 +1394,14 @@ int moe_ffn(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_to
         const LimbPlanes lx = limb_planes(xp, n_tok, c_in), lf = limb_planes(fp, slots, c_ff);
         if (!x_planes_ready && (st = launch_limbs(ctx, d_x, (int)n_tok, (int)d->width, lx)) != EMU_OK) return st;
         switch (d->enc_gate_up) {
-        case EMU_ENC_Q6_K: st = launch_mma_up<FmtQ6K>(ctx, a, lx); break;
-        case EMU_ENC_Q8_0: st = launch_mma_up<FmtQ8_0>(ctx, a, lx); break;
-        case EMU_ENC_Q5_K: st = launch_mma_up<FmtQ5K>(ctx, a, lx); break;
-        case EMU_ENC_Q2_K: st = launch_mma_up<FmtQ2K>(ctx, a, lx); break;
+        case EMU_ENC_Q6_K: st = launch_mma_up<FmtQ6K>(ctx, a, lx, lf, span_counters); break;
+        case EMU_ENC_Q8_0: st = launch_mma_up<FmtQ8_0>(ctx, a, lx, lf, span_counters); break;
+        case EMU_ENC_Q5_K: st = launch_mma_up<FmtQ5K>(ctx, a, lx, lf, span_counters); break;
+        case EMU_ENC_Q2_K: st = launch_mma_up<FmtQ2K>(ctx, a, lx, lf, span_counters); break;
         default: return EMU_E_UNSUPPORTED;
         }
         if (st != EMU_OK) return st;
-        if ((st = launch_limbs(ctx, a.act_buf, (int)slots, (int)d->ff, lf)) != EMU_OK) return st;
+        if (!span_counters && (st = launch_limbs(ctx, a.act_buf, (int)slots, (int)d->ff, lf)) != EMU_OK) return st;
         switch (d->enc_down) {
         case EMU_ENC_Q6_K: st = launch_mma<FmtQ6K, kMmaDown, 0>(ctx, a, lf); break;
         case EMU_ENC_Q8_0: st = launch_mma<FmtQ8_0, kMmaDown, 0>(ctx, a, lf); break;
@@ -1410,12 +1458,14 @@ int emu_moe_ffn_table(emu_ctx *ctx, const emu_moe_desc *d, const uint8_t *const 
 
 int emu_moe_ffn_resid(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok, const int32_t *d_ids,
                       const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_state,
-                      float scale, bool combine, bool x_planes_ready)
+                      float scale, bool combine, bool x_planes_ready, uint32_t *span_counters)
 {
     if (!d_state) return EMU_E_ARG;
     return moe_ffn(ctx, d, d_x, n_tok, d_ids, d_weights, d_workspace, workspace_bytes, nullptr, d_state, scale,
-                   combine, nullptr, x_planes_ready && mma_form(d));
+                   combine, nullptr, x_planes_ready && mma_form(d), span_counters);
 }
+
+size_t emu_moe_span_counters() { return (size_t)kMaxTok * 8 * kMmaMaxSpans; }
 
 bool emu_moe_mma_form(const emu_moe_desc *d) { return d && mma_form(d); }
 
