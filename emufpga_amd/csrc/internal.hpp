@@ -75,6 +75,28 @@ __device__ __forceinline__ uint16_t ld2(const uint8_t *p)
     return v;
 }
 
+// Loads with the non-temporal hint, for weight bytes that a decode step reads
+// once: their cache lines are marked for early eviction instead of displacing
+// lines that are read again (activations, the KV cache, partial sums).  Like
+// ld16, these compile to single dwordx4 (dwordx2, ushort) loads, which the
+// hardware takes at any address.
+__device__ __forceinline__ uint4 ldnt16(const uint8_t *p)
+{
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ldnt8(const uint8_t *p)
+{
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p));
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint16_t ldnt2(const uint8_t *p)
+{
+    return __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));
+}
+
 // f16 -> f32 is exact (hardware conversion handles subnormal halves), the same
 // value as f16_to_f32 of spm-gguf/src/tensor.rs:82-98.
 __device__ __forceinline__ float h2f(uint16_t bits)

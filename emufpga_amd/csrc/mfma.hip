@@ -337,8 +337,9 @@ struct Unit {
 // each 32-row x 256-column tile block is one 6720-byte chunk whose code words
 // are already in each lane's operand order, so six 1 KB loads per wavefront
 // bring them straight into registers (no LDS round trip), and its scales and
-// d follow.  The codes are the same, so the results are bit for bit those of
-// the GGUF-order path.
+// d follow, all with the non-temporal hint (each weight byte is read once per
+// step; batch 8 measured 0.7% faster than with plain loads).  The codes are
+// the same, so the results are bit for bit those of the GGUF-order path.
 template <bool MM>
 __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs a, int units)
 {
@@ -382,14 +383,14 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
             const uint8_t *cp = a.w[b.mat] + ((size_t)b.rt * (a.cols / 256) + cb) * kMmChunk;
 #pragma unroll
             for (int i = 0; i < 6; ++i) {
-                const uint4 q4 = ld16(cp + 1024 * i + 16 * lane);
+                const uint4 q4 = ldnt16(cp + 1024 * i + 16 * lane);
                 b.cw[4 * i] = q4.x;
                 b.cw[4 * i + 1] = q4.y;
                 b.cw[4 * i + 2] = q4.z;
                 b.cw[4 * i + 3] = q4.w;
             }
-            b.sc = ld16(cp + 6144 + 16 * j);
-            b.d = ld2(cp + 6656 + 2 * j);
+            b.sc = ldnt16(cp + 6144 + 16 * j);
+            b.d = ldnt2(cp + 6656 + 2 * j);
         } else if (has) { // uniform
             uint4 raw[8];
             uint16_t dd[8];
