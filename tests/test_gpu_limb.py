@@ -54,6 +54,28 @@ def test_plain_matches_oracle(ctx, rows, cols):
     check(got, ref, limb_bound(raw, rows, cols, x))
 
 
+@pytest.mark.parametrize("rows,cols", [(300, 4096), (97, 12288)])
+def test_dyadic_inputs_bit_exact(ctx, rows, cols):
+    """Power-of-two d, sub-block scales in -2..2 and activations k/16 with
+    |k| <= 32: the three limbs hold every activation exactly (k * 2^(16-e) <
+    2^21), each sub-block's integer dot is a multiple of 2^12 below 2^30 (so
+    its float conversion is exact), and every product and partial sum is a
+    multiple of 2^-8 (the row sums of these random rows stay far below 2^15,
+    inside f32's 24 bits).  So the limb kernel must equal the oracle's f32
+    fold bit for bit."""
+    rng = np.random.default_rng(rows + cols)
+    nblk = rows * cols // 256
+    raw = npref.random_blocks(Q6, nblk, rng).reshape(nblk, 210)
+    raw[:, 192:208] = rng.integers(-2, 3, size=(nblk, 16)).astype(np.int8).view(np.uint8)
+    raw[:, 208:210] = np.frombuffer(np.float16(2.0 ** -4).tobytes(), np.uint8)
+    raw = raw.reshape(-1)
+    x = npref.dyadic(rng, (1, cols), lo=-32, hi=32)
+    m = QuantMatrix(ctx, Q6, rows, cols, raw)
+    got = streamed(ctx, m, (x, 1)).reshape(rows)
+    ref = oracle.qmatvec(oracle.OR_Q6_K, raw, rows, cols, x, 1).reshape(rows)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("cols", [4096, 12288])
 def test_accumulate_matches_oracle(ctx, cols):
     rows = 515
