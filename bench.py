@@ -46,6 +46,16 @@ KERNEL = "qmv_limb_kernel<LimbQ6KLM, S=1, D=1, dual, norm> (fused gate|up, 2 x 1
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "qmv_limb_gate_up_qwen3_8b_pmc.txt")
 COPY_BYTES = 256 << 20  # calibration copy for the PMC byte counters
 TRACE_DIR = ""  # --trace-dir
+DIRECT = False  # --direct
+
+
+def session(model: Model, n: int, context: int) -> Session:
+    """A decode session with an fp16 KV cache; with --direct its steps are
+    launched kernel by kernel instead of replayed from a captured graph."""
+    sess = Session(model, n, context, kv_f16=True)
+    if DIRECT:
+        sess.set_options(direct=True)
+    return sess
 
 
 def measured_traffic():
@@ -199,7 +209,7 @@ def smol_leg(ctx, rng, with_cpu: bool) -> dict:
     cfg = SMOLLM2_135M_Q8
     model = Model(ctx, cfg)
     model.synth(135)
-    sess = Session(model, 1, 512, kv_f16=True)
+    sess = session(model, 1, 512)
     prompt = rng.integers(0, cfg.vocab, size=(1, 32)).astype(np.uint32)
     sess.generate(prompt, 1 + 8)
     ctx.sync()
@@ -372,7 +382,7 @@ def moe_leg(ctx, rng, name: str, cfg, n_clients: int, prompt_len: int, steps: in
     model.synth(seed)
     ctx.sync()
     log(f"{name}: synthesised in {time.perf_counter() - t0:.1f} s")
-    sess = Session(model, n_clients, prompt_len + steps + 64 + 16, kv_f16=True)
+    sess = session(model, n_clients, prompt_len + steps + 64 + 16)
     sess.route_zipf(zipf_s, seed)
     prompt = rng.integers(0, cfg.vocab, size=(n_clients, prompt_len)).astype(np.uint32)
     t0 = time.perf_counter()
@@ -424,7 +434,7 @@ def moe_leg(ctx, rng, name: str, cfg, n_clients: int, prompt_len: int, steps: in
 def decode_256(ctx, model: Model, rng, batch: int, prompt: int, context: int) -> dict:
     """The workload's full decode: a `prompt`-token prompt, then 256 timed
     greedy steps (context prompt -> prompt + 256)."""
-    sess = Session(model, batch, context, kv_f16=True)
+    sess = session(model, batch, context)
     toks = rng.integers(0, model.cfg.vocab, size=(batch, prompt)).astype(np.uint32)
     sess.generate(toks, 1)
     ctx.sync()
@@ -465,11 +475,15 @@ def main() -> int:
     ap.add_argument("--smol-only", action="store_true",
                     help="only the SmolLM2 decode leg, logged without the JSON line; for profiling")
     ap.add_argument("--roofline-rounds", type=int, default=8)
+    ap.add_argument("--direct", action="store_true",
+                    help="launch each decode step's kernels one by one instead of replaying a captured graph "
+                         "(same kernels and results); for kernel tracers and counter passes")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only time the dominant kernel (the fused gate|up matvec over all layers); for profiling")
     args = ap.parse_args()
-    global TRACE_DIR
+    global TRACE_DIR, DIRECT
     TRACE_DIR = args.trace_dir
+    DIRECT = args.direct
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: this decode path runs "
               "on one GPU, whose share of a sharded model is the same kernels at their real shapes",
@@ -519,7 +533,7 @@ def main() -> int:
     rng = np.random.default_rng(42)
     results = {}
     for batch in ([8] if args.batch8_only else [1] if args.no_batch8 else [1, 8]):
-        sess = Session(model, batch, args.context, kv_f16=True)
+        sess = session(model, batch, args.context)
         prompt = rng.integers(0, cfg.vocab, size=(batch, args.prompt)).astype(np.uint32)
         t0 = time.perf_counter()
         sess.generate(prompt, 1 + args.warmup)  # prefill + warmup decode steps, untimed

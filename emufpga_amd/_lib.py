@@ -32,6 +32,10 @@ ENCODINGS = {"F32": F32, "F16": F16, "Q8_0": Q8_0, "Q2_K": Q2_K, "Q5_K": Q5_K, "
 EMU_MV_ACCUMULATE = 1
 EMU_MV_LANE_MAJOR = 2
 EMU_MV_MFMA_MAJOR = 4
+EMU_MV_F32_ACT = 8
+EMU_MOE_F32_ACT = 1
+EMU_SESSION_F32_ACT = 1
+EMU_SESSION_DIRECT = 2
 EMU_ROPE_NEOX = 0
 EMU_ROPE_INTERLEAVED = 1
 EMU_ROPE_NEOX_FMA = 2
@@ -126,6 +130,7 @@ class MoeDesc(C.Structure):
         ("enc_gate_up", C.c_int32), ("enc_down", C.c_int32), ("d_gate", C.c_void_p), ("d_up", C.c_void_p),
         ("d_down", C.c_void_p), ("d_down_scale", C.c_void_p), ("n_experts", C.c_uint32),
         ("width", C.c_uint32), ("ff", C.c_uint32), ("k", C.c_uint32), ("act", C.c_int32),
+        ("flags", C.c_uint32),
     ]
 
 
@@ -207,6 +212,9 @@ SIGNATURES = {
     "emu_moe_ffn_cached": [P, P, P, U32, P, U32, P, P, P, P, SZ, P],
     "emu_expert_cache_policy_trace": [U32, I, P, P, P, U32, P, P],
     "emu_session_route_zipf": [P, F, C.c_uint64],
+    "emu_session_set_options": [P, U32],
+    "emu_session_time_layers": [P, P, U32],
+    "emu_hbm_read_rate": [P, P, SZ, U32, P],
     "emu_session_route_trace": [P, U32],
     "emu_session_read_routes": [P, U32, P, P],
     "emu_model_tensor_lane_major": [P, I, U32, C.POINTER(P), C.POINTER(SZ)],

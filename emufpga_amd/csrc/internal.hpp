@@ -769,6 +769,7 @@ struct QmvArgs {
     int mfma_major;        // w / w_up in the Q6_K matrix-core operand layout (emu_mfma_major_q6k)
     int act;               // gate|up pair: EMU_ACT_SILU (SwiGLU) or EMU_ACT_GELU_TANH (GeGLU)
     float softcap;         // results -> softcap * tanh(v / softcap) after out_div (0: none)
+    int f32_act;           // f32 activations: the dequant + f32 FMA kernels, not the int8-limb ones
 };
 
 // A matvec result's epilogue: divided by out_div (when set), then added to

@@ -520,31 +520,9 @@ template <int S, bool DUAL> struct LimbTune {
     static constexpr int PER_CU = DUAL ? 2 : 1;
 };
 
-// Sixteen wavefronts per workgroup (one workgroup per CU doing one
-// prologue) instead of eight, for S = 1: EMU_LIMB_W=16, a sweep override.
-bool limb_wide()
-{
-    static const bool w = [] {
-        const char *v = getenv("EMU_LIMB_W");
-        return v && atoi(v) == 16;
-    }();
-    return w;
-}
-
 template <class LF, int S, int D, bool DUAL, bool NORM, bool ACC>
 void launch_limb_d(emu_ctx *ctx, const QmvArgs &a, int blocks)
 {
-    if constexpr (S == 1) {
-        if (limb_wide()) {
-            using SH = LimbShape<S, 16>;
-            const int wb = (blocks + 1) / 2;
-            const int total_rg = wb * SH::RG;
-            const int rounds = (a.rows + total_rg * D - 1) / (total_rg * D);
-            hipLaunchKernelGGL((qmv_limb_kernel<LF, S, D, DUAL, NORM, ACC, 16>), dim3(wb), dim3(SH::T), 0,
-                               ctx->stream, a, rounds);
-            return;
-        }
-    }
     using SH = LimbShape<S>;
     const int total_rg = blocks * SH::RG;
     const int rounds = (a.rows + total_rg * D - 1) / (total_rg * D);
@@ -552,25 +530,10 @@ void launch_limb_d(emu_ctx *ctx, const QmvArgs &a, int blocks)
                        a, rounds);
 }
 
-// Rows in flight per wavefront: the tuned depth, or EMU_LIMB_D (1..3) for sweeps.
-int limb_depth_override()
-{
-    static const int d = [] {
-        const char *v = getenv("EMU_LIMB_D");
-        const int f = v ? atoi(v) : 0;
-        return f >= 1 && f <= 3 ? f : 0;
-    }();
-    return d;
-}
-
 template <class LF, int S, bool DUAL, bool NORM, bool ACC>
 void launch_limb_cfg(emu_ctx *ctx, const QmvArgs &a, int blocks)
 {
-    switch (limb_depth_override() ? limb_depth_override() : LimbTune<S, DUAL>::D) {
-    case 1: launch_limb_d<LF, S, 1, DUAL, NORM, ACC>(ctx, a, blocks); break;
-    case 2: launch_limb_d<LF, S, 2, DUAL, NORM, ACC>(ctx, a, blocks); break;
-    default: launch_limb_d<LF, S, 3, DUAL, NORM, ACC>(ctx, a, blocks); break;
-    }
+    launch_limb_d<LF, S, LimbTune<S, DUAL>::D, DUAL, NORM, ACC>(ctx, a, blocks);
 }
 
 template <class LF, int S>
@@ -579,17 +542,13 @@ int launch_limb_s(emu_ctx *ctx, const QmvArgs &a, int *key_slots)
     const bool dual = a.w_up != nullptr, norm = a.gain != nullptr, acc = a.accumulate != 0;
     if (dual && acc) return EMU_E_ARG; // the fused entry point never asks for this
     const int cus = ctx->cus > 0 ? ctx->cus : 256;
-    int per_cu = dual ? LimbTune<S, true>::PER_CU : LimbTune<S, false>::PER_CU;
-    if (const char *v = getenv("EMU_LIMB_BPC")) { // sweep override
-        const int f = atoi(v);
-        if (f >= 1 && f <= 4) per_cu = f;
-    }
+    const int per_cu = dual ? LimbTune<S, true>::PER_CU : LimbTune<S, false>::PER_CU;
     // No more row-groups than rows (a key slot per row-group must fit the
     // caller's key stride, which holds rows + 8).
     const int need = (a.rows + LimbShape<S>::RG - 1) / LimbShape<S>::RG;
     const int blocks = cus * per_cu < need ? cus * per_cu : need;
     // key slots the launch writes: one per row-group of the grid it takes
-    const int slots = S == 1 && limb_wide() ? (blocks + 1) / 2 * LimbShape<1, 16>::RG : blocks * LimbShape<S>::RG;
+    const int slots = blocks * LimbShape<S>::RG;
     if (a.keys && slots > a.key_stride) return EMU_E_CONFIG;
     if (dual) {
         if (norm) launch_limb_cfg<LF, S, true, true, false>(ctx, a, blocks);
@@ -606,20 +565,10 @@ int launch_limb_s(emu_ctx *ctx, const QmvArgs &a, int *key_slots)
     return EMU_OK;
 }
 
-bool limb_disabled()
-{
-    static const bool off = [] {
-        const char *v = getenv("EMU_QMV_LIMB");
-        return v && v[0] == '0';
-    }();
-    return off;
-}
-
 } // namespace
 
 bool emu_limb_supports(int encoding, int cols)
 {
-    if (limb_disabled()) return false;
     if (encoding != EMU_ENC_Q6_K) return false;
     return cols == 4096 || cols == 12288;
 }

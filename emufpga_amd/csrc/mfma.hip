@@ -567,15 +567,6 @@ __global__ __launch_bounds__(kFinishThreads) void mfma_finish_kernel(FinishArgs 
     }
 }
 
-bool mfma_disabled()
-{
-    static const bool off = [] {
-        const char *v = getenv("EMU_QMV_MFMA");
-        return v && v[0] == '0';
-    }();
-    return off;
-}
-
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // Workspace: A operands and scales for up to cols_cap columns, then the
@@ -636,14 +627,12 @@ int emu_mfma_reserve(emu_ctx *ctx, size_t bytes)
 
 bool emu_mfma_shape_ok(int encoding, int cols)
 {
-    if (mfma_disabled()) return false;
     return encoding == EMU_ENC_Q6_K && cols > 0 && (cols % kSlice == 0 || (cols % 256 == 0 && cols >= 2048)) &&
            (cols + kSlice - 1) / kSlice <= kMaxSlices && cols <= 8 * kLinkThreads * kLinkPairs;
 }
 
 bool emu_mfma_supports(int encoding, int cols, int n_tok)
 {
-    if (mfma_disabled()) return false;
     // Widths that are not whole slices (a multiple of 256 columns, the last
     // slice partly empty) only from 2048 columns: below that the single-launch
     // vector kernel costs less than link, matvec and finish.

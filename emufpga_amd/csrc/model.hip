@@ -65,10 +65,11 @@ struct emu_model {
     bool moe() const { return cfg.style == EMU_STYLE_GRANITE; }
     bool lm_takes(uint32_t cols) const { return lm && emu_limb_supports(cfg.encoding, (int)cols); }
     // The matrix a batch-1 matvec over `cols` columns reads, and whether it
-    // is the lane-major copy.
-    const uint8_t *lm_or(const uint8_t *w, uint32_t cols, uint32_t n, int *lane_major) const
+    // is the lane-major copy (never with f32 activations, whose kernels read
+    // GGUF order).
+    const uint8_t *lm_or(const uint8_t *w, uint32_t cols, uint32_t n, int *lane_major, bool f32 = false) const
     {
-        *lane_major = n == 1 && lm_takes(cols);
+        *lane_major = !f32 && n == 1 && lm_takes(cols);
         return *lane_major ? lm + (w - base) : w;
     }
     // Matrix-core operand copy (emu_mfma_major_q6k) of the Q6_K matrices the
@@ -99,6 +100,8 @@ struct emu_session {
     emu_model *m = nullptr;
     uint32_t n = 0, context = 0;
     int kv_f16 = 1;
+    uint32_t flags = 0; // EMU_SESSION_*
+    bool f32() const { return (flags & EMU_SESSION_F32_ACT) != 0; }
     void *k_cache = nullptr, *v_cache = nullptr;
     size_t kv_bytes = 0;
     uint32_t *positions = nullptr, *tokens = nullptr, *steps = nullptr, *prompt = nullptr,
@@ -127,6 +130,10 @@ struct emu_session {
     std::vector<uint32_t> host_pos;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    // emu_session_time_layers: events after the embedding, after each layer
+    // and after the selection, recorded only while `marking`
+    std::vector<hipEvent_t> marks;
+    bool marking = false;
 };
 
 namespace {
@@ -141,12 +148,105 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t z)
     return z ^ (z >> 31);
 }
 
+// Box-Muller, r * cos(2 pi u2) with r = sqrt(-2 ln u1), evaluated in double
+// precision by additions, multiplications and one division per logarithm
+// (every one correctly rounded, none contracted), then rounded once to
+// float: the same bits on any IEEE-754 machine, so a CPU can synthesise the
+// same weights.  u1 = k / 2^24 (k = 1 .. 2^24) and u2 = j / 2^24 are exact.
+//   ln k = e ln 2 + ln m, k = 2^e m, m in [sqrt(1/2), sqrt(2)), by
+//          2 atanh(s) = 2 (s + s^3/3 + ... + s^23/23), s = (m - 1) / (m + 1);
+//   cos(2 pi j / 2^24) by the quadrant of j and a Taylor polynomial of sin or
+//          cos on [0, pi/4] (terms to x^17 / x^18);
+//   sqrt(y) = y / sqrt(y) from six Newton steps of 1/sqrt(y) started at a
+//          guess built from y's exponent.
+__device__ __forceinline__ double synth_ln_int(uint32_t k) // ln k, k >= 1
+{
+#pragma clang fp contract(off)
+    int e = 31 - __builtin_clz(k);
+    double m = (double)k * __longlong_as_double((long long)(1023 - e) << 52); // k / 2^e, exact
+    if (m > 1.4142135623730951) {
+        m = m * 0.5;
+        e += 1;
+    }
+    const double s = (m - 1.0) / (m + 1.0), s2 = s * s;
+    double p = 1.0 / 23.0;
+    p = p * s2 + 1.0 / 21.0;
+    p = p * s2 + 1.0 / 19.0;
+    p = p * s2 + 1.0 / 17.0;
+    p = p * s2 + 1.0 / 15.0;
+    p = p * s2 + 1.0 / 13.0;
+    p = p * s2 + 1.0 / 11.0;
+    p = p * s2 + 1.0 / 9.0;
+    p = p * s2 + 1.0 / 7.0;
+    p = p * s2 + 1.0 / 5.0;
+    p = p * s2 + 1.0 / 3.0;
+    p = p * s2 + 1.0;
+    return (double)e * 0.6931471805599453 + 2.0 * (s * p);
+}
+
+__device__ __forceinline__ double synth_sin_poly(double x) // x in [0, pi/4]
+{
+#pragma clang fp contract(off)
+    const double x2 = x * x;
+    double p = 1.0 / 355687428096000.0; // 1/17!
+    p = p * x2 - 1.0 / 1307674368000.0; // 1/15!
+    p = p * x2 + 1.0 / 6227020800.0;
+    p = p * x2 - 1.0 / 39916800.0;
+    p = p * x2 + 1.0 / 362880.0;
+    p = p * x2 - 1.0 / 5040.0;
+    p = p * x2 + 1.0 / 120.0;
+    p = p * x2 - 1.0 / 6.0;
+    p = p * x2 + 1.0;
+    return x * p;
+}
+
+__device__ __forceinline__ double synth_cos_poly(double x) // x in [0, pi/4]
+{
+#pragma clang fp contract(off)
+    const double x2 = x * x;
+    double p = 1.0 / 6402373705728000.0; // 1/18!
+    p = p * x2 - 1.0 / 20922789888000.0; // 1/16!
+    p = p * x2 + 1.0 / 87178291200.0;
+    p = p * x2 - 1.0 / 479001600.0;
+    p = p * x2 + 1.0 / 3628800.0;
+    p = p * x2 - 1.0 / 40320.0;
+    p = p * x2 + 1.0 / 720.0;
+    p = p * x2 - 1.0 / 24.0;
+    p = p * x2 + 1.0 / 2.0;
+    return 1.0 - x2 * p;
+}
+
+__device__ __forceinline__ double synth_cos_turn(uint32_t j) // cos(2 pi j / 2^24), j < 2^24
+{
+#pragma clang fp contract(off)
+    const uint32_t q = j >> 22, f = j & 0x3fffffu; // angle = pi/2 (q + f / 2^22)
+    const bool hi = f > 0x200000u;                 // past pi/4 in the quadrant: the co-function
+    const double g = (double)(hi ? 0x400000u - f : f) * (1.0 / 4194304.0);
+    const double x = g * 1.5707963267948966;
+    const double cg = synth_cos_poly(x), sg = synth_sin_poly(x);
+    const double c = hi ? sg : cg, sn = hi ? cg : sg; // cos and sin of pi/2 * f / 2^22
+    return q == 0 ? c : q == 1 ? -sn : q == 2 ? -c : sn;
+}
+
+__device__ __forceinline__ double synth_sqrt(double y) // y >= 0
+{
+#pragma clang fp contract(off)
+    if (y == 0.0) return 0.0;
+    const long long b = __double_as_longlong(y);
+    double r = __longlong_as_double(0x5fe6eb50c7b537a9ll - (b >> 1)); // ~1/sqrt(y)
+    for (int i = 0; i < 6; ++i) r = r * (1.5 - (0.5 * y) * (r * r));
+    return y * r;
+}
+
 __device__ __forceinline__ float gauss(uint64_t seed, uint64_t stream, uint64_t idx, float sd)
 {
+#pragma clang fp contract(off)
     const uint64_t h = splitmix64(seed ^ splitmix64(stream * 0x632be59bd9b4e019ull + idx));
-    const float u1 = (float)((h >> 40) + 1) * (1.0f / 16777216.0f); // (0, 1]
-    const float u2 = (float)(h & 0xffffffu) * (1.0f / 16777216.0f); // [0, 1)
-    return sd * sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+    const uint32_t k = (uint32_t)(h >> 40) + 1u; // u1 = k / 2^24 in (0, 1]
+    const uint32_t j = (uint32_t)(h & 0xffffffu); // u2 = j / 2^24 in [0, 1)
+    const double ln_u1 = synth_ln_int(k) - 24.0 * 0.6931471805599453;
+    const double r = synth_sqrt(-2.0 * ln_u1);
+    return (float)(((double)sd * r) * synth_cos_turn(j));
 }
 
 // Zipf(s) routing for throughput runs: expert e (Zipf rank e + 1) gets the
@@ -174,10 +274,12 @@ __device__ __forceinline__ uint16_t f2h(float x) { return __half_as_ushort(__flo
 __device__ __forceinline__ float clampf(float v, float lo, float hi) { return fminf(fmaxf(v, lo), hi); }
 
 // One thread per block; the block is assembled in private memory then stored.
+// No contraction, so the bits are those of the same arithmetic on a CPU.
 template <int ENC>
 __global__ __launch_bounds__(kThreads) void synth_kernel(uint8_t *dst, size_t nblocks, uint64_t seed,
                                                          uint64_t stream, float sd)
 {
+#pragma clang fp contract(off)
     const size_t b = (size_t)blockIdx.x * kThreads + threadIdx.x;
     if (b >= nblocks) return;
     if constexpr (ENC == EMU_ENC_Q8_0) {
@@ -731,6 +833,15 @@ EmuAttnLaunch layer_attn(emu_session *s, uint32_t layer)
     return al;
 }
 
+// The step's interval marks (emu_session_time_layers), a no-op otherwise.
+int mark(emu_session *s, size_t i)
+{
+    if (!s->marking) return EMU_OK;
+    if (i >= s->marks.size()) return EMU_E_CONFIG;
+    EMU_HIP(s->m->ctx, hipEventRecord(s->marks[i], s->m->ctx->stream));
+    return EMU_OK;
+}
+
 int launch_finalize(emu_session *s, int slots)
 {
     emu_ctx *ctx = s->m->ctx;
@@ -839,6 +950,7 @@ int run_chain(emu_session *s)
         if ((st = matvec(lw + m->off_d, nullptr, m->rb_f, H, F, &nks)) != EMU_OK) return st;
         const float *next = layer + 1 < c.layers ? attn_norm + (size_t)(layer + 1) * H : out_norm;
         if ((st = link(1, nks, 1, s->state, nullptr, H, next, true)) != EMU_OK) return st;
+        if ((st = mark(s, layer + 1)) != EMU_OK) return st;
     }
     QmvArgs out{};
     out.w = m->mm_or(m->base + (c.tied ? m->off_embed : m->off_output), &out.mfma_major);
@@ -853,7 +965,8 @@ int run_chain(emu_session *s)
     if ((st = emu_mfma_matvec(ctx, out, n, cap, nullptr)) != EMU_OK) return st;
     int slots = 0;
     if ((st = emu_mfma_finish(ctx, out, n, cap, &slots)) != EMU_OK) return st;
-    return launch_finalize(s, slots);
+    if ((st = launch_finalize(s, slots)) != EMU_OK) return st;
+    return mark(s, c.layers + 1);
 }
 
 // The layers, output matvec and selection of a mixture-of-experts step
@@ -904,7 +1017,7 @@ int run_moe(emu_session *s)
     // cores with the attention adding q|k|v's partial sums and writing o's
     // operands, and the gate kernel adding o's partial sums to the residual
     // (no finishing or link launch around the attention).
-    const bool chain = moe_chain(m, s->n);
+    const bool chain = !s->f32() && moe_chain(m, s->n);
     const int cap = (int)std::max(H, QW);
     uint8_t *xa = nullptr;
     float *xs = nullptr, *part = nullptr;
@@ -974,9 +1087,11 @@ int run_moe(emu_session *s)
         a.gain = attn_norm + (size_t)layer * H;
         a.eps = c.eps;
         a.y = s->qkv;
+        a.f32_act = s->f32();
         if ((st = emu_launch_qmv(ctx, c.encoding, a, n)) != EMU_OK) return st;
         if ((st = emu_launch_attn(ctx, layer_attn(s, layer))) != EMU_OK) return st;
         QmvArgs o{};
+        o.f32_act = s->f32();
         o.w = lw + m->off_o;
         o.row_bytes = m->rb_q;
         o.rows = (int)H;
@@ -1000,6 +1115,7 @@ int run_moe(emu_session *s)
         d.ff = c.expert_ff;
         d.k = K;
         d.act = m->gemma() ? EMU_ACT_GELU_TANH : EMU_ACT_SILU;
+        d.flags = s->f32() ? EMU_MOE_F32_ACT : 0u;
         // the gate writes the experts' limb planes of the expert input
         const bool planes = emu_moe_mma_form(&d);
         GateArgs ga{};
@@ -1114,6 +1230,7 @@ int run_moe(emu_session *s)
         if ((st = emu_moe_ffn_resid(ctx, &d, s->xn, (uint32_t)n, s->rids_s, s->rwts_s, s->moe_ws, s->moe_ws_bytes,
                                     s->state, c.residual_scale, combine, planes, s->span_counters)) != EMU_OK)
             return st;
+        if ((st = mark(s, layer + 1)) != EMU_OK) return st;
     }
     QmvArgs out{};
     out.w = m->base + (c.tied ? m->off_embed : m->off_output); // Granite: tied (model.rs:403-407)
@@ -1131,13 +1248,15 @@ int run_moe(emu_session *s)
     out.tie_last = 0; // top_k: ties to the lowest index (math.rs:35-40)
     out.out_div = c.logit_div;
     out.softcap = c.logit_softcap;
+    out.f32_act = s->f32();
     int slots = 0;
     // chained: the output on the matrix cores at any client count, as the
     // projections before it (a client's logits do not depend on the batch)
     if ((st = chain ? emu_launch_mfma(ctx, c.encoding, out, n, &slots) : emu_launch_qmv(ctx, c.encoding, out, n, &slots)) !=
         EMU_OK)
         return st;
-    return launch_finalize(s, slots);
+    if ((st = launch_finalize(s, slots)) != EMU_OK) return st;
+    return mark(s, c.layers + 1);
 }
 
 int run_step(emu_session *s)
@@ -1156,8 +1275,10 @@ int run_step(emu_session *s)
     default: return EMU_E_UNSUPPORTED;
     }
     if (st != EMU_OK) return st;
+    if ((st = mark(s, 0)) != EMU_OK) return st;
     if (m->moe()) return run_moe(s);
-    if (mfma_chain(m, s->n)) return run_chain(s);
+    const bool f32 = s->f32();
+    if (!f32 && mfma_chain(m, s->n)) return run_chain(s);
     uint32_t be = 0, bb = 0;
     emu_block_layout(c.encoding, &be, &bb);
     const int smol = c.style == EMU_STYLE_SMOL;
@@ -1165,7 +1286,8 @@ int run_step(emu_session *s)
         const uint8_t *lw = m->base + m->off_layers + (size_t)layer * m->layer_bytes;
         QmvArgs a{};
         // q|k|v with the attention RMSNorm fused.
-        a.w = m->lm_or(lw + m->off_q, H, s->n, &a.lane_major);
+        a.f32_act = f32;
+        a.w = m->lm_or(lw + m->off_q, H, s->n, &a.lane_major, f32);
         a.row_bytes = m->rb_h;
         a.rows = (int)(QW + 2 * KW);
         a.cols = (int)H;
@@ -1178,7 +1300,8 @@ int run_step(emu_session *s)
         if ((st = emu_launch_attn(ctx, layer_attn(s, layer))) != EMU_OK) return st;
         // o projection + residual.
         QmvArgs o{};
-        o.w = m->lm_or(lw + m->off_o, QW, s->n, &o.lane_major);
+        o.f32_act = f32;
+        o.w = m->lm_or(lw + m->off_o, QW, s->n, &o.lane_major, f32);
         o.row_bytes = m->rb_q;
         o.rows = (int)H;
         o.cols = (int)QW;
@@ -1189,8 +1312,9 @@ int run_step(emu_session *s)
         if ((st = emu_launch_qmv(ctx, c.encoding, o, n)) != EMU_OK) return st;
         // gate|up with the FFN RMSNorm and SwiGLU fused.
         QmvArgs g{};
-        g.w = m->lm_or(lw + m->off_g, H, s->n, &g.lane_major);
-        g.w_up = m->lm_or(lw + m->off_u, H, s->n, &g.lane_major);
+        g.f32_act = f32;
+        g.w = m->lm_or(lw + m->off_g, H, s->n, &g.lane_major, f32);
+        g.w_up = m->lm_or(lw + m->off_u, H, s->n, &g.lane_major, f32);
         g.row_bytes = m->rb_h;
         g.rows = (int)F;
         g.cols = (int)H;
@@ -1202,7 +1326,8 @@ int run_step(emu_session *s)
         if ((st = emu_launch_qmv(ctx, c.encoding, g, n)) != EMU_OK) return st;
         // down projection + residual.
         QmvArgs d{};
-        d.w = m->lm_or(lw + m->off_d, F, s->n, &d.lane_major);
+        d.f32_act = f32;
+        d.w = m->lm_or(lw + m->off_d, F, s->n, &d.lane_major, f32);
         d.row_bytes = m->rb_f;
         d.rows = (int)H;
         d.cols = (int)F;
@@ -1211,10 +1336,12 @@ int run_step(emu_session *s)
         d.y = s->state;
         d.accumulate = 1;
         if ((st = emu_launch_qmv(ctx, c.encoding, d, n)) != EMU_OK) return st;
+        if ((st = mark(s, layer + 1)) != EMU_OK) return st;
     }
     QmvArgs out{};
     out.w = m->base + (c.tied ? m->off_embed : m->off_output);
-    if (n == 1 && m->lm_takes(H)) {
+    out.f32_act = f32;
+    if (!f32 && n == 1 && m->lm_takes(H)) {
         out.w = m->lm + m->off_embed;
         out.lane_major = 1;
     }
@@ -1231,7 +1358,8 @@ int run_step(emu_session *s)
     out.tie_last = smol ? 1 : 0;
     int slots = 0;
     if ((st = emu_launch_qmv(ctx, c.encoding, out, n, &slots)) != EMU_OK) return st;
-    return launch_finalize(s, slots);
+    if ((st = launch_finalize(s, slots)) != EMU_OK) return st;
+    return mark(s, c.layers + 1);
 }
 
 // Rebuild the lane-major copy (outside any graph capture).
@@ -1291,23 +1419,16 @@ int ensure_graph(emu_session *s)
     return EMU_OK;
 }
 
-// EMU_GRAPH=0 launches the step's kernels directly instead of replaying the
-// captured graph (same kernels, same order; for profilers that cannot trace
-// graph launches, and to measure what the graph saves).
-bool graphs_enabled()
-{
-    static const bool on = [] {
-        const char *v = getenv("EMU_GRAPH");
-        return !(v && v[0] == '0');
-    }();
-    return on;
-}
+// EMU_SESSION_DIRECT launches the step's kernels directly instead of
+// replaying the captured graph (same kernels, same order; for profilers, and
+// to measure what the graph saves).
+bool graphs_enabled(const emu_session *s) { return !(s->flags & EMU_SESSION_DIRECT); }
 
 int launch_steps(emu_session *s, uint32_t count)
 {
     emu_ctx *ctx = s->m->ctx;
     if (int st = model_sync(s->m); st != EMU_OK) return st;
-    if (!graphs_enabled()) {
+    if (!graphs_enabled(s)) {
         for (uint32_t i = 0; i < count; ++i) {
             const int st = run_step(s);
             if (st != EMU_OK) return st;
@@ -1866,6 +1987,7 @@ extern "C" int emu_session_destroy(emu_session *s)
     emu_ctx *ctx = s->m->ctx;
     if (s->exec) (void)hipGraphExecDestroy(s->exec);
     if (s->graph) (void)hipGraphDestroy(s->graph);
+    for (hipEvent_t e : s->marks) (void)hipEventDestroy(e);
     void *ptrs[] = {s->k_cache, s->v_cache, s->positions, s->tokens, s->steps, s->last, s->prompt, s->hist,
                     s->ctrl, s->counters, s->state, s->qkv, s->attn, s->act, s->logits, s->keys, s->partial,
                     s->rope, s->xn, s->rlog, s->rids, s->rwts, s->rids_s, s->rwts_s, s->moe_ws, s->gate_counters,
@@ -1954,12 +2076,45 @@ extern "C" int emu_time_decode(emu_session *s, uint32_t steps, float *ms)
     if (st != EMU_OK) return st;
     emu_ctx *ctx = s->m->ctx;
     if ((st = set_ctrl(s, 0, 0)) != EMU_OK) return st;
-    if (graphs_enabled() && (st = ensure_graph(s)) != EMU_OK) return st;
+    if (graphs_enabled(s) && (st = ensure_graph(s)) != EMU_OK) return st;
     if ((st = emu_ctx_sync(ctx)) != EMU_OK) return st;
     if ((st = emu_event_record(ctx, 14)) != EMU_OK) return st;
     if ((st = launch_steps(s, steps)) != EMU_OK) return st;
     if ((st = emu_event_record(ctx, 15)) != EMU_OK) return st;
     return emu_event_elapsed(ctx, 14, 15, ms);
+}
+
+extern "C" int emu_session_time_layers(emu_session *s, float *h_us, uint32_t n)
+{
+    if (!s || !h_us) return EMU_E_ARG;
+    const uint32_t L = s->m->cfg.layers;
+    if (n < L + 2) return EMU_E_ARG;
+    int st = check_room(s, 1);
+    if (st != EMU_OK) return st;
+    emu_ctx *ctx = s->m->ctx;
+    if ((st = model_sync(s->m)) != EMU_OK) return st;
+    while (s->marks.size() < L + 2) {
+        hipEvent_t e = nullptr;
+        EMU_HIP(ctx, hipEventCreate(&e));
+        s->marks.push_back(e);
+    }
+    if ((st = set_ctrl(s, 0, 0)) != EMU_OK) return st;
+    if ((st = emu_ctx_sync(ctx)) != EMU_OK) return st;
+    if ((st = emu_event_record(ctx, 13)) != EMU_OK) return st;
+    s->marking = true; // direct launches: a replayed graph would not record the marks
+    st = run_step(s);
+    s->marking = false;
+    if (st != EMU_OK) return st;
+    for (auto &p : s->host_pos) p += 1;
+    EMU_HIP(ctx, hipEventSynchronize(s->marks[L + 1]));
+    hipEvent_t prev = ctx->events[13];
+    for (uint32_t i = 0; i < L + 2; ++i) {
+        float ms = 0.0f;
+        EMU_HIP(ctx, hipEventElapsedTime(&ms, prev, s->marks[i]));
+        h_us[i] = ms * 1e3f;
+        prev = s->marks[i];
+    }
+    return EMU_OK;
 }
 
 namespace {
@@ -1973,6 +2128,15 @@ void drop_graph(emu_session *s)
     s->graph = nullptr;
 }
 } // namespace
+
+extern "C" int emu_session_set_options(emu_session *s, uint32_t flags)
+{
+    if (!s) return EMU_E_ARG;
+    if (flags & ~(uint32_t)(EMU_SESSION_F32_ACT | EMU_SESSION_DIRECT)) return EMU_E_ARG;
+    s->flags = flags;
+    drop_graph(s);
+    return EMU_OK;
+}
 
 extern "C" int emu_session_route_zipf(emu_session *s, float zipf_s, uint64_t seed)
 {

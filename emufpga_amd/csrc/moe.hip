@@ -1254,15 +1254,6 @@ __global__ __launch_bounds__(kThreads, 2) void moe_mma_kernel(MmaArgs g)
         if (p < cnt) emu_span_limbs_wave(xv[p], live, position_vec<kMmaDown>(a, slot, p), span, g.out); // uniform
 }
 
-bool mma_enabled()
-{
-    static const bool on = [] {
-        const char *v = getenv("EMU_MOE_MMA");
-        return !(v && v[0] == '0');
-    }();
-    return on;
-}
-
 // Wavefronts per tile: enough shares of the spans for about `budget`
 // wavefronts over the experts eight tokens can route to -- 8192 for gate|up,
 // 2048 for down, as measured in the decode steps (with every layer's experts
@@ -1329,9 +1320,14 @@ extern "C" size_t emu_moe_workspace_bytes(uint32_t n_tok, uint32_t k, uint32_t w
 
 namespace {
 
+// The matrix-core form finds a workgroup's expert in a 256-bit mask of the
+// routed experts, so it takes layers of up to 256 experts; wider layers, and
+// calls that ask for f32 activations, take the vector form.
+constexpr uint32_t kMmaMaxExperts = 256;
+
 bool mma_form(const emu_moe_desc *d)
 {
-    return mma_enabled() && d->width <= kMmaMaxCols && d->ff <= kMmaMaxCols && d->width % 16 == 0 && d->ff % 16 == 0;
+    return !(d->flags & EMU_MOE_F32_ACT) && d->n_experts <= kMmaMaxExperts && d->width <= kMmaMaxCols && d->ff <= kMmaMaxCols && d->width % 16 == 0 && d->ff % 16 == 0;
 }
 
 // The workspace: activations, contributions, the tokens' limb planes, the

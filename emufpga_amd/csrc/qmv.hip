@@ -391,10 +391,6 @@ int launch_pipe(emu_ctx *ctx, const QmvArgs &a, int *key_slots)
     // CU its full complement of wavefronts; gate/up pairs count double.
     int R = dual ? 2 : 4;
     while (R > 1 && (a.rows + R - 1) / R < want_waves) R /= 2;
-    if (const char *force = getenv("EMU_QMV_R")) { // fixed rows per wave, for tuning sweeps
-        const int f = atoi(force);
-        if (f == 1 || f == 2 || (f == 4 && !dual)) R = f;
-    }
     const int n_rg = (a.rows + R - 1) / R;
     int blocks = (n_rg + waves_per_block - 1) / waves_per_block;
     blocks = blocks < max_blocks ? blocks : max_blocks;
@@ -413,21 +409,10 @@ int launch_pipe(emu_ctx *ctx, const QmvArgs &a, int *key_slots)
 
 constexpr int kPipeMaxCols = 12288; // padded activations + group sums fit in 58 KB of LDS
 
-// EMU_QMV_PIPE=0 routes batch-1 matvecs to the row-per-wave kernel instead
-// (for comparing the two).
-bool pipe_disabled()
-{
-    static const bool off = [] {
-        const char *v = getenv("EMU_QMV_PIPE");
-        return v && v[0] == '0';
-    }();
-    return off;
-}
-
 template <class F>
 int launch_fmt(emu_ctx *ctx, const QmvArgs &a, int n_tok, int *key_slots)
 {
-    if (n_tok == 1 && a.cols <= kPipeMaxCols && a.cols % 4 == 0 && !pipe_disabled())
+    if (n_tok == 1 && a.cols <= kPipeMaxCols && a.cols % 4 == 0)
         return launch_pipe<F>(ctx, a, key_slots);
     if (a.keys && a.w_up) return EMU_E_ARG; // keys select among plain matvec rows
     if (key_slots) {
@@ -641,14 +626,15 @@ int emu_row_bytes(int encoding, uint32_t cols, size_t *row_bytes)
 int emu_launch_qmv(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int *key_slots)
 {
     if (a.rows == 0 || n_tok == 0) return EMU_OK;
+    if (a.f32_act && (a.mfma_major || a.lane_major)) return EMU_E_UNSUPPORTED; // int8-limb layouts
     if (a.mfma_major) { // only the multi-token matrix-core kernel reads that layout
         if (!emu_mfma_supports(encoding, a.cols, n_tok) || (a.w_up && a.accumulate)) return EMU_E_UNSUPPORTED;
         return emu_launch_mfma(ctx, encoding, a, n_tok, key_slots);
     }
-    if (n_tok == 1 && emu_limb_supports(encoding, a.cols) && !(a.w_up && a.accumulate))
+    if (!a.f32_act && n_tok == 1 && emu_limb_supports(encoding, a.cols) && !(a.w_up && a.accumulate))
         return emu_launch_limb(ctx, encoding, a, key_slots);
     if (a.lane_major) return EMU_E_UNSUPPORTED; // only the batch-1 limb kernel reads that layout
-    if (emu_mfma_supports(encoding, a.cols, n_tok) && !(a.w_up && a.accumulate))
+    if (!a.f32_act && emu_mfma_supports(encoding, a.cols, n_tok) && !(a.w_up && a.accumulate))
         return emu_launch_mfma(ctx, encoding, a, n_tok, key_slots);
     switch (encoding) {
     case EMU_ENC_Q6_K: return launch_fmt<FmtQ6K>(ctx, a, n_tok, key_slots);
@@ -703,6 +689,7 @@ extern "C" int emu_qmatvec(emu_ctx *ctx, int encoding, const void *d_w, size_t w
     a.accumulate = (flags & EMU_MV_ACCUMULATE) ? 1 : 0;
     a.lane_major = (flags & EMU_MV_LANE_MAJOR) ? 1 : 0;
     a.mfma_major = mm ? 1 : 0;
+    a.f32_act = (flags & EMU_MV_F32_ACT) ? 1 : 0;
     return emu_launch_qmv(ctx, encoding, a, (int)n_tok);
 }
 
@@ -731,6 +718,7 @@ extern "C" int emu_qmatvec_fused(emu_ctx *ctx, int encoding, const void *d_w, co
     a.accumulate = (flags & EMU_MV_ACCUMULATE) ? 1 : 0;
     a.lane_major = (flags & EMU_MV_LANE_MAJOR) ? 1 : 0;
     a.mfma_major = (flags & EMU_MV_MFMA_MAJOR) ? 1 : 0;
+    a.f32_act = (flags & EMU_MV_F32_ACT) ? 1 : 0;
     if (a.lane_major && a.mfma_major) return EMU_E_ARG;
     return emu_launch_qmv(ctx, encoding, a, (int)n_tok);
 }

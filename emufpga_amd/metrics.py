@@ -20,10 +20,18 @@ The counters come from the device here, not from a file scan:
 * resident_parameter_bytes / total_parameter_bytes -- parameter bytes held
   in HBM over the model's (1 for a resident model, less with the expert
   cache);
-* storage_time -- the time HBM needs to deliver parameter_bytes_read at the
-  given rate (8 TB/s by default), compute_time -- the measured step.  The
-  two overlap on the GPU, so eta = storage / compute is the step's fraction
-  of that rate: eta < 1 says the engine, not HBM, sets the pace.
+* storage_time -- the time the store needs to deliver parameter_bytes_read
+  at the rate measured on the same device (emu_hbm_read_rate: a read-only
+  stream of a buffer larger than the Infinity Cache), so raw_bandwidth is
+  that measured rate; absent a measured rate, storage_time is 0 and
+  raw_bandwidth and eta are None (nothing is assumed);
+* compute_time -- the measured step;
+* wall_time -- the measured step as well: on the GPU the HBM stream and the
+  arithmetic run inside the same kernels, overlapped, which is the case the
+  reference's elapsed() anticipates (model.rs:31-40: with overlap the sum
+  becomes an upper bound), so elapsed() is the measured wall clock and the
+  weight rates are over it.  eta = storage / compute is the step's fraction
+  of the measured HBM rate: eta < 1 says the engine, not HBM, sets the pace.
 """
 from __future__ import annotations
 
@@ -34,7 +42,7 @@ import numpy as np
 
 from .gguf import row_bytes
 
-HBM_PEAK_BYTES_PER_S = 8.0e12
+HBM_PEAK_BYTES_PER_S = 8.0e12  # published peak: for roofline fractions only, never a storage time
 
 
 def widen(value: int) -> float:
@@ -52,9 +60,12 @@ class ScanMetrics:
     total_parameter_bytes: int = 0
     storage_time: float = 0.0  # seconds
     compute_time: float = 0.0  # seconds
+    wall_time: Optional[float] = None  # seconds, when storage and compute overlap
 
     def elapsed(self) -> float:
-        return self.storage_time + self.compute_time
+        """Storage + compute when they do not overlap (model.rs:31-40); the
+        measured wall clock when they do."""
+        return self.wall_time if self.wall_time is not None else self.storage_time + self.compute_time
 
     def scan_productivity(self) -> Optional[float]:
         """Ps: useful parameter applications per weight read."""
@@ -89,7 +100,9 @@ class ScanMetrics:
                 "parameter_bytes_read": self.parameter_bytes_read, "weights_decoded": self.weights_decoded,
                 "weight_applications": self.weight_applications,
                 "resident_parameter_bytes": self.resident_parameter_bytes,
-                "total_parameter_bytes": self.total_parameter_bytes}
+                "total_parameter_bytes": self.total_parameter_bytes,
+                "storage_time_s": r(self.storage_time), "compute_time_s": r(self.compute_time),
+                "elapsed_s": r(self.elapsed())}
 
 
 # ---- traces (spm-viz-trace/src/lib.rs) ------------------------------------
@@ -103,24 +116,40 @@ class RouteEvent:
 
 @dataclass
 class RoutingTrace:
+    """Schema emufpga.moe-routing.v1 (lib.rs:25-80) when the model routes 8
+    of at most 32 experts, as v1 requires (ids below 32, exactly 8 per
+    event).  Wider models (OLMoE's 64, the Gemma-4 form's 128 experts, or
+    another k) write emufpga-amd.moe-routing.wide.v1: the same fields and
+    event bound, ids below n_experts (at most 256), k experts per event."""
     model: str
     events: list = field(default_factory=list)
-    n_experts: int = 32  # the reference bounds ids to Granite's 32 experts (lib.rs:51-53)
+    n_experts: int = 32
+    k: int = 8
     MAX_EVENTS = 24 * 128
 
+    @property
+    def schema(self) -> str:
+        return "emufpga.moe-routing.v1" if self.n_experts <= 32 and self.k == 8 else "emufpga-amd.moe-routing.wide.v1"
+
     def push(self, event: RouteEvent) -> None:
-        """Refuses past the event bound and out-of-range ids (lib.rs:41-56)."""
+        """Refuses past the event bound, out-of-range ids and events of
+        another width (lib.rs:41-56)."""
         if len(self.events) == self.MAX_EVENTS:
             raise ValueError(f"routing trace exceeds {self.MAX_EVENTS:,} events")
-        if any(e >= self.n_experts or e < 0 for e in event.experts):
-            raise ValueError(f"routing trace expert is outside 0..{self.n_experts}")
+        bound = 32 if self.schema == "emufpga.moe-routing.v1" else min(self.n_experts, 256)
+        if any(e >= bound or e < 0 for e in event.experts):
+            raise ValueError(f"routing trace expert is outside 0..{bound}")
+        if len(event.experts) != self.k:
+            raise ValueError(f"routing trace event holds {len(event.experts)} experts, not {self.k}")
+        if not (0 <= event.layer < 256 and 0 <= event.token < 65536):
+            raise ValueError("routing trace layer or token out of range")
         self.events.append(event)
 
     def to_json(self) -> str:
         ev = ",".join('{"layer":%d,"token":%d,"experts":[%s]}' % (e.layer, e.token, ",".join(str(int(x))
                                                                                             for x in e.experts))
                       for e in self.events)
-        return '{"schema":"emufpga.moe-routing.v1","model":"%s","events":[%s]}' % (self.model, ev)
+        return '{"schema":"%s","model":"%s","events":[%s]}' % (self.schema, self.model, ev)
 
 
 @dataclass
@@ -212,9 +241,11 @@ def model_parameter_bytes(cfg) -> int:
 
 
 def step_metrics(cfg, n_clients: int, step_seconds: float, routes: Optional[np.ndarray] = None,
-                 resident_bytes: Optional[int] = None, hbm_bytes_per_s: float = HBM_PEAK_BYTES_PER_S) -> ScanMetrics:
+                 resident_bytes: Optional[int] = None, hbm_bytes_per_s: Optional[float] = None) -> ScanMetrics:
     """ScanMetrics of one decode step of n_clients.  routes: the step's expert
-    ids [layer][client][k] from the device route trace (MoE models)."""
+    ids [layer][client][k] from the device route trace (MoE models);
+    hbm_bytes_per_s: the HBM read rate measured on the device
+    (emu_hbm_read_rate), which sets storage_time (0 without it)."""
     sb, sw = _weights(_shared_matrices(cfg))
     read_b, read_w, apps = sb, sw, sw * n_clients
     if cfg.n_experts:
@@ -229,15 +260,17 @@ def step_metrics(cfg, n_clients: int, step_seconds: float, routes: Optional[np.n
     total = model_parameter_bytes(cfg)
     return ScanMetrics(parameter_bytes_read=int(read_b), weights_decoded=int(read_w), weight_applications=int(apps),
                        resident_parameter_bytes=int(total if resident_bytes is None else resident_bytes),
-                       total_parameter_bytes=int(total), storage_time=read_b / hbm_bytes_per_s,
-                       compute_time=step_seconds)
+                       total_parameter_bytes=int(total),
+                       storage_time=read_b / hbm_bytes_per_s if hbm_bytes_per_s else 0.0,
+                       compute_time=step_seconds, wall_time=step_seconds)
 
 
 def routing_trace(model: str, steps_routes, n_clients: int, n_experts: int, max_events: Optional[int] = None
                   ) -> RoutingTrace:
     """RouteEvents of traced steps (each [layer][client][k] ids): token =
     step * n_clients + client, as many events as the schema's bound allows."""
-    t = RoutingTrace(model=model, n_experts=n_experts)
+    k = int(np.asarray(steps_routes[0]).shape[-1]) if len(steps_routes) else 8
+    t = RoutingTrace(model=model, n_experts=n_experts, k=k)
     limit = t.MAX_EVENTS if max_events is None else min(max_events, t.MAX_EVENTS)
     for s, ids in enumerate(steps_routes):
         for layer in range(ids.shape[0]):
@@ -248,16 +281,18 @@ def routing_trace(model: str, steps_routes, n_clients: int, n_experts: int, max_
     return t
 
 
-def expert_trace(model: str, cfg, routes: np.ndarray, step_seconds: float, layers: Optional[int] = None) -> Trace:
+def expert_trace(model: str, cfg, routes: np.ndarray, layer_us, layers: Optional[int] = None) -> Trace:
     """ExpertEvents of one traced step: every (layer, expert) with whether the
     step routed to it and how many tokens, its packed bytes and decoded
-    (f32) bytes.  The GPU streams and decodes inside the expert kernels, so
+    (f32) bytes, and the layer's measured time (layer_us[layer], from
+    emu_session_time_layers: HIP events around each layer's kernels).  The
+    GPU streams and decodes inside the same kernels as the arithmetic, so
     there is no separate read or decode phase: those times are 0 and the
-    measured step time is spread evenly over the layers as compute."""
+    whole layer interval is compute."""
     t = Trace(model=model, schedule="gpu-resident")
     eb, ew = _weights(_expert_matrices(cfg))
-    us = int(round(step_seconds * 1e6 / cfg.layers))
     for layer in range(cfg.layers if layers is None else min(layers, cfg.layers)):
+        us = int(round(float(layer_us[layer])))
         ids = np.asarray(routes[layer]).reshape(-1)
         for e in range(cfg.n_experts):
             n = int(np.count_nonzero(ids == e))

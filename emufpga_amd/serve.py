@@ -363,6 +363,13 @@ class Session:
         self.ctx.check(self.ctx.lib.emu_time_decode(self.h, steps, C.byref(ms)), "emu_time_decode")
         return ms.value
 
+    def set_options(self, f32_act: bool = False, direct: bool = False) -> None:
+        """f32_act: f32 activations in every matvec and expert (the int8-limb
+        kernels otherwise); direct: launch the step's kernels one by one
+        instead of replaying a captured graph."""
+        flags = (_lib.EMU_SESSION_F32_ACT if f32_act else 0) | (_lib.EMU_SESSION_DIRECT if direct else 0)
+        self.ctx.check(self.ctx.lib.emu_session_set_options(self.h, flags), "emu_session_set_options")
+
     def route_zipf(self, s: float, seed: int = 0) -> None:
         """Zipf(s) routing for throughput runs (0: the model's own router)."""
         self.ctx.check(self.ctx.lib.emu_session_route_zipf(self.h, float(s), int(seed)), "emu_session_route_zipf")

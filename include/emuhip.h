@@ -126,8 +126,16 @@ int emu_dequant(emu_ctx *ctx, int encoding, const void *d_src, size_t src_len, f
  * emu_weights_mfma_major makes (w_len = emu_weights_mfma_major_bytes(rows,
  * cols), EMU_E_SHAPE otherwise); taken by Q6_K at 2..8 tokens on the widths
  * the matrix-core matvec takes, EMU_E_UNSUPPORTED otherwise.  Same results
- * as GGUF order on that kernel, bit for bit. */
-enum { EMU_MV_ACCUMULATE = 1u, EMU_MV_LANE_MAJOR = 2u, EMU_MV_MFMA_MAJOR = 4u };
+ * as GGUF order on that kernel, bit for bit.
+ * Activations: by default a Q6_K matvec at one token over 4096 or 12288
+ * columns, or at 2..8 tokens on the matrix-core widths, carries x as three
+ * int8 limbs per column with a power-of-two scale per 16 columns (exact to
+ * 2^-20 of each 16-column group's largest |x|) and sums codes x limbs in
+ * int32.  EMU_MV_F32_ACT keeps x in f32 for every shape: each weight is
+ * dequantized and multiplied in f32, the reference's arithmetic
+ * (spm-qwen3-slice/src/math.rs:12-20) up to the order of the additions.
+ * It cannot be combined with the two layout flags (EMU_E_UNSUPPORTED). */
+enum { EMU_MV_ACCUMULATE = 1u, EMU_MV_LANE_MAJOR = 2u, EMU_MV_MFMA_MAJOR = 4u, EMU_MV_F32_ACT = 8u };
 int emu_qmatvec(emu_ctx *ctx, int encoding, const void *d_w, size_t w_len, uint32_t rows,
                 uint32_t cols, const float *d_x, size_t x_len, uint32_t n_tok, float *d_y,
                 uint32_t flags);
@@ -196,6 +204,16 @@ int emu_qmatvec_i8(emu_ctx *ctx, int encoding, const void *d_w, size_t w_len, ui
                    uint32_t cols, const int8_t *d_q, const float *d_scales, uint32_t n_tok,
                    float *d_y);
 
+/* What HBM delivers on this device: every 16-byte word of d_buf (bytes long,
+ * larger than the 256 MB Infinity Cache for a DRAM figure) read once per
+ * pass with the non-temporal hint the decode step's weight loads use, passes
+ * back to back after one untimed pass, timed with HIP events; gbs = bytes *
+ * passes / time.  The storage rate of the scan metrics' storage_time (the
+ * reference's raw_bandwidth is bytes over measured storage time,
+ * spm-stream-metrics/src/rates.rs:12-17).  The buffer's first word may be
+ * overwritten. */
+int emu_hbm_read_rate(emu_ctx *ctx, const void *d_buf, size_t bytes, uint32_t passes, float *gbs);
+
 /* ---- norms, RoPE, attention, router, selection -------------------------- */
 /* out[r] = x[r] * (1/sqrt(mean(x[r]^2) + eps)) * gain, for n_rows rows of width
  * (spm-smol-ops/src/norm.rs:12-21; spm-qwen3-slice/src/math.rs:1-10). */
@@ -263,12 +281,18 @@ int emu_route(emu_ctx *ctx, const float *d_logits, uint32_t n_tok, uint32_t n_ex
  * workspace holds n_tok*k activation rows and contributions
  * (emu_moe_workspace_bytes). */
 enum { EMU_ACT_SILU = 0, EMU_ACT_GELU_TANH = 1 };
+/* flags: EMU_MOE_F32_ACT runs the experts on f32 activations (the vector
+ * form: dequant + f32 FMA per weight) instead of the int8-limb matrix-core
+ * form.  The matrix-core form takes layers of up to 256 experts; wider layers
+ * take the vector form whatever the flags say. */
+enum { EMU_MOE_F32_ACT = 1u };
 typedef struct emu_moe_desc {
     int32_t enc_gate_up, enc_down;
     const void *d_gate, *d_up, *d_down;
     const float *d_down_scale; /* per-expert output scale or NULL */
     uint32_t n_experts, width, ff, k;
     int32_t act;               /* EMU_ACT_* */
+    uint32_t flags;            /* EMU_MOE_* */
 } emu_moe_desc;
 size_t emu_moe_workspace_bytes(uint32_t n_tok, uint32_t k, uint32_t width, uint32_t ff);
 int emu_moe_ffn(emu_ctx *ctx, const emu_moe_desc *desc, const float *d_x, uint32_t n_tok,
@@ -432,6 +456,31 @@ int emu_generate(emu_session *s, const uint32_t *h_prompt, uint32_t prompt_len, 
 /* Time `steps` greedy steps (after the caller's warmup) with events around the
  * region; ms receives the elapsed time. */
 int emu_time_decode(emu_session *s, uint32_t steps, float *ms);
+/* One decode step timed interval by interval (HIP events on the library's
+ * stream, kernels launched one by one): h_us[0] the embedding, h_us[1 + l]
+ * layer l, h_us[layers + 1] the output matvec and the selection, in
+ * microseconds; n must be at least layers + 2 (EMU_E_ARG).  Consumes one
+ * position like emu_time_decode (EMU_E_CONTEXT_FULL when none is left).  The
+ * reference times its serial MoE layers the same way, read/decode/compute per
+ * layer (spm-granite-moe/src/layout.rs:215-239); here reading and decoding
+ * happen inside the same kernels as the arithmetic, so a layer is one
+ * interval. */
+int emu_session_time_layers(emu_session *s, float *h_us, uint32_t n);
+/* Session options (0 by default), applied from the next step on:
+ *  - EMU_SESSION_F32_ACT: every matvec and expert keeps its activations in
+ *    f32 (dequant + f32 FMA per weight, the reference's arithmetic up to the
+ *    order of the additions: spm-qwen3-slice/src/math.rs:12-20,
+ *    spm-linear/src/stream.rs:31-125) instead of the int8-limb kernels
+ *    (activations exact to 2^-20 of each 16- or 256-column group's largest
+ *    |x|).  Slower; the mode in which greedy tokens are held identical to the
+ *    reference's over long runs.
+ *  - EMU_SESSION_DIRECT: the step's kernels are launched one by one instead
+ *    of being captured once into a HIP graph and replayed (same kernels,
+ *    same order, same results), for profilers and tracers.
+ * No reference counterpart (the reference has one arithmetic and no graphs).
+ * EMU_E_ARG for unknown bits. */
+enum { EMU_SESSION_F32_ACT = 1u, EMU_SESSION_DIRECT = 2u };
+int emu_session_set_options(emu_session *s, uint32_t flags);
 /* Routing for throughput runs of a mixture-of-experts model: with zipf_s > 0
  * every (client, position, layer) routes by the logits -s*ln(e+1) + G_e
  * (G_e Gumbel draws seeded by `seed`) in place of the router's, so its top k

@@ -94,10 +94,24 @@ def load() -> C.CDLL:
             "or_moe_layer_bytes": ([C.POINTER(MoeModelCfg)], SZ),
             "or_moe_model_step": ([C.POINTER(MoeModelCfg), C.POINTER(MoeModelWeights), P, P, P, P, U, P, U], I),
         }
+        # synth.c (absent from the planted-mistake builds of oracle.c alone)
+        optional = {
+            "or_synth_gauss": ([C.c_uint64, C.c_uint64, C.c_uint64, F], F),
+            "or_synth_ln_int": ([U], C.c_double),
+            "or_synth_cos_turn": ([U], C.c_double),
+            "or_synth_sqrt": ([C.c_double], C.c_double),
+            "or_synth_blocks": ([I, P, SZ, C.c_uint64, C.c_uint64, F], I),
+            "or_synth_f32": ([P, SZ, C.c_uint64, C.c_uint64, F], None),
+        }
         for name, (args, res) in sig.items():
             fn = getattr(lib, name)
             fn.argtypes = args
             fn.restype = res
+        for name, (args, res) in optional.items():
+            if hasattr(lib, name):
+                fn = getattr(lib, name)
+                fn.argtypes = args
+                fn.restype = res
         _lib = lib
     return _lib
 
@@ -327,3 +341,106 @@ class DenseOracle:
         buf = self.v if values else self.k
         base = (client * c.layers + layer) * c.context * kw
         return buf[base: base + c.context * kw].reshape(c.context, kw)
+
+
+def synth_blocks(dtype: int, nbytes: int, seed: int, stream: int, sd: float = 0.02) -> np.ndarray:
+    """The bytes emu_model_synth writes for one quantized tensor (synth.c)."""
+    be, bb = BLOCK[dtype]
+    if nbytes % bb:
+        raise ValueError(f"{nbytes} bytes is not whole {bb}-byte blocks")
+    out = np.empty(nbytes, np.uint8)
+    if load().or_synth_blocks(dtype, _p(out), nbytes // bb, seed, stream, sd) != 0:
+        raise ValueError(f"dtype {dtype} has no synthesis")
+    return out
+
+
+def synth_f32(n: int, seed: int, stream: int, sd: float = 0.02) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    load().or_synth_f32(_p(out), n, seed, stream, sd)
+    return out
+
+
+def synth_dense_weights(cfg: DenseCfg, seed: int) -> dict:
+    """A dense decoder's weights as emu_model_synth writes them and
+    Model.host_weights() reads them back: per layer q, k, v, o, gate, up,
+    down (tensor t of layer l from stream 16 (l + 1) + t), the embedding
+    (stream 1), the output matrix (stream 2, unless tied) and every norm gain
+    1.0."""
+    be, bb = BLOCK[cfg.dtype]
+    qw, kw = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+
+    def rb(cols):
+        return cols // be * bb
+
+    shapes = [(qw, cfg.hidden), (kw, cfg.hidden), (kw, cfg.hidden), (cfg.hidden, qw), (cfg.ffn, cfg.hidden),
+              (cfg.ffn, cfg.hidden), (cfg.hidden, cfg.ffn)]
+    layer_bytes = sum(r * rb(c) for r, c in shapes)
+    layers = np.empty(cfg.layers * layer_bytes, np.uint8)
+    for l in range(cfg.layers):
+        off = l * layer_bytes
+        for t, (r, c) in enumerate(shapes):
+            n = r * rb(c)
+            layers[off:off + n] = synth_blocks(cfg.dtype, n, seed, 16 * (l + 1) + t)
+            off += n
+    embed = synth_blocks(cfg.dtype, cfg.vocab * rb(cfg.hidden), seed, 1)
+    ones = lambda n: np.ones(n, np.float32)  # noqa: E731
+    return {
+        "layers": layers, "embed": embed,
+        "output": embed if cfg.tied else synth_blocks(cfg.dtype, cfg.vocab * rb(cfg.hidden), seed, 2),
+        "attn_norm": ones(cfg.layers * cfg.hidden), "ffn_norm": ones(cfg.layers * cfg.hidden),
+        "q_norm": ones(cfg.layers * cfg.head_dim), "k_norm": ones(cfg.layers * cfg.head_dim),
+        "out_norm": ones(cfg.hidden),
+    }
+
+
+def _align(v: int, a: int) -> int:
+    return (v + a - 1) // a * a
+
+
+def synth_moe_layer(c, seed: int, layer: int) -> list[tuple[int, np.ndarray]]:
+    """The pieces (offset in the layer, bytes) of one mixture-of-experts layer
+    as emu_model_synth writes them, in the layer layout of emu_model_create:
+    q, k, v, o, the f32 router at 16-byte alignment, then Granite/OLMoE: gate,
+    up, down experts; Gemma form: router scale and per-expert down scales
+    (1.0), the shared FFN's gate, up and down, the fused gate|up experts and
+    the down experts.  `c` carries the model's shape (serve.DenseConfig's
+    field names).  Alignment padding between pieces is not written."""
+    enc = c.encoding
+
+    def rb(e, cols):
+        return cols // BLOCK[e][0] * BLOCK[e][1]
+
+    H, QW, KW, E, FF = c.hidden, c.heads * c.head_dim, c.kv_heads * c.head_dim, c.n_experts, c.expert_ff
+    rb_h, rb_q, rb_he = rb(enc, H), rb(enc, QW), rb(c.expert_encoding, H)
+    down_enc = c.expert_down_encoding if c.gemma else c.expert_encoding
+    rb_fe = rb(down_enc, FF)
+    st = 16 * (layer + 1)
+    pieces, off = [], 0
+    for t, rows in enumerate((QW, KW, KW)):
+        pieces.append((off, synth_blocks(enc, rows * rb_h, seed, st + t)))
+        off += rows * rb_h
+    pieces.append((off, synth_blocks(enc, H * rb_q, seed, st + 3)))
+    off_r = _align(off + H * rb_q, 16)
+    pieces.append((off_r, synth_f32(E * H, seed, st + 4).view(np.uint8)))
+    if c.gemma:
+        off_rs = off_r + 4 * E * H
+        pieces.append((off_rs, np.ones(H, np.float32).view(np.uint8)))
+        off_ds = _align(off_rs + 4 * H, 16)
+        pieces.append((off_ds, np.ones(E, np.float32).view(np.uint8)))
+        off_ge = _align(off_ds + 4 * E, 16)
+        if c.shared_ff:
+            rb_sf, sff = rb(enc, c.shared_ff), c.shared_ff
+            pieces.append((off_ge, synth_blocks(enc, sff * rb_h, seed, st + 8)))
+            pieces.append((off_ge + sff * rb_h, synth_blocks(enc, sff * rb_h, seed, st + 9)))
+            pieces.append((off_ge + 2 * sff * rb_h, synth_blocks(enc, H * rb_sf, seed, st + 10)))
+            off_ge += 2 * sff * rb_h + H * rb_sf
+        ge = E * 2 * FF * rb_he
+        pieces.append((off_ge, synth_blocks(c.expert_encoding, ge, seed, st + 5)))
+        pieces.append((off_ge + ge, synth_blocks(down_enc, E * H * rb_fe, seed, st + 7)))
+    else:
+        off_ge = off_r + 4 * E * H
+        ge = E * FF * rb_he
+        pieces.append((off_ge, synth_blocks(c.expert_encoding, ge, seed, st + 5)))
+        pieces.append((off_ge + ge, synth_blocks(c.expert_encoding, ge, seed, st + 6)))
+        pieces.append((off_ge + 2 * ge, synth_blocks(down_enc, E * H * rb_fe, seed, st + 7)))
+    return pieces

@@ -238,6 +238,17 @@ int or_moe_model_step(const or_moe_model_cfg *cfg, const or_moe_model_weights *w
 /* greedy selection: tie 0 -> lowest index (top_k), 1 -> last index (max_by). */
 uint32_t or_argmax(const float *v, uint32_t n, int tie_last);
 
+/* ---- seeded synthetic weights (synth.c; no reference counterpart) -------
+ * The bytes emu_model_synth writes: N(0, sd) draws keyed by (seed, stream,
+ * element index), quantized per block.  or_synth_blocks fills nblocks blocks
+ * of dtype (OR_Q8_0/Q6_K/Q5_K/Q2_K; -1 otherwise); or_synth_f32 n floats. */
+float or_synth_gauss(uint64_t seed, uint64_t stream, uint64_t idx, float sd);
+double or_synth_ln_int(uint32_t k);
+double or_synth_cos_turn(uint32_t j);
+double or_synth_sqrt(double y);
+int or_synth_blocks(int dtype, uint8_t *dst, size_t nblocks, uint64_t seed, uint64_t stream, float sd);
+void or_synth_f32(float *dst, size_t n, uint64_t seed, uint64_t stream, float sd);
+
 #ifdef __cplusplus
 }
 #endif

@@ -181,7 +181,7 @@ def moe_ffn_f64(enc_in, enc_down, gate, up, down, down_scale, n_experts, width, 
     return out
 
 
-def moe_model_f64(cfg, w: dict, tokens_per_step, layers_limit=0):
+def moe_model_f64(cfg, w: dict, tokens_per_step, layers_limit=0, router_eps=1e-6):
     """A mixture-of-experts decoder in float64 from this module's own
     decoders, for one client: the logits of every step.  Granite
     (spm-granite-moe model.rs:330-411: interleaved RoPE, scores x score_mul,
@@ -284,7 +284,7 @@ def moe_model_f64(cfg, w: dict, tokens_per_step, layers_limit=0):
                              float(np.float32(cfg.score_mul)))
             h = h + (m["o"] @ att) * res
             if gemma:
-                rin = h * m["rscale"] / np.sqrt(np.mean(h * h) + 1e-6) / np.sqrt(H)
+                rin = h * m["rscale"] / np.sqrt(np.mean(h * h) + router_eps) / np.sqrt(H)
                 xe = norm(h, gains("ffn_norm2", layer, H), 1e-6)
                 if SF:
                     xs = norm(h, gains("ffn_norm", layer, H))

@@ -37,12 +37,12 @@ def make_experts(rng, enc_in, enc_down, n_experts, width, ff, fused):
 
 
 def run_gpu(ctx, enc_in, enc_down, gate, up, down, scale, n_experts, width, ff, k, act, x, ids, wts,
-            on_device_ids=None):
+            on_device_ids=None, flags=0):
     n_tok = x.shape[0]
     bufs = [ctx.upload(a) if a is not None else None for a in (gate, up, down)]
     bs = ctx.upload(scale) if scale is not None else None
     desc = _lib.MoeDesc(enc_in, enc_down, bufs[0].addr, bufs[1].addr if bufs[1] else None, bufs[2].addr,
-                        bs.addr if bs else None, n_experts, width, ff, k, act)
+                        bs.addr if bs else None, n_experts, width, ff, k, act, flags)
     bx = ctx.upload(x)
     if on_device_ids is None:
         bi, bw = ctx.upload(np.asarray(ids, np.int32)), ctx.upload(np.asarray(wts, np.float32))
@@ -77,16 +77,36 @@ SHAPES = [
 ]
 
 
+@pytest.mark.parametrize("f32", [False, True], ids=["limbs", "f32"])
 @pytest.mark.parametrize("shape", SHAPES, ids=[s[0] for s in SHAPES])
-def test_moe_ffn_matches_oracle(ctx, shape):
+def test_moe_ffn_matches_oracle(ctx, shape, f32):
+    """Both activation forms: the int8-limb matrix-core form (the default
+    for inputs of up to 4096 columns) and, with EMU_MOE_F32_ACT, the f32
+    vector form, which every shape takes."""
     name, enc_in, enc_down, E, W, FF, K, T, fused, act, s = shape
     rng = np.random.default_rng(sum(map(ord, name)))
     gate, up, down = make_experts(rng, enc_in, enc_down, E, W, FF, fused)
     scale = rng.uniform(0.5, 2.0, E).astype(np.float32) if fused else None
     x = rng.normal(size=(T, W)).astype(np.float32)
     ids, wts = route(zipf_logits(rng, T, E, s), K)
-    got = run_gpu(ctx, enc_in, enc_down, gate, up, down, scale, E, W, FF, K, act, x, ids, wts)
+    got = run_gpu(ctx, enc_in, enc_down, gate, up, down, scale, E, W, FF, K, act, x, ids, wts,
+                  flags=_lib.EMU_MOE_F32_ACT if f32 else 0)
     ref = oracle.moe_ffn(enc_in, enc_down, gate, up, down, scale, E, W, FF, K, act, x, ids, wts)
+    assert np.max(np.abs(got - ref)) <= 1e-4 * np.max(np.abs(ref))
+
+
+def test_more_than_256_experts(ctx):
+    """A layer of 300 experts with routes to ids past 255: the matrix-core
+    form finds experts in a 256-bit mask, so such layers take the vector
+    form, and every route is computed (ids 256..299 included)."""
+    E, W, FF, K, T = 300, 256, 256, 4, 3
+    rng = np.random.default_rng(80)
+    gate, up, down = make_experts(rng, _lib.Q6_K, _lib.Q6_K, E, W, FF, False)
+    x = rng.normal(size=(T, W)).astype(np.float32)
+    ids = np.array([[299, 256, 3, 17], [255, 280, 0, 299], [100, 257, 258, 1]])
+    wts = rng.uniform(0.1, 1.0, (T, K)).astype(np.float32)
+    got = run_gpu(ctx, _lib.Q6_K, _lib.Q6_K, gate, up, down, None, E, W, FF, K, _lib.EMU_ACT_SILU, x, ids, wts)
+    ref = oracle.moe_ffn(_lib.Q6_K, _lib.Q6_K, gate, up, down, None, E, W, FF, K, oracle.OR_ACT_SILU, x, ids, wts)
     assert np.max(np.abs(got - ref)) <= 1e-4 * np.max(np.abs(ref))
 
 

@@ -48,13 +48,17 @@ def rel_inf(a, b):
     return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
 
 
-@pytest.mark.parametrize("expert_encoding,n_clients", [(_lib.Q6_K, 1), (_lib.Q6_K, 3), (_lib.Q2_K, 2)],
-                         ids=["q6k-1", "q6k-3", "q2k-2"])
-def test_moe_decode_steps_match_oracle(ctx, expert_encoding, n_clients):
+@pytest.mark.parametrize("expert_encoding,n_clients,f32", [(_lib.Q6_K, 1, False), (_lib.Q6_K, 3, False),
+                                                            (_lib.Q2_K, 2, False), (_lib.Q6_K, 3, True),
+                                                            (_lib.Q2_K, 2, True)],
+                         ids=["q6k-1", "q6k-3", "q2k-2", "q6k-3-f32", "q2k-2-f32"])
+def test_moe_decode_steps_match_oracle(ctx, expert_encoding, n_clients, f32):
+    """f32: EMU_SESSION_F32_ACT (projections and experts on f32 activations)."""
     model = Model(ctx, small_granite(expert_encoding))
     model.synth(2024 + expert_encoding)
     context = 80  # two attention chunks: the split merge
     sess = Session(model, n_clients, context, kv_f16=True)
+    sess.set_options(f32_act=f32)
     ref = oracle_for(model, context, True, n_clients)
     rng = np.random.default_rng(expert_encoding + n_clients)
     worst = 0.0

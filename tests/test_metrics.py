@@ -66,14 +66,35 @@ def test_trace_schemas():  # spm-viz-trace/tests/schema.rs
                            '"token":7,"experts":[1,3,5,7,9,11,13,15]}]}')
     with pytest.raises(ValueError):
         r.push(M.RouteEvent(layer=0, token=0, experts=[32, 0, 1, 2, 3, 4, 5, 6]))
+    with pytest.raises(ValueError):  # v1 holds exactly 8 experts per event
+        r.push(M.RouteEvent(layer=0, token=0, experts=[1, 2, 3]))
+    # wider models keep v1's fields under their own schema name and bounds
+    w = M.RoutingTrace(model="olmoe-test", n_experts=64)
+    w.push(M.RouteEvent(layer=1, token=3, experts=[63, 40, 32, 0, 1, 2, 3, 4]))
+    assert json.loads(w.to_json())["schema"] == "emufpga-amd.moe-routing.wide.v1"
+    with pytest.raises(ValueError):
+        w.push(M.RouteEvent(layer=0, token=0, experts=[64, 0, 1, 2, 3, 4, 5, 6]))
+    assert M.RoutingTrace(model="k2", n_experts=16, k=2).schema == "emufpga-amd.moe-routing.wide.v1"
 
 
 def test_dense_step_accounting():
     cfg = QWEN3_8B_Q6K
-    m = M.step_metrics(cfg, 8, 3.3e-3)
+    m = M.step_metrics(cfg, 8, 3.3e-3, hbm_bytes_per_s=6.1e12)
     assert m.parameter_bytes_read == 6_208_204_800  # every weight row once, the output rows included
     assert m.scan_productivity() == 8.0 and m.residency() == 1.0
-    assert abs(m.eta() - 6_208_204_800 / 8e12 / 3.3e-3) < 1e-12
+    # storage time at the measured rate; raw bandwidth is that rate back
+    assert abs(m.eta() - 6_208_204_800 / 6.1e12 / 3.3e-3) < 1e-12
+    assert abs(m.raw_bandwidth() - 6.1e12) < 1.0
+    # storage overlaps compute on the GPU: the rates are over the measured step
+    assert m.elapsed() == 3.3e-3
+    assert abs(m.decoded_weights_per_sec() - m.weights_decoded / 3.3e-3) < 1e-3
+    # no measured rate: nothing is assumed
+    u = M.step_metrics(cfg, 1, 1.8e-3)
+    assert u.storage_time == 0.0 and u.raw_bandwidth() is None and u.eta() == 0.0
+    # without overlap (no wall time) the reference's sum
+    s = M.ScanMetrics(parameter_bytes_read=10, weights_decoded=10, weight_applications=10, storage_time=1.0,
+                      compute_time=2.0)
+    assert s.elapsed() == 3.0
 
 
 def test_moe_step_accounting_counts_distinct_experts_and_routed_tokens():
@@ -92,8 +113,10 @@ def test_moe_step_accounting_counts_distinct_experts_and_routed_tokens():
     assert 1.0 < m.scan_productivity() < 4.0
     tr = M.routing_trace("granite", [routes, routes], 4, 32)
     assert len(tr.events) == 2 * cfg.layers * 4 and tr.events[-1].token == 7
-    et = M.expert_trace("granite", cfg, routes, 1.5e-3)
+    layer_us = [50.0 + l for l in range(cfg.layers)]
+    et = M.expert_trace("granite", cfg, routes, layer_us)
     assert len(et.events) == cfg.layers * 32
+    assert [et.events[32 * l].layer_compute_us for l in range(cfg.layers)] == [50 + l for l in range(cfg.layers)]
     assert sum(e.routed_tokens for e in et.events) == cfg.layers * 4 * 8
     with pytest.raises(ValueError):
         M.step_metrics(OLMOE_1B_7B, 8, 1e-3)  # an MoE step needs its routes

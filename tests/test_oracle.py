@@ -713,6 +713,34 @@ def test_moe_model_forms_match_float64_composition(form):
         assert np.max(np.abs(ref[-1])) < 30.0  # the soft-cap bounds the logits
 
 
+def test_moe_model_gemma_router_eps_pinned():  # spm-granite-moe/src/gemma_smoke.rs:62
+    """The Gemma router input's eps (1e-6 in x * scale / sqrt(mean x^2 +
+    eps) / sqrt(W)) only shows where mean x^2 is near it: here the o
+    projection is zero and the embeddings are scaled by 2^-10, so the first
+    layer's residual has mean x^2 of about 1e-6.  The float64 composition with
+    eps 1e-5 must differ from the one with 1e-6 far beyond the bar (so this
+    case sees the constant), and the oracle must follow 1e-6."""
+    cfg, w = small_gemma_model(87)
+    cfg.embed_scale = 2.0 ** -10
+    H, QW, KW = cfg.hidden, cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    per_layer = w["layers"].size // cfg.layers
+    o_off = (QW + 2 * KW) * H // 256 * 210
+    layers = w["layers"].copy()
+    for layer in range(cfg.layers):
+        base = layer * per_layer + o_off
+        layers[base:base + H * QW // 256 * 210] = 0  # d = 0: the o projection adds exact zeros
+    w = {**w, "layers": layers}
+    toks = [5, 17, 299, 42]
+    e6 = npref.moe_model_f64(cfg, w, toks)
+    e5 = npref.moe_model_f64(cfg, w, toks, router_eps=1e-5)
+    for a, b in zip(e6, e5):
+        assert np.max(np.abs(a - b)) > 10 * 1e-4 * np.max(np.abs(a))
+    orc = oracle.MoeModelOracle(cfg, w, 1)
+    for t, want in zip(toks, e6):
+        got = orc.step([t])[0].astype(np.float64)
+        assert np.max(np.abs(got - want)) <= 1e-4 * np.max(np.abs(want)), t
+
+
 def test_moe_model_batched_equals_alone():  # spm-batch/tests/batching.rs:128-145
     for cfg, w in (small_olmoe_model(85), small_gemma_model(86)):
         both, alone = oracle.MoeModelOracle(cfg, w, 2), oracle.MoeModelOracle(cfg, w, 1)
