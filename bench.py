@@ -46,7 +46,23 @@ KERNEL = "qmv_limb_kernel<LimbQ6KLM, S=1, D=1, dual, norm> (fused gate|up, 2 x 1
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "qmv_limb_gate_up_qwen3_8b_pmc.txt")
 COPY_BYTES = 256 << 20  # calibration copy for the PMC byte counters
 TRACE_DIR = ""  # --trace-dir
-DIRECT = False  # --direct
+DIRECT = False  # --direct: every step launched kernel by kernel
+DIRECT_TIMED = False  # --direct-timed: prompt and warmup from the graph, timed steps kernel by kernel
+HBM_READ_BPS = None  # bytes/s a read-only stream gets from HBM on this device, measured once per run
+
+
+def layer_times(sess: Session, reps: int = 5) -> np.ndarray:
+    """Median over `reps` decode steps of each interval of a step (us): the
+    embedding, every layer, the output matvec and selection."""
+    return np.median(np.stack([sess.time_layers() for _ in range(reps)]), axis=0)
+
+
+def layer_summary(us: np.ndarray) -> dict:
+    layers = us[1:-1]
+    return {"embed_us": round(float(us[0]), 2), "layer_mean_us": round(float(layers.mean()), 2),
+            "layer_min_us": round(float(layers.min()), 2), "layer_max_us": round(float(layers.max()), 2),
+            "output_us": round(float(us[-1]), 2),
+            "how": "HIP events between each layer's kernels of one directly launched step, median of 5 steps"}
 
 
 def session(model: Model, n: int, context: int) -> Session:
@@ -56,6 +72,23 @@ def session(model: Model, n: int, context: int) -> Session:
     if DIRECT:
         sess.set_options(direct=True)
     return sess
+
+
+def before_timing(sess: Session) -> None:
+    """With --direct-timed, the steps from here on are launched kernel by
+    kernel (a kernel tracer then sees the timed steps, at their context)."""
+    if DIRECT_TIMED:
+        sess.set_options(direct=True)
+
+
+def calibration_copy(ctx) -> None:
+    """One device-to-device copy of COPY_BYTES: its PMC byte-counter readings
+    calibrate the counters (it reads and writes COPY_BYTES)."""
+    src, dst = ctx.alloc(COPY_BYTES), ctx.alloc(COPY_BYTES)
+    ctx.check(ctx.lib.emu_memcpy_dtod(ctx.h, dst.ptr, src.ptr, COPY_BYTES), "calibration copy")
+    ctx.sync()
+    src.free()
+    dst.free()
 
 
 def measured_traffic():
@@ -214,6 +247,7 @@ def smol_leg(ctx, rng, with_cpu: bool) -> dict:
     sess.generate(prompt, 1 + 8)
     ctx.sync()
     steps = 256
+    before_timing(sess)
     ms = sess.time_decode(steps)
     pos = int(sess.positions()[0])
     tok_s = steps / (ms / 1e3)
@@ -389,6 +423,7 @@ def moe_leg(ctx, rng, name: str, cfg, n_clients: int, prompt_len: int, steps: in
     sess.generate(prompt, 1 + 8)
     ctx.sync()
     log(f"{name}: {prompt_len}-token prompts + 8 warmup steps in {time.perf_counter() - t0:.1f} s")
+    before_timing(sess)
     ms = sess.time_decode(steps)
     ctx.sync()
     pos = int(sess.positions()[0])
@@ -403,13 +438,14 @@ def moe_leg(ctx, rng, name: str, cfg, n_clients: int, prompt_len: int, steps: in
         traced.append(ids)
         us += [len(set(ids[layer].reshape(-1).tolist())) for layer in range(cfg.layers)]
     mean_u = float(np.mean(us))
+    lt = layer_times(sess)
     sess.close()
     if TRACE_DIR:
         os.makedirs(TRACE_DIR, exist_ok=True)
         with open(os.path.join(TRACE_DIR, f"{name}_routes.json"), "w") as f:
             f.write(metrics.routing_trace(name, traced, n_clients, cfg.n_experts).to_json())
         with open(os.path.join(TRACE_DIR, f"{name}_experts.json"), "w") as f:
-            f.write(metrics.expert_trace(name, cfg, traced[0], ms / steps / 1e3).to_json())
+            f.write(metrics.expert_trace(name, cfg, traced[0], lt[1:-1]).to_json())
     tok_s = n_clients * steps / (ms / 1e3)
     ctx_mid = pos - steps // 2
     kv_ctx = [min(ctx_mid, cfg.window) if cfg.gemma and cfg.window and (l + 1) % cfg.global_every else ctx_mid
@@ -424,11 +460,81 @@ def moe_leg(ctx, rng, name: str, cfg, n_clients: int, prompt_len: int, steps: in
            "distinct_experts_per_layer": round(mean_u, 2), "algorithmic_bytes_per_step": int(step_bytes),
            "step_hbm_gbs": round(gbs, 1), "step_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
            # Ps / Rp / eta of one traced step (its own routes) at the timed step time
-           "scan_metrics": metrics.step_metrics(cfg, n_clients, ms / steps / 1e3, traced[0]).report()}
+           "layer_times": layer_summary(lt),
+           "scan_metrics": metrics.step_metrics(cfg, n_clients, ms / steps / 1e3, traced[0],
+                                                hbm_bytes_per_s=HBM_READ_BPS).report()}
     if with_cpu:
         out["cpu_baseline"] = moe_cpu_baseline(model)
     model.close()
     return out
+
+
+def moe_cached_leg(ctx, rng, cfg, n_clients: int, prompt_len: int, warm: int, steps: int, zipf_s: float,
+                   seed: int, n_slots: int) -> dict:
+    """The Gemma-4-style decoder with its experts behind the expert cache:
+    every expert (layers x experts x expert bytes) in pinned host memory,
+    n_slots of them in HBM, the cache's policy (admit on second use, the
+    least recently used victim of the incoming expert's own layer first, as
+    mmid-cache does: plain LRU over all layers evicts every expert before its
+    next use once a step's ~1,000 distinct experts outnumber the slots) run
+    on the device inside the captured step, admissions copied into their
+    slots, other misses read by the expert kernels over PCIe.  The prompts
+    run resident; the cache is attached after them, warmed for `warm` steps,
+    then `steps` steps are timed with its counters read on either side."""
+    from emufpga_amd.expert_cache import ExpertCache
+
+    model = Model(ctx, cfg)
+    model.synth(seed)
+    down_enc = cfg.expert_down_encoding if cfg.gemma else cfg.expert_encoding
+    eb = 2 * cfg.expert_ff * row_bytes(cfg.expert_encoding, cfg.hidden) + cfg.hidden * row_bytes(down_enc, cfg.expert_ff)
+    cache = ExpertCache(ctx, cfg.layers, cfg.n_experts, eb, n_slots=n_slots, n_transient=1, layer_aware=True)
+    t0 = time.perf_counter()
+    cache.load_model(model)
+    log(f"cached: {cfg.layers * cfg.n_experts} experts ({cfg.layers * cfg.n_experts * eb / 1e9:.1f} GB) into pinned "
+        f"host memory in {time.perf_counter() - t0:.1f} s; {n_slots} HBM slots")
+    host_gbs = ctx.host_read_rate()
+    sess = session(model, n_clients, prompt_len + warm + steps + 16)
+    sess.route_zipf(zipf_s, seed)
+    prompt = rng.integers(0, cfg.vocab, size=(n_clients, prompt_len)).astype(np.uint32)
+    sess.generate(prompt, 1)
+    sess.attach_cache(cache)
+    sess.time_decode(warm)
+    s0 = cache.stats()
+    before_timing(sess)
+    ms = sess.time_decode(steps)
+    s1 = cache.stats()
+    sess.route_trace(2)
+    sess.time_decode(2)
+    routes = sess.read_routes(0)[0]
+    pos = int(sess.positions()[0])
+    sess.close()
+    d = {k: s1[k] - s0[k] for k in ("hits", "misses", "loads", "evictions", "streamed", "bytes_uploaded",
+                                     "bytes_streamed")}
+    step_s = ms / steps / 1e3
+    total = metrics.model_parameter_bytes(cfg)
+    resident = total - cfg.layers * cfg.n_experts * eb + n_slots * eb
+    sm = metrics.step_metrics(cfg, n_clients, step_s, routes, resident_bytes=resident, hbm_bytes_per_s=HBM_READ_BPS)
+    streamed = d["bytes_streamed"] / steps
+    if HBM_READ_BPS and host_gbs > 0:  # the misses come from host memory, the rest from HBM
+        sm.storage_time = (sm.parameter_bytes_read - streamed) / HBM_READ_BPS + streamed / (host_gbs * 1e9)
+    tok_s = n_clients * steps / (ms / 1e3)
+    hit = d["hits"] / max(1, d["hits"] + d["misses"])
+    log(f"cached: {steps} steps in {ms:.1f} ms -> {tok_s:.1f} tok/s; hit rate {hit:.3f}; per step "
+        f"{d['bytes_uploaded'] / steps / 1e6:.1f} MB copied into slots, {streamed / 1e6:.1f} MB read from host "
+        f"memory; host stream {host_gbs:.1f} GB/s")
+    cache.close()
+    model.close()
+    return {"value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": round(ms / steps, 4), "clients": n_clients,
+            "context_at_timing": [pos - steps - 2, pos - 2], "hbm_slots": n_slots, "expert_bytes": eb,
+            "Rp": round(resident / total, 4), "hit_rate": round(hit, 4),
+            "bytes_copied_into_slots_per_step": int(d["bytes_uploaded"] / steps),
+            "bytes_read_from_host_per_step": int(streamed), "host_read_gbs": round(host_gbs, 1),
+            "cache_counters": d, "routing": f"Zipf(s={zipf_s}) Gumbel-top-k, seed {seed}",
+            "scan_metrics": sm.report(),
+            "workload": (f"Gemma-4-style MoE decoder as moe_gemma_b8, {n_clients} clients after {prompt_len}-token "
+                         f"prompts; its {cfg.layers * cfg.n_experts} experts in pinned host memory behind "
+                         f"{n_slots} HBM slots (admit on second use, layer-aware LRU), the policy on the device in the step; "
+                         f"{warm} warm-up steps, then {steps} timed")}
 
 
 def decode_256(ctx, model: Model, rng, batch: int, prompt: int, context: int) -> dict:
@@ -461,6 +567,10 @@ def main() -> int:
     ap.add_argument("--no-load", action="store_true", help="skip the GGUF -> HBM load leg")
     ap.add_argument("--no-smol", action="store_true", help="skip the SmolLM2 decode leg")
     ap.add_argument("--no-gemma", action="store_true", help="skip the Gemma-4-style MoE leg")
+    ap.add_argument("--no-cached", action="store_true", help="skip the Gemma-4-style leg behind the expert cache")
+    ap.add_argument("--cached-only", action="store_true",
+                    help="only the Gemma-4-style leg behind the expert cache, logged without the JSON line")
+    ap.add_argument("--cache-slots", type=int, default=1536, help="HBM slots of the expert-cache leg")
     ap.add_argument("--trace-dir", default="",
                     help="write each MoE leg's routing trace (emufpga.moe-routing.v1) and one step's expert "
                          "trace (emufpga.serial-moe.v1) as JSON files here")
@@ -477,13 +587,17 @@ def main() -> int:
     ap.add_argument("--roofline-rounds", type=int, default=8)
     ap.add_argument("--direct", action="store_true",
                     help="launch each decode step's kernels one by one instead of replaying a captured graph "
-                         "(same kernels and results); for kernel tracers and counter passes")
+                         "(same kernels and results); for counter passes, which fail on graph launches")
+    ap.add_argument("--direct-timed", action="store_true",
+                    help="replay the prompt and warmup steps from the captured graph, launch the timed steps "
+                         "kernel by kernel; for kernel traces of the timed steps at their context")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only time the dominant kernel (the fused gate|up matvec over all layers); for profiling")
     args = ap.parse_args()
-    global TRACE_DIR, DIRECT
+    global TRACE_DIR, DIRECT, DIRECT_TIMED, HBM_READ_BPS
     TRACE_DIR = args.trace_dir
     DIRECT = args.direct
+    DIRECT_TIMED = args.direct_timed
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: this decode path runs "
               "on one GPU, whose share of a sharded model is the same kernels at their real shapes",
@@ -498,7 +612,14 @@ def main() -> int:
         log(json.dumps(moe_layer_leg(ctx, args.moe_layer, args.steps)))
         ctx.close()
         return 0
+    if args.cached_only:
+        HBM_READ_BPS = ctx.hbm_read_rate() * 1e9
+        log(json.dumps(moe_cached_leg(ctx, np.random.default_rng(44), GEMMA4_MOE, 8, args.moe_prompt or 2048, 32,
+                                      args.steps, 1.2, 20260404, args.cache_slots)))
+        ctx.close()
+        return 0
     if args.smol_only:
+        calibration_copy(ctx)
         log(json.dumps(smol_leg(ctx, np.random.default_rng(42), False)))
         ctx.close()
         return 0
@@ -507,6 +628,7 @@ def main() -> int:
                "olmoe": (OLMOE_1B_7B, 8, args.moe_prompt or 1024, args.steps, 1.0, 20260303),
                "gemma": (GEMMA4_MOE, 8, args.moe_prompt or 2048, args.steps, 1.2, 20260404)}[args.moe_only]
         m_cfg, n, prompt, steps, zs, seed = leg
+        calibration_copy(ctx)
         log(json.dumps(moe_leg(ctx, np.random.default_rng(43), args.moe_only, m_cfg, n, prompt, steps, zs, False,
                                seed)))
         ctx.close()
@@ -516,15 +638,13 @@ def main() -> int:
     model.synth(20260101)
     weight_bytes = model.weight_bytes()
     log(f"synthesised {weight_bytes / 1e9:.3f} GB of Q6_K weights in {time.perf_counter() - t0:.1f} s")
+    HBM_READ_BPS = ctx.hbm_read_rate() * 1e9
+    log(f"HBM read stream (2 GiB, non-temporal): {HBM_READ_BPS / 1e9:.0f} GB/s")
 
     if args.kernel_only:
         ku_ms, ku_bytes, launches = time_gate_up(ctx, model, args.roofline_rounds)
         achieved = ku_bytes / (ku_ms / 1e3) / 1e9
-        # One device-to-device copy of known size: its counter readings
-        # calibrate the PMC byte counters (reads COPY_BYTES, writes COPY_BYTES).
-        src, dst = ctx.alloc(COPY_BYTES), ctx.alloc(COPY_BYTES)
-        ctx.check(ctx.lib.emu_memcpy_dtod(ctx.h, dst.ptr, src.ptr, COPY_BYTES), "calibration copy")
-        ctx.sync()
+        calibration_copy(ctx)
         print(json.dumps({"kernel": KERNEL, "avg_launch_us": round(ku_ms * 1e3, 3), "launches": launches,
                           "achieved_gbs": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4),
                           "calibration_copy_bytes": COPY_BYTES}), flush=True)
@@ -539,10 +659,11 @@ def main() -> int:
         sess.generate(prompt, 1 + args.warmup)  # prefill + warmup decode steps, untimed
         log(f"batch {batch}: prompt {args.prompt} + {args.warmup} warmup steps in {time.perf_counter() - t0:.1f} s")
         ctx.sync()
+        before_timing(sess)
         ms = sess.time_decode(args.steps)
         ctx.sync()
         pos = int(sess.positions()[0])
-        results[batch] = (ms, pos)
+        results[batch] = (ms, pos, layer_times(sess))
         log(f"batch {batch}: {args.steps} steps in {ms:.2f} ms -> {batch * args.steps / (ms / 1e3):.1f} tok/s "
             f"(context {pos - args.steps}..{pos})")
         sess.close()
@@ -551,7 +672,7 @@ def main() -> int:
         model.close()
         ctx.close()
         return 0
-    ms1, pos1 = results[1]
+    ms1, pos1, lt1 = results[1]
     step_ms = ms1 / args.steps
     tok_s = args.steps / (ms1 / 1e3)
     ctx_mid = pos1 - args.steps // 2
@@ -584,7 +705,9 @@ def main() -> int:
         },
         "step_hbm_gbs": round(step_gbs, 1),
         "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
-        "scan_metrics": metrics.step_metrics(cfg, 1, step_ms / 1e3).report(),
+        "hbm_read_gbs": round(HBM_READ_BPS / 1e9, 1),
+        "layer_times": layer_summary(lt1),
+        "scan_metrics": metrics.step_metrics(cfg, 1, step_ms / 1e3, hbm_bytes_per_s=HBM_READ_BPS).report(),
         "weight_bytes_per_step": weight_bytes,
         "roofline": {
             "kernel": KERNEL,
@@ -602,13 +725,15 @@ def main() -> int:
         },
     }
     if 8 in results:
-        ms8, pos8 = results[8]
+        ms8, pos8, lt8 = results[8]
         kv8 = 8 * cfg.layers * 2 * cfg.kv_width * 2 * (pos8 - args.steps // 2)
         gbs8 = (weight_bytes + kv8) / (ms8 / args.steps / 1e3) / 1e9
         out["batch8"] = {"value": round(8 * args.steps / (ms8 / 1e3), 2), "unit": "tok/s",
                          "ms_per_step": round(ms8 / args.steps, 4), "context_at_timing": [pos8 - args.steps, pos8],
                          "step_hbm_gbs": round(gbs8, 1), "step_hbm_frac": round(gbs8 / HBM_PEAK_GBS, 4),
-                         "scan_metrics": metrics.step_metrics(cfg, 8, ms8 / args.steps / 1e3).report(),
+                         "layer_times": layer_summary(lt8),
+                         "scan_metrics": metrics.step_metrics(cfg, 8, ms8 / args.steps / 1e3,
+                                                              hbm_bytes_per_s=HBM_READ_BPS).report(),
                          "matvec": "int8 MFMA (v_mfma_i32_32x32x16_i8), activation limbs as the A operand"}
     if not args.no_smol:
         out["smollm2_b1"] = smol_leg(ctx, rng, not args.no_cpu)
@@ -635,6 +760,9 @@ def main() -> int:
                                "downs and per-expert scales, 8 routed, shared GeGLU FFN of 2048, Q6_K attention "
                                "and tied 262144-row output soft-capped at 30), 8 clients; " + wl)
             out["moe_gemma_b8"] = leg
+            if not args.no_cached:
+                out["moe_gemma_cached_b8"] = moe_cached_leg(ctx, rng, GEMMA4_MOE, 8, args.moe_prompt or 2048, 32,
+                                                            32, 1.2, 20260404, args.cache_slots)
     if not args.no_load:
         out["gguf_load"] = load_leg(ctx)
     if not args.no_cpu:

@@ -122,7 +122,8 @@ EMU_ACT_SILU, EMU_ACT_GELU_TANH = 0, 1
 
 class ExpertCacheStats(C.Structure):
     _fields_ = [("hits", C.c_uint64), ("misses", C.c_uint64), ("loads", C.c_uint64), ("evictions", C.c_uint64),
-                ("streamed", C.c_uint64), ("bytes_uploaded", C.c_uint64), ("resident", C.c_uint32)]
+                ("streamed", C.c_uint64), ("bytes_uploaded", C.c_uint64), ("resident", C.c_uint32),
+                ("bytes_streamed", C.c_uint64)]
 
 
 class MoeDesc(C.Structure):
@@ -214,6 +215,9 @@ SIGNATURES = {
     "emu_session_route_zipf": [P, F, C.c_uint64],
     "emu_session_set_options": [P, U32],
     "emu_session_time_layers": [P, P, U32],
+    "emu_session_attach_expert_cache": [P, P],
+    "emu_host_device_pointer": [P, P, C.POINTER(P)],
+    "emu_expert_cache_load_model": [P, P, P, SZ],
     "emu_hbm_read_rate": [P, P, SZ, U32, P],
     "emu_session_route_trace": [P, U32],
     "emu_session_read_routes": [P, U32, P, P],

@@ -918,11 +918,19 @@ int emu_launch_attn(emu_ctx *ctx, const EmuAttnLaunch &l);
 int emu_moe_ffn_resid(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok, const int32_t *d_ids,
                       const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_state,
                       float scale, bool combine = true, bool x_planes_ready = false,
-                      uint32_t *span_counters = nullptr);
+                      uint32_t *span_counters = nullptr, const uint8_t *const *d_table = nullptr);
 size_t emu_moe_span_counters();
 const float *emu_moe_contrib(const void *d_workspace, uint32_t n_tok, uint32_t k, uint32_t ff);
 // Whether the layer takes the matrix-core form, and where its workspace
 // keeps the tokens' limb planes.
 bool emu_moe_mma_form(const emu_moe_desc *d);
+// The expert cache's device policy (cache.hip), for the decode step: set-up
+// and one layer's plan (its table of expert addresses, then the admissions'
+// copies into their slots).
+size_t emu_cache_expert_bytes(const emu_expert_cache *c);
+uint32_t emu_cache_layers(const emu_expert_cache *c);
+uint32_t emu_cache_experts(const emu_expert_cache *c);
+int emu_cache_device_enable(emu_expert_cache *c);
+int emu_cache_plan(emu_expert_cache *c, uint32_t layer, const int32_t *d_ids, int nk, const uint8_t *const **table);
 EmuLimbPlanes emu_moe_x_planes(void *d_workspace, uint32_t n_tok, uint32_t k, uint32_t width, uint32_t ff);
 int emu_attn_max_chunks(int context);

@@ -134,6 +134,8 @@ struct emu_session {
     // and after the selection, recorded only while `marking`
     std::vector<hipEvent_t> marks;
     bool marking = false;
+    // experts behind the expert cache's HBM slots (emu_session_attach_expert_cache)
+    emu_expert_cache *cache = nullptr;
 };
 
 namespace {
@@ -1227,8 +1229,12 @@ int run_moe(emu_session *s)
         // chained: the next layer's link adds the expert sum (the last layer's
         // is combined here, for the output matvec)
         const bool combine = !chain || layer + 1 == c.layers;
+        // with the expert cache: this layer's expert addresses from the
+        // device policy over the routes just written
+        const uint8_t *const *table = nullptr;
+        if (s->cache && (st = emu_cache_plan(s->cache, layer, s->rids_s, n * (int)K, &table)) != EMU_OK) return st;
         if ((st = emu_moe_ffn_resid(ctx, &d, s->xn, (uint32_t)n, s->rids_s, s->rwts_s, s->moe_ws, s->moe_ws_bytes,
-                                    s->state, c.residual_scale, combine, planes, s->span_counters)) != EMU_OK)
+                                    s->state, c.residual_scale, combine, planes, s->span_counters, table)) != EMU_OK)
             return st;
         if ((st = mark(s, layer + 1)) != EMU_OK) return st;
     }
@@ -2135,6 +2141,58 @@ extern "C" int emu_session_set_options(emu_session *s, uint32_t flags)
     if (flags & ~(uint32_t)(EMU_SESSION_F32_ACT | EMU_SESSION_DIRECT)) return EMU_E_ARG;
     s->flags = flags;
     drop_graph(s);
+    return EMU_OK;
+}
+
+extern "C" int emu_session_attach_expert_cache(emu_session *s, emu_expert_cache *c)
+{
+    if (!s) return EMU_E_ARG;
+    drop_graph(s);
+    if (!c) {
+        s->cache = nullptr;
+        return EMU_OK;
+    }
+    const emu_model *m = s->m;
+    const emu_model_config &cf = m->cfg;
+    if (!m->moe()) return EMU_E_UNSUPPORTED;
+    const size_t gate = (size_t)cf.expert_ff * m->rb_he, down = (size_t)cf.hidden * m->rb_fe;
+    if (emu_cache_layers(c) != cf.layers || emu_cache_experts(c) != cf.n_experts ||
+        emu_cache_expert_bytes(c) != 2 * gate + down)
+        return EMU_E_SHAPE;
+    int st = emu_cache_device_enable(c);
+    if (st != EMU_OK) return st;
+    s->cache = c;
+    return EMU_OK;
+}
+
+extern "C" int emu_expert_cache_load_model(emu_expert_cache *c, emu_model *m, void *h_buf, size_t h_len)
+{
+    if (!c || !m || !h_buf) return EMU_E_ARG;
+    if (!m->moe()) return EMU_E_UNSUPPORTED;
+    const emu_model_config &cf = m->cfg;
+    const size_t gate = (size_t)cf.expert_ff * m->rb_he, down = (size_t)cf.hidden * m->rb_fe, eb = 2 * gate + down;
+    if (emu_cache_layers(c) != cf.layers || emu_cache_experts(c) != cf.n_experts || emu_cache_expert_bytes(c) != eb)
+        return EMU_E_SHAPE;
+    const size_t stride = (eb + 255) & ~(size_t)255;
+    if (h_len < (size_t)cf.layers * cf.n_experts * stride) return EMU_E_ARG;
+    emu_ctx *ctx = m->ctx;
+    int st = emu_ctx_sync(ctx);
+    if (st != EMU_OK) return st;
+    uint8_t *h = static_cast<uint8_t *>(h_buf);
+    for (uint32_t l = 0; l < cf.layers; ++l) {
+        const uint8_t *lw = m->base + m->off_layers + (size_t)l * m->layer_bytes;
+        for (uint32_t e = 0; e < cf.n_experts; ++e) {
+            uint8_t *dst = h + ((size_t)l * cf.n_experts + e) * stride;
+            if (m->gemma()) { // fused gate|up rows: 2 ff rows per expert
+                EMU_HIP(ctx, hipMemcpy(dst, lw + m->off_ge + (size_t)e * 2 * gate, 2 * gate, hipMemcpyDeviceToHost));
+            } else {
+                EMU_HIP(ctx, hipMemcpy(dst, lw + m->off_ge + (size_t)e * gate, gate, hipMemcpyDeviceToHost));
+                EMU_HIP(ctx, hipMemcpy(dst + gate, lw + m->off_ue + (size_t)e * gate, gate, hipMemcpyDeviceToHost));
+            }
+            EMU_HIP(ctx, hipMemcpy(dst + 2 * gate, lw + m->off_de + (size_t)e * down, down, hipMemcpyDeviceToHost));
+            if ((st = emu_expert_cache_set_source(c, l, e, dst)) != EMU_OK) return st;
+        }
+    }
     return EMU_OK;
 }
 

@@ -1454,11 +1454,12 @@ int emu_moe_ffn_table(emu_ctx *ctx, const emu_moe_desc *d, const uint8_t *const 
 
 int emu_moe_ffn_resid(emu_ctx *ctx, const emu_moe_desc *d, const float *d_x, uint32_t n_tok, const int32_t *d_ids,
                       const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_state,
-                      float scale, bool combine, bool x_planes_ready, uint32_t *span_counters)
+                      float scale, bool combine, bool x_planes_ready, uint32_t *span_counters,
+                      const uint8_t *const *d_table)
 {
     if (!d_state) return EMU_E_ARG;
     return moe_ffn(ctx, d, d_x, n_tok, d_ids, d_weights, d_workspace, workspace_bytes, nullptr, d_state, scale,
-                   combine, nullptr, x_planes_ready && mma_form(d), span_counters);
+                   combine, d_table, x_planes_ready && mma_form(d), span_counters);
 }
 
 size_t emu_moe_span_counters() { return (size_t)kMaxTok * 8 * kMmaMaxSpans; }

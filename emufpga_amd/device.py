@@ -70,6 +70,31 @@ class Context:
     def event_record(self, slot: int) -> None:
         self.check(self.lib.emu_event_record(self.h, slot), "emu_event_record")
 
+    def hbm_read_rate(self, nbytes: int = 2 << 30, passes: int = 4) -> float:
+        """GB/s that HBM delivers to a read-only stream of an nbytes buffer
+        (emu_hbm_read_rate), the storage rate of the scan metrics."""
+        buf = self.alloc(nbytes)
+        try:
+            gbs = C.c_float()
+            self.check(self.lib.emu_hbm_read_rate(self.h, buf.ptr, nbytes, passes, C.byref(gbs)),
+                       "emu_hbm_read_rate")
+            return float(gbs.value)
+        finally:
+            buf.free()
+
+    def host_read_rate(self, nbytes: int = 1 << 30, passes: int = 2) -> float:
+        """GB/s that kernels get reading pinned host memory (over PCIe)."""
+        h, d = C.c_void_p(), C.c_void_p()
+        self.check(self.lib.emu_host_alloc(self.h, nbytes, C.byref(h)), "emu_host_alloc")
+        try:
+            C.memset(h, 0, nbytes)
+            self.check(self.lib.emu_host_device_pointer(self.h, h, C.byref(d)), "emu_host_device_pointer")
+            gbs = C.c_float()
+            self.check(self.lib.emu_hbm_read_rate(self.h, d, nbytes, passes, C.byref(gbs)), "emu_hbm_read_rate")
+            return float(gbs.value)
+        finally:
+            self.lib.emu_host_free(self.h, h)
+
     def event_elapsed(self, a: int, b: int) -> float:
         ms = C.c_float()
         self.check(self.lib.emu_event_elapsed(self.h, a, b, C.byref(ms)), "emu_event_elapsed")

@@ -58,6 +58,17 @@ class ExpertCache:
                                                                     C.c_void_p(p.value + e * self.expert_bytes)),
                            "emu_expert_cache_set_source")
 
+    def load_model(self, model) -> None:
+        """Every expert of an MoE model (serve.Model) copied from its HBM
+        tensors into one pinned host buffer, as the backing store."""
+        stride = (self.expert_bytes + 255) // 256 * 256
+        nbytes = self.layers * self.n_experts * stride
+        p = C.c_void_p()
+        self.ctx.check(self.ctx.lib.emu_host_alloc(self.ctx.h, nbytes, C.byref(p)), "emu_host_alloc")
+        self._host.append(p)
+        self.ctx.check(self.ctx.lib.emu_expert_cache_load_model(self.h, model.h, p, nbytes),
+                       "emu_expert_cache_load_model")
+
     def moe_ffn(self, desc: MoeDesc, layer: int, d_x, n_tok: int, ids: np.ndarray, d_ids, d_weights, d_ws, ws_bytes,
                 d_out) -> None:
         ids = np.ascontiguousarray(ids, np.int32)

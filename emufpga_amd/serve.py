@@ -370,6 +370,20 @@ class Session:
         flags = (_lib.EMU_SESSION_F32_ACT if f32_act else 0) | (_lib.EMU_SESSION_DIRECT if direct else 0)
         self.ctx.check(self.ctx.lib.emu_session_set_options(self.h, flags), "emu_session_set_options")
 
+    def attach_cache(self, cache) -> None:
+        """Read the experts through an ExpertCache (its policy then runs on
+        the device, inside the step); None detaches."""
+        self.ctx.check(self.ctx.lib.emu_session_attach_expert_cache(self.h, cache.h if cache else None),
+                       "emu_session_attach_expert_cache")
+
+    def time_layers(self) -> np.ndarray:
+        """One decode step timed interval by interval (microseconds): the
+        embedding, each layer, then the output matvec and selection."""
+        out = np.zeros(self.cfg.layers + 2, np.float32)
+        self.ctx.check(self.ctx.lib.emu_session_time_layers(self.h, out.ctypes.data_as(C.c_void_p), out.size),
+                       "emu_session_time_layers")
+        return out
+
     def route_zipf(self, s: float, seed: int = 0) -> None:
         """Zipf(s) routing for throughput runs (0: the model's own router)."""
         self.ctx.check(self.ctx.lib.emu_session_route_zipf(self.h, float(s), int(seed)), "emu_session_route_zipf")

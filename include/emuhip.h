@@ -211,7 +211,9 @@ int emu_qmatvec_i8(emu_ctx *ctx, int encoding, const void *d_w, size_t w_len, ui
  * passes / time.  The storage rate of the scan metrics' storage_time (the
  * reference's raw_bandwidth is bytes over measured storage time,
  * spm-stream-metrics/src/rates.rs:12-17).  The buffer's first word may be
- * overwritten. */
+ * overwritten.  d_buf may be any device-addressable memory: with the device
+ * address of pinned host memory (emu_host_device_pointer) it measures the
+ * host-memory stream over PCIe instead. */
 int emu_hbm_read_rate(emu_ctx *ctx, const void *d_buf, size_t bytes, uint32_t passes, float *gbs);
 
 /* ---- norms, RoPE, attention, router, selection -------------------------- */
@@ -315,10 +317,15 @@ int emu_moe_ffn(emu_ctx *ctx, const emu_moe_desc *desc, const float *d_x, uint32
 typedef struct emu_expert_cache emu_expert_cache;
 typedef struct emu_cache_stats {
     uint64_t hits, misses, loads, evictions, streamed, bytes_uploaded;
-    uint32_t resident; /* slots holding an expert */
+    uint32_t resident;       /* slots holding an expert */
+    uint64_t bytes_streamed; /* device policy: miss bytes the expert kernels read from host memory */
 } emu_cache_stats;
 int emu_host_alloc(emu_ctx *ctx, size_t bytes, void **h_out);
 int emu_host_free(emu_ctx *ctx, void *h);
+/* The device address of pinned host memory (from emu_host_alloc), which
+ * kernels read over PCIe: the expert cache's misses, or emu_hbm_read_rate to
+ * measure what that stream delivers. */
+int emu_host_device_pointer(emu_ctx *ctx, void *h, void **d_out);
 int emu_expert_cache_create(emu_ctx *ctx, uint32_t layers, uint32_t n_experts, size_t expert_bytes,
                             uint32_t n_slots, uint32_t n_transient, int layer_aware, emu_expert_cache **out);
 int emu_expert_cache_destroy(emu_expert_cache *c);
@@ -335,6 +342,15 @@ int emu_expert_cache_slot(const emu_expert_cache *c, uint32_t layer, uint32_t ex
 int emu_moe_ffn_cached(emu_ctx *ctx, const emu_moe_desc *desc, emu_expert_cache *c, uint32_t layer,
                        const float *d_x, uint32_t n_tok, const int32_t *h_ids, const int32_t *d_ids,
                        const float *d_weights, void *d_workspace, size_t workspace_bytes, float *d_out);
+/* Every expert of a mixture-of-experts model as the cache's backing store:
+ * expert e of layer l (gate rows, up rows, down rows) copied from the
+ * model's HBM tensors to h_buf + (l * n_experts + e) * stride, stride =
+ * expert_bytes rounded up to 256, and registered as its source.  h_buf must
+ * hold layers * n_experts * stride bytes (EMU_E_ARG) and be pinned
+ * (emu_host_alloc) for the device policy; the cache's shape must be the
+ * model's (EMU_E_SHAPE).  No reference counterpart: the reference reads
+ * experts from its GGUF file (spm-granite-moe/src/weights.rs:57-73). */
+int emu_expert_cache_load_model(emu_expert_cache *c, emu_model *model, void *h_buf, size_t h_len);
 /* The cache policy alone, on the CPU (no device): n lookups (calls[i] groups
  * them into calls; layers[i], experts[i]), each outcome 0 hit, 1 admitted,
  * 2 streamed through, and the slot (-1 when streamed). */
@@ -481,6 +497,24 @@ int emu_session_time_layers(emu_session *s, float *h_us, uint32_t n);
  * EMU_E_ARG for unknown bits. */
 enum { EMU_SESSION_F32_ACT = 1u, EMU_SESSION_DIRECT = 2u };
 int emu_session_set_options(emu_session *s, uint32_t flags);
+/* The session's mixture-of-experts steps read their experts through the
+ * expert cache instead of the model's tensors: per layer, after routing, the
+ * cache's policy (the same admit-on-second-use LRU and layer-aware choice as
+ * emu_moe_ffn_cached, expert_cache.rs:20-90, mmid-cache.hpp:134-173) runs on
+ * the device over the routes the step just wrote, the layer's experts of the
+ * step all in use until it ends.  A hit reads its HBM slot; an admission is
+ * copied from its pinned host bytes into its slot by a copy kernel right
+ * after the plan and read from there; any other miss is read by the expert
+ * kernels straight from its host bytes (over PCIe, while the resident experts
+ * compute in the same launch), so every missed byte crosses PCIe once.  The
+ * step stays one captured graph.  Counters (emu_expert_cache_stats) come from
+ * the device: bytes_uploaded the admissions' copies, bytes_streamed the other
+ * misses read from host memory.  Sources: every (layer, expert) registered, pinned and 16-byte
+ * aligned (emu_expert_cache_load_model), EMU_E_ARG otherwise; at most 2048
+ * slots and 256 experts (EMU_E_CONFIG); the cache's shape must be the
+ * model's (EMU_E_SHAPE).  Once attached, the cache's policy state is the
+ * device's and emu_moe_ffn_cached refuses it (EMU_E_CONFIG).  NULL detaches. */
+int emu_session_attach_expert_cache(emu_session *s, emu_expert_cache *c);
 /* Routing for throughput runs of a mixture-of-experts model: with zipf_s > 0
  * every (client, position, layer) routes by the logits -s*ln(e+1) + G_e
  * (G_e Gumbel draws seeded by `seed`) in place of the router's, so its top k

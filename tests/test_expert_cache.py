@@ -60,3 +60,15 @@ def test_experts_of_the_call_in_progress_are_not_evicted():
 def test_no_slots_streams_everything():
     out, slot = run(0, True, [[(0, 1)], [(0, 1)], [(0, 1)]])
     assert out == [STREAM] * 3 and slot == [-1] * 3
+
+
+def test_experts_of_a_call_are_in_use_from_its_start():
+    """mmid-cache.hpp's acquire/release: every expert of a call is in use
+    from the call's start, whatever order the call looks them up in.  One
+    slot; expert 5 is admitted on its second use; expert 3 seen once.  A
+    call of {3, 5} looks 3 up first: its second use wants a slot, but the
+    only one holds 5, which the same call uses, so 3 streams through and 5
+    hits (evicting 5 would upload it again for this very call)."""
+    out, slot = policy_trace(1, False, [0, 1, 2, 3, 3], [0] * 5, [5, 5, 3, 3, 5])
+    assert list(out) == [2, 1, 2, 2, 0]
+    assert list(slot) == [-1, 0, -1, -1, 0]

@@ -98,3 +98,87 @@ def test_cache_refuses_mismatched_shapes_and_too_many_streams(ctx):
                                     bi.ptr, bw.ptr, ws.ptr, ws_bytes, out.ptr)
     assert st == _lib.EMU_E_SHAPE
     cache.close()
+
+
+# ---- the cache inside the decode step (device policy) ----------------------
+
+def _moe_model(cfg_kind):
+    from emufpga_amd.serve import DenseConfig
+    if cfg_kind == "granite":
+        return DenseConfig(hidden=256, heads=4, kv_heads=2, head_dim=64, ffn=0, vocab=300, layers=3,
+                           rope_theta=1.5e6, eps=1e-6, style=_lib.EMU_STYLE_GRANITE, encoding=_lib.Q6_K, tied=True,
+                           qk_norm=False, n_experts=12, experts_used=3, expert_ff=256, expert_encoding=_lib.Q6_K,
+                           embed_scale=12.0, residual_scale=0.22, logit_div=6.0, score_mul=0.015625)
+    return DenseConfig(512, 4, 2, 256, 0, 300, 3, 1e4, 1e-6, _lib.EMU_STYLE_GRANITE, _lib.Q6_K, True, True,
+                       n_experts=16, experts_used=4, expert_ff=256, expert_encoding=_lib.Q5_K, embed_scale=22.6,
+                       score_mul=1.0 / 16, rope_neox=True, gemma=True, expert_down_encoding=_lib.Q8_0, shared_ff=256,
+                       window=8, global_every=2, rope_theta_global=1e6, logit_softcap=30.0)
+
+
+def _expert_bytes(cfg):
+    down_enc = cfg.expert_down_encoding if cfg.gemma else cfg.expert_encoding
+    return 2 * cfg.expert_ff * row_bytes(cfg.expert_encoding, cfg.hidden) + cfg.hidden * row_bytes(down_enc,
+                                                                                                 cfg.expert_ff)
+
+
+def _replay(routes_per_step, n_slots, layer_aware):
+    """The host policy over the same calls: per step and layer, the distinct
+    routed experts ascending."""
+    calls, layers, experts = [], [], []
+    call = 0
+    for ids in routes_per_step:
+        for layer in range(ids.shape[0]):
+            for e in sorted(set(ids[layer].reshape(-1).tolist())):
+                calls.append(call)
+                layers.append(layer)
+                experts.append(e)
+            call += 1
+    out, _ = policy_trace(n_slots, layer_aware, calls, layers, experts)
+    return {"hits": int(np.sum(out == 0)), "loads": int(np.sum(out == 1)), "streamed": int(np.sum(out == 2)),
+            "misses": int(np.sum(out != 0)), "calls": len(out)}
+
+
+@pytest.mark.parametrize("kind,n_clients,n_slots,layer_aware",
+                         [("granite", 2, 8, False), ("granite", 3, 0, False), ("gemma", 2, 10, True)],
+                         ids=["granite-8-slots", "granite-no-slots", "gemma-10-slots-layer-aware"])
+def test_decode_step_through_the_device_cache(ctx, kind, n_clients, n_slots, layer_aware):
+    """A session whose experts come through the cache (hits from HBM slots,
+    admissions copied into their slots first, other misses read from pinned
+    host memory by the expert kernels), captured and replayed as a graph: logits bit for bit those of
+    the resident experts at every step, and the device's counters equal to
+    the host policy replayed over the traced routes.  Routing is Zipf(1.5)
+    (the same draws in both sessions), so popular experts come back and hit."""
+    from emufpga_amd.serve import Model, Session
+    cfg = _moe_model(kind)
+    model = Model(ctx, cfg)
+    model.synth(404)
+    rng = np.random.default_rng(9)
+    steps = 24
+    toks = rng.integers(0, cfg.vocab, size=(steps, n_clients)).astype(np.uint32)
+    plain = Session(model, n_clients, 64)
+    plain.route_zipf(1.5, 3)
+    want = [plain.decode_step(toks[i], want_logits=True) for i in range(steps)]
+    plain.close()
+    cache = ExpertCache(ctx, cfg.layers, cfg.n_experts, _expert_bytes(cfg), n_slots=n_slots, n_transient=1,
+                        layer_aware=layer_aware)
+    cache.load_model(model)
+    sess = Session(model, n_clients, 64)
+    sess.route_zipf(1.5, 3)
+    sess.route_trace(steps)
+    sess.attach_cache(cache)
+    for i in range(steps):
+        nxt, lg = sess.decode_step(toks[i], want_logits=True)
+        assert np.array_equal(nxt, want[i][0]), i
+        assert np.array_equal(lg.view(np.uint32), want[i][1].view(np.uint32)), i
+    got = cache.stats()
+    rep = _replay([sess.read_routes(i)[0] for i in range(steps)], n_slots, layer_aware)
+    for k in ("hits", "loads", "streamed", "misses"):
+        assert got[k] == rep[k], (k, got, rep)
+    eb = _expert_bytes(cfg)
+    assert got["bytes_uploaded"] == rep["loads"] * eb and got["bytes_streamed"] == rep["streamed"] * eb
+    assert got["resident"] == min(n_slots, rep["loads"])
+    if n_slots:
+        assert rep["hits"] > 0 and rep["loads"] > 0
+    sess.close()
+    cache.close()
+    model.close()
