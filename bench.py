@@ -48,6 +48,7 @@ COPY_BYTES = 256 << 20  # calibration copy for the PMC byte counters
 TRACE_DIR = ""  # --trace-dir
 DIRECT = False  # --direct: every step launched kernel by kernel
 DIRECT_TIMED = False  # --direct-timed: prompt and warmup from the graph, timed steps kernel by kernel
+NO_ROOFLINE = False  # --no-roofline: skip the kernels' back-to-back roofline timings (profiling runs)
 HBM_READ_BPS = None  # bytes/s a read-only stream gets from HBM on this device, measured once per run
 
 
@@ -89,6 +90,22 @@ def calibration_copy(ctx) -> None:
     ctx.sync()
     src.free()
     dst.free()
+
+
+STEP_PMC_SUMMARY = os.path.join(ROOT, "profiles", "decode_step_qwen3_8b_q6k_b1_pmc.txt")
+
+
+def measured_step_bytes():
+    """HBM bytes per batch-1 decode step from the committed FETCH_SIZE
+    summary of a whole step, if any."""
+    try:
+        with open(STEP_PMC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("hbm_bytes_per_step:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def measured_traffic():
@@ -148,6 +165,58 @@ def time_gate_up(ctx: Context, model: Model, rounds: int) -> tuple[float, int, i
     ms = ctx.event_elapsed(0, 1) / (rounds * len(bases))
     algo = 2 * cfg.ffn * rb_h
     return ms, algo, rounds * len(bases)
+
+
+def time_all_matvecs(ctx: Context, model: Model, rounds: int) -> tuple[float, int]:
+    """Every batch-1 matvec of a decode step -- per layer q|k|v (RMSNorm
+    fused), o (+ residual), gate|up (RMSNorm + SwiGLU fused), down
+    (+ residual), then the 151936-row output (final RMSNorm fused) -- launched
+    back to back over all 36 layers on the lane-major copies, as the step
+    launches them: average time per step (ms) and algorithmic bytes per step."""
+    cfg = model.cfg
+    H, QW, KW, F = cfg.hidden, cfg.q_width, cfg.kv_width, cfg.ffn
+    rb_h, rb_q, rb_f = row_bytes(cfg.encoding, H), row_bytes(cfg.encoding, QW), row_bytes(cfg.encoding, F)
+    off_o = (QW + 2 * KW) * rb_h
+    off_g = off_o + H * rb_q
+    off_u = off_g + F * rb_h
+    off_d = off_u + F * rb_h
+    rng = np.random.default_rng(1)
+    x = ctx.upload(rng.normal(size=H).astype(np.float32))
+    xq = ctx.upload(rng.normal(size=QW).astype(np.float32))
+    xf = ctx.upload(rng.normal(size=F).astype(np.float32) * 0.1)
+    gain = ctx.upload(np.ones(H, np.float32))
+    yqkv, ystate, yact, ylog = ctx.alloc((QW + 2 * KW) * 4), ctx.alloc(H * 4), ctx.alloc(F * 4), ctx.alloc(cfg.vocab * 4)
+    ystate.zero()
+    bases = [model.tensor_lane_major(_lib.EMU_T_LAYER, l)[0] for l in range(cfg.layers)]
+    out_w = model.tensor_lane_major(_lib.EMU_T_OUTPUT)[0]
+    lm, acc = _lib.EMU_MV_LANE_MAJOR, _lib.EMU_MV_LANE_MAJOR | _lib.EMU_MV_ACCUMULATE
+    f = ctx.lib.emu_qmatvec_fused
+
+    def step():
+        for b in bases:
+            ctx.check(f(ctx.h, cfg.encoding, C.c_void_p(b), None, QW + 2 * KW, H, x.ptr, 1, gain.ptr, cfg.eps,
+                        yqkv.ptr, lm), "qkv")
+            ctx.check(f(ctx.h, cfg.encoding, C.c_void_p(b + off_o), None, H, QW, xq.ptr, 1, None, 0.0, ystate.ptr,
+                        acc), "o")
+            ctx.check(f(ctx.h, cfg.encoding, C.c_void_p(b + off_g), C.c_void_p(b + off_u), F, H, x.ptr, 1, gain.ptr,
+                        cfg.eps, yact.ptr, lm), "gate_up")
+            ctx.check(f(ctx.h, cfg.encoding, C.c_void_p(b + off_d), None, H, F, xf.ptr, 1, None, 0.0, ystate.ptr,
+                        acc), "down")
+        ctx.check(f(ctx.h, cfg.encoding, C.c_void_p(out_w), None, cfg.vocab, H, x.ptr, 1, gain.ptr, cfg.eps,
+                    ylog.ptr, lm), "output")
+
+    step()  # warm
+    spacer = ctx.alloc(1 << 30)
+    ctx.sync()
+    for _ in range(8 + rounds * (4 * cfg.layers + 1) // 12):
+        spacer.zero()
+    ctx.event_record(0)
+    for _ in range(rounds):
+        step()
+    ctx.event_record(1)
+    ms = ctx.event_elapsed(0, 1) / rounds
+    per_step = cfg.layers * (off_d + H * rb_f) + cfg.vocab * rb_h
+    return ms, per_step
 
 
 def cpu_baseline(model: Model, budget_s: float = 40.0) -> dict:
@@ -391,17 +460,44 @@ def moe_layer_leg(ctx, name: str, reps: int) -> dict:
 
     for _ in range(5):
         call()
+    # queued behind fills so the events time the GPU, not the host's ctypes calls
+    spacer = ctx.alloc(1 << 30)
     ctx.sync()
-    t0 = time.perf_counter()
+    for _ in range(4 + reps // 8):
+        spacer.zero()
+    ctx.event_record(0)
     for _ in range(reps):
         call()
-    ctx.sync()
-    us = (time.perf_counter() - t0) / reps * 1e6
+    ctx.event_record(1)
+    us = ctx.event_elapsed(0, 1) / reps * 1e3
+    spacer.free()
     expert_bytes = 2 * FF * (W // be_in) * bb_in + W * (FF // be_ff) * bb_ff
+    gbs = distinct * expert_bytes / (us * 1e-6) / 1e9
     log(f"{name} expert layer: {T} tokens x {K} routes, {distinct} distinct experts of {expert_bytes} B: "
-        f"{us:.1f} us per call ({reps} calls)")
+        f"{us:.1f} us per call ({reps} calls) -> {gbs:.0f} GB/s")
     return {"layer": name, "us_per_call": round(us, 2), "distinct_experts": distinct,
-            "expert_bytes": expert_bytes, "algorithmic_bytes": distinct * expert_bytes}
+            "expert_bytes": expert_bytes, "algorithmic_bytes": distinct * expert_bytes, "achieved_gbs": round(gbs, 1)}
+
+
+# Matrix-pipe busy fraction of the expert kernels, from the committed counter
+# summary (SQ_VALU_MFMA_BUSY_CYCLES over SQ_BUSY_CYCLES per SIMD).
+MFMA_BUSY = {"granite": (0.043, 0.035), "olmoe": (0.157, 0.130), "gemma": (0.109, 0.072)}
+MFMA_SOURCE = "profiles/moe_experts_layer_counters.txt"
+
+
+def expert_roofline(ctx, name: str) -> dict:
+    """The leg's selected-expert FFN layer (one emu_moe_ffn call: limbs, gate|up,
+    limbs, down, combine) at the workload's shape and skew, called back to
+    back, timed with HIP events: the experts' algorithmic bytes over the
+    call's time, and the matrix pipe's busy fraction from the counters."""
+    r = moe_layer_leg(ctx, name, 40)
+    gu, dn = MFMA_BUSY[name]
+    return {"kernel": "emu_moe_ffn (moe_mma_kernel gate|up and down on v_mfma_i32_32x32x16_i8, limbs, combine)",
+            "bound": "hbm", "achieved": r["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(r["achieved_gbs"] / HBM_PEAK_GBS, 4), "us_per_call": r["us_per_call"],
+            "algorithmic_bytes_per_call": r["algorithmic_bytes"], "distinct_experts": r["distinct_experts"],
+            "mfma_busy_gate_up": gu, "mfma_busy_down": dn, "mfma_busy_source": MFMA_SOURCE,
+            "note": "layer called back to back: its experts' rows stay in the 256 MB Infinity Cache between calls"}
 
 
 def moe_leg(ctx, rng, name: str, cfg, n_clients: int, prompt_len: int, steps: int, zipf_s: float,
@@ -462,7 +558,9 @@ def moe_leg(ctx, rng, name: str, cfg, n_clients: int, prompt_len: int, steps: in
            # Ps / Rp / eta of one traced step (its own routes) at the timed step time
            "layer_times": layer_summary(lt),
            "scan_metrics": metrics.step_metrics(cfg, n_clients, ms / steps / 1e3, traced[0],
-                                                hbm_bytes_per_s=HBM_READ_BPS).report()}
+                                                resident_bytes=model.resident_bytes(),
+                                                hbm_bytes_per_s=HBM_READ_BPS).report(),
+           "roofline": None if NO_ROOFLINE else expert_roofline(ctx, name)}
     if with_cpu:
         out["cpu_baseline"] = moe_cpu_baseline(model)
     model.close()
@@ -530,6 +628,9 @@ def moe_cached_leg(ctx, rng, cfg, n_clients: int, prompt_len: int, warm: int, st
             "bytes_copied_into_slots_per_step": int(d["bytes_uploaded"] / steps),
             "bytes_read_from_host_per_step": int(streamed), "host_read_gbs": round(host_gbs, 1),
             "cache_counters": d, "routing": f"Zipf(s={zipf_s}) Gumbel-top-k, seed {seed}",
+            "note": ("Rp counts what the step reads from HBM: every non-expert parameter and the slots; the "
+                     "synthetic model's own expert tensors, the source of the pinned host copies, also stay "
+                     "in HBM here but the cached step reads none of them"),
             "scan_metrics": sm.report(),
             "workload": (f"Gemma-4-style MoE decoder as moe_gemma_b8, {n_clients} clients after {prompt_len}-token "
                          f"prompts; its {cfg.layers * cfg.n_experts} experts in pinned host memory behind "
@@ -552,6 +653,37 @@ def decode_256(ctx, model: Model, rng, batch: int, prompt: int, context: int) ->
     log(f"batch {batch}: 256 steps from context {pos - 256} to {pos} in {ms:.1f} ms -> {tok_s:.1f} tok/s")
     return {"value": round(tok_s, 2), "unit": "tok/s", "ms_per_step": round(ms / 256, 4),
             "context_at_timing": [pos - 256, pos]}
+
+
+def trace_summary(trace_dir: str, steps: int) -> str:
+    """Kernel statistics of the last `steps` decode steps of a rocprofv3
+    kernel trace (the steps counted by their embed_kernel dispatches from the
+    end), so a profile of a run covers the timed steps at their context and
+    not its prompt."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    rows = []
+    for f in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    rows.sort()
+    embeds = [i for i, r in enumerate(rows) if "embed_kernel" in r[2]]
+    sel = rows[embeds[-steps]:]
+    agg = defaultdict(list)
+    for s0, e0, name in sel:
+        agg[name].append((e0 - s0) / 1e3)
+    tot = sum(sum(v) for v in agg.values())
+    span = (sel[-1][1] - sel[0][0]) / 1e3
+    out = [f"last {steps} decode steps: {len(sel)} dispatches, kernel time {tot:.1f} us, wall {span:.1f} us "
+           f"({span / steps:.1f} us per step, launched one by one)",
+           " share    calls    avg_us    min_us    max_us  kernel"]
+    for name, v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        out.append(f"{100 * sum(v) / tot:5.1f}%  {len(v):7d}  {sum(v) / len(v):8.2f}  {min(v):8.2f}  {max(v):8.2f}  "
+                   f"{name}")
+    return "\n".join(out)
 
 
 def main() -> int:
@@ -588,16 +720,26 @@ def main() -> int:
     ap.add_argument("--direct", action="store_true",
                     help="launch each decode step's kernels one by one instead of replaying a captured graph "
                          "(same kernels and results); for counter passes, which fail on graph launches")
+    ap.add_argument("--trace-summary", nargs=2, metavar=("TRACE_DIR", "STEPS"),
+                    help="print the kernel statistics of the last STEPS decode steps of a rocprofv3 kernel trace "
+                         "(no GPU used)")
+    ap.add_argument("--no-roofline", action="store_true",
+                    help="skip the back-to-back kernel timings (gate|up, all matvecs, expert layers), so a kernel "
+                         "trace holds the decode steps only")
     ap.add_argument("--direct-timed", action="store_true",
                     help="replay the prompt and warmup steps from the captured graph, launch the timed steps "
                          "kernel by kernel; for kernel traces of the timed steps at their context")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only time the dominant kernel (the fused gate|up matvec over all layers); for profiling")
     args = ap.parse_args()
-    global TRACE_DIR, DIRECT, DIRECT_TIMED, HBM_READ_BPS
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary[0], int(args.trace_summary[1])))
+        return 0
+    global TRACE_DIR, DIRECT, DIRECT_TIMED, HBM_READ_BPS, NO_ROOFLINE
     TRACE_DIR = args.trace_dir
     DIRECT = args.direct
     DIRECT_TIMED = args.direct_timed
+    NO_ROOFLINE = args.no_roofline
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: this decode path runs "
               "on one GPU, whose share of a sharded model is the same kernels at their real shapes",
@@ -637,6 +779,7 @@ def main() -> int:
     model = Model(ctx, cfg)
     model.synth(20260101)
     weight_bytes = model.weight_bytes()
+    resident_bytes = model.resident_bytes()
     log(f"synthesised {weight_bytes / 1e9:.3f} GB of Q6_K weights in {time.perf_counter() - t0:.1f} s")
     HBM_READ_BPS = ctx.hbm_read_rate() * 1e9
     log(f"HBM read stream (2 GiB, non-temporal): {HBM_READ_BPS / 1e9:.0f} GB/s")
@@ -679,9 +822,18 @@ def main() -> int:
     kv_bytes = cfg.layers * 2 * cfg.kv_width * 2 * ctx_mid  # fp16 K and V read per token
     step_gbs = (weight_bytes + kv_bytes) / (step_ms / 1e3) / 1e9
 
+    if args.no_roofline:
+        log(f"batch 1: {tok_s:.1f} tok/s (no roofline timings: profiling run)")
+        model.close()
+        ctx.close()
+        return 0
     ku_ms, ku_bytes, launches = time_gate_up(ctx, model, args.roofline_rounds)
     achieved = ku_bytes / (ku_ms / 1e3) / 1e9
     log(f"gate|up matvec: {ku_ms * 1e3:.2f} us avg over {launches} launches -> {achieved:.0f} GB/s")
+    am_ms, am_bytes = time_all_matvecs(ctx, model, 4)
+    am_gbs = am_bytes / (am_ms / 1e3) / 1e9
+    log(f"all batch-1 matvecs of a step back to back: {am_ms * 1e3:.1f} us for {am_bytes / 1e9:.3f} GB -> "
+        f"{am_gbs:.0f} GB/s")
 
     out = {
         "metric": METRIC,
@@ -707,7 +859,12 @@ def main() -> int:
         "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
         "hbm_read_gbs": round(HBM_READ_BPS / 1e9, 1),
         "layer_times": layer_summary(lt1),
-        "scan_metrics": metrics.step_metrics(cfg, 1, step_ms / 1e3, hbm_bytes_per_s=HBM_READ_BPS).report(),
+        # resident: every HBM copy of the weights (GGUF order, lane-major, operand order)
+        "scan_metrics": {**metrics.step_metrics(cfg, 1, step_ms / 1e3, resident_bytes=resident_bytes,
+                                                hbm_bytes_per_s=HBM_READ_BPS, read_bytes=measured_step_bytes()
+                                                ).report(),
+                         "parameter_bytes_read_source": os.path.relpath(STEP_PMC_SUMMARY, ROOT)
+                         if measured_step_bytes() else "algorithmic", "algorithmic_bytes_read": weight_bytes},
         "weight_bytes_per_step": weight_bytes,
         "roofline": {
             "kernel": KERNEL,
@@ -722,6 +879,11 @@ def main() -> int:
                               "(rocprofv3 FETCH_SIZE + WRITE_SIZE passes, each scaled by a 256 MiB copy's reading)",
             "avg_launch_us": round(ku_ms * 1e3, 3),
             "algorithmic_bytes_per_launch": ku_bytes,
+            # every matvec of a batch-1 step (145 launches), bytes over their summed time
+            "all_matvecs_b1": {"achieved": round(am_gbs, 1), "frac": round(am_gbs / HBM_PEAK_GBS, 4),
+                               "bytes_per_step": am_bytes, "us_per_step": round(am_ms * 1e3, 1),
+                               "how": "q|k|v, o, gate|up, down of 36 layers and the output matvec launched back "
+                                      "to back on the lane-major copies, HIP events over 4 rounds"},
         },
     }
     if 8 in results:
@@ -733,6 +895,7 @@ def main() -> int:
                          "step_hbm_gbs": round(gbs8, 1), "step_hbm_frac": round(gbs8 / HBM_PEAK_GBS, 4),
                          "layer_times": layer_summary(lt8),
                          "scan_metrics": metrics.step_metrics(cfg, 8, ms8 / args.steps / 1e3,
+                                                              resident_bytes=resident_bytes,
                                                               hbm_bytes_per_s=HBM_READ_BPS).report(),
                          "matvec": "int8 MFMA (v_mfma_i32_32x32x16_i8), activation limbs as the A operand"}
     if not args.no_smol:

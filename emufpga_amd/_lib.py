@@ -215,6 +215,7 @@ SIGNATURES = {
     "emu_session_route_zipf": [P, F, C.c_uint64],
     "emu_session_set_options": [P, U32],
     "emu_session_time_layers": [P, P, U32],
+    "emu_model_resident_bytes": [P, C.POINTER(C.c_uint64)],
     "emu_session_attach_expert_cache": [P, P],
     "emu_host_device_pointer": [P, P, C.POINTER(P)],
     "emu_expert_cache_load_model": [P, P, P, SZ],

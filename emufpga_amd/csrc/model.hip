@@ -61,6 +61,7 @@ struct emu_model {
     // at off_embed for the output matrix (tied or not).  Rebuilt before the
     // next decode launch whenever the weights may have changed.
     uint8_t *lm = nullptr;
+    size_t lm_bytes = 0, mm_bytes = 0; // the two derived copies' allocations
     bool lm_dirty = true;
     bool moe() const { return cfg.style == EMU_STYLE_GRANITE; }
     bool lm_takes(uint32_t cols) const { return lm && emu_limb_supports(cfg.encoding, (int)cols); }
@@ -1570,6 +1571,7 @@ extern "C" int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_m
             return st;
         }
         m->lm = static_cast<uint8_t *>(q);
+        m->lm_bytes = m->off_embed + m->embed_bytes;
     }
     // The matrix-core operand copy: every Q6_K matrix that a chained
     // matrix-core matvec reads (a width it takes, whole 32-row tiles but for
@@ -1606,6 +1608,7 @@ extern "C" int emu_model_create(emu_ctx *ctx, const emu_model_config *cfg, emu_m
                 return st;
             }
             m->mm = static_cast<uint8_t *>(q);
+            m->mm_bytes = mm_off;
         } else {
             m->mm_map.clear();
         }
@@ -1871,6 +1874,13 @@ extern "C" int emu_model_load_gguf(emu_model *m, emu_gguf *g)
         const int st = place(m, g, p);
         if (st != EMU_OK) return st;
     }
+    return EMU_OK;
+}
+
+extern "C" int emu_model_resident_bytes(const emu_model *m, uint64_t *bytes)
+{
+    if (!m || !bytes) return EMU_E_ARG;
+    *bytes = (uint64_t)m->total + m->lm_bytes + m->mm_bytes;
     return EMU_OK;
 }
 

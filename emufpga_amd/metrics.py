@@ -241,11 +241,14 @@ def model_parameter_bytes(cfg) -> int:
 
 
 def step_metrics(cfg, n_clients: int, step_seconds: float, routes: Optional[np.ndarray] = None,
-                 resident_bytes: Optional[int] = None, hbm_bytes_per_s: Optional[float] = None) -> ScanMetrics:
+                 resident_bytes: Optional[int] = None, hbm_bytes_per_s: Optional[float] = None,
+                 read_bytes: Optional[int] = None) -> ScanMetrics:
     """ScanMetrics of one decode step of n_clients.  routes: the step's expert
     ids [layer][client][k] from the device route trace (MoE models);
     hbm_bytes_per_s: the HBM read rate measured on the device
-    (emu_hbm_read_rate), which sets storage_time (0 without it)."""
+    (emu_hbm_read_rate), which sets storage_time (0 without it); read_bytes:
+    the step's HBM bytes as a counter pass measured them (FETCH_SIZE), in
+    place of the algorithmic bytes."""
     sb, sw = _weights(_shared_matrices(cfg))
     read_b, read_w, apps = sb, sw, sw * n_clients
     if cfg.n_experts:
@@ -258,6 +261,8 @@ def step_metrics(cfg, n_clients: int, step_seconds: float, routes: Optional[np.n
             read_w += ew * ids.size
             apps += ew * int(counts.sum())
     total = model_parameter_bytes(cfg)
+    if read_bytes is not None:
+        read_b = read_bytes
     return ScanMetrics(parameter_bytes_read=int(read_b), weights_decoded=int(read_w), weight_applications=int(apps),
                        resident_parameter_bytes=int(total if resident_bytes is None else resident_bytes),
                        total_parameter_bytes=int(total),

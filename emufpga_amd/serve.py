@@ -291,6 +291,12 @@ class Model:
         self.ctx.check(self.ctx.lib.emu_model_weight_bytes(self.h, C.byref(v)), "emu_model_weight_bytes")
         return v.value
 
+    def resident_bytes(self) -> int:
+        """HBM held by the parameters: GGUF order plus the derived copies."""
+        v = C.c_uint64()
+        self.ctx.check(self.ctx.lib.emu_model_resident_bytes(self.h, C.byref(v)), "emu_model_resident_bytes")
+        return v.value
+
     def host_weights(self) -> dict:
         """Every tensor copied to host memory (for the checker)."""
         c = self.cfg
@@ -379,7 +385,7 @@ class Session:
     def time_layers(self) -> np.ndarray:
         """One decode step timed interval by interval (microseconds): the
         embedding, each layer, then the output matvec and selection."""
-        out = np.zeros(self.cfg.layers + 2, np.float32)
+        out = np.zeros(self.model.cfg.layers + 2, np.float32)
         self.ctx.check(self.ctx.lib.emu_session_time_layers(self.h, out.ctypes.data_as(C.c_void_p), out.size),
                        "emu_session_time_layers")
         return out

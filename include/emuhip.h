@@ -446,6 +446,11 @@ int emu_model_sync(emu_model *model);
 int emu_model_tensor_lane_major(emu_model *model, int kind, uint32_t layer, void **d_ptr, size_t *bytes);
 /* Algorithmic weight bytes one decode step reads (all linears + output rows). */
 int emu_model_weight_bytes(const emu_model *model, uint64_t *bytes);
+/* HBM the model's parameters hold: its allocation in GGUF order (every
+ * tensor, norms included) plus the lane-major and matrix-core operand copies
+ * of its Q6_K matrices (about three times the weights for a dense Q6_K
+ * model).  No reference counterpart. */
+int emu_model_resident_bytes(const emu_model *model, uint64_t *bytes);
 
 /* A set of clients (spm-batch/src/session.rs:13-38 Client, :46-79 Scratch):
  * per-client KV caches of `context` positions (f16 when kv_f16, else f32). */

@@ -299,15 +299,17 @@ class MoeModelOracle:
         self.v = np.zeros_like(self.k)
         self.pos = np.zeros(n_clients, np.uint32)
 
-    def step(self, tokens, layers_limit: int = 0) -> np.ndarray:
+    def step(self, tokens, layers_limit: int = 0, want_logits: bool = True):
+        """One decode step; without want_logits the output projection is
+        skipped (the cache is filled the same) and None is returned."""
         toks = np.ascontiguousarray(tokens, np.uint32)
-        logits = np.empty(self.n * self.cfg.vocab, np.float32)
+        logits = np.empty(self.n * self.cfg.vocab, np.float32) if want_logits else None
         st = load().or_moe_model_step(C.byref(self.cfg), C.byref(self.ws), _p(self.k), _p(self.v), _p(self.pos),
-                                      _p(toks), self.n, _p(logits), layers_limit)
+                                      _p(toks), self.n, _p(logits) if logits is not None else None, layers_limit)
         if st != 0:
             raise ValueError(f"oracle MoE step failed ({st})")
         self.pos += 1
-        return logits.reshape(self.n, self.cfg.vocab)
+        return logits.reshape(self.n, self.cfg.vocab) if logits is not None else None
 
 
 class DenseOracle:
@@ -325,15 +327,17 @@ class DenseOracle:
         self.v = np.zeros_like(self.k)
         self.pos = np.zeros(n_clients, np.uint32)
 
-    def step(self, tokens, layers_limit: int = 0) -> np.ndarray:
+    def step(self, tokens, layers_limit: int = 0, want_logits: bool = True):
+        """One decode step; without want_logits the output projection is
+        skipped (the cache is filled the same) and None is returned."""
         toks = np.ascontiguousarray(tokens, np.uint32)
-        logits = np.empty(self.n * self.cfg.vocab, np.float32)
+        logits = np.empty(self.n * self.cfg.vocab, np.float32) if want_logits else None
         st = load().or_dense_step(C.byref(self.cfg), C.byref(self.ws), _p(self.k), _p(self.v), _p(self.pos),
-                                  _p(toks), self.n, _p(logits), layers_limit)
+                                  _p(toks), self.n, _p(logits) if logits is not None else None, layers_limit)
         if st != 0:
             raise ValueError(f"oracle dense step failed ({st})")
         self.pos += 1
-        return logits.reshape(self.n, self.cfg.vocab)
+        return logits.reshape(self.n, self.cfg.vocab) if logits is not None else None
 
     def cache(self, client: int, layer: int, values: bool) -> np.ndarray:
         c = self.cfg
@@ -397,14 +401,15 @@ def _align(v: int, a: int) -> int:
     return (v + a - 1) // a * a
 
 
-def synth_moe_layer(c, seed: int, layer: int) -> list[tuple[int, np.ndarray]]:
-    """The pieces (offset in the layer, bytes) of one mixture-of-experts layer
-    as emu_model_synth writes them, in the layer layout of emu_model_create:
-    q, k, v, o, the f32 router at 16-byte alignment, then Granite/OLMoE: gate,
-    up, down experts; Gemma form: router scale and per-expert down scales
-    (1.0), the shared FFN's gate, up and down, the fused gate|up experts and
-    the down experts.  `c` carries the model's shape (serve.DenseConfig's
-    field names).  Alignment padding between pieces is not written."""
+def moe_layer_pieces(c, layer: int) -> list[tuple[int, int, str, int, int]]:
+    """The pieces of one mixture-of-experts layer in the layer layout of
+    emu_model_create, as (offset in the layer, bytes, kind, encoding or 0,
+    synthesis stream): q, k, v, o, the f32 router at 16-byte alignment, then
+    Granite/OLMoE: gate, up, down experts; Gemma form: router scale and
+    per-expert down scales (1.0), the shared FFN's gate, up and down, the
+    fused gate|up experts and the down experts.  `c` carries the model's
+    shape (serve.DenseConfig's field names).  Alignment padding between
+    pieces belongs to no piece."""
     enc = c.encoding
 
     def rb(e, cols):
@@ -417,30 +422,68 @@ def synth_moe_layer(c, seed: int, layer: int) -> list[tuple[int, np.ndarray]]:
     st = 16 * (layer + 1)
     pieces, off = [], 0
     for t, rows in enumerate((QW, KW, KW)):
-        pieces.append((off, synth_blocks(enc, rows * rb_h, seed, st + t)))
+        pieces.append((off, rows * rb_h, "blocks", enc, st + t))
         off += rows * rb_h
-    pieces.append((off, synth_blocks(enc, H * rb_q, seed, st + 3)))
+    pieces.append((off, H * rb_q, "blocks", enc, st + 3))
     off_r = _align(off + H * rb_q, 16)
-    pieces.append((off_r, synth_f32(E * H, seed, st + 4).view(np.uint8)))
+    pieces.append((off_r, 4 * E * H, "f32", 0, st + 4))
     if c.gemma:
         off_rs = off_r + 4 * E * H
-        pieces.append((off_rs, np.ones(H, np.float32).view(np.uint8)))
+        pieces.append((off_rs, 4 * H, "ones", 0, 0))
         off_ds = _align(off_rs + 4 * H, 16)
-        pieces.append((off_ds, np.ones(E, np.float32).view(np.uint8)))
+        pieces.append((off_ds, 4 * E, "ones", 0, 0))
         off_ge = _align(off_ds + 4 * E, 16)
         if c.shared_ff:
             rb_sf, sff = rb(enc, c.shared_ff), c.shared_ff
-            pieces.append((off_ge, synth_blocks(enc, sff * rb_h, seed, st + 8)))
-            pieces.append((off_ge + sff * rb_h, synth_blocks(enc, sff * rb_h, seed, st + 9)))
-            pieces.append((off_ge + 2 * sff * rb_h, synth_blocks(enc, H * rb_sf, seed, st + 10)))
+            pieces.append((off_ge, sff * rb_h, "blocks", enc, st + 8))
+            pieces.append((off_ge + sff * rb_h, sff * rb_h, "blocks", enc, st + 9))
+            pieces.append((off_ge + 2 * sff * rb_h, H * rb_sf, "blocks", enc, st + 10))
             off_ge += 2 * sff * rb_h + H * rb_sf
         ge = E * 2 * FF * rb_he
-        pieces.append((off_ge, synth_blocks(c.expert_encoding, ge, seed, st + 5)))
-        pieces.append((off_ge + ge, synth_blocks(down_enc, E * H * rb_fe, seed, st + 7)))
+        pieces.append((off_ge, ge, "blocks", c.expert_encoding, st + 5))
+        pieces.append((off_ge + ge, E * H * rb_fe, "blocks", down_enc, st + 7))
     else:
         off_ge = off_r + 4 * E * H
         ge = E * FF * rb_he
-        pieces.append((off_ge, synth_blocks(c.expert_encoding, ge, seed, st + 5)))
-        pieces.append((off_ge + ge, synth_blocks(c.expert_encoding, ge, seed, st + 6)))
-        pieces.append((off_ge + 2 * ge, synth_blocks(down_enc, E * H * rb_fe, seed, st + 7)))
+        pieces.append((off_ge, ge, "blocks", c.expert_encoding, st + 5))
+        pieces.append((off_ge + ge, ge, "blocks", c.expert_encoding, st + 6))
+        pieces.append((off_ge + 2 * ge, E * H * rb_fe, "blocks", down_enc, st + 7))
     return pieces
+
+
+def synth_moe_layer(c, seed: int, layer: int) -> list[tuple[int, np.ndarray]]:
+    """The pieces (offset in the layer, bytes) of one mixture-of-experts layer
+    as emu_model_synth writes them (moe_layer_pieces)."""
+    out = []
+    for off, n, kind, enc, stream in moe_layer_pieces(c, layer):
+        if kind == "blocks":
+            data = synth_blocks(enc, n, seed, stream)
+        elif kind == "f32":
+            data = synth_f32(n // 4, seed, stream).view(np.uint8)
+        else:
+            data = np.ones(n // 4, np.float32).view(np.uint8)
+        out.append((off, data))
+    return out
+
+
+def synth_moe_weights(c, mcfg: "MoeModelCfg", seed: int) -> dict:
+    """A mixture-of-experts decoder's weights as emu_model_synth writes them,
+    in the layout the oracle's MoE step reads (padding zero): the layers, the
+    embedding (stream 1), the output matrix (stream 2) when untied, every
+    norm gain 1.0."""
+    lb = moe_layer_bytes(mcfg)
+    layers = np.zeros(c.layers * lb, np.uint8)
+    for l in range(c.layers):
+        for off, data in synth_moe_layer(c, seed, l):
+            layers[l * lb + off:l * lb + off + data.size] = data
+    be, bb = BLOCK[c.encoding]
+    embed = synth_blocks(c.encoding, c.vocab * (c.hidden // be) * bb, seed, 1)
+    ones = lambda n: np.ones(n, np.float32)  # noqa: E731
+    w = {"layers": layers, "embed": embed,
+         "attn_norm": ones(c.layers * c.hidden), "ffn_norm": ones(c.layers * c.hidden),
+         "q_norm": ones(c.layers * c.head_dim), "k_norm": ones(c.layers * c.head_dim), "out_norm": ones(c.hidden)}
+    if not c.tied:
+        w["output"] = synth_blocks(c.encoding, c.vocab * (c.hidden // be) * bb, seed, 2)
+    if c.gemma:
+        w["ffn_norm2"] = ones(c.layers * c.hidden)
+    return w

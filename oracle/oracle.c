@@ -793,8 +793,9 @@ int or_dense_step(const or_dense_cfg *cfg, const or_dense_weights *w, float *kv_
     }
     const uint8_t *out_w = cfg->tied ? w->embed : w->output;
     /* logits: M1 over vocabulary rows (spm-qwen3-slice/src/weights.rs:41-63,
-     * spm-batch/src/inner.rs:97-104) */
-    or_qmatvec(cfg->dtype, out_w, cfg->vocab, H, xn, n, logits, 1);
+     * spm-batch/src/inner.rs:97-104); none when the caller passes no buffer
+     * (a prompt step that only fills the cache) */
+    if (logits) or_qmatvec(cfg->dtype, out_w, cfg->vocab, H, xn, n, logits, 1);
     free(buf);
     return 0;
 }
@@ -1065,7 +1066,10 @@ int or_moe_model_step(const or_moe_model_cfg *c, const or_moe_model_weights *w, 
             }
             add_scaled(state, moe, H, c->residual_scale);
         }
-        /* run (model.rs:403-407): output norm, tied projection, / 6.0 */
+        /* run (model.rs:403-407): output norm, tied projection, / 6.0;
+         * none without a logits buffer (a prompt step that only fills the
+         * cache) */
+        if (!logits) continue;
         or_rms_norm(state, w->out_norm, H, c->eps, xn);
         float *lg = logits + (size_t)ci * c->vocab;
         or_qmatvec(c->dtype, c->untied ? w->output : w->embed, c->vocab, H, xn, 1, lg, 1);

@@ -342,3 +342,22 @@ def test_argmax_tie_rules(ctx):
     assert list(bo.read(np.int32)) == [150000, 150000]
     for t in range(2):
         assert oracle.argmax(v[t], False) == 5 and oracle.argmax(v[t], True) == 150000
+
+
+def test_session_time_layers_and_hbm_read_rate(ctx):
+    """emu_session_time_layers: one step timed interval by interval (the
+    embedding, each layer, the output), consuming one position; and the HBM
+    read-rate probe returns a plausible rate."""
+    from emufpga_amd.serve import Model, Session
+    from tests.test_gpu_model import SMALL_QWEN3
+    model = Model(ctx, SMALL_QWEN3)
+    model.synth(5)
+    sess = Session(model, 1, 8)
+    sess.decode_step([3])
+    us = sess.time_layers()
+    assert us.shape == (SMALL_QWEN3.layers + 2,) and np.all(us > 0.0) and np.all(us < 1e5)
+    assert list(sess.positions()) == [2]
+    sess.close()
+    model.close()
+    gbs = ctx.hbm_read_rate(512 << 20, 2)
+    assert 500.0 < gbs < 8000.0, gbs

@@ -120,3 +120,11 @@ def test_moe_step_accounting_counts_distinct_experts_and_routed_tokens():
     assert sum(e.routed_tokens for e in et.events) == cfg.layers * 4 * 8
     with pytest.raises(ValueError):
         M.step_metrics(OLMOE_1B_7B, 8, 1e-3)  # an MoE step needs its routes
+
+
+def test_measured_read_bytes_replace_the_algorithmic_ones():
+    cfg = QWEN3_8B_Q6K
+    m = M.step_metrics(cfg, 1, 1.8e-3, hbm_bytes_per_s=5.9e12, read_bytes=6_284_260_277)
+    assert m.parameter_bytes_read == 6_284_260_277
+    assert abs(m.storage_time - 6_284_260_277 / 5.9e12) < 1e-15
+    assert m.weights_decoded == M.step_metrics(cfg, 1, 1.8e-3).weights_decoded

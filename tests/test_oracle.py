@@ -746,3 +746,22 @@ def test_moe_model_batched_equals_alone():  # spm-batch/tests/batching.rs:128-14
         both, alone = oracle.MoeModelOracle(cfg, w, 2), oracle.MoeModelOracle(cfg, w, 1)
         for a, b in [(3, 7), (11, 2), (5, 5), (1, 0), (2, 2), (9, 8)]:
             assert np.array_equal(bits(both.step([a, b])[0]), bits(alone.step([a])[0]))
+
+
+def test_steps_without_logits_fill_the_same_cache():
+    """A prompt step without a logits buffer skips only the output
+    projection: the following step's logits are the same bits."""
+    for make in (lambda: small_olmoe_model(88), lambda: small_gemma_model(89)):
+        cfg, w = make()
+        a, b = oracle.MoeModelOracle(cfg, w, 1), oracle.MoeModelOracle(cfg, w, 1)
+        for t in (3, 7, 11):
+            a.step([t])
+            assert b.step([t], want_logits=False) is None
+        assert np.array_equal(bits(a.step([5])[0]), bits(b.step([5])[0]))
+    cfg = oracle.DenseCfg(hidden=256, heads=2, kv_heads=1, head_dim=128, ffn=256, vocab=300, layers=2, context=8,
+                          rope_theta=1e6, eps=1e-6, style=0, dtype=Q6, kv_f16=1, tied=0, qk_norm=1)
+    w = oracle.synth_dense_weights(cfg, 17)
+    a, b = oracle.DenseOracle(cfg, w, 1), oracle.DenseOracle(cfg, w, 1)
+    a.step([4])
+    assert b.step([4], want_logits=False) is None
+    assert np.array_equal(bits(a.step([9])[0]), bits(b.step([9])[0]))
