@@ -37,6 +37,8 @@
 // scales and lose precision (as f32 products of such values do).
 #include "internal.hpp"
 
+#include <type_traits>
+
 #include <math.h>
 #include <stdlib.h>
 
@@ -167,6 +169,40 @@ struct LimbQ6K {
     {
         return q6k_dot<LimbQ6K>(r, L, unit);
     }
+    // The staged dot's pieces: sub-block j's chains combined into
+    // t = 16384 s0 + 128 s1 + s2 (as in q6k_dot), and its float factor.
+    template <class CODES> __device__ static __forceinline__ int q6k_chain(const Raw &r, const Limbs &L, int j)
+    {
+        // Each chain starts with the three-operand form, its accumulator
+        // (0, or the bias term, which later rows reuse) read in place: the
+        // accumulate-in-place form the compiler picks would need a register
+        // copy of it first.
+        int a0, a1, a2;
+        {
+            const int q = (int)CODES::code(r, j, 0);
+            asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(a0) : "v"(q), "v"(comp(L.l[j][0], 0)));
+            asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(a1) : "v"(q), "v"(comp(L.l[j][1], 0)));
+            asm("v_dot4_i32_i8 %0, %1, %2, %3" : "=v"(a2) : "v"(q), "v"(comp(L.l[j][2], 0)), "v"(L.c[j]));
+        }
+#pragma unroll
+        for (int i = 1; i < 4; ++i) {
+            const int q = (int)CODES::code(r, j, i);
+            a0 = __builtin_amdgcn_sdot4(q, comp(L.l[j][0], i), a0, false);
+            a1 = __builtin_amdgcn_sdot4(q, comp(L.l[j][1], i), a1, false);
+            a2 = __builtin_amdgcn_sdot4(q, comp(L.l[j][2], i), a2, false);
+        }
+        // |result| < 2^31 by the limb bounds; unsigned arithmetic keeps the
+        // intermediate sums well defined.
+        return (int)(((uint32_t)a0 << 14) + ((uint32_t)a1 << 7) + (uint32_t)a2);
+    }
+    // Sub-block j's float factor: d folded in before t, since t * s alone
+    // (a sum of codes times x) can overflow where the dot itself does not.
+    __device__ static __forceinline__ float q6k_factor(const Raw &r, const Limbs &L, int unit, int j, float d)
+    {
+        const uint32_t sw = j < 2 ? r.sc.x : r.sc.y;
+        const float sc = (float)(int)__builtin_amdgcn_sbfe(sw, 8u * (uint32_t)((unit & 1) + 2 * (j & 1)), 8u);
+        return (sc * d) * L.s[j];
+    }
     // The limb dots of one unit: per sub-block three v_dot4_i32_i8 chains
     // over its four code words, combined exactly, then one float step.
     template <class CODES>
@@ -219,6 +255,13 @@ struct LimbQ6K {
 // for the 6-bit codes c0..c3 of sub-blocks j = 0..3 (the GGUF form takes
 // three or four operations per code word).  Same codes, so the arithmetic
 // and its results are identical to the GGUF-order kernel's.
+// An ordering point for the staged dot: t (a finished chain) is computed
+// before it, no memory access crosses it, and w reads as written by it.
+__device__ __forceinline__ void pin_word(uint4 &w, int t)
+{
+    asm volatile("" : "+v"(w.x), "+v"(w.y), "+v"(w.z), "+v"(w.w) : "v"(t) : "memory");
+}
+
 struct LimbQ6KLM : LimbQ6K {
     __device__ static __forceinline__ uint32_t code(const Raw &r, int j, int i)
     {
@@ -243,6 +286,65 @@ struct LimbQ6KLM : LimbQ6K {
         r.q = ldnt16(c + 2048u + 16u * L);
         r.sc = ldnt8(c + 3072u + 8u * (L >> 1));
         r.d = ldnt2(c + 3328u + 2u * (L >> 2));
+    }
+    // The dot with the next row's loads (next: that row's start) staged
+    // into the same registers as each code word's last use passes.  Sub-blocks 0,
+    // 1 and 2 read one word each (a, b, q) and sub-block 3 reads all three,
+    // so sub-block 3's chains go first, then 0 and a's refill, 1 and b's, 2
+    // and q's with the scales and d (the float factors are formed before).
+    // The float steps then run in sub-block order, as in q6k_dot: the same
+    // bits, with the next row's first loads out about three quarters of the
+    // dots earlier than a refill after the whole dot.
+    static constexpr bool kStaged = true;
+    __device__ static __forceinline__ float dot_staged(Raw &r, const Limbs &L, int unit, const uint8_t *next)
+    {
+        const float d = h2f((uint16_t)r.d);
+        float f[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f[j] = q6k_factor(r, L, unit, j, d);
+        const uint32_t Lu = (uint32_t)unit & 63u;
+        const uint8_t *c = next + 3360u * ((uint32_t)unit >> 6);
+        int t[4];
+        // Each chain is pinned before the refill that follows it ("memory":
+        // no load moves above the pin), and the pin nominally rewrites the
+        // word the next chain reads, so no chain moves above it either: a
+        // word's old and new values are never both live.
+        t[3] = q6k_chain<LimbQ6KLM>(r, L, 3);
+        pin_word(r.a, t[3]);
+        t[0] = q6k_chain<LimbQ6KLM>(r, L, 0);
+        pin_word(r.b, t[0]);
+        r.a = ldnt16(c + 16u * Lu);
+        t[1] = q6k_chain<LimbQ6KLM>(r, L, 1);
+        pin_word(r.q, t[1]);
+        r.b = ldnt16(c + 1024u + 16u * Lu);
+        t[2] = q6k_chain<LimbQ6KLM>(r, L, 2);
+        asm volatile("" ::"v"(t[2]), "v"(f[0]), "v"(f[1]), "v"(f[2]), "v"(f[3]) : "memory");
+        r.q = ldnt16(c + 2048u + 16u * Lu);
+        r.sc = ldnt8(c + 3072u + 8u * (Lu >> 1));
+        r.d = ldnt2(c + 3328u + 2u * (Lu >> 2));
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc = __builtin_fmaf((float)t[j], f[j], acc);
+        return acc;
+    }
+};
+
+// Whether a format stages the next row's loads inside its dot, and the call
+// to that dot (named only where a format has it).
+template <class LF, class = void> struct StagedDot {
+    static constexpr bool value = false;
+};
+template <class LF> struct StagedDot<LF, decltype((void)LF::kStaged)> {
+    static constexpr bool value = LF::kStaged;
+};
+template <bool STAGED> struct StagedCall {
+    template <class LF, class R> __device__ static float dot(R &, const Limbs &, int, const uint8_t *) { return 0.0f; }
+};
+template <> struct StagedCall<true> {
+    template <class LF, class R>
+    __device__ static __forceinline__ float dot(R &r, const Limbs &L, int unit, const uint8_t *next)
+    {
+        return LF::dot_staged(r, L, unit, next);
     }
 };
 
@@ -359,10 +461,12 @@ __global__ __launch_bounds__((EMU_WAVE * LimbShape<S, WV>::W)) void qmv_limb_ker
         typename LF::Raw raw[NR];
         float resid;
     };
+    auto row_of = [&](int k, int d) {
+        const int row = grg + (k * D + d) * total_rg;
+        return __builtin_amdgcn_readfirstlane(row < a.rows ? row : a.rows - 1);
+    };
     auto load_slot = [&](int k, int d, Slot &s) {
-        int row = grg + (k * D + d) * total_rg;
-        row = row < a.rows ? row : a.rows - 1;
-        row = __builtin_amdgcn_readfirstlane(row);
+        const int row = row_of(k, d);
 #pragma unroll
         for (int n = 0; n < NR; ++n) LF::load((n ? a.w_up : a.w) + (size_t)row * a.row_bytes, unit, s.raw[n]);
         if (ACC) s.resid = a.y[row];
@@ -442,22 +546,41 @@ __global__ __launch_bounds__((EMU_WAVE * LimbShape<S, WV>::W)) void qmv_limb_ker
     float dv[NR], dr = 0.0f;
 #pragma unroll
     for (int n = 0; n < NR; ++n) dv[n] = 0.0f;
-    for (int k = 0; k < rounds; ++k) {
+    // One round: the D slots' dots (with the next round's loads staged into
+    // them when `staged`), their reductions and the epilogue.  The gate|up
+    // pair of a format with a staged dot runs every round but the last
+    // staged, so the staged loads need no branch around them and each round
+    // waits only for the loads of the row it starts on (gate|up 16.7 ->
+    // 16.4 us back to back; the single matrices measured no better staged).
+    auto round = [&](int k, auto staged) {
         float resid[D]; // this round's residuals (the slots are refilled below)
         float v[NV];
 #pragma unroll
         for (int d = 0; d < D; ++d) {
+            if constexpr (decltype(staged)::value) {
+                // the next round's row loads go out inside the dots (every
+                // round but the last, which the caller runs unstaged)
+                const int nrow = row_of(k + 1, d);
 #pragma unroll
-            for (int n = 0; n < NR; ++n) {
-                v[d * NR + n] = LF::dot(buf[d].raw[n], L, unit);
-                // The dot is finished here, above the refill: sunk below it
-                // (its sums are not used before the reduction), it would
-                // keep the slot's old words alive beside the new ones, a
-                // register copy per word and a wavefront per SIMD lost.
-                asm volatile("" ::"v"(v[d * NR + n]));
+                for (int n = 0; n < NR; ++n)
+                    v[d * NR + n] = StagedCall<StagedDot<LF>::value>::template dot<LF>(
+                        buf[d].raw[n], L, unit, (n ? a.w_up : a.w) + (size_t)nrow * a.row_bytes);
+                resid[d] = ACC ? buf[d].resid : 0.0f;
+                if (ACC) buf[d].resid = a.y[nrow];
+            } else {
+#pragma unroll
+                for (int n = 0; n < NR; ++n) {
+                    v[d * NR + n] = LF::dot(buf[d].raw[n], L, unit);
+                    // The dot is finished here, above the refill: sunk below
+                    // it (its sums are not used before the reduction), it
+                    // would keep the slot's old words alive beside the new
+                    // ones, a register copy per word and a wavefront per
+                    // SIMD lost.
+                    asm volatile("" ::"v"(v[d * NR + n]));
+                }
+                resid[d] = ACC ? buf[d].resid : 0.0f;
+                if (k + 1 < rounds) load_slot(k + 1, d, buf[d]);
             }
-            resid[d] = ACC ? buf[d].resid : 0.0f;
-            if (k + 1 < rounds) load_slot(k + 1, d, buf[d]);
         }
         float tot[NP];
 #pragma unroll
@@ -499,6 +622,72 @@ __global__ __launch_bounds__((EMU_WAVE * LimbShape<S, WV>::W)) void qmv_limb_ker
 #pragma unroll
                 for (int e = 1; e < D; ++e) r = d == e ? resid[e] : r;
                 finish(grg + (k * D + d) * total_rg, p, r);
+            }
+        }
+    };
+    if constexpr (StagedDot<LF>::value && S == 1 && DUAL) {
+        for (int k = 0; k + 1 < rounds; ++k) round(k, std::true_type{});
+        round(rounds - 1, std::false_type{});
+    } else {
+        (void)round;
+        for (int k = 0; k < rounds; ++k) {
+            float resid[D]; // this round's residuals (the slots are refilled below)
+            float v[NV];
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+#pragma unroll
+                for (int n = 0; n < NR; ++n) {
+                    v[d * NR + n] = LF::dot(buf[d].raw[n], L, unit);
+                    // The dot is finished here, above the refill: sunk below it
+                    // (its sums are not used before the reduction), it would
+                    // keep the slot's old words alive beside the new ones, a
+                    // register copy per word and a wavefront per SIMD lost.
+                    asm volatile("" ::"v"(v[d * NR + n]));
+                }
+                resid[d] = ACC ? buf[d].resid : 0.0f;
+                if (k + 1 < rounds) load_slot(k + 1, d, buf[d]);
+            }
+            float tot[NP];
+#pragma unroll
+            for (int i = 0; i < NP; ++i) tot[i] = 2 * i + 1 < NV ? pair_sum(v[2 * i], v[2 * i + 1]) : wave_total(v[2 * i]);
+            if constexpr (S == 1) {
+#pragma unroll
+                for (int d = 0; d < D; ++d) {
+                    const int slot = k * D + d, pos = slot & (EMU_WAVE - 1);
+#pragma unroll
+                    for (int n = 0; n < NR; ++n) {
+                        const int i = d * NR + n;
+                        dv[n] = set_lane(dv[n], lane_value(tot[i / 2], (i & 1) * 16), pos);
+                    }
+                    if (ACC) dr = set_lane(dr, lane_value(resid[d], 0), pos);
+                    if (pos == EMU_WAVE - 1 || slot == rounds * D - 1) {
+                        if (lane <= pos) finish(grg + (slot - pos + lane) * total_rg, dv, dr);
+                    }
+                }
+            } else {
+                // Double-buffered by round parity: one barrier per round suffices.
+                float *pk = &part[k & 1][rg][sl][0][0];
+#pragma unroll
+                for (int i = 0; i < NP; ++i) {
+                    const int idx = 2 * i + ((lane >> 4) & 1);
+                    if ((lane & 47) == 0 && idx < NV) pk[idx] = tot[i]; // lanes 0 and 16
+                }
+                __syncthreads();
+                if (sl == 0 && lane < D) { // lane d finishes the round's row d
+                    const int d = lane;
+                    float p[NR];
+#pragma unroll
+                    for (int n = 0; n < NR; ++n) {
+                        float t = part[k & 1][rg][0][d][n];
+#pragma unroll
+                        for (int s2 = 1; s2 < S; ++s2) t += part[k & 1][rg][s2][d][n];
+                        p[n] = t;
+                    }
+                    float r = resid[0];
+#pragma unroll
+                    for (int e = 1; e < D; ++e) r = d == e ? resid[e] : r;
+                    finish(grg + (k * D + d) * total_rg, p, r);
+                }
             }
         }
     }
