@@ -655,11 +655,12 @@ def decode_256(ctx, model: Model, rng, batch: int, prompt: int, context: int) ->
             "context_at_timing": [pos - 256, pos]}
 
 
-def trace_summary(trace_dir: str, steps: int) -> str:
+def trace_summary(trace_dir: str, steps: int, by_grid: bool = False) -> str:
     """Kernel statistics of the last `steps` decode steps of a rocprofv3
     kernel trace (the steps counted by their embed_kernel dispatches from the
     end), so a profile of a run covers the timed steps at their context and
-    not its prompt."""
+    not its prompt.  With by_grid each launch shape (grid size in threads)
+    of a kernel is a line of its own."""
     import csv
     import glob
     from collections import defaultdict
@@ -668,9 +669,13 @@ def trace_summary(trace_dir: str, steps: int) -> str:
     for f in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
         with open(f) as fh:
             for r in csv.DictReader(fh):
-                rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+                name = r["Kernel_Name"]
+                if by_grid:
+                    grid = "x".join(r.get(f"Grid_Size_{a}", "") or "1" for a in "XYZ")
+                    name = f"[grid {grid}] {name}"
+                rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), name))
     rows.sort()
-    embeds = [i for i, r in enumerate(rows) if "embed_kernel" in r[2]]
+    embeds = [i for i, r in enumerate(rows) if "embed_kernel<" in r[2]]
     sel = rows[embeds[-steps]:]
     agg = defaultdict(list)
     for s0, e0, name in sel:
@@ -723,6 +728,7 @@ def main() -> int:
     ap.add_argument("--trace-summary", nargs=2, metavar=("TRACE_DIR", "STEPS"),
                     help="print the kernel statistics of the last STEPS decode steps of a rocprofv3 kernel trace "
                          "(no GPU used)")
+    ap.add_argument("--by-grid", action="store_true", help="--trace-summary: a line per launch shape")
     ap.add_argument("--no-roofline", action="store_true",
                     help="skip the back-to-back kernel timings (gate|up, all matvecs, expert layers), so a kernel "
                          "trace holds the decode steps only")
@@ -733,7 +739,7 @@ def main() -> int:
                     help="only time the dominant kernel (the fused gate|up matvec over all layers); for profiling")
     args = ap.parse_args()
     if args.trace_summary:
-        print(trace_summary(args.trace_summary[0], int(args.trace_summary[1])))
+        print(trace_summary(args.trace_summary[0], int(args.trace_summary[1]), args.by_grid))
         return 0
     global TRACE_DIR, DIRECT, DIRECT_TIMED, HBM_READ_BPS, NO_ROOFLINE
     TRACE_DIR = args.trace_dir

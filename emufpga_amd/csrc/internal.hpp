@@ -770,6 +770,7 @@ struct QmvArgs {
     int act;               // gate|up pair: EMU_ACT_SILU (SwiGLU) or EMU_ACT_GELU_TANH (GeGLU)
     float softcap;         // results -> softcap * tanh(v / softcap) after out_div (0: none)
     int f32_act;           // f32 activations: the dequant + f32 FMA kernels, not the int8-limb ones
+    int span_scales;       // multi-token chain: the A operands carry one scale per 256-column span
 };
 
 // A matvec result's epilogue: divided by out_div (when set), then added to
@@ -873,6 +874,11 @@ struct EmuMfmaLink {
     float d_scale;
     // Mode 2: the gate/up pair's activation (EMU_ACT_SILU or EMU_ACT_GELU_TANH).
     int act;
+    // The limbs under one power-of-two scale per 256-column span (xs holds
+    // [span][8 tokens]) instead of per 16-column sub-block: exact to 2^-20 of
+    // the span's largest |x|, as the expert kernels' limb planes.  Only for a
+    // matvec launched with QmvArgs::span_scales.
+    int span;
 };
 size_t emu_mfma_chain_bytes(int cols_cap, size_t max_part_bytes);
 size_t emu_mfma_part_bytes(int rows, int cols, int nmat);

@@ -87,6 +87,7 @@ struct LinkArgs {
     int d_nks;
     float d_scale;
     int act; // kLinkSwiglu: EMU_ACT_SILU or EMU_ACT_GELU_TANH
+    int span; // one limb scale per 256-column span (xs: [span][8]) instead of per sub-block
 };
 
 // A-operand layout: sub-block sb, half kh (columns 8kh..8kh+7 of the
@@ -262,6 +263,13 @@ __global__ __launch_bounds__(kLinkThreads) void mfma_link_kernel(LinkArgs a)
         }
         amax = fmaxf(amax, __shfl_xor(amax, 1, EMU_WAVE));
         bad |= __shfl_xor(bad, 1, EMU_WAVE);
+        if (a.span) { // the span's 32 pairs are 32 neighbouring lanes (npairs is whole spans)
+#pragma unroll
+            for (int o = 2; o < 32; o <<= 1) {
+                amax = fmaxf(amax, __shfl_xor(amax, o, EMU_WAVE));
+                bad |= __shfl_xor(bad, o, EMU_WAVE);
+            }
+        }
         const bool finite = !bad;
         int e2 = 0;
         (void)frexpf(finite ? amax : 0.0f, &e2); // amax < 2^e2, so |x| * 2^(6-e2) < 64
@@ -283,7 +291,9 @@ __global__ __launch_bounds__(kLinkThreads) void mfma_link_kernel(LinkArgs a)
         uint8_t *dst = a.xa + (size_t)sb * kSbBytes + (size_t)(kh * 24 + t) * 8;
 #pragma unroll
         for (int l = 0; l < 3; ++l) *reinterpret_cast<uint2 *>(dst + 64 * l) = make_uint2(lo[l], hi[l]);
-        if (kh == 0) a.xs[(size_t)sb * kMaxTok + t] = finite ? ldexpf(1.0f, e2 - 20) : __int_as_float(0x7fc00000);
+        const float scale = finite ? ldexpf(1.0f, e2 - 20) : __int_as_float(0x7fc00000);
+        if (!a.span && kh == 0) a.xs[(size_t)sb * kMaxTok + t] = scale;
+        if (a.span && (p & 31) == 0) a.xs[(size_t)(p >> 5) * kMaxTok + t] = scale;
     }
 }
 
@@ -357,13 +367,16 @@ struct Unit {
 // d follow, all with the non-temporal hint (each weight byte is read once per
 // step; batch 8 measured 0.7% faster than with plain loads).  The codes are
 // the same, so the results are bit for bit those of the GGUF-order path.
-template <bool MM>
+template <bool MM, bool SPAN>
 __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs a, int units)
 {
     const int nks = (a.cols + kSlice - 1) / kSlice, nrt = (a.rows + kTileRows - 1) / kTileRows;
     const int tid = threadIdx.x, lane = tid & (EMU_WAVE - 1), w = tid / EMU_WAVE;
     const int j = lane & 31, kh = lane >> 5;
-    const bool live = j < 24 && (j & 7) < a.n_tok; // A row j: limb j / 8 of token j % 8
+    // A row j: limb j / 8 of token j % 8.  Rows 24..31 and the rows of tokens
+    // past n_tok hold whatever the operand area holds: an MFMA output row
+    // depends on its own A row only, and those rows' outputs are never stored.
+    const int arow = j < 24 ? j : 0;
     __shared__ __align__(16) float xs[kSlice / 16 * kMaxTok];
     __shared__ float red[kWaves][kMaxTok][kTileRows];
 
@@ -383,15 +396,20 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
         // The A operands (activation limbs, from L2) load before the weights
         // (from HBM): loads complete in issue order, so the other way round
         // their round trip would follow the weights' instead of overlapping it.
-        const uint8_t *ap = a.xa + (size_t)cb * 16 * kSbBytes + (size_t)(kh * 24 + (live ? j : 0)) * 8;
+        const uint8_t *ap = a.xa + (size_t)cb * 16 * kSbBytes + (size_t)(kh * 24 + arow) * 8;
 #pragma unroll
         for (int sb = 0; sb < 16; ++sb) b.av[sb] = has ? *reinterpret_cast<const long *>(ap + sb * kSbBytes) : 0;
         // and so do the slice's activation scales (one float4 per thread:
         // half a sub-block's eight tokens; zero past the row)
         static_assert(kSlice / 16 * kMaxTok / 4 <= EMU_WAVE * kWaves, "one scale load per thread");
-        const float4 *xsrc = reinterpret_cast<const float4 *>(a.xs + (size_t)b.ks * (kSlice / 16) * kMaxTok);
-        const int t4 = tid < kSlice / 16 * kMaxTok / 4 ? tid : 0;
-        xsv = b.ks * (kSlice / 16) + t4 / 2 < a.cols / 16 ? xsrc[t4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if constexpr (SPAN) { // the block's span scale for this lane's four tokens
+            xsv = has ? *reinterpret_cast<const float4 *>(a.xs + (size_t)cb * kMaxTok + 4 * kh)
+                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        } else {
+            const float4 *xsrc = reinterpret_cast<const float4 *>(a.xs + (size_t)b.ks * (kSlice / 16) * kMaxTok);
+            const int t4 = tid < kSlice / 16 * kMaxTok / 4 ? tid : 0;
+            xsv = b.ks * (kSlice / 16) + t4 / 2 < a.cols / 16 ? xsrc[t4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
         __builtin_amdgcn_sched_barrier(0);
         // Coalesced: instruction k covers rows 4k..4k+3 of the tile, 16 lanes
         // per row (13 x 16 bytes + the 2-byte d), into this wavefront's LDS rows.
@@ -460,10 +478,8 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
             b.sc = make_uint4(0u, 0u, 0u, 0u);
             b.d = 0;
         }
-#pragma unroll
-        for (int sb = 0; sb < 16; ++sb) b.av[sb] = live ? b.av[sb] : 0; // rows past the tokens are zero
     }
-    if (tid < kSlice / 16 * kMaxTok / 4) reinterpret_cast<float4 *>(xs)[tid] = xsv;
+    if (!SPAN && tid < kSlice / 16 * kMaxTok / 4) reinterpret_cast<float4 *>(xs)[tid] = xsv;
     __syncthreads();
 
     // Sub-block sb = 8h + 2q + p: D = A x codes + A x (-32), then the float
@@ -489,18 +505,33 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
         return __builtin_amdgcn_mfma_i32_32x32x16_i8(b.av[sb], neg32, D, 0, 0, 0);
     };
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // Span scales: the block is one span, so the limb sums stay integers
+    // across its sixteen sub-blocks, each times its 8-bit scale
+    // (|D| <= 16 * 32 * 64 = 2^15, |sc| <= 2^7, sixteen of them < 2^27; the
+    // operands sign-extended from 24 bits, which the compiler folds into
+    // the full-rate v_mad_i32_i24), and one float step per block forms
+    // (16384 S0 + 128 S1 + S2) * d * s in double, rounded once.
+    int acci[3][4] = {};
     auto epi = [&](int sb, const v16i &D) {
         const uint32_t sw = sb < 4 ? b.sc.x : sb < 8 ? b.sc.y : sb < 12 ? b.sc.z : b.sc.w;
-        const float scd = (float)(int)__builtin_amdgcn_sbfe(sw, 8u * (uint32_t)(sb & 3), 8u) * d;
-        const float4 s4 = *reinterpret_cast<const float4 *>(sp + sb * kMaxTok);
-        const float s[4] = {s4.x, s4.y, s4.z, s4.w};
+        if constexpr (SPAN) {
+            const int sc = (int)__builtin_amdgcn_sbfe(sw, 8u * (uint32_t)(sb & 3), 8u);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            // |t| < 2^30 by the limb bounds; unsigned arithmetic keeps the
-            // intermediate sums well defined.
-            const uint32_t t1 = ((uint32_t)D[r] << 7) + (uint32_t)D[r + 4];
-            const int t = (int)((t1 << 7) + (uint32_t)D[r + 8]);
-            acc[r] = __builtin_fmaf((float)t, scd * s[r], acc[r]);
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int l = 0; l < 3; ++l) acci[l][r] = ((D[r + 4 * l] << 8) >> 8) * ((sc << 8) >> 8) + acci[l][r];
+        } else {
+            const float scd = (float)(int)__builtin_amdgcn_sbfe(sw, 8u * (uint32_t)(sb & 3), 8u) * d;
+            const float4 s4 = *reinterpret_cast<const float4 *>(sp + sb * kMaxTok);
+            const float s[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                // |t| < 2^30 by the limb bounds; unsigned arithmetic keeps the
+                // intermediate sums well defined.
+                const uint32_t t1 = ((uint32_t)D[r] << 7) + (uint32_t)D[r + 4];
+                const int t = (int)((t1 << 7) + (uint32_t)D[r + 8]);
+                acc[r] = __builtin_fmaf((float)t, scd * s[r], acc[r]);
+            }
         }
     };
     v16i cur = mma(0);
@@ -511,6 +542,14 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
         epi(sb, cur);
         __builtin_amdgcn_sched_barrier(0);
         if (sb + 1 < 16) cur = next;
+    }
+    if constexpr (SPAN) {
+        const float s[4] = {xsv.x, xsv.y, xsv.z, xsv.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const double t = (double)acci[0][r] * 16384.0 + (double)acci[1][r] * 128.0 + (double)acci[2][r]; // exact
+            acc[r] = (float)(t * (double)(d * s[r]));
+        }
     }
 
     // The four wavefronts' sums meet in LDS in a fixed order.
@@ -702,6 +741,8 @@ int emu_mfma_link(emu_ctx *ctx, const EmuMfmaLink &l)
     a.d_nks = l.d_nks;
     a.d_scale = l.d_scale;
     a.act = l.act;
+    a.span = l.span;
+    if (a.span && (l.cols % 256 != 0 || !a.xa)) return EMU_E_CONFIG;
     if (a.m_contrib && (!a.h || !a.m_ids || !a.m_wts || a.m_k < 1 || a.m_k > 8)) return EMU_E_CONFIG;
     if (a.d_part && (!a.h || a.d_nks < 1 || a.d_nks > kMaxSlices ||
                      (size_t)a.d_nks * kMaxTok * (size_t)l.cols * sizeof(float) > w.part_bytes))
@@ -743,12 +784,15 @@ int emu_mfma_matvec(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int
     ma.part = w.part;
     const int nks = (q.cols + kSlice - 1) / kSlice, nrt = (q.rows + kTileRows - 1) / kTileRows;
     const int units = nks * nrt * nmat;
-    if (q.mfma_major)
-        hipLaunchKernelGGL(qmv_mfma_kernel<true>, dim3((unsigned)units), dim3(EMU_WAVE * kWaves), 0, ctx->stream, ma,
-                           units);
+    const dim3 grid((unsigned)units), block(EMU_WAVE * kWaves);
+    if (q.mfma_major && q.span_scales)
+        hipLaunchKernelGGL((qmv_mfma_kernel<true, true>), grid, block, 0, ctx->stream, ma, units);
+    else if (q.mfma_major)
+        hipLaunchKernelGGL((qmv_mfma_kernel<true, false>), grid, block, 0, ctx->stream, ma, units);
+    else if (q.span_scales)
+        hipLaunchKernelGGL((qmv_mfma_kernel<false, true>), grid, block, 0, ctx->stream, ma, units);
     else
-        hipLaunchKernelGGL(qmv_mfma_kernel<false>, dim3((unsigned)units), dim3(EMU_WAVE * kWaves), 0, ctx->stream, ma,
-                           units);
+        hipLaunchKernelGGL((qmv_mfma_kernel<false, false>), grid, block, 0, ctx->stream, ma, units);
     EMU_LAUNCH_CHECK(ctx);
     if (part_nks) *part_nks = nks;
     return EMU_OK;
@@ -812,6 +856,7 @@ int emu_launch_mfma(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int
     l.gain = a.gain;
     l.eps = a.eps;
     l.limbs = true;
+    l.span = a.span_scales; // the chained steps' output matvec; the C ABI's calls keep per-sub-block scales
     if ((st = emu_mfma_link(ctx, l)) != EMU_OK) return st;
     if ((st = emu_mfma_matvec(ctx, a, n_tok, a.cols, nullptr)) != EMU_OK) return st;
     return emu_mfma_finish(ctx, a, n_tok, a.cols, key_slots);

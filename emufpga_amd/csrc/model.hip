@@ -915,9 +915,12 @@ int run_chain(emu_session *s)
         l.gain = gain;
         l.eps = c.eps;
         l.limbs = limbs;
+        l.span = 1;
         return emu_mfma_link(ctx, l);
     };
-    auto matvec = [&](const uint8_t *w, const uint8_t *w_up, size_t rb, int rows, int cols, int *nks) {
+    // span: the operands come from a link (one scale per 256-column span);
+    // the o projection's come from the attention, per 16-column sub-block
+    auto matvec = [&](const uint8_t *w, const uint8_t *w_up, size_t rb, int rows, int cols, int *nks, bool span) {
         QmvArgs q{};
         q.w = m->mm_or(w, &q.mfma_major);
         q.w_up = w_up ? m->mm_or(w_up, &q.mfma_major) : nullptr;
@@ -925,6 +928,7 @@ int run_chain(emu_session *s)
         q.rows = rows;
         q.cols = cols;
         q.nb = cols / (int)be;
+        q.span_scales = span ? 1 : 0;
         return emu_mfma_matvec(ctx, q, n, cap, nks);
     };
     uint8_t *xa = nullptr;
@@ -935,7 +939,7 @@ int run_chain(emu_session *s)
     for (uint32_t layer = 0; layer < c.layers; ++layer) {
         const uint8_t *lw = m->base + m->off_layers + (size_t)layer * m->layer_bytes;
         int nks = 0;
-        if ((st = matvec(lw + m->off_q, nullptr, m->rb_h, QW + 2 * KW, H, &nks)) != EMU_OK) return st;
+        if ((st = matvec(lw + m->off_q, nullptr, m->rb_h, QW + 2 * KW, H, &nks, true)) != EMU_OK) return st;
         // Attention adds the q|k|v slices itself and writes the o
         // projection's operands: no link kernel on either side of it.
         EmuAttnLaunch al = layer_attn(s, layer);
@@ -946,11 +950,11 @@ int run_chain(emu_session *s)
         al.xa = xa;
         al.xs = xs;
         if ((st = emu_launch_attn(ctx, al)) != EMU_OK) return st;
-        if ((st = matvec(lw + m->off_o, nullptr, m->rb_q, H, QW, &nks)) != EMU_OK) return st;
+        if ((st = matvec(lw + m->off_o, nullptr, m->rb_q, H, QW, &nks, false)) != EMU_OK) return st;
         if ((st = link(1, nks, 1, s->state, nullptr, H, ffn_norm + (size_t)layer * H, true)) != EMU_OK) return st;
-        if ((st = matvec(lw + m->off_g, lw + m->off_u, m->rb_h, F, H, &nks)) != EMU_OK) return st;
+        if ((st = matvec(lw + m->off_g, lw + m->off_u, m->rb_h, F, H, &nks, true)) != EMU_OK) return st;
         if ((st = link(2, nks, 2, nullptr, nullptr, F, nullptr, true)) != EMU_OK) return st;
-        if ((st = matvec(lw + m->off_d, nullptr, m->rb_f, H, F, &nks)) != EMU_OK) return st;
+        if ((st = matvec(lw + m->off_d, nullptr, m->rb_f, H, F, &nks, true)) != EMU_OK) return st;
         const float *next = layer + 1 < c.layers ? attn_norm + (size_t)(layer + 1) * H : out_norm;
         if ((st = link(1, nks, 1, s->state, nullptr, H, next, true)) != EMU_OK) return st;
         if ((st = mark(s, layer + 1)) != EMU_OK) return st;
@@ -965,6 +969,7 @@ int run_chain(emu_session *s)
     out.keys = s->keys;
     out.key_stride = (int)s->key_stride;
     out.tie_last = c.style == EMU_STYLE_SMOL ? 1 : 0;
+    out.span_scales = 1;
     if ((st = emu_mfma_matvec(ctx, out, n, cap, nullptr)) != EMU_OK) return st;
     int slots = 0;
     if ((st = emu_mfma_finish(ctx, out, n, cap, &slots)) != EMU_OK) return st;
@@ -1041,6 +1046,7 @@ int run_moe(emu_session *s)
             l.gain = attn_norm + (size_t)layer * H;
             l.eps = c.eps;
             l.limbs = true;
+            l.span = 1;
             if (layer > 0) { // the previous layer's (shared down and) expert sum join the residual here
                 l.h = s->state;
                 l.d_part = sd_nks > 0;
@@ -1061,6 +1067,7 @@ int run_moe(emu_session *s)
             q.rows = (int)(QW + 2 * KW);
             q.cols = (int)H;
             q.nb = (int)(H / be);
+            q.span_scales = 1; // the link's operands
             int nks = 0;
             if ((st = emu_mfma_matvec(ctx, q, n, cap, &nks)) != EMU_OK) return st;
             EmuAttnLaunch al = layer_attn(s, layer);
@@ -1174,6 +1181,7 @@ int run_moe(emu_session *s)
                 la.cols_cap = cap;
                 la.n_tok = n;
                 la.limbs = true;
+                la.span = 1;
                 la.act = EMU_ACT_GELU_TANH;
                 if ((st = emu_mfma_link(ctx, la)) != EMU_OK) return st;
                 QmvArgs dq{};
@@ -1185,6 +1193,7 @@ int run_moe(emu_session *s)
                 dq.y = s->state;
                 dq.accumulate = 1;
                 dq.acc_scale = c.residual_scale;
+                dq.span_scales = 1; // the link's operands
                 if ((st = emu_mfma_matvec(ctx, dq, n, cap, &sd_nks)) != EMU_OK) return st;
                 if (layer + 1 == c.layers && (st = emu_mfma_finish(ctx, dq, n, cap, nullptr)) != EMU_OK) return st;
             } else if (c.shared_ff) {
@@ -1256,6 +1265,7 @@ int run_moe(emu_session *s)
     out.out_div = c.logit_div;
     out.softcap = c.logit_softcap;
     out.f32_act = s->f32();
+    out.span_scales = chain ? 1 : 0;
     int slots = 0;
     // chained: the output on the matrix cores at any client count, as the
     // projections before it (a client's logits do not depend on the batch)
