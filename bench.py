@@ -691,6 +691,33 @@ def trace_summary(trace_dir: str, steps: int, by_grid: bool = False) -> str:
     return "\n".join(out)
 
 
+def pmc_summary(pmc_dir: str, match: str) -> str:
+    """Median counter values per dispatch of the kernels whose name contains
+    `match` in a rocprofv3 --pmc run, one line per (kernel, grid size)."""
+    import csv
+    import glob
+    import statistics
+    from collections import defaultdict
+
+    per = defaultdict(lambda: defaultdict(float))  # (kernel, grid) -> (dispatch, counter) -> value
+    for f in glob.glob(os.path.join(pmc_dir, "**", "*counter_collection.csv"), recursive=True):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                if match not in r["Kernel_Name"]:
+                    continue
+                grid = r.get("Grid_Size") or "x".join(r.get(f"Grid_Size_{a}", "") or "1" for a in "XYZ")
+                per[(r["Kernel_Name"], grid)][(r["Dispatch_Id"], r["Counter_Name"])] += float(r["Counter_Value"])
+    out = []
+    for (name, grid), vals in sorted(per.items(), key=lambda kv: kv[0][1]):
+        by_counter = defaultdict(list)
+        for (_, counter), v in vals.items():
+            by_counter[counter].append(v)
+        n = max(len(v) for v in by_counter.values())
+        cs = ", ".join(f"{c} {statistics.median(v):.0f}" for c, v in sorted(by_counter.items()))
+        out.append(f"[grid {grid}] {n} dispatches: {cs}  {name}")
+    return "\n".join(out)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -729,6 +756,9 @@ def main() -> int:
                     help="print the kernel statistics of the last STEPS decode steps of a rocprofv3 kernel trace "
                          "(no GPU used)")
     ap.add_argument("--by-grid", action="store_true", help="--trace-summary: a line per launch shape")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("PMC_DIR", "MATCH"),
+                    help="print median counters per dispatch of the kernels matching MATCH in a rocprofv3 --pmc run "
+                         "(no GPU used)")
     ap.add_argument("--no-roofline", action="store_true",
                     help="skip the back-to-back kernel timings (gate|up, all matvecs, expert layers), so a kernel "
                          "trace holds the decode steps only")
@@ -740,6 +770,9 @@ def main() -> int:
     args = ap.parse_args()
     if args.trace_summary:
         print(trace_summary(args.trace_summary[0], int(args.trace_summary[1]), args.by_grid))
+        return 0
+    if args.pmc_summary:
+        print(pmc_summary(args.pmc_summary[0], args.pmc_summary[1]))
         return 0
     global TRACE_DIR, DIRECT, DIRECT_TIMED, HBM_READ_BPS, NO_ROOFLINE
     TRACE_DIR = args.trace_dir
