@@ -391,20 +391,22 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
         b.mat = v / nrt;
         const int cb = b.ks * kWaves + w; // this wavefront's 256-column block
         // The last slice of a row whose width is not a multiple of the slice
-        // has wavefronts past the row: they load nothing and add zeros.
+        // has wavefronts past the row: they read the row's last block and
+        // add zeros (d = 0, and every sum is a finite integer).
         const bool has = cb < a.cols / 256;
+        const int cbl = has ? cb : a.cols / 256 - 1; // a block of the row: past it, scaled by zero
         // The A operands (activation limbs, from L2) load before the weights
         // (from HBM): loads complete in issue order, so the other way round
         // their round trip would follow the weights' instead of overlapping it.
-        const uint8_t *ap = a.xa + (size_t)cb * 16 * kSbBytes + (size_t)(kh * 24 + arow) * 8;
+        const uint8_t *ap = a.xa + (size_t)cbl * 16 * kSbBytes + (size_t)(kh * 24 + arow) * 8;
 #pragma unroll
-        for (int sb = 0; sb < 16; ++sb) b.av[sb] = has ? *reinterpret_cast<const long *>(ap + sb * kSbBytes) : 0;
+        for (int sb = 0; sb < 16; ++sb) b.av[sb] = *reinterpret_cast<const long *>(ap + sb * kSbBytes);
         // and so do the slice's activation scales (one float4 per thread:
         // half a sub-block's eight tokens; zero past the row)
         static_assert(kSlice / 16 * kMaxTok / 4 <= EMU_WAVE * kWaves, "one scale load per thread");
         if constexpr (SPAN) { // the block's span scale for this lane's four tokens
-            xsv = has ? *reinterpret_cast<const float4 *>(a.xs + (size_t)cb * kMaxTok + 4 * kh)
-                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            xsv = *reinterpret_cast<const float4 *>(a.xs + (size_t)cbl * kMaxTok + 4 * kh);
+            if (!has) xsv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         } else {
             const float4 *xsrc = reinterpret_cast<const float4 *>(a.xs + (size_t)b.ks * (kSlice / 16) * kMaxTok);
             const int t4 = tid < kSlice / 16 * kMaxTok / 4 ? tid : 0;
@@ -414,8 +416,8 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
         // Coalesced: instruction k covers rows 4k..4k+3 of the tile, 16 lanes
         // per row (13 x 16 bytes + the 2-byte d), into this wavefront's LDS rows.
         const int r4 = lane >> 4, c16 = lane & 15;
-        if (MM && has) { // uniform
-            const uint8_t *cp = a.w[b.mat] + ((size_t)b.rt * (a.cols / 256) + cb) * kMmChunk;
+        if (MM) {
+            const uint8_t *cp = a.w[b.mat] + ((size_t)b.rt * (a.cols / 256) + cbl) * kMmChunk;
 #pragma unroll
             for (int i = 0; i < 6; ++i) {
                 const uint4 q4 = ldnt16(cp + 1024 * i + 16 * lane);
@@ -431,14 +433,14 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
             // conversion of d, whose wait then took the whole first batch (a
             // second HBM round trip per workgroup; batch 8 2,500 -> 2,590 tok/s).
             __builtin_amdgcn_sched_barrier(0);
-        } else if (has) { // uniform
+        } else {
             uint4 raw[8];
             uint16_t dd[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 int row = b.rt * kTileRows + 4 * k + r4;
                 row = row < a.rows ? row : a.rows - 1; // a valid row; never stored
-                const uint8_t *bp = a.w[b.mat] + (size_t)row * a.row_bytes + (size_t)cb * 210;
+                const uint8_t *bp = a.w[b.mat] + (size_t)row * a.row_bytes + (size_t)cbl * 210;
                 if (c16 < 13) raw[k] = ld16(bp + 16 * c16);
                 else if (c16 == 13) dd[k] = ld2(bp + 208);
             }
@@ -466,21 +468,13 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
             const uint2 s0 = *reinterpret_cast<const uint2 *>(bp + 192), s1 = *reinterpret_cast<const uint2 *>(bp + 200);
             b.sc = make_uint4(s0.x, s0.y, s1.x, s1.y);
             b.d = *reinterpret_cast<const uint16_t *>(bp + 208);
-        } else { // zero codes, scales and d: this wavefront adds exact zeros
-#pragma unroll
-            for (int i = 0; i < 24; ++i) b.cw[i] = 0u;
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int p = 0; p < 2; ++p) {
-                    b.ql[h][0][p] = b.ql[h][1][p] = b.qh[h][p] = make_uint2(0u, 0u);
-                }
-            b.sc = make_uint4(0u, 0u, 0u, 0u);
-            b.d = 0;
         }
+        if (!has) b.d = 0; // d = 0: the block's (finite, integer) sums add exact zeros
     }
-    if (!SPAN && tid < kSlice / 16 * kMaxTok / 4) reinterpret_cast<float4 *>(xs)[tid] = xsv;
-    __syncthreads();
+    if constexpr (!SPAN) { // the slice's scales, shared by the workgroup
+        if (tid < kSlice / 16 * kMaxTok / 4) reinterpret_cast<float4 *>(xs)[tid] = xsv;
+        __syncthreads();
+    }
 
     // Sub-block sb = 8h + 2q + p: D = A x codes + A x (-32), then the float
     // step.  Software-pipelined by hand (the next sub-block's MFMAs go out
