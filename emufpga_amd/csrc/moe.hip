@@ -1104,8 +1104,8 @@ template <int KIND> __device__ __forceinline__ int position_vec(const MoeArgs &a
     return KIND == kMmaUp ? v / a.k : v;
 }
 
-template <class F, int KIND, int ACT>
-__global__ __launch_bounds__(kThreads, 2) void moe_mma_kernel(MmaArgs g)
+template <class F, int KIND, int ACT, bool ONE>
+__global__ __launch_bounds__(kThreads, ONE ? 3 : 2) void moe_mma_kernel(MmaArgs g)
 {
     using M = Mma<F>;
     const MoeArgs &a = g.a;
@@ -1124,7 +1124,7 @@ __global__ __launch_bounds__(kThreads, 2) void moe_mma_kernel(MmaArgs g)
     const int tl = w / ks, kp = w % ks;
     const int tile_raw = blockIdx.x * (kWaves / ks) + tl;
     const int tile = tile_raw < g.tiles ? tile_raw : g.tiles - 1;
-    const int s0 = kp * ns / ks, s1 = (kp + 1) * ns / ks;
+    const int s0 = kp * ns / ks, s1 = ONE ? s0 + 1 : (kp + 1) * ns / ks;
     // The first span's rows go out first: they do not depend on the routes.
     const RowBases<KIND> rbs = row_bases<KIND>(a, e);
     SpanW<M> sw;
@@ -1151,9 +1151,9 @@ __global__ __launch_bounds__(kThreads, 2) void moe_mma_kernel(MmaArgs g)
     for (int s = s0; s < s1; ++s) {
         const int nch = C - kSpanChunks * s < kSpanChunks ? C - kSpanChunks * s : kSpanChunks;
         span_stage<F>(sw, stage, lane, nch);
-        if (s + 1 < s1) span_wload<F, KIND>(a, rbs, C, tile, s + 1, lane, sw); // in flight
+        if (!ONE && s + 1 < s1) span_wload<F, KIND>(a, rbs, C, tile, s + 1, lane, sw); // in flight
         __builtin_amdgcn_wave_barrier(); // LDS accesses of one wavefront complete in order
-        const bool more = s + 1 < s1;
+        const bool more = !ONE && s + 1 < s1;
         // The next span's A operands go into each register as soon as its
         // MFMA has issued (lanes outside the positions keep their zeros).
         const int nchn = more ? (C - kSpanChunks * (s + 1) < kSpanChunks ? C - kSpanChunks * (s + 1) : kSpanChunks) : 0;
@@ -1285,7 +1285,10 @@ int launch_mma(emu_ctx *ctx, const MoeArgs &a, const LimbPlanes &in, const LimbP
     const size_t lds = kWaves * kMaxTok * 32 * 4 + kWaves * kMaxTok * 4 + kWaves * 32 * M::STRIDE;
     const int routed = a.n_tok * a.k < a.n_experts ? a.n_tok * a.k : a.n_experts; // grid rows: at most this many experts
     const dim3 grid((g.tiles + tpw - 1) / tpw, routed);
-    hipLaunchKernelGGL((moe_mma_kernel<F, KIND, ACT>), grid, dim3(kThreads), lds, ctx->stream, g);
+    if (g.ks == in.ns)
+        hipLaunchKernelGGL((moe_mma_kernel<F, KIND, ACT, true>), grid, dim3(kThreads), lds, ctx->stream, g);
+    else
+        hipLaunchKernelGGL((moe_mma_kernel<F, KIND, ACT, false>), grid, dim3(kThreads), lds, ctx->stream, g);
     EMU_LAUNCH_CHECK(ctx);
     return EMU_OK;
 }
