@@ -35,6 +35,7 @@
 
 #include <math.h>
 #include <stdlib.h>
+#include <type_traits>
 
 namespace {
 
@@ -534,10 +535,20 @@ template <class F> void launch_down(emu_ctx *ctx, const MoeArgs &a)
 // A workgroup's wavefronts each own a 32-row tile (gate|up: 16 gate rows and
 // the 16 matching up rows, so the activation meets its pair in a lane
 // shuffle) and a share of its spans; the shares meet in LDS in a fixed order.
-// A wavefront stages each span's 32 rows through its own LDS rows with
-// coalesced 16-byte loads while the next span's loads are in flight; a
+// A wavefront stages each span's 32 rows through its own LDS rows, and a
 // chunk's A operand register is refilled with the next span's chunk as soon
-// as its MFMA has issued.
+// as its MFMA has issued.  Three forms of the span loop:
+//   one span per wavefront (the shares equal the spans): the rows come in by
+//         coalesced 16-byte loads into registers and are stored to LDS;
+//         nothing is prefetched, so the kernel holds 104-111 registers and
+//         four workgroups fit a CU;
+//   direct (Q5_K, Q2_K: 4-byte aligned spans): the rows go from memory
+//         straight into LDS (global_load_lds_dword, one instruction per
+//         row), and the next span's rows are requested as soon as the
+//         current span's operand words have been read out of LDS, so the
+//         prefetch holds no registers;
+//   loop (Q6_K and Q8_0 spans start 2-byte aligned): the next span's rows
+//         are in flight in registers while the current span computes.
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kChunkBytes = kEmuChunkBytes; // three int8 limbs of 16 columns
@@ -771,8 +782,9 @@ template <> struct Mma<FmtQ6K> {
     __device__ static int lt(int) { return 208; }
     __device__ static bool live_p(int, int) { return true; }
     __device__ static bool live_t(int, int) { return true; }
-    template <class Refill>
-    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int, int kh, float (&v)[4], const Refill &refill)
+    template <class Refill, class Issue>
+    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int, int kh, float (&v)[4], const Refill &refill,
+                                     const Issue &issue)
     {
         // The span's operand words, read once: ql of (h, q&1, p) and qh of (h, p).
         uint2 ql[8], qh[4];
@@ -783,6 +795,7 @@ template <> struct Mma<FmtQ6K> {
         for (int i = 0; i < 4; ++i) qh[i] = *reinterpret_cast<const uint2 *>(rp + 128 + 32 * (i >> 1) + 16 * (i & 1) + 8 * kh);
         const uint2 s0 = *reinterpret_cast<const uint2 *>(rp + 192), s1 = *reinterpret_cast<const uint2 *>(rp + 200);
         const float d = h2f(*reinterpret_cast<const uint16_t *>(rp + 208));
+        issue();
         int I[12];
 #pragma unroll
         for (int i = 0; i < 12; ++i) I[i] = 0;
@@ -824,8 +837,9 @@ template <> struct Mma<FmtQ5K> {
     __device__ static int lt(int) { return 0; }
     __device__ static bool live_p(int, int) { return true; }
     __device__ static bool live_t(int, int) { return true; }
-    template <class Refill>
-    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int, int kh, float (&v)[4], const Refill &refill)
+    template <class Refill, class Issue>
+    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int, int kh, float (&v)[4], const Refill &refill,
+                                     const Issue &issue)
     {
         FmtQ5K::Raw r;
         const uint2 a = *reinterpret_cast<const uint2 *>(rp), b = *reinterpret_cast<const uint2 *>(rp + 8);
@@ -839,6 +853,7 @@ template <> struct Mma<FmtQ5K> {
         for (int i = 0; i < 8; ++i) qs[i] = *reinterpret_cast<const uint2 *>(rp + 48 + 32 * (i >> 1) + 16 * (i & 1) + 8 * kh);
 #pragma unroll
         for (int i = 0; i < 2; ++i) qh[i] = *reinterpret_cast<const uint2 *>(rp + 16 + 16 * i + 8 * kh);
+        issue();
         auto codes = [&](int m) {
             // chunk m: group g = m/4, nibble half = (m/2)&1, l in 16(m&1) + [0, 16)
             const int g = m >> 2, half = (m >> 1) & 1;
@@ -866,10 +881,11 @@ template <> struct Mma<FmtQ5K> {
         // the mins of chunks 8kh .. 8kh + 7: sub-blocks 4kh .. 4kh + 3, two chunks each
         uint32_t mb[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            uint32_t sc, mn;
-            FmtQ5K::scale_min(r, 4 * kh + k, sc, mn);
-            mb[k] = mn * 0x0101u;
+        for (int k = 0; k < 4; ++k) { // constant indices, then a select: no per-lane index into the scale words
+            uint32_t sc0, mn0, sc1, mn1;
+            FmtQ5K::scale_min(r, k, sc0, mn0);
+            FmtQ5K::scale_min(r, 4 + k, sc1, mn1);
+            mb[k] = (kh ? mn1 : mn0) * 0x0101u;
         }
         double ts[4];
         digit_sums(A.ad, pack8(mb[0] | (mb[1] << 16), mb[2] | (mb[3] << 16)), ts);
@@ -893,8 +909,9 @@ template <> struct Mma<FmtQ2K> {
     __device__ static int lt(int) { return 80; }
     __device__ static bool live_p(int, int) { return true; }
     __device__ static bool live_t(int, int) { return true; }
-    template <class Refill>
-    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int, int kh, float (&v)[4], const Refill &refill)
+    template <class Refill, class Issue>
+    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int, int kh, float (&v)[4], const Refill &refill,
+                                     const Issue &issue)
     {
         const uint2 s0 = *reinterpret_cast<const uint2 *>(rp), s1 = *reinterpret_cast<const uint2 *>(rp + 8);
         const uint32_t dd = *reinterpret_cast<const uint32_t *>(rp + 80);
@@ -902,6 +919,7 @@ template <> struct Mma<FmtQ2K> {
         uint2 qs[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) qs[i] = *reinterpret_cast<const uint2 *>(rp + 16 + 32 * (i >> 1) + 16 * (i & 1) + 8 * kh);
+        issue();
         v16i Dq = {};
 #pragma unroll
         for (int m = 0; m < kSpanChunks; ++m) {
@@ -938,9 +956,9 @@ template <> struct Mma<FmtQ8_0> {
     // nch chunks of the span are present: blocks below nch / 2
     __device__ static bool live_p(int k, int nch) { return (k >> 1) < (nch >> 1); }
     __device__ static bool live_t(int k, int nch) { return k < (nch >> 1); }
-    template <class Refill>
+    template <class Refill, class Issue>
     __device__ static void span_dots(const uint8_t *rp, SpanA &A, int nch, int kh, float (&v)[4],
-                                     const Refill &refill)
+                                     const Refill &refill, const Issue &issue)
     {
         const uint2 d0 = *reinterpret_cast<const uint2 *>(rp + 256), d1 = *reinterpret_cast<const uint2 *>(rp + 264);
         float acc[12];
@@ -949,6 +967,7 @@ template <> struct Mma<FmtQ8_0> {
         long cw[kSpanChunks]; // the span's codes, read once
 #pragma unroll
         for (int m = 0; m < kSpanChunks; ++m) cw[m] = *reinterpret_cast<const long *>(rp + 16 * m + 8 * kh);
+        issue();
 #pragma unroll
         for (int b = 0; b < kSpanChunks / 2; ++b) {
             v16i D = {};
@@ -1095,6 +1114,55 @@ __device__ __forceinline__ void span_stage(const SpanW<Mma<F>> &sw, uint8_t *sta
     }
 }
 
+// One span of the tile's 32 rows straight into this wavefront's LDS rows:
+// one instruction per row, lane l bringing the row's dword l (the rows are
+// the layout span_stage writes; the rows tile_row names).  The row
+// addresses are formed per call in scalar registers from wave-uniform bases
+// (gate|up: the tile's first gate and up rows; down: its first row) behind
+// an empty asm statement: left free, the compiler hoists all 32 out of the
+// span loop into 64 vector registers.
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) const void gvoid;
+template <class F, int KIND>
+__device__ __forceinline__ void span_dma(const MoeArgs &a, const RowBases<KIND> &rbs, int tile, int span, int lane,
+                                         uint8_t *stage)
+{
+    using M = Mma<F>;
+    static_assert(M::SPAN % 4 == 0 && M::STRIDE % 4 == 0 && M::SPAN <= 4 * EMU_WAVE, "dword rows");
+    constexpr int W = M::SPAN / 4;
+    const uint64_t so = (uint64_t)span * M::SPAN;
+    uint64_t b0, b1, rb = rbs.rb;
+    int last = 31; // down: the last row inside the matrix, relative to the tile (rows past it read it again)
+    if (KIND == kMmaUp) {
+        b0 = (uint64_t)(rbs.lo + (size_t)(uint32_t)(16 * tile) * rbs.rb) + so;
+        b1 = (uint64_t)(rbs.hi + (size_t)(uint32_t)(16 * tile) * rbs.rb) + so;
+    } else {
+        b0 = (uint64_t)(rbs.lo + (size_t)(uint32_t)(32 * tile) * rbs.rb) + so;
+        b1 = b0;
+        last = a.width - 1 - 32 * tile; // tile < ceil(width / 32): last >= 0
+    }
+    auto sgpr = [](uint64_t v) {
+        return (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v) |
+               ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32)) << 32);
+    };
+    b0 = sgpr(b0);
+    b1 = sgpr(b1);
+    rb = sgpr(rb);
+    last = __builtin_amdgcn_readfirstlane(last);
+    asm volatile("" : "+s"(b0), "+s"(b1), "+s"(rb), "+s"(last));
+#pragma unroll
+    for (int rr = 0; rr < 32; ++rr) {
+        // gate|up: gate row rr or up row rr - 16; down: row min(rr, last) (0 <= last)
+        const int r = KIND == kMmaUp ? (rr & 15) : (rr < last ? rr : last);
+        const uint64_t row = (KIND == kMmaUp && rr >= 16 ? b1 : b0) + (uint64_t)(uint32_t)r * rb;
+        if (lane < W)
+            __builtin_amdgcn_global_load_lds((gvoid *)(row + 4 * (uint32_t)lane), (lds_void *)(stage + rr * M::STRIDE),
+                                             4, 0, 0);
+    }
+}
+
+enum { kFormLoop = 0, kFormOne = 1, kFormDirect = 2 };
+
 // The routed position p's vector: the token (gate|up) or the route (down).
 template <int KIND> __device__ __forceinline__ int position_vec(const MoeArgs &a, const int (&slot)[kMaxTok], int p)
 {
@@ -1104,15 +1172,17 @@ template <int KIND> __device__ __forceinline__ int position_vec(const MoeArgs &a
     return KIND == kMmaUp ? v / a.k : v;
 }
 
-template <class F, int KIND, int ACT, bool ONE>
-__global__ __launch_bounds__(kThreads, ONE ? 3 : 2) void moe_mma_kernel(MmaArgs g)
+template <class F, int KIND, int ACT, int FORM>
+__global__ __launch_bounds__(kThreads, FORM == kFormLoop ? 2 : 3) void moe_mma_kernel(MmaArgs g)
 {
     using M = Mma<F>;
     const MoeArgs &a = g.a;
     extern __shared__ __align__(16) uint8_t smem[];
     const int C = g.in.C, ns = g.in.ns, ks = g.ks;
     float *red = reinterpret_cast<float *>(smem); // [kWaves][8][32]
-    const int tid = threadIdx.x, lane = tid & (EMU_WAVE - 1), w = tid / EMU_WAVE;
+    const int tid = threadIdx.x, lane = tid & (EMU_WAVE - 1);
+    // wave-uniform (the direct form's row addresses are scalar)
+    const int w = FORM == kFormDirect ? __builtin_amdgcn_readfirstlane(tid / EMU_WAVE) : tid / EMU_WAVE;
     float *wsc = red + kWaves * kMaxTok * 32 + w * kMaxTok; // this wavefront's positions' span scales
     uint8_t *stage = reinterpret_cast<uint8_t *>(red + kWaves * kMaxTok * 32 + kWaves * kMaxTok) + w * 32 * M::STRIDE;
     // Grid: x = tile group, fastest, so that consecutive workgroups -- which
@@ -1124,11 +1194,14 @@ __global__ __launch_bounds__(kThreads, ONE ? 3 : 2) void moe_mma_kernel(MmaArgs 
     const int tl = w / ks, kp = w % ks;
     const int tile_raw = blockIdx.x * (kWaves / ks) + tl;
     const int tile = tile_raw < g.tiles ? tile_raw : g.tiles - 1;
-    const int s0 = kp * ns / ks, s1 = ONE ? s0 + 1 : (kp + 1) * ns / ks;
+    const int s0 = kp * ns / ks, s1 = FORM == kFormOne ? s0 + 1 : (kp + 1) * ns / ks;
     // The first span's rows go out first: they do not depend on the routes.
     const RowBases<KIND> rbs = row_bases<KIND>(a, e);
     SpanW<M> sw;
-    if (s0 < s1) span_wload<F, KIND>(a, rbs, C, tile, s0, lane, sw);
+    if (s0 < s1) {
+        if constexpr (FORM == kFormDirect) span_dma<F, KIND>(a, rbs, tile, s0, lane, stage);
+        else span_wload<F, KIND>(a, rbs, C, tile, s0, lane, sw);
+    }
     const int j = lane & 31, kh = lane >> 5;
     ASource src;
     src.live = j < 24 && (j & 7) < cnt;
@@ -1150,10 +1223,14 @@ __global__ __launch_bounds__(kThreads, ONE ? 3 : 2) void moe_mma_kernel(MmaArgs 
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int s = s0; s < s1; ++s) {
         const int nch = C - kSpanChunks * s < kSpanChunks ? C - kSpanChunks * s : kSpanChunks;
-        span_stage<F>(sw, stage, lane, nch);
-        if (!ONE && s + 1 < s1) span_wload<F, KIND>(a, rbs, C, tile, s + 1, lane, sw); // in flight
+        if constexpr (FORM == kFormDirect) {
+            __builtin_amdgcn_s_waitcnt(0); // the span's rows are in LDS, its A operands in registers
+        } else {
+            span_stage<F>(sw, stage, lane, nch);
+            if (FORM == kFormLoop && s + 1 < s1) span_wload<F, KIND>(a, rbs, C, tile, s + 1, lane, sw); // in flight
+        }
         __builtin_amdgcn_wave_barrier(); // LDS accesses of one wavefront complete in order
-        const bool more = !ONE && s + 1 < s1;
+        const bool more = FORM != kFormOne && s + 1 < s1;
         // The next span's A operands go into each register as soon as its
         // MFMA has issued (lanes outside the positions keep their zeros).
         const int nchn = more ? (C - kSpanChunks * (s + 1) < kSpanChunks ? C - kSpanChunks * (s + 1) : kSpanChunks) : 0;
@@ -1170,8 +1247,18 @@ __global__ __launch_bounds__(kThreads, ONE ? 3 : 2) void moe_mma_kernel(MmaArgs 
         };
         if (lane < kMaxTok) wsc[lane] = A.sc; // positions past the count: 0
         if (more) A.sc = src.scale(s + 1);
+        // Direct form: once the span's operand words are in registers (the
+        // LDS reads complete: lgkmcnt 0), the next span's rows replace them.
+        auto issue = [&]() {
+            if constexpr (FORM == kFormDirect) {
+                if (more) {
+                    __builtin_amdgcn_s_waitcnt(0xc07f);
+                    span_dma<F, KIND>(a, rbs, tile, s + 1, lane, stage);
+                }
+            }
+        };
         float v[4];
-        M::span_dots(stage + j * M::STRIDE, A, nch, kh, v, refill);
+        M::span_dots(stage + j * M::STRIDE, A, nch, kh, v, refill, issue);
         const float4 s4 = *reinterpret_cast<const float4 *>(wsc + 4 * kh);
         acc[0] = __builtin_fmaf(v[0], s4.x, acc[0]);
         acc[1] = __builtin_fmaf(v[1], s4.y, acc[1]);
@@ -1254,17 +1341,20 @@ __global__ __launch_bounds__(kThreads, ONE ? 3 : 2) void moe_mma_kernel(MmaArgs 
         if (p < cnt) emu_span_limbs_wave(xv[p], live, position_vec<kMmaDown>(a, slot, p), span, g.out); // uniform
 }
 
-// Wavefronts per tile: enough shares of the spans for about `budget`
-// wavefronts over the experts eight tokens can route to -- 8192 for gate|up,
-// 2048 for down, as measured in the decode steps (with every layer's experts
-// coming from HBM, gate|up gains from more rows in flight: OLMoE 4,318 ->
-// 4,511 tok/s, Granite 2,591 -> 2,619; the downs lose with more shares).  It
-// depends on the layer's shape only, not on the token count, so that a
-// token's sums are added in the same order whichever tokens share the call.
+// Wavefronts per tile.  A matrix of 1, 2 or 4 spans gets a share per span
+// (the one-span form, whose wavefronts hold no prefetch: four workgroups a
+// CU).  Otherwise enough shares for about `budget` wavefronts
+// over the experts eight tokens can route to -- 16384 for gate|up, 2048 for
+// down -- as measured in the decode steps (with every layer's experts coming
+// from HBM, gate|up gains from more rows in flight; the downs lose with more
+// shares).  The shares depend on the layer's shape only, not on the token
+// count, so that a token's sums are added in the same order whichever tokens
+// share the call.
 int mma_shares(const MoeArgs &a, int tiles, int spans, int budget)
 {
-    const int active = kMaxTok * a.k < a.n_experts ? kMaxTok * a.k : a.n_experts;
+    if (spans <= kWaves && (spans & (spans - 1)) == 0) return spans;
     int ks = 1;
+    const int active = kMaxTok * a.k < a.n_experts ? kMaxTok * a.k : a.n_experts;
     while (ks < kWaves && 2 * ks <= spans && active * tiles * ks < budget) ks *= 2;
     return ks;
 }
@@ -1280,15 +1370,22 @@ int launch_mma(emu_ctx *ctx, const MoeArgs &a, const LimbPlanes &in, const LimbP
     g.out = out;
     g.counters = KIND == kMmaUp ? counters : nullptr;
     g.tiles = KIND == kMmaUp ? a.ff / 16 : (a.width + 31) / 32;
-    g.ks = mma_shares(a, g.tiles, in.ns, KIND == kMmaUp ? 8192 : 2048);
+    g.ks = mma_shares(a, g.tiles, in.ns, KIND == kMmaUp ? 16384 : 2048);
     const int tpw = kWaves / g.ks;
     const size_t lds = kWaves * kMaxTok * 32 * 4 + kWaves * kMaxTok * 4 + kWaves * 32 * M::STRIDE;
     const int routed = a.n_tok * a.k < a.n_experts ? a.n_tok * a.k : a.n_experts; // grid rows: at most this many experts
     const dim3 grid((g.tiles + tpw - 1) / tpw, routed);
+    // The direct form for 4-byte aligned spans of device-resident rows (an
+    // expert table may point some experts at pinned host memory; those
+    // launches keep the register form).
+    constexpr bool direct = std::is_same<F, FmtQ5K>::value || std::is_same<F, FmtQ2K>::value;
     if (g.ks == in.ns)
-        hipLaunchKernelGGL((moe_mma_kernel<F, KIND, ACT, true>), grid, dim3(kThreads), lds, ctx->stream, g);
+        hipLaunchKernelGGL((moe_mma_kernel<F, KIND, ACT, kFormOne>), grid, dim3(kThreads), lds, ctx->stream, g);
+    else if (direct && !a.table)
+        hipLaunchKernelGGL((moe_mma_kernel<F, KIND, ACT, direct ? kFormDirect : kFormLoop>), grid, dim3(kThreads),
+                           lds, ctx->stream, g);
     else
-        hipLaunchKernelGGL((moe_mma_kernel<F, KIND, ACT, false>), grid, dim3(kThreads), lds, ctx->stream, g);
+        hipLaunchKernelGGL((moe_mma_kernel<F, KIND, ACT, kFormLoop>), grid, dim3(kThreads), lds, ctx->stream, g);
     EMU_LAUNCH_CHECK(ctx);
     return EMU_OK;
 }
