@@ -831,6 +831,7 @@ template <> struct Mma<FmtQ6K> {
 template <> struct Mma<FmtQ5K> {
     static constexpr int SPAN = 176, STRIDE = 184, NP = 11, NT = 0, TB = 2;
     static constexpr bool DIGITS = true;
+    __device__ static int bytes(int) { return SPAN; }
     __device__ static int gp(int k) { return 16 * k; }
     __device__ static int lp(int k) { return 16 * k; }
     __device__ static int gt(int) { return 0; }
@@ -903,6 +904,7 @@ template <> struct Mma<FmtQ5K> {
 template <> struct Mma<FmtQ2K> {
     static constexpr int SPAN = 84, STRIDE = 88, NP = 5, NT = 1, TB = 4;
     static constexpr bool DIGITS = true;
+    __device__ static int bytes(int) { return SPAN; }
     __device__ static int gp(int k) { return 16 * k; }
     __device__ static int lp(int k) { return 16 * k; }
     __device__ static int gt(int) { return 80; }
@@ -978,6 +980,64 @@ template <> struct Mma<FmtQ8_0> {
             if (2 * b < nch) { // uniform
                 const uint2 dv = b < 4 ? d0 : d1;
                 const float db = h2f((uint16_t)(((b & 3) < 2 ? dv.x : dv.y) >> (16 * (b & 1))));
+#pragma unroll
+                for (int i = 0; i < 12; ++i) acc[i] = __builtin_fmaf((float)D[i], db, acc[i]);
+            }
+        }
+        refill(kSpanChunks);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = __builtin_fmaf(acc[q], 16384.0f, __builtin_fmaf(acc[q + 4], 128.0f, acc[q + 8]));
+    }
+};
+
+// Q8_0 rows as stored (the direct form's LDS rows): block b at 34b, its d
+// then its 32 codes.  The codes of even blocks start 2 bytes past a dword
+// boundary: their 8-byte operands are assembled from three dword reads by
+// v_alignbyte; odd blocks' start on one.  The same products, in the same
+// order, as Mma<FmtQ8_0>.
+struct MmaQ8Raw {
+    static constexpr int SPAN = 272, STRIDE = 280;
+    static constexpr bool DIGITS = false;
+    __device__ static int bytes(int nch) { return 17 * nch; } // nch / 2 blocks of 34 bytes
+    template <class Refill, class Issue>
+    __device__ static void span_dots(const uint8_t *rp, SpanA &A, int nch, int kh, float (&v)[4],
+                                     const Refill &refill, const Issue &issue)
+    {
+        auto rd = [&](int off) { return *reinterpret_cast<const uint32_t *>(rp + off); }; // off % 4 == 0
+        long cw[kSpanChunks];
+        uint32_t dd[kSpanChunks / 2];
+#pragma unroll
+        for (int b = 0; b < kSpanChunks / 2; ++b) {
+            const int base = 34 * b;
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const int o = base + 16 * p + 8 * kh; // the operand's bytes start at o + 2
+                uint32_t lo, hi;
+                if (b % 2 == 0) {
+                    const uint32_t x0 = rd(o), x1 = rd(o + 4), x2 = rd(o + 8);
+                    lo = __builtin_amdgcn_alignbyte(x1, x0, 2);
+                    hi = __builtin_amdgcn_alignbyte(x2, x1, 2);
+                } else {
+                    lo = rd(o + 2);
+                    hi = rd(o + 6);
+                }
+                cw[2 * b + p] = (long)(((uint64_t)hi << 32) | lo);
+            }
+            dd[b] = b % 2 == 0 ? rd(base) & 0xffffu : rd(base - 2) >> 16;
+        }
+        issue();
+        float acc[12];
+#pragma unroll
+        for (int i = 0; i < 12; ++i) acc[i] = 0.0f;
+#pragma unroll
+        for (int b = 0; b < kSpanChunks / 2; ++b) {
+            v16i D = {};
+            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.av[2 * b], cw[2 * b], D, 0, 0, 0);
+            D = __builtin_amdgcn_mfma_i32_32x32x16_i8(A.av[2 * b + 1], cw[2 * b + 1], D, 0, 0, 0);
+            refill(2 * b);
+            refill(2 * b + 1);
+            if (2 * b < nch) { // uniform
+                const float db = h2f((uint16_t)dd[b]);
 #pragma unroll
                 for (int i = 0; i < 12; ++i) acc[i] = __builtin_fmaf((float)D[i], db, acc[i]);
             }
@@ -1123,13 +1183,12 @@ __device__ __forceinline__ void span_stage(const SpanW<Mma<F>> &sw, uint8_t *sta
 // span loop into 64 vector registers.
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) const void gvoid;
-template <class F, int KIND>
-__device__ __forceinline__ void span_dma(const MoeArgs &a, const RowBases<KIND> &rbs, int tile, int span, int lane,
-                                         uint8_t *stage)
+template <class M, int KIND>
+__device__ __forceinline__ void span_dma(const MoeArgs &a, const RowBases<KIND> &rbs, int tile, int span, int nbytes,
+                                         int lane, uint8_t *stage)
 {
-    using M = Mma<F>;
-    static_assert(M::SPAN % 4 == 0 && M::STRIDE % 4 == 0 && M::SPAN <= 4 * EMU_WAVE, "dword rows");
-    constexpr int W = M::SPAN / 4;
+    static_assert(M::SPAN % 4 == 0 && M::STRIDE % 4 == 0 && M::SPAN <= 8 * EMU_WAVE, "dword rows");
+    const int W = nbytes / 4; // the span's bytes in the row (a multiple of 4)
     const uint64_t so = (uint64_t)span * M::SPAN;
     uint64_t b0, b1, rb = rbs.rb;
     int last = 31; // down: the last row inside the matrix, relative to the tile (rows past it read it again)
@@ -1158,10 +1217,21 @@ __device__ __forceinline__ void span_dma(const MoeArgs &a, const RowBases<KIND> 
         if (lane < W)
             __builtin_amdgcn_global_load_lds((gvoid *)(row + 4 * (uint32_t)lane), (lds_void *)(stage + rr * M::STRIDE),
                                              4, 0, 0);
+        if (M::SPAN > 4 * EMU_WAVE && lane + EMU_WAVE < W) // rows of more than 64 dwords: the rest
+            __builtin_amdgcn_global_load_lds((gvoid *)(row + 4 * (uint32_t)(lane + EMU_WAVE)),
+                                             (lds_void *)(stage + rr * M::STRIDE + 4 * EMU_WAVE), 4, 0, 0);
     }
 }
 
+// The span arithmetic of each form: the direct form reads Q8_0 rows as stored.
 enum { kFormLoop = 0, kFormOne = 1, kFormDirect = 2 };
+template <class F, int FORM> struct MmaSel {
+    using type = Mma<F>;
+};
+template <> struct MmaSel<FmtQ8_0, kFormDirect> {
+    using type = MmaQ8Raw;
+};
+
 
 // The routed position p's vector: the token (gate|up) or the route (down).
 template <int KIND> __device__ __forceinline__ int position_vec(const MoeArgs &a, const int (&slot)[kMaxTok], int p)
@@ -1175,7 +1245,7 @@ template <int KIND> __device__ __forceinline__ int position_vec(const MoeArgs &a
 template <class F, int KIND, int ACT, int FORM>
 __global__ __launch_bounds__(kThreads, FORM == kFormLoop ? 2 : 3) void moe_mma_kernel(MmaArgs g)
 {
-    using M = Mma<F>;
+    using M = typename MmaSel<F, FORM>::type;
     const MoeArgs &a = g.a;
     extern __shared__ __align__(16) uint8_t smem[];
     const int C = g.in.C, ns = g.in.ns, ks = g.ks;
@@ -1197,9 +1267,10 @@ __global__ __launch_bounds__(kThreads, FORM == kFormLoop ? 2 : 3) void moe_mma_k
     const int s0 = kp * ns / ks, s1 = FORM == kFormOne ? s0 + 1 : (kp + 1) * ns / ks;
     // The first span's rows go out first: they do not depend on the routes.
     const RowBases<KIND> rbs = row_bases<KIND>(a, e);
-    SpanW<M> sw;
+    SpanW<Mma<F>> sw; // the register forms' rows in flight
     if (s0 < s1) {
-        if constexpr (FORM == kFormDirect) span_dma<F, KIND>(a, rbs, tile, s0, lane, stage);
+        if constexpr (FORM == kFormDirect)
+            span_dma<M, KIND>(a, rbs, tile, s0, M::bytes(C - kSpanChunks * s0 < kSpanChunks ? C - kSpanChunks * s0 : kSpanChunks), lane, stage);
         else span_wload<F, KIND>(a, rbs, C, tile, s0, lane, sw);
     }
     const int j = lane & 31, kh = lane >> 5;
@@ -1253,7 +1324,7 @@ __global__ __launch_bounds__(kThreads, FORM == kFormLoop ? 2 : 3) void moe_mma_k
             if constexpr (FORM == kFormDirect) {
                 if (more) {
                     __builtin_amdgcn_s_waitcnt(0xc07f);
-                    span_dma<F, KIND>(a, rbs, tile, s + 1, lane, stage);
+                    span_dma<M, KIND>(a, rbs, tile, s + 1, M::bytes(nchn), lane, stage);
                 }
             }
         };
@@ -1375,13 +1446,20 @@ int launch_mma(emu_ctx *ctx, const MoeArgs &a, const LimbPlanes &in, const LimbP
     const size_t lds = kWaves * kMaxTok * 32 * 4 + kWaves * kMaxTok * 4 + kWaves * 32 * M::STRIDE;
     const int routed = a.n_tok * a.k < a.n_experts ? a.n_tok * a.k : a.n_experts; // grid rows: at most this many experts
     const dim3 grid((g.tiles + tpw - 1) / tpw, routed);
-    // The direct form for 4-byte aligned spans of device-resident rows (an
-    // expert table may point some experts at pinned host memory; those
-    // launches keep the register form).
-    constexpr bool direct = std::is_same<F, FmtQ5K>::value || std::is_same<F, FmtQ2K>::value;
+    // The direct form for device-resident rows whose spans start and end on
+    // 4-byte boundaries (an expert table may point some experts at pinned
+    // host memory; those launches keep the register form).  Q5_K and Q2_K
+    // spans are 176 and 84 bytes; Q8_0 spans are 272 bytes, the last one
+    // (C % 16) / 2 blocks of 34 bytes.
+    constexpr bool direct = std::is_same<F, FmtQ5K>::value || std::is_same<F, FmtQ2K>::value ||
+                            std::is_same<F, FmtQ8_0>::value;
+    const size_t rb = KIND == kMmaUp ? a.rb_in : a.rb_ff;
+    const uintptr_t p0 = (uintptr_t)(KIND == kMmaUp ? a.gate : a.down), p1 = (uintptr_t)(KIND == kMmaUp ? a.up : a.down);
+    const bool aligned = rb % 4 == 0 && p0 % 4 == 0 && p1 % 4 == 0 &&
+                         (!std::is_same<F, FmtQ8_0>::value || (in.C % kSpanChunks) % 4 == 0);
     if (g.ks == in.ns)
         hipLaunchKernelGGL((moe_mma_kernel<F, KIND, ACT, kFormOne>), grid, dim3(kThreads), lds, ctx->stream, g);
-    else if (direct && !a.table)
+    else if (direct && !a.table && aligned)
         hipLaunchKernelGGL((moe_mma_kernel<F, KIND, ACT, direct ? kFormDirect : kFormLoop>), grid, dim3(kThreads),
                            lds, ctx->stream, g);
     else
