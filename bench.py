@@ -481,7 +481,7 @@ def moe_layer_leg(ctx, name: str, reps: int) -> dict:
 
 # Matrix-pipe busy fraction of the expert kernels, from the committed counter
 # summary (SQ_VALU_MFMA_BUSY_CYCLES over SQ_BUSY_CYCLES per SIMD).
-MFMA_BUSY = {"granite": (0.043, 0.035), "olmoe": (0.157, 0.130), "gemma": (0.109, 0.072)}
+MFMA_BUSY = {"granite": (0.056, 0.037), "olmoe": (0.169, 0.149), "gemma": (0.133, 0.086)}
 MFMA_SOURCE = "profiles/moe_experts_layer_counters.txt"
 
 
