@@ -74,6 +74,15 @@ SHAPES = [
     ("one-token-olmoe", _lib.Q2_K, _lib.Q2_K, 64, 2048, 1024, 8, 1, False, _lib.EMU_ACT_SILU, 1.0),
     # a partial last span of Q8_0 down input (ff = 704: 2.75 spans) and 128 experts
     ("gemma-b1", _lib.Q5_K, _lib.Q8_0, 128, 2816, 704, 8, 1, True, _lib.EMU_ACT_GELU_TANH, 1.2),
+    # the span loop's forms: Q6_K rows of 5 and 3 spans (the register loop:
+    # 210-byte spans start 2-byte aligned); Q2_K and Q5_K down rows of 6 and
+    # 5 spans (rows staged straight into LDS); Q8_0 down rows whose last span
+    # holds an odd number of 34-byte blocks (ff = 736: 23 blocks, so rows
+    # and that span end 2 bytes past a dword: the register loop again)
+    ("q6k-loop", _lib.Q6_K, _lib.Q6_K, 16, 1280, 768, 4, 5, False, _lib.EMU_ACT_SILU, 1.0),
+    ("q2k-direct-down", _lib.Q2_K, _lib.Q2_K, 24, 2048, 1536, 4, 6, False, _lib.EMU_ACT_SILU, 1.0),
+    ("q5k-direct-down", _lib.Q5_K, _lib.Q5_K, 12, 1024, 1280, 4, 4, True, _lib.EMU_ACT_GELU_TANH, 1.0),
+    ("q8-unaligned-down", _lib.Q5_K, _lib.Q8_0, 12, 1024, 736, 4, 4, True, _lib.EMU_ACT_SILU, 1.0),
 ]
 
 
