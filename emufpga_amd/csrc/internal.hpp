@@ -771,6 +771,7 @@ struct QmvArgs {
     float softcap;         // results -> softcap * tanh(v / softcap) after out_div (0: none)
     int f32_act;           // f32 activations: the dequant + f32 FMA kernels, not the int8-limb ones
     int span_scales;       // multi-token chain: the A operands carry one scale per 256-column span
+    int span_norm;         // with span_scales: apply the deferring link's RMS factor (with eps)
 };
 
 // A matvec result's epilogue: divided by out_div (when set), then added to
@@ -879,7 +880,15 @@ struct EmuMfmaLink {
     // the span's largest |x|, as the expert kernels' limb planes.  Only for a
     // matvec launched with QmvArgs::span_scales.
     int span;
+    // With gain and span: the row's RMS factor is left to the consuming
+    // matvec (QmvArgs::span_norm), so no workgroup needs the whole row and
+    // the link runs as many small ones.  The limbs are of x * gain.
+    int defer_norm;
 };
+// Rows from this width on defer the norm: narrower ones (Granite's 1024)
+// already spread over a token's workgroup, and the consuming matvec's factor
+// costs more than the link saves (0.4% of the step).
+constexpr int kEmuDeferNormCols = 2048;
 size_t emu_mfma_chain_bytes(int cols_cap, size_t max_part_bytes);
 size_t emu_mfma_part_bytes(int rows, int cols, int nmat);
 int emu_mfma_link(emu_ctx *ctx, const EmuMfmaLink &l);

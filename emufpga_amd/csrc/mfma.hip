@@ -88,6 +88,10 @@ struct LinkArgs {
     float d_scale;
     int act; // kLinkSwiglu: EMU_ACT_SILU or EMU_ACT_GELU_TANH
     int span; // one limb scale per 256-column span (xs: [span][8]) instead of per sub-block
+    // With gain, optional: the RMS factor is left to the consuming matvec.
+    // The limbs are of x * gain; each (one-wavefront) workgroup writes the
+    // sum of squares of its columns to ssp[token * kSsGroups + blockIdx.y].
+    float *ssp;
 };
 
 // A-operand layout: sub-block sb, half kh (columns 8kh..8kh+7 of the
@@ -120,9 +124,14 @@ template <int MAXS> __device__ __forceinline__ void slice_add(const float (&q)[M
 
 constexpr int kLinkThreads = 512;
 constexpr int kLinkPairs = 3; // columns per token up to 8 * kLinkThreads * kLinkPairs = 12288
+// Without a norm nothing spans the row, so the link runs as many small
+// workgroups (one 8-column piece per thread): the partial sums it reads are
+// spread over the CUs instead of queueing at a few.
+constexpr int kLinkSmall = 64;
+constexpr int kSsGroups = kLinkThreads * kLinkPairs / kLinkSmall; // small workgroups per token, at most
 
-template <int MAXS, int MODE>
-__global__ __launch_bounds__(kLinkThreads) void mfma_link_kernel(LinkArgs a)
+template <int MAXS, int MODE, int TH>
+__global__ __launch_bounds__(TH) void mfma_link_kernel(LinkArgs a)
 {
     const int t = blockIdx.x, tid = threadIdx.x;
     const int npairs = a.cols / 8;
@@ -132,13 +141,13 @@ __global__ __launch_bounds__(kLinkThreads) void mfma_link_kernel(LinkArgs a)
     if (a.gain && a.xa) {
 #pragma unroll
         for (int k = 0; k < kLinkPairs; ++k) {
-            const int p = (blockIdx.y + k * gridDim.y) * kLinkThreads + tid;
+            const int p = (blockIdx.y + k * gridDim.y) * TH + tid;
             if (p < npairs) ld8f(a.gain + 8 * p, gn[k]);
         }
     }
 #pragma unroll
     for (int k = 0; k < kLinkPairs; ++k) {
-        const int p = (blockIdx.y + k * gridDim.y) * kLinkThreads + tid;
+        const int p = (blockIdx.y + k * gridDim.y) * TH + tid;
         if (p >= npairs) break;
         const int c0 = 8 * p;
         if constexpr (MODE == kLinkInput) {
@@ -231,19 +240,22 @@ __global__ __launch_bounds__(kLinkThreads) void mfma_link_kernel(LinkArgs a)
     }
     if (!a.xa) return; // uniform
     float scale = 1.0f;
-    if (a.gain) {
-        __shared__ float red[kLinkThreads / EMU_WAVE];
+    if (a.gain && a.ssp) { // the factor comes later: this workgroup's share of the sum of squares
+        ss = wave_sum(ss);
+        if (tid == 0) a.ssp[t * kSsGroups + blockIdx.y] = ss;
+    } else if (a.gain) {
+        __shared__ float red[TH / EMU_WAVE];
         ss = wave_sum(ss);
         if ((tid & (EMU_WAVE - 1)) == 0) red[tid / EMU_WAVE] = ss;
         __syncthreads();
         float tot = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kLinkThreads / EMU_WAVE; ++k) tot += red[k];
+        for (int k = 0; k < TH / EMU_WAVE; ++k) tot += red[k];
         scale = 1.0f / sqrtf(tot / (float)a.cols + a.eps);
     }
 #pragma unroll
     for (int k = 0; k < kLinkPairs; ++k) {
-        const int p = (blockIdx.y + k * gridDim.y) * kLinkThreads + tid;
+        const int p = (blockIdx.y + k * gridDim.y) * TH + tid;
         if (p >= npairs) break; // pairs (2m, 2m+1) stop together: npairs is even
         const int sb = p >> 1, kh = p & 1;
         float w[8];
@@ -305,6 +317,11 @@ struct MfmaArgs {
     const uint8_t *xa;
     const float *xs;
     float *part; // [slices][nmat][kMaxTok][rows], slices = ceil(cols / kSlice)
+    // Span form, optional: each token's RMS factor 1 / sqrt(sum / cols + eps)
+    // from the link's ss_groups sums of squares (LinkArgs::ssp).
+    const float *ssp;
+    int ss_groups;
+    float eps;
 };
 
 // Q6_K codes (0..63) of 8 columns, two dwords: sub-block (h, q, p) takes
@@ -382,6 +399,7 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
 
     Unit b;
     float4 xsv;
+    float sq[3];
     __shared__ __align__(16) uint8_t wl[kWaves][kTileRows * kRowStride];
     {
         const int u = blockIdx.x;
@@ -471,6 +489,17 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
         }
         if (!has) b.d = 0; // d = 0: the block's (finite, integer) sums add exact zeros
     }
+    // The deferred norm's sums of squares load behind the weights (nothing
+    // needs them before the float step): lane 8 t + i, token t's sums i,
+    // i + 8, i + 16.
+    if constexpr (SPAN) {
+        if (a.ssp) {
+            const int tt = lane >> 3, g = lane & 7;
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+                sq[k] = tt < a.n_tok && g + 8 * k < a.ss_groups ? a.ssp[tt * kSsGroups + g + 8 * k] : 0.0f;
+        }
+    }
     if constexpr (!SPAN) { // the slice's scales, shared by the workgroup
         if (tid < kSlice / 16 * kMaxTok / 4) reinterpret_cast<float4 *>(xs)[tid] = xsv;
         __syncthreads();
@@ -545,11 +574,22 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
         if (sb + 1 < 16) cur = next;
     }
     if constexpr (SPAN) {
+        if (a.ssp) { // the sums in a fixed order (the same in every workgroup), then the factor
+            float tot = (sq[0] + sq[1]) + sq[2];
+            tot += __shfl_xor(tot, 1, EMU_WAVE);
+            tot += __shfl_xor(tot, 2, EMU_WAVE);
+            tot += __shfl_xor(tot, 4, EMU_WAVE);
+            const float rs = 1.0f / sqrtf(tot / (float)a.cols + a.eps);
+            xsv.x *= __shfl(rs, 8 * (4 * kh), EMU_WAVE); // a power of two times rs: exact
+            xsv.y *= __shfl(rs, 8 * (4 * kh + 1), EMU_WAVE);
+            xsv.z *= __shfl(rs, 8 * (4 * kh + 2), EMU_WAVE);
+            xsv.w *= __shfl(rs, 8 * (4 * kh + 3), EMU_WAVE);
+        }
         const float s[4] = {xsv.x, xsv.y, xsv.z, xsv.w};
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const double t = (double)acci[0][r] * 16384.0 + (double)acci[1][r] * 128.0 + (double)acci[2][r]; // exact
-            acc[r] = (float)(t * (double)(d * s[r]));
+            acc[r] = (float)(t * ((double)d * (double)s[r]));
         }
     }
 
@@ -631,13 +671,14 @@ __global__ __launch_bounds__(kFinishThreads) void mfma_finish_kernel(FinishArgs 
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// Workspace: A operands and scales for up to cols_cap columns, then the
-// partial sums.
+// Workspace: A operands and scales for up to cols_cap columns, the
+// partial sums, and at its end the deferred norms' sums of squares.
 struct Ws {
     uint8_t *xa;
-    float *xs, *part;
+    float *xs, *part, *ss;
     size_t part_bytes;
 };
+constexpr size_t kSsBytes = (size_t)kMaxTok * kSsGroups * sizeof(float);
 size_t operand_bytes(int cols_cap)
 {
     const size_t nsb = (size_t)cols_cap / 16;
@@ -647,11 +688,13 @@ Ws workspace(emu_ctx *ctx, int cols_cap)
 {
     const size_t nsb = (size_t)cols_cap / 16;
     uint8_t *base = static_cast<uint8_t *>(ctx->mfma_ws);
+    const size_t fixed = operand_bytes(cols_cap) + align256(kSsBytes);
     Ws w;
     w.xa = base;
     w.xs = reinterpret_cast<float *>(base + align256(nsb * kSbBytes));
     w.part = reinterpret_cast<float *>(base + operand_bytes(cols_cap));
-    w.part_bytes = ctx->mfma_ws_bytes > operand_bytes(cols_cap) ? ctx->mfma_ws_bytes - operand_bytes(cols_cap) : 0;
+    w.part_bytes = ctx->mfma_ws_bytes > fixed ? ctx->mfma_ws_bytes - fixed : 0;
+    w.ss = reinterpret_cast<float *>(base + operand_bytes(cols_cap) + w.part_bytes);
     return w;
 }
 size_t part_bytes(int rows, int cols, int nmat)
@@ -663,12 +706,12 @@ size_t part_bytes(int rows, int cols, int nmat)
 
 size_t emu_mfma_workspace_bytes(int rows, int cols, int nmat)
 {
-    return operand_bytes(cols) + align256(part_bytes(rows, cols, nmat));
+    return operand_bytes(cols) + align256(part_bytes(rows, cols, nmat)) + align256(kSsBytes);
 }
 
 size_t emu_mfma_chain_bytes(int cols_cap, size_t max_part_bytes)
 {
-    return operand_bytes(cols_cap) + align256(max_part_bytes);
+    return operand_bytes(cols_cap) + align256(max_part_bytes) + align256(kSsBytes);
 }
 
 size_t emu_mfma_part_bytes(int rows, int cols, int nmat) { return part_bytes(rows, cols, nmat); }
@@ -705,10 +748,18 @@ bool emu_mfma_supports(int encoding, int cols, int n_tok)
 
 template <int MODE> static void launch_link(bool narrow, dim3 grid, hipStream_t stream, const LinkArgs &a)
 {
-    if (narrow)
-        hipLaunchKernelGGL((mfma_link_kernel<4, MODE>), grid, dim3(kLinkThreads), 0, stream, a);
-    else
-        hipLaunchKernelGGL((mfma_link_kernel<kMaxSlices, MODE>), grid, dim3(kLinkThreads), 0, stream, a);
+    if (a.gain && !a.ssp) { // the row's sum of squares in one workgroup
+        if (narrow)
+            hipLaunchKernelGGL((mfma_link_kernel<4, MODE, kLinkThreads>), grid, dim3(kLinkThreads), 0, stream, a);
+        else
+            hipLaunchKernelGGL((mfma_link_kernel<kMaxSlices, MODE, kLinkThreads>), grid, dim3(kLinkThreads), 0, stream,
+                               a);
+    } else {
+        if (narrow)
+            hipLaunchKernelGGL((mfma_link_kernel<4, MODE, kLinkSmall>), grid, dim3(kLinkSmall), 0, stream, a);
+        else
+            hipLaunchKernelGGL((mfma_link_kernel<kMaxSlices, MODE, kLinkSmall>), grid, dim3(kLinkSmall), 0, stream, a);
+    }
 }
 
 int emu_mfma_link(emu_ctx *ctx, const EmuMfmaLink &l)
@@ -717,7 +768,8 @@ int emu_mfma_link(emu_ctx *ctx, const EmuMfmaLink &l)
         l.cols > 8 * kLinkThreads * kLinkPairs)
         return EMU_E_CONFIG;
     const Ws w = workspace(ctx, l.cols_cap);
-    if (!ctx->mfma_ws || (l.limbs && ctx->mfma_ws_bytes < operand_bytes(l.cols_cap))) return EMU_E_CONFIG;
+    if (!ctx->mfma_ws || (l.limbs && ctx->mfma_ws_bytes < operand_bytes(l.cols_cap) + align256(kSsBytes)))
+        return EMU_E_CONFIG;
     LinkArgs a{};
     a.part = l.from_part ? w.part : nullptr;
     a.nks = l.from_part ? l.part_nks : 0;
@@ -743,15 +795,18 @@ int emu_mfma_link(emu_ctx *ctx, const EmuMfmaLink &l)
     a.d_scale = l.d_scale;
     a.act = l.act;
     a.span = l.span;
+    a.ssp = l.defer_norm && a.gain && a.xa ? w.ss : nullptr;
     if (a.span && (l.cols % 256 != 0 || !a.xa)) return EMU_E_CONFIG;
+    if (l.defer_norm && (!a.gain || !a.span || !a.xa)) return EMU_E_CONFIG; // only before a span matvec
     if (a.m_contrib && (!a.h || !a.m_ids || !a.m_wts || a.m_k < 1 || a.m_k > 8)) return EMU_E_CONFIG;
     if (a.d_part && (!a.h || a.d_nks < 1 || a.d_nks > kMaxSlices ||
                      (size_t)a.d_nks * kMaxTok * (size_t)l.cols * sizeof(float) > w.part_bytes))
         return EMU_E_CONFIG;
     if (l.from_part && (size_t)a.nks * a.nmat * kMaxTok * (size_t)l.cols * sizeof(float) > w.part_bytes)
         return EMU_E_CONFIG;
-    // Without a norm there is no row-wide sum: one workgroup per 4096 columns.
-    const int gy = a.gain ? 1 : (l.cols / 8 + kLinkThreads - 1) / kLinkThreads;
+    // Without a norm (or with it deferred) there is no row-wide sum: one
+    // small workgroup per 512 columns.
+    const int gy = a.gain && !a.ssp ? 1 : (l.cols / 8 + kLinkSmall - 1) / kLinkSmall;
     const bool narrow = a.nks <= 4 && a.d_nks <= 4;
     const dim3 grid(l.n_tok, gy);
     switch (a.mode) {
@@ -783,6 +838,12 @@ int emu_mfma_matvec(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int
     ma.xa = w.xa;
     ma.xs = w.xs;
     ma.part = w.part;
+    if (q.span_norm) {
+        if (!q.span_scales) return EMU_E_CONFIG;
+        ma.ssp = w.ss;
+        ma.ss_groups = (q.cols / 8 + kLinkSmall - 1) / kLinkSmall;
+        ma.eps = q.eps;
+    }
     const int nks = (q.cols + kSlice - 1) / kSlice, nrt = (q.rows + kTileRows - 1) / kTileRows;
     const int units = nks * nrt * nmat;
     const dim3 grid((unsigned)units), block(EMU_WAVE * kWaves);
@@ -858,8 +919,11 @@ int emu_launch_mfma(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int
     l.eps = a.eps;
     l.limbs = true;
     l.span = a.span_scales; // the chained steps' output matvec; the C ABI's calls keep per-sub-block scales
+    l.defer_norm = a.span_scales && a.gain && a.cols >= kEmuDeferNormCols; // the matvec takes the RMS factor
     if ((st = emu_mfma_link(ctx, l)) != EMU_OK) return st;
-    if ((st = emu_mfma_matvec(ctx, a, n_tok, a.cols, nullptr)) != EMU_OK) return st;
+    QmvArgs q = a;
+    q.span_norm = l.defer_norm;
+    if ((st = emu_mfma_matvec(ctx, q, n_tok, a.cols, nullptr)) != EMU_OK) return st;
     return emu_mfma_finish(ctx, a, n_tok, a.cols, key_slots);
 }
 

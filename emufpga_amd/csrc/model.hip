@@ -901,6 +901,9 @@ int run_chain(emu_session *s)
     const float *ffn_norm = reinterpret_cast<const float *>(m->base + m->off_ffn_norm);
     const float *out_norm = reinterpret_cast<const float *>(m->base + m->off_out_norm);
     int st = EMU_OK;
+    // every normalising link's row is the width H; from kEmuDeferNormCols on
+    // its RMS factor is left to the span matvec that consumes it
+    const bool defer = H >= kEmuDeferNormCols;
     auto link = [&](int mode, int nks, int nmat, float *h, const float *x, int cols, const float *gain, bool limbs) {
         EmuMfmaLink l{};
         l.mode = mode;
@@ -916,12 +919,17 @@ int run_chain(emu_session *s)
         l.eps = c.eps;
         l.limbs = limbs;
         l.span = 1;
+        l.defer_norm = gain && defer;
         return emu_mfma_link(ctx, l);
     };
     // span: the operands come from a link (one scale per 256-column span);
-    // the o projection's come from the attention, per 16-column sub-block
-    auto matvec = [&](const uint8_t *w, const uint8_t *w_up, size_t rb, int rows, int cols, int *nks, bool span) {
+    // the o projection's come from the attention, per 16-column sub-block.
+    // norm: that link normalised (its RMS factor left to this matvec when deferred).
+    auto matvec = [&](const uint8_t *w, const uint8_t *w_up, size_t rb, int rows, int cols, int *nks, bool span,
+                      bool norm) {
         QmvArgs q{};
+        q.span_norm = norm && defer;
+        q.eps = c.eps;
         q.w = m->mm_or(w, &q.mfma_major);
         q.w_up = w_up ? m->mm_or(w_up, &q.mfma_major) : nullptr;
         q.row_bytes = rb;
@@ -939,7 +947,7 @@ int run_chain(emu_session *s)
     for (uint32_t layer = 0; layer < c.layers; ++layer) {
         const uint8_t *lw = m->base + m->off_layers + (size_t)layer * m->layer_bytes;
         int nks = 0;
-        if ((st = matvec(lw + m->off_q, nullptr, m->rb_h, QW + 2 * KW, H, &nks, true)) != EMU_OK) return st;
+        if ((st = matvec(lw + m->off_q, nullptr, m->rb_h, QW + 2 * KW, H, &nks, true, true)) != EMU_OK) return st;
         // Attention adds the q|k|v slices itself and writes the o
         // projection's operands: no link kernel on either side of it.
         EmuAttnLaunch al = layer_attn(s, layer);
@@ -950,11 +958,11 @@ int run_chain(emu_session *s)
         al.xa = xa;
         al.xs = xs;
         if ((st = emu_launch_attn(ctx, al)) != EMU_OK) return st;
-        if ((st = matvec(lw + m->off_o, nullptr, m->rb_q, H, QW, &nks, false)) != EMU_OK) return st;
+        if ((st = matvec(lw + m->off_o, nullptr, m->rb_q, H, QW, &nks, false, false)) != EMU_OK) return st;
         if ((st = link(1, nks, 1, s->state, nullptr, H, ffn_norm + (size_t)layer * H, true)) != EMU_OK) return st;
-        if ((st = matvec(lw + m->off_g, lw + m->off_u, m->rb_h, F, H, &nks, true)) != EMU_OK) return st;
+        if ((st = matvec(lw + m->off_g, lw + m->off_u, m->rb_h, F, H, &nks, true, true)) != EMU_OK) return st;
         if ((st = link(2, nks, 2, nullptr, nullptr, F, nullptr, true)) != EMU_OK) return st;
-        if ((st = matvec(lw + m->off_d, nullptr, m->rb_f, H, F, &nks, true)) != EMU_OK) return st;
+        if ((st = matvec(lw + m->off_d, nullptr, m->rb_f, H, F, &nks, true, false)) != EMU_OK) return st;
         const float *next = layer + 1 < c.layers ? attn_norm + (size_t)(layer + 1) * H : out_norm;
         if ((st = link(1, nks, 1, s->state, nullptr, H, next, true)) != EMU_OK) return st;
         if ((st = mark(s, layer + 1)) != EMU_OK) return st;
@@ -970,6 +978,8 @@ int run_chain(emu_session *s)
     out.key_stride = (int)s->key_stride;
     out.tie_last = c.style == EMU_STYLE_SMOL ? 1 : 0;
     out.span_scales = 1;
+    out.span_norm = defer;
+    out.eps = c.eps;
     if ((st = emu_mfma_matvec(ctx, out, n, cap, nullptr)) != EMU_OK) return st;
     int slots = 0;
     if ((st = emu_mfma_finish(ctx, out, n, cap, &slots)) != EMU_OK) return st;
@@ -1047,6 +1057,7 @@ int run_moe(emu_session *s)
             l.eps = c.eps;
             l.limbs = true;
             l.span = 1;
+            l.defer_norm = H >= (uint32_t)kEmuDeferNormCols; // the q|k|v matvec applies the RMS factor
             if (layer > 0) { // the previous layer's (shared down and) expert sum join the residual here
                 l.h = s->state;
                 l.d_part = sd_nks > 0;
@@ -1068,6 +1079,8 @@ int run_moe(emu_session *s)
             q.cols = (int)H;
             q.nb = (int)(H / be);
             q.span_scales = 1; // the link's operands
+            q.span_norm = l.defer_norm;
+            q.eps = c.eps;
             int nks = 0;
             if ((st = emu_mfma_matvec(ctx, q, n, cap, &nks)) != EMU_OK) return st;
             EmuAttnLaunch al = layer_attn(s, layer);
