@@ -273,16 +273,17 @@ __global__ __launch_bounds__(TH) void mfma_link_kernel(LinkArgs a)
             amax = fmaxf(amax, fabsf(w[e]));
             bad |= !(fabsf(w[e]) <= 3.402823466e38f);
         }
-        amax = fmaxf(amax, __shfl_xor(amax, 1, EMU_WAVE));
-        bad |= __shfl_xor(bad, 1, EMU_WAVE);
+        // One exchange chain carries both: a non-finite piece enters as +inf,
+        // which every max keeps.  DPP and permlane moves, no LDS round trips.
+        amax = bad ? __int_as_float(0x7f800000) : amax;
+        amax = fmaxf(amax, emu_xor_get<1>(amax));
         if (a.span) { // the span's 32 pairs are 32 neighbouring lanes (npairs is whole spans)
-#pragma unroll
-            for (int o = 2; o < 32; o <<= 1) {
-                amax = fmaxf(amax, __shfl_xor(amax, o, EMU_WAVE));
-                bad |= __shfl_xor(bad, o, EMU_WAVE);
-            }
+            amax = fmaxf(amax, emu_xor_get<2>(amax));
+            amax = fmaxf(amax, emu_xor_get<4>(amax));
+            amax = fmaxf(amax, emu_xor_get<8>(amax));
+            amax = fmaxf(amax, emu_xor_get<16>(amax));
         }
-        const bool finite = !bad;
+        const bool finite = amax <= 3.402823466e38f;
         int e2 = 0;
         (void)frexpf(finite ? amax : 0.0f, &e2); // amax < 2^e2, so |x| * 2^(6-e2) < 64
         uint32_t lo[3] = {0u, 0u, 0u}, hi[3] = {0u, 0u, 0u};
@@ -576,14 +577,17 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
     if constexpr (SPAN) {
         if (a.ssp) { // the sums in a fixed order (the same in every workgroup), then the factor
             float tot = (sq[0] + sq[1]) + sq[2];
-            tot += __shfl_xor(tot, 1, EMU_WAVE);
-            tot += __shfl_xor(tot, 2, EMU_WAVE);
-            tot += __shfl_xor(tot, 4, EMU_WAVE);
-            const float rs = 1.0f / sqrtf(tot / (float)a.cols + a.eps);
-            xsv.x *= __shfl(rs, 8 * (4 * kh), EMU_WAVE); // a power of two times rs: exact
-            xsv.y *= __shfl(rs, 8 * (4 * kh + 1), EMU_WAVE);
-            xsv.z *= __shfl(rs, 8 * (4 * kh + 2), EMU_WAVE);
-            xsv.w *= __shfl(rs, 8 * (4 * kh + 3), EMU_WAVE);
+            tot += emu_xor_lane<1>(tot);
+            tot += emu_xor_lane<2>(tot);
+            tot += emu_xor_lane<4>(tot);
+            const int rb = __float_as_int(1.0f / sqrtf(tot / (float)a.cols + a.eps)); // token t's in lane 8 t
+            float rs[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) rs[t] = __int_as_float(__builtin_amdgcn_readlane(rb, 8 * t));
+            xsv.x *= kh ? rs[4] : rs[0]; // a power of two times the factor: exact
+            xsv.y *= kh ? rs[5] : rs[1];
+            xsv.z *= kh ? rs[6] : rs[2];
+            xsv.w *= kh ? rs[7] : rs[3];
         }
         const float s[4] = {xsv.x, xsv.y, xsv.z, xsv.w};
 #pragma unroll
