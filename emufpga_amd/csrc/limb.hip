@@ -495,22 +495,27 @@ __global__ __launch_bounds__((EMU_WAVE * LimbShape<S, WV>::W)) void qmv_limb_ker
         for (int d = 0; d < D; ++d) load_slot(0, d, buf[d]);
         __builtin_amdgcn_sched_barrier(0);
         if (NORM) {
+            // The limbs are of x * gain and the RMS factor multiplies each
+            // row's dot, so the row's sum of squares is needed only after
+            // the limb records' barrier, not before the limbs: one barrier.
             float ss = 0.0f;
 #pragma unroll
             for (int k = 0; k < SH::CPT; ++k) ss = __builtin_fmaf(xv[k], xv[k], ss);
             ss = wave_sum63(ss);
             if (lane == EMU_WAVE - 1) red[wv] = ss;
-            __syncthreads();
-            float tot = 0.0f;
 #pragma unroll
-            for (int k = 0; k < SH::W; ++k) tot += red[k];
-            const float scale = 1.0f / sqrtf(tot / (float)a.cols + a.eps);
-#pragma unroll
-            for (int k = 0; k < SH::CPT; ++k) xv[k] = __fmul_rn(__fmul_rn(xv[k], scale), gv[k]);
+            for (int k = 0; k < SH::CPT; ++k) xv[k] = __fmul_rn(xv[k], gv[k]);
         }
         make_limbs<SH::G, SH::CPT>(xv, rec, sb, pi);
     }
     __syncthreads();
+    float rscale = 1.0f;
+    if (NORM) {
+        float tot = 0.0f;
+#pragma unroll
+        for (int k = 0; k < SH::W; ++k) tot += red[k];
+        rscale = 1.0f / sqrtf(tot / (float)a.cols + a.eps);
+    }
     Limbs L;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -524,8 +529,8 @@ __global__ __launch_bounds__((EMU_WAVE * LimbShape<S, WV>::W)) void qmv_limb_ker
 
     uint64_t best = 0;
     auto finish = [&](int row, const float (&p)[NR], float resid) {
-        float val = p[0];
-        if (DUAL) val = emu_glu(val, p[1], a.act);
+        float val = NORM ? __fmul_rn(p[0], rscale) : p[0];
+        if (DUAL) val = emu_glu(val, NORM ? __fmul_rn(p[1], rscale) : p[1], a.act);
         val = emu_out_epi(val, a.out_div, a.softcap);
         if (row < a.rows) {
             a.y[row] = ACC ? emu_resid_add(resid, val, a.acc_scale) : val;
