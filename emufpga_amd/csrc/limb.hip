@@ -380,15 +380,12 @@ __device__ __forceinline__ void make_limbs(const float (&xv)[CPT], LimbRec *rec,
         amax = fmaxf(amax, fabsf(xv[k]));
         bad |= !(fabsf(xv[k]) <= 3.402823466e38f);
     }
-    if (G >= 2) {
-        amax = fmaxf(amax, __shfl_xor(amax, 1, EMU_WAVE));
-        bad |= __shfl_xor(bad, 1, EMU_WAVE);
-    }
-    if (G >= 4) {
-        amax = fmaxf(amax, __shfl_xor(amax, 2, EMU_WAVE));
-        bad |= __shfl_xor(bad, 2, EMU_WAVE);
-    }
-    const bool finite = !bad;
+    // The G threads' exchanges by DPP (no LDS round trips); a non-finite
+    // value enters the max as +inf, which every max keeps.
+    amax = bad ? __int_as_float(0x7f800000) : amax;
+    if (G >= 2) amax = fmaxf(amax, emu_xor_lane<1>(amax));
+    if (G >= 4) amax = fmaxf(amax, emu_xor_lane<2>(amax));
+    const bool finite = amax <= 3.402823466e38f;
     int e = 0;
     (void)frexpf(finite ? amax : 0.0f, &e);      // amax < 2^e, so |x| * 2^(6-e) < 64
     // Digits by the float recurrence f0 = rint(v), r1 = (v - f0) * 128,
@@ -426,8 +423,8 @@ __device__ __forceinline__ void make_limbs(const float (&xv)[CPT], LimbRec *rec,
         s2 = __builtin_amdgcn_sdot4((int)b2, 0x01010101, s2, false);
     }
     int sum = s0 * 16384 + s1 * 128 + s2;
-    if (G >= 2) sum += __shfl_xor(sum, 1, EMU_WAVE);
-    if (G >= 4) sum += __shfl_xor(sum, 2, EMU_WAVE);
+    if (G >= 2) sum += __float_as_int(emu_xor_lane<1>(__int_as_float(sum)));
+    if (G >= 4) sum += __float_as_int(emu_xor_lane<2>(__int_as_float(sum)));
     uint32_t *d0 = reinterpret_cast<uint32_t *>(&rec[sb].l0);
     uint32_t *d1 = reinterpret_cast<uint32_t *>(&rec[sb].l1);
     uint32_t *d2 = reinterpret_cast<uint32_t *>(&rec[sb].l2);
