@@ -183,6 +183,9 @@ int emu_weights_mfma_major(emu_ctx *ctx, int encoding, const void *d_src, size_t
  * each equals a composition of reference calls):
  *  - gain != NULL: x is RMS-normalised with gain and eps first
  *    (spm-smol-ops/src/norm.rs:12-32 pre_norm, spm-qwen3-slice/src/math.rs:1-10);
+ *    on the int8-limb kernels the limbs are of x * gain and the RMS factor
+ *    multiplies each row's (each gate/up row's) sum, the same product with
+ *    the factor's rounding moved: the limb bound above holds for x * gain;
  *  - d_w_up != NULL: SwiGLU pair, y = silu(W x) * (W_up x)
  *    (spm-batch/src/inner.rs:103-107, spm-qwen3-slice/src/model.rs:93-116). */
 int emu_qmatvec_fused(emu_ctx *ctx, int encoding, const void *d_w, const void *d_w_up,
