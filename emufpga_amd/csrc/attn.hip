@@ -268,8 +268,17 @@ __device__ __forceinline__ void unpack_row(const V &raw, float (&out)[EPL])
     }
 }
 
+// One query head per kv head (head dim 128, f16 K/V) fits in 80 registers
+// (83 with twelve q|k|v slices), so six (five) workgroups share a CU instead
+// of four: at eight clients and 1k positions (2,176 workgroups) the chunks
+// run in fewer rounds.
+constexpr int attn_per_cu(int hd, bool f16, int gqp, int ms)
+{
+    return gqp == 1 && hd == 128 && f16 ? (ms <= 4 ? 6 : 5) : 1;
+}
+
 template <int HD, bool F16, int GQP, int MS>
-__global__ __launch_bounds__(kThreads) void attn_decode_kernel(AttnArgs a)
+__global__ __launch_bounds__(kThreads, attn_per_cu(HD, F16, GQP, MS)) void attn_decode_kernel(AttnArgs a)
 {
     using kv_t = typename std::conditional<F16, __half, float>::type;
     constexpr int EPL = HD / EMU_WAVE;          // head elements per lane
