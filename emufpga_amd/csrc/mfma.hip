@@ -129,6 +129,8 @@ constexpr int kLinkPairs = 3; // columns per token up to 8 * kLinkThreads * kLin
 // spread over the CUs instead of queueing at a few.
 constexpr int kLinkSmall = 64;
 constexpr int kSsGroups = kLinkThreads * kLinkPairs / kLinkSmall; // small workgroups per token, at most
+constexpr size_t kSsBytes = (size_t)kMaxTok * kSsGroups * sizeof(float);
+constexpr size_t kSsRegion = (kSsBytes + 255) & ~(size_t)255; // just ahead of the A operands
 
 template <int MAXS, int MODE, int TH>
 __global__ __launch_bounds__(TH) void mfma_link_kernel(LinkArgs a)
@@ -318,11 +320,7 @@ struct MfmaArgs {
     const uint8_t *xa;
     const float *xs;
     float *part; // [slices][nmat][kMaxTok][rows], slices = ceil(cols / kSlice)
-    // Span form, optional: each token's RMS factor 1 / sqrt(sum / cols + eps)
-    // from the link's ss_groups sums of squares (LinkArgs::ssp).
-    const float *ssp;
-    int ss_groups;
-    float eps;
+    float eps; // NORM: each token's RMS factor 1 / sqrt(sum / cols + eps)
 };
 
 // Q6_K codes (0..63) of 8 columns, two dwords: sub-block (h, q, p) takes
@@ -385,7 +383,10 @@ struct Unit {
 // d follow, all with the non-temporal hint (each weight byte is read once per
 // step; batch 8 measured 0.7% faster than with plain loads).  The codes are
 // the same, so the results are bit for bit those of the GGUF-order path.
-template <bool MM, bool SPAN>
+// NORM (span form only): the operands come from a link that left its RMS
+// factor to this matvec; the link's sums of squares sit kSsRegion bytes
+// ahead of xa.
+template <bool MM, bool SPAN, bool NORM>
 __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs a, int units)
 {
     const int nks = (a.cols + kSlice - 1) / kSlice, nrt = (a.rows + kTileRows - 1) / kTileRows;
@@ -420,6 +421,12 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
         const uint8_t *ap = a.xa + (size_t)cbl * 16 * kSbBytes + (size_t)(kh * 24 + arow) * 8;
 #pragma unroll
         for (int sb = 0; sb < 16; ++sb) b.av[sb] = *reinterpret_cast<const long *>(ap + sb * kSbBytes);
+        if constexpr (NORM) { // the link's sums of squares: lane 8 t + i, token t's sums i, i + 8, i + 16
+            const float *ssp = reinterpret_cast<const float *>(a.xa - kSsRegion);
+            const int tt = lane >> 3, g = lane & 7, groups = (a.cols / 8 + kLinkSmall - 1) / kLinkSmall;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) sq[k] = g + 8 * k < groups ? ssp[tt * kSsGroups + g + 8 * k] : 0.0f;
+        }
         // and so do the slice's activation scales (one float4 per thread:
         // half a sub-block's eight tokens; zero past the row)
         static_assert(kSlice / 16 * kMaxTok / 4 <= EMU_WAVE * kWaves, "one scale load per thread");
@@ -490,16 +497,24 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
         }
         if (!has) b.d = 0; // d = 0: the block's (finite, integer) sums add exact zeros
     }
-    // The deferred norm's sums of squares load behind the weights (nothing
-    // needs them before the float step): lane 8 t + i, token t's sums i,
-    // i + 8, i + 16.
-    if constexpr (SPAN) {
-        if (a.ssp) {
-            const int tt = lane >> 3, g = lane & 7;
+    static_assert(SPAN || !NORM, "the deferred norm comes with span scales");
+    if constexpr (NORM) {
+        // The factor, formed while the weights are in flight: the sums in a
+        // fixed order (the same in every workgroup), token t's in lane 8 t.
+        // Tokens past n_tok take whatever their slots hold; their outputs
+        // are never stored.
+        float tot = (sq[0] + sq[1]) + sq[2];
+        tot += emu_xor_lane<1>(tot);
+        tot += emu_xor_lane<2>(tot);
+        tot += emu_xor_lane<4>(tot);
+        const int rb = __float_as_int(1.0f / sqrtf(tot / (float)a.cols + a.eps));
+        float rs[8];
 #pragma unroll
-            for (int k = 0; k < 3; ++k)
-                sq[k] = tt < a.n_tok && g + 8 * k < a.ss_groups ? a.ssp[tt * kSsGroups + g + 8 * k] : 0.0f;
-        }
+        for (int t = 0; t < 8; ++t) rs[t] = __int_as_float(__builtin_amdgcn_readlane(rb, 8 * t));
+        xsv.x *= kh ? rs[4] : rs[0]; // a power of two times the factor: exact
+        xsv.y *= kh ? rs[5] : rs[1];
+        xsv.z *= kh ? rs[6] : rs[2];
+        xsv.w *= kh ? rs[7] : rs[3];
     }
     if constexpr (!SPAN) { // the slice's scales, shared by the workgroup
         if (tid < kSlice / 16 * kMaxTok / 4) reinterpret_cast<float4 *>(xs)[tid] = xsv;
@@ -575,20 +590,6 @@ __global__ __launch_bounds__(EMU_WAVE * kWaves, 4) void qmv_mfma_kernel(MfmaArgs
         if (sb + 1 < 16) cur = next;
     }
     if constexpr (SPAN) {
-        if (a.ssp) { // the sums in a fixed order (the same in every workgroup), then the factor
-            float tot = (sq[0] + sq[1]) + sq[2];
-            tot += emu_xor_lane<1>(tot);
-            tot += emu_xor_lane<2>(tot);
-            tot += emu_xor_lane<4>(tot);
-            const int rb = __float_as_int(1.0f / sqrtf(tot / (float)a.cols + a.eps)); // token t's in lane 8 t
-            float rs[8];
-#pragma unroll
-            for (int t = 0; t < 8; ++t) rs[t] = __int_as_float(__builtin_amdgcn_readlane(rb, 8 * t));
-            xsv.x *= kh ? rs[4] : rs[0]; // a power of two times the factor: exact
-            xsv.y *= kh ? rs[5] : rs[1];
-            xsv.z *= kh ? rs[6] : rs[2];
-            xsv.w *= kh ? rs[7] : rs[3];
-        }
         const float s[4] = {xsv.x, xsv.y, xsv.z, xsv.w};
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -675,30 +676,29 @@ __global__ __launch_bounds__(kFinishThreads) void mfma_finish_kernel(FinishArgs 
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// Workspace: A operands and scales for up to cols_cap columns, the
-// partial sums, and at its end the deferred norms' sums of squares.
+// Workspace: the deferred norms' sums of squares (kSsRegion bytes, so a
+// matvec finds them just ahead of its A operands), the A operands and
+// scales for up to cols_cap columns, then the partial sums.
 struct Ws {
     uint8_t *xa;
     float *xs, *part, *ss;
     size_t part_bytes;
 };
-constexpr size_t kSsBytes = (size_t)kMaxTok * kSsGroups * sizeof(float);
 size_t operand_bytes(int cols_cap)
 {
     const size_t nsb = (size_t)cols_cap / 16;
-    return align256(nsb * kSbBytes) + align256(nsb * kMaxTok * sizeof(float));
+    return kSsRegion + align256(nsb * kSbBytes) + align256(nsb * kMaxTok * sizeof(float));
 }
 Ws workspace(emu_ctx *ctx, int cols_cap)
 {
     const size_t nsb = (size_t)cols_cap / 16;
     uint8_t *base = static_cast<uint8_t *>(ctx->mfma_ws);
-    const size_t fixed = operand_bytes(cols_cap) + align256(kSsBytes);
     Ws w;
-    w.xa = base;
-    w.xs = reinterpret_cast<float *>(base + align256(nsb * kSbBytes));
+    w.ss = reinterpret_cast<float *>(base);
+    w.xa = base + kSsRegion;
+    w.xs = reinterpret_cast<float *>(w.xa + align256(nsb * kSbBytes));
     w.part = reinterpret_cast<float *>(base + operand_bytes(cols_cap));
-    w.part_bytes = ctx->mfma_ws_bytes > fixed ? ctx->mfma_ws_bytes - fixed : 0;
-    w.ss = reinterpret_cast<float *>(base + operand_bytes(cols_cap) + w.part_bytes);
+    w.part_bytes = ctx->mfma_ws_bytes > operand_bytes(cols_cap) ? ctx->mfma_ws_bytes - operand_bytes(cols_cap) : 0;
     return w;
 }
 size_t part_bytes(int rows, int cols, int nmat)
@@ -710,12 +710,12 @@ size_t part_bytes(int rows, int cols, int nmat)
 
 size_t emu_mfma_workspace_bytes(int rows, int cols, int nmat)
 {
-    return operand_bytes(cols) + align256(part_bytes(rows, cols, nmat)) + align256(kSsBytes);
+    return operand_bytes(cols) + align256(part_bytes(rows, cols, nmat));
 }
 
 size_t emu_mfma_chain_bytes(int cols_cap, size_t max_part_bytes)
 {
-    return operand_bytes(cols_cap) + align256(max_part_bytes) + align256(kSsBytes);
+    return operand_bytes(cols_cap) + align256(max_part_bytes);
 }
 
 size_t emu_mfma_part_bytes(int rows, int cols, int nmat) { return part_bytes(rows, cols, nmat); }
@@ -772,8 +772,7 @@ int emu_mfma_link(emu_ctx *ctx, const EmuMfmaLink &l)
         l.cols > 8 * kLinkThreads * kLinkPairs)
         return EMU_E_CONFIG;
     const Ws w = workspace(ctx, l.cols_cap);
-    if (!ctx->mfma_ws || (l.limbs && ctx->mfma_ws_bytes < operand_bytes(l.cols_cap) + align256(kSsBytes)))
-        return EMU_E_CONFIG;
+    if (!ctx->mfma_ws || (l.limbs && ctx->mfma_ws_bytes < operand_bytes(l.cols_cap))) return EMU_E_CONFIG;
     LinkArgs a{};
     a.part = l.from_part ? w.part : nullptr;
     a.nks = l.from_part ? l.part_nks : 0;
@@ -842,23 +841,23 @@ int emu_mfma_matvec(emu_ctx *ctx, const QmvArgs &q, int n_tok, int cols_cap, int
     ma.xa = w.xa;
     ma.xs = w.xs;
     ma.part = w.part;
-    if (q.span_norm) {
-        if (!q.span_scales) return EMU_E_CONFIG;
-        ma.ssp = w.ss;
-        ma.ss_groups = (q.cols / 8 + kLinkSmall - 1) / kLinkSmall;
-        ma.eps = q.eps;
-    }
+    if (q.span_norm && !q.span_scales) return EMU_E_CONFIG;
+    ma.eps = q.eps;
     const int nks = (q.cols + kSlice - 1) / kSlice, nrt = (q.rows + kTileRows - 1) / kTileRows;
     const int units = nks * nrt * nmat;
     const dim3 grid((unsigned)units), block(EMU_WAVE * kWaves);
-    if (q.mfma_major && q.span_scales)
-        hipLaunchKernelGGL((qmv_mfma_kernel<true, true>), grid, block, 0, ctx->stream, ma, units);
+    if (q.mfma_major && q.span_norm)
+        hipLaunchKernelGGL((qmv_mfma_kernel<true, true, true>), grid, block, 0, ctx->stream, ma, units);
+    else if (q.mfma_major && q.span_scales)
+        hipLaunchKernelGGL((qmv_mfma_kernel<true, true, false>), grid, block, 0, ctx->stream, ma, units);
     else if (q.mfma_major)
-        hipLaunchKernelGGL((qmv_mfma_kernel<true, false>), grid, block, 0, ctx->stream, ma, units);
+        hipLaunchKernelGGL((qmv_mfma_kernel<true, false, false>), grid, block, 0, ctx->stream, ma, units);
+    else if (q.span_norm)
+        hipLaunchKernelGGL((qmv_mfma_kernel<false, true, true>), grid, block, 0, ctx->stream, ma, units);
     else if (q.span_scales)
-        hipLaunchKernelGGL((qmv_mfma_kernel<false, true>), grid, block, 0, ctx->stream, ma, units);
+        hipLaunchKernelGGL((qmv_mfma_kernel<false, true, false>), grid, block, 0, ctx->stream, ma, units);
     else
-        hipLaunchKernelGGL((qmv_mfma_kernel<false, false>), grid, block, 0, ctx->stream, ma, units);
+        hipLaunchKernelGGL((qmv_mfma_kernel<false, false, false>), grid, block, 0, ctx->stream, ma, units);
     EMU_LAUNCH_CHECK(ctx);
     if (part_nks) *part_nks = nks;
     return EMU_OK;
