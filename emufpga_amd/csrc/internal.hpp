@@ -885,10 +885,6 @@ struct EmuMfmaLink {
     // the link runs as many small ones.  The limbs are of x * gain.
     int defer_norm;
 };
-// Rows from this width on defer the norm: narrower ones (Granite's 1024)
-// already spread over a token's workgroup, and the consuming matvec's factor
-// costs more than the link saves (0.4% of the step).
-constexpr int kEmuDeferNormCols = 2048;
 size_t emu_mfma_chain_bytes(int cols_cap, size_t max_part_bytes);
 size_t emu_mfma_part_bytes(int rows, int cols, int nmat);
 int emu_mfma_link(emu_ctx *ctx, const EmuMfmaLink &l);

@@ -922,7 +922,7 @@ int emu_launch_mfma(emu_ctx *ctx, int encoding, const QmvArgs &a, int n_tok, int
     l.eps = a.eps;
     l.limbs = true;
     l.span = a.span_scales; // the chained steps' output matvec; the C ABI's calls keep per-sub-block scales
-    l.defer_norm = a.span_scales && a.gain && a.cols >= kEmuDeferNormCols; // the matvec takes the RMS factor
+    l.defer_norm = a.span_scales && a.gain; // the matvec takes the RMS factor
     if ((st = emu_mfma_link(ctx, l)) != EMU_OK) return st;
     QmvArgs q = a;
     q.span_norm = l.defer_norm;

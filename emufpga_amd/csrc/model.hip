@@ -901,9 +901,6 @@ int run_chain(emu_session *s)
     const float *ffn_norm = reinterpret_cast<const float *>(m->base + m->off_ffn_norm);
     const float *out_norm = reinterpret_cast<const float *>(m->base + m->off_out_norm);
     int st = EMU_OK;
-    // every normalising link's row is the width H; from kEmuDeferNormCols on
-    // its RMS factor is left to the span matvec that consumes it
-    const bool defer = H >= kEmuDeferNormCols;
     auto link = [&](int mode, int nks, int nmat, float *h, const float *x, int cols, const float *gain, bool limbs) {
         EmuMfmaLink l{};
         l.mode = mode;
@@ -919,16 +916,16 @@ int run_chain(emu_session *s)
         l.eps = c.eps;
         l.limbs = limbs;
         l.span = 1;
-        l.defer_norm = gain && defer;
+        l.defer_norm = gain ? 1 : 0; // the consuming span matvec applies the RMS factor
         return emu_mfma_link(ctx, l);
     };
     // span: the operands come from a link (one scale per 256-column span);
     // the o projection's come from the attention, per 16-column sub-block.
-    // norm: that link normalised (its RMS factor left to this matvec when deferred).
+    // norm: that link normalised, its RMS factor left to this matvec.
     auto matvec = [&](const uint8_t *w, const uint8_t *w_up, size_t rb, int rows, int cols, int *nks, bool span,
                       bool norm) {
         QmvArgs q{};
-        q.span_norm = norm && defer;
+        q.span_norm = norm ? 1 : 0;
         q.eps = c.eps;
         q.w = m->mm_or(w, &q.mfma_major);
         q.w_up = w_up ? m->mm_or(w_up, &q.mfma_major) : nullptr;
@@ -978,7 +975,7 @@ int run_chain(emu_session *s)
     out.key_stride = (int)s->key_stride;
     out.tie_last = c.style == EMU_STYLE_SMOL ? 1 : 0;
     out.span_scales = 1;
-    out.span_norm = defer;
+    out.span_norm = 1;
     out.eps = c.eps;
     if ((st = emu_mfma_matvec(ctx, out, n, cap, nullptr)) != EMU_OK) return st;
     int slots = 0;
@@ -1057,7 +1054,7 @@ int run_moe(emu_session *s)
             l.eps = c.eps;
             l.limbs = true;
             l.span = 1;
-            l.defer_norm = H >= (uint32_t)kEmuDeferNormCols; // the q|k|v matvec applies the RMS factor
+            l.defer_norm = 1; // the q|k|v matvec applies the RMS factor
             if (layer > 0) { // the previous layer's (shared down and) expert sum join the residual here
                 l.h = s->state;
                 l.d_part = sd_nks > 0;
